@@ -1,0 +1,71 @@
+/*
+ * yanchor_amd C ABI: MI355X (gfx950) kernels for YANchor's batched recurrent
+ * decode / prefill hot path.
+ *
+ * Conventions for every entry point:
+ *   - all tensor arguments are device pointers to caller-owned memory; the
+ *     library never allocates or frees device memory;
+ *   - tensors are dense row-major in the layout written next to each argument;
+ *   - `stream` is a hipStream_t (passed as void* so this header needs no HIP
+ *     include); work is enqueued on it and the call returns without a sync;
+ *   - the return value is 0 (YH_OK) or a negative error code; yh_last_error()
+ *     returns a message for the calling thread's last failure;
+ *   - dtype codes are the yh_dtype values below.
+ */
+#ifndef YANCHOR_AMD_H
+#define YANCHOR_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* yh_stream_t;
+
+enum yh_dtype { YH_F32 = 0, YH_BF16 = 1, YH_F16 = 2, YH_I32 = 3, YH_I64 = 4, YH_U8 = 5 };
+
+enum yh_status { YH_OK = 0, YH_ERR_INVALID = -1, YH_ERR_HIP = -2, YH_ERR_UNSUPPORTED = -3 };
+
+/* Message describing the calling thread's most recent error ("" if none). */
+const char* yh_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int yh_abi_version(void);
+
+/*
+ * Gated delta rule, token-recurrent form, state updated IN PLACE.
+ *
+ * Replaces the FLA fused_recurrent_gated_delta_rule launch with
+ * h0 == ht == initial_state in runtime/model/inference_kernels.py:147-173
+ * (called from the decode forward at inference_kernels.py:716) and the torch
+ * reference torch_recurrent_gated_delta_rule in the vendored Transformers wheel
+ * (transformers/models/qwen3_5/modeling_qwen3_5.py:314-353).
+ *
+ *   q, k   [B, T, H, K]   (qkv_dtype)
+ *   v      [B, T, HV, V]  (qkv_dtype)
+ *   g      [B, T, HV]     (g_dtype)     log-decay, state *= exp(g)
+ *   beta   [B, T, HV]     (beta_dtype)
+ *   state  [n_state_rows, HV, K, V] float32, read and written in place
+ *   state_indices  NULL, or int32 [B]: batch row b uses state row
+ *                  state_indices[b]; a negative index skips the row (its
+ *                  output is zero and no state is touched)
+ *   o      [B, T, HV, V]  (qkv_dtype)
+ *   scale  multiplier applied to q after the optional L2 normalisation
+ *          (the reference uses K ** -0.5)
+ *   use_qk_l2norm  nonzero: q and k are L2-normalised over K (eps 1e-6 inside
+ *          the rsqrt) before use, as use_qk_l2norm_in_kernel=True
+ * Requirements: HV % H == 0; K in {64, 128}; V in {64, 128}; without
+ * state_indices, n_state_rows >= B.
+ */
+int yh_gdn_recurrent(const void* q, const void* k, const void* v, const void* g,
+                     const void* beta, float* state, const int32_t* state_indices,
+                     void* o, int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K,
+                     int64_t V, int64_t n_state_rows, float scale, int use_qk_l2norm,
+                     int qkv_dtype, int g_dtype, int beta_dtype, yh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YANCHOR_AMD_H */

@@ -1,0 +1,192 @@
+"""Fixed-slot anchor memory on the CPU (oracle; test infrastructure only).
+
+Restates, from the reference:
+
+* ``MemoryState``        IndependentMemoryState, modeling_yanchor.py:80-120
+* ``select_topk``        modeling_yanchor.py:51-60
+* ``merge_topk``         modeling_yanchor.py:62-63
+* ``exclusive_prefix_topk``  modeling_yanchor.py:65-78 (brute-force form)
+* ``committed_read``     the decode read, modeling_yanchor.py:283-290, with the
+                         slot indirection and zero-logit sink of
+                         runtime/model/independent_memory.py:47-88, 177-188
+* ``commit_decode``      the decode push + Top-K commit, modeling_yanchor.py:
+                         291-312, with the slot indirection of
+                         runtime/model/independent_memory.py:90-175, 190-201
+
+Ordering contract of every Top-K here: candidates are ordered by
+(score descending, position ascending with invalid last, candidate index
+ascending); -0.0 ranks equal to +0.0.  That is the composition of the two
+stable sorts in select_topk (position first, then score) and the two packed
+u64 sorts of _push_select (independent_memory.py:115-128).
+
+Pins (tests/test_oracle_anchor.py): the tensor ``select_topk`` agrees with a
+brute-force ``sorted()`` on random inputs with forced ties, -0.0 and invalid
+slots; the read equals a softmax over [logits, 0] computed independently and
+reduces to closed forms for zero / one valid slot; ``exclusive_prefix_topk``
+is checked against the O(n^2) definition "Top-K of every earlier block".
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, fields
+
+import torch
+
+INT64_MAX = torch.iinfo(torch.long).max
+
+
+@dataclass
+class MemoryState:
+    keys: torch.Tensor            # [B, G, K_cap, D]
+    values: torch.Tensor          # [B, G, K_cap, D]
+    scores: torch.Tensor          # [B, G, K_cap] f32, -inf = empty
+    positions: torch.Tensor       # [B, G, K_cap] i32, -1 = empty (the validity mask)
+    pending_keys: torch.Tensor    # [B, G, PC, D]
+    pending_values: torch.Tensor  # [B, G, PC, D]
+    pending_scores: torch.Tensor  # [B, G, PC] f32
+    count: torch.Tensor           # [B] i64
+    total: torch.Tensor           # [B] i64
+
+    @classmethod
+    def empty(cls, batch, groups, capacity, chunk, dim, dtype=torch.bfloat16):
+        kv = (batch, groups, capacity, dim)
+        pend = (batch, groups, chunk, dim)
+        return cls(torch.zeros(kv, dtype=dtype), torch.zeros(kv, dtype=dtype),
+                   torch.full(kv[:-1], -math.inf), torch.full(kv[:-1], -1, dtype=torch.int32),
+                   torch.zeros(pend, dtype=dtype), torch.zeros(pend, dtype=dtype),
+                   torch.full(pend[:-1], -math.inf), torch.zeros(batch, dtype=torch.long),
+                   torch.zeros(batch, dtype=torch.long))
+
+    def clone(self) -> "MemoryState":
+        return MemoryState(*(getattr(self, f.name).clone() for f in fields(self)))
+
+    def to(self, device) -> "MemoryState":
+        return MemoryState(*(getattr(self, f.name).to(device) for f in fields(self)))
+
+
+def select_topk(scores, positions, references, capacity):
+    """Keep the best ``capacity`` candidates along the last dim
+    (modeling_yanchor.py:51-60).  Returns (scores, positions, references),
+    padded with (-inf, -1, -1) when there are fewer candidates."""
+    positions = positions.long().masked_fill(references < 0, -1)
+    pos_key = positions.masked_fill(references < 0, INT64_MAX)
+    order = pos_key.argsort(dim=-1, stable=True)
+    scores, positions, references = (x.gather(-1, order) for x in (scores, positions, references))
+    order = scores.argsort(dim=-1, descending=True, stable=True)[..., :capacity]
+    out = [x.gather(-1, order) for x in (scores, positions, references)]
+    missing = capacity - order.shape[-1]
+    if missing:
+        out = [torch.nn.functional.pad(x, (0, missing), value=v)
+               for x, v in zip(out, (-math.inf, -1, -1))]
+    return tuple(out)
+
+
+def merge_topk(left, right, capacity):
+    """Top-K of the concatenation of two candidate lists (modeling_yanchor.py:62-63)."""
+    return select_topk(*(torch.cat((a, b), -1) for a, b in zip(left, right)), capacity)
+
+
+def select_topk_bruteforce(scores, positions, references, capacity):
+    """The same selection with Python's sorted() on one 1-D candidate list."""
+    items = []
+    for i, (s, p, r) in enumerate(zip(scores.tolist(), positions.tolist(), references.tolist())):
+        p = -1 if r < 0 else int(p)
+        pk = INT64_MAX if r < 0 else p
+        items.append((-(s + 0.0), pk, i, s, p, r))  # s + 0.0 maps -0.0 to +0.0
+    items.sort(key=lambda x: (x[0], x[1], x[2]))
+    chosen = items[:capacity]
+    out_s = [c[3] for c in chosen] + [-math.inf] * (capacity - len(chosen))
+    out_p = [c[4] for c in chosen] + [-1] * (capacity - len(chosen))
+    out_r = [c[5] for c in chosen] + [-1] * (capacity - len(chosen))
+    return out_s, out_p, out_r
+
+
+def exclusive_prefix_topk(scores, positions, references, capacity):
+    """For every block j of ``[B, NB, G, C]`` candidates: Top-K over all
+    candidates in blocks < j (an empty set for j = 0), plus a final entry
+    j = NB over all blocks.  Returns tensors ``[B, NB + 1, G, capacity]``.
+    Definition form of modeling_yanchor.py:65-78 (the reference computes it
+    with an up-sweep / down-sweep tree of merge_topk)."""
+    b, nb, g, c = scores.shape
+    outs = ([], [], [])
+    for j in range(nb + 1):
+        s = scores[:, :j].permute(0, 2, 1, 3).reshape(b, g, j * c)
+        p = positions[:, :j].permute(0, 2, 1, 3).reshape(b, g, j * c)
+        r = references[:, :j].permute(0, 2, 1, 3).reshape(b, g, j * c)
+        sel = select_topk(s, p, r, capacity)
+        for o, x in zip(outs, sel):
+            o.append(x)
+    return tuple(torch.stack(o, 1) for o in outs)
+
+
+def _rows(batch, indices):
+    if indices is None:
+        return list(range(batch))
+    return [int(i) for i in indices.tolist()]
+
+
+def committed_read(query, state: MemoryState, indices=None, dtype=torch.float64):
+    """Decode read of the committed slots (modeling_yanchor.py:283-290).
+
+    query ``[B, 1, H, D]``; H = G * R with query head h reading group h // R.
+    Per (row, head): logits = q.K^T / sqrt(D) over slots whose position >= 0;
+    weights = softmax([logits, 0])[:-1] (a sink logit of 0 with value 0);
+    read = weights @ V, cast to the query dtype.  With ``indices`` row r reads
+    state row indices[r]; a negative index reads nothing (output 0)."""
+    bq, _, h, d = query.shape
+    g = state.keys.shape[1]
+    r = h // g
+    out = torch.zeros(bq, 1, h, d, dtype=dtype)
+    for row, b in enumerate(_rows(bq, indices)):
+        if b < 0:
+            continue
+        q = query[row, 0].to(dtype).reshape(g, r, d)
+        keys = state.keys[b].to(dtype)
+        vals = state.values[b].to(dtype)
+        logits = q @ keys.transpose(-1, -2) / math.sqrt(d)               # [G, R, K]
+        logits = logits.masked_fill((state.positions[b] < 0)[:, None, :], -math.inf)
+        w = torch.nn.functional.pad(logits, (0, 1), value=0.0).softmax(-1)[..., :-1]
+        out[row, 0] = (w @ vals).reshape(h, d)
+    return out.to(query.dtype)
+
+
+def commit_decode(key, value, scores, active, chunk, state: MemoryState, indices=None):
+    """Push one token per row and commit a full chunk, IN PLACE on ``state``
+    (modeling_yanchor.py:291-312; independent_memory.py:90-175).
+
+    key, value ``[B, 1, G, D]``; scores ``[B, 1, G]`` fp32; active ``[B]`` bool.
+    For each active row (state row b = indices[row] or row, skipped if < 0):
+    write (key, value, score) to pending slot ``count[b]``; if that fills the
+    chunk (count + 1 == chunk) replace the committed slots of every group by
+    the Top-K_cap of committed + pending candidates (pending j has position
+    total - count + j) and reset count to 0, else count += 1; total += 1."""
+    bsz = key.shape[0]
+    g_n, cap, d = state.keys.shape[1:]
+    for row, b in enumerate(_rows(bsz, indices)):
+        if b < 0 or not bool(active[row]):
+            continue
+        c = int(state.count[b])
+        state.pending_keys[b, :, c] = key[row, 0]
+        state.pending_values[b, :, c] = value[row, 0]
+        state.pending_scores[b, :, c] = scores[row, 0]
+        if c + 1 == chunk:
+            base = int(state.total[b]) - c
+            for g in range(g_n):
+                pos = state.positions[b, g].long()
+                ref = torch.arange(cap).masked_fill(pos < 0, -1)
+                cand_s = torch.cat((state.scores[b, g], state.pending_scores[b, g, :chunk]))
+                cand_p = torch.cat((pos, base + torch.arange(chunk)))
+                cand_r = torch.cat((ref, cap + torch.arange(chunk)))
+                ss, pp, rr = select_topk_bruteforce(cand_s, cand_p, cand_r, cap)
+                src_k = torch.cat((state.keys[b, g], state.pending_keys[b, g, :chunk]))
+                src_v = torch.cat((state.values[b, g], state.pending_values[b, g, :chunk]))
+                take = torch.tensor([max(x, 0) for x in rr])
+                state.keys[b, g] = src_k[take]
+                state.values[b, g] = src_v[take]
+                state.scores[b, g] = torch.tensor(ss, dtype=torch.float32)
+                state.positions[b, g] = torch.tensor(pp, dtype=torch.int32)
+            state.count[b] = 0
+        else:
+            state.count[b] = c + 1
+        state.total[b] += 1
+    return state

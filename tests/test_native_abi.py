@@ -1,0 +1,64 @@
+"""The C-ABI library loads and exports every entry point include/*.h declares.
+
+Runs without a GPU: it only resolves symbols and checks argument validation
+paths that return before any device work.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from yanchor_amd import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(yh_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert "yh_gdn_recurrent" in names and "yh_last_error" in names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        pytest.fail(f"native library not built at {_native.LIB_PATH} (run `python -m yanchor_amd.build`)")
+    return _native.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"missing exports: {missing}"
+
+
+def test_every_declared_entry_point_has_a_binding():
+    bound = set(_native.SIGNATURES) | {"yh_last_error", "yh_abi_version"}
+    assert set(declared_symbols()) <= bound
+
+
+def test_abi_version(lib):
+    assert lib.yh_abi_version() >= 100
+
+
+def test_invalid_arguments_return_error_without_device_work(lib):
+    # null pointers are rejected before any HIP call
+    rc = lib.yh_gdn_recurrent(None, None, None, None, None, None, None, None, 1, 1, 1, 1, 128, 128, 1,
+                              1.0, 1, 1, 0, 0, None)
+    assert rc == -1
+    assert b"null" in lib.yh_last_error()
+    # a K the kernels do not support is rejected with a message
+    fake = ctypes.c_void_p(16)
+    rc = lib.yh_gdn_recurrent(fake, fake, fake, fake, fake, fake, None, fake, 1, 1, 1, 1, 96, 128, 1,
+                              1.0, 1, 1, 0, 0, None)
+    assert rc == -1 and b"K must be" in lib.yh_last_error()
+    rc = lib.yh_gdn_recurrent(fake, fake, fake, fake, fake, fake, None, fake, 1, 1, 3, 4, 128, 128, 1,
+                              1.0, 1, 1, 0, 0, None)
+    assert rc == -1 and b"multiple" in lib.yh_last_error()

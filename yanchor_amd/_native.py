@@ -1,0 +1,96 @@
+"""ctypes binding of ``lib/libyanchor_amd.so`` (the C ABI in include/yanchor_amd.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch has
+already loaded.  There is no fallback: if the library is missing every kernel
+call raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libyanchor_amd.so"
+
+F32, BF16, F16, I32, I64, U8 = 0, 1, 2, 3, 4, 5
+DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16,
+              torch.int32: I32, torch.int64: I64, torch.uint8: U8, torch.bool: U8}
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> argtypes; every entry point returns int status.
+SIGNATURES: dict[str, list] = {
+    "yh_gdn_recurrent": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                         _f32, _i32, _i32, _i32, _i32, _p],
+}
+
+_lib = None
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load the native library once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"yanchor_amd native library not found at {LIB_PATH}; build it with "
+                "`python -m yanchor_amd.build` (hipcc, gfx950)")
+        handle = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+        handle.yh_last_error.restype = ctypes.c_char_p
+        handle.yh_last_error.argtypes = []
+        handle.yh_abi_version.restype = ctypes.c_int
+        for name, args in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke entry point ``name``; raise NativeError with the library's message on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().yh_last_error().decode(errors="replace")
+        raise NativeError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+def require_device(*tensors: torch.Tensor | None) -> torch.device:
+    """All non-None tensors must live on one ROCm device."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("yanchor_amd kernels take ROCm device tensors "
+                             f"(got a tensor on {t.device})")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no device tensor given")
+    return dev

@@ -1,0 +1,259 @@
+// Gated delta rule, token-recurrent form, fp32 state updated in place.
+//
+// Replaces the FLA fused_recurrent_gated_delta_rule launch with h0 == ht
+// (runtime/model/inference_kernels.py:147-173) and follows the arithmetic of
+// torch_recurrent_gated_delta_rule (transformers wheel,
+// models/qwen3_5/modeling_qwen3_5.py:314-353):
+//   S <- exp(g) S;  kv = S^T k;  delta = beta (v - kv);  S <- S + k delta^T;
+//   o = S^T q
+// with q, k optionally L2-normalised (eps 1e-6 inside rsqrt) and q scaled.
+//
+// Decode (T = 1) is HBM-bound on the state read-modify-write: every state
+// element is read once and written once.  One workgroup owns one
+// (batch row, value head, value tile) and keeps its K x VT slice of the state
+// in registers for all T steps:
+//   * LPR = VT/4 lanes cover one state row with 16-byte accesses, so a wave's
+//     load/store instruction touches whole contiguous rows;
+//   * the K rows are dealt round-robin to RG = NT/LPR row groups;
+//   * the column reductions S^T k and S^T q are xor-shuffle reductions across
+//     the row groups of a wave followed by one LDS exchange across waves;
+//   * o = exp(g) S^T q + delta (k.q) is formed from the same pass, so the
+//     updated state is never re-read.
+// The state loads are issued before anything else so their HBM latency
+// overlaps the q/k normalisation.
+#include "common.h"
+
+#include <stdlib.h>
+
+namespace yh {
+namespace {
+
+struct GdnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  float* state;
+  const int32_t* idx;
+  void* o;
+  int B, T, H, HV, V;
+  int64_t n_rows;
+  float scale;
+  int l2;
+  int g_dt, beta_dt;
+};
+
+__device__ __forceinline__ float4 f4(float x) { return make_float4(x, x, x, x); }
+__device__ __forceinline__ float4 fma4(float4 a, float b, float4 c) {
+  return make_float4(fmaf(a.x, b, c.x), fmaf(a.y, b, c.y), fmaf(a.z, b, c.z), fmaf(a.w, b, c.w));
+}
+
+template <int DT, int K, int VT, int NT>
+__global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
+  constexpr int LPR = VT / 4;
+  constexpr int RG = NT / LPR;
+  constexpr int RPT = K / RG;
+  constexpr int NW = NT / kWave;
+  constexpr int KPL = K / kWave;  // q/k elements per lane in the normalising wave
+  static_assert(RPT * RG == K, "row split");
+  static_assert(LPR <= kWave && kWave % LPR == 0, "lanes per row");
+
+  __shared__ float kn[2][K];
+  __shared__ float qn[2][K];
+  __shared__ float kq_s[2];
+  __shared__ float4 red[NW][2][LPR];
+
+  const int nvt = a.V / VT;
+  const int vt = blockIdx.x % nvt;
+  const int bh = blockIdx.x / nvt;
+  const int hv = bh % a.HV;
+  const int b = bh / a.HV;
+  const int hk = hv / (a.HV / a.H);
+  const int tid = threadIdx.x;
+  const int lc = tid % LPR;
+  const int rg = tid / LPR;
+  const int lane = tid & (kWave - 1);
+  const int wid = tid / kWave;
+  const int col0 = vt * VT + lc * 4;
+
+  int64_t srow = a.idx ? static_cast<int64_t>(a.idx[b]) : static_cast<int64_t>(b);
+  if (srow < 0 || srow >= a.n_rows) {
+    if (rg == 0) {
+      for (int t = 0; t < a.T; ++t) {
+        const int64_t tok = static_cast<int64_t>(b) * a.T + t;
+        store4<DT>(a.o, (tok * a.HV + hv) * a.V + col0, f4(0.f));
+      }
+    }
+    return;
+  }
+
+  float* S = a.state + (srow * a.HV + hv) * static_cast<int64_t>(K) * a.V + col0;
+  float4 s[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+    s[i] = *reinterpret_cast<const float4*>(S + static_cast<int64_t>(rg + i * RG) * a.V);
+
+  for (int t = 0; t < a.T; ++t) {
+    const int buf = t & 1;
+    const int64_t tok = static_cast<int64_t>(b) * a.T + t;
+    if (wid == 0) {
+      const int64_t base = (tok * a.H + hk) * K;
+      float kx[KPL], qx[KPL];
+      float ssk = 0.f, ssq = 0.f, dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        kx[j] = Elem<DT>::ld(static_cast<const typename Elem<DT>::T*>(a.k), base + lane + j * kWave);
+        qx[j] = Elem<DT>::ld(static_cast<const typename Elem<DT>::T*>(a.q), base + lane + j * kWave);
+        ssk = fmaf(kx[j], kx[j], ssk);
+        ssq = fmaf(qx[j], qx[j], ssq);
+        dot = fmaf(kx[j], qx[j], dot);
+      }
+      float rk = 1.f, rq = 1.f;
+      if (a.l2) {
+        rk = rsqrtf(wave_sum(ssk) + 1e-6f);
+        rq = rsqrtf(wave_sum(ssq) + 1e-6f);
+      }
+      rq *= a.scale;
+      dot = wave_sum(dot);
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        kn[buf][lane + j * kWave] = kx[j] * rk;
+        qn[buf][lane + j * kWave] = qx[j] * rq;
+      }
+      if (lane == 0) kq_s[buf] = dot * rk * rq;
+    }
+    const int64_t vh = tok * a.HV + hv;
+    const float4 vv = load4<DT>(a.v, vh * a.V + col0);
+    const float eg = expf(load_any(a.g, vh, a.g_dt));
+    const float bt = load_any(a.beta, vh, a.beta_dt);
+    __syncthreads();
+
+    float4 pk = f4(0.f), pq = f4(0.f);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int r = rg + i * RG;
+      pk = fma4(s[i], kn[buf][r], pk);
+      pq = fma4(s[i], qn[buf][r], pq);
+    }
+#pragma unroll
+    for (int off = LPR; off < kWave; off <<= 1) {
+      pk.x += __shfl_xor(pk.x, off, kWave);
+      pk.y += __shfl_xor(pk.y, off, kWave);
+      pk.z += __shfl_xor(pk.z, off, kWave);
+      pk.w += __shfl_xor(pk.w, off, kWave);
+      pq.x += __shfl_xor(pq.x, off, kWave);
+      pq.y += __shfl_xor(pq.y, off, kWave);
+      pq.z += __shfl_xor(pq.z, off, kWave);
+      pq.w += __shfl_xor(pq.w, off, kWave);
+    }
+    if (lane < LPR) {
+      red[wid][0][lc] = pk;
+      red[wid][1][lc] = pq;
+    }
+    __syncthreads();
+    float4 kv = red[0][0][lc], sq = red[0][1][lc];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+      const float4 x = red[w][0][lc], y = red[w][1][lc];
+      kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
+      sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
+    }
+    const float kq = kq_s[buf];
+    float4 d;
+    d.x = bt * (vv.x - eg * kv.x);
+    d.y = bt * (vv.y - eg * kv.y);
+    d.z = bt * (vv.z - eg * kv.z);
+    d.w = bt * (vv.w - eg * kv.w);
+    if (rg == 0) {
+      float4 o;
+      o.x = fmaf(eg, sq.x, d.x * kq);
+      o.y = fmaf(eg, sq.y, d.y * kq);
+      o.z = fmaf(eg, sq.z, d.z * kq);
+      o.w = fmaf(eg, sq.w, d.w * kq);
+      store4<DT>(a.o, vh * a.V + col0, o);
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const float kr = kn[buf][rg + i * RG];
+      s[i].x = fmaf(s[i].x, eg, kr * d.x);
+      s[i].y = fmaf(s[i].y, eg, kr * d.y);
+      s[i].z = fmaf(s[i].z, eg, kr * d.z);
+      s[i].w = fmaf(s[i].w, eg, kr * d.w);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+    *reinterpret_cast<float4*>(S + static_cast<int64_t>(rg + i * RG) * a.V) = s[i];
+}
+
+template <int K, int VT, int NT>
+int launch_tile(int dt, const GdnArgs& a, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.HV * (a.V / VT)));
+  switch (dt) {
+    case YH_F32: hipLaunchKernelGGL((gdn_recurrent_kernel<YH_F32, K, VT, NT>), grid, dim3(NT), 0, st, a); break;
+    case YH_BF16: hipLaunchKernelGGL((gdn_recurrent_kernel<YH_BF16, K, VT, NT>), grid, dim3(NT), 0, st, a); break;
+    case YH_F16: hipLaunchKernelGGL((gdn_recurrent_kernel<YH_F16, K, VT, NT>), grid, dim3(NT), 0, st, a); break;
+    default: set_error("gdn_recurrent: unsupported q/k/v dtype %d", dt); return YH_ERR_INVALID;
+  }
+  YH_CHECK_LAUNCH("gdn_recurrent");
+  return YH_OK;
+}
+
+// Tile choice.  YH_GDN_TILE="VT:NT" overrides the default (tuning sweeps);
+// it is read on every call so a process can sweep tiles.
+void pick_tile(int K, int V, int* vt, int* nt) {
+  const char* e = getenv("YH_GDN_TILE");
+  int x = 0, y = 0;
+  if (e && sscanf(e, "%d:%d", &x, &y) == 2 && x > 0 && V % x == 0) { *vt = x; *nt = y; return; }
+  if (K == 128) { *vt = 64; *nt = 256; }
+  else { *vt = 64; *nt = 128; }
+}
+
+}  // namespace
+}  // namespace yh
+
+extern "C" int yh_gdn_recurrent(const void* q, const void* k, const void* v, const void* g,
+                                const void* beta, float* state, const int32_t* state_indices,
+                                void* o, int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K,
+                                int64_t V, int64_t n_state_rows, float scale, int use_qk_l2norm,
+                                int qkv_dtype, int g_dtype, int beta_dtype, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(q && k && v && g && beta && state && o, "gdn_recurrent: null tensor pointer");
+  YH_CHECK_ARG(B >= 0 && T >= 0 && H > 0 && HV > 0, "gdn_recurrent: bad sizes B=%lld T=%lld H=%lld HV=%lld",
+               (long long)B, (long long)T, (long long)H, (long long)HV);
+  YH_CHECK_ARG(HV % H == 0, "gdn_recurrent: HV (%lld) must be a multiple of H (%lld)", (long long)HV, (long long)H);
+  YH_CHECK_ARG(K == 64 || K == 128, "gdn_recurrent: K must be 64 or 128 (got %lld)", (long long)K);
+  YH_CHECK_ARG(V == 64 || V == 128, "gdn_recurrent: V must be 64 or 128 (got %lld)", (long long)V);
+  YH_CHECK_ARG(is_float_dtype(qkv_dtype) && is_float_dtype(g_dtype) && is_float_dtype(beta_dtype),
+               "gdn_recurrent: unsupported dtype codes %d/%d/%d", qkv_dtype, g_dtype, beta_dtype);
+  YH_CHECK_ARG(state_indices != nullptr || n_state_rows >= B,
+               "gdn_recurrent: state has %lld rows for batch %lld", (long long)n_state_rows, (long long)B);
+  YH_CHECK_ARG(B * HV * 2 < (1LL << 31), "gdn_recurrent: grid too large");
+  {
+    // the kernel moves 16-byte state vectors and 4-element q/k/v/o groups
+    const uintptr_t vec = qkv_dtype == YH_F32 ? 15 : 7;
+    YH_CHECK_ARG((reinterpret_cast<uintptr_t>(state) & 15) == 0, "gdn_recurrent: state must be 16-byte aligned");
+    YH_CHECK_ARG((reinterpret_cast<uintptr_t>(v) & vec) == 0 && (reinterpret_cast<uintptr_t>(o) & vec) == 0,
+                 "gdn_recurrent: v and o must be aligned to 4 elements");
+  }
+  if (B == 0 || T == 0) return YH_OK;
+  GdnArgs a{q, k, v, g, beta, state, state_indices, o,
+            (int)B, (int)T, (int)H, (int)HV, (int)V, n_state_rows, scale, use_qk_l2norm ? 1 : 0,
+            g_dtype, beta_dtype};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int vt = 0, nt = 0;
+  pick_tile((int)K, (int)V, &vt, &nt);
+  if (K == 128) {
+    if (vt == 128 && nt == 256) return launch_tile<128, 128, 256>(qkv_dtype, a, st);
+    if (vt == 64 && nt == 256) return launch_tile<128, 64, 256>(qkv_dtype, a, st);
+    if (vt == 64 && nt == 128) return launch_tile<128, 64, 128>(qkv_dtype, a, st);
+    if (vt == 32 && nt == 128) return launch_tile<128, 32, 128>(qkv_dtype, a, st);
+    if (vt == 32 && nt == 256) return launch_tile<128, 32, 256>(qkv_dtype, a, st);
+    return launch_tile<128, 64, 256>(qkv_dtype, a, st);
+  }
+  if (vt == 64 && nt == 64) return launch_tile<64, 64, 64>(qkv_dtype, a, st);
+  if (vt == 32 && nt == 64) return launch_tile<64, 32, 64>(qkv_dtype, a, st);
+  return launch_tile<64, 64, 128>(qkv_dtype, a, st);
+}

@@ -1,0 +1,84 @@
+"""Gated DeltaNet kernels behind the reference's call signatures.
+
+``recurrent_gated_delta_rule`` is the drop-in for the function the GDN layer
+binds as ``module.recurrent_gated_delta_rule`` (reference modeling_yanchor.py:
+401-407; called at transformers wheel models/qwen3_5/modeling_qwen3_5.py:
+508-517 and runtime/model/inference_kernels.py:716).  Like the reference's
+in-place FLA launch (runtime/model/inference_kernels.py:147-173) it updates
+``initial_state`` in place and returns that same tensor, so the cache's alias
+check (modeling_yanchor.py:702-710) skips the copy.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+
+def _contig(x: torch.Tensor) -> torch.Tensor:
+    return x if x.is_contiguous() else x.contiguous()
+
+
+def recurrent_gated_delta_rule(query, key, value, g=None, beta=None, initial_state=None,
+                               output_final_state=True, use_qk_l2norm_in_kernel=True,
+                               scale=None, state_indices=None, inplace=True, **unused):
+    """Token-recurrent gated delta rule on the GPU.
+
+    query, key ``[B, T, H, K]``; value ``[B, T, HV, V]``; g, beta ``[B, T, HV]``;
+    initial_state float32 ``[N, HV, K, V]`` (N >= B, or any N with
+    ``state_indices``).  ``state_indices`` (int ``[B]``, -1 = skip) selects the
+    state row of each batch row, the slot indirection of the vLLM/SGLang
+    adapters.  Returns ``(o [B, T, HV, V], state)``; ``state`` is
+    ``initial_state`` itself (updated in place) unless ``inplace=False``, or a
+    new zero-initialised tensor when ``initial_state`` is None.  With
+    ``output_final_state=False`` the second element is None.
+    """
+    if g is None or beta is None:
+        raise ValueError("recurrent_gated_delta_rule needs g and beta")
+    if query.ndim != 4 or key.shape != query.shape or value.ndim != 4:
+        raise ValueError("query/key must be [B, T, H, K] and value [B, T, HV, V]")
+    b, t, h, kd = key.shape
+    hv, vd = value.shape[2], value.shape[3]
+    if value.shape[:2] != (b, t) or g.shape != (b, t, hv) or beta.shape != (b, t, hv):
+        raise ValueError("value/g/beta shapes do not match query/key")
+    if query.dtype != key.dtype or value.dtype != key.dtype:
+        raise ValueError("query, key and value must share one dtype")
+    dev = N.require_device(query, key, value, g, beta, initial_state, state_indices)
+    if initial_state is None:
+        if state_indices is not None:
+            raise ValueError("state_indices needs an initial_state pool")
+        state = torch.zeros(b, hv, kd, vd, device=dev, dtype=torch.float32)
+    else:
+        if initial_state.dtype != torch.float32:
+            raise ValueError("the recurrent state must be float32")
+        if initial_state.ndim != 4 or tuple(initial_state.shape[1:]) != (hv, kd, vd):
+            raise ValueError(f"initial_state must be [N, {hv}, {kd}, {vd}]")
+        if not initial_state.is_contiguous():
+            raise ValueError("initial_state must be contiguous (it is updated in place)")
+        state = initial_state if inplace else initial_state.clone()
+    idx = None
+    if state_indices is not None:
+        if state_indices.shape != (b,):
+            raise ValueError("state_indices must be [B]")
+        idx = _contig(state_indices.to(torch.int32))
+    elif state.shape[0] < b:
+        raise ValueError("state pool has fewer rows than the batch")
+    q, k, v, g_, be = (_contig(x) for x in (query, key, value, g, beta))
+    o = torch.empty(b, t, hv, vd, device=dev, dtype=value.dtype)
+    sc = float(kd ** -0.5 if scale is None else scale)
+    N.call("yh_gdn_recurrent", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_.data_ptr(),
+           be.data_ptr(), state.data_ptr(), N.ptr(idx), o.data_ptr(), b, t, h, hv, kd, vd,
+           state.shape[0], sc, int(bool(use_qk_l2norm_in_kernel)), N.code(q), N.code(g_),
+           N.code(be), N.stream_of(q))
+    return o, (state if output_final_state else None)
+
+
+def fused_recurrent_gated_delta_rule(q, k, v, g=None, beta=None, scale=None, initial_state=None,
+                                     output_final_state=False, use_qk_l2norm_in_kernel=False,
+                                     **kw):
+    """FLA-style keyword order (fla.ops.gated_delta_rule.fused_recurrent), the
+    name the reference binds at modeling_yanchor.py:404."""
+    return recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=initial_state,
+                                      output_final_state=output_final_state,
+                                      use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+                                      scale=scale, inplace=bool(output_final_state), **kw)
