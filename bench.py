@@ -5,12 +5,13 @@
 Prints one JSON line.  Workloads:
 
 * ``gdn_decode`` (default): one decode step of the gated-delta state update on
-  the decode configuration -- 64 live sequences picked from a 96-slot pool,
-  HV = 32 heads, dk = dv = 128, fp32 state ~ N(0, 0.02) updated in place,
-  bf16 q/k/v, fp32 g/beta.  Steps cycle over 4 independent layer state pools
-  (4 x 192 MiB) so no launch finds its state in the 256 MB Infinity Cache
+  the decode configuration -- 64 live sequences, HV = 32 heads,
+  dk = dv = 128, fp32 state [64, 32, 128, 128] ~ N(0, 0.02) updated in place,
+  bf16 q/k/v, fp32 g/beta.  Steps cycle over 4 independent layer states
+  (4 x 128 MiB) so no launch finds its state in the 256 MB Infinity Cache
   left behind by the previous one.  value = decode tokens/s of that layer step
-  (64 tokens per step).
+  (64 tokens per step).  The same step through a 96-row slot pool with
+  state_indices (the vLLM-style indirection) is reported as ``pooled_slots``.
 
 Timing: W untimed steps, then K steps between two stream synchronisations,
 with HIP events (torch.cuda.Event on the stream the kernels are launched on)
@@ -32,6 +33,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of gdn_recurrent_kernel on the decode workload, from
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled by the same
+# counters on a copy kernel of known size (FETCH x 2.0, WRITE x 1.0).
+TRAFFIC_GDN_DECODE = None
 METRIC = "decode tokens/s at B=128 on 1 GPU; state-update HBM GB/s as % of peak"
 
 
@@ -53,25 +58,10 @@ def cpu_threads() -> int:
     return max(1, min(16, n))
 
 
-def bench_gdn_decode(steps: int, warmup: int, cpu: bool) -> dict:
+def _time_steps(step, steps, warmup):
+    """W untimed steps, then K timed steps between stream synchronisations.
+    Returns (wall ms per step, event ms per step on the launch stream)."""
     import torch
-    from yanchor_amd import gdn, workloads
-
-    dev = torch.device("cuda:0")
-    b, h, hv, kd, vd, pool, layers = 64, 32, 32, 128, 128, 96, 4
-    xs = []
-    for layer in range(layers):
-        x = workloads.gdn_inputs(b, 1, h, hv, kd, vd, dtype=torch.bfloat16,
-                                 seed=workloads.SEED0 + 1 + 1000 * layer, state_std=0.02,
-                                 pool_rows=pool).to(dev)
-        xs.append(x)
-    torch.cuda.synchronize()
-
-    def step(i):
-        x = xs[i % layers]
-        gdn.recurrent_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta, initial_state=x.state,
-                                       state_indices=x.state_indices)
-
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -84,23 +74,64 @@ def bench_gdn_decode(steps: int, warmup: int, cpu: bool) -> dict:
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = ev0.elapsed_time(ev1) / steps
-    ms_per_step = wall * 1e3 / steps
-    nbytes = gdn_state_bytes(b, h, hv, kd, vd, 2, 4, True)
+    return wall * 1e3 / steps, ev0.elapsed_time(ev1) / steps
+
+
+def bench_gdn_decode(steps: int, warmup: int, cpu: bool) -> dict:
+    """Decode state update on the [64, 32, 128, 128] fp32 state (rows indexed
+    densely, like the reference's in-place decode launch), plus the same step
+    through a 96-slot pool with state_indices as a secondary figure."""
+    import torch
+    from yanchor_amd import gdn, workloads
+
+    dev = torch.device("cuda:0")
+    b, h, hv, kd, vd, layers = 64, 32, 32, 128, 128, 4
+
+    def make(pool):
+        xs = []
+        for layer in range(layers):
+            x = workloads.gdn_inputs(b, 1, h, hv, kd, vd, dtype=torch.bfloat16,
+                                     seed=workloads.SEED0 + 1 + 1000 * layer, state_std=0.02,
+                                     pool_rows=pool).to(dev)
+            if pool is None:
+                x.state_indices = None
+            xs.append(x)
+        return xs
+
+    def stepper(xs):
+        def step(i):
+            x = xs[i % layers]
+            gdn.recurrent_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta,
+                                           initial_state=x.state, state_indices=x.state_indices)
+        return step
+
+    xs = make(None)
+    torch.cuda.synchronize()
+    ms_per_step, kernel_ms = _time_steps(stepper(xs), steps, warmup)
+    del xs
+    pooled = make(96)
+    _, pooled_ms = _time_steps(stepper(pooled), steps, warmup)
+    del pooled
+    torch.cuda.empty_cache()
+    nbytes = gdn_state_bytes(b, h, hv, kd, vd, 2, 4, False)
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    pooled_gbs = gdn_state_bytes(b, h, hv, kd, vd, 2, 4, True) / (pooled_ms * 1e-3) / 1e9
     res = {
         "metric": METRIC,
         "value": b / (ms_per_step * 1e-3),
         "unit": "tokens/s",
         "ms_per_step": ms_per_step,
         "dtype": "f32",
-        "config": {"workload": "gdn_decode_state_update: one layer step, 64 live of 96 slots, "
-                               "HV=32, dk=dv=128, fp32 state, bf16 qkv, 4 rotating layer pools",
+        "config": {"workload": "gdn_decode_state_update: one layer decode step, state fp32 "
+                               "[64, 32, 128, 128] in place, bf16 q/k/v, fp32 g/beta, "
+                               "4 rotating layer states",
                    "global_batch": b, "seq_len": 1, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_GDN_DECODE,
                      "kernel": "gdn_recurrent_kernel", "bytes_per_launch": nbytes,
                      "avg_launch_us": kernel_ms * 1e3},
+        "pooled_slots": {"pool_rows": 96, "avg_launch_us": pooled_ms * 1e3,
+                         "achieved_GBs": pooled_gbs, "frac": pooled_gbs / HBM_PEAK_GBS},
     }
     if cpu:
         res["cpu_baseline"] = cpu_gdn_decode(b, h, hv, kd, vd)
@@ -155,6 +186,8 @@ def main() -> int:
             "config": res["config"], "roofline": res["roofline"]}
     if "cpu_baseline" in res:
         line["cpu_baseline"] = res["cpu_baseline"]
+    if "pooled_slots" in res:
+        line["pooled_slots"] = res["pooled_slots"]
     print(json.dumps(line), flush=True)
     return 0
 

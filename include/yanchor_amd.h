@@ -64,6 +64,57 @@ int yh_gdn_recurrent(const void* q, const void* k, const void* v, const void* g,
                      int64_t V, int64_t n_state_rows, float scale, int use_qk_l2norm,
                      int qkv_dtype, int g_dtype, int beta_dtype, yh_stream_t stream);
 
+/*
+ * Anchor memory, decode read of the committed slots.
+ *
+ * Replaces committed_gqa (_read_parts + _read_reduce) in
+ * runtime/model/independent_memory.py:47-88, 177-188 and the torch branch of
+ * IndependentGQAMemory._decode, modeling_yanchor.py:283-290.
+ *
+ *   query      [B, H, D]   (dtype)     H = G * R, head h reads group h / R
+ *   keys, values [NB, G, capacity, D] (dtype)
+ *   positions  [NB, G, capacity] int32, slot live iff >= 0
+ *   indices    NULL or int32 [B]: row b reads state row indices[b]; < 0 reads
+ *              nothing (output 0)
+ *   out        [B, H, D]   (dtype)
+ * Per head: out = softmax([q.K^T / sqrt(D) over live slots, 0]) . [V; 0] (a
+ * sink logit of 0 with value 0), accumulated in fp32.
+ * Requirements: D in {64, 128}; H / G in {1, 2, 4}; capacity a multiple of 64,
+ * at most 1024; 16-byte aligned query/keys/values.
+ */
+int yh_anchor_read(const void* query, const void* keys, const void* values, const int32_t* positions,
+                   const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t capacity,
+                   int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream);
+
+/*
+ * Anchor memory, decode push and Top-K commit, IN PLACE on the memory state.
+ *
+ * Replaces commit_decode (_push_select, _gather_commit, _write_commit,
+ * _advance) in runtime/model/independent_memory.py:90-175, 190-201 and the
+ * torch branch modeling_yanchor.py:291-312.
+ *
+ *   key, value  [B, G, D] (dtype);  score [B, G] float32;  active uint8/bool [B]
+ *   indices     NULL or int32 [B] (row -> state row; < 0 skips the row)
+ *   keys, values [NB, G, capacity, D]; scores float [NB, G, capacity];
+ *   positions int32 [NB, G, capacity]; pending_keys, pending_values
+ *   [NB, G, pending_capacity, D]; pending_scores float [NB, G, pending_capacity];
+ *   count, total int64 [NB]
+ * For each active row with state row b and c = count[b]: (key, value, score)
+ * goes to pending slot c; if c + 1 == chunk, every group keeps the best
+ * `capacity` of its capacity committed + chunk pending candidates, ordered by
+ * score descending, then position ascending (empty slots last), then candidate
+ * index (committed 0..capacity-1, then pending 0..chunk-1); pending j has
+ * position total[b] - c + j.  Then count = (c + 1) mod chunk and total += 1.
+ * Requirements: 1 <= chunk <= pending_capacity; capacity + chunk <= 2048;
+ * D * element size a multiple of 16 and capacity * D * element size <= 128 KiB;
+ * no state row may appear twice in one call.
+ */
+int yh_anchor_commit(const void* key, const void* value, const float* score, const uint8_t* active,
+                     const int32_t* indices, void* keys, void* values, float* scores, int32_t* positions,
+                     void* pending_keys, void* pending_values, float* pending_scores, int64_t* count,
+                     int64_t* total, int64_t B, int64_t G, int64_t capacity, int64_t pending_capacity,
+                     int64_t chunk, int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,148 @@
+"""Pins for oracle.anchor.
+
+* the tensor select_topk / merge_topk (the reference's two stable sorts) agree
+  with the brute-force sorted() selection on random candidates with forced
+  score ties, -0.0 vs +0.0, -inf scores and dead slots;
+* a selection that drops the position tie-break (a plausible mistake) is
+  caught on a crafted tie;
+* the committed read equals an independent formulation -- SDPA over
+  [K; 0], [V; 0] with mask [live; True], the reference's own _gqa_tile
+  construction (modeling_yanchor.py:22-32) -- and closed forms for zero and one
+  live slot;
+* exclusive_prefix_topk's definition form satisfies its recursion
+  prefix[j+1] = merge(prefix[j], block j).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import anchor
+from oracle.anchor import MemoryState
+from yanchor_amd import workloads
+
+
+def _cands(n, seed, ties=True):
+    g = torch.Generator().manual_seed(seed)
+    s = torch.randn(n, generator=g)
+    if ties:
+        s = (s * 2).round() / 2  # many exact ties
+    s[torch.rand(n, generator=g) < 0.1] = -math.inf
+    z = torch.rand(n, generator=g) < 0.1
+    s[z] = torch.where(torch.rand(int(z.sum()), generator=g) < 0.5, torch.tensor(0.0), torch.tensor(-0.0))
+    p = torch.randperm(4 * n, generator=g)[:n].long()
+    r = torch.arange(n)
+    r[torch.rand(n, generator=g) < 0.2] = -1
+    return s, p, r
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("cap", [5, 32, 64])
+def test_tensor_select_matches_bruteforce(seed, cap):
+    s, p, r = _cands(96, seed)
+    ts, tp, tr = anchor.select_topk(s[None], p[None], r[None], cap)
+    bs, bp, br = anchor.select_topk_bruteforce(s, p, r, cap)
+    assert tr[0].tolist() == br and tp[0].tolist() == bp
+    assert torch.equal(ts[0], torch.tensor(bs, dtype=ts.dtype))
+
+
+def test_merge_pads_when_short():
+    s, p, r = _cands(3, 1)
+    out = anchor.merge_topk((s[None, :1], p[None, :1], r[None, :1]), (s[None, 1:], p[None, 1:], r[None, 1:]), 6)
+    assert out[0].shape == (1, 6) and out[2][0, 3:].tolist() == [-1, -1, -1]
+    assert out[1][0, 3:].tolist() == [-1, -1, -1]
+
+
+def test_position_tiebreak_matters():
+    """Equal scores: the earlier position wins, not the earlier index."""
+    s = torch.tensor([1.0, 1.0, 1.0])
+    p = torch.tensor([30, 10, 20])
+    r = torch.tensor([0, 1, 2])
+    _, _, ref = anchor.select_topk_bruteforce(s, p, r, 2)
+    assert ref == [1, 2]
+    wrong = sorted(range(3), key=lambda i: (-s[i].item(), i))[:2]  # index tie-break only
+    assert wrong != ref
+
+
+def test_negative_zero_ties_with_zero():
+    s = torch.tensor([-0.0, 0.0])
+    p = torch.tensor([5, 3])
+    r = torch.tensor([0, 1])
+    _, _, ref = anchor.select_topk_bruteforce(s, p, r, 1)
+    assert ref == [1]  # tie on score (-0 == +0), position 3 first
+
+
+def _sdpa_read(query, st):
+    """The reference's _gqa_tile construction with torch SDPA (float64)."""
+    b, _, h, d = query.shape
+    g, cap = st.keys.shape[1:3]
+    key = torch.nn.functional.pad(st.keys.double(), (0, 0, 0, 1))      # zero sink key
+    val = torch.nn.functional.pad(st.values.double(), (0, 0, 0, 1))    # zero sink value
+    mask = torch.nn.functional.pad(st.positions >= 0, (0, 1), value=True)
+    q = query.double().reshape(b, g, h // g, d)
+    out = torch.nn.functional.scaled_dot_product_attention(q, key, val, attn_mask=mask[:, :, None, :])
+    return out.reshape(b, 1, h, d)
+
+
+@pytest.mark.parametrize("r", [1, 2])
+def test_read_matches_sdpa_with_sink(r):
+    st = workloads.anchor_state(3, 2, 64, 8, 16, dtype=torch.float64, seed=4)
+    q = workloads.anchor_query(3, 2 * r, 16, dtype=torch.float64, seed=5)
+    got = anchor.committed_read(q, st)
+    assert torch.allclose(got, _sdpa_read(q, st), atol=1e-12)
+
+
+def test_read_closed_forms():
+    st = workloads.anchor_state(1, 1, 64, 8, 8, dtype=torch.float64, seed=6)
+    q = workloads.anchor_query(1, 1, 8, dtype=torch.float64, seed=7)
+    st.positions.fill_(-1)
+    assert torch.count_nonzero(anchor.committed_read(q, st)) == 0   # only the sink
+    st.positions[0, 0, 17] = 3
+    logit = (q[0, 0, 0] @ st.keys[0, 0, 17]).item() / math.sqrt(8)
+    p = math.exp(logit) / (math.exp(logit) + 1.0)
+    assert torch.allclose(anchor.committed_read(q, st)[0, 0, 0], p * st.values[0, 0, 17], atol=1e-12)
+
+
+def test_read_skips_negative_index_rows():
+    st = workloads.anchor_state(2, 1, 64, 8, 8, dtype=torch.float64, seed=8)
+    q = workloads.anchor_query(2, 1, 8, dtype=torch.float64, seed=9)
+    out = anchor.committed_read(q, st, torch.tensor([1, -1]))
+    assert torch.count_nonzero(out[1]) == 0
+    assert torch.allclose(out[0], anchor.committed_read(q[:1], MemoryState(
+        *(getattr(st, f)[1:2] for f in MemoryState.__dataclass_fields__)))[0])
+
+
+def test_commit_keeps_topk_of_union():
+    """After a full chunk the committed slots are exactly the Top-K of
+    committed + pending by (score desc, position, index), with K/V rows moved
+    along; merge_topk (the reference's tensor path) selects the same."""
+    cap, c, d = 16, 4, 8
+    st = workloads.anchor_state(1, 2, cap, c, d, dtype=torch.float32, seed=10, fill_pending=c - 1, total0=100)
+    before = MemoryState(*(getattr(st, f).clone() for f in MemoryState.__dataclass_fields__))
+    g = torch.Generator().manual_seed(11)
+    key, val = torch.randn(1, 1, 2, d, generator=g), torch.randn(1, 1, 2, d, generator=g)
+    sc = torch.randn(1, 1, 2, generator=g)
+    anchor.commit_decode(key, val, sc, torch.tensor([True]), c, st)
+    assert st.count.item() == 0 and st.total.item() == 101
+    for grp in range(2):
+        cs = torch.cat((before.scores[0, grp], before.pending_scores[0, grp, :c - 1], sc[0, 0, grp:grp + 1]))
+        cp = torch.cat((before.positions[0, grp].long(), 100 - (c - 1) + torch.arange(c)))
+        cr = torch.cat((torch.arange(cap).masked_fill(before.positions[0, grp] < 0, -1), cap + torch.arange(c)))
+        ts, tp, tr = anchor.select_topk(cs[None], cp[None], cr[None], cap)
+        assert st.positions[0, grp].tolist() == tp[0].tolist()
+        assert torch.equal(st.scores[0, grp], ts[0])
+        src = torch.cat((before.keys[0, grp], before.pending_keys[0, grp, :c - 1], key[0, 0, grp:grp + 1]))
+        assert torch.equal(st.keys[0, grp], src[tr[0].clamp_min(0)])
+
+
+def test_prefix_topk_recursion():
+    b, nb, g, c, cap = 1, 5, 2, 4, 6
+    gen = torch.Generator().manual_seed(12)
+    s = (torch.randn(b, nb, g, c, generator=gen) * 2).round()
+    p = torch.arange(nb * c).reshape(1, nb, 1, c).expand(b, nb, g, c).clone()
+    r = p.clone()
+    ps, pp, pr = anchor.exclusive_prefix_topk(s, p, r, cap)
+    assert (pr[:, 0] == -1).all()
+    for j in range(nb):
+        nxt = anchor.merge_topk((ps[:, j], pp[:, j], pr[:, j]), (s[:, j], p[:, j], r[:, j]), cap)
+        assert torch.equal(nxt[2], pr[:, j + 1]) and torch.equal(nxt[0], ps[:, j + 1])

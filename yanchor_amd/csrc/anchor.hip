@@ -1,0 +1,470 @@
+// Fixed-slot anchor memory: decode read and decode push / Top-K commit.
+//
+// State layout (IndependentMemoryState, reference modeling_yanchor.py:80-120):
+//   keys, values      [NB, G, KC, D]   (bf16 / fp16 / fp32)
+//   scores            [NB, G, KC]      fp32, -inf = empty
+//   positions         [NB, G, KC]      int32, -1 = empty (the validity mask)
+//   pending_keys/vals [NB, G, PC, D]
+//   pending_scores    [NB, G, PC]      fp32
+//   count, total      [NB]             int64
+//
+// anchor_read_kernel   replaces _read_parts + _read_reduce / committed_gqa
+//                      (runtime/model/independent_memory.py:47-88, 177-188) and
+//                      the torch branch modeling_yanchor.py:283-290.
+// anchor_commit_kernel replaces _push_select + _gather_commit + _write_commit
+//                      (independent_memory.py:90-164) and modeling_yanchor.py:
+//                      291-310.
+// anchor_advance_kernel replaces _advance (independent_memory.py:166-175).
+#include "common.h"
+
+namespace yh {
+namespace {
+
+constexpr int kReadThreads = 256;
+constexpr int kReadWaves = kReadThreads / kWave;
+constexpr int kMaxCap = 1024;
+
+struct ReadArgs {
+  const void* q;          // [B, H, D]
+  const void* keys;       // [NB, G, KC, D]
+  const void* values;
+  const int32_t* pos;     // [NB, G, KC]
+  const int32_t* idx;     // [B] or null
+  void* out;              // [B, H, D]
+  int B, G, KC;
+  int64_t n_rows;
+  float scale;
+};
+
+// 8 consecutive elements of a bf16/fp16/fp32 row as floats (16 B for 2-byte
+// types, 2 x 16 B for fp32).
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, int64_t i, float* f) {
+  if constexpr (DT == YH_F32) {
+    const float4 a = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i)[0];
+    const float4 b = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    const uint4 w = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i)[0];
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == YH_BF16) {
+        f[2 * j] = __uint_as_float(u[j] << 16);
+        f[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+      } else {
+        f[2 * j] = f16_to_f32(u[j] & 0xffff);
+        f[2 * j + 1] = f16_to_f32(u[j] >> 16);
+      }
+    }
+  }
+}
+
+// One workgroup per (batch row, group).  Each wave takes 64-slot blocks;
+// within a block, LPR = D/8 lanes cover one key row (8 elements each) and a
+// wave instruction covers RPI = 64/LPR rows, so NI = LPR instructions cover the
+// block.  The LPR-lane dot products are finished with a reduce-scatter
+// butterfly that leaves lane (s, rr) holding the logit of slot s*RPI + rr.
+template <int DT, int D, int R>
+__global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
+  constexpr int LPR = D / 8;
+  constexpr int RPI = kWave / LPR;
+  constexpr int NI = LPR;
+  static_assert(NI * RPI == 64, "64-slot blocks");
+
+  __shared__ float prob[R][kMaxCap];
+  __shared__ float wmax[kReadWaves][R];
+  __shared__ float wsum[kReadWaves][R];
+  __shared__ float accs[kReadWaves][R][D];
+
+  const int bg = blockIdx.x;
+  const int row = bg / a.G, g = bg % a.G;
+  const int H = a.G * R;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int s = lane % LPR, rr = lane / LPR;
+  const int64_t b = a.idx ? static_cast<int64_t>(a.idx[row]) : static_cast<int64_t>(row);
+  const int64_t qbase = (static_cast<int64_t>(row) * H + static_cast<int64_t>(g) * R) * D;
+  if (b < 0 || b >= a.n_rows) {
+    for (int e = tid; e < R * D; e += kReadThreads) store_any(a.out, qbase + e, DT, 0.f);
+    return;
+  }
+  const int64_t slot0 = (b * a.G + g) * static_cast<int64_t>(a.KC);  // first slot of (b, g)
+  const int32_t* pos = a.pos + slot0;
+
+  float qf[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    load8<DT>(a.q, qbase + static_cast<int64_t>(r) * D + s * 8, qf[r]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qf[r][j] *= a.scale;
+  }
+
+  const int nblk = a.KC / 64;
+  // ---- logits ----
+  for (int blk = wid; blk < nblk; blk += kReadWaves) {
+    float part[R][NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int n = blk * 64 + i * RPI + rr;
+      float kf[8];
+      if (pos[n] >= 0) {
+        load8<DT>(a.keys, (slot0 + n) * D + s * 8, kf);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kf[j] = 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = fmaf(qf[r][j], kf[j], acc);
+        part[r][i] = acc;
+      }
+    }
+    // reduce-scatter over the LPR lanes of a row group
+#pragma unroll
+    for (int m = LPR / 2, h = NI / 2; m >= 1; m >>= 1, h >>= 1) {
+      const bool up = (s & m) != 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int j = 0; j < h; ++j) {
+          const float send = up ? part[r][j] : part[r][j + h];
+          const float keep = up ? part[r][j + h] : part[r][j];
+          part[r][j] = keep + __shfl_xor(send, m, kWave);
+        }
+      }
+    }
+    const int n = blk * 64 + s * RPI + rr;
+    const bool valid = pos[n] >= 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) prob[r][n] = valid ? part[r][0] : -INFINITY;
+  }
+  __syncthreads();
+
+  // ---- softmax over [logits, 0] (the sink logit 0 carries value 0) ----
+  float m[R], den[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float x = 0.f;  // the sink is part of the max
+    for (int n = tid; n < a.KC; n += kReadThreads) x = fmaxf(x, prob[r][n]);
+    x = wave_max(x);
+    if (lane == 0) wmax[wid][r] = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float x = wmax[0][r];
+#pragma unroll
+    for (int w = 1; w < kReadWaves; ++w) x = fmaxf(x, wmax[w][r]);
+    m[r] = x;
+    float sum = 0.f;
+    for (int n = tid; n < a.KC; n += kReadThreads) {
+      const float p = __expf(prob[r][n] - x);
+      prob[r][n] = p;
+      sum += p;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) wsum[wid][r] = sum;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float sum = __expf(-m[r]);
+#pragma unroll
+    for (int w = 0; w < kReadWaves; ++w) sum += wsum[w][r];
+    den[r] = sum;
+  }
+
+  // ---- P . V ----
+  float acc[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[r][j] = 0.f;
+  for (int blk = wid; blk < nblk; blk += kReadWaves) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int n = blk * 64 + i * RPI + rr;
+      if (pos[n] >= 0) {
+        float vf[8];
+        load8<DT>(a.values, (slot0 + n) * D + s * 8, vf);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float p = prob[r][n];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(p, vf[j], acc[r][j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = LPR; off < kWave; off <<= 1)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[r][j] += __shfl_xor(acc[r][j], off, kWave);
+  if (rr == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) accs[wid][r][s * 8 + j] = acc[r][j];
+  }
+  __syncthreads();
+  for (int e = tid; e < R * D; e += kReadThreads) {
+    const int r = e / D, d = e % D;
+    float x = 0.f;
+#pragma unroll
+    for (int w = 0; w < kReadWaves; ++w) x += accs[w][r][d];
+    store_any(a.out, qbase + e, DT, x / den[r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+struct CommitArgs {
+  const void* key;          // [B, G, D]
+  const void* value;        // [B, G, D]
+  const float* score;       // [B, G]
+  const uint8_t* active;    // [B]
+  const int32_t* idx;       // [B] or null
+  void* keys;               // [NB, G, KC, D]
+  void* values;
+  float* scores;            // [NB, G, KC]
+  int32_t* pos;             // [NB, G, KC]
+  void* pkeys;              // [NB, G, PC, D]
+  void* pvalues;
+  float* pscores;           // [NB, G, PC]
+  const int64_t* count;     // [NB]
+  const int64_t* total;     // [NB]
+  int B, G, KC, PC, C, D, esize;
+  int64_t n_rows;
+};
+
+constexpr int kCommitThreads = 512;
+constexpr int kMaxCand = 2048;
+constexpr int kMaxPieces = 16;  // 16-byte pieces per thread per tensor: 128 KiB per (row, group)
+
+// Order-preserving 32-bit key of an fp32 score (bigger score -> bigger key);
+// -0.0 is mapped to +0.0 first so the two compare equal.
+__device__ __forceinline__ uint32_t score_key(float x) {
+  if (x == 0.f) x = 0.f;
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u ^ 0x80000000u);
+}
+
+// Copy `n` bytes (multiple of 16) between two 16-byte aligned rows.
+__device__ __forceinline__ void copy_row16(void* dst, const void* src, int n, int lane, int lanes) {
+  const uint4* s = static_cast<const uint4*>(src);
+  uint4* d = static_cast<uint4*>(dst);
+  for (int i = lane; i < n / 16; i += lanes) d[i] = s[i];
+}
+
+// One workgroup per (batch row, group).  Push the token into pending[count];
+// on a full chunk rank the KC + C candidates by counting (score desc, position
+// asc with invalid last, candidate index asc) and rewrite the committed slots.
+// count / total are only read here (every group of a row reads them); the
+// advance kernel updates them afterwards.
+__global__ void __launch_bounds__(kCommitThreads) anchor_commit_kernel(CommitArgs a) {
+  __shared__ uint64_t ckey[kMaxCand];   // (~score_key << 32) | position key
+  __shared__ float cscore[kMaxCand];
+  __shared__ int32_t cpos[kMaxCand];
+  __shared__ int32_t chosen[kMaxCand];
+
+  const int bg = blockIdx.x;
+  const int row = bg / a.G, g = bg % a.G;
+  const int tid = threadIdx.x;
+  const int64_t b = a.idx ? static_cast<int64_t>(a.idx[row]) : static_cast<int64_t>(row);
+  if (b < 0 || b >= a.n_rows || a.active[row] == 0) return;
+  const int64_t cnt = a.count[b];
+  if (cnt < 0 || cnt >= a.C) return;  // corrupt counter: leave the row untouched
+  const int64_t rowbytes = static_cast<int64_t>(a.D) * a.esize;
+  char* pk = static_cast<char*>(a.pkeys) + ((b * a.G + g) * a.PC) * rowbytes;
+  char* pv = static_cast<char*>(a.pvalues) + ((b * a.G + g) * a.PC) * rowbytes;
+  const char* src_k = static_cast<const char*>(a.key) + (static_cast<int64_t>(row) * a.G + g) * rowbytes;
+  const char* src_v = static_cast<const char*>(a.value) + (static_cast<int64_t>(row) * a.G + g) * rowbytes;
+  float* ps = a.pscores + (b * a.G + g) * a.PC;
+  const float new_score = a.score[static_cast<int64_t>(row) * a.G + g];
+  // push
+  if (tid < 64) copy_row16(pk + cnt * rowbytes, src_k, static_cast<int>(rowbytes), tid, 64);
+  else if (tid < 128) copy_row16(pv + cnt * rowbytes, src_v, static_cast<int>(rowbytes), tid - 64, 64);
+  else if (tid == 128) ps[cnt] = new_score;
+  if (cnt + 1 != a.C) return;  // uniform over the workgroup
+  __syncthreads();             // the pushed row is visible to the whole workgroup
+
+  const int KC = a.KC, C = a.C, N = KC + C;
+  const int64_t meta = (b * a.G + g) * static_cast<int64_t>(KC);
+  const int64_t base_pos = a.total[b] - cnt;
+  for (int n = tid; n < N; n += kCommitThreads) {
+    float sc;
+    int32_t p;
+    if (n < KC) {
+      sc = a.scores[meta + n];
+      p = a.pos[meta + n];
+      if (p < 0) p = -1;
+    } else {
+      sc = n - KC == cnt ? new_score : ps[n - KC];
+      p = static_cast<int32_t>(base_pos + (n - KC));
+    }
+    const uint32_t pkey = p >= 0 ? static_cast<uint32_t>(p) : 0x7fffffffu;
+    ckey[n] = (static_cast<uint64_t>(~score_key(sc)) << 32) | pkey;
+    cscore[n] = sc;
+    cpos[n] = p;
+  }
+  __syncthreads();
+  for (int n = tid; n < N; n += kCommitThreads) {
+    const uint64_t mine = ckey[n];
+    int rank = 0;
+    for (int j = 0; j < N; ++j) {
+      const uint64_t o = ckey[j];
+      rank += (o < mine) | ((o == mine) & (j < n));
+    }
+    if (rank < KC) chosen[rank] = n;
+  }
+  __syncthreads();
+  // Keys, then values: gather every selected row of the tensor into registers
+  // before any committed row of it is overwritten (the sources include the
+  // committed rows themselves), then write them back.
+  const int chunks = static_cast<int>(rowbytes / 16);  // 16-byte pieces per row
+  const int total_pieces = KC * chunks;
+  char* ck = static_cast<char*>(a.keys) + meta * rowbytes;
+  char* cv = static_cast<char*>(a.values) + meta * rowbytes;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    char* committed = pass == 0 ? ck : cv;
+    const char* pending = pass == 0 ? pk : pv;
+    uint4 buf[kMaxPieces];
+#pragma unroll
+    for (int i = 0; i < kMaxPieces; ++i) {
+      const int piece = tid + i * kCommitThreads;
+      if (piece < total_pieces) {
+        const int slot = piece / chunks, c = piece % chunks;
+        const int src = chosen[slot];
+        // an invalid selection reads committed row 0, as the reference does
+        const char* from = cpos[src] < 0 ? committed
+                           : (src < KC ? committed + src * rowbytes : pending + (src - KC) * rowbytes);
+        buf[i] = reinterpret_cast<const uint4*>(from)[c];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kMaxPieces; ++i) {
+      const int piece = tid + i * kCommitThreads;
+      if (piece < total_pieces) {
+        const int slot = piece / chunks, c = piece % chunks;
+        reinterpret_cast<uint4*>(committed + slot * rowbytes)[c] = buf[i];
+      }
+    }
+  }
+  for (int n = tid; n < KC; n += kCommitThreads) {
+    const int src = chosen[n];
+    a.scores[meta + n] = cscore[src];
+    a.pos[meta + n] = cpos[src];
+  }
+}
+
+// count = (count + active) % C, total += active, once per state row.
+__global__ void anchor_advance_kernel(int64_t* count, int64_t* total, const uint8_t* active,
+                                      const int32_t* idx, int B, int C, int64_t n_rows) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= B) return;
+  const int64_t b = idx ? static_cast<int64_t>(idx[row]) : static_cast<int64_t>(row);
+  if (b < 0 || b >= n_rows) return;
+  const int64_t act = active[row] ? 1 : 0;
+  const int64_t c = count[b] + act;
+  count[b] = c == C ? 0 : c;
+  total[b] += act;
+}
+
+template <int DT, int D>
+int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(kReadThreads);
+  switch (R) {
+    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4>), grid, block, 0, st, a); break;
+    default: set_error("anchor_read: heads per group must be 1, 2 or 4 (got %d)", R); return YH_ERR_INVALID;
+  }
+  YH_CHECK_LAUNCH("anchor_read");
+  return YH_OK;
+}
+
+template <int DT>
+int launch_read_d(int D, int R, const ReadArgs& a, hipStream_t st) {
+  if (D == 128) return launch_read_r<DT, 128>(R, a, st);
+  if (D == 64) return launch_read_r<DT, 64>(R, a, st);
+  set_error("anchor_read: head dim must be 64 or 128 (got %d)", D);
+  return YH_ERR_INVALID;
+}
+
+}  // namespace
+}  // namespace yh
+
+extern "C" int yh_anchor_read(const void* query, const void* keys, const void* values,
+                              const int32_t* positions, const int32_t* indices, void* out,
+                              int64_t B, int64_t H, int64_t G, int64_t capacity, int64_t D,
+                              int64_t n_state_rows, int dtype, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(query && keys && values && positions && out, "anchor_read: null tensor pointer");
+  YH_CHECK_ARG(B >= 0 && G > 0 && H > 0 && H % G == 0, "anchor_read: bad B/H/G (%lld/%lld/%lld)",
+               (long long)B, (long long)H, (long long)G);
+  YH_CHECK_ARG(capacity > 0 && capacity % 64 == 0 && capacity <= kMaxCap,
+               "anchor_read: capacity must be a positive multiple of 64 up to %d (got %lld)", kMaxCap,
+               (long long)capacity);
+  YH_CHECK_ARG(is_float_dtype(dtype), "anchor_read: unsupported dtype %d", dtype);
+  YH_CHECK_ARG(indices != nullptr || n_state_rows >= B, "anchor_read: state has fewer rows than the batch");
+  YH_CHECK_ARG(B * G < (1LL << 31), "anchor_read: grid too large");
+  const uintptr_t al = 15;
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(keys) |
+                 reinterpret_cast<uintptr_t>(values)) & al) == 0,
+               "anchor_read: query/keys/values must be 16-byte aligned");
+  if (B == 0) return YH_OK;
+  ReadArgs a{query, keys, values, positions, indices, out, (int)B, (int)G, (int)capacity, n_state_rows,
+             1.0f / sqrtf(static_cast<float>(D))};
+  const int R = static_cast<int>(H / G);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case YH_BF16: return launch_read_d<YH_BF16>((int)D, R, a, st);
+    case YH_F16: return launch_read_d<YH_F16>((int)D, R, a, st);
+    default: return launch_read_d<YH_F32>((int)D, R, a, st);
+  }
+}
+
+extern "C" int yh_anchor_commit(const void* key, const void* value, const float* score,
+                                const uint8_t* active, const int32_t* indices, void* keys, void* values,
+                                float* scores, int32_t* positions, void* pending_keys,
+                                void* pending_values, float* pending_scores, int64_t* count,
+                                int64_t* total, int64_t B, int64_t G, int64_t capacity,
+                                int64_t pending_capacity, int64_t chunk, int64_t D, int64_t n_state_rows,
+                                int dtype, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(key && value && score && active && keys && values && scores && positions && pending_keys &&
+                   pending_values && pending_scores && count && total,
+               "anchor_commit: null tensor pointer");
+  YH_CHECK_ARG(B >= 0 && G > 0 && capacity > 0 && D > 0, "anchor_commit: bad sizes");
+  YH_CHECK_ARG(chunk >= 1 && chunk <= pending_capacity, "anchor_commit: chunk %lld outside [1, %lld]",
+               (long long)chunk, (long long)pending_capacity);
+  YH_CHECK_ARG(capacity + chunk <= kMaxCand, "anchor_commit: capacity + chunk must be <= %d", kMaxCand);
+  YH_CHECK_ARG(is_float_dtype(dtype), "anchor_commit: unsupported dtype %d", dtype);
+  const int esize = dtype == YH_F32 ? 4 : 2;
+  YH_CHECK_ARG((D * esize) % 16 == 0, "anchor_commit: a row must be a multiple of 16 bytes");
+  YH_CHECK_ARG(capacity * D * esize <= static_cast<int64_t>(kCommitThreads) * kMaxPieces * 16,
+               "anchor_commit: capacity x row bytes exceeds %d", kCommitThreads * kMaxPieces * 16);
+  YH_CHECK_ARG(indices != nullptr || n_state_rows >= B, "anchor_commit: state has fewer rows than the batch");
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value) |
+                 reinterpret_cast<uintptr_t>(keys) | reinterpret_cast<uintptr_t>(values) |
+                 reinterpret_cast<uintptr_t>(pending_keys) | reinterpret_cast<uintptr_t>(pending_values)) & 15) == 0,
+               "anchor_commit: key/value rows must be 16-byte aligned");
+  YH_CHECK_ARG(B * G < (1LL << 31), "anchor_commit: grid too large");
+  if (B == 0) return YH_OK;
+  CommitArgs a{key, value, score, active, indices, keys, values, scores, positions, pending_keys, pending_values,
+               pending_scores, count, total, (int)B, (int)G, (int)capacity, (int)pending_capacity, (int)chunk,
+               (int)D, esize, n_state_rows};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(anchor_commit_kernel, dim3(static_cast<unsigned>(B * G)), dim3(kCommitThreads), 0, st, a);
+  YH_CHECK_LAUNCH("anchor_commit");
+  const int threads = 256;
+  hipLaunchKernelGGL(anchor_advance_kernel, dim3(static_cast<unsigned>((B + threads - 1) / threads)), dim3(threads),
+                     0, st, count, total, active, indices, (int)B, (int)chunk, n_state_rows);
+  YH_CHECK_LAUNCH("anchor_advance");
+  return YH_OK;
+}

@@ -124,6 +124,19 @@ __device__ __forceinline__ void store4(void* p, int64_t i, float4 x) {
   }
 }
 
+// Streaming (nontemporal) 16-byte access for data touched exactly once per
+// launch, e.g. the recurrent state read-modify-write: it keeps the stream from
+// displacing reusable lines in L2 / the Infinity Cache.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_stream4(const float* p) {
+  const f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_stream4(float* p, float4 x) {
+  const f32x4_t v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t*>(p));
+}
+
 // Wave-wide sum (64 lanes) with xor shuffles.
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll

@@ -20,7 +20,8 @@
 //   * o = exp(g) S^T q + delta (k.q) is formed from the same pass, so the
 //     updated state is never re-read.
 // The state loads are issued before anything else so their HBM latency
-// overlaps the q/k normalisation.
+// overlaps the q/k normalisation, and both state directions use nontemporal
+// (streaming) accesses.
 #include "common.h"
 
 #include <stdlib.h>
@@ -47,6 +48,81 @@ struct GdnArgs {
 __device__ __forceinline__ float4 f4(float x) { return make_float4(x, x, x, x); }
 __device__ __forceinline__ float4 fma4(float4 a, float b, float4 c) {
   return make_float4(fmaf(a.x, b, c.x), fmaf(a.y, b, c.y), fmaf(a.z, b, c.z), fmaf(a.w, b, c.w));
+}
+
+// Per-token inputs of one step, loaded ahead of use (for step 0 before the
+// state loads, for step t+1 before the state update of step t).  They are kept
+// as raw bits and converted only where they are used, so no wait on them is
+// placed in front of the state stream.
+template <int DT> struct Raw4 { using T = uint2; };
+template <> struct Raw4<YH_F32> { using T = uint4; };
+
+template <int DT>
+__device__ __forceinline__ typename Raw4<DT>::T ld_raw4(const void* p, int64_t i) {
+  if constexpr (DT == YH_F32) return reinterpret_cast<const uint4*>(static_cast<const float*>(p) + i)[0];
+  else return reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i)[0];
+}
+template <int DT>
+__device__ __forceinline__ float4 cvt4(const typename Raw4<DT>::T& w) {
+  if constexpr (DT == YH_F32) {
+    return make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
+  } else if constexpr (DT == YH_BF16) {
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+  } else {
+    return make_float4(f16_to_f32(w.x & 0xffff), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xffff),
+                       f16_to_f32(w.y >> 16));
+  }
+}
+template <int DT>
+__device__ __forceinline__ uint32_t ld_raw1(const void* p, int64_t i) {
+  if constexpr (DT == YH_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const uint16_t*>(p)[i];
+}
+template <int DT>
+__device__ __forceinline__ float cvt1(uint32_t w) {
+  if constexpr (DT == YH_F32) return __uint_as_float(w);
+  else if constexpr (DT == YH_BF16) return __uint_as_float(w << 16);
+  else return f16_to_f32(static_cast<uint16_t>(w));
+}
+__device__ __forceinline__ uint32_t ld_raw_any(const void* p, int64_t i, int dt) {
+  return dt == YH_F32 ? static_cast<const uint32_t*>(p)[i] : static_cast<const uint16_t*>(p)[i];
+}
+__device__ __forceinline__ float cvt_any(uint32_t w, int dt) {
+  return dt == YH_F32 ? __uint_as_float(w)
+         : dt == YH_BF16 ? __uint_as_float(w << 16) : f16_to_f32(static_cast<uint16_t>(w));
+}
+
+template <int DT, int KPL>
+struct TokIn {
+  uint32_t kx[KPL], qx[KPL];  // raw q / k (normalising wave only)
+  typename Raw4<DT>::T v;     // this thread's 4 value columns
+  uint32_t g, beta;
+};
+
+template <int DT, int K, int KPL>
+__device__ __forceinline__ void load_tok(TokIn<DT, KPL>& in, const GdnArgs& a, int64_t tok, int hk,
+                                         int hv, int col0, bool norm_wave, int lane) {
+  if (norm_wave) {
+    const int64_t base = (tok * a.H + hk) * K;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      in.kx[j] = ld_raw1<DT>(a.k, base + lane + j * kWave);
+      in.qx[j] = ld_raw1<DT>(a.q, base + lane + j * kWave);
+    }
+  }
+  const int64_t vh = tok * a.HV + hv;
+  in.v = ld_raw4<DT>(a.v, vh * a.V + col0);
+  in.g = ld_raw_any(a.g, vh, a.g_dt);
+  in.beta = ld_raw_any(a.beta, vh, a.beta_dt);
+}
+
+__device__ __forceinline__ void wave_sum3(float& x, float& y, float& z) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float a = __shfl_xor(x, off, kWave), b = __shfl_xor(y, off, kWave), c = __shfl_xor(z, off, kWave);
+    x += a; y += b; z += c;
+  }
 }
 
 template <int DT, int K, int VT, int NT>
@@ -76,6 +152,7 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;
   const int col0 = vt * VT + lc * 4;
+  const bool norm_wave = wid == 0;
 
   int64_t srow = a.idx ? static_cast<int64_t>(a.idx[b]) : static_cast<int64_t>(b);
   if (srow < 0 || srow >= a.n_rows) {
@@ -88,45 +165,41 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
     return;
   }
 
+  TokIn<DT, KPL> in;
+  load_tok<DT, K, KPL>(in, a, static_cast<int64_t>(b) * a.T, hk, hv, col0, norm_wave, lane);
+
   float* S = a.state + (srow * a.HV + hv) * static_cast<int64_t>(K) * a.V + col0;
   float4 s[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i)
-    s[i] = *reinterpret_cast<const float4*>(S + static_cast<int64_t>(rg + i * RG) * a.V);
+    s[i] = ld_stream4(S + static_cast<int64_t>(rg + i * RG) * a.V);
 
   for (int t = 0; t < a.T; ++t) {
     const int buf = t & 1;
     const int64_t tok = static_cast<int64_t>(b) * a.T + t;
-    if (wid == 0) {
-      const int64_t base = (tok * a.H + hk) * K;
-      float kx[KPL], qx[KPL];
-      float ssk = 0.f, ssq = 0.f, dot = 0.f;
+    if (norm_wave) {
+      float ssk = 0.f, ssq = 0.f, dot = 0.f, kf[KPL], qf[KPL];
 #pragma unroll
       for (int j = 0; j < KPL; ++j) {
-        kx[j] = Elem<DT>::ld(static_cast<const typename Elem<DT>::T*>(a.k), base + lane + j * kWave);
-        qx[j] = Elem<DT>::ld(static_cast<const typename Elem<DT>::T*>(a.q), base + lane + j * kWave);
-        ssk = fmaf(kx[j], kx[j], ssk);
-        ssq = fmaf(qx[j], qx[j], ssq);
-        dot = fmaf(kx[j], qx[j], dot);
+        kf[j] = cvt1<DT>(in.kx[j]);
+        qf[j] = cvt1<DT>(in.qx[j]);
+        ssk = fmaf(kf[j], kf[j], ssk);
+        ssq = fmaf(qf[j], qf[j], ssq);
+        dot = fmaf(kf[j], qf[j], dot);
       }
-      float rk = 1.f, rq = 1.f;
-      if (a.l2) {
-        rk = rsqrtf(wave_sum(ssk) + 1e-6f);
-        rq = rsqrtf(wave_sum(ssq) + 1e-6f);
-      }
-      rq *= a.scale;
-      dot = wave_sum(dot);
+      wave_sum3(ssk, ssq, dot);
+      const float rk = a.l2 ? rsqrtf(ssk + 1e-6f) : 1.f;
+      const float rq = (a.l2 ? rsqrtf(ssq + 1e-6f) : 1.f) * a.scale;
 #pragma unroll
       for (int j = 0; j < KPL; ++j) {
-        kn[buf][lane + j * kWave] = kx[j] * rk;
-        qn[buf][lane + j * kWave] = qx[j] * rq;
+        kn[buf][lane + j * kWave] = kf[j] * rk;
+        qn[buf][lane + j * kWave] = qf[j] * rq;
       }
       if (lane == 0) kq_s[buf] = dot * rk * rq;
     }
-    const int64_t vh = tok * a.HV + hv;
-    const float4 vv = load4<DT>(a.v, vh * a.V + col0);
-    const float eg = expf(load_any(a.g, vh, a.g_dt));
-    const float bt = load_any(a.beta, vh, a.beta_dt);
+    const float4 vv = cvt4<DT>(in.v);
+    const float eg = expf(cvt_any(in.g, a.g_dt));
+    const float bt = cvt_any(in.beta, a.beta_dt);
     __syncthreads();
 
     float4 pk = f4(0.f), pq = f4(0.f);
@@ -160,6 +233,7 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
       sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
     }
     const float kq = kq_s[buf];
+    if (t + 1 < a.T) load_tok<DT, K, KPL>(in, a, tok + 1, hk, hv, col0, norm_wave, lane);
     float4 d;
     d.x = bt * (vv.x - eg * kv.x);
     d.y = bt * (vv.y - eg * kv.y);
@@ -171,7 +245,7 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
       o.y = fmaf(eg, sq.y, d.y * kq);
       o.z = fmaf(eg, sq.z, d.z * kq);
       o.w = fmaf(eg, sq.w, d.w * kq);
-      store4<DT>(a.o, vh * a.V + col0, o);
+      store4<DT>(a.o, (tok * a.HV + hv) * a.V + col0, o);
     }
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -185,7 +259,7 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
 
 #pragma unroll
   for (int i = 0; i < RPT; ++i)
-    *reinterpret_cast<float4*>(S + static_cast<int64_t>(rg + i * RG) * a.V) = s[i];
+    st_stream4(S + static_cast<int64_t>(rg + i * RG) * a.V, s[i]);
 }
 
 template <int K, int VT, int NT>
@@ -203,11 +277,13 @@ int launch_tile(int dt, const GdnArgs& a, hipStream_t st) {
 
 // Tile choice.  YH_GDN_TILE="VT:NT" overrides the default (tuning sweeps);
 // it is read on every call so a process can sweep tiles.
-void pick_tile(int K, int V, int* vt, int* nt) {
+void pick_tile(int K, int V, int64_t B, int64_t HV, int* vt, int* nt) {
   const char* e = getenv("YH_GDN_TILE");
   int x = 0, y = 0;
   if (e && sscanf(e, "%d:%d", &x, &y) == 2 && x > 0 && V % x == 0) { *vt = x; *nt = y; return; }
-  if (K == 128) { *vt = 64; *nt = 256; }
+  // Measured on MI355X (decode, HV = 32, dk = dv = 128): 64-column tiles of
+  // 256 threads are best up to ~4096 tiles (B = 64), 512 threads above.
+  if (K == 128) { *vt = 64; *nt = B * HV * (V / 64) > 4096 ? 512 : 256; }
   else { *vt = 64; *nt = 128; }
 }
 
@@ -244,13 +320,17 @@ extern "C" int yh_gdn_recurrent(const void* q, const void* k, const void* v, con
             g_dtype, beta_dtype};
   hipStream_t st = static_cast<hipStream_t>(stream);
   int vt = 0, nt = 0;
-  pick_tile((int)K, (int)V, &vt, &nt);
+  pick_tile((int)K, (int)V, B, HV, &vt, &nt);
   if (K == 128) {
     if (vt == 128 && nt == 256) return launch_tile<128, 128, 256>(qkv_dtype, a, st);
+    if (vt == 128 && nt == 512) return launch_tile<128, 128, 512>(qkv_dtype, a, st);
+    if (vt == 64 && nt == 512) return launch_tile<128, 64, 512>(qkv_dtype, a, st);
     if (vt == 64 && nt == 256) return launch_tile<128, 64, 256>(qkv_dtype, a, st);
     if (vt == 64 && nt == 128) return launch_tile<128, 64, 128>(qkv_dtype, a, st);
     if (vt == 32 && nt == 128) return launch_tile<128, 32, 128>(qkv_dtype, a, st);
     if (vt == 32 && nt == 256) return launch_tile<128, 32, 256>(qkv_dtype, a, st);
+    if (vt == 32 && nt == 64) return launch_tile<128, 32, 64>(qkv_dtype, a, st);
+    if (vt == 16 && nt == 64) return launch_tile<128, 16, 64>(qkv_dtype, a, st);
     return launch_tile<128, 64, 256>(qkv_dtype, a, st);
   }
   if (vt == 64 && nt == 64) return launch_tile<64, 64, 64>(qkv_dtype, a, st);

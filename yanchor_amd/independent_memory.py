@@ -1,0 +1,158 @@
+"""Anchor-memory kernels behind the reference's ``model.independent_memory`` API.
+
+The reference imports this module through ``_cuda_module('independent_memory')``
+(modeling_yanchor.py:19-20, used at 249 and 278-282) and calls
+``committed_gqa(query, state, indices)`` and
+``commit_decode(key, value, scores, active, chunk, state, indices)``
+(runtime/model/independent_memory.py:177-201).  ``IndependentMemoryState``
+mirrors the reference dataclass (modeling_yanchor.py:80-120) field for field, so
+a state built by either side works with the other.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, fields
+
+import torch
+
+from . import _native as N
+
+
+@dataclass
+class IndependentMemoryState:
+    keys: torch.Tensor            # [B, G, K_cap, D]
+    values: torch.Tensor          # [B, G, K_cap, D]
+    scores: torch.Tensor          # [B, G, K_cap] float32, -inf = empty
+    positions: torch.Tensor       # [B, G, K_cap] int32, -1 = empty
+    pending_keys: torch.Tensor    # [B, G, C_max, D]
+    pending_values: torch.Tensor  # [B, G, C_max, D]
+    pending_scores: torch.Tensor  # [B, G, C_max] float32
+    count: torch.Tensor           # [B] int64
+    total: torch.Tensor           # [B] int64
+
+    @classmethod
+    def empty(cls, batch, groups, capacity, chunk, dim, device, dtype):
+        kv = (batch, groups, capacity, dim)
+        pend = (batch, groups, chunk, dim)
+        return cls(torch.zeros(kv, device=device, dtype=dtype), torch.zeros(kv, device=device, dtype=dtype),
+                   torch.full(kv[:-1], -math.inf, device=device, dtype=torch.float32),
+                   torch.full(kv[:-1], -1, device=device, dtype=torch.int32),
+                   torch.zeros(pend, device=device, dtype=dtype), torch.zeros(pend, device=device, dtype=dtype),
+                   torch.full(pend[:-1], -math.inf, device=device, dtype=torch.float32),
+                   torch.zeros(batch, device=device, dtype=torch.long),
+                   torch.zeros(batch, device=device, dtype=torch.long))
+
+    def select(self, indices):
+        return type(self)(*(getattr(self, f.name).index_select(0, indices.to(self.keys.device))
+                            for f in fields(self)))
+
+    def repeat(self, repeats):
+        return type(self)(*(getattr(self, f.name).repeat_interleave(repeats, 0) for f in fields(self)))
+
+    def scatter_(self, source, target_indices, source_indices):
+        for f in fields(self):
+            target, value = getattr(self, f.name), getattr(source, f.name)
+            target.index_copy_(0, target_indices.to(target.device),
+                               value.index_select(0, source_indices.to(value.device)).to(target.device))
+
+    def reset_(self, rows=None):
+        for f in fields(self):
+            value = getattr(self, f.name)
+            fill = -math.inf if "scores" in f.name else -1 if f.name == "positions" else 0
+            if rows is None:
+                value.fill_(fill)
+            else:
+                value.index_fill_(0, rows.to(value.device), fill)
+
+    def to_(self, device):
+        for f in fields(self):
+            setattr(self, f.name, getattr(self, f.name).to(device, non_blocking=True))
+
+
+def _check_state(state: IndependentMemoryState):
+    b, g, cap, d = state.keys.shape
+    if state.values.shape != state.keys.shape or state.values.dtype != state.keys.dtype:
+        raise ValueError("memory keys and values must match")
+    if state.scores.shape != (b, g, cap) or state.scores.dtype != torch.float32:
+        raise ValueError("memory scores must be float32 [B, G, K_cap]")
+    if state.positions.shape != (b, g, cap) or state.positions.dtype != torch.int32:
+        raise ValueError("memory positions must be int32 [B, G, K_cap]")
+    pc = state.pending_keys.shape[2]
+    if state.pending_keys.shape != (b, g, pc, d) or state.pending_values.shape != (b, g, pc, d):
+        raise ValueError("pending keys/values must be [B, G, C, D]")
+    if state.pending_scores.shape != (b, g, pc) or state.pending_scores.dtype != torch.float32:
+        raise ValueError("pending scores must be float32 [B, G, C]")
+    if state.count.dtype != torch.long or state.total.dtype != torch.long:
+        raise ValueError("count/total must be int64")
+    for f in fields(state):
+        if not getattr(state, f.name).is_contiguous():
+            raise ValueError(f"memory state field {f.name} must be contiguous")
+    return b, g, cap, pc, d
+
+
+def _indices(indices, batch):
+    if indices is None:
+        return None
+    if indices.shape != (batch,):
+        raise ValueError("state indices must have one entry per batch row")
+    return indices.to(torch.int32).contiguous()
+
+
+def committed_gqa(query, state: IndependentMemoryState, indices=None):
+    """Read the committed anchor slots for one decode token.
+
+    query ``[B, 1, H, D]``; returns ``[B, 1, H, D]`` in the query dtype: per
+    head, softmax over [q.K^T / sqrt(D) on live slots, 0] applied to V (the
+    zero-logit sink).  Row b reads state row ``indices[b]`` when given (-1 reads
+    nothing and returns 0)."""
+    nb, g, cap, _, d = _check_state(state)
+    if query.ndim != 4 or query.shape[1] != 1 or query.shape[3] != d:
+        raise ValueError("query must be [B, 1, H, D] with the memory head dim")
+    b, _, h, _ = query.shape
+    if h % g:
+        raise ValueError("query heads must be a multiple of memory groups")
+    if query.dtype != state.keys.dtype:
+        raise ValueError("query and memory must share a dtype")
+    N.require_device(query, state.keys, indices)
+    idx = _indices(indices, b)
+    if idx is None and nb < b:
+        raise ValueError("memory state has fewer rows than the batch")
+    q = query.contiguous()
+    out = torch.empty_like(q)
+    N.call("yh_anchor_read", q.data_ptr(), state.keys.data_ptr(), state.values.data_ptr(),
+           state.positions.data_ptr(), N.ptr(idx), out.data_ptr(), b, h, g, cap, d, nb, N.code(q),
+           N.stream_of(q))
+    return out
+
+
+def commit_decode(key, value, scores, active, chunk, state: IndependentMemoryState, indices=None):
+    """Push one token per active row into the pending chunk and, when that
+    fills the chunk, keep the Top-K_cap of committed + pending slots (score
+    descending, then position, then candidate index).  IN PLACE on ``state``.
+
+    key, value ``[B, 1, G, D]``; scores ``[B, 1, G]`` float32; active ``[B]``
+    bool."""
+    nb, g, cap, pc, d = _check_state(state)
+    b = key.shape[0]
+    if key.shape != (b, 1, g, d) or value.shape != key.shape:
+        raise ValueError("key/value must be [B, 1, G, D]")
+    if scores.shape != (b, 1, g):
+        raise ValueError("scores must be [B, 1, G]")
+    if active.shape != (b,):
+        raise ValueError("active must be [B]")
+    if not 1 <= int(chunk) <= pc:
+        raise ValueError(f"chunk {chunk} must lie in [1, {pc}]")
+    if key.dtype != state.keys.dtype or value.dtype != state.keys.dtype:
+        raise ValueError("key/value must match the memory dtype")
+    N.require_device(key, value, scores, active, state.keys, indices)
+    idx = _indices(indices, b)
+    if idx is None and nb < b:
+        raise ValueError("memory state has fewer rows than the batch")
+    k, v = key.contiguous(), value.contiguous()
+    sc = scores.to(torch.float32).contiguous()
+    act = active.to(torch.bool).contiguous()
+    N.call("yh_anchor_commit", k.data_ptr(), v.data_ptr(), sc.data_ptr(), act.data_ptr(), N.ptr(idx),
+           state.keys.data_ptr(), state.values.data_ptr(), state.scores.data_ptr(),
+           state.positions.data_ptr(), state.pending_keys.data_ptr(), state.pending_values.data_ptr(),
+           state.pending_scores.data_ptr(), state.count.data_ptr(), state.total.data_ptr(), b, g, cap, pc,
+           int(chunk), d, nb, N.code(k), N.stream_of(k))

@@ -78,3 +78,33 @@ def decode_gdn_config1(pool_rows: int = 96) -> GdnInputs:
     q/k/v bf16, g/beta fp32."""
     return gdn_inputs(64, 1, 32, 32, 128, 128, dtype=torch.bfloat16, seed=SEED0 + 1,
                       state_std=0.02, pool_rows=pool_rows)
+
+
+def anchor_state(B, G, capacity, chunk, D, *, p_live=0.7, seed=SEED0 + 1, dtype=torch.bfloat16,
+                 fill_pending=0, total0=None):
+    """Anchor memory state on the CPU: keys/values ~ N(0, 1); slot n of (b, g)
+    live with probability p_live (position >= 0, score ~ N(0, 1)), dead slots
+    carry position -1 and score -inf.  ``fill_pending`` pending entries are
+    already pushed (count = fill_pending) and total = total0 (default
+    capacity + fill_pending)."""
+    from .independent_memory import IndependentMemoryState
+    gen = _gen(seed)
+    st = IndependentMemoryState.empty(B, G, capacity, chunk, D, "cpu", dtype)
+    st.keys.copy_(torch.randn(B, G, capacity, D, generator=gen).to(dtype))
+    st.values.copy_(torch.randn(B, G, capacity, D, generator=gen).to(dtype))
+    live = torch.rand(B, G, capacity, generator=gen) < p_live
+    pos = torch.randperm(capacity * 4, generator=gen)[:capacity].sort().values.to(torch.int32)
+    st.positions.copy_(torch.where(live, pos.expand(B, G, capacity), torch.tensor(-1, dtype=torch.int32)))
+    sc = torch.randn(B, G, capacity, generator=gen)
+    st.scores.copy_(torch.where(live, sc, torch.tensor(-float("inf"))))
+    if fill_pending:
+        st.pending_keys[:, :, :fill_pending] = torch.randn(B, G, fill_pending, D, generator=gen).to(dtype)
+        st.pending_values[:, :, :fill_pending] = torch.randn(B, G, fill_pending, D, generator=gen).to(dtype)
+        st.pending_scores[:, :, :fill_pending] = torch.randn(B, G, fill_pending, generator=gen)
+    st.count.fill_(fill_pending)
+    st.total.fill_(capacity * 4 + fill_pending if total0 is None else total0)
+    return st
+
+
+def anchor_query(B, H, D, *, seed=SEED0 + 2, dtype=torch.bfloat16):
+    return torch.randn(B, 1, H, D, generator=_gen(seed)).to(dtype)
