@@ -115,6 +115,125 @@ int yh_anchor_commit(const void* key, const void* value, const float* score, con
                      int64_t* total, int64_t B, int64_t G, int64_t capacity, int64_t pending_capacity,
                      int64_t chunk, int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream);
 
+/* Sampling semantics of yh_topk_sample. */
+enum yh_sample_mode {
+  /* _qwen35_top20_counter_sample_kernel (runtime/model/inference_kernels.py:
+   * 1119-1145): softmax of the top-k after temperature, keep p where the mass
+   * before it is < top_p, u unclamped, rank = #(cumulative < u * retained). */
+  YH_SAMPLE_FUSED = 0,
+  /* sample_top_k_top_p_counter (inference_kernels.py:35-88): the same
+   * truncation, renormalised, u clamped below 1, threshold
+   * min(u * total, nextafter(total, 0)), searchsorted left. */
+  YH_SAMPLE_TORCH = 1
+};
+
+/*
+ * Top-k / top-p counter sampling of one token per row, with the dense presence
+ * penalty fused in (scores are not modified).
+ *
+ * Replaces torch.topk + _qwen35_top20_counter_sample_kernel
+ * (_sample_top_k_top_p_counter_triton, runtime/model/inference_kernels.py:
+ * 1147-1167) and sample_top_k_top_p_counter (inference_kernels.py:73-88) for
+ * 1 <= top_k <= 64.
+ *
+ *   scores       [B, V] rows `row_stride` elements apart (f32 / bf16 / f16)
+ *   seen         NULL or uint8/bool [B, V] rows `seen_stride` apart; where set,
+ *                `penalty` is subtracted from the score before selection
+ *   attempt_ids  int64 [B]; steps int64 [B] or NULL (then `step` for all rows)
+ *   seed, stream_id  counter-hash seed and stream (taken mod 2^32)
+ *   tokens       int64 [B] output
+ *   out_values, out_indices  NULL or [B, top_k] float / int64: the selected
+ *                top-k (descending; equal values by ascending index)
+ *   workspace    device scratch of at least yh_topk_workspace_bytes(B, V, k)
+ * top_k == 1 returns the argmax.  Otherwise temperature > 0, 0 < top_p <= 1.
+ */
+int yh_topk_sample(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen, int64_t seen_stride,
+                   float penalty, const int64_t* attempt_ids, const int64_t* steps, int64_t step, uint64_t seed,
+                   uint64_t stream_id, float temperature, int64_t top_k, float top_p, int mode, int64_t* tokens,
+                   float* out_values, int64_t* out_indices, void* workspace, int64_t workspace_bytes, int64_t B,
+                   int64_t V, yh_stream_t stream);
+
+/* Workspace bytes yh_topk_sample needs, and its vocabulary split. */
+int64_t yh_topk_workspace_bytes(int64_t B, int64_t V, int64_t top_k);
+void yh_topk_segments(int64_t V, int64_t top_k, int* n_segments, int* seg_len);
+
+/*
+ * scores[i] -= penalty where seen[i], float32, in place; n elements.
+ * Replaces _qwen35_dense_presence_penalty_kernel / _apply_dense_presence_penalty_
+ * (runtime/model/inference_kernels.py:1095-1114).
+ */
+int yh_presence_penalty(float* scores, const uint8_t* seen, int64_t n, float penalty, yh_stream_t stream);
+
+/*
+ * u = float32((hash + 0.5) / 2^32), clamped below 1, for n counters
+ * (attempt_ids[i], steps ? steps[i] : step, seed, stream_id).
+ * Replaces counter_uniform (runtime/model/inference_kernels.py:24-33).
+ */
+int yh_counter_uniform(const int64_t* attempt_ids, const int64_t* steps, int64_t step, uint64_t seed,
+                       uint64_t stream_id, float* out, int64_t n, yh_stream_t stream);
+
+/*
+ * Per-step slot bookkeeping after sampling, for all `slots` rows:
+ *   active = !finished[r] && slot_rows[r] >= 0
+ *   storage[active ? slot_rows[r] : sink_rows[r], active ? row_steps[r] :
+ *           maximum_new_tokens] = active ? token : pad
+ *   dense_seen[r, stored] = 1; generated_lengths / finished_by_eos of the
+ *   written row; finished[r] |= active && (eos || steps >= cap);
+ *   row_steps[r] += active; row_positions[r] += active;
+ *   decode_ids[r] = finished ? pad : stored; *decode_useful_events += #active.
+ * Replaces _qwen35_decode_state_update_kernel / _update_fixed_decode_state_
+ * (runtime/model/inference_kernels.py:1169-1208).
+ * Types: sampled_token, decode_ids int64 [slots] (the [slots, 1] token
+ * tensors); storage int32 [storage_rows, storage_width]; dense_seen bool
+ * [slots, seen_width]; generated_lengths int64 and finished_by_eos bool
+ * [storage_rows]; finished bool and slot_rows, sink_rows, slot_caps, row_steps,
+ * row_positions int64 [slots]; decode_useful_events int64 scalar.
+ * eos_token_ids is a HOST array of eos_count ids (the first two are used).
+ * Stores that would fall outside their tensor are skipped.
+ */
+int yh_decode_bookkeeping(const int64_t* sampled_token, int32_t* storage, uint8_t* dense_seen,
+                          int64_t* generated_lengths, uint8_t* finished_by_eos, uint8_t* finished,
+                          const int64_t* slot_rows, const int64_t* sink_rows, const int64_t* slot_caps,
+                          int64_t* row_steps, int64_t* row_positions, int64_t* decode_ids,
+                          int64_t* decode_useful_events, int64_t slots, int64_t storage_rows, int64_t storage_width,
+                          int64_t seen_width, int64_t maximum_new_tokens, int64_t pad_token_id,
+                          const int64_t* eos_token_ids, int64_t eos_count, yh_stream_t stream);
+
+/*
+ * cu_seqlens[0] = 0, cu_seqlens[i + 1] = sum(lengths[:i + 1]) (int32 out,
+ * lengths int32 or int64, n sequences): the packed-varlen offsets consumed by
+ * the chunked prefill (the cu_seqlens argument mirrored at
+ * runtime/model/inference_kernels.py:147; vLLM's query_start_loc,
+ * vllm_yanchor.py:85-96).
+ */
+int yh_cu_seqlens(const void* lengths, int lengths_dtype, int32_t* cu_seqlens, int64_t n, yh_stream_t stream);
+
+enum yh_select_mode {
+  YH_SELECT_KEEP = 0,     /* !finished && slot_rows >= 0: tail-compaction keep-list
+                             (torch.nonzero at runtime/model/inference_kernels.py:1725) */
+  YH_SELECT_FINISHED = 1  /* finished: refill targets (inference_kernels.py:1549) */
+};
+
+/*
+ * Ascending indices i < n that satisfy the mode's predicate into out[0..count),
+ * out[count..n) = -1, *count (device int64) = number selected.
+ */
+int yh_select_slots(const uint8_t* finished, const int64_t* slot_rows, int mode, int64_t* out, int64_t* count,
+                    int64_t n, yh_stream_t stream);
+
+/*
+ * For each of n_tensors tensors t (host arrays of device pointers and sizes):
+ * dst[t][dst_index[i]] = src[t][src_index[i]] for i < n, rows of row_bytes[t]
+ * bytes; a NULL index array means the identity.  Indices outside
+ * [0, src_rows[t]) / [0, dst_rows[t]) are skipped.  src[t] and dst[t] must be
+ * different buffers.  The row ops of the fixed-memory caches:
+ * batch_select_indices / batch_scatter_from (modeling_yanchor.py:540-554,
+ * 647-683, 723-731).
+ */
+int yh_gather_rows(int n_tensors, const void* const* src, void* const* dst, const int64_t* row_bytes,
+                   const int64_t* src_rows, const int64_t* dst_rows, const int64_t* src_index,
+                   const int64_t* dst_index, int64_t n, yh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

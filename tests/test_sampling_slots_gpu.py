@@ -1,0 +1,185 @@
+"""GPU parity of sampling and slot kernels (C-ABI path).
+
+Bit-exact bars: counter uniforms (golden vectors of the reference), top-k
+indices and values (vs torch.topk on the CPU, and a stable (value desc, index
+asc) sort where values tie), sampled token ids on every row whose threshold is
+not within float rounding of a CDF boundary (such rows are counted and must be
+rare), bookkeeping state, slot selections, cu_seqlens and gathered rows.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling, slots
+from yanchor_amd import inference_kernels as ik
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(Path(__file__).parent / "golden" / "counter_sampling.npz", allow_pickle=False)
+
+
+def test_counter_uniform_golden(gpu):
+    ids, steps = torch.from_numpy(GOLD["ids"]).to(gpu), torch.from_numpy(GOLD["steps"]).to(gpu)
+    for key in GOLD["uniform_keys"]:
+        seed, stream = (int(x) for x in str(key).split("_"))
+        u = ik.counter_uniform(ids, steps, seed=seed, stream=stream).cpu().numpy()
+        assert np.array_equal(u, GOLD[f"uniform_{key}"])
+
+
+def _ambiguous(values, idx_count, temperature, top_p, u, fused):
+    """True when the draw sits within rounding of a CDF boundary (float64 check)."""
+    x = values.double() / temperature
+    p = torch.softmax(x, -1)
+    keep = (p.cumsum(-1) - p) < top_p
+    t = p * keep
+    cum = t.cumsum(-1)
+    thr = u * cum[-1]
+    near = (cum - thr).abs().min().item() < 1e-5
+    before = ((p.cumsum(-1) - p) - top_p).abs().min().item() < 1e-5
+    return near or before
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_torch_semantics_golden(gpu, case):
+    logits = torch.from_numpy(GOLD["logits"])
+    att, st = torch.from_numpy(GOLD["attempt_ids"]), torch.from_numpy(GOLD["row_steps"])
+    t, k, p, seed = GOLD["sample_cases"][case].tolist()
+    tok = ik.sample_top_k_top_p_counter(logits.to(gpu), att.to(gpu), st.to(gpu), seed=int(seed), temperature=t,
+                                        top_k=int(k), top_p=p).cpu()
+    want = torch.from_numpy(GOLD[f"tokens_{case}"])
+    u = sampling.counter_uniform(att, st, seed=int(seed)).double()
+    vals = torch.topk(logits, int(k)).values
+    bad = [r for r in range(tok.shape[0]) if tok[r, 0] != want[r, 0]]
+    amb = [r for r in bad if int(k) > 1 and _ambiguous(vals[r], k, t, p, u[r], False)]
+    assert bad == amb, f"mismatching rows {bad}"
+
+
+@pytest.mark.parametrize("b,v,k", [(8, 1000, 20), (128, 151936, 20), (5, 70000, 64), (3, 37, 7), (4, 4096, 1)])
+def test_topk_matches_torch(gpu, b, v, k):
+    g = torch.Generator().manual_seed(b * v + k)
+    logits = torch.randn(b, v, generator=g) * 4
+    tok, vals, idx = ik.topk_sample(logits.to(gpu), torch.arange(b).to(gpu), 0, seed=1, temperature=0.6,
+                                    top_k=k, top_p=0.95, mode=ik.SAMPLE_FUSED, return_topk=True)
+    rv, ri = torch.topk(logits, k)
+    assert torch.equal(idx.cpu(), ri) and torch.equal(vals.cpu(), rv)
+
+
+def test_topk_ties_lower_index_first(gpu):
+    logits = torch.zeros(3, 5000)
+    logits[0, ::7] = 1.0          # many equal maxima
+    logits[1] = -0.0              # all -0.0 == +0.0
+    logits[2, 100:200] = 2.5
+    _, vals, idx = ik.topk_sample(logits.to(gpu), torch.arange(3).to(gpu), 0, seed=1, temperature=1.0, top_k=16,
+                                  top_p=1.0, mode=ik.SAMPLE_FUSED, return_topk=True)
+    for r in range(3):
+        order = sorted(range(5000), key=lambda i: (-logits[r, i].item(), i))[:16]
+        assert idx[r].cpu().tolist() == order
+
+
+@pytest.mark.parametrize("temperature,top_p", [(0.6, 0.95), (1.0, 0.5), (1.7, 1.0)])
+def test_fused_semantics_vs_oracle(gpu, temperature, top_p):
+    b, v = 128, 151936
+    g = torch.Generator().manual_seed(17)
+    logits = torch.randn(b, v, generator=g) * 3
+    att = torch.randint(0, 10**9, (b,), generator=g)
+    steps = torch.randint(0, 10**5, (b,), generator=g)
+    tok = ik.sample_top20_counter(logits.to(gpu), att.to(gpu), steps.to(gpu), seed=20260923,
+                                  temperature=temperature, top_p=top_p).cpu()
+    vals, idx = torch.topk(logits, 20)
+    want = sampling.top20_counter_sample(vals / temperature, idx, att, steps, seed=20260923, top_p=top_p)
+    u = torch.tensor([(sampling.counter_word(int(a), int(s), 20260923) + 0.5) / 2**32 for a, s in zip(att, steps)])
+    bad = [r for r in range(b) if tok[r, 0] != want[r, 0]]
+    amb = [r for r in bad if _ambiguous(vals[r], 20, temperature, top_p, u[r], True)]
+    assert bad == amb and len(amb) <= 2, f"mismatching rows {bad}"
+
+
+def test_fused_presence_penalty(gpu):
+    b, v = 16, 20000
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(b, v, generator=g) * 3
+    seen = torch.rand(b, v, generator=g) < 0.3
+    att, steps = torch.arange(b), torch.full((b,), 9)
+    tok = ik.sample_top20_counter(logits.to(gpu), att.to(gpu), steps.to(gpu), seed=3, temperature=0.6,
+                                  top_p=0.95, seen=seen.to(gpu), presence_penalty=1.5).cpu()
+    adjusted = sampling.presence_penalty(logits, seen, 1.5)
+    vals, idx = torch.topk(adjusted, 20)
+    want = sampling.top20_counter_sample(vals / 0.6, idx, att, steps, seed=3, top_p=0.95)
+    assert (tok == want).all()
+    # the standalone in-place kernel gives the same adjusted scores
+    sc = logits.clone().to(gpu)
+    ik._apply_dense_presence_penalty_(sc, seen.to(gpu), 1.5)
+    assert torch.equal(sc.cpu(), adjusted)
+
+
+def test_strided_rows(gpu):
+    logits = torch.randn(6, 3000)
+    view = logits.to(gpu)[:, :2500]
+    _, vals, idx = ik.topk_sample(view, torch.arange(6).to(gpu), 0, seed=1, temperature=1.0, top_k=20, top_p=1.0,
+                                  mode=ik.SAMPLE_TORCH, return_topk=True)
+    rv, ri = torch.topk(logits[:, :2500], 20)
+    assert torch.equal(idx.cpu(), ri)
+
+
+def _scenario(seed, slots_n=96, attempts=300, width=40, vocab=1000):
+    g = torch.Generator().manual_seed(seed)
+    return dict(
+        sampled=torch.randint(0, vocab, (slots_n, 1), generator=g),
+        storage=torch.full((attempts + slots_n, width + 1), 7, dtype=torch.int32),
+        dense_seen=torch.rand(slots_n, vocab, generator=g) < 0.05,
+        generated_lengths=torch.randint(0, 3, (attempts + slots_n,), generator=g),
+        finished_by_eos=torch.zeros(attempts + slots_n, dtype=torch.bool),
+        finished=torch.rand(slots_n, generator=g) < 0.2,
+        slot_rows=torch.where(torch.rand(slots_n, generator=g) < 0.85,
+                              torch.randperm(attempts, generator=g)[:slots_n], torch.tensor(-1)),
+        sink_rows=attempts + torch.arange(slots_n),
+        slot_caps=torch.randint(2, width, (slots_n,), generator=g),
+        row_steps=torch.randint(1, 3, (slots_n,), generator=g),
+        row_positions=torch.randint(5, 50, (slots_n,), generator=g),
+        decode_ids=torch.zeros(slots_n, 1, dtype=torch.long),
+        useful=torch.zeros((), dtype=torch.long),
+    ), g
+
+
+def test_bookkeeping_bit_exact(gpu):
+    cpu, g = _scenario(1)
+    dev = {k: v.to(gpu) for k, v in cpu.items()}
+    kw = dict(maximum_new_tokens=40, pad_token_id=7, eos_token_ids=(3, 4))
+    for step in range(30):
+        tok = torch.randint(0, 1000, (96, 1), generator=g)
+        tok[tok % 97 == 0] = 3  # some eos
+        cpu["sampled"], dev["sampled"] = tok.clone(), tok.to(gpu)
+        slots.decode_state_update(*cpu.values(), **kw)
+        ik._update_fixed_decode_state_(*dev.values(), **kw)
+        torch.cuda.synchronize()
+        for k in cpu:
+            assert torch.equal(dev[k].cpu(), cpu[k]), f"{k} differs at step {step}"
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 1024, 1500, 5000])
+def test_selection_and_cu_seqlens(gpu, n):
+    g = torch.Generator().manual_seed(n)
+    fin = torch.rand(n, generator=g) < 0.4
+    rows = torch.where(torch.rand(n, generator=g) < 0.8, torch.arange(n), torch.tensor(-1))
+    keep = ik.compaction_keep(fin.to(gpu), rows.to(gpu)).cpu().tolist()
+    assert keep == slots.compaction_keep(fin, rows)
+    assert ik.refill_targets(fin.to(gpu)).cpu().tolist() == slots.refill_targets(fin)
+    lengths = torch.randint(0, 9000, (n,), generator=g)
+    for dt in (torch.int32, torch.int64):
+        cu = ik.cu_seqlens(lengths.to(dt).to(gpu)).cpu().tolist()
+        assert cu == slots.cu_seqlens(lengths.tolist())
+
+
+def test_gather_rows(gpu):
+    g = torch.Generator().manual_seed(2)
+    src = [torch.randn(10, 32, 128, 128, generator=g), torch.randint(0, 100, (10,), generator=g),
+           torch.randn(10, 3, 5, generator=g).to(torch.bfloat16), torch.rand(10, generator=g) < 0.5]
+    dst = [torch.zeros_like(t) for t in src]
+    si = torch.tensor([9, 0, 3, 3])
+    di = torch.tensor([1, 2, 5, 8])
+    ds = [t.to(gpu) for t in src]
+    dd = [t.to(gpu) for t in dst]
+    ik.gather_rows(list(zip(ds, dd)), si.to(gpu), di.to(gpu))
+    for s, d, outd in zip(src, dst, dd):
+        d.index_copy_(0, di, s.index_select(0, si))
+        assert torch.equal(outd.cpu(), d)

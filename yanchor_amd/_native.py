@@ -29,6 +29,21 @@ SIGNATURES: dict[str, list] = {
     "yh_anchor_read": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_anchor_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                          _i64, _i64, _i64, _i32, _p],
+    "yh_topk_sample": [_p, _i32, _i64, _p, _i64, _f32, _p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32,
+                       _i64, _f32, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "yh_presence_penalty": [_p, _p, _i64, _f32, _p],
+    "yh_counter_uniform": [_p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64, _p, _i64, _p],
+    "yh_decode_bookkeeping": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                              _i64, _i64, _p, _i64, _p],
+    "yh_cu_seqlens": [_p, _i32, _p, _i64, _p],
+    "yh_select_slots": [_p, _p, _i32, _p, _p, _i64, _p],
+    "yh_gather_rows": [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p],
+}
+
+# entry points that do not return a status
+PLAIN: dict[str, tuple] = {
+    "yh_topk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "yh_topk_segments": (None, [_i64, _i64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
 }
 
 _lib = None
@@ -53,6 +68,10 @@ def lib() -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = ctypes.c_int
+            fn.argtypes = args
+        for name, (res, args) in PLAIN.items():
+            fn = getattr(handle, name)
+            fn.restype = res
             fn.argtypes = args
         _lib = handle
     return _lib
