@@ -60,11 +60,55 @@ __device__ __forceinline__ void load8(const void* p, int64_t i, float* f) {
   }
 }
 
-// One workgroup per (batch row, group).  Each wave takes 64-slot blocks;
-// within a block, LPR = D/8 lanes cover one key row (8 elements each) and a
-// wave instruction covers RPI = 64/LPR rows, so NI = LPR instructions cover the
-// block.  The LPR-lane dot products are finished with a reduce-scatter
-// butterfly that leaves lane (s, rr) holding the logit of slot s*RPI + rr.
+// Raw 8 elements (16 B for 2-byte types, 32 B for fp32) of a key/value row.
+template <int DT> struct Raw8 { uint4 w[DT == YH_F32 ? 2 : 1]; };
+
+template <int DT>
+__device__ __forceinline__ void ld_raw8(Raw8<DT>& r, const void* p, int64_t i) {
+  if constexpr (DT == YH_F32) {
+    r.w[0] = reinterpret_cast<const uint4*>(static_cast<const float*>(p) + i)[0];
+    r.w[1] = reinterpret_cast<const uint4*>(static_cast<const float*>(p) + i)[1];
+  } else {
+    r.w[0] = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i)[0];
+  }
+}
+template <int DT>
+__device__ __forceinline__ void zero_raw8(Raw8<DT>& r) {
+#pragma unroll
+  for (int j = 0; j < (DT == YH_F32 ? 2 : 1); ++j) r.w[j] = make_uint4(0, 0, 0, 0);
+}
+template <int DT>
+__device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
+  if constexpr (DT == YH_F32) {
+    const uint32_t u[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = __uint_as_float(u[j]);
+  } else {
+    const uint32_t u[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == YH_BF16) {
+        f[2 * j] = __uint_as_float(u[j] << 16);
+        f[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+      } else {
+        f[2 * j] = f16_to_f32(u[j] & 0xffff);
+        f[2 * j + 1] = f16_to_f32(u[j] >> 16);
+      }
+    }
+  }
+}
+
+// One workgroup per (batch row, group), one pass over the committed slots.
+// Each wave takes 64-slot blocks: a ballot of the 64 positions gives the live
+// mask, then every lane issues all of its key AND value loads for the block at
+// once (dead slots are not fetched).  Within a block LPR = D/8 lanes cover one
+// row with 8 elements each and a wave instruction covers RPI = 64/LPR rows, so
+// NI = LPR instructions cover the block; a reduce-scatter butterfly over the
+// LPR lanes leaves lane (s, rr) with the logit of slot s*RPI + rr.  Each wave
+// keeps a running (max, sum, P.V) over its blocks (online softmax); waves are
+// combined at the end together with the sink logit 0, which has value 0:
+//   out = sum_w acc_w e^{m_w - M} / (e^{-M} + sum_w l_w e^{m_w - M}),
+//   M = max(0, max_w m_w).
 template <int DT, int D, int R>
 __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
   constexpr int LPR = D / 8;
@@ -72,9 +116,8 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
   constexpr int NI = LPR;
   static_assert(NI * RPI == 64, "64-slot blocks");
 
-  __shared__ float prob[R][kMaxCap];
-  __shared__ float wmax[kReadWaves][R];
-  __shared__ float wsum[kReadWaves][R];
+  __shared__ float wm[kReadWaves][R];
+  __shared__ float wl[kReadWaves][R];
   __shared__ float accs[kReadWaves][R][D];
 
   const int bg = blockIdx.x;
@@ -89,39 +132,55 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
     return;
   }
   const int64_t slot0 = (b * a.G + g) * static_cast<int64_t>(a.KC);  // first slot of (b, g)
-  const int32_t* pos = a.pos + slot0;
 
   float qf[R][8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    load8<DT>(a.q, qbase + static_cast<int64_t>(r) * D + s * 8, qf[r]);
+    Raw8<DT> raw;
+    ld_raw8<DT>(raw, a.q, qbase + static_cast<int64_t>(r) * D + s * 8);
+    cvt8<DT>(raw, qf[r]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) qf[r][j] *= a.scale;
   }
 
+  float m_run[R], l_run[R], acc[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m_run[r] = -INFINITY;
+    l_run[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[r][j] = 0.f;
+  }
+
   const int nblk = a.KC / 64;
-  // ---- logits ----
   for (int blk = wid; blk < nblk; blk += kReadWaves) {
+    const int base = blk * 64;
+    const uint64_t live = __ballot(a.pos[slot0 + base + lane] >= 0);
+    Raw8<DT> kr[NI], vr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int n = i * RPI + rr;
+      if ((live >> n) & 1ull) {
+        ld_raw8<DT>(kr[i], a.keys, (slot0 + base + n) * D + s * 8);
+        ld_raw8<DT>(vr[i], a.values, (slot0 + base + n) * D + s * 8);
+      } else {
+        zero_raw8<DT>(kr[i]);
+        zero_raw8<DT>(vr[i]);
+      }
+    }
     float part[R][NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int n = blk * 64 + i * RPI + rr;
       float kf[8];
-      if (pos[n] >= 0) {
-        load8<DT>(a.keys, (slot0 + n) * D + s * 8, kf);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kf[j] = 0.f;
-      }
+      cvt8<DT>(kr[i], kf);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        float acc = 0.f;
+        float x = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc = fmaf(qf[r][j], kf[j], acc);
-        part[r][i] = acc;
+        for (int j = 0; j < 8; ++j) x = fmaf(qf[r][j], kf[j], x);
+        part[r][i] = x;
       }
     }
-    // reduce-scatter over the LPR lanes of a row group
 #pragma unroll
     for (int m = LPR / 2, h = NI / 2; m >= 1; m >>= 1, h >>= 1) {
       const bool up = (s & m) != 0;
@@ -135,66 +194,28 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
         }
       }
     }
-    const int n = blk * 64 + s * RPI + rr;
-    const bool valid = pos[n] >= 0;
+    // lane (s, rr) holds the logit of slot s*RPI + rr of this block
+    const bool mine_live = (live >> (s * RPI + rr)) & 1ull;
 #pragma unroll
-    for (int r = 0; r < R; ++r) prob[r][n] = valid ? part[r][0] : -INFINITY;
-  }
-  __syncthreads();
-
-  // ---- softmax over [logits, 0] (the sink logit 0 carries value 0) ----
-  float m[R], den[R];
+    for (int r = 0; r < R; ++r) {
+      const float logit = mine_live ? part[r][0] : -INFINITY;
+      const float bm = wave_max(logit);
+      const float m_new = fmaxf(m_run[r], bm);
+      const float m_safe = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __expf(m_run[r] - m_safe);
+      const float p = __expf(logit - m_safe);
+      l_run[r] = l_run[r] * alpha + wave_sum(p);
+      m_run[r] = m_new;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float x = 0.f;  // the sink is part of the max
-    for (int n = tid; n < a.KC; n += kReadThreads) x = fmaxf(x, prob[r][n]);
-    x = wave_max(x);
-    if (lane == 0) wmax[wid][r] = x;
-  }
-  __syncthreads();
+      for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float x = wmax[0][r];
-#pragma unroll
-    for (int w = 1; w < kReadWaves; ++w) x = fmaxf(x, wmax[w][r]);
-    m[r] = x;
-    float sum = 0.f;
-    for (int n = tid; n < a.KC; n += kReadThreads) {
-      const float p = __expf(prob[r][n] - x);
-      prob[r][n] = p;
-      sum += p;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) wsum[wid][r] = sum;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float sum = __expf(-m[r]);
-#pragma unroll
-    for (int w = 0; w < kReadWaves; ++w) sum += wsum[w][r];
-    den[r] = sum;
-  }
-
-  // ---- P . V ----
-  float acc[R][8];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[r][j] = 0.f;
-  for (int blk = wid; blk < nblk; blk += kReadWaves) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int n = blk * 64 + i * RPI + rr;
-      if (pos[n] >= 0) {
+      for (int i = 0; i < NI; ++i) {
+        // weight of the row this lane loaded at instruction i (slot i*RPI + rr)
+        const float w = __shfl(p, rr * LPR + i, kWave);
         float vf[8];
-        load8<DT>(a.values, (slot0 + n) * D + s * 8, vf);
+        cvt8<DT>(vr[i], vf);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const float p = prob[r][n];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(p, vf[j], acc[r][j]);
-        }
+        for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(w, vf[j], acc[r][j]);
       }
     }
   }
@@ -210,13 +231,27 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) accs[wid][r][s * 8 + j] = acc[r][j];
   }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      wm[wid][r] = m_run[r];
+      wl[wid][r] = l_run[r];
+    }
+  }
   __syncthreads();
   for (int e = tid; e < R * D; e += kReadThreads) {
     const int r = e / D, d = e % D;
-    float x = 0.f;
+    float mx = 0.f;  // the sink logit
 #pragma unroll
-    for (int w = 0; w < kReadWaves; ++w) x += accs[w][r][d];
-    store_any(a.out, qbase + e, DT, x / den[r]);
+    for (int w = 0; w < kReadWaves; ++w) mx = fmaxf(mx, wm[w][r]);
+    float den = __expf(-mx), x = 0.f;
+#pragma unroll
+    for (int w = 0; w < kReadWaves; ++w) {
+      const float f = __expf(wm[w][r] - mx);  // 0 for a wave with no live slot
+      den = fmaf(wl[w][r], f, den);
+      x = fmaf(accs[w][r][d], f, x);
+    }
+    store_any(a.out, qbase + e, DT, x / den);
   }
 }
 
@@ -257,6 +292,38 @@ __device__ __forceinline__ void copy_row16(void* dst, const void* src, int n, in
   const uint4* s = static_cast<const uint4*>(src);
   uint4* d = static_cast<uint4*>(dst);
   for (int i = lane; i < n / 16; i += lanes) d[i] = s[i];
+}
+
+// Gather every selected row of one tensor into registers, then (after a
+// barrier) write them over the committed rows.  Sources include the committed
+// rows themselves, so no row may be written before all are read.
+__device__ __forceinline__ void commit_gather_pass(char* committed, const char* pending, const int32_t* chosen,
+                                                   const int32_t* cpos, int KC, int chunks, int total_pieces,
+                                                   int64_t rowbytes) {
+  const int tid = threadIdx.x;
+  uint4 buf[kMaxPieces];
+#pragma unroll
+  for (int i = 0; i < kMaxPieces; ++i) {
+    const int piece = tid + i * kCommitThreads;
+    buf[i] = make_uint4(0, 0, 0, 0);
+    if (piece < total_pieces) {
+      const int slot = piece / chunks, c = piece % chunks;
+      const int src = chosen[slot];
+      // an invalid selection reads committed row 0, as the reference does
+      const char* from = cpos[src] < 0 ? committed
+                         : (src < KC ? committed + src * rowbytes : pending + (src - KC) * rowbytes);
+      buf[i] = reinterpret_cast<const uint4*>(from)[c];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kMaxPieces; ++i) {
+    const int piece = tid + i * kCommitThreads;
+    if (piece < total_pieces) {
+      const int slot = piece / chunks, c = piece % chunks;
+      reinterpret_cast<uint4*>(committed + slot * rowbytes)[c] = buf[i];
+    }
+  }
 }
 
 // One workgroup per (batch row, group).  Push the token into pending[count];
@@ -328,33 +395,8 @@ __global__ void __launch_bounds__(kCommitThreads) anchor_commit_kernel(CommitArg
   const int total_pieces = KC * chunks;
   char* ck = static_cast<char*>(a.keys) + meta * rowbytes;
   char* cv = static_cast<char*>(a.values) + meta * rowbytes;
-#pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    char* committed = pass == 0 ? ck : cv;
-    const char* pending = pass == 0 ? pk : pv;
-    uint4 buf[kMaxPieces];
-#pragma unroll
-    for (int i = 0; i < kMaxPieces; ++i) {
-      const int piece = tid + i * kCommitThreads;
-      if (piece < total_pieces) {
-        const int slot = piece / chunks, c = piece % chunks;
-        const int src = chosen[slot];
-        // an invalid selection reads committed row 0, as the reference does
-        const char* from = cpos[src] < 0 ? committed
-                           : (src < KC ? committed + src * rowbytes : pending + (src - KC) * rowbytes);
-        buf[i] = reinterpret_cast<const uint4*>(from)[c];
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kMaxPieces; ++i) {
-      const int piece = tid + i * kCommitThreads;
-      if (piece < total_pieces) {
-        const int slot = piece / chunks, c = piece % chunks;
-        reinterpret_cast<uint4*>(committed + slot * rowbytes)[c] = buf[i];
-      }
-    }
-  }
+  commit_gather_pass(ck, pk, chosen, cpos, KC, chunks, total_pieces, rowbytes);
+  commit_gather_pass(cv, pv, chosen, cpos, KC, chunks, total_pieces, rowbytes);
   for (int n = tid; n < KC; n += kCommitThreads) {
     const int src = chosen[n];
     a.scores[meta + n] = cscore[src];

@@ -44,35 +44,85 @@ struct TopkArgs {
   const void* scores;      // [B, V]
   const uint8_t* seen;     // [B, V] or null
   uint64_t* work;          // [B, S, k] composite keys
-  int B, V, S, seg, k, dtype;
+  int B, V, S, seg, k;
   int64_t row_stride, seen_stride;
   float penalty;
 };
 
-__device__ __forceinline__ float load_score(const TopkArgs& a, int64_t b, int64_t i) {
-  float v = a.dtype == YH_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(a.scores)[b * a.row_stride + i])
-            : a.dtype == YH_F16 ? f16_to_f32(static_cast<const uint16_t*>(a.scores)[b * a.row_stride + i])
-                                : static_cast<const float*>(a.scores)[b * a.row_stride + i];
-  if (a.seen && a.seen[b * a.seen_stride + i]) v = v - a.penalty;
-  return v;
+constexpr int kVecPerThread = 8;                       // 4-element vectors per thread
+constexpr int kSegLen = kTopkThreads * 4 * kVecPerThread;  // 8192 elements per segment
+static_assert(kVecPerThread * 4 <= kMaxPerThread, "elements per thread");
+
+// 4 scores (with the presence penalty) starting at element i of row b.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load_scores4(const TopkArgs& a, int64_t b, int i, float* v) {
+  const int64_t off = b * a.row_stride + i;
+  if constexpr (VEC) {
+    if (i + 3 < a.V) {
+      if constexpr (DT == YH_F32) {
+        const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(a.scores) + off);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      } else {
+        const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.scores) + off);
+        if constexpr (DT == YH_BF16) {
+          v[0] = __uint_as_float(w.x << 16); v[1] = __uint_as_float(w.x & 0xffff0000u);
+          v[2] = __uint_as_float(w.y << 16); v[3] = __uint_as_float(w.y & 0xffff0000u);
+        } else {
+          v[0] = f16_to_f32(w.x & 0xffff); v[1] = f16_to_f32(w.x >> 16);
+          v[2] = f16_to_f32(w.y & 0xffff); v[3] = f16_to_f32(w.y >> 16);
+        }
+      }
+      if (a.seen) {
+        const uint32_t m = *reinterpret_cast<const uint32_t*>(a.seen + b * a.seen_stride + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if ((m >> (8 * j)) & 0xffu) v[j] = v[j] - a.penalty;
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (i + j < a.V) {
+      v[j] = Elem<DT>::ld(static_cast<const typename Elem<DT>::T*>(a.scores), off + j);
+      if (a.seen && a.seen[b * a.seen_stride + i + j]) v[j] = v[j] - a.penalty;
+    } else {
+      v[j] = NAN;  // marks "no element"; never becomes a candidate
+    }
+  }
 }
 
+template <int DT, bool VEC>
 __global__ void __launch_bounds__(kTopkThreads) topk_segment_kernel(TopkArgs a) {
   __shared__ uint64_t maxima[kTopkThreads];
   __shared__ uint64_t cand[kCandCap];
   __shared__ uint64_t thr_s;
   __shared__ int ncand;
   const int seg = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int lo = seg * a.seg;
-  const int hi = min(a.V, lo + a.seg);
-  uint64_t best = 0;  // key 0 is below every real element key
+  const int lo = seg * kSegLen;
   if (tid == 0) {
     ncand = 0;
     thr_s = 0;
   }
-  for (int i = lo + tid; i < hi; i += kTopkThreads) {
-    const uint64_t c = ckey(load_score(a, b, i), static_cast<uint32_t>(i));
-    best = c > best ? c : best;
+  // issue every load of this thread first, then build the keys
+  float v[kVecPerThread][4];
+#pragma unroll
+  for (int c = 0; c < kVecPerThread; ++c) {
+    const int i = lo + (c * kTopkThreads + tid) * 4;
+    if (i < a.V) load_scores4<DT, VEC>(a, b, i, v[c]);
+    else v[c][0] = v[c][1] = v[c][2] = v[c][3] = NAN;
+  }
+  uint64_t key[kVecPerThread][4];
+  uint64_t best = 0;  // key 0 is below every real element key
+#pragma unroll
+  for (int c = 0; c < kVecPerThread; ++c) {
+    const int i = lo + (c * kTopkThreads + tid) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool real = i + j < a.V;
+      key[c][j] = real ? ckey(v[c][j], static_cast<uint32_t>(i + j)) : 0ull;
+      best = key[c][j] > best ? key[c][j] : best;
+    }
   }
   maxima[tid] = best;
   __syncthreads();
@@ -87,12 +137,15 @@ __global__ void __launch_bounds__(kTopkThreads) topk_segment_kernel(TopkArgs a) 
   }
   __syncthreads();
   const uint64_t thr = thr_s;
-  for (int i = lo + tid; i < hi; i += kTopkThreads) {
-    const uint64_t c = ckey(load_score(a, b, i), static_cast<uint32_t>(i));
-    if (c >= thr && c != 0) {
-      const int slot = atomicAdd(&ncand, 1);
-      if (slot < kCandCap) cand[slot] = c;
-    }
+  if (best >= thr && best != 0) {
+#pragma unroll
+    for (int c = 0; c < kVecPerThread; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (key[c][j] >= thr && key[c][j] != 0) {
+          const int slot = atomicAdd(&ncand, 1);
+          if (slot < kCandCap) cand[slot] = key[c][j];
+        }
   }
   __syncthreads();
   const int n = min(ncand, kCandCap);
@@ -233,7 +286,7 @@ extern "C" int yh_topk_sample(const void* scores, int dtype, int64_t row_stride,
                               int64_t workspace_bytes, int64_t B, int64_t V, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(scores && tokens && workspace && attempt_ids, "topk_sample: null pointer");
-  YH_CHECK_ARG(B >= 0 && V > 0 && V < (1LL << 31) - 1, "topk_sample: bad B/V");
+  YH_CHECK_ARG(B >= 0 && V > 0 && V <= 64LL * kSegLen, "topk_sample: V must lie in [1, %d]", 64 * kSegLen);
   YH_CHECK_ARG(top_k >= 1 && top_k <= kMaxK && top_k <= V, "topk_sample: top_k must lie in [1, %d]", kMaxK);
   YH_CHECK_ARG(dtype == YH_F32 || dtype == YH_BF16 || dtype == YH_F16, "topk_sample: unsupported dtype");
   YH_CHECK_ARG(mode == YH_SAMPLE_FUSED || mode == YH_SAMPLE_TORCH, "topk_sample: unknown mode %d", mode);
@@ -248,9 +301,20 @@ extern "C" int yh_topk_sample(const void* scores, int dtype, int64_t row_stride,
   int S = 0, seg = 0;
   yh_topk_segments(V, top_k, &S, &seg);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  TopkArgs ta{scores, seen, static_cast<uint64_t*>(workspace), (int)B, (int)V, S, seg, (int)top_k, dtype,
+  TopkArgs ta{scores, seen, static_cast<uint64_t*>(workspace), (int)B, (int)V, S, seg, (int)top_k,
               row_stride, seen_stride, penalty};
-  hipLaunchKernelGGL(topk_segment_kernel, dim3(S, static_cast<unsigned>(B)), dim3(kTopkThreads), 0, st, ta);
+  const size_t esz = dtype == YH_F32 ? 4 : 2;
+  const bool vec = (reinterpret_cast<uintptr_t>(scores) % (4 * esz)) == 0 && row_stride % 4 == 0 &&
+                   (seen == nullptr || ((reinterpret_cast<uintptr_t>(seen) & 3) == 0 && seen_stride % 4 == 0));
+  const dim3 grid(S, static_cast<unsigned>(B));
+  switch (dtype * 2 + (vec ? 1 : 0)) {
+    case YH_F32 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_F32, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
+    case YH_F32 * 2: hipLaunchKernelGGL((topk_segment_kernel<YH_F32, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
+    case YH_BF16 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_BF16, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
+    case YH_BF16 * 2: hipLaunchKernelGGL((topk_segment_kernel<YH_BF16, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
+    case YH_F16 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_F16, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
+    default: hipLaunchKernelGGL((topk_segment_kernel<YH_F16, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
+  }
   YH_CHECK_LAUNCH("topk_segment");
   SampleArgs sa{static_cast<const uint64_t*>(workspace), attempt_ids, steps, tokens, out_values, out_indices,
                 (int)B, S, (int)top_k, mode, step, static_cast<uint32_t>(seed & 0xffffffffu),
@@ -261,17 +325,11 @@ extern "C" int yh_topk_sample(const void* scores, int dtype, int64_t row_stride,
 }
 
 extern "C" void yh_topk_segments(int64_t V, int64_t top_k, int* n_segments, int* seg_len) {
-  // about 32 elements per thread, at most 64 segments; k * per-thread <= 4096
-  int64_t S = (V + yh::kTopkThreads * 32 - 1) / (yh::kTopkThreads * 32);
-  if (S < 1) S = 1;
-  if (S > 64) S = 64;
-  int64_t seg = (V + S - 1) / S;
-  while ((seg + yh::kTopkThreads - 1) / yh::kTopkThreads * (top_k < 1 ? 1 : top_k) > yh::kCandCap && S < 64) {
-    ++S;
-    seg = (V + S - 1) / S;
-  }
-  *n_segments = static_cast<int>(S);
-  *seg_len = static_cast<int>(seg);
+  // fixed 8192-element segments: 256 threads x 8 vectors of 4; the candidate
+  // bound k * 32 <= 2048 fits the LDS list for every k <= 64
+  (void)top_k;
+  *n_segments = static_cast<int>((V + yh::kSegLen - 1) / yh::kSegLen);
+  *seg_len = yh::kSegLen;
 }
 
 extern "C" int64_t yh_topk_workspace_bytes(int64_t B, int64_t V, int64_t top_k) {
