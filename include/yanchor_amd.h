@@ -65,6 +65,42 @@ int yh_gdn_recurrent(const void* q, const void* k, const void* v, const void* g,
                      int qkv_dtype, int g_dtype, int beta_dtype, yh_stream_t stream);
 
 /*
+ * Packed-varlen form of yh_gdn_recurrent: n_seqs sequences concatenated on one
+ * token axis, sequence b owning tokens [cu_seqlens[b], cu_seqlens[b + 1]).
+ * q, k [total, H, K]; v, o [total, HV, V]; g, beta [total, HV]; state
+ * [n_state_rows, HV, K, V] fp32 in place (row b, or state_indices[b]).
+ * Replaces the cu_seqlens form of the FLA call mirrored at
+ * runtime/model/inference_kernels.py:147 and the per-request prefill loop of
+ * the vLLM adapter (vllm_yanchor.py:85-96).
+ */
+int yh_gdn_recurrent_varlen(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                            float* state, const int32_t* state_indices, const int32_t* cu_seqlens, void* o,
+                            int64_t n_seqs, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t n_state_rows,
+                            float scale, int use_qk_l2norm, int qkv_dtype, int g_dtype, int beta_dtype,
+                            yh_stream_t stream);
+
+/*
+ * Chunked packed-varlen prefill of the gated delta rule on bf16 MFMA (chunk 64).
+ *
+ * Replaces FLA chunk_gated_delta_rule with cu_seqlens (bound at
+ * modeling_yanchor.py:397, 403; called at transformers wheel
+ * models/qwen3_5/modeling_qwen3_5.py:519-529) and follows
+ * torch_chunk_gated_delta_rule (same file, 234-311).
+ *
+ *   q, k [total, H, 128] bf16; v, o [total, HV, V] bf16 (V a multiple of 64);
+ *   g, beta [total, HV] (f32 / bf16 / f16); cu_seqlens int32 [n_seqs + 1]
+ *   initial_state NULL (zeros) or fp32 [n_seqs, HV, 128, V] (read only)
+ *   final_state fp32 [n_seqs, HV, 128, V] (written)
+ *   order NULL or int32 [n_seqs]: dispatch order of the sequences (longest
+ *   first balances the grid); every sequence must appear once.
+ */
+int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                        const float* initial_state, float* final_state, void* o, const int32_t* cu_seqlens,
+                        const int32_t* order, int64_t n_seqs, int64_t H, int64_t HV, int64_t K, int64_t V,
+                        float scale, int use_qk_l2norm, int qkv_dtype, int g_dtype, int beta_dtype,
+                        yh_stream_t stream);
+
+/*
  * Anchor memory, decode read of the committed slots.
  *
  * Replaces committed_gqa (_read_parts + _read_reduce) in

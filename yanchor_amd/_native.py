@@ -26,6 +26,10 @@ _f32 = ctypes.c_float
 SIGNATURES: dict[str, list] = {
     "yh_gdn_recurrent": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                          _f32, _i32, _i32, _i32, _i32, _p],
+    "yh_gdn_recurrent_varlen": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                                _i32, _i32, _i32, _i32, _p],
+    "yh_gdn_chunk_varlen": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
+                            _i32, _i32, _i32, _p],
     "yh_anchor_read": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_anchor_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                          _i64, _i64, _i64, _i32, _p],

@@ -37,6 +37,7 @@ struct GdnArgs {
   const void* beta;
   float* state;
   const int32_t* idx;
+  const int32_t* cu;  // packed varlen offsets [B + 1] or null
   void* o;
   int B, T, H, HV, V;
   int64_t n_rows;
@@ -154,11 +155,14 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
   const int col0 = vt * VT + lc * 4;
   const bool norm_wave = wid == 0;
 
+  // tokens of row b: [t0, t0 + Tb) of the token axis
+  const int64_t t0 = a.cu ? static_cast<int64_t>(a.cu[b]) : static_cast<int64_t>(b) * a.T;
+  const int Tb = a.cu ? a.cu[b + 1] - a.cu[b] : a.T;
   int64_t srow = a.idx ? static_cast<int64_t>(a.idx[b]) : static_cast<int64_t>(b);
   if (srow < 0 || srow >= a.n_rows) {
     if (rg == 0) {
-      for (int t = 0; t < a.T; ++t) {
-        const int64_t tok = static_cast<int64_t>(b) * a.T + t;
+      for (int t = 0; t < Tb; ++t) {
+        const int64_t tok = t0 + t;
         store4<DT>(a.o, (tok * a.HV + hv) * a.V + col0, f4(0.f));
       }
     }
@@ -166,7 +170,7 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
   }
 
   TokIn<DT, KPL> in;
-  load_tok<DT, K, KPL>(in, a, static_cast<int64_t>(b) * a.T, hk, hv, col0, norm_wave, lane);
+  if (Tb > 0) load_tok<DT, K, KPL>(in, a, t0, hk, hv, col0, norm_wave, lane);
 
   float* S = a.state + (srow * a.HV + hv) * static_cast<int64_t>(K) * a.V + col0;
   float4 s[RPT];
@@ -174,9 +178,9 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
   for (int i = 0; i < RPT; ++i)
     s[i] = ld_stream4(S + static_cast<int64_t>(rg + i * RG) * a.V);
 
-  for (int t = 0; t < a.T; ++t) {
+  for (int t = 0; t < Tb; ++t) {
     const int buf = t & 1;
-    const int64_t tok = static_cast<int64_t>(b) * a.T + t;
+    const int64_t tok = t0 + t;
     if (norm_wave) {
       float ssk = 0.f, ssq = 0.f, dot = 0.f, kf[KPL], qf[KPL];
 #pragma unroll
@@ -233,7 +237,7 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
       sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
     }
     const float kq = kq_s[buf];
-    if (t + 1 < a.T) load_tok<DT, K, KPL>(in, a, tok + 1, hk, hv, col0, norm_wave, lane);
+    if (t + 1 < Tb) load_tok<DT, K, KPL>(in, a, tok + 1, hk, hv, col0, norm_wave, lane);
     float4 d;
     d.x = bt * (vv.x - eg * kv.x);
     d.y = bt * (vv.y - eg * kv.y);
@@ -290,9 +294,10 @@ void pick_tile(int K, int V, int64_t B, int64_t HV, int* vt, int* nt) {
 }  // namespace
 }  // namespace yh
 
-extern "C" int yh_gdn_recurrent(const void* q, const void* k, const void* v, const void* g,
+
+static int gdn_recurrent_impl(const void* q, const void* k, const void* v, const void* g,
                                 const void* beta, float* state, const int32_t* state_indices,
-                                void* o, int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K,
+                                const int32_t* cu_seqlens, void* o, int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K,
                                 int64_t V, int64_t n_state_rows, float scale, int use_qk_l2norm,
                                 int qkv_dtype, int g_dtype, int beta_dtype, yh_stream_t stream) {
   using namespace yh;
@@ -315,7 +320,7 @@ extern "C" int yh_gdn_recurrent(const void* q, const void* k, const void* v, con
                  "gdn_recurrent: v and o must be aligned to 4 elements");
   }
   if (B == 0 || T == 0) return YH_OK;
-  GdnArgs a{q, k, v, g, beta, state, state_indices, o,
+  GdnArgs a{q, k, v, g, beta, state, state_indices, cu_seqlens, o,
             (int)B, (int)T, (int)H, (int)HV, (int)V, n_state_rows, scale, use_qk_l2norm ? 1 : 0,
             g_dtype, beta_dtype};
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -336,4 +341,25 @@ extern "C" int yh_gdn_recurrent(const void* q, const void* k, const void* v, con
   if (vt == 64 && nt == 64) return launch_tile<64, 64, 64>(qkv_dtype, a, st);
   if (vt == 32 && nt == 64) return launch_tile<64, 32, 64>(qkv_dtype, a, st);
   return launch_tile<64, 64, 128>(qkv_dtype, a, st);
+}
+
+extern "C" int yh_gdn_recurrent(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                float* state, const int32_t* state_indices, void* o, int64_t B, int64_t T,
+                                int64_t H, int64_t HV, int64_t K, int64_t V, int64_t n_state_rows, float scale,
+                                int use_qk_l2norm, int qkv_dtype, int g_dtype, int beta_dtype, yh_stream_t stream) {
+  return gdn_recurrent_impl(q, k, v, g, beta, state, state_indices, nullptr, o, B, T, H, HV, K, V, n_state_rows,
+                            scale, use_qk_l2norm, qkv_dtype, g_dtype, beta_dtype, stream);
+}
+
+extern "C" int yh_gdn_recurrent_varlen(const void* q, const void* k, const void* v, const void* g,
+                                       const void* beta, float* state, const int32_t* state_indices,
+                                       const int32_t* cu_seqlens, void* o, int64_t n_seqs, int64_t H, int64_t HV,
+                                       int64_t K, int64_t V, int64_t n_state_rows, float scale, int use_qk_l2norm,
+                                       int qkv_dtype, int g_dtype, int beta_dtype, yh_stream_t stream) {
+  if (cu_seqlens == nullptr) {
+    yh::set_error("gdn_recurrent_varlen: cu_seqlens is required");
+    return YH_ERR_INVALID;
+  }
+  return gdn_recurrent_impl(q, k, v, g, beta, state, state_indices, cu_seqlens, o, n_seqs, 1, H, HV, K, V,
+                            n_state_rows, scale, use_qk_l2norm, qkv_dtype, g_dtype, beta_dtype, stream);
 }

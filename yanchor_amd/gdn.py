@@ -82,3 +82,78 @@ def fused_recurrent_gated_delta_rule(q, k, v, g=None, beta=None, scale=None, ini
                                       output_final_state=output_final_state,
                                       use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
                                       scale=scale, inplace=bool(output_final_state), **kw)
+
+
+def _packed_or_batched(query, key, value, g, beta, cu_seqlens):
+    if cu_seqlens is None:
+        return None
+    if query.shape[0] != 1:
+        raise ValueError("with cu_seqlens the inputs must be packed as [1, total, ...]")
+    cu = cu_seqlens.to(device=query.device, dtype=torch.int32).contiguous()
+    if cu.ndim != 1 or cu.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D offset vector")
+    return cu
+
+
+def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, initial_state=None,
+                           output_final_state=False, use_qk_l2norm_in_kernel=False, cu_seqlens=None,
+                           lengths=None, force_recurrent=False, **unused):
+    """Prefill form of the gated delta rule with the FLA / Transformers
+    signature (bound at modeling_yanchor.py:397, 403; called at transformers
+    wheel models/qwen3_5/modeling_qwen3_5.py:519-529).
+
+    Batched: query/key ``[B, T, H, K]``, value ``[B, T, HV, V]``, g/beta
+    ``[B, T, HV]``, initial_state ``[B, HV, K, V]``.  Packed varlen:
+    ``cu_seqlens`` (int, N + 1 offsets) with inputs ``[1, total, ...]`` and
+    initial_state ``[N, HV, K, V]``.  ``initial_state`` is read, not modified;
+    returns ``(o, final_state or None)``.
+
+    Packed inputs with K = 128, V a multiple of 64 and bf16 q/k/v run the MFMA
+    chunk kernel (chunk 64); other shapes, or ``force_recurrent=True``, run the
+    token-recurrent kernel over each sequence.  ``lengths`` (host ints, one per
+    sequence) lets the chunk kernel start the longest sequences first.
+    """
+    if g is None or beta is None:
+        raise ValueError("chunk_gated_delta_rule needs g and beta")
+    cu = _packed_or_batched(query, key, value, g, beta, cu_seqlens)
+    if cu is None:
+        o, st = recurrent_gated_delta_rule(query, key, value, g=g, beta=beta, initial_state=initial_state,
+                                           output_final_state=True,
+                                           use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel, scale=scale,
+                                           inplace=False)
+        return o, (st if output_final_state else None)
+    if query.ndim != 4 or key.shape != query.shape or value.ndim != 4:
+        raise ValueError("query/key must be [1, total, H, K] and value [1, total, HV, V]")
+    _, total, h, kd = key.shape
+    hv, vd = value.shape[2], value.shape[3]
+    n = cu.numel() - 1
+    if g.shape != (1, total, hv) or beta.shape != (1, total, hv) or value.shape[1] != total:
+        raise ValueError("value/g/beta shapes do not match the packed query/key")
+    if query.dtype != key.dtype or value.dtype != key.dtype:
+        raise ValueError("query, key and value must share one dtype")
+    dev = N.require_device(query, key, value, g, beta, initial_state)
+    if initial_state is not None and (initial_state.shape != (n, hv, kd, vd)
+                                      or initial_state.dtype != torch.float32):
+        raise ValueError(f"initial_state must be float32 [{n}, {hv}, {kd}, {vd}]")
+    q, k, v, g_, be = (_contig(x) for x in (query, key, value, g, beta))
+    o = torch.empty(1, total, hv, vd, device=dev, dtype=value.dtype)
+    sc = float(kd ** -0.5 if scale is None else scale)
+    if kd == 128 and vd % 64 == 0 and q.dtype == torch.bfloat16 and not force_recurrent:
+        h0 = None if initial_state is None else initial_state.contiguous()
+        state = torch.empty(n, hv, kd, vd, device=dev, dtype=torch.float32)
+        order = None
+        if lengths is not None:  # longest sequences first balances the grid
+            order = torch.tensor(sorted(range(n), key=lambda i: -int(lengths[i])), dtype=torch.int32,
+                                 device=dev)
+        N.call("yh_gdn_chunk_varlen", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_.data_ptr(), be.data_ptr(),
+               N.ptr(h0), state.data_ptr(), o.data_ptr(), cu.data_ptr(), N.ptr(order), n, h, hv, kd, vd, sc,
+               int(bool(use_qk_l2norm_in_kernel)), N.code(q), N.code(g_), N.code(be), N.stream_of(q))
+        return o, (state if output_final_state else None)
+    if initial_state is None:
+        state = torch.zeros(n, hv, kd, vd, device=dev, dtype=torch.float32)
+    else:
+        state = initial_state.clone()
+    N.call("yh_gdn_recurrent_varlen", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_.data_ptr(), be.data_ptr(),
+           state.data_ptr(), None, cu.data_ptr(), o.data_ptr(), n, h, hv, kd, vd, n, sc,
+           int(bool(use_qk_l2norm_in_kernel)), N.code(q), N.code(g_), N.code(be), N.stream_of(q))
+    return o, (state if output_final_state else None)

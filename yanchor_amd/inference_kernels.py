@@ -176,10 +176,11 @@ def select_slots(finished, slot_rows=None, *, mode):
         if slot_rows.shape != (n,):
             raise ValueError("slot_rows must match finished")
         rows = slot_rows.to(torch.int64).contiguous()
+    fin = finished.contiguous()
     out = torch.empty(n, dtype=torch.int64, device=dev)
     count = torch.empty(1, dtype=torch.int64, device=dev)
-    N.call("yh_select_slots", finished.contiguous().data_ptr(), N.ptr(rows), int(mode), out.data_ptr(),
-           count.data_ptr(), n, N.stream_of(finished))
+    N.call("yh_select_slots", fin.data_ptr(), N.ptr(rows), int(mode), out.data_ptr(), count.data_ptr(), n,
+           N.stream_of(fin))
     return out, count
 
 

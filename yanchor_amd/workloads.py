@@ -108,3 +108,39 @@ def anchor_state(B, G, capacity, chunk, D, *, p_live=0.7, seed=SEED0 + 1, dtype=
 
 def anchor_query(B, H, D, *, seed=SEED0 + 2, dtype=torch.bfloat16):
     return torch.randn(B, 1, H, D, generator=_gen(seed)).to(dtype)
+
+
+@dataclass
+class PackedInputs:
+    q: torch.Tensor        # [1, total, H, K]
+    k: torch.Tensor
+    v: torch.Tensor        # [1, total, HV, V]
+    g: torch.Tensor        # [1, total, HV]
+    beta: torch.Tensor
+    cu_seqlens: torch.Tensor  # int32 [N + 1]
+    lengths: list
+    h0: torch.Tensor | None
+
+    def to(self, device) -> "PackedInputs":
+        return PackedInputs(*(x.to(device) for x in (self.q, self.k, self.v, self.g, self.beta,
+                                                       self.cu_seqlens)),
+                            self.lengths, None if self.h0 is None else self.h0.to(device))
+
+
+def prefill_lengths(n=32, lo=512, hi=8192, seed=SEED0 + 2):
+    """Sequence lengths uniform in [lo, hi] (seeded)."""
+    return torch.randint(lo, hi + 1, (n,), generator=_gen(seed)).tolist()
+
+
+def packed_inputs(lengths, H, HV, K, V, *, dtype=torch.bfloat16, seed=SEED0 + 2, h0_std=0.0):
+    """Packed varlen inputs with the distributions of the module docstring."""
+    gen = _gen(seed)
+    total = int(sum(lengths))
+    q = _unit(torch.randn(1, total, H, K, generator=gen))
+    k = _unit(torch.randn(1, total, H, K, generator=gen))
+    v = torch.randn(1, total, HV, V, generator=gen)
+    beta = torch.sigmoid(torch.randn(1, total, HV, generator=gen))
+    g = F.logsigmoid(torch.randn(1, total, HV, generator=gen) + 3.0)
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0).tolist()), dtype=torch.int32)
+    h0 = torch.randn(len(lengths), HV, K, V, generator=gen) * h0_std if h0_std else None
+    return PackedInputs(q.to(dtype), k.to(dtype), v.to(dtype), g, beta, cu, list(lengths), h0)
