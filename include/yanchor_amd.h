@@ -123,6 +123,19 @@ int yh_anchor_read(const void* query, const void* keys, const void* values, cons
                    int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream);
 
 /*
+ * Decode attention of one query token over a physical ring of `window` cached
+ * key/value slots: the read of yh_anchor_read without the sink (plain softmax
+ * over the live slots; no live slot gives 0).  positions [NB, G, window] int32
+ * marks live slots (>= 0).  Replaces the physical-ring SWA decode attention
+ * (fixed_memory_physical_ring_decode_attention, runtime/model/
+ * inference_kernels.py:555-640) for D in {64, 128}, H / G in {1, 2, 4} and a
+ * window that is a multiple of 64, at most 1024.
+ */
+int yh_window_attend(const void* query, const void* keys, const void* values, const int32_t* positions,
+                     const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t window, int64_t D,
+                     int64_t n_state_rows, int dtype, yh_stream_t stream);
+
+/*
  * Anchor memory, decode push and Top-K commit, IN PLACE on the memory state.
  *
  * Replaces commit_decode (_push_select, _gather_commit, _write_commit,

@@ -109,7 +109,7 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 // combined at the end together with the sink logit 0, which has value 0:
 //   out = sum_w acc_w e^{m_w - M} / (e^{-M} + sum_w l_w e^{m_w - M}),
 //   M = max(0, max_w m_w).
-template <int DT, int D, int R>
+template <int DT, int D, int R, bool SINK>
 __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
   constexpr int LPR = D / 8;
   constexpr int RPI = kWave / LPR;
@@ -241,17 +241,18 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
   __syncthreads();
   for (int e = tid; e < R * D; e += kReadThreads) {
     const int r = e / D, d = e % D;
-    float mx = 0.f;  // the sink logit
+    float mx = SINK ? 0.f : -INFINITY;  // the sink logit is 0
 #pragma unroll
     for (int w = 0; w < kReadWaves; ++w) mx = fmaxf(mx, wm[w][r]);
-    float den = __expf(-mx), x = 0.f;
+    const float ms = mx == -INFINITY ? 0.f : mx;  // no live slot and no sink
+    float den = SINK ? __expf(-ms) : 0.f, x = 0.f;
 #pragma unroll
     for (int w = 0; w < kReadWaves; ++w) {
-      const float f = __expf(wm[w][r] - mx);  // 0 for a wave with no live slot
+      const float f = __expf(wm[w][r] - ms);  // 0 for a wave with no live slot
       den = fmaf(wl[w][r], f, den);
       x = fmaf(accs[w][r][d], f, x);
     }
-    store_any(a.out, qbase + e, DT, x / den);
+    store_any(a.out, qbase + e, DT, den > 0.f ? x / den : 0.f);
   }
 }
 
@@ -417,13 +418,13 @@ __global__ void anchor_advance_kernel(int64_t* count, int64_t* total, const uint
   total[b] += act;
 }
 
-template <int DT, int D>
+template <int DT, int D, bool SINK>
 int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(kReadThreads);
   switch (R) {
-    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK>), grid, block, 0, st, a); break;
     default: set_error("anchor_read: heads per group must be 1, 2 or 4 (got %d)", R); return YH_ERR_INVALID;
   }
   YH_CHECK_LAUNCH("anchor_read");
@@ -431,9 +432,9 @@ int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
 }
 
 template <int DT>
-int launch_read_d(int D, int R, const ReadArgs& a, hipStream_t st) {
-  if (D == 128) return launch_read_r<DT, 128>(R, a, st);
-  if (D == 64) return launch_read_r<DT, 64>(R, a, st);
+int launch_read_d(int D, int R, bool sink, const ReadArgs& a, hipStream_t st) {
+  if (D == 128) return sink ? launch_read_r<DT, 128, true>(R, a, st) : launch_read_r<DT, 128, false>(R, a, st);
+  if (D == 64) return sink ? launch_read_r<DT, 64, true>(R, a, st) : launch_read_r<DT, 64, false>(R, a, st);
   set_error("anchor_read: head dim must be 64 or 128 (got %d)", D);
   return YH_ERR_INVALID;
 }
@@ -441,7 +442,7 @@ int launch_read_d(int D, int R, const ReadArgs& a, hipStream_t st) {
 }  // namespace
 }  // namespace yh
 
-extern "C" int yh_anchor_read(const void* query, const void* keys, const void* values,
+static int anchor_read_impl(bool sink, const void* query, const void* keys, const void* values,
                               const int32_t* positions, const int32_t* indices, void* out,
                               int64_t B, int64_t H, int64_t G, int64_t capacity, int64_t D,
                               int64_t n_state_rows, int dtype, yh_stream_t stream) {
@@ -465,10 +466,24 @@ extern "C" int yh_anchor_read(const void* query, const void* keys, const void* v
   const int R = static_cast<int>(H / G);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case YH_BF16: return launch_read_d<YH_BF16>((int)D, R, a, st);
-    case YH_F16: return launch_read_d<YH_F16>((int)D, R, a, st);
-    default: return launch_read_d<YH_F32>((int)D, R, a, st);
+    case YH_BF16: return launch_read_d<YH_BF16>((int)D, R, sink, a, st);
+    case YH_F16: return launch_read_d<YH_F16>((int)D, R, sink, a, st);
+    default: return launch_read_d<YH_F32>((int)D, R, sink, a, st);
   }
+}
+
+extern "C" int yh_anchor_read(const void* query, const void* keys, const void* values, const int32_t* positions,
+                              const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t capacity,
+                              int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream) {
+  return anchor_read_impl(true, query, keys, values, positions, indices, out, B, H, G, capacity, D, n_state_rows,
+                          dtype, stream);
+}
+
+extern "C" int yh_window_attend(const void* query, const void* keys, const void* values, const int32_t* positions,
+                                const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t window,
+                                int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream) {
+  return anchor_read_impl(false, query, keys, values, positions, indices, out, B, H, G, window, D, n_state_rows,
+                          dtype, stream);
 }
 
 extern "C" int yh_anchor_commit(const void* key, const void* value, const float* score,

@@ -115,8 +115,10 @@ __device__ __forceinline__ f32x4v mfma(bf16x8_t a, bf16x8_t b, f32x4v c) {
 }
 
 // (I + L)^{-1} for strictly lower triangular L (64 x 64, fp32, LDS), by 16 x 16
-// blocks: diagonal blocks by column-parallel forward substitution, then the
-// off-diagonal blocks level by level, T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj.
+// blocks: the diagonal blocks by column-parallel forward substitution (one lane
+// per column, L rows read as 16-byte vectors), then the off-diagonal blocks
+// level by level, T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj, one thread per
+// 4 adjacent columns so T and X rows are read as vectors.
 __device__ void invert_unit_lower(Smem& sm) {
   const int tid = threadIdx.x;
   if (tid < 64) {
@@ -124,9 +126,12 @@ __device__ void invert_unit_lower(Smem& sm) {
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
+      float lr[16];
+      ld8f(&sm.l[(16 * b + i) * SF + 16 * b], lr);
+      ld8f(&sm.l[(16 * b + i) * SF + 16 * b + 8], lr + 8);
       float acc = i == j ? 1.f : 0.f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(-sm.l[(16 * b + i) * SF + 16 * b + m], x[m], acc);
+      for (int m = 0; m < i; ++m) acc = fmaf(-lr[m], x[m], acc);
       x[i] = acc;
     }
 #pragma unroll
@@ -141,25 +146,44 @@ __device__ void invert_unit_lower(Smem& sm) {
   __syncthreads();
 #pragma unroll 1
   for (int lev = 1; lev < 4; ++lev) {
-    const int nb = 4 - lev;  // blocks (i, i - lev), i = lev..3
-    for (int e = tid; e < nb * 256; e += kThreads) {
-      const int bi = e >> 8, r = (e >> 4) & 15, c = e & 15;
+    const int nb = 4 - lev;  // blocks (i, i - lev), i = lev..3; 64 threads per block
+    if (tid < nb * 64) {
+      const int bi = tid >> 6, r = (tid >> 2) & 15, c4 = (tid & 3) * 4;
       const int i = lev + bi, j = i - lev;
-      float acc = 0.f;
-      for (int m = j; m < i; ++m)
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int m = j; m < i; ++m) {
+        float lr[16];
+        ld8f(&sm.l[(16 * i + r) * SF + 16 * m], lr);
+        ld8f(&sm.l[(16 * i + r) * SF + 16 * m + 8], lr + 8);
 #pragma unroll
-        for (int q = 0; q < 16; ++q)
-          acc = fmaf(sm.l[(16 * i + r) * SF + 16 * m + q], sm.t[(16 * m + q) * SF + 16 * j + c], acc);
-      sm.x[bi * 256 + r * 16 + c] = acc;
+        for (int q = 0; q < 16; ++q) {
+          const float4 tv = *reinterpret_cast<const float4*>(&sm.t[(16 * m + q) * SF + 16 * j + c4]);
+          acc.x = fmaf(lr[q], tv.x, acc.x);
+          acc.y = fmaf(lr[q], tv.y, acc.y);
+          acc.z = fmaf(lr[q], tv.z, acc.z);
+          acc.w = fmaf(lr[q], tv.w, acc.w);
+        }
+      }
+      *reinterpret_cast<float4*>(&sm.x[bi * 256 + r * 16 + c4]) = acc;
     }
     __syncthreads();
-    for (int e = tid; e < nb * 256; e += kThreads) {
-      const int bi = e >> 8, r = (e >> 4) & 15, c = e & 15;
+    if (tid < nb * 64) {
+      const int bi = tid >> 6, r = (tid >> 2) & 15, c4 = (tid & 3) * 4;
       const int i = lev + bi, j = i - lev;
-      float acc = 0.f;
+      float tr[16];
+      ld8f(&sm.t[(16 * i + r) * SF + 16 * i], tr);
+      ld8f(&sm.t[(16 * i + r) * SF + 16 * i + 8], tr + 8);
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int q = 0; q < 16; ++q) acc = fmaf(sm.t[(16 * i + r) * SF + 16 * i + q], sm.x[bi * 256 + q * 16 + c], acc);
-      sm.t[(16 * i + r) * SF + 16 * j + c] = -acc;
+      for (int q = 0; q < 16; ++q) {
+        const float4 xv = *reinterpret_cast<const float4*>(&sm.x[bi * 256 + q * 16 + c4]);
+        acc.x = fmaf(tr[q], xv.x, acc.x);
+        acc.y = fmaf(tr[q], xv.y, acc.y);
+        acc.z = fmaf(tr[q], xv.z, acc.z);
+        acc.w = fmaf(tr[q], xv.w, acc.w);
+      }
+      *reinterpret_cast<float4*>(&sm.t[(16 * i + r) * SF + 16 * j + c4]) =
+          make_float4(-acc.x, -acc.y, -acc.z, -acc.w);
     }
     __syncthreads();
   }
@@ -334,7 +358,9 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_kernel(ChunkArgs a) {
       const int tau = 2 * w + tt, mt = tau >> 2, m0 = 16 * mt, n0 = 16 * (tau & 3);
       f32x4v u = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
       const int ksteps = (16 * (mt + 1) + 31) / 32;
-      for (int ks = 0; ks < ksteps; ++ks) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks >= ksteps) break;
         const int k0 = 32 * ks;
         float trow[8], bsc[8], dsc[8], xa[8], pv[8];
         ld8f(&sm.t[(m0 + r16) * SF + k0 + kq], trow);
@@ -380,7 +406,9 @@ __global__ void __launch_bounds__(kThreads) gdn_chunk_kernel(ChunkArgs a) {
       const int tau = 2 * w + tt, mt = tau >> 2, m0 = 16 * mt, n0 = 16 * (tau & 3);
       const int ksteps = (16 * (mt + 1) + 31) / 32;
       f32x4v acc = oacc[tt];
-      for (int ks = 0; ks < ksteps; ++ks) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks >= ksteps) break;
         const int k0 = 32 * ks;
         float ar[8];
         ld8f(&sm.aqk[(m0 + r16) * SF + k0 + kq], ar);

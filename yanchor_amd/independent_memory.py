@@ -156,3 +156,29 @@ def commit_decode(key, value, scores, active, chunk, state: IndependentMemorySta
            state.positions.data_ptr(), state.pending_keys.data_ptr(), state.pending_values.data_ptr(),
            state.pending_scores.data_ptr(), state.count.data_ptr(), state.total.data_ptr(), b, g, cap, pc,
            int(chunk), d, nb, N.code(k), N.stream_of(k))
+
+
+def ring_decode_attention(query, keys, values, positions, indices=None):
+    """Decode attention of one token over a physical ring of cached K/V slots
+    (the sliding-window decode path, reference runtime/model/
+    inference_kernels.py:555-640): softmax over the live slots (positions
+    >= 0) without the anchor sink.  query [B, 1, H, D]; keys/values
+    [NB, G, window, D]; positions int32 [NB, G, window]."""
+    nb, g, window, d = keys.shape
+    if values.shape != keys.shape or positions.shape != (nb, g, window) or positions.dtype != torch.int32:
+        raise ValueError("ring keys/values must be [NB, G, W, D] with int32 positions [NB, G, W]")
+    if query.ndim != 4 or query.shape[1] != 1 or query.shape[3] != d or query.dtype != keys.dtype:
+        raise ValueError("query must be [B, 1, H, D] in the cache dtype")
+    b, _, h, _ = query.shape
+    N.require_device(query, keys, values, positions, indices)
+    for t in (keys, values, positions):
+        if not t.is_contiguous():
+            raise ValueError("ring tensors must be contiguous")
+    idx = _indices(indices, b)
+    if idx is None and nb < b:
+        raise ValueError("ring has fewer rows than the batch")
+    q = query.contiguous()
+    out = torch.empty_like(q)
+    N.call("yh_window_attend", q.data_ptr(), keys.data_ptr(), values.data_ptr(), positions.data_ptr(), N.ptr(idx),
+           out.data_ptr(), b, h, g, window, d, nb, N.code(q), N.stream_of(q))
+    return out

@@ -1,0 +1,590 @@
+"""Continuous-batching decode runtime over a random-init 4B-shaped YANchor model.
+
+This is the workload that drives the hot path end to end: a Qwen3.5-style
+hybrid stack where every 4th layer is sliding-window attention plus the
+independent anchor memory and the others are Gated DeltaNet layers
+(reference modeling_yanchor.py:877-964; layer pattern configuration_yanchor.py:
+19).  Weights are random N(0, 0.02) bf16 (no checkpoint is available).
+
+Per decode step (``Model.decode_step``): embedding, per layer RMSNorm and
+projections on hipBLASLt (torch GEMMs), the GDN recurrent state update, the SWA
+ring attention and the anchor read / commit on this package's HIP kernels,
+final norm and lm_head, then sampling and slot bookkeeping on HIP kernels.  The
+whole step is captured once into a HIP graph and replayed.
+
+``Engine`` is the continuous-batching driver: Poisson arrivals, refill of
+finished slots at poll points (a host sync, as in the reference), and the
+reference's decode tokens/s definition -- useful decode token events (each
+sequence's first token comes from prefill and is not counted) over
+wall - initial prefill - refill prefill (runtime/inference.py:105-106,
+180, 230-235; runtime/model/inference_kernels.py:1204, 1351-1765).
+"""
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+
+@dataclass
+class ModelConfig:
+    layers: int = 36
+    hidden: int = 2560
+    intermediate: int = 9728
+    vocab: int = 151936
+    gdn_heads_k: int = 32
+    gdn_heads_v: int = 32
+    gdn_dk: int = 128
+    gdn_dv: int = 128
+    conv_kernel: int = 4
+    attn_heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    rotary_dim: int = 32           # partial rotary factor 0.25 of the head dim
+    rope_theta: float = 1.0e7
+    swa_window: int = 1024
+    memory_capacity: int = 256
+    memory_chunk: int = 64
+    writer_intermediate: int = 2560
+    admission_rank: int = 64
+    memory_interval: int = 4       # layer i is SWA + memory when (i + 1) % interval == 0
+    rms_eps: float = 1e-6
+    init_std: float = 0.02
+
+    def is_memory_layer(self, i: int) -> bool:
+        return (i + 1) % self.memory_interval == 0
+
+    @property
+    def conv_dim(self) -> int:
+        return 2 * self.gdn_heads_k * self.gdn_dk + self.gdn_heads_v * self.gdn_dv
+
+
+# ---------------------------------------------------------------------------
+# hot-path operations: the HIP kernels (default) -- a CPU restatement can be
+# injected for a baseline run, nothing here imports one.
+
+class HipOps:
+    """The package's HIP kernels behind the reference's call signatures."""
+
+    def __init__(self):
+        from . import gdn, independent_memory, inference_kernels
+        self.gdn = gdn
+        self.mem = independent_memory
+        self.ik = inference_kernels
+
+    def gdn_decode(self, q, k, v, g, beta, state):
+        o, _ = self.gdn.recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=state,
+                                                   output_final_state=True, use_qk_l2norm_in_kernel=True)
+        return o
+
+    def gdn_prefill(self, q, k, v, g, beta, cu_seqlens, lengths):
+        return self.gdn.chunk_gated_delta_rule(q, k, v, g=g, beta=beta, output_final_state=True,
+                                               use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
+                                               lengths=lengths)
+
+    def window_attend(self, q, keys, values, positions):
+        return self.mem.ring_decode_attention(q, keys, values, positions)
+
+    def memory_read(self, q, state):
+        return self.mem.committed_gqa(q, state)
+
+    def memory_commit(self, key, value, scores, active, chunk, state):
+        self.mem.commit_decode(key, value, scores, active, chunk, state)
+
+    def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty):
+        return self.ik.sample_top20_counter(logits, attempt_ids, steps, seed=seed, temperature=temperature,
+                                            top_k=top_k, top_p=top_p, seen=seen, presence_penalty=penalty)
+
+    def bookkeeping(self, *args, **kw):
+        self.ik._update_fixed_decode_state_(*args, **kw)
+
+
+# ---------------------------------------------------------------------------
+
+def rms_norm(x, w, eps, plus_one=True):
+    """Qwen3.5 RMSNorm: x / rms(x) * (1 + w), computed in fp32."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    y = y * ((1.0 + w.float()) if plus_one else w.float())
+    return y.to(x.dtype)
+
+
+def gated_rms_norm(x, gate, w, eps):
+    """Qwen3_5RMSNormGated: normalise, scale by w, times silu(gate) (wheel:175-190)."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    y = (w.float() * y.to(x.dtype).float()) * F.silu(gate.float())
+    return y.to(x.dtype)
+
+
+def rope_tables(positions, cfg: ModelConfig):
+    """cos / sin [*, rotary_dim] for integer positions (rotate_half layout)."""
+    half = cfg.rotary_dim // 2
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, half, device=positions.device, dtype=torch.float32) / half))
+    ang = positions.float()[..., None] * inv
+    ang = torch.cat((ang, ang), -1)
+    return ang.cos(), ang.sin()
+
+
+def apply_rope(x, cos, sin, rd):
+    """Rotate the first rd dims of x [..., D] (cos/sin broadcast over heads)."""
+    xr = x[..., :rd].float()
+    x1, x2 = xr[..., : rd // 2], xr[..., rd // 2:]
+    rot = torch.cat((-x2, x1), -1)
+    out = xr * cos + rot * sin
+    return torch.cat((out.to(x.dtype), x[..., rd:]), -1)
+
+
+class Model:
+    """Random-init 4B-shaped hybrid recurrent model with its decode caches."""
+
+    def __init__(self, cfg: ModelConfig, batch: int, device, *, seed=0, ops=None, dtype=torch.bfloat16,
+                 max_prompt=128):
+        self.cfg, self.B, self.device, self.dtype = cfg, int(batch), torch.device(device), dtype
+        self.ops = ops if ops is not None else HipOps()
+        gen = torch.Generator(device=self.device).manual_seed(seed)
+        std = cfg.init_std
+
+        def w(*shape):
+            return (torch.randn(*shape, device=self.device, generator=gen, dtype=torch.float32) * std).to(dtype)
+
+        def zeros(*shape):
+            return torch.zeros(*shape, device=self.device, dtype=dtype)
+
+        c = cfg
+        self.embed = w(c.vocab, c.hidden)
+        self.lm_head = w(c.vocab, c.hidden)
+        self.final_norm = zeros(c.hidden)
+        self.layers = []
+        for i in range(c.layers):
+            L = {"in_norm": zeros(c.hidden), "post_norm": zeros(c.hidden),
+                 "mlp_gate_up": w(2 * c.intermediate, c.hidden), "mlp_down": w(c.hidden, c.intermediate)}
+            if c.is_memory_layer(i):
+                qkv_out = 2 * c.attn_heads * c.head_dim + 2 * c.kv_heads * c.head_dim
+                L.update(kind="attn", w_qkv=w(qkv_out, c.hidden), q_norm=zeros(c.head_dim),
+                         k_norm=zeros(c.head_dim), w_o=w(c.hidden, c.attn_heads * c.head_dim),
+                         m_in_norm=zeros(c.hidden), m_q=w(c.attn_heads * c.head_dim, c.hidden),
+                         m_q_norm=zeros(c.head_dim), m_k_norm=zeros(c.head_dim),
+                         read_scale=w(c.attn_heads).float(), read_gate_w=w(c.attn_heads, c.head_dim).float(),
+                         read_gate_b=w(c.attn_heads).float(),
+                         writer_gate_up=w(2 * c.writer_intermediate, c.hidden),
+                         writer_down=w(c.hidden, c.writer_intermediate),
+                         m_kv=w(2 * c.kv_heads * c.head_dim, c.hidden),
+                         adm_down=w(c.admission_rank, c.hidden), adm_up=w(c.kv_heads, c.admission_rank).float(),
+                         m_o=w(c.hidden, c.attn_heads * c.head_dim))
+            else:
+                in_out = c.conv_dim + c.gdn_heads_v * c.gdn_dv + 2 * c.gdn_heads_v
+                a_log = torch.log(torch.empty(c.gdn_heads_v, device=self.device).uniform_(1.0, 16.0,
+                                                                                          generator=gen))
+                L.update(kind="gdn", w_in=w(in_out, c.hidden), conv_w=w(c.conv_dim, c.conv_kernel),
+                         a_log=a_log, dt_bias=torch.ones(c.gdn_heads_v, device=self.device),
+                         gnorm=torch.ones(c.gdn_dv, device=self.device, dtype=dtype),
+                         w_out=w(c.hidden, c.gdn_heads_v * c.gdn_dv))
+            self.layers.append(L)
+        self._alloc_caches()
+
+    # ---------------- caches ----------------
+    def _alloc_caches(self):
+        c, B, dev = self.cfg, self.B, self.device
+        self.gdn_state, self.conv_state, self.ring_k, self.ring_v, self.ring_pos, self.memory = {}, {}, {}, {}, {}, {}
+        from .independent_memory import IndependentMemoryState
+        for i, L in enumerate(self.layers):
+            if L["kind"] == "gdn":
+                self.gdn_state[i] = torch.zeros(B, c.gdn_heads_v, c.gdn_dk, c.gdn_dv, device=dev)
+                self.conv_state[i] = torch.zeros(B, c.conv_dim, c.conv_kernel - 1, device=dev, dtype=self.dtype)
+            else:
+                self.ring_k[i] = torch.zeros(B, c.kv_heads, c.swa_window, c.head_dim, device=dev, dtype=self.dtype)
+                self.ring_v[i] = torch.zeros_like(self.ring_k[i])
+                self.ring_pos[i] = torch.full((B, c.kv_heads, c.swa_window), -1, device=dev, dtype=torch.int32)
+                self.memory[i] = IndependentMemoryState.empty(B, c.kv_heads, c.memory_capacity, c.memory_chunk,
+                                                              c.head_dim, dev, self.dtype)
+
+    def cache_tensors(self):
+        """Every per-slot cache tensor (dim 0 = slot), for refill and compaction."""
+        from dataclasses import fields as dfields
+        out = []
+        for i in self.gdn_state:
+            out += [self.gdn_state[i], self.conv_state[i]]
+        for i in self.ring_k:
+            out += [self.ring_k[i], self.ring_v[i], self.ring_pos[i]]
+            st = self.memory[i]
+            out += [getattr(st, f.name) for f in dfields(st)]
+        return out
+
+    # ---------------- layers ----------------
+    def _mlp(self, L, x):
+        gu = F.linear(x, L["mlp_gate_up"])
+        gate, up = gu.chunk(2, -1)
+        return F.linear(F.silu(gate) * up, L["mlp_down"])
+
+    def _gdn_split(self, L, proj):
+        c = self.cfg
+        qkv = proj[..., : c.conv_dim]
+        z = proj[..., c.conv_dim: c.conv_dim + c.gdn_heads_v * c.gdn_dv]
+        b = proj[..., c.conv_dim + c.gdn_heads_v * c.gdn_dv: c.conv_dim + c.gdn_heads_v * c.gdn_dv + c.gdn_heads_v]
+        a = proj[..., -c.gdn_heads_v:]
+        beta = torch.sigmoid(b.float())
+        g = -torch.exp(L["a_log"]) * F.softplus(a.float() + L["dt_bias"])
+        return qkv, z, beta, g
+
+    def _gdn_decode(self, i, L, x):
+        c, B = self.cfg, x.shape[0]
+        proj = F.linear(rms_norm(x, L["in_norm"], c.rms_eps), L["w_in"])
+        qkv, z, beta, g = self._gdn_split(L, proj)
+        cs = self.conv_state[i]
+        window = torch.cat((cs, qkv[:, :, None]), -1)                      # [B, C, K]
+        cs.copy_(window[:, :, 1:])
+        mixed = F.silu((window.float() * L["conv_w"].float()).sum(-1)).to(self.dtype)
+        hk, dk, dv = c.gdn_heads_k * c.gdn_dk, c.gdn_dk, c.gdn_dv
+        q = mixed[:, :hk].reshape(B, 1, c.gdn_heads_k, dk)
+        k = mixed[:, hk: 2 * hk].reshape(B, 1, c.gdn_heads_k, dk)
+        v = mixed[:, 2 * hk:].reshape(B, 1, c.gdn_heads_v, dv)
+        o = self.ops.gdn_decode(q, k, v, g[:, None], beta[:, None], self.gdn_state[i])
+        o = gated_rms_norm(o.reshape(B, c.gdn_heads_v, dv), z.reshape(B, c.gdn_heads_v, dv), L["gnorm"], c.rms_eps)
+        return F.linear(o.reshape(B, -1), L["w_out"])
+
+    def _attn_project(self, L, x, cos, sin):
+        c = self.cfg
+        proj = F.linear(x, L["w_qkv"])
+        hq = 2 * c.attn_heads * c.head_dim
+        qg = proj[..., :hq].unflatten(-1, (c.attn_heads, 2 * c.head_dim))
+        q, gate = qg[..., : c.head_dim], qg[..., c.head_dim:]
+        k = proj[..., hq: hq + c.kv_heads * c.head_dim].unflatten(-1, (c.kv_heads, c.head_dim))
+        v = proj[..., hq + c.kv_heads * c.head_dim:].unflatten(-1, (c.kv_heads, c.head_dim))
+        q = apply_rope(rms_norm(q, L["q_norm"], c.rms_eps), cos, sin, c.rotary_dim)
+        k = apply_rope(rms_norm(k, L["k_norm"], c.rms_eps), cos, sin, c.rotary_dim)
+        return q, gate.reshape(*gate.shape[:-2], -1), k, v
+
+    def _memory_qkvs(self, L, hidden, cos, sin):
+        """_query_scores + _write_kv of IndependentGQAMemory (modeling_yanchor.py:147-176)."""
+        c = self.cfg
+        u = rms_norm(hidden, L["m_in_norm"], c.rms_eps)
+        q = rms_norm(F.linear(u, L["m_q"]).unflatten(-1, (c.attn_heads, c.head_dim)), L["m_q_norm"], c.rms_eps)
+        gate = torch.tanh(L["read_scale"]) * 2 * torch.sigmoid(
+            (q.float() * L["read_gate_w"]).sum(-1) / math.sqrt(c.head_dim) + L["read_gate_b"])
+        q = apply_rope(q, cos, sin, c.rotary_dim)
+        feats = F.silu(F.linear(u, L["adm_down"]))
+        scores = F.linear(feats.float(), L["adm_up"])
+        gu = F.linear(u, L["writer_gate_up"])
+        wg, wu = gu.chunk(2, -1)
+        zz = u + F.linear(F.silu(wg) * wu, L["writer_down"])
+        kv = F.linear(zz, L["m_kv"])
+        key = kv[..., : c.kv_heads * c.head_dim].unflatten(-1, (c.kv_heads, c.head_dim))
+        val = kv[..., c.kv_heads * c.head_dim:].unflatten(-1, (c.kv_heads, c.head_dim))
+        key = apply_rope(rms_norm(key, L["m_k_norm"], c.rms_eps), cos, sin, c.rotary_dim)
+        return q, gate, key, val.contiguous(), scores
+
+    def _attn_decode(self, i, L, x, hidden, positions, cos, sin, valid):
+        c, B = self.cfg, x.shape[0]
+        cs, sn = cos[:, None], sin[:, None]
+        q, gate, k, v = self._attn_project(L, rms_norm(x, L["in_norm"], c.rms_eps), cs, sn)
+        slot = (positions % c.swa_window).long()
+        rows = torch.arange(B, device=x.device)
+        self.ring_k[i][rows, :, slot] = k
+        self.ring_v[i][rows, :, slot] = v
+        self.ring_pos[i][rows, :, slot] = positions.to(torch.int32)[:, None]
+        att = self.ops.window_attend(q[:, None].contiguous(), self.ring_k[i], self.ring_v[i], self.ring_pos[i])
+        att = att.reshape(B, -1) * torch.sigmoid(gate)
+        out = F.linear(att, L["w_o"])
+        mq, mgate, mk, mv, mscores = self._memory_qkvs(L, hidden, cs, sn)
+        read = self.ops.memory_read(mq[:, None].contiguous(), self.memory[i])
+        self.ops.memory_commit(mk[:, None].contiguous(), mv[:, None], mscores[:, None], valid,
+                               c.memory_chunk, self.memory[i])
+        read = read[:, 0] * valid[:, None, None].to(read.dtype)
+        mem_out = F.linear((read * mgate[..., None].to(read.dtype)).reshape(B, -1), L["m_o"])
+        return out + mem_out
+
+    def decode_step(self, tokens, positions, valid):
+        """One token for every slot: tokens, positions [B] int64, valid [B] bool
+        -> logits [B, V] float32.  Updates every cache in place."""
+        c = self.cfg
+        h = self.embed[tokens]
+        cos, sin = rope_tables(positions, c)
+        for i, L in enumerate(self.layers):
+            if L["kind"] == "gdn":
+                h = h + self._gdn_decode(i, L, h)
+            else:
+                h = h + self._attn_decode(i, L, h, h, positions, cos, sin, valid)
+            h = h + self._mlp(L, rms_norm(h, L["post_norm"], c.rms_eps))
+        return F.linear(rms_norm(h, self.final_norm, c.rms_eps), self.lm_head).float()
+
+    # ---------------- prefill ----------------
+    def prefill(self, prompts):
+        """Prefill fresh sequences from empty caches.  prompts [R, T] int64
+        -> (logits of the last token [R, V] float32, caches dict of [R, ...]
+        tensors in cache_tensors() order)."""
+        c, dev = self.cfg, self.device
+        R, T = prompts.shape
+        if T > c.swa_window:
+            raise ValueError("prompts longer than the SWA window are not supported by this prefill")
+        tmp = Model.__new__(Model)
+        tmp.cfg, tmp.B, tmp.device, tmp.dtype, tmp.ops, tmp.layers = c, R, dev, self.dtype, self.ops, self.layers
+        tmp._alloc_caches()
+        pos = torch.arange(T, device=dev)
+        cos, sin = rope_tables(pos, c)
+        h = self.embed[prompts]                                            # [R, T, hidden]
+        lengths = [T] * R
+        cu = torch.arange(0, (R + 1) * T, T, device=dev, dtype=torch.int32)
+        for i, L in enumerate(self.layers):
+            if L["kind"] == "gdn":
+                proj = F.linear(rms_norm(h, L["in_norm"], c.rms_eps), L["w_in"])
+                qkv, z, beta, g = self._gdn_split(L, proj)
+                xw = F.pad(qkv.float(), (0, 0, c.conv_kernel - 1, 0))           # causal conv over time
+                mixed = sum(xw[:, j: j + T] * L["conv_w"].float()[:, j] for j in range(c.conv_kernel))
+                mixed = F.silu(mixed).to(self.dtype)
+                tmp.conv_state[i].copy_(qkv[:, T - (c.conv_kernel - 1):].transpose(1, 2))
+                hk, dk, dv = c.gdn_heads_k * c.gdn_dk, c.gdn_dk, c.gdn_dv
+                q = mixed[..., :hk].reshape(1, R * T, c.gdn_heads_k, dk)
+                k = mixed[..., hk: 2 * hk].reshape(1, R * T, c.gdn_heads_k, dk)
+                v = mixed[..., 2 * hk:].reshape(1, R * T, c.gdn_heads_v, dv)
+                o, st = self.ops.gdn_prefill(q, k, v, g.reshape(1, R * T, -1), beta.reshape(1, R * T, -1), cu,
+                                             lengths)
+                tmp.gdn_state[i].copy_(st)
+                o = gated_rms_norm(o.reshape(R, T, c.gdn_heads_v, dv), z.reshape(R, T, c.gdn_heads_v, dv),
+                                   L["gnorm"], c.rms_eps)
+                h = h + F.linear(o.reshape(R, T, -1), L["w_out"])
+            else:
+                cs, sn = cos[None, :, None], sin[None, :, None]
+                q, gate, k, v = self._attn_project(L, rms_norm(h, L["in_norm"], c.rms_eps), cs, sn)
+                # causal attention inside the prompt (T <= window), float32
+                rep = c.attn_heads // c.kv_heads
+                qh = q.float().transpose(1, 2)                                  # [R, H, T, D]
+                kh = k.float().repeat_interleave(rep, 2).transpose(1, 2).contiguous()
+                vh = v.float().repeat_interleave(rep, 2).transpose(1, 2).contiguous()
+                att = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) / math.sqrt(c.head_dim)
+                att = att.masked_fill(torch.ones(T, T, device=dev, dtype=torch.bool).triu(1), float("-inf"))
+                ctx = torch.matmul(att.softmax(-1), vh).transpose(1, 2).reshape(R, T, -1).to(self.dtype)
+                out = F.linear(ctx * torch.sigmoid(gate), L["w_o"])
+                tmp.ring_k[i][:, :, :T] = k.transpose(1, 2)
+                tmp.ring_v[i][:, :, :T] = v.transpose(1, 2)
+                tmp.ring_pos[i][:, :, :T] = pos.to(torch.int32)
+                # anchor memory, token by token: the decode read / commit sequence
+                # leaves the same state and outputs as the reference's prefill path
+                mq, mgate, mk, mv, msc = self._memory_qkvs(L, h, cs, sn)
+                valid = torch.ones(R, dtype=torch.bool, device=dev)
+                reads = []
+                for t in range(T):
+                    reads.append(self.ops.memory_read(mq[:, t:t + 1].contiguous(), tmp.memory[i])[:, 0])
+                    self.ops.memory_commit(mk[:, t:t + 1].contiguous(), mv[:, t:t + 1].contiguous(),
+                                           msc[:, t:t + 1], valid, c.memory_chunk, tmp.memory[i])
+                read = torch.stack(reads, 1)
+                mem_out = F.linear((read * mgate[..., None].to(read.dtype)).reshape(R, T, -1), L["m_o"])
+                h = h + out + mem_out
+            h = h + self._mlp(L, rms_norm(h, L["post_norm"], c.rms_eps))
+        logits = F.linear(rms_norm(h[:, -1], self.final_norm, c.rms_eps), self.lm_head).float()
+        return logits, tmp.cache_tensors()
+
+
+@dataclass
+class Request:
+    attempt_id: int
+    prompt: torch.Tensor
+    cap: int
+    arrival_step: int
+
+
+@dataclass
+class EngineMetrics:
+    decode_useful_token_events: int = 0
+    decode_scheduled_token_events: int = 0
+    decode_steps: int = 0
+    generation_wall_seconds: float = 0.0
+    initial_prefill_seconds: float = 0.0
+    refill_prefill_seconds: float = 0.0
+    refilled: int = 0
+    completed: int = 0
+    peak_allocated_gib: float = 0.0
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def decode_seconds(self):
+        return self.generation_wall_seconds - self.initial_prefill_seconds - self.refill_prefill_seconds
+
+    @property
+    def decode_tokens_per_second(self):
+        return self.decode_useful_token_events / max(self.decode_seconds, 1e-9)
+
+
+class Engine:
+    """Continuous-batching decode driver over ``Model`` (the synthetic-request
+    counterpart of cuda_graph_generate_top20_dynamic_refill,
+    runtime/model/inference_kernels.py:1351-1765).
+
+    Slots are a fixed physical batch; every decode step computes all of them
+    (finished / empty slots are scheduled but not useful, as in the reference).
+    At poll points (every ``poll_interval`` steps, a host sync) finished slots
+    are refilled from the arrival queue in ascending slot order: the new
+    requests are prefilled together and their caches scattered into the slots.
+    The decode step -- model forward, top-k/top-p counter sampling with the
+    presence penalty fused, slot bookkeeping -- is one captured HIP graph.
+    """
+
+    def __init__(self, model: Model, *, seed=20260923, temperature=0.6, top_k=20, top_p=0.95,
+                 presence_penalty=1.5, poll_interval=32, max_rows=4096, max_new_tokens=8192, use_graph=True):
+        self.m, self.B, self.dev = model, model.B, model.device
+        self.seed, self.temperature, self.top_k, self.top_p = seed, temperature, top_k, top_p
+        self.penalty, self.poll_interval, self.use_graph = presence_penalty, poll_interval, use_graph
+        self.max_rows, self.max_new = max_rows, max_new_tokens
+        B, dev, V = self.B, self.dev, model.cfg.vocab
+        self.decode_ids = torch.zeros(B, 1, dtype=torch.long, device=dev)
+        self.positions = torch.zeros(B, dtype=torch.long, device=dev)
+        self.finished = torch.ones(B, dtype=torch.bool, device=dev)
+        self.slot_rows = torch.full((B,), -1, dtype=torch.long, device=dev)
+        self.slot_caps = torch.zeros(B, dtype=torch.long, device=dev)
+        self.row_steps = torch.ones(B, dtype=torch.long, device=dev)
+        self.attempt_ids = torch.zeros(B, dtype=torch.long, device=dev)
+        self.dense_seen = torch.zeros(B, V, dtype=torch.bool, device=dev)
+        self.storage = torch.zeros(max_rows + B, max_new_tokens + 1, dtype=torch.int32, device=dev)
+        self.generated = torch.zeros(max_rows + B, dtype=torch.long, device=dev)
+        self.finished_by_eos = torch.zeros(max_rows + B, dtype=torch.bool, device=dev)
+        self.sink_rows = max_rows + torch.arange(B, device=dev)
+        self.useful = torch.zeros((), dtype=torch.long, device=dev)
+        self.graph = None
+        self.next_row = 0
+        self.slot_request: list = [None] * B
+
+    # one decode step on the device (captured)
+    def _step(self):
+        valid = (~self.finished) & (self.slot_rows >= 0)
+        logits = self.m.decode_step(self.decode_ids[:, 0], self.positions, valid)
+        tok = self.m.ops.sample(logits, self.attempt_ids, self.row_steps, self.dense_seen, seed=self.seed,
+                                temperature=self.temperature, top_k=self.top_k, top_p=self.top_p,
+                                penalty=self.penalty)
+        self.m.ops.bookkeeping(tok, self.storage, self.dense_seen, self.generated, self.finished_by_eos,
+                               self.finished, self.slot_rows, self.sink_rows, self.slot_caps, self.row_steps,
+                               self.positions, self.decode_ids, self.useful,
+                               maximum_new_tokens=self.max_new, pad_token_id=0, eos_token_ids=())
+
+    def capture(self):
+        """Warm up and capture the decode step.  Call while every slot is empty:
+        the warm-up steps then only touch rows that admission overwrites whole."""
+        if not self.use_graph or self.graph is not None:
+            return
+        for _ in range(2):  # warm the allocator and the sampler workspace outside capture
+            self._step()
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        torch.cuda.synchronize()
+
+    def step(self):
+        if self.use_graph:
+            if self.graph is None:
+                raise RuntimeError("Engine.capture() must run before the first admission")
+            self.graph.replay()
+        else:
+            self._step()
+
+    def admit(self, requests, targets):
+        """Prefill ``requests`` and place them in slots ``targets`` (host lists)."""
+        if not requests:
+            return 0.0
+        from . import inference_kernels as ik
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        prompts = torch.stack([r.prompt for r in requests]).to(self.dev)
+        logits, caches = self.m.prefill(prompts)
+        n = len(requests)
+        ids = torch.tensor([r.attempt_id for r in requests], dtype=torch.long, device=self.dev)
+        first = self.m.ops.sample(logits, ids, 0, None, seed=self.seed, temperature=self.temperature,
+                                  top_k=self.top_k, top_p=self.top_p, penalty=0.0)
+        tgt = torch.tensor(targets, dtype=torch.long, device=self.dev)
+        ik.gather_rows(list(zip(caches, self.m.cache_tensors())), None, tgt, n)
+        rows = torch.arange(self.next_row, self.next_row + n, dtype=torch.long, device=self.dev)
+        self.next_row += n
+        caps = torch.tensor([r.cap for r in requests], dtype=torch.long, device=self.dev)
+        self.slot_rows.index_copy_(0, tgt, rows)
+        self.slot_caps.index_copy_(0, tgt, caps)
+        self.attempt_ids.index_copy_(0, tgt, ids)
+        self.row_steps.index_fill_(0, tgt, 1)
+        self.positions.index_fill_(0, tgt, prompts.shape[1])
+        done = caps <= 1
+        self.finished.index_copy_(0, tgt, done)
+        self.decode_ids.index_copy_(0, tgt, torch.where(done[:, None], torch.zeros_like(first), first))
+        self.dense_seen.index_fill_(0, tgt, False)
+        self.dense_seen[tgt, first[:, 0]] = True
+        self.storage[rows, 0] = first[:, 0].to(torch.int32)
+        self.generated[rows] = 1
+        for r, s in zip(requests, targets):
+            self.slot_request[s] = r
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    def poll(self, queue):
+        """Host sync: refill finished slots (ascending) from the queue."""
+        fin = self.finished.cpu().tolist()
+        free = [s for s, f in enumerate(fin) if f]
+        completed = sum(1 for s in free if self.slot_request[s] is not None)
+        for s in free:
+            self.slot_request[s] = None
+        take = min(len(free), len(queue), self.max_rows - self.next_row)
+        reqs = [queue.pop(0) for _ in range(take)]
+        t = self.admit(reqs, free[:take])
+        empty = torch.tensor(free[take:], dtype=torch.long, device=self.dev)
+        if empty.numel():
+            self.slot_rows.index_fill_(0, empty, -1)
+            self.finished.index_fill_(0, empty, True)
+        return t, completed, take
+
+
+def synthetic_requests(steps, *, rate=4.0, prompt_len=128, mean_len=1024, max_len=8192, vocab=151936,
+                       seed=20260923):
+    """Poisson(rate) arrivals per step with uniform-random prompts and
+    geometric(mean_len) generation lengths (capped at max_len)."""
+    gen = torch.Generator().manual_seed(seed)
+    arrivals = torch.poisson(torch.full((steps,), float(rate)), generator=gen).long().tolist()
+    reqs, aid = [], 0
+    p = 1.0 / mean_len
+    for step, n in enumerate(arrivals):
+        for _ in range(n):
+            u = torch.rand((), generator=gen).item()
+            length = min(max_len, max(1, int(math.ceil(math.log1p(-u) / math.log1p(-p)))))
+            prompt = torch.randint(0, vocab, (prompt_len,), generator=gen)
+            reqs.append(Request(aid, prompt, length, step))
+            aid += 1
+    return reqs
+
+
+def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=128, mean_len=1024,
+                         poll_interval=32, seed=20260923, use_graph=True, max_new_tokens=8192):
+    """Continuous batching for warmup + steps decode steps; returns metrics of
+    the timed steps (the reference's decode tokens/s definition)."""
+    eng = Engine(model, seed=seed, poll_interval=poll_interval, use_graph=use_graph,
+                 max_new_tokens=max_new_tokens)
+    eng.capture()
+    arrivals = synthetic_requests(warmup + steps, rate=rate, prompt_len=prompt_len, mean_len=mean_len,
+                                  max_len=max_new_tokens, vocab=model.cfg.vocab, seed=seed)
+    queue, pending, idx = [], list(arrivals), 0
+    m = EngineMetrics()
+    total = warmup + steps
+    t_start = None
+    useful0 = 0
+    for step in range(total):
+        while idx < len(pending) and pending[idx].arrival_step <= step:
+            queue.append(pending[idx])
+            idx += 1
+        if step == warmup:
+            torch.cuda.synchronize()
+            useful0 = int(eng.useful.item())
+            t_start = time.perf_counter()
+            m.refill_prefill_seconds = 0.0
+        if step % poll_interval == 0:
+            t, done, taken = eng.poll(queue)
+            if t_start is not None:
+                m.refill_prefill_seconds += t
+                m.refilled += taken
+                m.completed += done
+        eng.step()
+        if t_start is not None:
+            m.decode_steps += 1
+    torch.cuda.synchronize()
+    m.generation_wall_seconds = time.perf_counter() - t_start
+    m.decode_useful_token_events = int(eng.useful.item()) - useful0
+    m.decode_scheduled_token_events = m.decode_steps * model.B
+    m.peak_allocated_gib = torch.cuda.max_memory_allocated() / 2**30
+    m.extra = {"queue_left": len(queue), "live_slots_end": int(((~eng.finished) & (eng.slot_rows >= 0)).sum())}
+    return m
