@@ -283,6 +283,61 @@ int yh_gather_rows(int n_tensors, const void* const* src, void* const* dst, cons
                    const int64_t* src_rows, const int64_t* dst_rows, const int64_t* src_index,
                    const int64_t* dst_index, int64_t n, yh_stream_t stream);
 
+/* ---- fused decode-layer neighbours (bf16 activations) ------------------- */
+
+/*
+ * Qwen3.5 RMSNorm over rows of D bf16 values: s = residual ? bf16(x + residual)
+ * : x; residual_out (optional) = s; out = bf16(s / sqrt(mean(s^2) + eps) *
+ * (plus_one ? 1 + w : w)).  x rows x_stride apart, out rows out_stride apart,
+ * residual / residual_out contiguous [N, D].  D % 8 == 0, D <= 8192.
+ * Replaces _qwen35_rmsnorm_torch_tree_kernel / the fused residual RMSNorm
+ * (runtime/model/inference_kernels.py:227-271, 1767-1797).
+ */
+int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual, void* residual_out, const void* w, void* out,
+               int64_t out_stride, int64_t N, int64_t D, float eps, int plus_one, yh_stream_t stream);
+
+/*
+ * GDN decode prologue for B rows of the packed projection proj [B, proj_stride]
+ * (bf16) = [q k v (conv_dim) | z | b (HV) at b_offset | a (HV) at a_offset]:
+ * depthwise causal conv1d update with conv_state [B, conv_kernel - 1, conv_dim]
+ * (bf16, time-major, shifted in place) and conv_w [conv_dim, conv_kernel], SiLU,
+ * split into q, k [B, qk_dim] and v [B, conv_dim - 2 qk_dim] (bf16), and the gates
+ * beta = sigmoid(b), g = -exp(a_log) * softplus(a + dt_bias) (float [B, HV]).
+ * Replaces _qwen35_graph_safe_conv_update_kernel and
+ * _qwen35_fused_gdn_gates_kernel (runtime/model/inference_kernels.py:339-376,
+ * 668-691).  conv_kernel must be 4.
+ */
+int yh_gdn_decode_prep(const void* proj, int64_t proj_stride, void* conv_state, const void* conv_w,
+                       const float* a_log, const float* dt_bias, void* q, void* k, void* v, float* g, float* beta,
+                       int64_t B, int64_t conv_dim, int64_t qk_dim, int64_t HV, int64_t b_offset, int64_t a_offset,
+                       int64_t conv_kernel, yh_stream_t stream);
+
+/*
+ * Qwen3_5RMSNormGated per head of D = 128: out = bf16(bf16(w * bf16(o / rms(o)))
+ * * silu(z)); o, out [N, H, 128] contiguous bf16, z head h of row n at
+ * z + n * z_stride + h * 128.  (transformers wheel
+ * models/qwen3_5/modeling_qwen3_5.py:175-190)
+ */
+int yh_gated_rmsnorm(const void* o, const void* z, int64_t z_stride, const void* w, void* out, int64_t N, int64_t H,
+                     int64_t D, float eps, yh_stream_t stream);
+
+/* out[n, i] = bf16(bf16(silu(gu[n, i])) * gu[n, I + i]) for gate_up [N, 2I]
+ * (runtime/model/inference_kernels.py:642-666).  I % 8 == 0. */
+int yh_silu_mul(const void* gate_up, void* out, int64_t N, int64_t I, yh_stream_t stream);
+
+/*
+ * Per-head RMSNorm (1 + w) and rotate-half RoPE on the first rotary_dim of
+ * D = 128 dims, cos / sin float [N, rotary_dim]: head h of token n is read at
+ * x + n * x_tok_stride + h * x_head_stride and written at
+ * out + r * out_tok_stride + h * out_head_stride with r = out_tok_index ?
+ * out_tok_index[n] : n (e.g. a ring slot).  (modeling_yanchor.py:46-49 and the
+ * Qwen3.5 attention q / k path)
+ */
+int yh_head_norm_rope(const void* x, int64_t x_tok_stride, int64_t x_head_stride, const void* w, const float* cos,
+                      const float* sin, void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                      const int64_t* out_tok_index, int64_t N, int64_t H, int64_t D, int64_t rotary_dim, float eps,
+                      yh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,145 @@
+"""Fused decode-layer kernels against their torch formulations (GPU).
+
+Each kernel keeps the torch formulation's bf16 rounding points, so outputs
+agree to within one bf16 rounding of values that differ only by fp32
+summation order: checked as at most 1 bf16 ulp per element, with all but a
+small fraction of elements bit-equal.  Pure data movement (the residual sum,
+the conv window shift, ring-slot placement) is checked bit-exact.
+"""
+import pytest
+import torch
+
+from yanchor_amd import layers
+from yanchor_amd import runtime as rt
+from yanchor_amd.runtime import TorchGlue
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp_check(x, ref, max_frac=0.02):
+    """bf16 x vs bf16 ref: |x - ref| <= 1 ulp of ref everywhere (or below
+    2^-16 of the largest |ref|, where a sum cancels and fp32 ordering alone
+    decides the low bits), and at most ``max_frac`` of the elements differ."""
+    assert x.shape == ref.shape and x.dtype == ref.dtype == torch.bfloat16
+    xf, rf = x.float(), ref.float()
+    atol = rf.abs().max() * 2.0 ** -16
+    ulp = torch.clamp(rf.abs() * 2.0 ** -7, min=atol)
+    bad = (xf - rf).abs() > ulp * 1.0001
+    assert not bad.any(), f"{int(bad.sum())} elements beyond 1 ulp; first at {bad.nonzero()[0].tolist()}"
+    frac = (xf != rf).float().mean().item()
+    assert frac <= max_frac, frac
+
+
+def rnd(*shape, dev, scale=1.0, seed=0, dtype=torch.bfloat16):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(*shape, device=dev, generator=g) * scale).to(dtype)
+
+
+@pytest.mark.parametrize("n,d", [(1, 2560), (130, 2560), (7, 256), (3, 8192)])
+def test_rmsnorm(gpu, n, d):
+    x, r = rnd(n, d, dev=gpu, scale=3.0, seed=1), rnd(n, d, dev=gpu, seed=2)
+    w = rnd(d, dev=gpu, scale=0.1, seed=3)
+    ulp_check(layers.rmsnorm(x, w, 1e-6), TorchGlue.rmsnorm(x, w, 1e-6))
+    out, s = layers.rmsnorm(x, w, 1e-6, residual=r)
+    ref_out, ref_s = TorchGlue.rmsnorm(x, w, 1e-6, r)
+    assert torch.equal(s, ref_s)
+    ulp_check(out, ref_out)
+
+
+def test_rmsnorm_strided_rows(gpu):
+    base = rnd(9, 3072, dev=gpu, seed=4)
+    x = base[:, :2560]                                   # row stride 3072
+    w = rnd(2560, dev=gpu, scale=0.1, seed=5)
+    ulp_check(layers.rmsnorm(x, w, 1e-6), TorchGlue.rmsnorm(x.contiguous(), w, 1e-6))
+
+
+def test_rmsnorm_empty_and_bad(gpu):
+    w = rnd(256, dev=gpu, seed=6)
+    assert layers.rmsnorm(torch.empty(0, 256, device=gpu, dtype=torch.bfloat16), w, 1e-6).shape == (0, 256)
+    with pytest.raises(ValueError):
+        layers.rmsnorm(torch.zeros(2, 256, device=gpu), w, 1e-6)     # fp32 activations
+
+
+@pytest.mark.parametrize("b", [1, 5, 128])
+def test_gdn_decode_prep(gpu, b):
+    cfg = rt.ModelConfig()
+    hv, vd = cfg.gdn_heads_v, cfg.gdn_heads_v * cfg.gdn_dv
+    p = cfg.conv_dim + vd + 2 * hv
+    proj = rnd(b, p, dev=gpu, scale=2.0, seed=7)
+    conv = rnd(b, 3, cfg.conv_dim, dev=gpu, seed=8)
+    conv_w = rnd(cfg.conv_dim, 4, dev=gpu, scale=0.5, seed=9)
+    a_log = torch.log(torch.linspace(1.0, 16.0, hv, device=gpu))
+    dt_bias = torch.linspace(-1.0, 1.0, hv, device=gpu)
+    kw = dict(conv_dim=cfg.conv_dim, qk_dim=cfg.gdn_heads_k * cfg.gdn_dk, hv=hv, b_offset=cfg.conv_dim + vd,
+              a_offset=cfg.conv_dim + vd + hv)
+    conv_ref = conv.clone()
+    got = layers.gdn_decode_prep(proj, conv, conv_w, a_log, dt_bias, **kw)
+    ref = TorchGlue.gdn_prep(proj, conv_ref, conv_w, a_log, dt_bias, **kw)
+    assert torch.equal(conv, conv_ref)                   # window shifted by one token
+    for x, r in zip(got[:3], ref[:3]):
+        ulp_check(x, r.contiguous())
+    for x, r in zip(got[3:], ref[3:]):
+        assert rel_err(x, r) <= 1e-6
+
+
+def test_gdn_decode_prep_large_gate_softplus(gpu):
+    """a + dt_bias above the softplus threshold (20) takes the identity branch."""
+    hv = 4
+    proj = torch.zeros(2, 256 * 3 + 2 * hv, device=gpu, dtype=torch.bfloat16)
+    proj[:, -hv:] = torch.tensor([25.0, 19.0, -30.0, 0.0])
+    conv = torch.zeros(2, 3, 256 * 3, device=gpu, dtype=torch.bfloat16)
+    kw = dict(conv_dim=256 * 3, qk_dim=256, hv=hv, b_offset=256 * 3, a_offset=256 * 3 + hv)
+    a_log, dt = torch.zeros(hv, device=gpu), torch.zeros(hv, device=gpu)
+    got = layers.gdn_decode_prep(proj, conv, torch.ones(768, 4, device=gpu, dtype=torch.bfloat16), a_log, dt, **kw)
+    ref = TorchGlue.gdn_prep(proj, conv.clone(), torch.ones(768, 4, device=gpu, dtype=torch.bfloat16), a_log, dt,
+                             **kw)
+    assert rel_err(got[3], ref[3]) <= 1e-6 and rel_err(got[4], ref[4]) <= 1e-6
+
+
+@pytest.mark.parametrize("b,h", [(1, 32), (128, 32), (3, 5)])
+def test_gated_rmsnorm(gpu, b, h):
+    o = rnd(b, h, 128, dev=gpu, scale=0.3, seed=10)
+    proj = rnd(b, h * 128 + 96, dev=gpu, seed=11)
+    z = proj[:, 32: 32 + h * 128]                         # strided view, as in the projection
+    w = (1.0 + rnd(128, dev=gpu, scale=0.1, seed=12).float()).to(torch.bfloat16)
+    ulp_check(layers.gated_rmsnorm(o, z, w, 1e-6), TorchGlue.gated_rmsnorm(o, z, w, 1e-6))
+
+
+@pytest.mark.parametrize("n,i", [(1, 9728), (128, 9728), (5, 2560), (3, 8)])
+def test_silu_mul(gpu, n, i):
+    gu = rnd(n, 2 * i, dev=gpu, scale=3.0, seed=13)
+    ulp_check(layers.silu_mul(gu), TorchGlue.silu_mul(gu))
+
+
+@pytest.mark.parametrize("rd", [0, 32, 64, 128])
+def test_head_norm_rope(gpu, rd):
+    n, h = 37, 8
+    proj = rnd(n, h, 256, dev=gpu, scale=2.0, seed=14)
+    x = proj[..., :128]                                   # head stride 256, as in the fused q | gate layout
+    w = rnd(128, dev=gpu, scale=0.1, seed=15)
+    pos = torch.randint(0, 100000, (n,), device=gpu)
+    cfg = rt.ModelConfig(rotary_dim=max(rd, 2))
+    cos, sin = rt.rope_tables(pos, cfg)
+    ulp_check(layers.head_norm_rope(x, w, cos, sin, rd, 1e-6),
+              TorchGlue.head_norm_rope(x.contiguous(), w, cos, sin, rd, 1e-6))
+
+
+def test_head_norm_rope_ring_write(gpu):
+    """Keys land in ring slot positions % window of each row, nothing else moves."""
+    b, kvh, win, d = 6, 4, 16, 128
+    x = rnd(b, kvh, d, dev=gpu, seed=16)
+    w = rnd(d, dev=gpu, scale=0.1, seed=17)
+    pos = torch.tensor([0, 5, 15, 16, 33, 1000], device=gpu)
+    cos, sin = rt.rope_tables(pos, rt.ModelConfig())
+    ring = rnd(b, kvh, win, d, dev=gpu, seed=18)
+    ring_ref = ring.clone()
+    rows = torch.arange(b, device=gpu) * kvh * win + pos % win
+    kw = dict(out_tok_index=rows, out_tok_stride=d, out_head_stride=win * d)
+    layers.head_norm_rope(x, w, cos, sin, 32, 1e-6, out=ring, **kw)
+    TorchGlue.head_norm_rope(x, w, cos, sin, 32, 1e-6, out=ring_ref, **kw)
+    touched = torch.zeros(b, kvh, win, dtype=torch.bool, device=gpu)
+    touched[torch.arange(b, device=gpu), :, pos % win] = True
+    assert torch.equal(ring[~touched], ring_ref[~touched])
+    ulp_check(ring[touched], ring_ref[touched])

@@ -43,6 +43,12 @@ SIGNATURES: dict[str, list] = {
     "yh_cu_seqlens": [_p, _i32, _p, _i64, _p],
     "yh_select_slots": [_p, _p, _i32, _p, _p, _i64, _p],
     "yh_gather_rows": [_i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p],
+    "yh_rmsnorm": [_p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p],
+    "yh_gdn_decode_prep": [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                           _p],
+    "yh_gated_rmsnorm": [_p, _p, _i64, _p, _p, _i64, _i64, _i64, _f32, _p],
+    "yh_silu_mul": [_p, _p, _i64, _i64, _p],
+    "yh_head_norm_rope": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p],
 }
 
 # entry points that do not return a status

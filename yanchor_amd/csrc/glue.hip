@@ -1,0 +1,324 @@
+// Fused decode-layer neighbours of the hot path (one launch each instead of a
+// chain of elementwise kernels):
+//
+//   rmsnorm_kernel        Qwen3_5RMSNorm, y = x / rms(x) * (1 + w), with an
+//                         optional fused residual add (the
+//                         _qwen35_rmsnorm_torch_tree / fused residual RMSNorm
+//                         of runtime/model/inference_kernels.py:227-271,
+//                         1767-1797)
+//   gdn_prep_kernel       causal conv1d decode update + SiLU, q/k/v split, and
+//                         the GDN gates beta = sigmoid(b),
+//                         g = -exp(A_log) softplus(a + dt_bias)
+//                         (inference_kernels.py:339-376, 668-691; transformers
+//                         wheel models/qwen3_5/modeling_qwen3_5.py:210-225,
+//                         500-502)
+//   gated_rmsnorm_kernel  Qwen3_5RMSNormGated (wheel:175-190)
+//   silu_mul_kernel       silu(gate) * up (inference_kernels.py:642-666)
+//   head_norm_rope_kernel per-head RMSNorm (1 + w) and rotate-half RoPE on the
+//                         leading rotary dims (modeling_yanchor.py:46-49 and the
+//                         Qwen3.5 attention q/k path)
+//
+// Every rounding point of the torch formulation is kept (bf16 where torch
+// materialises a bf16 tensor), so results match it to bf16 precision.
+#include "common.h"
+
+namespace yh {
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+__device__ __forceinline__ uint16_t tobf(float x) { return f32_to_bf16(x); }
+__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+
+constexpr int kNormThreads = 256;
+
+// Block-wide fp32 sum for 256 threads.
+__device__ __forceinline__ float block_sum256(float x) {
+  __shared__ float part[kNormThreads / kWave];
+  x = wave_sum(x);
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  if (lane == 0) part[w] = x;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / kWave; ++i) t += part[i];
+  __syncthreads();
+  return t;
+}
+
+// One workgroup per row of D bf16 elements (D % 8 == 0, D <= 8 * 256 * 4).
+// s = residual ? bf16(x + residual) : x; residual_out = s;
+// out = bf16(s / sqrt(mean(s^2) + eps) * (1 + w)).
+constexpr int kNormMaxVec = 4;  // 8-element vectors per thread
+__global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(const uint16_t* x, const uint16_t* res,
+                                                               uint16_t* res_out, const uint16_t* w, uint16_t* out,
+                                                               int D, int64_t x_stride, int64_t out_stride,
+                                                               float eps, int plus_one) {
+  const int64_t row = blockIdx.x;
+  const int nvec = D / 8;
+  float v[kNormMaxVec][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormMaxVec; ++i) {
+    const int c = threadIdx.x + i * kNormThreads;
+    if (c < nvec) {
+      const uint4 a = *reinterpret_cast<const uint4*>(x + row * x_stride + c * 8);
+      const uint16_t* ah = reinterpret_cast<const uint16_t*>(&a);
+      if (res) {
+        const uint4 r = *reinterpret_cast<const uint4*>(res + row * D + c * 8);
+        const uint16_t* rh = reinterpret_cast<const uint16_t*>(&r);
+        uint16_t sh[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sh[j] = tobf(bf(ah[j]) + bf(rh[j]));
+          v[i][j] = bf(sh[j]);
+        }
+        if (res_out) *reinterpret_cast<uint4*>(res_out + row * D + c * 8) = *reinterpret_cast<const uint4*>(sh);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[i][j] = bf(ah[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], v[i][j], ss);
+    }
+  }
+  const float r = rsqrtf(block_sum256(ss) / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int i = 0; i < kNormMaxVec; ++i) {
+    const int c = threadIdx.x + i * kNormThreads;
+    if (c < nvec) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(w + c * 8);
+      const uint16_t* wh = reinterpret_cast<const uint16_t*>(&wv);
+      uint16_t o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = tobf(v[i][j] * r * (plus_one ? 1.f + bf(wh[j]) : bf(wh[j])));
+      *reinterpret_cast<uint4*>(out + row * out_stride + c * 8) = *reinterpret_cast<const uint4*>(o);
+    }
+  }
+}
+
+// grid (B, ceil(C / 256)): channel c of row b.  proj [B, P] (row stride P)
+// holds [qkv (C) | z | b (HV) | a (HV)] at offsets 0 / -- / boff / aoff.
+// conv_state [B, K-1, C] (time-major), conv_w [C, K], K = 4.
+struct PrepArgs {
+  const uint16_t* proj;
+  uint16_t* conv_state;
+  const uint16_t* conv_w;
+  const float* a_log;
+  const float* dt_bias;
+  uint16_t* q;    // [B, QK]
+  uint16_t* k;    // [B, QK]
+  uint16_t* v;    // [B, VV]
+  float* g;       // [B, HV]
+  float* beta;    // [B, HV]
+  int C, QK, HV, boff, aoff;
+  int64_t P;
+};
+
+__global__ void __launch_bounds__(256) gdn_prep_kernel(PrepArgs a) {
+  const int64_t b = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c < a.C) {
+    uint16_t* st = a.conv_state + b * 3 * a.C;
+    const float s0 = bf(st[c]), s1 = bf(st[a.C + c]), s2 = bf(st[2 * a.C + c]);
+    const uint16_t xh = a.proj[b * a.P + c];
+    const float x = bf(xh);
+    const uint16_t* wc = a.conv_w + static_cast<int64_t>(c) * 4;
+    float acc = s0 * bf(wc[0]);
+    acc = fmaf(s1, bf(wc[1]), acc);
+    acc = fmaf(s2, bf(wc[2]), acc);
+    acc = fmaf(x, bf(wc[3]), acc);
+    const uint16_t y = tobf(silu(acc));
+    st[c] = st[a.C + c];
+    st[a.C + c] = st[2 * a.C + c];
+    st[2 * a.C + c] = xh;
+    if (c < a.QK) a.q[b * a.QK + c] = y;
+    else if (c < 2 * a.QK) a.k[b * a.QK + c - a.QK] = y;
+    else a.v[b * (a.C - 2 * a.QK) + c - 2 * a.QK] = y;
+  }
+  if (blockIdx.y == 0 && threadIdx.x < a.HV) {
+    const int h = threadIdx.x;
+    const float bb = bf(a.proj[b * a.P + a.boff + h]);
+    const float aa = bf(a.proj[b * a.P + a.aoff + h]) + a.dt_bias[h];
+    const float sp = aa > 20.f ? aa : log1pf(expf(aa));
+    a.beta[b * a.HV + h] = 1.f / (1.f + expf(-bb));
+    a.g[b * a.HV + h] = -expf(a.a_log[h]) * sp;
+  }
+}
+
+// One wave per (row, head) of 128 elements: o [N, H, 128] bf16 contiguous,
+// z with row stride z_stride (head h at z + row * z_stride + h * 128).
+__global__ void __launch_bounds__(256) gated_rmsnorm_kernel(const uint16_t* o, const uint16_t* z, int64_t z_stride,
+                                                            const uint16_t* w, uint16_t* out, int64_t NH, int H,
+                                                            float eps) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (item >= NH) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = item / H, h = item % H;
+  const uint32_t ov = reinterpret_cast<const uint32_t*>(o + item * 128)[lane];
+  const uint32_t zv = reinterpret_cast<const uint32_t*>(z + row * z_stride + h * 128)[lane];
+  const uint32_t wv = reinterpret_cast<const uint32_t*>(w)[lane];
+  const float o0 = bf(ov & 0xffff), o1 = bf(ov >> 16);
+  const float r = rsqrtf(wave_sum(o0 * o0 + o1 * o1) / 128.f + eps);
+  const float y0 = bf(tobf(bf(wv & 0xffff) * bf(tobf(o0 * r))));
+  const float y1 = bf(tobf(bf(wv >> 16) * bf(tobf(o1 * r))));
+  const uint32_t res = tobf(y0 * silu(bf(zv & 0xffff))) | (static_cast<uint32_t>(tobf(y1 * silu(bf(zv >> 16)))) << 16);
+  reinterpret_cast<uint32_t*>(out + item * 128)[lane] = res;
+}
+
+// out[n, i] = bf16(bf16(silu(gu[n, i])) * gu[n, I + i]), gu rows of 2I.
+__global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* gu, uint16_t* out, int64_t N, int I) {
+  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (idx >= N * I) return;
+  const int64_t n = idx / I, i = idx % I;
+  const uint4 gv = *reinterpret_cast<const uint4*>(gu + n * 2 * I + i);
+  const uint4 uv = *reinterpret_cast<const uint4*>(gu + n * 2 * I + I + i);
+  const uint16_t* g = reinterpret_cast<const uint16_t*>(&gv);
+  const uint16_t* u = reinterpret_cast<const uint16_t*>(&uv);
+  uint16_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = tobf(bf(tobf(silu(bf(g[j])))) * bf(u[j]));
+  *reinterpret_cast<uint4*>(out + n * I + i) = *reinterpret_cast<const uint4*>(o);
+}
+
+// One wave per (token, head) of D = 128: y = bf16(x / rms(x) * (1 + w)), then
+// rotate-half RoPE on the first rd dims with cos/sin [N_tok, rd] (fp32):
+// out = bf16(y * cos + rotate_half(y) * sin), the rest copied.  The output
+// row of (token n, head h) is out + n * out_tok_stride + h * out_head_stride.
+struct RopeArgs {
+  const uint16_t* x;
+  int64_t x_tok_stride, x_head_stride;
+  const uint16_t* w;
+  const float* cos;
+  const float* sin;
+  uint16_t* out;
+  int64_t out_tok_stride, out_head_stride;
+  const int64_t* out_tok_index;  // optional: output row of token n is out_tok_index[n] (e.g. a ring slot)
+  int64_t NH;
+  int H, rd;
+  float eps;
+};
+
+__global__ void __launch_bounds__(256) head_norm_rope_kernel(RopeArgs a) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (item >= a.NH) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t n = item / a.H, h = item % a.H;
+  const uint32_t xv = reinterpret_cast<const uint32_t*>(a.x + n * a.x_tok_stride + h * a.x_head_stride)[lane];
+  const uint32_t wv = reinterpret_cast<const uint32_t*>(a.w)[lane];
+  const float x0 = bf(xv & 0xffff), x1 = bf(xv >> 16);
+  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / 128.f + a.eps);
+  float y0 = bf(tobf(x0 * r * (1.f + bf(wv & 0xffff))));
+  float y1 = bf(tobf(x1 * r * (1.f + bf(wv >> 16))));
+  // rotary part: element e = 2 * lane + {0, 1}; partner e +- rd/2
+  const int e0 = 2 * lane, half = a.rd / 2;
+  const bool rot = e0 < a.rd;
+  const int pl = e0 < half ? lane + half / 2 : lane - half / 2;  // partner lane (rd/2 is even)
+  const float p0 = __shfl(y0, rot ? pl : lane, kWave), p1 = __shfl(y1, rot ? pl : lane, kWave);
+  if (rot) {
+    const float c0 = a.cos[n * a.rd + e0], c1 = a.cos[n * a.rd + e0 + 1];
+    const float s0 = a.sin[n * a.rd + e0], s1 = a.sin[n * a.rd + e0 + 1];
+    const float sg = e0 < half ? -1.f : 1.f;
+    y0 = y0 * c0 + sg * p0 * s0;
+    y1 = y1 * c1 + sg * p1 * s1;
+  }
+  const int64_t orow = a.out_tok_index ? a.out_tok_index[n] : n;
+  reinterpret_cast<uint32_t*>(a.out + orow * a.out_tok_stride + h * a.out_head_stride)[lane] =
+      tobf(y0) | (static_cast<uint32_t>(tobf(y1)) << 16);
+}
+
+}  // namespace
+}  // namespace yh
+
+extern "C" int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual, void* residual_out, const void* w,
+                          void* out, int64_t out_stride, int64_t N, int64_t D, float eps, int plus_one,
+                          yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(w && N >= 0 && (N == 0 || (x && out)), "rmsnorm: bad arguments");
+  YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= 8 * kNormThreads * kNormMaxVec, "rmsnorm: D must be a multiple of 8 up to %d",
+               8 * kNormThreads * kNormMaxVec);
+  YH_CHECK_ARG(x_stride % 8 == 0 && out_stride % 8 == 0, "rmsnorm: strides must be multiples of 8 elements");
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w) |
+                 reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(residual_out)) & 15) == 0,
+               "rmsnorm: pointers must be 16-byte aligned");
+  if (N == 0) return YH_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(N)), dim3(kNormThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
+                     static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
+                     static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), (int)D, x_stride, out_stride, eps,
+                     plus_one);
+  YH_CHECK_LAUNCH("rmsnorm");
+  return YH_OK;
+}
+
+extern "C" int yh_gdn_decode_prep(const void* proj, int64_t proj_stride, void* conv_state, const void* conv_w,
+                                  const float* a_log, const float* dt_bias, void* q, void* k, void* v, float* g,
+                                  float* beta, int64_t B, int64_t conv_dim, int64_t qk_dim, int64_t HV,
+                                  int64_t b_offset, int64_t a_offset, int64_t conv_kernel, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(B == 0 || (proj && conv_state && conv_w && a_log && dt_bias && q && k && v && g && beta),
+               "gdn_prep: null pointer");
+  YH_CHECK_ARG(conv_kernel == 4, "gdn_prep: conv kernel must be 4");
+  YH_CHECK_ARG(B >= 0 && conv_dim > 2 * qk_dim && qk_dim > 0 && HV > 0 && HV <= 256, "gdn_prep: bad sizes");
+  YH_CHECK_ARG(b_offset + HV <= proj_stride && a_offset + HV <= proj_stride && conv_dim <= proj_stride,
+               "gdn_prep: projection layout exceeds the row");
+  if (B == 0) return YH_OK;
+  PrepArgs a{static_cast<const uint16_t*>(proj), static_cast<uint16_t*>(conv_state),
+             static_cast<const uint16_t*>(conv_w), a_log, dt_bias, static_cast<uint16_t*>(q),
+             static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), g, beta, (int)conv_dim, (int)qk_dim, (int)HV,
+             (int)b_offset, (int)a_offset, proj_stride};
+  hipLaunchKernelGGL(gdn_prep_kernel, dim3(static_cast<unsigned>(B), static_cast<unsigned>((conv_dim + 255) / 256)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  YH_CHECK_LAUNCH("gdn_prep");
+  return YH_OK;
+}
+
+extern "C" int yh_gated_rmsnorm(const void* o, const void* z, int64_t z_stride, const void* w, void* out, int64_t N,
+                                int64_t H, int64_t D, float eps, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(N >= 0 && H > 0 && (N == 0 || (o && z && w && out)), "gated_rmsnorm: bad arguments");
+  YH_CHECK_ARG(D == 128, "gated_rmsnorm: head dim must be 128");
+  YH_CHECK_ARG(z_stride % 2 == 0 && ((reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(o)) & 3) == 0,
+               "gated_rmsnorm: 4-byte alignment");
+  if (N == 0) return YH_OK;
+  const int64_t nh = N * H;
+  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(static_cast<unsigned>((nh + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(o),
+                     static_cast<const uint16_t*>(z), z_stride, static_cast<const uint16_t*>(w),
+                     static_cast<uint16_t*>(out), nh, (int)H, eps);
+  YH_CHECK_LAUNCH("gated_rmsnorm");
+  return YH_OK;
+}
+
+extern "C" int yh_silu_mul(const void* gate_up, void* out, int64_t N, int64_t I, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(N >= 0 && (N == 0 || (gate_up && out)) && I > 0 && I % 8 == 0, "silu_mul: I must be a positive multiple of 8");
+  if (N == 0) return YH_OK;
+  const int64_t vecs = N * I / 8;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((vecs + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up),
+                     static_cast<uint16_t*>(out), N, (int)I);
+  YH_CHECK_LAUNCH("silu_mul");
+  return YH_OK;
+}
+
+extern "C" int yh_head_norm_rope(const void* x, int64_t x_tok_stride, int64_t x_head_stride, const void* w,
+                                 const float* cos, const float* sin, void* out, int64_t out_tok_stride,
+                                 int64_t out_head_stride, const int64_t* out_tok_index, int64_t N, int64_t H,
+                                 int64_t D, int64_t rotary_dim, float eps, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(N >= 0 && H > 0 && (N == 0 || (x && w && out)), "head_norm_rope: bad arguments");
+  YH_CHECK_ARG(D == 128, "head_norm_rope: head dim must be 128");
+  YH_CHECK_ARG(rotary_dim >= 0 && rotary_dim <= D && rotary_dim % 4 == 0, "head_norm_rope: rotary dim %lld",
+               (long long)rotary_dim);
+  YH_CHECK_ARG(rotary_dim == 0 || (cos && sin), "head_norm_rope: cos/sin required");
+  YH_CHECK_ARG((x_tok_stride | x_head_stride | out_tok_stride | out_head_stride) % 2 == 0,
+               "head_norm_rope: strides must be even");
+  if (N == 0) return YH_OK;
+  RopeArgs a{static_cast<const uint16_t*>(x), x_tok_stride, x_head_stride, static_cast<const uint16_t*>(w), cos, sin,
+             static_cast<uint16_t*>(out), out_tok_stride, out_head_stride, out_tok_index, N * H, (int)H,
+             (int)rotary_dim, eps};
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3(static_cast<unsigned>((N * H + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  YH_CHECK_LAUNCH("head_norm_rope");
+  return YH_OK;
+}

@@ -1,0 +1,119 @@
+"""Fused decode-layer neighbours of the hot path (HIP kernels, bf16 activations).
+
+RMSNorm with a fused residual add, the GDN decode prologue (causal conv1d
+update + SiLU + q/k/v split + beta/g gates), the gated RMSNorm of the GDN
+output, silu(gate) * up, and per-head RMSNorm + partial RoPE.  Each keeps the
+rounding points of the torch formulation it replaces (cited per function).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+
+def _bf16(*ts):
+    for t in ts:
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError("fused layer kernels take bfloat16 activations")
+
+
+def rmsnorm(x, w, eps, residual=None, plus_one=True):
+    """Qwen3.5 RMSNorm over the last dim (x / rms(x) * (1 + w)).  With
+    ``residual``: s = x + residual is formed first and ``(norm(s), s)`` is
+    returned (the fused residual RMSNorm, runtime/model/inference_kernels.py:
+    1767-1797)."""
+    _bf16(x, w, residual)
+    d = x.shape[-1]
+    if x.stride(-1) != 1 or (x.ndim > 1 and x.stride(-2) % 8):
+        x = x.contiguous()
+    rows = x.numel() // d
+    N.require_device(x, w, residual)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    res_out = None
+    if residual is not None:
+        residual = residual.contiguous()
+        res_out = torch.empty_like(residual)
+    x_stride = x.stride(-2) if x.ndim > 1 else d
+    if x.ndim > 2 and not x.is_contiguous():
+        x = x.contiguous()
+        x_stride = d
+    N.call("yh_rmsnorm", x.data_ptr(), x_stride, N.ptr(residual), N.ptr(res_out), w.data_ptr(), out.data_ptr(), d,
+           rows, d, float(eps), int(plus_one), N.stream_of(x))
+    return out if residual is None else (out, res_out)
+
+
+def gdn_decode_prep(proj, conv_state, conv_w, a_log, dt_bias, *, conv_dim, qk_dim, hv, b_offset, a_offset):
+    """Decode prologue of a GDN layer from the packed projection ``proj``
+    [B, P] (qkv | z | b | a): returns q, k [B, 1, H, dk], v [B, 1, HV, dv]
+    (bf16), g, beta [B, 1, HV] (float32); ``conv_state`` [B, 3, conv_dim] is
+    shifted in place.  Replaces the graph-safe conv update and the fused GDN
+    gates (runtime/model/inference_kernels.py:339-376, 668-691)."""
+    _bf16(proj, conv_state, conv_w)
+    b = proj.shape[0]
+    if proj.stride(-1) != 1:
+        raise ValueError("proj must have unit column stride")
+    if conv_state.shape != (b, 3, conv_dim) or not conv_state.is_contiguous():
+        raise ValueError("conv_state must be contiguous [B, 3, conv_dim]")
+    dev = N.require_device(proj, conv_state, conv_w, a_log, dt_bias)
+    q = torch.empty(b, qk_dim, dtype=proj.dtype, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(b, conv_dim - 2 * qk_dim, dtype=proj.dtype, device=dev)
+    g = torch.empty(b, hv, dtype=torch.float32, device=dev)
+    beta = torch.empty_like(g)
+    N.call("yh_gdn_decode_prep", proj.data_ptr(), proj.stride(0), conv_state.data_ptr(), conv_w.data_ptr(),
+           a_log.data_ptr(), dt_bias.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(),
+           beta.data_ptr(), b, conv_dim, qk_dim, hv, b_offset, a_offset, 4, N.stream_of(proj))
+    return q, k, v, g, beta
+
+
+def gated_rmsnorm(o, z, w, eps):
+    """Qwen3_5RMSNormGated (transformers wheel models/qwen3_5/modeling_qwen3_5.py:
+    175-190) per head of 128: o [B, H, 128] contiguous, z a [B, H * 128] view
+    (any row stride).  Returns [B, H * 128]."""
+    _bf16(o, z, w)
+    b, h, d = o.shape
+    o = o.contiguous()
+    if z.stride(-1) != 1:
+        z = z.contiguous()
+    N.require_device(o, z, w)
+    out = torch.empty(b, h * d, dtype=o.dtype, device=o.device)
+    N.call("yh_gated_rmsnorm", o.data_ptr(), z.data_ptr(), z.stride(0), w.data_ptr(), out.data_ptr(), b, h, d,
+           float(eps), N.stream_of(o))
+    return out
+
+
+def silu_mul(gate_up):
+    """silu(gate) * up of a packed [*, 2I] projection (runtime/model/
+    inference_kernels.py:642-666); returns [*, I]."""
+    _bf16(gate_up)
+    gu = gate_up.contiguous()
+    i2 = gu.shape[-1]
+    n = gu.numel() // i2
+    N.require_device(gu)
+    out = torch.empty(*gu.shape[:-1], i2 // 2, dtype=gu.dtype, device=gu.device)
+    N.call("yh_silu_mul", gu.data_ptr(), out.data_ptr(), n, i2 // 2, N.stream_of(gu))
+    return out
+
+
+def head_norm_rope(x, w, cos, sin, rotary_dim, eps, *, out=None, out_tok_index=None, out_tok_stride=None,
+                   out_head_stride=None):
+    """Per-head RMSNorm (1 + w) then rotate-half RoPE on the first
+    ``rotary_dim`` dims.  x [N, H, 128] (any token / head strides, unit last
+    stride); cos / sin float [N, rotary_dim].  Writes a new [N, H, 128] tensor,
+    or into ``out`` at row ``out_tok_index[n]`` with the given strides."""
+    _bf16(x, w)
+    n, h, d = x.shape
+    if x.stride(-1) != 1:
+        raise ValueError("x must have unit last stride")
+    dev = N.require_device(x, w, cos, sin, out, out_tok_index)
+    if out is None:
+        out = torch.empty(n, h, d, dtype=x.dtype, device=dev)
+        out_tok_stride, out_head_stride = h * d, d
+    cs = None if cos is None else cos.float().contiguous()
+    sn = None if sin is None else sin.float().contiguous()
+    idx = None if out_tok_index is None else out_tok_index.to(torch.int64).contiguous()
+    N.call("yh_head_norm_rope", x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), N.ptr(cs), N.ptr(sn),
+           out.data_ptr(), out_tok_stride, out_head_stride, N.ptr(idx), n, h, d, rotary_dim, float(eps),
+           N.stream_of(x))
+    return out

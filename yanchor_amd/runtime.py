@@ -70,10 +70,39 @@ class HipOps:
     """The package's HIP kernels behind the reference's call signatures."""
 
     def __init__(self):
-        from . import gdn, independent_memory, inference_kernels
+        from . import gdn, independent_memory, inference_kernels, layers
         self.gdn = gdn
         self.mem = independent_memory
         self.ik = inference_kernels
+        self.layers = layers
+
+    # Fused decode-layer neighbours: HIP kernels for bf16 activations (the
+    # served configuration).  A float32 model (used to pin the cache logic
+    # without bf16 rounding) runs the torch formulations of the same layers.
+    def rmsnorm(self, x, w, eps, residual=None):
+        if x.dtype != torch.bfloat16:
+            return TorchGlue.rmsnorm(x, w, eps, residual)
+        return self.layers.rmsnorm(x, w, eps, residual=residual)
+
+    def gdn_prep(self, proj, conv_state, conv_w, a_log, dt_bias, **kw):
+        if proj.dtype != torch.bfloat16:
+            return TorchGlue.gdn_prep(proj, conv_state, conv_w, a_log, dt_bias, **kw)
+        return self.layers.gdn_decode_prep(proj, conv_state, conv_w, a_log, dt_bias, **kw)
+
+    def gated_rmsnorm(self, o, z, w, eps):
+        if o.dtype != torch.bfloat16:
+            return TorchGlue.gated_rmsnorm(o, z, w, eps)
+        return self.layers.gated_rmsnorm(o, z, w, eps)
+
+    def silu_mul(self, gate_up):
+        if gate_up.dtype != torch.bfloat16:
+            return TorchGlue.silu_mul(gate_up)
+        return self.layers.silu_mul(gate_up)
+
+    def head_norm_rope(self, x, w, cos, sin, rotary_dim, eps, **kw):
+        if x.dtype != torch.bfloat16:
+            return TorchGlue.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
+        return self.layers.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
 
     def gdn_decode(self, q, k, v, g, beta, state):
         o, _ = self.gdn.recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=state,
@@ -113,10 +142,12 @@ def rms_norm(x, w, eps, plus_one=True):
 
 
 def gated_rms_norm(x, gate, w, eps):
-    """Qwen3_5RMSNormGated: normalise, scale by w, times silu(gate) (wheel:175-190)."""
+    """Qwen3_5RMSNormGated (transformers wheel models/qwen3_5/modeling_qwen3_5.py:
+    175-184): normalise in fp32, round, scale by w in the weight dtype, times
+    silu(gate) in fp32."""
     xf = x.float()
     y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    y = (w.float() * y.to(x.dtype).float()) * F.silu(gate.float())
+    y = (w * y.to(x.dtype)).float() * F.silu(gate.float())
     return y.to(x.dtype)
 
 
@@ -136,6 +167,51 @@ def apply_rope(x, cos, sin, rd):
     rot = torch.cat((-x2, x1), -1)
     out = xr * cos + rot * sin
     return torch.cat((out.to(x.dtype), x[..., rd:]), -1)
+
+
+class TorchGlue:
+    """Torch formulations of the fused decode-layer kernels, argument for
+    argument (the definitions the kernels are tested against)."""
+
+    @staticmethod
+    def rmsnorm(x, w, eps, residual=None):
+        if residual is None:
+            return rms_norm(x, w, eps)
+        s = x + residual
+        return rms_norm(s, w, eps), s
+
+    @staticmethod
+    def gdn_prep(proj, conv_state, conv_w, a_log, dt_bias, *, conv_dim, qk_dim, hv, b_offset, a_offset):
+        window = torch.cat((conv_state, proj[:, None, :conv_dim]), 1)          # [B, K, C], oldest first
+        conv_state.copy_(window[:, 1:])
+        mixed = F.silu((window.float() * conv_w.float().t()[None]).sum(1)).to(proj.dtype)
+        beta = torch.sigmoid(proj[:, b_offset: b_offset + hv].float())
+        g = -torch.exp(a_log) * F.softplus(proj[:, a_offset: a_offset + hv].float() + dt_bias)
+        return mixed[:, :qk_dim], mixed[:, qk_dim: 2 * qk_dim], mixed[:, 2 * qk_dim:], g, beta
+
+    @staticmethod
+    def gated_rmsnorm(o, z, w, eps):
+        b, h, d = o.shape
+        return gated_rms_norm(o, z.reshape(b, h, d), w, eps).reshape(b, h * d)
+
+    @staticmethod
+    def silu_mul(gate_up):
+        gate, up = gate_up.chunk(2, -1)
+        return F.silu(gate) * up
+
+    @staticmethod
+    def head_norm_rope(x, w, cos, sin, rotary_dim, eps, *, out=None, out_tok_index=None, out_tok_stride=None,
+                       out_head_stride=None):
+        y = rms_norm(x, w, eps)
+        if rotary_dim:
+            y = apply_rope(y, cos[:, None], sin[:, None], rotary_dim)
+        if out is None:
+            return y
+        n, h, d = y.shape
+        rows = (out.numel() - (h - 1) * out_head_stride - d) // out_tok_stride + 1
+        dst = out.as_strided((rows, h, d), (out_tok_stride, out_head_stride, 1))
+        dst[out_tok_index] = y
+        return out
 
 
 class Model:
@@ -194,7 +270,8 @@ class Model:
         for i, L in enumerate(self.layers):
             if L["kind"] == "gdn":
                 self.gdn_state[i] = torch.zeros(B, c.gdn_heads_v, c.gdn_dk, c.gdn_dv, device=dev)
-                self.conv_state[i] = torch.zeros(B, c.conv_dim, c.conv_kernel - 1, device=dev, dtype=self.dtype)
+                # time-major [B, K-1, C]: the decode prologue reads one coalesced row per tap
+                self.conv_state[i] = torch.zeros(B, c.conv_kernel - 1, c.conv_dim, device=dev, dtype=self.dtype)
             else:
                 self.ring_k[i] = torch.zeros(B, c.kv_heads, c.swa_window, c.head_dim, device=dev, dtype=self.dtype)
                 self.ring_v[i] = torch.zeros_like(self.ring_k[i])
@@ -216,9 +293,7 @@ class Model:
 
     # ---------------- layers ----------------
     def _mlp(self, L, x):
-        gu = F.linear(x, L["mlp_gate_up"])
-        gate, up = gu.chunk(2, -1)
-        return F.linear(F.silu(gate) * up, L["mlp_down"])
+        return F.linear(self.ops.silu_mul(F.linear(x, L["mlp_gate_up"])), L["mlp_down"])
 
     def _gdn_split(self, L, proj):
         c = self.cfg
@@ -230,21 +305,18 @@ class Model:
         g = -torch.exp(L["a_log"]) * F.softplus(a.float() + L["dt_bias"])
         return qkv, z, beta, g
 
-    def _gdn_decode(self, i, L, x):
-        c, B = self.cfg, x.shape[0]
-        proj = F.linear(rms_norm(x, L["in_norm"], c.rms_eps), L["w_in"])
-        qkv, z, beta, g = self._gdn_split(L, proj)
-        cs = self.conv_state[i]
-        window = torch.cat((cs, qkv[:, :, None]), -1)                      # [B, C, K]
-        cs.copy_(window[:, :, 1:])
-        mixed = F.silu((window.float() * L["conv_w"].float()).sum(-1)).to(self.dtype)
-        hk, dk, dv = c.gdn_heads_k * c.gdn_dk, c.gdn_dk, c.gdn_dv
-        q = mixed[:, :hk].reshape(B, 1, c.gdn_heads_k, dk)
-        k = mixed[:, hk: 2 * hk].reshape(B, 1, c.gdn_heads_k, dk)
-        v = mixed[:, 2 * hk:].reshape(B, 1, c.gdn_heads_v, dv)
-        o = self.ops.gdn_decode(q, k, v, g[:, None], beta[:, None], self.gdn_state[i])
-        o = gated_rms_norm(o.reshape(B, c.gdn_heads_v, dv), z.reshape(B, c.gdn_heads_v, dv), L["gnorm"], c.rms_eps)
-        return F.linear(o.reshape(B, -1), L["w_out"])
+    def _gdn_decode(self, i, L, xn):
+        """GDN mixer for one token per slot; xn is the normalised layer input."""
+        c, B, ops = self.cfg, xn.shape[0], self.ops
+        hv, dv, vd = c.gdn_heads_v, c.gdn_dv, c.gdn_heads_v * c.gdn_dv
+        proj = F.linear(xn, L["w_in"])                                     # [B, qkv | z | b | a]
+        q, k, v, g, beta = ops.gdn_prep(proj, self.conv_state[i], L["conv_w"], L["a_log"], L["dt_bias"],
+                                        conv_dim=c.conv_dim, qk_dim=c.gdn_heads_k * c.gdn_dk, hv=hv,
+                                        b_offset=c.conv_dim + vd, a_offset=c.conv_dim + vd + hv)
+        o = ops.gdn_decode(q.view(B, 1, c.gdn_heads_k, c.gdn_dk), k.view(B, 1, c.gdn_heads_k, c.gdn_dk),
+                           v.view(B, 1, hv, dv), g[:, None], beta[:, None], self.gdn_state[i])
+        y = ops.gated_rmsnorm(o.view(B, hv, dv), proj[:, c.conv_dim: c.conv_dim + vd], L["gnorm"], c.rms_eps)
+        return F.linear(y, L["w_out"])
 
     def _attn_project(self, L, x, cos, sin):
         c = self.cfg
@@ -277,39 +349,67 @@ class Model:
         key = apply_rope(rms_norm(key, L["m_k_norm"], c.rms_eps), cos, sin, c.rotary_dim)
         return q, gate, key, val.contiguous(), scores
 
-    def _attn_decode(self, i, L, x, hidden, positions, cos, sin, valid):
-        c, B = self.cfg, x.shape[0]
-        cs, sn = cos[:, None], sin[:, None]
-        q, gate, k, v = self._attn_project(L, rms_norm(x, L["in_norm"], c.rms_eps), cs, sn)
-        slot = (positions % c.swa_window).long()
-        rows = torch.arange(B, device=x.device)
-        self.ring_k[i][rows, :, slot] = k
-        self.ring_v[i][rows, :, slot] = v
+    def _memory_decode(self, L, hidden, cos, sin):
+        """``_memory_qkvs`` for one token per slot on the fused kernels."""
+        c, B, ops = self.cfg, hidden.shape[0], self.ops
+        H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
+        u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
+        mq = F.linear(u, L["m_q"]).view(B, H, D)
+        qn = ops.head_norm_rope(mq, L["m_q_norm"], None, None, 0, c.rms_eps)
+        gate = torch.tanh(L["read_scale"]) * 2 * torch.sigmoid(
+            (qn.float() * L["read_gate_w"]).sum(-1) / math.sqrt(D) + L["read_gate_b"])
+        q = ops.head_norm_rope(mq, L["m_q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
+        scores = F.linear(F.silu(F.linear(u, L["adm_down"])).float(), L["adm_up"])
+        zz = u + F.linear(ops.silu_mul(F.linear(u, L["writer_gate_up"])), L["writer_down"])
+        kv = F.linear(zz, L["m_kv"])
+        key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
+                                 c.rms_eps)
+        return q, gate, key, kv[:, KVH * D:].reshape(B, KVH, D), scores
+
+    def _attn_decode(self, i, L, xn, hidden, positions, cos, sin, valid, ring_rows):
+        """SWA + anchor-memory mixer for one token per slot.  xn is the
+        normalised layer input, hidden the residual stream entering the layer;
+        ring_rows[b] = b * kv_heads * window + positions[b] % window."""
+        c, B, ops = self.cfg, xn.shape[0], self.ops
+        H, KVH, D, W = c.attn_heads, c.kv_heads, c.head_dim, c.swa_window
+        proj = F.linear(xn, L["w_qkv"])                                    # [B, (q|gate) per head | k | v]
+        hq = 2 * H * D
+        qg = proj[:, :hq].view(B, H, 2 * D)
+        q = ops.head_norm_rope(qg[..., :D], L["q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
+        ops.head_norm_rope(proj[:, hq: hq + KVH * D].view(B, KVH, D), L["k_norm"], cos, sin, c.rotary_dim,
+                           c.rms_eps, out=self.ring_k[i], out_tok_index=ring_rows, out_tok_stride=D,
+                           out_head_stride=W * D)
+        slot = positions % W
+        rows = torch.arange(B, device=xn.device)
+        self.ring_v[i][rows, :, slot] = proj[:, hq + KVH * D:].view(B, KVH, D)
         self.ring_pos[i][rows, :, slot] = positions.to(torch.int32)[:, None]
-        att = self.ops.window_attend(q[:, None].contiguous(), self.ring_k[i], self.ring_v[i], self.ring_pos[i])
-        att = att.reshape(B, -1) * torch.sigmoid(gate)
-        out = F.linear(att, L["w_o"])
-        mq, mgate, mk, mv, mscores = self._memory_qkvs(L, hidden, cs, sn)
-        read = self.ops.memory_read(mq[:, None].contiguous(), self.memory[i])
-        self.ops.memory_commit(mk[:, None].contiguous(), mv[:, None], mscores[:, None], valid,
-                               c.memory_chunk, self.memory[i])
+        att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i])
+        out = F.linear((att[:, 0] * torch.sigmoid(qg[..., D:])).reshape(B, -1), L["w_o"])
+        mq, mgate, mk, mv, mscores = self._memory_decode(L, hidden, cos, sin)
+        read = ops.memory_read(mq[:, None], self.memory[i])
+        ops.memory_commit(mk[:, None], mv[:, None], mscores[:, None], valid, c.memory_chunk, self.memory[i])
         read = read[:, 0] * valid[:, None, None].to(read.dtype)
         mem_out = F.linear((read * mgate[..., None].to(read.dtype)).reshape(B, -1), L["m_o"])
         return out + mem_out
 
     def decode_step(self, tokens, positions, valid):
         """One token for every slot: tokens, positions [B] int64, valid [B] bool
-        -> logits [B, V] float32.  Updates every cache in place."""
-        c = self.cfg
+        -> logits [B, V] float32.  Updates every cache in place.  Each residual
+        add is fused into the RMSNorm that follows it."""
+        c, ops, B = self.cfg, self.ops, tokens.shape[0]
         h = self.embed[tokens]
         cos, sin = rope_tables(positions, c)
+        ring_rows = torch.arange(B, device=h.device) * (c.kv_heads * c.swa_window) + positions % c.swa_window
+        xn = ops.rmsnorm(h, self.layers[0]["in_norm"], c.rms_eps)
         for i, L in enumerate(self.layers):
             if L["kind"] == "gdn":
-                h = h + self._gdn_decode(i, L, h)
+                delta = self._gdn_decode(i, L, xn)
             else:
-                h = h + self._attn_decode(i, L, h, h, positions, cos, sin, valid)
-            h = h + self._mlp(L, rms_norm(h, L["post_norm"], c.rms_eps))
-        return F.linear(rms_norm(h, self.final_norm, c.rms_eps), self.lm_head).float()
+                delta = self._attn_decode(i, L, xn, h, positions, cos, sin, valid, ring_rows)
+            xn, h = ops.rmsnorm(delta, L["post_norm"], c.rms_eps, residual=h)
+            nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
+            xn, h = ops.rmsnorm(self._mlp(L, xn), nxt, c.rms_eps, residual=h)
+        return F.linear(xn, self.lm_head).float()
 
     # ---------------- prefill ----------------
     def prefill(self, prompts):
@@ -335,7 +435,7 @@ class Model:
                 xw = F.pad(qkv.float(), (0, 0, c.conv_kernel - 1, 0))           # causal conv over time
                 mixed = sum(xw[:, j: j + T] * L["conv_w"].float()[:, j] for j in range(c.conv_kernel))
                 mixed = F.silu(mixed).to(self.dtype)
-                tmp.conv_state[i].copy_(qkv[:, T - (c.conv_kernel - 1):].transpose(1, 2))
+                tmp.conv_state[i].copy_(xw[:, T:])                              # last K-1 inputs, zero-padded
                 hk, dk, dv = c.gdn_heads_k * c.gdn_dk, c.gdn_dk, c.gdn_dv
                 q = mixed[..., :hk].reshape(1, R * T, c.gdn_heads_k, dk)
                 k = mixed[..., hk: 2 * hk].reshape(1, R * T, c.gdn_heads_k, dk)
