@@ -1,53 +1,70 @@
 """Benchmark of the YANchor recurrent decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
 
 Prints one JSON line.  Workloads:
 
-* ``gdn_decode`` (default): one decode step of the gated-delta state update on
-  the decode configuration -- 64 live sequences, HV = 32 heads,
-  dk = dv = 128, fp32 state [64, 32, 128, 128] ~ N(0, 0.02) updated in place,
-  bf16 q/k/v, fp32 g/beta.  Steps cycle over 4 independent layer states
-  (4 x 128 MiB) so no launch finds its state in the 256 MB Infinity Cache
-  left behind by the previous one.  value = decode tokens/s of that layer step
-  (64 tokens per step).  The same step through a 96-row slot pool with
-  state_indices (the vLLM-style indirection) is reported as ``pooled_slots``.
+* ``model_decode`` (default): continuous-batching decode of the random-init
+  4B-shaped hybrid model (36 layers: 27 Gated DeltaNet + 9 sliding-window /
+  anchor-memory layers, hidden 2560, 32 heads, dk = dv = 128, 256 anchor slots,
+  vocab 151936, bf16 weights ~ N(0, 0.02)) over a physical batch of 128 slots.
+  Requests arrive as a Poisson process (mean 4 per step) with random 128-token
+  prompts and geometric generation lengths (mean 1024); finished slots are
+  refilled at poll points every 32 steps; sampling is top-k 20 / top-p 0.95 /
+  T = 0.6 with presence penalty 1.5.  One step = one captured HIP graph of the
+  whole model forward + sampling + slot bookkeeping for all 128 slots.
+  value = useful decode tokens / (timed wall - refill prefill time), the
+  reference's decode tokens/s definition.
+* ``gdn_decode``: the state-update kernel alone on a [B, 32, 128, 128] fp32
+  state (``--batch``, default 64) with bf16 q/k/v, cycling over 4 layer states.
+* ``hbm_copy``: a 128 MiB device copy, the calibration kernel for the HBM byte
+  counters behind ``roofline.traffic``.
 
-Timing: W untimed steps, then K steps between two stream synchronisations,
-with HIP events (torch.cuda.Event on the stream the kernels are launched on)
-around the timed region.  ``roofline`` prices the state-update kernel's
-algorithmic bytes per launch against the 8 TB/s HBM peak.  ``cpu_baseline``
-times the CPU oracle (torch float32, host threads) on a bounded sample of the
-same workload.
+Timing: W untimed steps, then K steps between two device synchronisations.
+``roofline`` prices the GDN state-update kernel (the dominant hot-path kernel):
+its algorithmic bytes per launch at the model's decode shape over its average
+launch time, measured here with HIP events on the stream the kernel runs on,
+cycling over the model's 27 layer states.  ``cpu_baseline`` runs the same
+model's decode step on the host cores with the oracle's recurrence, anchor
+memory, sampler and bookkeeping, on a bounded number of steps.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
 from pathlib import Path
 
+import torch
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per launch of gdn_recurrent_kernel on the decode workload, from
-# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled by the same
-# counters on a copy kernel of known size (FETCH x 2.0, WRITE x 1.0).
-TRAFFIC_GDN_DECODE = None
 METRIC = "decode tokens/s at B=128 on 1 GPU; state-update HBM GB/s as % of peak"
+# HBM bytes per launch of gdn_recurrent_kernel, by batch rows, from rocprofv3
+# --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) on
+# ``bench.py --workload gdn_decode --batch B``, scaled by what the same counters
+# read for a 128 MiB float4 copy kernel (FETCH x 2.0, WRITE x 1.0).
+TRAFFIC_GDN_DECODE = {128: (133803.7 * 2.0 + 263283.8) * 1024}
 
 
 def gdn_state_bytes(b, h, hv, kd, vd, qkv_size, gate_size, with_indices):
     """Algorithmic HBM bytes of one decode step of the state update."""
-    state = 2 * b * hv * kd * vd * 4            # fp32 state read + write
-    inputs = b * (2 * h * kd + hv * vd) * qkv_size  # q, k, v
-    gates = 2 * b * hv * gate_size                # g, beta
-    out = b * hv * vd * qkv_size                  # o
+    state = 2 * b * hv * kd * vd * 4                 # fp32 state read + write
+    inputs = b * (2 * h * kd + hv * vd) * qkv_size   # q, k, v
+    gates = 2 * b * hv * gate_size                   # g, beta
+    out = b * hv * vd * qkv_size                     # o
     idx = 4 * b if with_indices else 0
     return state + inputs + gates + out + idx
+
+
+def _log(msg):
+    """Progress line on stderr (stdout carries only the JSON result)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def cpu_threads() -> int:
@@ -58,10 +75,10 @@ def cpu_threads() -> int:
     return max(1, min(16, n))
 
 
-def _time_steps(step, steps, warmup):
-    """W untimed steps, then K timed steps between stream synchronisations.
-    Returns (wall ms per step, event ms per step on the launch stream)."""
-    import torch
+def _time_launches(step, steps, warmup):
+    """W untimed calls, then K calls between stream synchronisations, with HIP
+    events on the current stream (the one the kernels are launched on).
+    Returns (wall ms per call, event ms per call)."""
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -77,117 +94,256 @@ def _time_steps(step, steps, warmup):
     return wall * 1e3 / steps, ev0.elapsed_time(ev1) / steps
 
 
-def bench_gdn_decode(steps: int, warmup: int, cpu: bool) -> dict:
-    """Decode state update on the [64, 32, 128, 128] fp32 state (rows indexed
-    densely, like the reference's in-place decode launch), plus the same step
-    through a 96-slot pool with state_indices as a secondary figure."""
-    import torch
+def gdn_roofline(states, b, h, kd, vd, launches=216, warmup=27):
+    """Average launch time of the GDN decode state update cycling over
+    ``states`` (each [b, HV, kd, vd] fp32, updated in place) with fresh bf16
+    q/k/v and fp32 gates; returns the roofline object."""
+    from yanchor_amd import gdn, workloads
+
+    hv = states[0].shape[1]
+    x = workloads.gdn_inputs(b, 1, h, hv, kd, vd, dtype=torch.bfloat16, seed=workloads.SEED0 + 7)
+    q, k, v, g, beta = (t.to(states[0].device) for t in (x.q, x.k, x.v, x.g, x.beta))
+
+    def step(i):
+        gdn.recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=states[i % len(states)])
+
+    _, ms = _time_launches(step, launches, warmup)
+    nbytes = gdn_state_bytes(b, h, hv, kd, vd, 2, 4, False)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_GDN_DECODE.get(b),
+            "kernel": "gdn_recurrent_kernel", "bytes_per_launch": nbytes, "avg_launch_us": ms * 1e3,
+            "launches": launches, "shape": f"state fp32 [{b}, {hv}, {kd}, {vd}], {len(states)} rotating layer states"}
+
+
+# ---------------------------------------------------------------------------
+# model_decode
+
+def bench_model_decode(steps, warmup, cpu, batch=128):
+    from yanchor_amd import runtime as rt
+
+    dev = torch.device("cuda:0")
+    cfg = rt.ModelConfig()
+    model = rt.Model(cfg, batch=batch, device=dev, seed=0)
+    _log(f"model_decode: model built, {warmup} warm-up + {steps} timed steps")
+    met = rt.run_decode_benchmark(model, steps=steps, warmup=warmup, rate=4.0, prompt_len=128, mean_len=1024,
+                                  poll_interval=32)
+    states = [model.gdn_state[i] for i in sorted(model.gdn_state)]
+    _log(f"model_decode: {met.decode_tokens_per_second:.0f} tokens/s; timing the GDN state update")
+    roof = gdn_roofline(states, batch, cfg.gdn_heads_k, cfg.gdn_dk, cfg.gdn_dv)
+    res = {
+        "value": met.decode_tokens_per_second,
+        "unit": "tokens/s",
+        "ms_per_step": met.decode_seconds * 1e3 / met.decode_steps,
+        "dtype": "bf16",
+        "config": {"workload": "model_decode: random-init 4B-shaped hybrid recurrent model (36 layers = 27 GDN "
+                               "+ 9 SWA/anchor-memory, hidden 2560, 32 heads, dk=dv=128, 256 anchor slots, "
+                               "vocab 151936), continuous batching over 128 slots, Poisson(4) arrivals of "
+                               "128-token prompts, geometric(1024) lengths, refill every 32 steps, "
+                               "top-k 20 / top-p 0.95 / T 0.6 sampling",
+                   "global_batch": batch, "seq_len": 1, "parallelism": "single GPU"},
+        "roofline": roof,
+        "decode": {"useful_token_events": met.decode_useful_token_events,
+                   "scheduled_token_events": met.decode_scheduled_token_events,
+                   "decode_seconds": met.decode_seconds, "refill_prefill_seconds": met.refill_prefill_seconds,
+                   "wall_seconds": met.generation_wall_seconds, "refilled": met.refilled,
+                   "completed": met.completed, "peak_hbm_gib": met.peak_allocated_gib, **met.extra},
+    }
+    del model, states
+    torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = cpu_model_decode(batch)
+    return res
+
+
+class _OracleOps:
+    """The oracle's CPU recurrence, anchor memory, sampler and bookkeeping
+    behind the runtime's ops interface (float32), plus the torch layer glue."""
+
+    def __init__(self):
+        from oracle import anchor, gdn, sampling, slots
+        from yanchor_amd.runtime import TorchGlue
+        self.gdn_ref, self.anchor, self.sampling, self.slots = gdn, anchor, sampling, slots
+        self.glue = TorchGlue
+        for name in ("rmsnorm", "gdn_prep", "gated_rmsnorm", "silu_mul", "head_norm_rope"):
+            setattr(self, name, getattr(TorchGlue, name))
+
+    def gdn_decode(self, q, k, v, g, beta, state):
+        o, st = self.gdn_ref.recurrent_gated_delta_rule(q, k, v, g, beta, state, dtype=torch.float32)
+        state.copy_(st)
+        return o.to(q.dtype)
+
+    def window_attend(self, q, keys, values, positions):
+        b, _, h, d = q.shape
+        g = keys.shape[1]
+        qq = q[:, 0].reshape(b, g, h // g, d).float()
+        logits = torch.matmul(qq, keys.float().transpose(-1, -2)) / math.sqrt(d)     # [B, G, R, W]
+        logits = logits.masked_fill((positions < 0)[:, :, None, :], -math.inf)
+        out = torch.matmul(logits.softmax(-1), values.float())
+        return out.reshape(b, 1, h, d).to(q.dtype)
+
+    def memory_read(self, q, state):
+        return self.anchor.committed_read(q, state, dtype=torch.float32)
+
+    def memory_commit(self, key, value, scores, active, chunk, state):
+        self.anchor.commit_decode(key, value, scores, active, chunk, state)
+
+    def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty):
+        sc = self.sampling.presence_penalty(logits, seen, penalty) if seen is not None else logits.float()
+        vals, idx = torch.topk(sc / temperature, top_k, dim=-1)
+        return self.sampling.top20_counter_sample(vals, idx, attempt_ids, steps, seed=seed, top_p=top_p)
+
+    def bookkeeping(self, *args, **kw):
+        self.slots.decode_state_update_torch(*args, **kw)
+
+
+def cpu_model_decode(batch, budget_s=20.0, max_steps=32):
+    """Decode steps of the same model shape on the host cores: float32 weights
+    (tiled N(0, 0.02) block), every slot live at position 128, the oracle's
+    recurrence / anchor memory / sampler / bookkeeping.  Timed until
+    ``budget_s`` of CPU work (at least one step after one warm-up step)."""
+    from yanchor_amd import runtime as rt
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    cfg = rt.ModelConfig()
+    m = rt.Model(cfg, batch=batch, device="cpu", seed=0, ops=_OracleOps(), dtype=torch.float32, init="tiled")
+    gen = torch.Generator().manual_seed(5)
+    tokens = torch.randint(0, cfg.vocab, (batch,), generator=gen)
+    positions = torch.full((batch,), 128, dtype=torch.long)
+    valid = torch.ones(batch, dtype=torch.bool)
+    ids = torch.arange(batch)
+    seen = torch.zeros(batch, cfg.vocab, dtype=torch.bool)
+
+    def step(i):
+        logits = m.decode_step(tokens, positions + i, valid)
+        return m.ops.sample(logits, ids, torch.full((batch,), i + 1), seen, seed=20260923, temperature=0.6,
+                            top_k=20, top_p=0.95, penalty=1.5)
+
+    _log("cpu baseline: model built on the host")
+    step(0)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step(n + 1)
+        n += 1
+        el = time.perf_counter() - t0
+        _log(f"cpu baseline: step {n} done, {el:.1f} s")
+        if el >= budget_s or n >= max_steps:
+            break
+    return {"value": batch * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps x {batch} live slots of the same 36-layer model in float32 on "
+                      f"{threads} host threads (oracle recurrence, anchor memory, sampler), {el:.1f} s; "
+                      "refill prefill excluded as in the GPU figure"}
+
+
+# ---------------------------------------------------------------------------
+# gdn_decode
+
+def bench_gdn_decode(steps, warmup, cpu, batch=64):
     from yanchor_amd import gdn, workloads
 
     dev = torch.device("cuda:0")
-    b, h, hv, kd, vd, layers = 64, 32, 32, 128, 128, 4
+    h, hv, kd, vd, layers = 32, 32, 128, 128, 4
+    xs = [workloads.gdn_inputs(batch, 1, h, hv, kd, vd, dtype=torch.bfloat16,
+                               seed=workloads.SEED0 + 1 + 1000 * layer, state_std=0.02).to(dev)
+          for layer in range(layers)]
 
-    def make(pool):
-        xs = []
-        for layer in range(layers):
-            x = workloads.gdn_inputs(b, 1, h, hv, kd, vd, dtype=torch.bfloat16,
-                                     seed=workloads.SEED0 + 1 + 1000 * layer, state_std=0.02,
-                                     pool_rows=pool).to(dev)
-            if pool is None:
-                x.state_indices = None
-            xs.append(x)
-        return xs
+    def step(i):
+        x = xs[i % layers]
+        gdn.recurrent_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta, initial_state=x.state)
 
-    def stepper(xs):
-        def step(i):
-            x = xs[i % layers]
-            gdn.recurrent_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta,
-                                           initial_state=x.state, state_indices=x.state_indices)
-        return step
-
-    xs = make(None)
-    torch.cuda.synchronize()
-    ms_per_step, kernel_ms = _time_steps(stepper(xs), steps, warmup)
-    del xs
-    pooled = make(96)
-    _, pooled_ms = _time_steps(stepper(pooled), steps, warmup)
-    del pooled
-    torch.cuda.empty_cache()
-    nbytes = gdn_state_bytes(b, h, hv, kd, vd, 2, 4, False)
+    ms_per_step, kernel_ms = _time_launches(step, steps, warmup)
+    nbytes = gdn_state_bytes(batch, h, hv, kd, vd, 2, 4, False)
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
-    pooled_gbs = gdn_state_bytes(b, h, hv, kd, vd, 2, 4, True) / (pooled_ms * 1e-3) / 1e9
     res = {
-        "metric": METRIC,
-        "value": b / (ms_per_step * 1e-3),
+        "value": batch / (ms_per_step * 1e-3),
         "unit": "tokens/s",
         "ms_per_step": ms_per_step,
         "dtype": "f32",
-        "config": {"workload": "gdn_decode_state_update: one layer decode step, state fp32 "
-                               "[64, 32, 128, 128] in place, bf16 q/k/v, fp32 g/beta, "
-                               "4 rotating layer states",
-                   "global_batch": b, "seq_len": 1, "parallelism": "single GPU"},
+        "config": {"workload": f"gdn_decode_state_update: one layer decode step, state fp32 "
+                               f"[{batch}, 32, 128, 128] in place, bf16 q/k/v, fp32 g/beta, 4 rotating layer states",
+                   "global_batch": batch, "seq_len": 1, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_GDN_DECODE,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_GDN_DECODE.get(batch),
                      "kernel": "gdn_recurrent_kernel", "bytes_per_launch": nbytes,
                      "avg_launch_us": kernel_ms * 1e3},
-        "pooled_slots": {"pool_rows": 96, "avg_launch_us": pooled_ms * 1e3,
-                         "achieved_GBs": pooled_gbs, "frac": pooled_gbs / HBM_PEAK_GBS},
     }
+    del xs
     if cpu:
-        res["cpu_baseline"] = cpu_gdn_decode(b, h, hv, kd, vd)
+        res["cpu_baseline"] = cpu_gdn_decode(batch, h, hv, kd, vd)
     return res
 
 
 def cpu_gdn_decode(b, h, hv, kd, vd, budget_s=12.0) -> dict:
     """The oracle's token recurrence in torch float32 on the host cores, on the
     same decode shape, repeated until ~budget_s of CPU work."""
-    import torch
     from oracle import gdn as ref
     from yanchor_amd import workloads
 
     threads = cpu_threads()
     torch.set_num_threads(threads)
-    x = workloads.gdn_inputs(b, 1, h, hv, kd, vd, dtype=torch.bfloat16, seed=workloads.SEED0 + 1,
-                             state_std=0.02)
+    x = workloads.gdn_inputs(b, 1, h, hv, kd, vd, dtype=torch.bfloat16, seed=workloads.SEED0 + 1, state_std=0.02)
     state = x.state
-    for _ in range(2):
-        ref.recurrent_gated_delta_rule(x.q, x.k, x.v, x.g, x.beta, state, dtype=torch.float32)
+    ref.recurrent_gated_delta_rule(x.q, x.k, x.v, x.g, x.beta, state, dtype=torch.float32)
     n, t0 = 0, time.perf_counter()
     while True:
-        _, state = ref.recurrent_gated_delta_rule(x.q, x.k, x.v, x.g, x.beta, state,
-                                                  dtype=torch.float32)
+        _, state = ref.recurrent_gated_delta_rule(x.q, x.k, x.v, x.g, x.beta, state, dtype=torch.float32)
         n += 1
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 2000:
             break
     return {"value": b * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps of the same layer shape (B={b}, HV={hv}, "
-                      f"dk=dv={kd}) with the float32 torch oracle, {el:.1f} s"}
+            "sample": f"{n} decode steps of the same layer shape (B={b}, HV={hv}, dk=dv={kd}) with the "
+                      f"float32 torch oracle, {el:.1f} s"}
+
+
+def bench_hbm_copy(steps, warmup, cpu, batch=None):
+    """A plain 128 MiB device-to-device copy (torch's copy kernel): the
+    calibration kernel for the HBM byte counters, and the bandwidth a simple
+    streaming kernel reaches on this GPU."""
+    del cpu, batch
+    n = 32 << 20
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    ms_per_step, kernel_ms = _time_launches(lambda i: dst.copy_(src), steps, warmup)
+    nbytes = 2 * n * 4
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    return {"value": achieved, "unit": "GB/s", "ms_per_step": ms_per_step, "dtype": "f32",
+            "config": {"workload": "hbm_copy: 128 MiB float32 device copy (read 128 MiB + write 128 MiB)",
+                       "global_batch": 1, "seq_len": 1, "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "copy",
+                         "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3}}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="gdn_decode", choices=["gdn_decode"])
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (model_decode 2048, gdn_decode 200)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (model_decode 64, gdn_decode 20)")
+    ap.add_argument("--workload", default="model_decode", choices=["model_decode", "gdn_decode", "hbm_copy"])
+    ap.add_argument("--batch", type=int, default=None, help="slots (model_decode 128) / rows (gdn_decode 64)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the hot path shards by sequence with no exchange; see the design notes)",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: every run here has one "
+              "GPU (the decode path shards by sequence slot with no exchange between GPUs)", file=sys.stderr)
         return 2
-    res = bench_gdn_decode(args.steps, args.warmup, not args.no_cpu)
-    line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
+    if args.workload == "model_decode":
+        steps, warmup = args.steps or 2048, 64 if args.warmup is None else args.warmup
+        res = bench_model_decode(steps, warmup, not args.no_cpu, batch=args.batch or 128)
+    else:
+        steps, warmup = args.steps or 200, 20 if args.warmup is None else args.warmup
+        fn = bench_gdn_decode if args.workload == "gdn_decode" else bench_hbm_copy
+        res = fn(steps, warmup, not args.no_cpu, batch=args.batch or 64)
+    line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1,
+            "steps": steps, "warmup": warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": res["dtype"], "data": "synthetic (seeded torch.Generator)",
+            "dtype": res["dtype"], "data": "synthetic (seeded random-init weights and requests)",
             "config": res["config"], "roofline": res["roofline"]}
-    if "cpu_baseline" in res:
-        line["cpu_baseline"] = res["cpu_baseline"]
-    if "pooled_slots" in res:
-        line["pooled_slots"] = res["pooled_slots"]
+    for key in ("cpu_baseline", "decode"):
+        if key in res:
+            line[key] = res[key]
     print(json.dumps(line), flush=True)
     return 0
 

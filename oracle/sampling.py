@@ -11,8 +11,9 @@ Restates runtime/model/inference_kernels.py:
                                           caller 1147-1167 does torch.topk and /T)
 * ``presence_penalty``            1095-1114
 
-Pins (tests/test_oracle_sampling.py): golden vectors in
-tests/golden/counter_sampling.json; integer hash values checked with numpy
+Pins (tests/test_oracle_sampling_slots.py): golden vectors written from the
+reference's own functions in tests/golden/counter_sampling.npz; integer hash
+values checked with numpy
 uint32 wrap-around arithmetic (an independent evaluation order); special cases
 top_k = 1 -> argmax, top_p = 1 -> plain inverse CDF; the output of the hash is
 a permutation-free uniform (mean/variance over 1e5 counters).

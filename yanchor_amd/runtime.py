@@ -218,13 +218,28 @@ class Model:
     """Random-init 4B-shaped hybrid recurrent model with its decode caches."""
 
     def __init__(self, cfg: ModelConfig, batch: int, device, *, seed=0, ops=None, dtype=torch.bfloat16,
-                 max_prompt=128):
+                 init="normal"):
+        """``init="normal"`` draws every weight from N(0, init_std);
+        ``init="tiled"`` repeats one 16M-value N(0, init_std) block (fast on a
+        host, for timing runs where the values do not matter)."""
         self.cfg, self.B, self.device, self.dtype = cfg, int(batch), torch.device(device), dtype
         self.ops = ops if ops is not None else HipOps()
         gen = torch.Generator(device=self.device).manual_seed(seed)
         std = cfg.init_std
+        block = None
+        if init == "tiled":
+            block = (torch.randn(1 << 24, device=self.device, generator=gen) * std).to(dtype)
+        elif init != "normal":
+            raise ValueError(f"unknown init {init!r}")
 
         def w(*shape):
+            if block is not None:
+                n, bn = math.prod(shape), block.numel()
+                out = torch.empty(n, device=self.device, dtype=dtype)
+                full = n // bn * bn
+                out[:full].view(-1, bn).copy_(block.expand(n // bn, bn))
+                out[full:].copy_(block[: n - full])
+                return out.view(*shape)
             return (torch.randn(*shape, device=self.device, generator=gen, dtype=torch.float32) * std).to(dtype)
 
         def zeros(*shape):
