@@ -17,6 +17,9 @@ Prints one JSON line.  Workloads:
   reference's decode tokens/s definition.
 * ``gdn_decode``: the state-update kernel alone on a [B, 32, 128, 128] fp32
   state (``--batch``, default 64) with bf16 q/k/v, cycling over 4 layer states.
+* ``gdn_prefill``: varlen chunked prefill of one GDN layer on the MFMA chunk
+  kernel (32 packed sequences, lengths U[512, 8192]); reports MFMA utilisation
+  beside the HBM fraction.
 * ``hbm_copy``: a 128 MiB device copy, the calibration kernel for the HBM byte
   counters behind ``roofline.traffic``.
 
@@ -297,6 +300,84 @@ def cpu_gdn_decode(b, h, hv, kd, vd, budget_s=12.0) -> dict:
                       f"float32 torch oracle, {el:.1f} s"}
 
 
+CHUNK = 64
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def chunk_flops(n_chunks, heads, d=128, c=CHUNK):
+    """Algorithmic FLOP of the chunked form: per (chunk, head)
+    10 C^2 d + 6 C d^2 + 2/3 C^3 (the intra-chunk products, the WY/UT
+    transform and the state scan)."""
+    return n_chunks * heads * (10 * c * c * d + 6 * c * d * d + (2 * c ** 3) / 3)
+
+
+def bench_gdn_prefill(steps, warmup, cpu, batch=None):
+    """Varlen chunked prefill of one GDN layer: 32 packed sequences with
+    lengths uniform in [512, 8192] (seeded), H = HV = 32, dk = dv = 128, bf16
+    q/k/v/o, fp32 gates and final states, zero initial state."""
+    from yanchor_amd import gdn, workloads
+
+    del batch
+    lengths = workloads.prefill_lengths()
+    h = hv = 32
+    d = 128
+    x = workloads.packed_inputs(lengths, h, hv, d, d).to("cuda:0")
+
+    def step(i):
+        gdn.chunk_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta, output_final_state=True,
+                                   use_qk_l2norm_in_kernel=True, cu_seqlens=x.cu_seqlens, lengths=lengths)
+
+    ms_per_step, kernel_ms = _time_launches(step, steps, warmup)
+    tokens = sum(lengths)
+    n_chunks = sum(-(-n // CHUNK) for n in lengths)
+    flops = chunk_flops(n_chunks, hv, d)
+    nbytes = tokens * (h * d * 2 * 2 + hv * d * 2 * 2 + hv * 8) + len(lengths) * hv * d * d * 4
+    gbs = nbytes / (kernel_ms * 1e-3) / 1e9
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    res = {"metric": "varlen chunked prefill tokens/s, one GDN layer (MFMA utilisation and HBM fraction)",
+           "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s", "ms_per_step": ms_per_step, "dtype": "bf16",
+           "config": {"workload": f"gdn_prefill: {len(lengths)} packed sequences, lengths U[512, 8192] "
+                                  f"({tokens} tokens), H=HV=32, dk=dv=128, chunk 64, bf16 q/k/v/o, fp32 gates/state",
+                      "global_batch": len(lengths), "seq_len": tokens, "parallelism": "single GPU"},
+           "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "gdn_chunk_kernel",
+                        "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3,
+                        "mfma_tflops": tflops, "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                        "mfma_util": tflops / MFMA_BF16_PEAK_TFLOPS, "flops_per_launch": flops,
+                        "roofline_frac": max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_BF16_PEAK_TFLOPS * 1e12))
+                        / (kernel_ms * 1e-3)}}
+    del x
+    if cpu:
+        res["cpu_baseline"] = cpu_gdn_prefill(lengths, h, hv, d)
+    return res
+
+
+def cpu_gdn_prefill(lengths, h, hv, d, budget_s=15.0):
+    """The oracle's chunked form in float32 on the host cores, sequence by
+    sequence over the same packed set until ~budget_s."""
+    from oracle import gdn as ref
+    from yanchor_amd import workloads
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    x = workloads.packed_inputs(lengths, h, hv, d, d)
+    cu = x.cu_seqlens.tolist()
+    n_tok, n_seq, t0 = 0, 0, time.perf_counter()
+    for i in range(len(lengths)):
+        sl = slice(cu[i], cu[i + 1])
+        ref.chunk_gated_delta_rule(x.q[:, sl], x.k[:, sl], x.v[:, sl], x.g[:, sl], x.beta[:, sl],
+                                   dtype=torch.float32)
+        n_tok += lengths[i]
+        n_seq += 1
+        el = time.perf_counter() - t0
+        _log(f"cpu baseline: sequence {n_seq} ({lengths[i]} tokens) done, {el:.1f} s")
+        if el >= budget_s:
+            break
+    return {"value": n_tok / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"the first {n_seq} of the same packed sequences ({n_tok} tokens, all 32 heads) through "
+                      f"the float32 torch oracle's chunked form, {el:.1f} s"}
+
+
 def bench_hbm_copy(steps, warmup, cpu, batch=None):
     """A plain 128 MiB device-to-device copy (torch's copy kernel): the
     calibration kernel for the HBM byte counters, and the bandwidth a simple
@@ -321,7 +402,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (model_decode 2048, gdn_decode 200)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (model_decode 64, gdn_decode 20)")
-    ap.add_argument("--workload", default="model_decode", choices=["model_decode", "gdn_decode", "hbm_copy"])
+    ap.add_argument("--workload", default="model_decode",
+                    choices=["model_decode", "gdn_decode", "gdn_prefill", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=None, help="slots (model_decode 128) / rows (gdn_decode 64)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -334,9 +416,9 @@ def main() -> int:
         res = bench_model_decode(steps, warmup, not args.no_cpu, batch=args.batch or 128)
     else:
         steps, warmup = args.steps or 200, 20 if args.warmup is None else args.warmup
-        fn = bench_gdn_decode if args.workload == "gdn_decode" else bench_hbm_copy
-        res = fn(steps, warmup, not args.no_cpu, batch=args.batch or 64)
-    line = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1,
+        fn = {"gdn_decode": bench_gdn_decode, "gdn_prefill": bench_gdn_prefill, "hbm_copy": bench_hbm_copy}
+        res = fn[args.workload](steps, warmup, not args.no_cpu, batch=args.batch or 64)
+    line = {"metric": res.get("metric", METRIC), "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": steps, "warmup": warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": res["dtype"], "data": "synthetic (seeded random-init weights and requests)",

@@ -108,9 +108,3 @@ def test_state_not_inplace_when_requested(gpu):
                                           inplace=False)
     torch.cuda.synchronize()
     assert torch.equal(x.state, before) and s is not x.state
-
-
-def test_rejects_cpu_tensors():
-    x = workloads.gdn_inputs(1, 1, 1, 1, 64, 64)
-    with pytest.raises(ValueError, match="ROCm device"):
-        gdn.recurrent_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta, initial_state=x.state)

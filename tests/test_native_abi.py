@@ -62,3 +62,14 @@ def test_invalid_arguments_return_error_without_device_work(lib):
     rc = lib.yh_gdn_recurrent(fake, fake, fake, fake, fake, fake, None, fake, 1, 1, 3, 4, 128, 128, 1,
                               1.0, 1, 1, 0, 0, None)
     assert rc == -1 and b"multiple" in lib.yh_last_error()
+
+
+def test_wrappers_reject_host_tensors():
+    """The product path never falls back to a host computation."""
+    import torch
+    from yanchor_amd import gdn, layers, workloads
+    x = workloads.gdn_inputs(1, 1, 1, 1, 64, 64)
+    with pytest.raises(ValueError, match="ROCm device"):
+        gdn.recurrent_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta, initial_state=x.state)
+    with pytest.raises(ValueError, match="ROCm device"):
+        layers.silu_mul(torch.zeros(2, 16, dtype=torch.bfloat16))

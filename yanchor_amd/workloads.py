@@ -86,7 +86,7 @@ def anchor_state(B, G, capacity, chunk, D, *, p_live=0.7, seed=SEED0 + 1, dtype=
     live with probability p_live (position >= 0, score ~ N(0, 1)), dead slots
     carry position -1 and score -inf.  ``fill_pending`` pending entries are
     already pushed (count = fill_pending) and total = total0 (default
-    capacity + fill_pending)."""
+    4 * capacity + fill_pending, past the largest committed position)."""
     from .independent_memory import IndependentMemoryState
     gen = _gen(seed)
     st = IndependentMemoryState.empty(B, G, capacity, chunk, D, "cpu", dtype)
