@@ -164,6 +164,26 @@ int yh_anchor_commit(const void* key, const void* value, const float* score, con
                      int64_t* total, int64_t B, int64_t G, int64_t capacity, int64_t pending_capacity,
                      int64_t chunk, int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream);
 
+/*
+ * Anchor memory, prefill read: each query of a C-token block attends over the
+ * source tokens the block references, with the zero-logit sink.
+ *
+ * Replaces indexed_gqa / _indexed_forward (runtime/model/independent_memory.py:
+ * 6-45) and indexed_gqa_torch / _gqa_tile (modeling_yanchor.py:22-42), called
+ * from IndependentGQAMemory._sequence (modeling_yanchor.py:249).
+ *
+ *   query       [B, NB, C, H, D] (dtype)
+ *   key, value  [KB, S, G, D]    (dtype); KB == B, or 1 (shared by all rows)
+ *   references  [B, NB, G, CAP]  int32 or int64 (ref_dtype): row of S, -1 = none
+ *   out         [B, NB, C, H, D]
+ * Query head h reads group h / (H / G): out = softmax([q.K^T / sqrt(D), 0]) V
+ * over the referenced rows (an index outside [0, S) counts as none).
+ * Requirements: D == 128; dtype bf16 or fp16 (YH_ERR_UNSUPPORTED otherwise).
+ */
+int yh_indexed_gqa(const void* query, const void* key, const void* value, const void* references, int ref_dtype,
+                   void* out, int64_t B, int64_t NB, int64_t C, int64_t H, int64_t G, int64_t D, int64_t KB,
+                   int64_t S, int64_t CAP, int dtype, yh_stream_t stream);
+
 /* Sampling semantics of yh_topk_sample. */
 enum yh_sample_mode {
   /* _qwen35_top20_counter_sample_kernel (runtime/model/inference_kernels.py:

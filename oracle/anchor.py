@@ -6,6 +6,8 @@ Restates, from the reference:
 * ``select_topk``        modeling_yanchor.py:51-60
 * ``merge_topk``         modeling_yanchor.py:62-63
 * ``exclusive_prefix_topk``  modeling_yanchor.py:65-78 (brute-force form)
+* ``indexed_gqa``        the prefill read over referenced rows,
+                         modeling_yanchor.py:22-42, independent_memory.py:6-45
 * ``committed_read``     the decode read, modeling_yanchor.py:283-290, with the
                          slot indirection and zero-logit sink of
                          runtime/model/independent_memory.py:47-88, 177-188
@@ -22,7 +24,9 @@ u64 sorts of _push_select (independent_memory.py:115-128).
 Pins (tests/test_oracle_anchor.py): the tensor ``select_topk`` agrees with a
 brute-force ``sorted()`` on random inputs with forced ties, -0.0 and invalid
 slots; the read equals a softmax over [logits, 0] computed independently and
-reduces to closed forms for zero / one valid slot; ``exclusive_prefix_topk``
+reduces to closed forms for zero / one valid slot; ``indexed_gqa`` equals an
+SDPA over the gathered rows plus a zero row, and equals ``committed_read`` when
+a single token references the committed slots; ``exclusive_prefix_topk``
 is checked against the O(n^2) definition "Top-K of every earlier block".
 """
 from __future__ import annotations
@@ -123,6 +127,37 @@ def _rows(batch, indices):
     if indices is None:
         return list(range(batch))
     return [int(i) for i in indices.tolist()]
+
+
+def indexed_gqa(query, key, value, references, dtype=torch.float64):
+    """Prefill read of referenced source rows (modeling_yanchor.py:22-42;
+    runtime/model/independent_memory.py:6-45).
+
+    query ``[B, NB, C, H, D]``; key, value ``[KB, S, G, D]`` (KB == B, or 1 =
+    one source for every row, as the Triton kernel's key_batch); references
+    ``[B, NB, G, CAP]`` (-1 = none).  For row b, block nb, group g: the queries
+    of heads g*R .. g*R+R-1 (R = H / G) at every block position attend over
+    key/value rows ``references[b, nb, g, :]`` with logits q.k / sqrt(D) and
+    one extra logit 0 whose value is 0 (the padded zero key / value row of
+    _gqa_tile, the max-0 / denominator-1 start of _indexed_forward)."""
+    b, nb, c, h, d = query.shape
+    kb, s, g, _ = key.shape
+    r = h // g
+    out = torch.zeros(b, nb, c, h, d, dtype=dtype)
+    for bi in range(b):
+        src = 0 if kb == 1 else bi
+        for blk in range(nb):
+            for gi in range(g):
+                refs = references[bi, blk, gi].long()
+                ok = (refs >= 0) & (refs < s)
+                idx = refs.clamp(0, max(s - 1, 0))
+                keys = key[src, idx, gi].to(dtype)                            # [CAP, D]
+                vals = value[src, idx, gi].to(dtype)
+                q = query[bi, blk, :, gi * r:(gi + 1) * r].to(dtype)          # [C, R, D]
+                logits = (q @ keys.T / math.sqrt(d)).masked_fill(~ok, -math.inf)
+                w = torch.nn.functional.pad(logits, (0, 1), value=0.0).softmax(-1)[..., :-1]
+                out[bi, blk, :, gi * r:(gi + 1) * r] = w @ vals
+    return out.to(query.dtype)
 
 
 def committed_read(query, state: MemoryState, indices=None, dtype=torch.float64):

@@ -4,7 +4,11 @@
   (observed ~2e-3); fp32 within 1e-3;
 * commit: bit-exact state (keys, values, scores, positions, pending, count,
   total) after every step of multi-chunk decode sequences, with forced score
-  ties, -0.0, inactive rows and slot indirection.
+  ties, -0.0, inactive rows and slot indirection;
+* prefill read (indexed_gqa): bf16 / fp16 output within 1e-2 of the float64
+  oracle, with dead and out-of-range references, ragged tiles (CAP and
+  C * H/G not multiples of 64), a shared key batch and int32 / int64
+  references.
 """
 import math
 from dataclasses import fields
@@ -117,3 +121,34 @@ def test_commit_decode_config_chunk64(gpu):
 def test_commit_fp32_rows(gpu):
     st = workloads.anchor_state(2, 2, 64, 4, 64, dtype=torch.float32, seed=27)
     assert _drive(gpu, st, 12, 4, seed=28) > 2
+
+
+def _prefill(b, nb, c, h, g, s, cap, kb, dtype, ref_dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, nb, c, h, 128, generator=gen).to(dtype)
+    k = torch.randn(kb, s, g, 128, generator=gen).to(dtype)
+    v = torch.randn(kb, s, g, 128, generator=gen).to(dtype)
+    refs = torch.randint(0, s, (b, nb, g, cap), generator=gen)
+    refs[torch.rand(b, nb, g, cap, generator=gen) < 0.3] = -1
+    refs[..., -1] = s + 3                     # out of range: counts as none
+    return q, k, v, refs.to(ref_dtype)
+
+
+@pytest.mark.parametrize("b,nb,c,h,g,s,cap,kb", [(2, 3, 64, 8, 2, 300, 256, 2), (1, 2, 10, 8, 2, 50, 100, 1),
+                                                 (3, 1, 64, 4, 4, 700, 64, 3), (2, 2, 33, 16, 2, 129, 130, 1)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ref_dtype", [torch.int64, torch.int32])
+def test_indexed_read_matches_oracle(gpu, b, nb, c, h, g, s, cap, kb, dtype, ref_dtype):
+    q, k, v, refs = _prefill(b, nb, c, h, g, s, cap, kb, dtype, ref_dtype, seed=b * 1000 + c + cap)
+    got = im.indexed_gqa(q.to(gpu), k.to(gpu), v.to(gpu), refs.to(gpu))
+    torch.cuda.synchronize()
+    want = ref.indexed_gqa(q, k, v, refs)
+    assert got.dtype == dtype and got.shape == q.shape
+    assert rel_err(got, want) <= 1e-2, rel_err(got, want)
+
+
+def test_indexed_read_no_references(gpu):
+    q, k, v, refs = _prefill(1, 2, 64, 4, 2, 20, 64, 1, torch.bfloat16, torch.int64, seed=3)
+    refs.fill_(-1)
+    got = im.indexed_gqa(q.to(gpu), k.to(gpu), v.to(gpu), refs.to(gpu))
+    assert torch.count_nonzero(got) == 0

@@ -146,3 +146,58 @@ def test_prefix_topk_recursion():
     for j in range(nb):
         nxt = anchor.merge_topk((ps[:, j], pp[:, j], pr[:, j]), (s[:, j], p[:, j], r[:, j]), cap)
         assert torch.equal(nxt[2], pr[:, j + 1]) and torch.equal(nxt[0], ps[:, j + 1])
+
+
+def _prefill_inputs(b, nb, c, h, g, d, s, cap, kb, seed):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, nb, c, h, d, generator=gen, dtype=torch.float64)
+    k = torch.randn(kb, s, g, d, generator=gen, dtype=torch.float64)
+    v = torch.randn(kb, s, g, d, generator=gen, dtype=torch.float64)
+    refs = torch.randint(0, s, (b, nb, g, cap), generator=gen)
+    refs[torch.rand(b, nb, g, cap, generator=gen) < 0.3] = -1
+    return q, k, v, refs
+
+
+@pytest.mark.parametrize("kb", [1, 2])
+def test_indexed_read_matches_sdpa_over_gathered_rows(kb):
+    """The _gqa_tile construction: gather the referenced rows, append a zero
+    key / value row that is always visible, mask dead references, SDPA."""
+    b, nb, c, h, g, d = 2, 3, 5, 4, 2, 8
+    q, k, v, refs = _prefill_inputs(b, nb, c, h, g, d, 11, 7, kb, seed=12)
+    got = anchor.indexed_gqa(q, k, v, refs)
+    r = h // g
+    for bi in range(b):
+        src = 0 if kb == 1 else bi
+        for blk in range(nb):
+            for gi in range(g):
+                ref = refs[bi, blk, gi]
+                kk = torch.nn.functional.pad(k[src, ref.clamp_min(0), gi], (0, 0, 0, 1))
+                vv = torch.nn.functional.pad(v[src, ref.clamp_min(0), gi], (0, 0, 0, 1))
+                mask = torch.nn.functional.pad(ref >= 0, (0, 1), value=True)
+                qq = q[bi, blk, :, gi * r:(gi + 1) * r].permute(1, 0, 2)       # [R, C, D]
+                want = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, attn_mask=mask[None, None, :])
+                assert torch.allclose(got[bi, blk, :, gi * r:(gi + 1) * r], want.permute(1, 0, 2), atol=1e-12)
+
+
+def test_indexed_read_of_committed_slots_is_the_decode_read():
+    """One query token referencing the committed slots (dead slots as -1)
+    reads exactly what the decode read returns."""
+    st = workloads.anchor_state(2, 2, 64, 8, 16, dtype=torch.float64, seed=13)
+    q = workloads.anchor_query(2, 4, 16, dtype=torch.float64, seed=14)
+    refs = torch.arange(64).expand(2, 2, 64).masked_fill(st.positions < 0, -1)
+    key = st.keys.permute(0, 2, 1, 3)                                         # [B, cap, G, D]
+    val = st.values.permute(0, 2, 1, 3)
+    got = anchor.indexed_gqa(q[:, None], key, val, refs[:, None])            # [B, 1, 1, H, D]
+    assert torch.allclose(got[:, 0], anchor.committed_read(q, st), atol=1e-12)
+
+
+def test_indexed_read_closed_forms():
+    q, k, v, refs = _prefill_inputs(1, 1, 2, 1, 1, 8, 9, 4, 1, seed=15)
+    refs.fill_(-1)
+    assert torch.count_nonzero(anchor.indexed_gqa(q, k, v, refs)) == 0
+    refs[0, 0, 0, 2] = 5
+    out = anchor.indexed_gqa(q, k, v, refs)
+    for t in range(2):
+        logit = (q[0, 0, t, 0] @ k[0, 5, 0]).item() / math.sqrt(8)
+        p = math.exp(logit) / (math.exp(logit) + 1.0)
+        assert torch.allclose(out[0, 0, t, 0], p * v[0, 5, 0], atol=1e-12)

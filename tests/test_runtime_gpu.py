@@ -83,3 +83,27 @@ def test_short_engine_run(gpu):
     assert met.decode_steps == 40
     assert 0 < met.decode_useful_token_events <= met.decode_scheduled_token_events
     assert met.decode_seconds > 0 and met.decode_tokens_per_second > 0
+
+
+def test_tail_compaction_keeps_every_sequence(gpu):
+    """Shrinking the physical batch mid-generation (live slots gathered in
+    ascending order, graph captured again) leaves every sequence's tokens and
+    length as in a run without compaction (float32, so the smaller GEMMs do
+    not change the sampled tokens)."""
+    cfg = small_cfg()
+    g = torch.Generator().manual_seed(9)
+    caps = [3, 5, 9, 20, 31, 40]
+    reqs = [rt.Request(i, torch.randint(0, cfg.vocab, (16,), generator=g), c, 0) for i, c in enumerate(caps)]
+    out = []
+    for compact in (False, True):
+        m = rt.Model(cfg, batch=8, device=gpu, seed=3, dtype=torch.float32)
+        eng = rt.Engine(m, poll_interval=4, max_rows=16, max_new_tokens=64, tail_compaction=compact)
+        met = rt.run_decode_benchmark(m, steps=56, warmup=0, poll_interval=4, requests=copy.deepcopy(reqs),
+                                      engine=eng)
+        assert met.extra["live_slots_end"] == 0
+        out.append((eng.storage[:6].cpu(), eng.generated[:6].cpu(), met.extra["tail_compactions"]))
+    (s0, n0, c0), (s1, n1, c1) = out
+    assert c0 == [] and len(c1) >= 1 and all(0 < x < 8 for x in c1), c1
+    assert torch.equal(n0, torch.tensor(caps)) and torch.equal(n1, n0)
+    for i, c in enumerate(caps):
+        assert torch.equal(s0[i, :c], s1[i, :c]), i

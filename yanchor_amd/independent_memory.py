@@ -2,6 +2,7 @@
 
 The reference imports this module through ``_cuda_module('independent_memory')``
 (modeling_yanchor.py:19-20, used at 249 and 278-282) and calls
+``indexed_gqa(query, key, value, references)`` (prefill),
 ``committed_gqa(query, state, indices)`` and
 ``commit_decode(key, value, scores, active, chunk, state, indices)``
 (runtime/model/independent_memory.py:177-201).  ``IndependentMemoryState``
@@ -96,6 +97,41 @@ def _indices(indices, batch):
     if indices.shape != (batch,):
         raise ValueError("state indices must have one entry per batch row")
     return indices.to(torch.int32).contiguous()
+
+
+def indexed_gqa(query, key, value, references):
+    """Prefill read of the anchor memory (runtime/model/independent_memory.py:
+    38-45; torch form modeling_yanchor.py:22-42).
+
+    query ``[B, NB, C, H, D]``; key, value ``[KB, S, G, D]`` (KB == B, or 1 for
+    a source shared by every row); references ``[B, NB, G, CAP]`` int32/int64
+    rows of S (-1 = none).  Each query of block ``nb`` and head ``h`` attends
+    over the referenced rows of group ``h // (H // G)`` with the zero-logit
+    sink; returns ``[B, NB, C, H, D]`` in the query dtype."""
+    if query.ndim != 5 or key.ndim != 4 or references.ndim != 4:
+        raise ValueError("indexed_gqa expects query [B, NB, C, H, D], key/value [KB, S, G, D], "
+                         "references [B, NB, G, CAP]")
+    b, nb, c, h, d = query.shape
+    kb, s, g, kd = key.shape
+    if value.shape != key.shape or kd != d:
+        raise ValueError("key/value must be [KB, S, G, D] with the query head dim")
+    if references.shape[:3] != (b, nb, g):
+        raise ValueError("references must be [B, NB, G, CAP]")
+    if kb not in (1, b):
+        raise ValueError("key batch must be 1 or B")
+    if h % g:
+        raise ValueError("query heads must be a multiple of the groups")
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise ValueError("query, key and value must share a dtype")
+    if references.dtype not in (torch.int32, torch.int64):
+        raise ValueError("references must be int32 or int64")
+    N.require_device(query, key, value, references)
+    q, k, v, refs = (x.contiguous() for x in (query, key, value, references))
+    out = torch.empty_like(q)
+    N.call("yh_indexed_gqa", q.data_ptr(), k.data_ptr(), v.data_ptr(), refs.data_ptr(),
+           N.DTYPE_CODE[refs.dtype], out.data_ptr(), b, nb, c, h, g, d, kb, s, refs.shape[-1], N.code(q),
+           N.stream_of(q))
+    return out
 
 
 def committed_gqa(query, state: IndependentMemoryState, indices=None):

@@ -538,10 +538,13 @@ class Engine:
     """
 
     def __init__(self, model: Model, *, seed=20260923, temperature=0.6, top_k=20, top_p=0.95,
-                 presence_penalty=1.5, poll_interval=32, max_rows=4096, max_new_tokens=8192, use_graph=True):
+                 presence_penalty=1.5, poll_interval=32, max_rows=4096, max_new_tokens=8192, use_graph=True,
+                 tail_compaction=False, tail_compaction_live_fraction=0.5):
         self.m, self.B, self.dev = model, model.B, model.device
         self.seed, self.temperature, self.top_k, self.top_p = seed, temperature, top_k, top_p
         self.penalty, self.poll_interval, self.use_graph = presence_penalty, poll_interval, use_graph
+        self.tail_compaction, self.tail_fraction = tail_compaction, tail_compaction_live_fraction
+        self.compactions: list = []
         self.max_rows, self.max_new = max_rows, max_new_tokens
         B, dev, V = self.B, self.dev, model.cfg.vocab
         self.decode_ids = torch.zeros(B, 1, dtype=torch.long, device=dev)
@@ -573,11 +576,15 @@ class Engine:
                                self.positions, self.decode_ids, self.useful,
                                maximum_new_tokens=self.max_new, pad_token_id=0, eos_token_ids=())
 
-    def capture(self):
-        """Warm up and capture the decode step.  Call while every slot is empty:
-        the warm-up steps then only touch rows that admission overwrites whole."""
+    def capture(self, live=False):
+        """Warm up and capture the decode step.  The two eager warm-up steps
+        are ordinary decode steps: call with every slot empty (they then only
+        touch rows that admission overwrites whole), or with ``live`` set when
+        live slots may take them as real steps (after compaction)."""
         if not self.use_graph or self.graph is not None:
             return
+        if not live and bool(((~self.finished) & (self.slot_rows >= 0)).any()):
+            raise RuntimeError("capture() with live slots would advance them; pass live=True to allow it")
         for _ in range(2):  # warm the allocator and the sampler workspace outside capture
             self._step()
         torch.cuda.synchronize()
@@ -629,8 +636,10 @@ class Engine:
         torch.cuda.synchronize()
         return time.perf_counter() - t0
 
-    def poll(self, queue):
-        """Host sync: refill finished slots (ascending) from the queue."""
+    def poll(self, queue, exhausted=False):
+        """Host sync: refill finished slots (ascending) from the queue; with
+        tail compaction on and no more arrivals (``exhausted``), shrink the
+        physical batch once few slots are live."""
         fin = self.finished.cpu().tolist()
         free = [s for s, f in enumerate(fin) if f]
         completed = sum(1 for s in free if self.slot_request[s] is not None)
@@ -643,7 +652,39 @@ class Engine:
         if empty.numel():
             self.slot_rows.index_fill_(0, empty, -1)
             self.finished.index_fill_(0, empty, True)
+        live = self.B - len(free) + take
+        if self.tail_compaction and self.B > 1 and exhausted and not queue and \
+                0 < live < self.B and live <= max(1, int(self.B * self.tail_fraction)):
+            self.compact()
         return t, completed, take
+
+    def compact(self):
+        """Tail compaction (runtime/model/inference_kernels.py:1724-1745): keep
+        the live slots in ascending order, gather their cache rows into a
+        smaller physical batch in one launch, and capture the decode step
+        again.  The capture's eager warm-up steps are real decode steps of the
+        live slots (bookkeeping counts them), as the reference's
+        consume_capture_steps."""
+        from . import inference_kernels as ik
+        keep = ik.compaction_keep(self.finished, self.slot_rows)
+        n = int(keep.numel())
+        if n == 0 or n == self.B:
+            return
+        torch.cuda.synchronize()
+        self.graph = None
+        old = self.m.cache_tensors()
+        self.m.B = n
+        self.m._alloc_caches()
+        ik.gather_rows(list(zip(old, self.m.cache_tensors())), keep, None, n)
+        del old
+        for name in ("decode_ids", "positions", "finished", "slot_rows", "slot_caps", "row_steps", "attempt_ids",
+                     "dense_seen"):
+            setattr(self, name, getattr(self, name).index_select(0, keep))
+        self.slot_request = [self.slot_request[i] for i in keep.tolist()]
+        self.B = n
+        self.sink_rows = self.max_rows + torch.arange(n, device=self.dev)
+        self.compactions.append(n)
+        self.capture(live=True)
 
 
 def synthetic_requests(steps, *, rate=4.0, prompt_len=128, mean_len=1024, max_len=8192, vocab=151936,
@@ -665,15 +706,18 @@ def synthetic_requests(steps, *, rate=4.0, prompt_len=128, mean_len=1024, max_le
 
 
 def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=128, mean_len=1024,
-                         poll_interval=32, seed=20260923, use_graph=True, max_new_tokens=8192):
+                         poll_interval=32, seed=20260923, use_graph=True, max_new_tokens=8192, requests=None,
+                         tail_compaction=False, engine=None):
     """Continuous batching for warmup + steps decode steps; returns metrics of
-    the timed steps (the reference's decode tokens/s definition)."""
-    eng = Engine(model, seed=seed, poll_interval=poll_interval, use_graph=use_graph,
-                 max_new_tokens=max_new_tokens)
+    the timed steps (the reference's decode tokens/s definition).  Arrivals are
+    ``synthetic_requests`` unless ``requests`` is given."""
+    eng = engine or Engine(model, seed=seed, poll_interval=poll_interval, use_graph=use_graph,
+                           max_new_tokens=max_new_tokens, tail_compaction=tail_compaction)
     eng.capture()
-    arrivals = synthetic_requests(warmup + steps, rate=rate, prompt_len=prompt_len, mean_len=mean_len,
-                                  max_len=max_new_tokens, vocab=model.cfg.vocab, seed=seed)
-    queue, pending, idx = [], list(arrivals), 0
+    if requests is None:
+        requests = synthetic_requests(warmup + steps, rate=rate, prompt_len=prompt_len, mean_len=mean_len,
+                                      max_len=max_new_tokens, vocab=model.cfg.vocab, seed=seed)
+    queue, pending, idx = [], sorted(requests, key=lambda r: r.arrival_step), 0
     m = EngineMetrics()
     total = warmup + steps
     t_start = None
@@ -688,7 +732,7 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
             t_start = time.perf_counter()
             m.refill_prefill_seconds = 0.0
         if step % poll_interval == 0:
-            t, done, taken = eng.poll(queue)
+            t, done, taken = eng.poll(queue, exhausted=idx >= len(pending))
             if t_start is not None:
                 m.refill_prefill_seconds += t
                 m.refilled += taken
@@ -696,10 +740,11 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
         eng.step()
         if t_start is not None:
             m.decode_steps += 1
+            m.decode_scheduled_token_events += eng.B
     torch.cuda.synchronize()
     m.generation_wall_seconds = time.perf_counter() - t_start
     m.decode_useful_token_events = int(eng.useful.item()) - useful0
-    m.decode_scheduled_token_events = m.decode_steps * model.B
     m.peak_allocated_gib = torch.cuda.max_memory_allocated() / 2**30
-    m.extra = {"queue_left": len(queue), "live_slots_end": int(((~eng.finished) & (eng.slot_rows >= 0)).sum())}
+    m.extra = {"queue_left": len(queue), "live_slots_end": int(((~eng.finished) & (eng.slot_rows >= 0)).sum()),
+               "tail_compactions": list(eng.compactions)}
     return m
