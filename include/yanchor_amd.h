@@ -113,14 +113,20 @@ int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, const void*
  *   indices    NULL or int32 [B]: row b reads state row indices[b]; < 0 reads
  *              nothing (output 0)
  *   out        [B, H, D]   (dtype)
+ *   keys_row_stride, values_row_stride, positions_row_stride
+ *              elements between consecutive state rows; 0 = dense
+ *              (G * capacity * D, G * capacity).  Larger strides address a
+ *              state inside slot pages, e.g. the vLLM wire format
+ *              (vllm_yanchor.py:21-24, 49-64).
  * Per head: out = softmax([q.K^T / sqrt(D) over live slots, 0]) . [V; 0] (a
  * sink logit of 0 with value 0), accumulated in fp32.
  * Requirements: D in {64, 128}; H / G in {1, 2, 4}; capacity a multiple of 64,
- * at most 1024; 16-byte aligned query/keys/values.
+ * at most 1024; 16-byte aligned query/keys/values rows.
  */
 int yh_anchor_read(const void* query, const void* keys, const void* values, const int32_t* positions,
                    const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t capacity,
-                   int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream);
+                   int64_t D, int64_t n_state_rows, int64_t keys_row_stride, int64_t values_row_stride,
+                   int64_t positions_row_stride, int dtype, yh_stream_t stream);
 
 /*
  * Decode attention of one query token over a physical ring of `window` cached
@@ -154,6 +160,11 @@ int yh_window_attend(const void* query, const void* keys, const void* values, co
  * score descending, then position ascending (empty slots last), then candidate
  * index (committed 0..capacity-1, then pending 0..chunk-1); pending j has
  * position total[b] - c + j.  Then count = (c + 1) mod chunk and total += 1.
+ * row_strides  NULL (dense state) or 9 int64: elements between consecutive
+ *   state rows of keys, values, scores, positions, pending_keys,
+ *   pending_values, pending_scores, count, total (the IndependentMemoryState
+ *   field order), for a state inside slot pages such as the vLLM wire format
+ *   (vllm_yanchor.py:21-24, 49-64).
  * Requirements: 1 <= chunk <= pending_capacity; capacity + chunk <= 2048;
  * D * element size a multiple of 16 and capacity * D * element size <= 128 KiB;
  * no state row may appear twice in one call.
@@ -162,7 +173,8 @@ int yh_anchor_commit(const void* key, const void* value, const float* score, con
                      const int32_t* indices, void* keys, void* values, float* scores, int32_t* positions,
                      void* pending_keys, void* pending_values, float* pending_scores, int64_t* count,
                      int64_t* total, int64_t B, int64_t G, int64_t capacity, int64_t pending_capacity,
-                     int64_t chunk, int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream);
+                     int64_t chunk, int64_t D, int64_t n_state_rows, const int64_t* row_strides, int dtype,
+                     yh_stream_t stream);
 
 /*
  * Anchor memory, prefill read: each query of a C-token block attends over the

@@ -1,6 +1,9 @@
 // Fixed-slot anchor memory: decode read and decode push / Top-K commit.
 //
-// State layout (IndependentMemoryState, reference modeling_yanchor.py:80-120):
+// State layout (IndependentMemoryState, reference modeling_yanchor.py:80-120),
+// each field [NB, ...] with its own row stride (elements between consecutive
+// state rows; the dense stride unless the state lives in a slot page such as
+// the vLLM wire format, vllm_yanchor.py:21-24, 49-64):
 //   keys, values      [NB, G, KC, D]   (bf16 / fp16 / fp32)
 //   scores            [NB, G, KC]      fp32, -inf = empty
 //   positions         [NB, G, KC]      int32, -1 = empty (the validity mask)
@@ -33,6 +36,7 @@ struct ReadArgs {
   void* out;              // [B, H, D]
   int B, G, KC;
   int64_t n_rows;
+  int64_t k_rs, v_rs, p_rs;  // row strides (elements) of keys, values, positions
   float scale;
 };
 
@@ -131,7 +135,9 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
     for (int e = tid; e < R * D; e += kReadThreads) store_any(a.out, qbase + e, DT, 0.f);
     return;
   }
-  const int64_t slot0 = (b * a.G + g) * static_cast<int64_t>(a.KC);  // first slot of (b, g)
+  const int64_t pos0 = b * a.p_rs + static_cast<int64_t>(g) * a.KC;  // first slot of (b, g)
+  const int64_t kbase = b * a.k_rs + static_cast<int64_t>(g) * a.KC * D;
+  const int64_t vbase = b * a.v_rs + static_cast<int64_t>(g) * a.KC * D;
 
   float qf[R][8];
 #pragma unroll
@@ -155,14 +161,14 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
   const int nblk = a.KC / 64;
   for (int blk = wid; blk < nblk; blk += kReadWaves) {
     const int base = blk * 64;
-    const uint64_t live = __ballot(a.pos[slot0 + base + lane] >= 0);
+    const uint64_t live = __ballot(a.pos[pos0 + base + lane] >= 0);
     Raw8<DT> kr[NI], vr[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int n = i * RPI + rr;
       if ((live >> n) & 1ull) {
-        ld_raw8<DT>(kr[i], a.keys, (slot0 + base + n) * D + s * 8);
-        ld_raw8<DT>(vr[i], a.values, (slot0 + base + n) * D + s * 8);
+        ld_raw8<DT>(kr[i], a.keys, kbase + static_cast<int64_t>(base + n) * D + s * 8);
+        ld_raw8<DT>(vr[i], a.values, vbase + static_cast<int64_t>(base + n) * D + s * 8);
       } else {
         zero_raw8<DT>(kr[i]);
         zero_raw8<DT>(vr[i]);
@@ -274,7 +280,10 @@ struct CommitArgs {
   const int64_t* total;     // [NB]
   int B, G, KC, PC, C, D, esize;
   int64_t n_rows;
+  int64_t rs[9];  // row strides (elements) in IndependentMemoryState field order
 };
+
+enum { kRsKeys, kRsValues, kRsScores, kRsPos, kRsPKeys, kRsPValues, kRsPScores, kRsCount, kRsTotal };
 
 constexpr int kCommitThreads = 512;
 constexpr int kMaxCand = 2048;
@@ -343,14 +352,14 @@ __global__ void __launch_bounds__(kCommitThreads) anchor_commit_kernel(CommitArg
   const int tid = threadIdx.x;
   const int64_t b = a.idx ? static_cast<int64_t>(a.idx[row]) : static_cast<int64_t>(row);
   if (b < 0 || b >= a.n_rows || a.active[row] == 0) return;
-  const int64_t cnt = a.count[b];
+  const int64_t cnt = a.count[b * a.rs[kRsCount]];
   if (cnt < 0 || cnt >= a.C) return;  // corrupt counter: leave the row untouched
   const int64_t rowbytes = static_cast<int64_t>(a.D) * a.esize;
-  char* pk = static_cast<char*>(a.pkeys) + ((b * a.G + g) * a.PC) * rowbytes;
-  char* pv = static_cast<char*>(a.pvalues) + ((b * a.G + g) * a.PC) * rowbytes;
+  char* pk = static_cast<char*>(a.pkeys) + b * a.rs[kRsPKeys] * a.esize + static_cast<int64_t>(g) * a.PC * rowbytes;
+  char* pv = static_cast<char*>(a.pvalues) + b * a.rs[kRsPValues] * a.esize + static_cast<int64_t>(g) * a.PC * rowbytes;
   const char* src_k = static_cast<const char*>(a.key) + (static_cast<int64_t>(row) * a.G + g) * rowbytes;
   const char* src_v = static_cast<const char*>(a.value) + (static_cast<int64_t>(row) * a.G + g) * rowbytes;
-  float* ps = a.pscores + (b * a.G + g) * a.PC;
+  float* ps = a.pscores + b * a.rs[kRsPScores] + static_cast<int64_t>(g) * a.PC;
   const float new_score = a.score[static_cast<int64_t>(row) * a.G + g];
   // push
   if (tid < 64) copy_row16(pk + cnt * rowbytes, src_k, static_cast<int>(rowbytes), tid, 64);
@@ -360,14 +369,15 @@ __global__ void __launch_bounds__(kCommitThreads) anchor_commit_kernel(CommitArg
   __syncthreads();             // the pushed row is visible to the whole workgroup
 
   const int KC = a.KC, C = a.C, N = KC + C;
-  const int64_t meta = (b * a.G + g) * static_cast<int64_t>(KC);
-  const int64_t base_pos = a.total[b] - cnt;
+  float* scores = a.scores + b * a.rs[kRsScores] + static_cast<int64_t>(g) * KC;
+  int32_t* pos = a.pos + b * a.rs[kRsPos] + static_cast<int64_t>(g) * KC;
+  const int64_t base_pos = a.total[b * a.rs[kRsTotal]] - cnt;
   for (int n = tid; n < N; n += kCommitThreads) {
     float sc;
     int32_t p;
     if (n < KC) {
-      sc = a.scores[meta + n];
-      p = a.pos[meta + n];
+      sc = scores[n];
+      p = pos[n];
       if (p < 0) p = -1;
     } else {
       sc = n - KC == cnt ? new_score : ps[n - KC];
@@ -394,28 +404,29 @@ __global__ void __launch_bounds__(kCommitThreads) anchor_commit_kernel(CommitArg
   // committed rows themselves), then write them back.
   const int chunks = static_cast<int>(rowbytes / 16);  // 16-byte pieces per row
   const int total_pieces = KC * chunks;
-  char* ck = static_cast<char*>(a.keys) + meta * rowbytes;
-  char* cv = static_cast<char*>(a.values) + meta * rowbytes;
+  char* ck = static_cast<char*>(a.keys) + b * a.rs[kRsKeys] * a.esize + static_cast<int64_t>(g) * KC * rowbytes;
+  char* cv = static_cast<char*>(a.values) + b * a.rs[kRsValues] * a.esize + static_cast<int64_t>(g) * KC * rowbytes;
   commit_gather_pass(ck, pk, chosen, cpos, KC, chunks, total_pieces, rowbytes);
   commit_gather_pass(cv, pv, chosen, cpos, KC, chunks, total_pieces, rowbytes);
   for (int n = tid; n < KC; n += kCommitThreads) {
     const int src = chosen[n];
-    a.scores[meta + n] = cscore[src];
-    a.pos[meta + n] = cpos[src];
+    scores[n] = cscore[src];
+    pos[n] = cpos[src];
   }
 }
 
 // count = (count + active) % C, total += active, once per state row.
 __global__ void anchor_advance_kernel(int64_t* count, int64_t* total, const uint8_t* active,
-                                      const int32_t* idx, int B, int C, int64_t n_rows) {
+                                      const int32_t* idx, int B, int C, int64_t n_rows, int64_t count_rs,
+                                      int64_t total_rs) {
   const int row = blockIdx.x * blockDim.x + threadIdx.x;
   if (row >= B) return;
   const int64_t b = idx ? static_cast<int64_t>(idx[row]) : static_cast<int64_t>(row);
   if (b < 0 || b >= n_rows) return;
   const int64_t act = active[row] ? 1 : 0;
-  const int64_t c = count[b] + act;
-  count[b] = c == C ? 0 : c;
-  total[b] += act;
+  const int64_t c = count[b * count_rs] + act;
+  count[b * count_rs] = c == C ? 0 : c;
+  total[b * total_rs] += act;
 }
 
 template <int DT, int D, bool SINK>
@@ -445,7 +456,8 @@ int launch_read_d(int D, int R, bool sink, const ReadArgs& a, hipStream_t st) {
 static int anchor_read_impl(bool sink, const void* query, const void* keys, const void* values,
                               const int32_t* positions, const int32_t* indices, void* out,
                               int64_t B, int64_t H, int64_t G, int64_t capacity, int64_t D,
-                              int64_t n_state_rows, int dtype, yh_stream_t stream) {
+                              int64_t n_state_rows, int64_t keys_rs, int64_t values_rs, int64_t positions_rs,
+                              int dtype, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(query && keys && values && positions && out, "anchor_read: null tensor pointer");
   YH_CHECK_ARG(B >= 0 && G > 0 && H > 0 && H % G == 0, "anchor_read: bad B/H/G (%lld/%lld/%lld)",
@@ -460,9 +472,18 @@ static int anchor_read_impl(bool sink, const void* query, const void* keys, cons
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(keys) |
                  reinterpret_cast<uintptr_t>(values)) & al) == 0,
                "anchor_read: query/keys/values must be 16-byte aligned");
+  const int64_t dense_kv = G * capacity * D, dense_pos = G * capacity;
+  if (keys_rs == 0) keys_rs = dense_kv;
+  if (values_rs == 0) values_rs = dense_kv;
+  if (positions_rs == 0) positions_rs = dense_pos;
+  YH_CHECK_ARG(keys_rs >= dense_kv && values_rs >= dense_kv && positions_rs >= dense_pos,
+               "anchor_read: a row stride is smaller than one state row");
+  const int64_t esz = dtype == YH_F32 ? 4 : 2;
+  YH_CHECK_ARG((keys_rs * esz) % 16 == 0 && (values_rs * esz) % 16 == 0,
+               "anchor_read: key/value row strides must keep 16-byte alignment");
   if (B == 0) return YH_OK;
   ReadArgs a{query, keys, values, positions, indices, out, (int)B, (int)G, (int)capacity, n_state_rows,
-             1.0f / sqrtf(static_cast<float>(D))};
+             keys_rs, values_rs, positions_rs, 1.0f / sqrtf(static_cast<float>(D))};
   const int R = static_cast<int>(H / G);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {
@@ -474,16 +495,17 @@ static int anchor_read_impl(bool sink, const void* query, const void* keys, cons
 
 extern "C" int yh_anchor_read(const void* query, const void* keys, const void* values, const int32_t* positions,
                               const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t capacity,
-                              int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream) {
+                              int64_t D, int64_t n_state_rows, int64_t keys_row_stride, int64_t values_row_stride,
+                              int64_t positions_row_stride, int dtype, yh_stream_t stream) {
   return anchor_read_impl(true, query, keys, values, positions, indices, out, B, H, G, capacity, D, n_state_rows,
-                          dtype, stream);
+                          keys_row_stride, values_row_stride, positions_row_stride, dtype, stream);
 }
 
 extern "C" int yh_window_attend(const void* query, const void* keys, const void* values, const int32_t* positions,
                                 const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t window,
                                 int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream) {
   return anchor_read_impl(false, query, keys, values, positions, indices, out, B, H, G, window, D, n_state_rows,
-                          dtype, stream);
+                          0, 0, 0, dtype, stream);
 }
 
 extern "C" int yh_anchor_commit(const void* key, const void* value, const float* score,
@@ -492,7 +514,7 @@ extern "C" int yh_anchor_commit(const void* key, const void* value, const float*
                                 void* pending_values, float* pending_scores, int64_t* count,
                                 int64_t* total, int64_t B, int64_t G, int64_t capacity,
                                 int64_t pending_capacity, int64_t chunk, int64_t D, int64_t n_state_rows,
-                                int dtype, yh_stream_t stream) {
+                                const int64_t* row_strides, int dtype, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(key && value && score && active && keys && values && scores && positions && pending_keys &&
                    pending_values && pending_scores && count && total,
@@ -512,16 +534,26 @@ extern "C" int yh_anchor_commit(const void* key, const void* value, const float*
                  reinterpret_cast<uintptr_t>(pending_keys) | reinterpret_cast<uintptr_t>(pending_values)) & 15) == 0,
                "anchor_commit: key/value rows must be 16-byte aligned");
   YH_CHECK_ARG(B * G < (1LL << 31), "anchor_commit: grid too large");
-  if (B == 0) return YH_OK;
+  const int64_t dense[9] = {G * capacity * D, G * capacity * D, G * capacity, G * capacity,
+                            G * pending_capacity * D, G * pending_capacity * D, G * pending_capacity, 1, 1};
   CommitArgs a{key, value, score, active, indices, keys, values, scores, positions, pending_keys, pending_values,
                pending_scores, count, total, (int)B, (int)G, (int)capacity, (int)pending_capacity, (int)chunk,
-               (int)D, esize, n_state_rows};
+               (int)D, esize, n_state_rows, {}};
+  for (int i = 0; i < 9; ++i) {
+    a.rs[i] = row_strides ? row_strides[i] : dense[i];
+    YH_CHECK_ARG(a.rs[i] >= dense[i], "anchor_commit: row stride %d (%lld) is smaller than one state row", i,
+                 (long long)a.rs[i]);
+  }
+  for (int i : {(int)kRsKeys, (int)kRsValues, (int)kRsPKeys, (int)kRsPValues})
+    YH_CHECK_ARG((a.rs[i] * esize) % 16 == 0, "anchor_commit: key/value row strides must keep 16-byte alignment");
+  if (B == 0) return YH_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(anchor_commit_kernel, dim3(static_cast<unsigned>(B * G)), dim3(kCommitThreads), 0, st, a);
   YH_CHECK_LAUNCH("anchor_commit");
   const int threads = 256;
   hipLaunchKernelGGL(anchor_advance_kernel, dim3(static_cast<unsigned>((B + threads - 1) / threads)), dim3(threads),
-                     0, st, count, total, active, indices, (int)B, (int)chunk, n_state_rows);
+                     0, st, count, total, active, indices, (int)B, (int)chunk, n_state_rows, a.rs[kRsCount],
+                     a.rs[kRsTotal]);
   YH_CHECK_LAUNCH("anchor_advance");
   return YH_OK;
 }

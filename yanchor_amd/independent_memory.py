@@ -11,6 +11,7 @@ a state built by either side works with the other.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass, fields
 
@@ -85,10 +86,23 @@ def _check_state(state: IndependentMemoryState):
         raise ValueError("pending scores must be float32 [B, G, C]")
     if state.count.dtype != torch.long or state.total.dtype != torch.long:
         raise ValueError("count/total must be int64")
-    for f in fields(state):
-        if not getattr(state, f.name).is_contiguous():
-            raise ValueError(f"memory state field {f.name} must be contiguous")
+    if state.count.shape != (b,) or state.total.shape != (b,):
+        raise ValueError("count/total must be [B]")
     return b, g, cap, pc, d
+
+
+def _row_strides(state: IndependentMemoryState):
+    """Elements between consecutive state rows of every field (field order).
+    Each row must be dense inside; rows may sit in larger slot pages (the vLLM
+    wire format keeps all fields of a slot in two page rows)."""
+    out = []
+    for f in fields(state):
+        t = getattr(state, f.name)
+        inner = t[0] if t.shape[0] else t
+        if t.shape[0] and not inner.is_contiguous():
+            raise ValueError(f"memory state field {f.name} must be dense within a row")
+        out.append(t.stride(0) if t.shape[0] > 1 else math.prod(t.shape[1:]))
+    return out
 
 
 def _indices(indices, batch):
@@ -155,9 +169,10 @@ def committed_gqa(query, state: IndependentMemoryState, indices=None):
         raise ValueError("memory state has fewer rows than the batch")
     q = query.contiguous()
     out = torch.empty_like(q)
+    rs = _row_strides(state)
     N.call("yh_anchor_read", q.data_ptr(), state.keys.data_ptr(), state.values.data_ptr(),
-           state.positions.data_ptr(), N.ptr(idx), out.data_ptr(), b, h, g, cap, d, nb, N.code(q),
-           N.stream_of(q))
+           state.positions.data_ptr(), N.ptr(idx), out.data_ptr(), b, h, g, cap, d, nb, rs[0], rs[1], rs[3],
+           N.code(q), N.stream_of(q))
     return out
 
 
@@ -187,11 +202,12 @@ def commit_decode(key, value, scores, active, chunk, state: IndependentMemorySta
     k, v = key.contiguous(), value.contiguous()
     sc = scores.to(torch.float32).contiguous()
     act = active.to(torch.bool).contiguous()
+    rs = (ctypes.c_int64 * 9)(*_row_strides(state))
     N.call("yh_anchor_commit", k.data_ptr(), v.data_ptr(), sc.data_ptr(), act.data_ptr(), N.ptr(idx),
            state.keys.data_ptr(), state.values.data_ptr(), state.scores.data_ptr(),
            state.positions.data_ptr(), state.pending_keys.data_ptr(), state.pending_values.data_ptr(),
            state.pending_scores.data_ptr(), state.count.data_ptr(), state.total.data_ptr(), b, g, cap, pc,
-           int(chunk), d, nb, N.code(k), N.stream_of(k))
+           int(chunk), d, nb, rs, N.code(k), N.stream_of(k))
 
 
 def ring_decode_attention(query, keys, values, positions, indices=None):
