@@ -196,6 +196,30 @@ int yh_indexed_gqa(const void* query, const void* key, const void* value, const 
                    void* out, int64_t B, int64_t NB, int64_t C, int64_t H, int64_t G, int64_t D, int64_t KB,
                    int64_t S, int64_t CAP, int dtype, yh_stream_t stream);
 
+/*
+ * Skinny bf16 projection of the decode step: out[M, N] = x[M, K] . W[N, K]^T,
+ * fp32 accumulation, bf16 output (torch.nn.functional.linear without bias, the
+ * q/k/v/z/b/a, output, MLP, memory-writer and lm_head projections of
+ * modeling_yanchor.py:147-176, 877-964 and the Qwen3.5 layers in the
+ * transformers wheel) for M <= 128 rows.
+ *
+ *   x    [M, K] bf16, rows x_stride elements apart (16-byte aligned rows)
+ *   w    [N, K] bf16, dense
+ *   out  [M, N] bf16, rows out_stride elements apart
+ *   split_k    K is split over this many workgroups per 64-column tile
+ *              (yh_linear_split gives the library's choice); with
+ *              split_k > 1 the partial sums go through `workspace`, which must
+ *              hold yh_linear_workspace_bytes(M, N, K, split_k) bytes (16-byte
+ *              aligned); a second kernel sums the partials in a fixed order,
+ *              so results are identical from call to call.  Calls sharing a
+ *              workspace must not overlap.
+ * Requirements: 0 <= M <= 128; N % 64 == 0; K % 64 == 0.
+ */
+int yh_linear(const void* x, int64_t x_stride, const void* w, void* out, int64_t out_stride, int64_t M, int64_t N,
+              int64_t K, int64_t split_k, void* workspace, int64_t workspace_bytes, yh_stream_t stream);
+int yh_linear_split(int64_t M, int64_t N, int64_t K);
+int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split_k);
+
 /* Sampling semantics of yh_topk_sample. */
 enum yh_sample_mode {
   /* _qwen35_top20_counter_sample_kernel (runtime/model/inference_kernels.py:

@@ -143,3 +143,36 @@ def test_head_norm_rope_ring_write(gpu):
     touched[torch.arange(b, device=gpu), :, pos % win] = True
     assert torch.equal(ring[~touched], ring_ref[~touched])
     ulp_check(ring[touched], ring_ref[touched])
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 2560, 4096), (128, 12352, 2560), (128, 2560, 9728), (1, 64, 64),
+                                   (37, 192, 320), (64, 19456, 2560), (100, 2048, 2560)])
+def test_linear_matches_fp32_reference(gpu, m, n, k):
+    """fp32-accumulated product rounded once to bf16, as F.linear; the order
+    of the fp32 sums differs, so outputs agree to 1 bf16 ulp."""
+    x = rnd(m, k, dev=gpu, seed=m + n)
+    w = rnd(n, k, dev=gpu, scale=0.02, seed=k)
+    ref = (x.float() @ w.float().t()).to(torch.bfloat16)
+    got = layers.linear(x, w)
+    ulp_check(got, ref, max_frac=0.05)
+
+
+@pytest.mark.parametrize("split", [1, 2, 5, 16])
+def test_linear_split_k_is_deterministic(gpu, split):
+    """Every split gives the same result on repeated calls (fixed-order
+    partial sums), including after a call with a different shape on the same
+    workspace."""
+    x = rnd(128, 4096, dev=gpu, seed=1)
+    w = rnd(2560, 4096, dev=gpu, scale=0.02, seed=2)
+    a = layers.linear(x, w, split_k=split)
+    layers.linear(rnd(64, 1024, dev=gpu, seed=3), rnd(640, 1024, dev=gpu, seed=4), split_k=4)
+    b = layers.linear(x, w, split_k=split)
+    assert torch.equal(a, b)
+    ulp_check(a, (x.float() @ w.float().t()).to(torch.bfloat16), max_frac=0.05)
+
+
+def test_linear_strided_rows(gpu):
+    base = rnd(16, 3072, dev=gpu, seed=5)
+    x = base[:, 512:]                                    # row stride 3072, 1024-byte offset
+    w = rnd(128, 2560, dev=gpu, seed=6)
+    ulp_check(layers.linear(x, w), (x.float() @ w.float().t()).to(torch.bfloat16))

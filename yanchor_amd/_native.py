@@ -35,6 +35,7 @@ SIGNATURES: dict[str, list] = {
     "yh_anchor_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                          _i64, _i64, _i64, _p, _i32, _p],
     "yh_indexed_gqa": [_p, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "yh_linear": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "yh_topk_sample": [_p, _i32, _i64, _p, _i64, _f32, _p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32,
                        _i64, _f32, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "yh_presence_penalty": [_p, _p, _i64, _f32, _p],
@@ -55,6 +56,8 @@ SIGNATURES: dict[str, list] = {
 # entry points that do not return a status
 PLAIN: dict[str, tuple] = {
     "yh_topk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "yh_linear_split": (_i32, [_i64, _i64, _i64]),
+    "yh_linear_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "yh_topk_segments": (None, [_i64, _i64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
 }
 

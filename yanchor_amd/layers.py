@@ -2,8 +2,9 @@
 
 RMSNorm with a fused residual add, the GDN decode prologue (causal conv1d
 update + SiLU + q/k/v split + beta/g gates), the gated RMSNorm of the GDN
-output, silu(gate) * up, and per-head RMSNorm + partial RoPE.  Each keeps the
-rounding points of the torch formulation it replaces (cited per function).
+output, silu(gate) * up, per-head RMSNorm + partial RoPE, and the skinny
+projection of the decode step.  Each keeps the rounding points of the torch
+formulation it replaces (cited per function).
 """
 from __future__ import annotations
 
@@ -116,4 +117,41 @@ def head_norm_rope(x, w, cos, sin, rotary_dim, eps, *, out=None, out_tok_index=N
     N.call("yh_head_norm_rope", x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), N.ptr(cs), N.ptr(sn),
            out.data_ptr(), out_tok_stride, out_head_stride, N.ptr(idx), n, h, d, rotary_dim, float(eps),
            N.stream_of(x))
+    return out
+
+
+_linear_ws: dict = {}
+
+
+def _linear_workspace(device, nbytes):
+    """Per-device zero-filled split-K workspace, grown on demand (the kernels
+    leave its arrival counters at zero after every call)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _linear_ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _linear_ws[key] = ws
+    return ws
+
+
+def linear(x, w, split_k=None):
+    """out = x . w^T for a decode batch (x [M, K] bf16 with M <= 128, w [N, K]
+    bf16): torch.nn.functional.linear without bias on the skinny-projection
+    kernel.  The split-K workspace is cached per device: concurrent calls on
+    different streams of one device must not overlap."""
+    _bf16(x, w)
+    if x.ndim != 2 or w.ndim != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError("linear expects x [M, K] and w [N, K]")
+    m, k = x.shape
+    n = w.shape[0]
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    w = w.contiguous()
+    dev = N.require_device(x, w)
+    out = torch.empty(m, n, dtype=x.dtype, device=dev)
+    s = int(split_k) if split_k is not None else N.lib().yh_linear_split(m, n, k)
+    nbytes = N.lib().yh_linear_workspace_bytes(m, n, k, s)
+    ws = _linear_workspace(dev, nbytes) if nbytes else None
+    N.call("yh_linear", x.data_ptr(), x.stride(0), w.data_ptr(), out.data_ptr(), n, m, n, k, s, N.ptr(ws),
+           0 if ws is None else ws.numel(), N.stream_of(x))
     return out

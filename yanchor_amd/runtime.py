@@ -104,6 +104,17 @@ class HipOps:
             return TorchGlue.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
         return self.layers.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
 
+    def linear(self, x, w):
+        """Decode projections: the skinny split-K kernel where it beats the
+        library GEMM on MI355X (bf16, <= 128 rows, output width <= 4096, K >=
+        2048: the GDN / attention output, MLP down and memory-writer
+        projections), torch (hipBLASLt) otherwise."""
+        n, k = w.shape
+        if (x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128 and n <= 4096 and n % 64 == 0
+                and k % 64 == 0 and k >= 2048):
+            return self.layers.linear(x, w)
+        return F.linear(x, w)
+
     def gdn_decode(self, q, k, v, g, beta, state):
         o, _ = self.gdn.recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=state,
                                                    output_final_state=True, use_qk_l2norm_in_kernel=True)
@@ -308,7 +319,7 @@ class Model:
 
     # ---------------- layers ----------------
     def _mlp(self, L, x):
-        return F.linear(self.ops.silu_mul(F.linear(x, L["mlp_gate_up"])), L["mlp_down"])
+        return self.ops.linear(self.ops.silu_mul(self.ops.linear(x, L["mlp_gate_up"])), L["mlp_down"])
 
     def _gdn_split(self, L, proj):
         c = self.cfg
@@ -324,14 +335,14 @@ class Model:
         """GDN mixer for one token per slot; xn is the normalised layer input."""
         c, B, ops = self.cfg, xn.shape[0], self.ops
         hv, dv, vd = c.gdn_heads_v, c.gdn_dv, c.gdn_heads_v * c.gdn_dv
-        proj = F.linear(xn, L["w_in"])                                     # [B, qkv | z | b | a]
+        proj = self.ops.linear(xn, L["w_in"])                                     # [B, qkv | z | b | a]
         q, k, v, g, beta = ops.gdn_prep(proj, self.conv_state[i], L["conv_w"], L["a_log"], L["dt_bias"],
                                         conv_dim=c.conv_dim, qk_dim=c.gdn_heads_k * c.gdn_dk, hv=hv,
                                         b_offset=c.conv_dim + vd, a_offset=c.conv_dim + vd + hv)
         o = ops.gdn_decode(q.view(B, 1, c.gdn_heads_k, c.gdn_dk), k.view(B, 1, c.gdn_heads_k, c.gdn_dk),
                            v.view(B, 1, hv, dv), g[:, None], beta[:, None], self.gdn_state[i])
         y = ops.gated_rmsnorm(o.view(B, hv, dv), proj[:, c.conv_dim: c.conv_dim + vd], L["gnorm"], c.rms_eps)
-        return F.linear(y, L["w_out"])
+        return self.ops.linear(y, L["w_out"])
 
     def _attn_project(self, L, x, cos, sin):
         c = self.cfg
@@ -369,14 +380,14 @@ class Model:
         c, B, ops = self.cfg, hidden.shape[0], self.ops
         H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
         u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
-        mq = F.linear(u, L["m_q"]).view(B, H, D)
+        mq = ops.linear(u, L["m_q"]).view(B, H, D)
         qn = ops.head_norm_rope(mq, L["m_q_norm"], None, None, 0, c.rms_eps)
         gate = torch.tanh(L["read_scale"]) * 2 * torch.sigmoid(
             (qn.float() * L["read_gate_w"]).sum(-1) / math.sqrt(D) + L["read_gate_b"])
         q = ops.head_norm_rope(mq, L["m_q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
-        scores = F.linear(F.silu(F.linear(u, L["adm_down"])).float(), L["adm_up"])
-        zz = u + F.linear(ops.silu_mul(F.linear(u, L["writer_gate_up"])), L["writer_down"])
-        kv = F.linear(zz, L["m_kv"])
+        scores = ops.linear(F.silu(ops.linear(u, L["adm_down"])).float(), L["adm_up"])
+        zz = u + ops.linear(ops.silu_mul(ops.linear(u, L["writer_gate_up"])), L["writer_down"])
+        kv = ops.linear(zz, L["m_kv"])
         key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
                                  c.rms_eps)
         return q, gate, key, kv[:, KVH * D:].reshape(B, KVH, D), scores
@@ -387,7 +398,7 @@ class Model:
         ring_rows[b] = b * kv_heads * window + positions[b] % window."""
         c, B, ops = self.cfg, xn.shape[0], self.ops
         H, KVH, D, W = c.attn_heads, c.kv_heads, c.head_dim, c.swa_window
-        proj = F.linear(xn, L["w_qkv"])                                    # [B, (q|gate) per head | k | v]
+        proj = ops.linear(xn, L["w_qkv"])                                    # [B, (q|gate) per head | k | v]
         hq = 2 * H * D
         qg = proj[:, :hq].view(B, H, 2 * D)
         q = ops.head_norm_rope(qg[..., :D], L["q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
@@ -399,12 +410,12 @@ class Model:
         self.ring_v[i][rows, :, slot] = proj[:, hq + KVH * D:].view(B, KVH, D)
         self.ring_pos[i][rows, :, slot] = positions.to(torch.int32)[:, None]
         att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i])
-        out = F.linear((att[:, 0] * torch.sigmoid(qg[..., D:])).reshape(B, -1), L["w_o"])
+        out = ops.linear((att[:, 0] * torch.sigmoid(qg[..., D:])).reshape(B, -1), L["w_o"])
         mq, mgate, mk, mv, mscores = self._memory_decode(L, hidden, cos, sin)
         read = ops.memory_read(mq[:, None], self.memory[i])
         ops.memory_commit(mk[:, None], mv[:, None], mscores[:, None], valid, c.memory_chunk, self.memory[i])
         read = read[:, 0] * valid[:, None, None].to(read.dtype)
-        mem_out = F.linear((read * mgate[..., None].to(read.dtype)).reshape(B, -1), L["m_o"])
+        mem_out = ops.linear((read * mgate[..., None].to(read.dtype)).reshape(B, -1), L["m_o"])
         return out + mem_out
 
     def decode_step(self, tokens, positions, valid):
@@ -424,7 +435,7 @@ class Model:
             xn, h = ops.rmsnorm(delta, L["post_norm"], c.rms_eps, residual=h)
             nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
             xn, h = ops.rmsnorm(self._mlp(L, xn), nxt, c.rms_eps, residual=h)
-        return F.linear(xn, self.lm_head).float()
+        return ops.linear(xn, self.lm_head).float()
 
     # ---------------- prefill ----------------
     def prefill(self, prompts):
