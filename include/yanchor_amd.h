@@ -87,18 +87,24 @@ int yh_gdn_recurrent_varlen(const void* q, const void* k, const void* v, const v
  * models/qwen3_5/modeling_qwen3_5.py:519-529) and follows
  * torch_chunk_gated_delta_rule (same file, 234-311).
  *
- *   q, k [total, H, 128] bf16; v, o [total, HV, V] bf16 (V a multiple of 64);
- *   g, beta [total, HV] (f32 / bf16 / f16); cu_seqlens int32 [n_seqs + 1]
+ *   q, k [total_tokens, H, 128] bf16; v, o [total_tokens, HV, V] bf16 (V 64 or
+ *   128); g, beta [total_tokens, HV] (f32 / bf16 / f16); cu_seqlens int32
+ *   [n_seqs + 1] (cu_seqlens[n_seqs] <= total_tokens)
  *   initial_state NULL (zeros) or fp32 [n_seqs, HV, 128, V] (read only)
  *   final_state fp32 [n_seqs, HV, 128, V] (written)
  *   order NULL or int32 [n_seqs]: dispatch order of the sequences (longest
  *   first balances the grid); every sequence must appear once.
+ *   workspace  device scratch of yh_gdn_chunk_workspace_bytes(total_tokens,
+ *   n_seqs, HV, V) bytes, 16-byte aligned: the per-chunk quantities the
+ *   state-independent pass hands to the sequential pass (about 25 KiB per
+ *   chunk of 64 tokens and value head).  Calls sharing it must not overlap.
  */
 int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, const void* g, const void* beta,
                         const float* initial_state, float* final_state, void* o, const int32_t* cu_seqlens,
-                        const int32_t* order, int64_t n_seqs, int64_t H, int64_t HV, int64_t K, int64_t V,
-                        float scale, int use_qk_l2norm, int qkv_dtype, int g_dtype, int beta_dtype,
-                        yh_stream_t stream);
+                        const int32_t* order, int64_t n_seqs, int64_t total_tokens, int64_t H, int64_t HV,
+                        int64_t K, int64_t V, float scale, int use_qk_l2norm, int qkv_dtype, int g_dtype,
+                        int beta_dtype, void* workspace, int64_t workspace_bytes, yh_stream_t stream);
+int64_t yh_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t n_seqs, int64_t HV, int64_t V);
 
 /*
  * Anchor memory, decode read of the committed slots.

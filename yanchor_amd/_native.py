@@ -28,8 +28,8 @@ SIGNATURES: dict[str, list] = {
                          _f32, _i32, _i32, _i32, _i32, _p],
     "yh_gdn_recurrent_varlen": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                 _i32, _i32, _i32, _i32, _p],
-    "yh_gdn_chunk_varlen": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
-                            _i32, _i32, _i32, _p],
+    "yh_gdn_chunk_varlen": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                            _i32, _i32, _i32, _i32, _p, _i64, _p],
     "yh_anchor_read": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_window_attend": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_anchor_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
@@ -57,6 +57,7 @@ SIGNATURES: dict[str, list] = {
 PLAIN: dict[str, tuple] = {
     "yh_topk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "yh_linear_split": (_i32, [_i64, _i64, _i64]),
+    "yh_gdn_chunk_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "yh_linear_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "yh_topk_segments": (None, [_i64, _i64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
 }

@@ -10,18 +10,29 @@
 //   S <- e^{G_last} S + K^T diag(e^{G_last - G}) v_new
 // with q, k L2-normalised (eps 1e-6 inside rsqrt) and q scaled.
 //
-// Layout of the work: one workgroup (8 waves) per (sequence, value head,
-// 64-wide value tile); the 128 x 64 fp32 state tile stays in MFMA
-// accumulators across the sequence's chunks (value tiles of one head evolve
-// independently).  Per-token L2 norms, beta and decays are diagonal factors,
-// so every product with the raw q / k / v tensors runs on exact bf16 MFMA
-// operands and the factors are applied in the epilogues.  Products whose
-// operands are fp32 on chip (the state, T, P = K S, v_new) split each fp32
-// operand into bf16 hi + lo and accumulate 2 or 3 MFMA passes (hi.hi, hi.lo,
-// lo.hi), which keeps the state path near fp32 accuracy; the output-only
-// product (Q K^T o Gamma) v_new and Q S use one pass.  T is inverted in fp32 on
-// the VALU by 16 x 16 blocks.  Sequences are independent; `order` lets the
-// caller dispatch the longest sequences first.
+// T and A = Q K^T o Gamma do not depend on the state S, so the work is split
+// in two kernels:
+//   chunk_prep_kernel   one workgroup per (chunk, value head), all chunks of
+//                       all sequences at once: norms, decays, K K^T and Q K^T
+//                       on MFMA, the fp32 inverse T.  Writes T diag(beta)
+//                       (bf16 hi + lo), A (bf16, with the q / k scalings) and
+//                       the per-token scalings to a workspace -- 25 KiB per
+//                       chunk and head.
+//   chunk_scan_kernel   one workgroup per (sequence, value head), walking the
+//                       sequence's chunks with the 128 x V fp32 state in MFMA
+//                       accumulators (wave w owns value columns 16w..16w+15):
+//                       Q S and W S, v_new, o, and the state update, with S
+//                       and v_new never leaving registers -- two barriers per
+//                       chunk, and the next chunk's inputs (which do not
+//                       depend on S) loaded into registers while the current
+//                       chunk computes.
+// Per-token L2 norms, beta and decays are diagonal factors, so products with
+// the raw q / k / v tensors take exact bf16 MFMA operands and the factors go
+// into the epilogues or the fp32 operand.  Products whose operands are fp32 on
+// chip (T, W, the state, v_new) split each fp32 operand into bf16 hi + lo and
+// accumulate 2 or 3 MFMA passes (hi.hi, hi.lo, lo.hi), which keeps the state
+// path near fp32 accuracy; the output-only products Q S and A v_new take one
+// pass.
 #include "common.h"
 
 namespace yh {
@@ -32,54 +43,10 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kC = 64;        // chunk length
 constexpr int kK = 128;       // key dim
-constexpr int kVT = 64;       // value tile
-constexpr int kThreads = 512;
 constexpr int SKR = 136;      // bf16 row stride of 128-wide matrices (padded: conflict-free 16 B reads)
 constexpr int SK64 = 72;      // bf16 row stride of 64-wide matrices
 constexpr int SF = 68;        // fp32 row stride of 64-wide matrices
-
-struct ChunkArgs {
-  const uint16_t* q;   // [total, H, K]
-  const uint16_t* k;   // [total, H, K]
-  const uint16_t* v;   // [total, HV, V]
-  const void* g;       // [total, HV]
-  const void* beta;    // [total, HV]
-  const float* h0;     // [N, HV, K, V] or null
-  float* ht;           // [N, HV, K, V]
-  uint16_t* o;         // [total, HV, V]
-  const int32_t* cu;   // [N + 1]
-  const int32_t* order;  // [N] or null
-  int n_seqs, H, HV, V;
-  float scale;
-  int l2, g_dt, beta_dt;
-};
-
-struct __align__(16) Smem {
-  uint16_t kr[kC * SKR];   // K [t][d]
-  uint16_t kt[kK * SK64];  // K^T [d][t]
-  union {
-    uint16_t q[kC * SKR];  // Q [t][d]
-    float pt[kVT * SF];    // P^T [v][t], P = K S
-  } qp;
-  uint16_t vt[kVT * SK64];  // V tile ^T [v][t]
-  union {
-    struct {
-      uint16_t hi[kVT * SKR];  // S^T [v][d], bf16 hi part
-      uint16_t lo[kVT * SKR];  // S^T, bf16 lo part
-    } st;
-    struct {
-      uint16_t vn[kVT * SK64];   // v_new^T [v][t]
-      uint16_t dhi[kVT * SK64];  // (diag(d2) v_new)^T hi
-      uint16_t dlo[kVT * SK64];  // (diag(d2) v_new)^T lo
-    } vn;
-  } sv;
-  float l[kC * SF];    // L
-  float t[kC * SF];    // T = (I + L)^{-1}
-  float aqk[kC * SF];  // (Q K^T o Gamma) with the q / k scalings
-  float x[3 * 256];    // block-inversion scratch
-  float rk[kC], rqs[kC], G[kC], beta[kC], d1[kC], d2[kC], orow[kC];
-  float gl;
-};
+constexpr int kScal = 196;    // per (chunk, head) scalars: orow[64], d2[64], ek[64], e^{G_last}, pad
 
 __device__ __forceinline__ bf16x8_t lds8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
@@ -89,22 +56,18 @@ __device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) {
 }
 __device__ __forceinline__ float bfv(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
-// 8 fp32 values (times optional per-element scales) -> bf16 hi / lo vectors.
+typedef float f32x8v __attribute__((ext_vector_type(8)));
+
+// 8 fp32 values -> bf16 hi (round to nearest even) and lo = bf16(x - hi), on
+// the packed hardware conversion (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ void split8(const float* x, bf16x8_t& hi, bf16x8_t& lo) {
-  uint16_t h[8], l[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    h[j] = f32_to_bf16(x[j]);
-    l[j] = f32_to_bf16(x[j] - bfv(h[j]));
-  }
-  hi = __builtin_bit_cast(bf16x8_t, make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])));
-  lo = __builtin_bit_cast(bf16x8_t, make_uint4(pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])));
+  const f32x8v v = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  hi = __builtin_convertvector(v, bf16x8_t);
+  lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x8v), bf16x8_t);
 }
-__device__ __forceinline__ bf16x8_t round8(const float* x) {
-  uint16_t h[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) h[j] = f32_to_bf16(x[j]);
-  return __builtin_bit_cast(bf16x8_t, make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])));
+__device__ __forceinline__ bf16x8_t round8v(const float* x) {
+  const f32x8v v = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  return __builtin_convertvector(v, bf16x8_t);
 }
 __device__ __forceinline__ void ld8f(const float* p, float* x) {
   const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
@@ -113,34 +76,116 @@ __device__ __forceinline__ void ld8f(const float* p, float* x) {
 __device__ __forceinline__ f32x4v mfma(bf16x8_t a, bf16x8_t b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+// Workgroup barrier that waits only for LDS traffic (__syncthreads() also
+// drains every outstanding global load, which would empty the prefetch).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// (I + L)^{-1} for strictly lower triangular L (64 x 64, fp32, LDS), by 16 x 16
-// blocks: the diagonal blocks by column-parallel forward substitution (one lane
-// per column, L rows read as 16-byte vectors), then the off-diagonal blocks
-// level by level, T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj, one thread per
-// 4 adjacent columns so T and X rows are read as vectors.
-__device__ void invert_unit_lower(Smem& sm) {
+// ---------------------------------------------------------------------------
+// Chunk table: chunk i of the packed batch starts at token table[4i], holds
+// table[4i+1] tokens and belongs to sequence table[4i+2]; sequence n owns
+// chunks [cstart[n], cstart[n+1]); cstart[n_seqs] is the chunk count.
+constexpr int kIdxThreads = 1024;
+__global__ void __launch_bounds__(kIdxThreads) chunk_index_kernel(const int32_t* cu, int n_seqs, int32_t* table,
+                                                                  int32_t* cstart, int nc_max) {
+  __shared__ int32_t wsum[kIdxThreads / 64];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  int32_t carry = 0;
+  for (int base = 0; base < n_seqs; base += kIdxThreads) {
+    const int i = base + threadIdx.x;
+    int32_t len = 0, cnt = 0;
+    if (i < n_seqs) {
+      len = max(cu[i + 1] - cu[i], 0);
+      cnt = (len + kC - 1) / kC;
+    }
+    int32_t incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    if (lane == 63) wsum[wid] = incl;
+    __syncthreads();
+    int32_t before = 0, all = 0;
+    for (int w = 0; w < kIdxThreads / 64; ++w) {
+      before += w < wid ? wsum[w] : 0;
+      all += wsum[w];
+    }
+    __syncthreads();
+    const int32_t first = carry + before + incl - cnt;
+    if (i < n_seqs) {
+      cstart[i] = first;
+      for (int j = 0; j < cnt && first + j < nc_max; ++j) {
+        int32_t* e = table + 4 * static_cast<int64_t>(first + j);
+        e[0] = cu[i] + j * kC;
+        e[1] = min(kC, len - j * kC);
+        e[2] = i;
+        e[3] = 0;
+      }
+    }
+    carry += all;
+  }
+  if (threadIdx.x == 0) cstart[n_seqs] = min(carry, nc_max);
+}
+
+// ---------------------------------------------------------------------------
+struct PrepArgs {
+  const uint16_t* q;     // [total, H, K]
+  const uint16_t* k;
+  const void* g;         // [total, HV]
+  const void* beta;
+  const int32_t* table;
+  const int32_t* cstart;
+  uint16_t* thi;         // [nc, HV, C, C]  T diag(beta), bf16 hi
+  uint16_t* tlo;         //                 bf16 lo
+  uint16_t* aqk;         // [nc, HV, C, C]  A
+  float* scal;           // [nc, HV, kScal]
+  int n_seqs, H, HV;
+  float scale;
+  int l2, g_dt, beta_dt;
+};
+
+constexpr int kPrepThreads = 256;
+
+struct __align__(16) PrepSmem {
+  union {
+    uint16_t kr[kC * SKR];  // K [t][d]          (K K^T, Q K^T)
+    float t[kC * SF];       // T = (I + L)^{-1}   (after the products)
+  } kt0;
+  union {
+    uint16_t q[kC * SKR];   // Q [t][d]          (Q K^T)
+    float x[3 * 256];       // inversion scratch (after the products)
+    uint16_t out[3 * kC * SK64];  // T beta hi / lo and A staged for coalesced stores (after the inversion)
+  } qx;
+  float l[kC * SF];         // L
+  float rk[kC], rqs[kC], G[kC], beta[kC];
+  float gl;
+};
+
+// T = (I + L)^{-1} for strictly lower triangular L (64 x 64 fp32 in LDS), by
+// 16 x 16 blocks: the diagonal blocks by column-parallel forward substitution
+// (one lane per column), then the off-diagonal blocks level by level,
+// T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj.
+__device__ void invert_unit_lower(const float* l, float* t, float* x) {
   const int tid = threadIdx.x;
   if (tid < 64) {
     const int b = tid >> 4, j = tid & 15;
-    float x[16];
+    float xs[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       float lr[16];
-      ld8f(&sm.l[(16 * b + i) * SF + 16 * b], lr);
-      ld8f(&sm.l[(16 * b + i) * SF + 16 * b + 8], lr + 8);
+      ld8f(&l[(16 * b + i) * SF + 16 * b], lr);
+      ld8f(&l[(16 * b + i) * SF + 16 * b + 8], lr + 8);
       float acc = i == j ? 1.f : 0.f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(-lr[m], x[m], acc);
-      x[i] = acc;
+      for (int m = 0; m < i; ++m) acc = fmaf(-lr[m], xs[m], acc);
+      xs[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sm.t[(16 * b + i) * SF + 16 * b + j] = x[i];
+    for (int i = 0; i < 16; ++i) t[(16 * b + i) * SF + 16 * b + j] = xs[i];
   } else {
-    // zero the strictly upper blocks
-    for (int e = tid - 64; e < 64 * 64; e += kThreads - 64) {
+    for (int e = tid - 64; e < 64 * 64; e += kPrepThreads - 64) {  // strictly upper blocks
       const int r = e >> 6, c = e & 63;
-      if ((c >> 4) > (r >> 4)) sm.t[r * SF + c] = 0.f;
+      if ((c >> 4) > (r >> 4)) t[r * SF + c] = 0.f;
     }
   }
   __syncthreads();
@@ -153,319 +198,548 @@ __device__ void invert_unit_lower(Smem& sm) {
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
       for (int m = j; m < i; ++m) {
         float lr[16];
-        ld8f(&sm.l[(16 * i + r) * SF + 16 * m], lr);
-        ld8f(&sm.l[(16 * i + r) * SF + 16 * m + 8], lr + 8);
+        ld8f(&l[(16 * i + r) * SF + 16 * m], lr);
+        ld8f(&l[(16 * i + r) * SF + 16 * m + 8], lr + 8);
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
-          const float4 tv = *reinterpret_cast<const float4*>(&sm.t[(16 * m + q) * SF + 16 * j + c4]);
+          const float4 tv = *reinterpret_cast<const float4*>(&t[(16 * m + q) * SF + 16 * j + c4]);
           acc.x = fmaf(lr[q], tv.x, acc.x);
           acc.y = fmaf(lr[q], tv.y, acc.y);
           acc.z = fmaf(lr[q], tv.z, acc.z);
           acc.w = fmaf(lr[q], tv.w, acc.w);
         }
       }
-      *reinterpret_cast<float4*>(&sm.x[bi * 256 + r * 16 + c4]) = acc;
+      *reinterpret_cast<float4*>(&x[bi * 256 + r * 16 + c4]) = acc;
     }
     __syncthreads();
     if (tid < nb * 64) {
       const int bi = tid >> 6, r = (tid >> 2) & 15, c4 = (tid & 3) * 4;
       const int i = lev + bi, j = i - lev;
       float tr[16];
-      ld8f(&sm.t[(16 * i + r) * SF + 16 * i], tr);
-      ld8f(&sm.t[(16 * i + r) * SF + 16 * i + 8], tr + 8);
+      ld8f(&t[(16 * i + r) * SF + 16 * i], tr);
+      ld8f(&t[(16 * i + r) * SF + 16 * i + 8], tr + 8);
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const float4 xv = *reinterpret_cast<const float4*>(&sm.x[bi * 256 + q * 16 + c4]);
+        const float4 xv = *reinterpret_cast<const float4*>(&x[bi * 256 + q * 16 + c4]);
         acc.x = fmaf(tr[q], xv.x, acc.x);
         acc.y = fmaf(tr[q], xv.y, acc.y);
         acc.z = fmaf(tr[q], xv.z, acc.z);
         acc.w = fmaf(tr[q], xv.w, acc.w);
       }
-      *reinterpret_cast<float4*>(&sm.t[(16 * i + r) * SF + 16 * j + c4]) =
-          make_float4(-acc.x, -acc.y, -acc.z, -acc.w);
+      *reinterpret_cast<float4*>(&t[(16 * i + r) * SF + 16 * j + c4]) = make_float4(-acc.x, -acc.y, -acc.z, -acc.w);
     }
     __syncthreads();
   }
 }
 
-__global__ void __launch_bounds__(kThreads) gdn_chunk_kernel(ChunkArgs a) {
-  __shared__ Smem sm;
-  const int nvt = a.V / kVT;
-  int blk = blockIdx.x;
-  const int vt = blk % nvt;
-  blk /= nvt;
-  const int hv = blk % a.HV;
-  const int sidx = blk / a.HV;
-  const int n = a.order ? a.order[sidx] : sidx;
+__global__ void __launch_bounds__(kPrepThreads) chunk_prep_kernel(PrepArgs a) {
+  __shared__ PrepSmem sm;
+  const int chunk = blockIdx.x, hv = blockIdx.y;
+  if (chunk >= a.cstart[a.n_seqs]) return;
+  const int64_t tok0 = a.table[4 * chunk];
+  const int Lc = a.table[4 * chunk + 1];
   const int hk = hv / (a.HV / a.H);
-  const int64_t tb = a.cu[n], te = a.cu[n + 1];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r16 = lane & 15, kq = (lane >> 4) * 8, rq4 = (lane >> 4) * 4;
-  const int vbase = vt * kVT;
+  const int64_t ch = static_cast<int64_t>(chunk) * a.HV + hv;  // (chunk, head) record
 
-  // state tile: wave w owns rows d in [16w, 16w + 16) and the four 16-wide value tiles
-  f32x4v S[4];
-  const int64_t sbase = (static_cast<int64_t>(n) * a.HV + hv) * kK;
+  // ---- stage K, Q rows (coalesced; rows t >= Lc are zero) and the gates ----
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      S[j][i] = a.h0 ? a.h0[(sbase + 16 * w + rq4 + i) * a.V + vbase + 16 * j + r16] : 0.f;
+  for (int it = 0; it < 4; ++it) {
+    const int ci = it * kPrepThreads + tid;
+    const int t = ci >> 4, d8 = (ci & 15) * 8;
+    uint4 kw = make_uint4(0, 0, 0, 0), qw = make_uint4(0, 0, 0, 0);
+    if (t < Lc) {
+      const int64_t off = ((tok0 + t) * a.H + hk) * kK + d8;
+      kw = *reinterpret_cast<const uint4*>(a.k + off);
+      qw = *reinterpret_cast<const uint4*>(a.q + off);
+    }
+    *reinterpret_cast<uint4*>(&sm.kt0.kr[t * SKR + d8]) = kw;
+    *reinterpret_cast<uint4*>(&sm.qx.q[t * SKR + d8]) = qw;
+  }
+  if (tid < kC) {
+    float gg = 0.f, bb = 0.f;
+    if (tid < Lc) {
+      gg = load_any(a.g, (tok0 + tid) * a.HV + hv, a.g_dt);
+      bb = load_any(a.beta, (tok0 + tid) * a.HV + hv, a.beta_dt);
+    }
+    sm.G[tid] = gg;
+    sm.beta[tid] = bb;
+  }
+  __syncthreads();
 
-  for (int64_t c0 = tb; c0 < te; c0 += kC) {
-    const int Lc = static_cast<int>(te - c0 < kC ? te - c0 : kC);
-    // ---- (a) stage K, Q, V tile and gates; state -> S^T hi / lo ----
-    for (int ci = tid; ci < kC * 16; ci += kThreads) {
-      const int t = ci >> 4, d8 = (ci & 15) * 8;
-      uint4 kw = make_uint4(0, 0, 0, 0), qw = make_uint4(0, 0, 0, 0);
-      if (t < Lc) {
-        const int64_t off = ((c0 + t) * a.H + hk) * kK + d8;
-        kw = *reinterpret_cast<const uint4*>(a.k + off);
-        qw = *reinterpret_cast<const uint4*>(a.q + off);
-      }
-      *reinterpret_cast<uint4*>(&sm.kr[t * SKR + d8]) = kw;
-      *reinterpret_cast<uint4*>(&sm.qp.q[t * SKR + d8]) = qw;
-      const uint32_t kk[4] = {kw.x, kw.y, kw.z, kw.w};
+  // ---- norms (4 lanes per token) and the decay scan ----
+  {
+    const int t = tid >> 2, p = tid & 3;
+    float sk = 0.f, sq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; e += 8) {
+      const uint4 kv = *reinterpret_cast<const uint4*>(&sm.kt0.kr[t * SKR + 32 * p + e]);
+      const uint4 qv = *reinterpret_cast<const uint4*>(&sm.qx.q[t * SKR + 32 * p + e]);
+      const uint32_t kk[4] = {kv.x, kv.y, kv.z, kv.w}, qq[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sm.kt[(d8 + 2 * j) * SK64 + t] = static_cast<uint16_t>(kk[j] & 0xffff);
-        sm.kt[(d8 + 2 * j + 1) * SK64 + t] = static_cast<uint16_t>(kk[j] >> 16);
+        const float k0 = __uint_as_float(kk[j] << 16), k1 = __uint_as_float(kk[j] & 0xffff0000u);
+        const float q0 = __uint_as_float(qq[j] << 16), q1 = __uint_as_float(qq[j] & 0xffff0000u);
+        sk = fmaf(k0, k0, fmaf(k1, k1, sk));
+        sq = fmaf(q0, q0, fmaf(q1, q1, sq));
       }
     }
-    {
-      const int t = tid >> 3, v8 = (tid & 7) * 8;
-      uint4 vw = make_uint4(0, 0, 0, 0);
-      if (t < Lc) vw = *reinterpret_cast<const uint4*>(a.v + ((c0 + t) * a.HV + hv) * a.V + vbase + v8);
-      const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sm.vt[(v8 + 2 * j) * SK64 + t] = static_cast<uint16_t>(vv[j] & 0xffff);
-        sm.vt[(v8 + 2 * j + 1) * SK64 + t] = static_cast<uint16_t>(vv[j] >> 16);
-      }
+    sk += __shfl_xor(sk, 1, kWave);
+    sq += __shfl_xor(sq, 1, kWave);
+    sk += __shfl_xor(sk, 2, kWave);
+    sq += __shfl_xor(sq, 2, kWave);
+    if (p == 0) {
+      sm.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
+      sm.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
     }
-    if (tid < kC) {
-      float gg = 0.f, bb = 0.f;
-      if (tid < Lc) {
-        gg = load_any(a.g, (c0 + tid) * a.HV + hv, a.g_dt);
-        bb = load_any(a.beta, (c0 + tid) * a.HV + hv, a.beta_dt);
-      }
-      sm.G[tid] = gg;
-      sm.beta[tid] = bb;
+  }
+  if (w == 0) {
+    float x = sm.G[lane];
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const float y = __shfl_up(x, off, kWave);
+      if (lane >= off) x += y;
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 16 * w + rq4 + i, vv = 16 * j + r16;
-        const float x = S[j][i];
-        const uint16_t h = f32_to_bf16(x);
-        sm.sv.st.hi[vv * SKR + d] = h;
-        sm.sv.st.lo[vv * SKR + d] = f32_to_bf16(x - bfv(h));
-      }
-    __syncthreads();
-    // ---- per-token scalars: norms (8 lanes per token), decay scan ----
-    {
-      const int t = tid >> 3, p = tid & 7;
-      float sk = 0.f, sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float kf = bfv(sm.kr[t * SKR + 16 * p + e]);
-        const float qf = bfv(sm.qp.q[t * SKR + 16 * p + e]);
-        sk = fmaf(kf, kf, sk);
-        sq = fmaf(qf, qf, sq);
-      }
-#pragma unroll
-      for (int off = 1; off < 8; off <<= 1) {
-        sk += __shfl_xor(sk, off, kWave);
-        sq += __shfl_xor(sq, off, kWave);
-      }
-      if (p == 0) {
-        sm.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
-        sm.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-      }
-    }
-    if (w == 7) {
-      float x = sm.G[lane];
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const float y = __shfl_up(x, off, kWave);
-        if (lane >= off) x += y;
-      }
-      sm.G[lane] = x;
-      if (lane == kWave - 1) sm.gl = x;
-    }
-    __syncthreads();
-    if (tid < kC) {
-      const float eg = expf(sm.G[tid]);
-      sm.d1[tid] = sm.beta[tid] * eg * sm.rk[tid];
-      sm.d2[tid] = sm.rk[tid] * expf(sm.gl - sm.G[tid]);
-      sm.orow[tid] = eg * sm.rqs[tid];
-    }
-    __syncthreads();
+    sm.G[lane] = x;
+    if (lane == kWave - 1) sm.gl = x;
+  }
+  __syncthreads();
+  if (tid < kC) {
+    const float eg = expf(sm.G[tid]);
+    float* sc = a.scal + ch * kScal;
+    sc[tid] = eg * sm.rqs[tid];                           // output row scale of Q S
+    sc[kC + tid] = sm.rk[tid] * expf(sm.gl - sm.G[tid]);  // state-update scale of v_new row t
+    sc[2 * kC + tid] = eg * sm.rk[tid];                   // row scale of K S inside W S
+    if (tid == 0) sc[3 * kC] = expf(sm.gl);
+  }
 
-    // ---- (c) K K^T, Q K^T, Q S, P = K S ----
-    f32x4v oacc[2], pacc[2];
+  // ---- K K^T -> L (LDS), Q K^T -> A (registers); wave w takes tiles w, w+4, ... ----
+  float areg[4][4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tau = 2 * w + tt, mt = tau >> 2, nt = tau & 3, m0 = 16 * mt, n0 = 16 * nt;
-      f32x4v kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-      if (nt <= mt) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const int k0 = 32 * ks;
-          const bf16x8_t b = lds8(&sm.kr[(n0 + r16) * SKR + k0 + kq]);
-          kk = mfma(lds8(&sm.kr[(m0 + r16) * SKR + k0 + kq]), b, kk);
-          qk = mfma(lds8(&sm.qp.q[(m0 + r16) * SKR + k0 + kq]), b, qk);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = m0 + rq4 + i, s = n0 + r16;
-        const float dec = s <= t ? expf(sm.G[t] - sm.G[s]) : 0.f;
-        sm.l[t * SF + s] = s < t ? sm.beta[t] * sm.rk[t] * sm.rk[s] * dec * kk[i] : 0.f;
-        sm.aqk[t * SF + s] = s <= t ? sm.rqs[t] * sm.rk[s] * dec * qk[i] : 0.f;
-      }
-      f32x4v qs = {0.f, 0.f, 0.f, 0.f}, pp = {0.f, 0.f, 0.f, 0.f};
+  for (int tt = 0; tt < 4; ++tt) {
+    const int tau = w + 4 * tt, mt = tau >> 2, nt = tau & 3, m0 = 16 * mt, n0 = 16 * nt;
+    f32x4v kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
+    if (nt <= mt) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int k0 = 32 * ks;
-        const bf16x8_t sh = lds8(&sm.sv.st.hi[(n0 + r16) * SKR + k0 + kq]);
-        const bf16x8_t sl = lds8(&sm.sv.st.lo[(n0 + r16) * SKR + k0 + kq]);
-        const bf16x8_t ka = lds8(&sm.kr[(m0 + r16) * SKR + k0 + kq]);
-        qs = mfma(lds8(&sm.qp.q[(m0 + r16) * SKR + k0 + kq]), sh, qs);
-        pp = mfma(ka, sh, pp);
-        pp = mfma(ka, sl, pp);
+        const bf16x8_t b = lds8(&sm.kt0.kr[(n0 + r16) * SKR + k0 + kq]);
+        kk = mfma(lds8(&sm.kt0.kr[(m0 + r16) * SKR + k0 + kq]), b, kk);
+        qk = mfma(lds8(&sm.qx.q[(m0 + r16) * SKR + k0 + kq]), b, qk);
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qs[i] *= sm.orow[m0 + rq4 + i];
-      oacc[tt] = qs;
-      pacc[tt] = pp;
     }
-    __syncthreads();  // Q and S^T are dead from here on
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tau = 2 * w + tt, m0 = 16 * (tau >> 2), n0 = 16 * (tau & 3);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm.qp.pt[(n0 + r16) * SF + m0 + rq4 + i] = pacc[tt][i];
+    for (int i = 0; i < 4; ++i) {
+      const int t = m0 + rq4 + i, s = n0 + r16;
+      const float dec = s <= t ? expf(sm.G[t] - sm.G[s]) : 0.f;
+      sm.l[t * SF + s] = s < t ? sm.beta[t] * sm.rk[t] * sm.rk[s] * dec * kk[i] : 0.f;
+      areg[tt][i] = s <= t ? sm.rqs[t] * sm.rk[s] * dec * qk[i] : 0.f;
     }
-    // ---- (e) T = (I + L)^{-1} ----
-    invert_unit_lower(sm);  // ends with a barrier (also orders the P^T writes)
+  }
+  __syncthreads();  // K and Q are dead from here on
 
-    // ---- (f) U = T diag(beta) V, Y = T diag(d1) P, v_new = U - Y ----
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tau = 2 * w + tt, mt = tau >> 2, m0 = 16 * mt, n0 = 16 * (tau & 3);
-      f32x4v u = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
-      const int ksteps = (16 * (mt + 1) + 31) / 32;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks >= ksteps) break;
-        const int k0 = 32 * ks;
-        float trow[8], bsc[8], dsc[8], xa[8], pv[8];
-        ld8f(&sm.t[(m0 + r16) * SF + k0 + kq], trow);
-        ld8f(&sm.beta[k0 + kq], bsc);
-        ld8f(&sm.d1[k0 + kq], dsc);
-        ld8f(&sm.qp.pt[(n0 + r16) * SF + k0 + kq], pv);
-        bf16x8_t ah, al, bh, bl;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xa[j] = trow[j] * bsc[j];
-        split8(xa, ah, al);
-        const bf16x8_t vb = lds8(&sm.vt[(n0 + r16) * SK64 + k0 + kq]);
-        u = mfma(ah, vb, u);
-        u = mfma(al, vb, u);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xa[j] = trow[j] * dsc[j];
-        split8(xa, ah, al);
-        split8(pv, bh, bl);
-        y = mfma(ah, bh, y);
-        y = mfma(ah, bl, y);
-        y = mfma(al, bh, y);
-      }
-      pacc[tt] = u - y;  // v_new tile (registers of P are free now)
-    }
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tau = 2 * w + tt, m0 = 16 * (tau >> 2), n0 = 16 * (tau & 3);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = m0 + rq4 + i, vv = n0 + r16;
-        const float x = pacc[tt][i];
-        sm.sv.vn.vn[vv * SK64 + t] = f32_to_bf16(x);
-        const float z = sm.d2[t] * x;
-        const uint16_t zh = f32_to_bf16(z);
-        sm.sv.vn.dhi[vv * SK64 + t] = zh;
-        sm.sv.vn.dlo[vv * SK64 + t] = f32_to_bf16(z - bfv(zh));
-      }
-    }
-    __syncthreads();
+  invert_unit_lower(sm.l, sm.kt0.t, sm.qx.x);  // ends with a barrier
 
-    // ---- (g) o += (Q K^T o Gamma) v_new; S <- e^{G_last} S + K^T diag(d2) v_new ----
+  // ---- T diag(beta) (hi / lo) and A -> LDS staging -> coalesced stores ----
+  uint16_t* thi_s = &sm.qx.out[0];
+  uint16_t* tlo_s = &sm.qx.out[kC * SK64];
+  uint16_t* a_s = &sm.qx.out[2 * kC * SK64];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tau = 2 * w + tt, mt = tau >> 2, m0 = 16 * mt, n0 = 16 * (tau & 3);
-      const int ksteps = (16 * (mt + 1) + 31) / 32;
-      f32x4v acc = oacc[tt];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks >= ksteps) break;
-        const int k0 = 32 * ks;
-        float ar[8];
-        ld8f(&sm.aqk[(m0 + r16) * SF + k0 + kq], ar);
-        acc = mfma(round8(ar), lds8(&sm.sv.vn.vn[(n0 + r16) * SK64 + k0 + kq]), acc);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = m0 + rq4 + i;
-        if (t < Lc) a.o[((c0 + t) * a.HV + hv) * a.V + vbase + n0 + r16] = f32_to_bf16(acc[i]);
-      }
-    }
-    const float egl = expf(sm.gl);
+  for (int it = 0; it < 4; ++it) {  // T rows: 64 x 64, 16 elements per thread
+    const int e = (it * kPrepThreads + tid) * 4;
+    const int t = e >> 6, s4 = e & 63;
+    const float4 tv = *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
+    const float4 bv = *reinterpret_cast<const float4*>(&sm.beta[s4]);
+    const float x[4] = {tv.x * bv.x, tv.y * bv.y, tv.z * bv.z, tv.w * bv.w};
+    uint16_t h[4], lo[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      f32x4v s = S[j] * egl;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int k0 = 32 * ks;
-        const bf16x8_t ak = lds8(&sm.kt[(16 * w + r16) * SK64 + k0 + kq]);
-        s = mfma(ak, lds8(&sm.sv.vn.dhi[(16 * j + r16) * SK64 + k0 + kq]), s);
-        s = mfma(ak, lds8(&sm.sv.vn.dlo[(16 * j + r16) * SK64 + k0 + kq]), s);
-      }
-      S[j] = s;
+      h[j] = f32_to_bf16(x[j]);
+      lo[j] = f32_to_bf16(x[j] - bfv(h[j]));
     }
-    __syncthreads();  // the next chunk restages every LDS buffer
+    *reinterpret_cast<uint2*>(&thi_s[t * SK64 + s4]) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+    *reinterpret_cast<uint2*>(&tlo_s[t * SK64 + s4]) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int tt = 0; tt < 4; ++tt) {
+    const int tau = w + 4 * tt, m0 = 16 * (tau >> 2), n0 = 16 * (tau & 3);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a.ht[(sbase + 16 * w + rq4 + i) * a.V + vbase + 16 * j + r16] = S[j][i];
+    for (int i = 0; i < 4; ++i) a_s[(m0 + rq4 + i) * SK64 + n0 + r16] = f32_to_bf16(areg[tt][i]);
+  }
+  __syncthreads();
+  uint16_t* dst[3] = {a.thi + ch * kC * kC, a.tlo + ch * kC * kC, a.aqk + ch * kC * kC};
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int ci = it * kPrepThreads + tid;  // 512 vectors of 8 per matrix
+      const int t = ci >> 3, s8 = (ci & 7) * 8;
+      *reinterpret_cast<uint4*>(dst[m] + t * kC + s8) =
+          *reinterpret_cast<const uint4*>(&sm.qx.out[m * kC * SK64 + t * SK64 + s8]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Sequential pass.  The state is partitioned by value column: wave w holds the
+// full 128 x 16 column block S[:, 16w .. 16w+15] as eight 16 x 16 accumulator
+// tiles, so every product that consumes S, K S or v_new takes it as the B
+// operand straight from the wave's own registers.  The MFMA reduction index
+// of a 32-deep step is visited in the order the accumulator layout provides:
+// element j of quad q is row 32 ks + 4 q + j (j < 4) or 32 ks + 16 + 4 q +
+// j - 4 (j >= 4), and the A operands (rows of Q, K, T diag(beta), A, K^T in
+// LDS) are read in that same order, two 8-byte pieces per lane.  Only the
+// chunk inputs go through LDS: two barriers per chunk.
+struct ScanArgs {
+  const uint16_t* q;     // [total, H, K]
+  const uint16_t* k;
+  const uint16_t* v;     // [total, HV, V]
+  const uint16_t* thi;
+  const uint16_t* tlo;
+  const uint16_t* aqk;
+  const float* scal;
+  const int32_t* cu;     // [N + 1]
+  const int32_t* cstart;
+  const int32_t* order;  // [N] or null
+  const float* h0;       // [N, HV, K, V] or null
+  float* ht;             // [N, HV, K, V]
+  uint16_t* o;           // [total, HV, V]
+  int n_seqs, H, HV;
+};
+
+template <int NW>
+struct __align__(16) ScanSmem {
+  uint16_t q[kC * SKR];        // Q [t][d]
+  uint16_t k[kC * SKR];        // K [t][d]
+  uint16_t kt[kK * SK64];      // K^T [d][t]
+  uint16_t vt[16 * NW * SK64];  // V^T [v][t]
+  uint16_t thi[kC * SK64];     // T diag(beta) [t][s], hi
+  uint16_t tlo[kC * SK64];     // lo
+  uint16_t aqk[kC * SK64];     // A [t][s]
+  float orow[kC], d2[kC], ek[kC];
+  float egl;
+};
+
+// Inputs of one chunk that do not depend on the state, held in registers
+// between their load and their move to LDS.  NW waves.
+template <int NW>
+struct ChunkRegs {
+  static constexpr int NT = NW * 64;
+  static constexpr int kRow = kC * kK / 8 / NT;        // 16-byte vectors per thread of a 64 x 128 matrix
+  static constexpr int kVec = kC * 16 * NW / 8 / NT;   // ... of the 64 x V value rows (= 2)
+  static constexpr int kSq = (kC * kC / 8 + NT - 1) / NT;  // ... of a 64 x 64 matrix
+  static constexpr int kSc = (3 * kC + 1 + NT - 1) / NT;
+  uint4 q[kRow], k[kRow], v[kVec];
+  uint4 thi[kSq], tlo[kSq], aqk[kSq];
+  float scal[kSc];
+};
+
+// chunk `chunk` of a sequence starting at token `tok0` (its j-th chunk) holds
+// tokens tok0 .. tok0 + Lc - 1
+template <int NW>
+__device__ __forceinline__ void load_chunk(ChunkRegs<NW>& r, const ScanArgs& a, int chunk, int64_t tok0, int Lc,
+                                           int hv, int hk) {
+  using R = ChunkRegs<NW>;
+  constexpr int NT = R::NT, V = 16 * NW;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t ch = static_cast<int64_t>(chunk) * a.HV + hv;
+  const bool live = lane < Lc;
+#pragma unroll
+  for (int it = 0; it < R::kRow; ++it) {
+    // lane = token: each wave instruction covers 64 tokens x 8 columns, so the
+    // transposed LDS writes of K are contiguous
+    const int d8 = (it * NW + w) * 8;
+    const int64_t off = ((tok0 + lane) * a.H + hk) * kK + d8;
+    r.q[it] = live ? *reinterpret_cast<const uint4*>(a.q + off) : make_uint4(0, 0, 0, 0);
+    r.k[it] = live ? *reinterpret_cast<const uint4*>(a.k + off) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int it = 0; it < R::kVec; ++it) {
+    const int v8 = (it * NW + w) * 8;
+    r.v[it] = live ? *reinterpret_cast<const uint4*>(a.v + ((tok0 + lane) * a.HV + hv) * V + v8)
+                   : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int it = 0; it < R::kSq; ++it) {
+    const int ci = it * NT + tid;
+    const bool in = ci < kC * kC / 8;
+    const int64_t off = ch * kC * kC + (ci >> 3) * kC + (ci & 7) * 8;
+    r.thi[it] = in ? *reinterpret_cast<const uint4*>(a.thi + off) : make_uint4(0, 0, 0, 0);
+    r.tlo[it] = in ? *reinterpret_cast<const uint4*>(a.tlo + off) : make_uint4(0, 0, 0, 0);
+    r.aqk[it] = in ? *reinterpret_cast<const uint4*>(a.aqk + off) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int it = 0; it < R::kSc; ++it) {
+    const int ci = it * NT + tid;
+    r.scal[it] = ci < 3 * kC + 1 ? a.scal[ch * kScal + ci] : 0.f;
+  }
+}
+
+// 8 bf16 of an LDS row in the permuted reduction order of quad `quad` for the
+// 32-deep step starting at column k0: columns k0 + 4 quad + 0..3, then
+// k0 + 16 + 4 quad + 0..3.
+__device__ __forceinline__ bf16x8_t lds8p(const uint16_t* row, int k0, int quad) {
+  const uint2 lo = *reinterpret_cast<const uint2*>(row + k0 + 4 * quad);
+  const uint2 hi = *reinterpret_cast<const uint2*>(row + k0 + 16 + 4 * quad);
+  return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+// The B operand of a 32-deep step from two accumulator tiles (rows 32 ks ..
+// 32 ks + 15 and 32 ks + 16 .. 32 ks + 31), as bf16 hi / lo.
+__device__ __forceinline__ void pack_b(const f32x4v& t0, const f32x4v& t1, bf16x8_t& hi, bf16x8_t& lo) {
+  const float x[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+  split8(x, hi, lo);
+}
+// Transposed write of one 16-byte vector (8 consecutive columns of row `t`).
+__device__ __forceinline__ void put_t(uint16_t* mt, int stride, int c8, int t, uint4 x) {
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    mt[(c8 + 2 * j) * stride + t] = static_cast<uint16_t>(xs[j] & 0xffff);
+    mt[(c8 + 2 * j + 1) * stride + t] = static_cast<uint16_t>(xs[j] >> 16);
+  }
+}
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
+  using R = ChunkRegs<NW>;
+  __shared__ ScanSmem<NW> sm;
+  constexpr int V = 16 * NW;
+  constexpr int NT = NW * 64;
+  const int hv = blockIdx.x % a.HV;
+  const int sidx = blockIdx.x / a.HV;
+  const int n = a.order ? a.order[sidx] : sidx;
+  const int hk = hv / (a.HV / a.H);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r16 = lane & 15, quad = lane >> 4, rq4 = quad * 4;
+  const int cs = a.cstart[n], ce = a.cstart[n + 1];
+  const int64_t seq0 = a.cu[n];
+  const int seqlen = a.cu[n + 1] - a.cu[n];
+  const int vcol = 16 * w + r16;  // this lane's value column
+
+  // S[dt][i] = S[16 dt + 4 quad + i][vcol]
+  f32x4v S[8];
+  const int64_t sbase = (static_cast<int64_t>(n) * a.HV + hv) * kK;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + 16 * dt + rq4 + i) * V + vcol] : 0.f;
+
+  R cur;
+  if (cs < ce) load_chunk<NW>(cur, a, cs, seq0, min(kC, seqlen), hv, hk);
+  for (int c = cs; c < ce; ++c) {
+    const int j = c - cs;
+    const int64_t tok0 = seq0 + static_cast<int64_t>(j) * kC;
+    const int Lc = min(kC, seqlen - j * kC);
+    // ---- this chunk's inputs -> LDS, then prefetch the next chunk ----
+#pragma unroll
+    for (int it = 0; it < R::kRow; ++it) {
+      const int d8 = (it * NW + w) * 8;
+      *reinterpret_cast<uint4*>(&sm.q[lane * SKR + d8]) = cur.q[it];
+      *reinterpret_cast<uint4*>(&sm.k[lane * SKR + d8]) = cur.k[it];
+      put_t(sm.kt, SK64, d8, lane, cur.k[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < R::kVec; ++it) put_t(sm.vt, SK64, (it * NW + w) * 8, lane, cur.v[it]);
+#pragma unroll
+    for (int it = 0; it < R::kSq; ++it) {
+      const int ci = it * NT + tid;
+      if (ci < kC * kC / 8) {
+        const int o = (ci >> 3) * SK64 + (ci & 7) * 8;
+        *reinterpret_cast<uint4*>(&sm.thi[o]) = cur.thi[it];
+        *reinterpret_cast<uint4*>(&sm.tlo[o]) = cur.tlo[it];
+        *reinterpret_cast<uint4*>(&sm.aqk[o]) = cur.aqk[it];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < R::kSc; ++it) {
+      const int ci = it * NT + tid;
+      if (ci < kC) sm.orow[ci] = cur.scal[it];
+      else if (ci < 2 * kC) sm.d2[ci - kC] = cur.scal[it];
+      else if (ci < 3 * kC) sm.ek[ci - 2 * kC] = cur.scal[it];
+      else if (ci == 3 * kC) sm.egl = cur.scal[it];
+    }
+    if (c + 1 < ce) load_chunk<NW>(cur, a, c + 1, tok0 + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
+    lds_barrier();
+
+    // ---- Q S (1 pass) and P = K S (2 passes), four row tiles of this column block ----
+    f32x4v qs[4], ps[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) qs[mt] = ps[mt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8_t bh, bl;
+      pack_b(S[2 * ks], S[2 * ks + 1], bh, bl);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = (16 * mt + r16) * SKR;
+        const bf16x8_t aq = lds8p(&sm.q[row], 32 * ks, quad);
+        const bf16x8_t ak = lds8p(&sm.k[row], 32 * ks, quad);
+        qs[mt] = mfma(aq, bh, qs[mt]);
+        ps[mt] = mfma(ak, bh, ps[mt]);
+        ps[mt] = mfma(ak, bl, ps[mt]);
+      }
+    }
+    // ---- v_new = T diag(beta) V - T diag(beta) (diag(e^G rk) P): 2 + 3 passes, T lower triangular ----
+    bf16x8_t vb[2], ph[2], pl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      vb[ks] = lds8p(&sm.vt[vcol * SK64], 32 * ks, quad);
+      f32x4v p0 = ps[2 * ks], p1 = ps[2 * ks + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p0[i] *= sm.ek[32 * ks + rq4 + i];
+        p1[i] *= sm.ek[32 * ks + 16 + rq4 + i];
+      }
+      pack_b(p0, p1, ph[ks], pl[ks]);
+    }
+    f32x4v vn[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      f32x4v u = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (32 * ks <= 16 * mt + 15) {
+          const int row = (16 * mt + r16) * SK64;
+          const bf16x8_t th = lds8p(&sm.thi[row], 32 * ks, quad);
+          const bf16x8_t tl = lds8p(&sm.tlo[row], 32 * ks, quad);
+          u = mfma(th, vb[ks], u);
+          u = mfma(tl, vb[ks], u);
+          y = mfma(th, ph[ks], y);
+          y = mfma(th, pl[ks], y);
+          y = mfma(tl, ph[ks], y);
+        }
+      }
+      vn[mt] = u - y;
+    }
+    // ---- o = diag(orow) Q S + A v_new (A lower triangular, 1 pass) ----
+    bf16x8_t vnb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const float x[8] = {vn[2 * ks][0], vn[2 * ks][1], vn[2 * ks][2], vn[2 * ks][3],
+                          vn[2 * ks + 1][0], vn[2 * ks + 1][1], vn[2 * ks + 1][2], vn[2 * ks + 1][3]};
+      vnb[ks] = round8v(x);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      f32x4v acc = qs[mt];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] *= sm.orow[16 * mt + rq4 + i];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        if (32 * ks <= 16 * mt + 15) acc = mfma(lds8p(&sm.aqk[(16 * mt + r16) * SK64], 32 * ks, quad), vnb[ks], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * mt + rq4 + i;
+        if (t < Lc) a.o[((tok0 + t) * a.HV + hv) * V + vcol] = f32_to_bf16(acc[i]);
+      }
+    }
+    // ---- S <- e^{G_last} S + K^T diag(d2) v_new (2 passes) ----
+    bf16x8_t zh[2], zl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      f32x4v z0 = vn[2 * ks], z1 = vn[2 * ks + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        z0[i] *= sm.d2[32 * ks + rq4 + i];
+        z1[i] *= sm.d2[32 * ks + 16 + rq4 + i];
+      }
+      pack_b(z0, z1, zh[ks], zl[ks]);
+    }
+    const float egl = sm.egl;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      f32x4v s = S[dt] * egl;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8_t ak = lds8p(&sm.kt[(16 * dt + r16) * SK64], 32 * ks, quad);
+        s = mfma(ak, zh[ks], s);
+        s = mfma(ak, zl[ks], s);
+      }
+      S[dt] = s;
+    }
+    lds_barrier();  // the next chunk restages every LDS buffer
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a.ht[(sbase + 16 * dt + rq4 + i) * V + vcol] = S[dt][i];
+}
+
+int64_t chunk_bound(int64_t total, int64_t n_seqs) { return total / kC + n_seqs; }
+
+struct WsLayout {
+  int64_t table, cstart, thi, tlo, aqk, scal, bytes;
+};
+WsLayout ws_layout(int64_t total, int64_t n_seqs, int64_t HV) {
+  const int64_t nc = chunk_bound(total, n_seqs);
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  WsLayout l;
+  l.table = 0;
+  l.cstart = up(nc * 16);
+  l.thi = up(l.cstart + (n_seqs + 1) * 4);
+  l.tlo = l.thi + up(nc * HV * kC * kC * 2);
+  l.aqk = l.tlo + up(nc * HV * kC * kC * 2);
+  l.scal = l.aqk + up(nc * HV * kC * kC * 2);
+  l.bytes = l.scal + up(nc * HV * kScal * 4);
+  return l;
 }
 
 }  // namespace
 }  // namespace yh
 
+extern "C" int64_t yh_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t n_seqs, int64_t HV, int64_t V) {
+  if (total_tokens < 0 || n_seqs < 0 || HV <= 0 || V <= 0) return 0;
+  return yh::ws_layout(total_tokens, n_seqs, HV).bytes;
+}
+
 extern "C" int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, const void* g, const void* beta,
                                    const float* initial_state, float* final_state, void* o,
-                                   const int32_t* cu_seqlens, const int32_t* order, int64_t n_seqs, int64_t H,
-                                   int64_t HV, int64_t K, int64_t V, float scale, int use_qk_l2norm, int qkv_dtype,
-                                   int g_dtype, int beta_dtype, yh_stream_t stream) {
+                                   const int32_t* cu_seqlens, const int32_t* order, int64_t n_seqs,
+                                   int64_t total_tokens, int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+                                   int use_qk_l2norm, int qkv_dtype, int g_dtype, int beta_dtype, void* workspace,
+                                   int64_t workspace_bytes, yh_stream_t stream) {
   using namespace yh;
-  YH_CHECK_ARG(q && k && v && g && beta && final_state && o && cu_seqlens, "gdn_chunk: null pointer");
-  YH_CHECK_ARG(n_seqs >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_chunk: bad sizes");
+  YH_CHECK_ARG(n_seqs >= 0 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_chunk: bad sizes");
   YH_CHECK_ARG(K == 128, "gdn_chunk: K must be 128 (got %lld)", (long long)K);
-  YH_CHECK_ARG(V > 0 && V % 64 == 0, "gdn_chunk: V must be a positive multiple of 64 (got %lld)", (long long)V);
+  YH_CHECK_ARG(V == 64 || V == 128, "gdn_chunk: V must be 64 or 128 (got %lld)", (long long)V);
   YH_CHECK_ARG(qkv_dtype == YH_BF16, "gdn_chunk: q/k/v must be bfloat16");
   YH_CHECK_ARG(is_float_dtype(g_dtype) && is_float_dtype(beta_dtype), "gdn_chunk: bad gate dtypes");
-  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) &
-                15) == 0,
-               "gdn_chunk: q/k/v must be 16-byte aligned");
-  YH_CHECK_ARG(n_seqs * HV * (V / 64) < (1LL << 31), "gdn_chunk: grid too large");
   if (n_seqs == 0) return YH_OK;
-  ChunkArgs a{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), g,
-              beta, initial_state, final_state, static_cast<uint16_t*>(o), cu_seqlens, order, (int)n_seqs, (int)H,
-              (int)HV, (int)V, scale, use_qk_l2norm ? 1 : 0, g_dtype, beta_dtype};
-  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(static_cast<unsigned>(n_seqs * HV * (V / 64))), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
-  YH_CHECK_LAUNCH("gdn_chunk");
+  YH_CHECK_ARG(q && k && v && g && beta && final_state && o && cu_seqlens && workspace, "gdn_chunk: null pointer");
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                 reinterpret_cast<uintptr_t>(workspace)) & 15) == 0,
+               "gdn_chunk: q/k/v and the workspace must be 16-byte aligned");
+  const WsLayout l = ws_layout(total_tokens, n_seqs, HV);
+  YH_CHECK_ARG(workspace_bytes >= l.bytes, "gdn_chunk: workspace of %lld bytes required", (long long)l.bytes);
+  const int64_t nc = chunk_bound(total_tokens, n_seqs);
+  YH_CHECK_ARG(nc < (1LL << 31) && n_seqs * HV < (1LL << 31) && HV < 65536, "gdn_chunk: grid too large");
+  char* ws = static_cast<char*>(workspace);
+  int32_t* table = reinterpret_cast<int32_t*>(ws + l.table);
+  int32_t* cstart = reinterpret_cast<int32_t*>(ws + l.cstart);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kIdxThreads), 0, st, cu_seqlens, (int)n_seqs, table, cstart,
+                     (int)nc);
+  YH_CHECK_LAUNCH("gdn_chunk_index");
+  uint16_t* thi = reinterpret_cast<uint16_t*>(ws + l.thi);
+  uint16_t* tlo = reinterpret_cast<uint16_t*>(ws + l.tlo);
+  uint16_t* aqk = reinterpret_cast<uint16_t*>(ws + l.aqk);
+  float* scal = reinterpret_cast<float*>(ws + l.scal);
+  if (nc > 0) {
+    PrepArgs p{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), g, beta, table, cstart, thi, tlo, aqk,
+               scal, (int)n_seqs, (int)H, (int)HV, scale, use_qk_l2norm ? 1 : 0, g_dtype, beta_dtype};
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3(static_cast<unsigned>(nc), static_cast<unsigned>(HV)),
+                       dim3(kPrepThreads), 0, st, p);
+    YH_CHECK_LAUNCH("gdn_chunk_prep");
+  }
+  ScanArgs s{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), thi, tlo,
+             aqk, scal, cu_seqlens, cstart, order, initial_state, final_state, static_cast<uint16_t*>(o), (int)n_seqs,
+             (int)H, (int)HV};
+  const dim3 grid(static_cast<unsigned>(n_seqs * HV));
+  if (V == 128)
+    hipLaunchKernelGGL(chunk_scan_kernel<8>, grid, dim3(512), 0, st, s);
+  else
+    hipLaunchKernelGGL(chunk_scan_kernel<4>, grid, dim3(256), 0, st, s);
+  YH_CHECK_LAUNCH("gdn_chunk_scan");
   return YH_OK;
 }

@@ -95,6 +95,19 @@ def _packed_or_batched(query, key, value, g, beta, cu_seqlens):
     return cu
 
 
+_chunk_ws: dict = {}
+
+
+def _chunk_workspace(device, nbytes):
+    """Per-device scratch of the chunk kernels, grown on demand."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _chunk_ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
+        _chunk_ws[key] = ws
+    return ws
+
+
 def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False, cu_seqlens=None,
                            lengths=None, force_recurrent=False, **unused):
@@ -108,10 +121,13 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
     initial_state ``[N, HV, K, V]``.  ``initial_state`` is read, not modified;
     returns ``(o, final_state or None)``.
 
-    Packed inputs with K = 128, V a multiple of 64 and bf16 q/k/v run the MFMA
-    chunk kernel (chunk 64); other shapes, or ``force_recurrent=True``, run the
-    token-recurrent kernel over each sequence.  ``lengths`` (host ints, one per
-    sequence) lets the chunk kernel start the longest sequences first.
+    Packed inputs with K = 128, V in {64, 128} and bf16 q/k/v run the MFMA
+    chunk kernels (chunk 64); other shapes, or ``force_recurrent=True``, run
+    the token-recurrent kernel over each sequence.  ``lengths`` (host ints, one
+    per sequence) lets the chunk kernels start the longest sequences first.
+    The chunk kernels use a per-device workspace that is cached and grown on
+    demand: concurrent calls on different streams of one device must not
+    overlap.
     """
     if g is None or beta is None:
         raise ValueError("chunk_gated_delta_rule needs g and beta")
@@ -138,16 +154,18 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
     q, k, v, g_, be = (_contig(x) for x in (query, key, value, g, beta))
     o = torch.empty(1, total, hv, vd, device=dev, dtype=value.dtype)
     sc = float(kd ** -0.5 if scale is None else scale)
-    if kd == 128 and vd % 64 == 0 and q.dtype == torch.bfloat16 and not force_recurrent:
+    if kd == 128 and vd in (64, 128) and q.dtype == torch.bfloat16 and not force_recurrent:
         h0 = None if initial_state is None else initial_state.contiguous()
         state = torch.empty(n, hv, kd, vd, device=dev, dtype=torch.float32)
         order = None
         if lengths is not None:  # longest sequences first balances the grid
             order = torch.tensor(sorted(range(n), key=lambda i: -int(lengths[i])), dtype=torch.int32,
                                  device=dev)
+        ws = _chunk_workspace(dev, N.lib().yh_gdn_chunk_workspace_bytes(total, n, hv, vd))
         N.call("yh_gdn_chunk_varlen", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_.data_ptr(), be.data_ptr(),
-               N.ptr(h0), state.data_ptr(), o.data_ptr(), cu.data_ptr(), N.ptr(order), n, h, hv, kd, vd, sc,
-               int(bool(use_qk_l2norm_in_kernel)), N.code(q), N.code(g_), N.code(be), N.stream_of(q))
+               N.ptr(h0), state.data_ptr(), o.data_ptr(), cu.data_ptr(), N.ptr(order), n, total, h, hv, kd, vd, sc,
+               int(bool(use_qk_l2norm_in_kernel)), N.code(q), N.code(g_), N.code(be), ws.data_ptr(), ws.numel(),
+               N.stream_of(q))
         return o, (state if output_final_state else None)
     if initial_state is None:
         state = torch.zeros(n, hv, kd, vd, device=dev, dtype=torch.float32)
