@@ -385,7 +385,7 @@ int yh_gated_rmsnorm(const void* o, const void* z, int64_t z_stride, const void*
 
 /* out[n, i] = bf16(bf16(silu(gu[n, i])) * gu[n, I + i]) for gate_up [N, 2I]
  * (runtime/model/inference_kernels.py:642-666).  I % 8 == 0. */
-int yh_silu_mul(const void* gate_up, void* out, int64_t N, int64_t I, yh_stream_t stream);
+int yh_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t N, int64_t I, yh_stream_t stream);
 
 /*
  * Per-head RMSNorm (1 + w) and rotate-half RoPE on the first rotary_dim of

@@ -202,6 +202,7 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
     }
     // lane (s, rr) holds the logit of slot s*RPI + rr of this block
     const bool mine_live = (live >> (s * RPI + rr)) & 1ull;
+    float pw[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float logit = mine_live ? part[r][0] : -INFINITY;
@@ -214,12 +215,17 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
       m_run[r] = m_new;
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
+      pw[r] = p;
+    }
+    // P.V: each value row is converted once and used for all R heads
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
+    for (int i = 0; i < NI; ++i) {
+      float vf[8];
+      cvt8<DT>(vr[i], vf);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
         // weight of the row this lane loaded at instruction i (slot i*RPI + rr)
-        const float w = __shfl(p, rr * LPR + i, kWave);
-        float vf[8];
-        cvt8<DT>(vr[i], vf);
+        const float w = __shfl(pw[r], rr * LPR + i, kWave);
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(w, vf[j], acc[r][j]);
       }

@@ -165,13 +165,15 @@ __global__ void __launch_bounds__(256) gated_rmsnorm_kernel(const uint16_t* o, c
   reinterpret_cast<uint32_t*>(out + item * 128)[lane] = res;
 }
 
-// out[n, i] = bf16(bf16(silu(gu[n, i])) * gu[n, I + i]), gu rows of 2I.
-__global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* gu, uint16_t* out, int64_t N, int I) {
+// out[n, i] = bf16(bf16(silu(gu[n, i])) * gu[n, I + i]), gu rows of 2I
+// elements `gs` apart.
+__global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* gu, int64_t gs, uint16_t* out, int64_t N,
+                                                       int I) {
   const int64_t idx = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
   if (idx >= N * I) return;
   const int64_t n = idx / I, i = idx % I;
-  const uint4 gv = *reinterpret_cast<const uint4*>(gu + n * 2 * I + i);
-  const uint4 uv = *reinterpret_cast<const uint4*>(gu + n * 2 * I + I + i);
+  const uint4 gv = *reinterpret_cast<const uint4*>(gu + n * gs + i);
+  const uint4 uv = *reinterpret_cast<const uint4*>(gu + n * gs + I + i);
   const uint16_t* g = reinterpret_cast<const uint16_t*>(&gv);
   const uint16_t* u = reinterpret_cast<const uint16_t*>(&uv);
   uint16_t o[8];
@@ -289,13 +291,17 @@ extern "C" int yh_gated_rmsnorm(const void* o, const void* z, int64_t z_stride, 
   return YH_OK;
 }
 
-extern "C" int yh_silu_mul(const void* gate_up, void* out, int64_t N, int64_t I, yh_stream_t stream) {
+extern "C" int yh_silu_mul(const void* gate_up, int64_t gate_up_stride, void* out, int64_t N, int64_t I,
+                           yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(N >= 0 && (N == 0 || (gate_up && out)) && I > 0 && I % 8 == 0, "silu_mul: I must be a positive multiple of 8");
+  YH_CHECK_ARG(gate_up_stride >= 2 * I && gate_up_stride % 8 == 0 &&
+                   (reinterpret_cast<uintptr_t>(gate_up) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "silu_mul: rows must be 16-byte aligned");
   if (N == 0) return YH_OK;
   const int64_t vecs = N * I / 8;
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((vecs + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up),
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up), gate_up_stride,
                      static_cast<uint16_t*>(out), N, (int)I);
   YH_CHECK_LAUNCH("silu_mul");
   return YH_OK;

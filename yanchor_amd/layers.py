@@ -86,14 +86,17 @@ def gated_rmsnorm(o, z, w, eps):
 
 def silu_mul(gate_up):
     """silu(gate) * up of a packed [*, 2I] projection (runtime/model/
-    inference_kernels.py:642-666); returns [*, I]."""
+    inference_kernels.py:642-666); returns [*, I].  A 2-D input may be a
+    column slice of a wider projection (any 16-byte aligned row stride)."""
     _bf16(gate_up)
-    gu = gate_up.contiguous()
+    gu = gate_up
+    if gu.ndim != 2 or gu.stride(-1) != 1 or gu.stride(0) % 8 or gu.data_ptr() % 16:
+        gu = gu.contiguous().view(-1, gate_up.shape[-1])
     i2 = gu.shape[-1]
-    n = gu.numel() // i2
+    n = gu.shape[0]
     N.require_device(gu)
-    out = torch.empty(*gu.shape[:-1], i2 // 2, dtype=gu.dtype, device=gu.device)
-    N.call("yh_silu_mul", gu.data_ptr(), out.data_ptr(), n, i2 // 2, N.stream_of(gu))
+    out = torch.empty(*gate_up.shape[:-1], i2 // 2, dtype=gu.dtype, device=gu.device)
+    N.call("yh_silu_mul", gu.data_ptr(), gu.stride(0), out.data_ptr(), n, i2 // 2, N.stream_of(gu))
     return out
 
 

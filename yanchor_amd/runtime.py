@@ -106,11 +106,11 @@ class HipOps:
 
     def linear(self, x, w):
         """Decode projections: the skinny split-K kernel where it beats the
-        library GEMM on MI355X (bf16, <= 128 rows, output width <= 4096, K >=
-        2048: the GDN / attention output, MLP down and memory-writer
+        library GEMM on MI355X (bf16, <= 128 rows, output width 1024 ... 4096,
+        K >= 2048: the GDN / attention output, MLP down and memory-writer
         projections), torch (hipBLASLt) otherwise."""
         n, k = w.shape
-        if (x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128 and n <= 4096 and n % 64 == 0
+        if (x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128 and 1024 <= n <= 4096 and n % 64 == 0
                 and k % 64 == 0 and k >= 2048):
             return self.layers.linear(x, w)
         return F.linear(x, w)
@@ -268,15 +268,19 @@ class Model:
                 qkv_out = 2 * c.attn_heads * c.head_dim + 2 * c.kv_heads * c.head_dim
                 L.update(kind="attn", w_qkv=w(qkv_out, c.hidden), q_norm=zeros(c.head_dim),
                          k_norm=zeros(c.head_dim), w_o=w(c.hidden, c.attn_heads * c.head_dim),
-                         m_in_norm=zeros(c.hidden), m_q=w(c.attn_heads * c.head_dim, c.hidden),
+                         m_in_norm=zeros(c.hidden),
                          m_q_norm=zeros(c.head_dim), m_k_norm=zeros(c.head_dim),
                          read_scale=w(c.attn_heads).float(), read_gate_w=w(c.attn_heads, c.head_dim).float(),
                          read_gate_b=w(c.attn_heads).float(),
-                         writer_gate_up=w(2 * c.writer_intermediate, c.hidden),
                          writer_down=w(c.hidden, c.writer_intermediate),
                          m_kv=w(2 * c.kv_heads * c.head_dim, c.hidden),
-                         adm_down=w(c.admission_rank, c.hidden), adm_up=w(c.kv_heads, c.admission_rank).float(),
+                         adm_up=w(c.kv_heads, c.admission_rank).float(),
                          m_o=w(c.hidden, c.attn_heads * c.head_dim))
+                # the three projections of u (query, admission features, writer
+                # gate|up) share one weight so the decode step runs one GEMM
+                qd, ad = c.attn_heads * c.head_dim, c.admission_rank
+                m_in = w(qd + ad + 2 * c.writer_intermediate, c.hidden)
+                L.update(m_in=m_in, m_q=m_in[:qd], adm_down=m_in[qd: qd + ad], writer_gate_up=m_in[qd + ad:])
             else:
                 in_out = c.conv_dim + c.gdn_heads_v * c.gdn_dv + 2 * c.gdn_heads_v
                 a_log = torch.log(torch.empty(c.gdn_heads_v, device=self.device).uniform_(1.0, 16.0,
@@ -380,13 +384,15 @@ class Model:
         c, B, ops = self.cfg, hidden.shape[0], self.ops
         H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
         u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
-        mq = ops.linear(u, L["m_q"]).view(B, H, D)
+        proj = ops.linear(u, L["m_in"])                                    # [q | admission features | gate | up]
+        qd, ad = H * D, c.admission_rank
+        mq = proj[:, :qd].view(B, H, D)
         qn = ops.head_norm_rope(mq, L["m_q_norm"], None, None, 0, c.rms_eps)
         gate = torch.tanh(L["read_scale"]) * 2 * torch.sigmoid(
             (qn.float() * L["read_gate_w"]).sum(-1) / math.sqrt(D) + L["read_gate_b"])
         q = ops.head_norm_rope(mq, L["m_q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
-        scores = ops.linear(F.silu(ops.linear(u, L["adm_down"])).float(), L["adm_up"])
-        zz = u + ops.linear(ops.silu_mul(ops.linear(u, L["writer_gate_up"])), L["writer_down"])
+        scores = ops.linear(F.silu(proj[:, qd: qd + ad]).float(), L["adm_up"])
+        zz = u + ops.linear(ops.silu_mul(proj[:, qd + ad:]), L["writer_down"])
         kv = ops.linear(zz, L["m_kv"])
         key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
                                  c.rms_eps)
