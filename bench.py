@@ -192,6 +192,9 @@ class _OracleOps:
     def memory_commit(self, key, value, scores, active, chunk, state):
         self.anchor.commit_decode(key, value, scores, active, chunk, state)
 
+    def memory_sequence(self, q, key, value, scores, valid, chunk, state):
+        return self.anchor.sequence(q, key, value, scores, valid, chunk, state, dtype=torch.float32)
+
     def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty):
         sc = self.sampling.presence_penalty(logits, seen, penalty) if seen is not None else logits.float()
         vals, idx = torch.topk(sc / temperature, top_k, dim=-1)

@@ -203,6 +203,54 @@ int yh_indexed_gqa(const void* query, const void* key, const void* value, const 
                    int64_t S, int64_t CAP, int dtype, yh_stream_t stream);
 
 /*
+ * Anchor memory, prefill continuation, step 1: the block-wise Top-K scan of
+ * IndependentGQAMemory._sequence with a state (modeling_yanchor.py:178-275:
+ * exclusive_prefix_topk 65-78 on the new blocks, merged with the committed
+ * slots at 217-219; the state update 256-274).
+ *
+ * A row's sequence is its old pending tokens (count[b] of them) followed by
+ * its counts[b] valid new tokens, cut into blocks of `chunk`.  Source rows of
+ * row b: [0, capacity) committed slot, [capacity, capacity + chunk) old
+ * pending slot, capacity + chunk + i new token i.
+ *
+ *   new_scores  [B, L, G] float32, valid tokens first; counts int64 [B]
+ *   scores [B, G, capacity] f32, positions [B, G, capacity] i32,
+ *   pending_scores [B, G, pending_capacity] f32, count / total int64 [B]
+ *               -- the state, dense; scores, positions and pending_scores
+ *               are rewritten IN PLACE with the final memory and pending tail
+ *   block_refs  [B, NB, G, capacity] int32 out: source rows of the memory in
+ *               force for block j (-1 = empty slot)
+ *   final_refs  [B, G, capacity] int32 out: source rows of the final memory
+ *   pending_refs [B, G, pending_capacity] int32 out: source rows of the new
+ *               pending tokens (-1 past the tail)
+ * Requirements: chunk <= pending_capacity, chunk <= 1024,
+ * capacity + chunk <= 2048, NB * chunk >= L + chunk - 1.  A row whose count is
+ * outside [0, chunk) reads nothing (block_refs -1) and keeps its state.
+ */
+int yh_anchor_prefix(const float* new_scores, const int64_t* counts, float* scores, int32_t* positions,
+                     float* pending_scores, const int64_t* count, const int64_t* total, int32_t* block_refs,
+                     int32_t* final_refs, int32_t* pending_refs, int64_t B, int64_t L, int64_t G, int64_t capacity,
+                     int64_t pending_capacity, int64_t chunk, int64_t NB, yh_stream_t stream);
+
+/*
+ * Anchor memory, prefill continuation, step 2: copy the key / value rows of
+ * the final memory and the pending tail out of the assembled sources into the
+ * state (zeros where a slot references nothing), then count = (count +
+ * counts) % chunk, total += counts (modeling_yanchor.py:256-274).
+ *
+ *   src_keys, src_values [B, S, G, D] (dtype): the source rows above,
+ *               S = capacity + chunk + L
+ *   final_refs, pending_refs, counts: as written / read by yh_anchor_prefix
+ *   keys, values [B, G, capacity, D]; pending_keys, pending_values
+ *   [B, G, pending_capacity, D]; count, total int64 [B] -- updated IN PLACE
+ */
+int yh_anchor_sequence_commit(const void* src_keys, const void* src_values, const int32_t* final_refs,
+                              const int32_t* pending_refs, const int64_t* counts, void* keys, void* values,
+                              void* pending_keys, void* pending_values, int64_t* count, int64_t* total, int64_t B,
+                              int64_t S, int64_t L, int64_t G, int64_t capacity, int64_t pending_capacity,
+                              int64_t chunk, int64_t D, int dtype, yh_stream_t stream);
+
+/*
  * Skinny bf16 projection of the decode step: out[M, N] = x[M, K] . W[N, K]^T,
  * fp32 accumulation, bf16 output (torch.nn.functional.linear without bias, the
  * q/k/v/z/b/a, output, MLP, memory-writer and lm_head projections of

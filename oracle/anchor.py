@@ -14,6 +14,9 @@ Restates, from the reference:
 * ``commit_decode``      the decode push + Top-K commit, modeling_yanchor.py:
                          291-312, with the slot indirection of
                          runtime/model/independent_memory.py:90-175, 190-201
+* ``sequence``           the prefill read / write continuing a state,
+                         IndependentGQAMemory._sequence, modeling_yanchor.py:
+                         178-275 (given every token's key / value)
 
 Ordering contract of every Top-K here: candidates are ordered by
 (score descending, position ascending with invalid last, candidate index
@@ -27,7 +30,10 @@ slots; the read equals a softmax over [logits, 0] computed independently and
 reduces to closed forms for zero / one valid slot; ``indexed_gqa`` equals an
 SDPA over the gathered rows plus a zero row, and equals ``committed_read`` when
 a single token references the committed slots; ``exclusive_prefix_topk``
-is checked against the O(n^2) definition "Top-K of every earlier block".
+is checked against the O(n^2) definition "Top-K of every earlier block";
+``sequence`` (prefix Top-K of blocks, merged with the committed slots, one
+indexed read per block) equals the token-by-token committed_read /
+commit_decode sequence it replaces -- reads, and the state it leaves.
 """
 from __future__ import annotations
 
@@ -225,3 +231,84 @@ def commit_decode(key, value, scores, active, chunk, state: MemoryState, indices
             state.count[b] = c + 1
         state.total[b] += 1
     return state
+
+
+def sequence(query, key, value, scores, valid, chunk, state: MemoryState, dtype=torch.float64):
+    """Anchor-memory read and write of a prefill chunk continuing ``state``,
+    IN PLACE (IndependentGQAMemory._sequence with a state,
+    modeling_yanchor.py:178-275), restated step by step: order the valid
+    tokens first (180-187); place them after the old pending tokens in an
+    extended sequence of whole chunks (189-206); exclusive prefix Top-K of the
+    blocks merged with the committed slots (207-219); every block's queries
+    read the memory in force before it (244-250); the state keeps the memory
+    after the last full block and the tokens after it as pending (256-274).
+
+    query ``[B, L, H, D]``; key, value ``[B, L, G, D]`` (every token's written
+    key / value: the reference writes only the tokens it will read, 220-231,
+    which changes no result); scores ``[B, L, G]``; valid ``None`` or bool
+    ``[B, L]``.  Returns ``[B, L, H, D]`` in the query dtype."""
+    b, length, h, d = query.shape
+    g_n, cap = state.keys.shape[1], state.keys.shape[2]
+    c = int(chunk)
+    bi = torch.arange(b)[:, None]
+    if valid is None:
+        order = None
+        q, k, v, s = query, key, value, scores
+        counts = torch.full((b,), length, dtype=torch.long)
+    else:
+        order = valid.long().argsort(dim=1, descending=True, stable=True)
+        q, k, v, s = (x[bi, order] for x in (query, key, value, scores))
+        counts = valid.long().sum(1)
+    old_count, old_total = state.count.clone(), state.total.clone()
+    extent = math.ceil((length + c) / c) * c
+    at = torch.arange(extent)[None].expand(b, -1)
+    valid_extent = at < (old_count + counts)[:, None]
+    select = torch.where(at < old_count[:, None], at, c + at - old_count[:, None]).clamp_max(c + length - 1)
+    qx = torch.cat((q.new_zeros(b, c, h, d), q), 1)[bi, select]
+    sx = torch.cat((state.pending_scores.transpose(1, 2)[:, :c], s.float()), 1)[bi, select]
+    sx = sx.masked_fill(~valid_extent[..., None], -math.inf)
+    positions = (old_total - old_count)[:, None] + at
+    refs = (at + cap).masked_fill(~valid_extent, -1)               # sequence index + committed slots
+    blocks = extent // c
+    meta = [x[:, :, None].expand(-1, -1, g_n) if x.ndim == 2 else x for x in (sx, positions, refs)]
+    meta = [x.reshape(b, blocks, c, g_n).transpose(2, 3) for x in meta]
+    prefix = exclusive_prefix_topk(*meta, cap)                      # [B, blocks + 1, G, cap]
+    slots = torch.arange(cap)[None, None].expand(b, g_n, -1).masked_fill(state.positions < 0, -1)
+    initial = (state.scores, state.positions, slots)
+    prefix = merge_topk(prefix, tuple(x[:, None].expand(-1, blocks + 1, -1, -1) for x in initial), cap)
+    # source rows: committed slot s -> s; old pending t -> cap + t; new token i -> cap + c + i
+    src_k = torch.cat((state.keys.transpose(1, 2), state.pending_keys[:, :, :c].transpose(1, 2), k), 1)
+    src_v = torch.cat((state.values.transpose(1, 2), state.pending_values[:, :, :c].transpose(1, 2), v), 1)
+    table = torch.full((b, cap + extent), -1, dtype=torch.long)    # reference -> source row
+    table[:, :cap] = torch.arange(cap)
+    t_idx = at
+    table[:, cap:] = torch.where(t_idx < old_count[:, None], cap + t_idx,
+                                 torch.where(valid_extent, cap + c + (t_idx - old_count[:, None]),
+                                             torch.full_like(t_idx, -1)))
+    def rows(r):
+        return table[bi.reshape(b, *([1] * (r.ndim - 1))).expand_as(r), r.clamp_min(0)].masked_fill(r < 0, -1)
+    read_refs = rows(prefix[2][:, :-1])                             # [B, blocks, G, cap]
+    read = indexed_gqa(qx.reshape(b, blocks, c, h, d), src_k, src_v, read_refs, dtype=dtype).flatten(1, 2)
+    out = read[bi, (old_count[:, None] + torch.arange(length)[None]).clamp_max(extent - 1)]
+    if order is not None:
+        out = out[bi, order.argsort(1)] * valid[..., None, None].to(out.dtype)
+    full = (old_count + counts) // c
+    score, position, reference = (x[torch.arange(b), full] for x in prefix)
+    src_rows = rows(reference)                                      # [B, G, cap]
+    g_idx = torch.arange(g_n)[None, :, None]
+    b_idx = torch.arange(b)[:, None, None]
+    state.keys.copy_(src_k[b_idx, src_rows.clamp_min(0), g_idx].masked_fill((src_rows < 0)[..., None], 0))
+    state.values.copy_(src_v[b_idx, src_rows.clamp_min(0), g_idx].masked_fill((src_rows < 0)[..., None], 0))
+    state.scores.copy_(score)
+    state.positions.copy_(position.to(torch.int32))
+    pc = state.pending_keys.shape[2]
+    remaining = (old_count + counts) % c
+    pend = (full[:, None] * c + torch.arange(pc)[None]).clamp_max(extent - 1)   # sequence indices
+    mask = torch.arange(pc)[None] < remaining[:, None]
+    prow = table[bi, cap + pend].clamp_min(0)                       # [B, pc]
+    state.pending_keys.copy_(src_k[bi, prow].masked_fill(~mask[..., None, None], 0).transpose(1, 2))
+    state.pending_values.copy_(src_v[bi, prow].masked_fill(~mask[..., None, None], 0).transpose(1, 2))
+    state.pending_scores.copy_(sx[bi, pend].masked_fill(~mask[..., None], -math.inf).transpose(1, 2))
+    state.count.copy_(remaining)
+    state.total.add_(counts)
+    return out

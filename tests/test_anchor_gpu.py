@@ -152,3 +152,77 @@ def test_indexed_read_no_references(gpu):
     refs.fill_(-1)
     got = im.indexed_gqa(q.to(gpu), k.to(gpu), v.to(gpu), refs.to(gpu))
     assert torch.count_nonzero(got) == 0
+
+
+@pytest.mark.parametrize("b,g,h,cap,pc,chunk,length,fill,holes,empty", [
+    (4, 2, 8, 64, 8, 8, 37, 3, False, False),     # unsorted committed slots, old pending tokens, ragged tail
+    (4, 2, 8, 64, 10, 8, 37, 5, True, False),     # invalid tokens; pending capacity > chunk
+    (3, 2, 4, 64, 8, 8, 5, 2, False, False),      # no block completes: the committed slots are only re-ranked
+    (2, 8, 32, 256, 64, 64, 300, 10, False, False),   # the decode layout: 256 slots, chunk 64, 8 groups
+    (5, 8, 32, 256, 64, 64, 128, 0, False, True),     # fresh state (a prompt prefill), whole blocks only
+])
+def test_sequence_matches_oracle(gpu, b, g, h, cap, pc, chunk, length, fill, holes, empty):
+    """Prefill continuation on the GPU against the oracle's restatement of
+    _sequence: the state bit-exact (memory kept in rank order, pending tail,
+    count, total, zeroed dead slots), the read within 1e-2 of the float64
+    oracle."""
+    d = 128
+    seed = b * 100 + length
+    if empty:
+        st = im.IndependentMemoryState.empty(b, g, cap, pc, d, "cpu", torch.bfloat16)
+    else:
+        st = workloads.anchor_state(b, g, cap, pc, d, seed=seed, fill_pending=fill)
+    gen = torch.Generator().manual_seed(seed + 1)
+    q = torch.randn(b, length, h, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, length, g, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, length, g, d, generator=gen).to(torch.bfloat16)
+    sc = torch.randn(b, length, g, generator=gen)
+    sc[:, 1::4] = sc[:, ::4][:, : sc[:, 1::4].shape[1]]      # score ties, broken by position
+    valid = (torch.rand(b, length, generator=gen) < 0.75) if holes else None
+    o_state = _oracle_state(st)
+    want = ref.sequence(q, k, v, sc, valid, chunk, o_state)
+    dev_state = _to(st, gpu)
+    got = im.sequence(q.to(gpu), k.to(gpu), v.to(gpu), sc.to(gpu), None if valid is None else valid.to(gpu), chunk,
+                      dev_state)
+    torch.cuda.synchronize()
+    assert got.shape == q.shape and got.dtype == q.dtype
+    _assert_state_equal(dev_state, o_state)
+    assert rel_err(got, want) <= 1e-2, rel_err(got, want)
+    if valid is not None:
+        assert not got.cpu()[~valid].any()
+
+
+def test_sequence_then_decode_continues(gpu):
+    """A prefill continuation followed by decode pushes leaves the same state
+    as the oracle doing the same, so the two paths hand over cleanly."""
+    b, g, h, cap, pc, chunk, d = 3, 2, 8, 64, 8, 8, 128
+    st = workloads.anchor_state(b, g, cap, pc, d, seed=41, fill_pending=6)
+    gen = torch.Generator().manual_seed(42)
+    q = torch.randn(b, 21, h, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, 21, g, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, 21, g, d, generator=gen).to(torch.bfloat16)
+    sc = torch.randn(b, 21, g, generator=gen)
+    o_state = _oracle_state(st)
+    ref.sequence(q, k, v, sc, None, chunk, o_state)
+    dev_state = _to(st, gpu)
+    im.sequence(q.to(gpu), k.to(gpu), v.to(gpu), sc.to(gpu), None, chunk, dev_state)
+    torch.cuda.synchronize()
+    _assert_state_equal(dev_state, o_state)
+    _drive_from(gpu, dev_state, o_state, 12, chunk, seed=43)
+
+
+def _drive_from(gpu, dev_state, o_state, steps, chunk, seed):
+    b, g, d = o_state.count.shape[0], o_state.keys.shape[1], o_state.keys.shape[3]
+    gen = torch.Generator().manual_seed(seed)
+    for _ in range(steps):
+        key = torch.randn(b, 1, g, d, generator=gen).to(o_state.keys.dtype)
+        val = torch.randn(b, 1, g, d, generator=gen).to(o_state.keys.dtype)
+        sc = torch.randn(b, 1, g, generator=gen)
+        active = torch.ones(b, dtype=torch.bool)
+        im.commit_decode(key.to(gpu), val.to(gpu), sc.to(gpu), active.to(gpu), chunk, dev_state)
+        ref.commit_decode(key, val, sc, active, chunk, o_state)
+        torch.cuda.synchronize()
+        live = o_state.positions >= 0
+        for name in ("scores", "positions", "count", "total"):
+            assert torch.equal(getattr(dev_state, name).cpu(), getattr(o_state, name)), name
+        assert torch.equal(dev_state.keys.cpu()[live], o_state.keys[live])

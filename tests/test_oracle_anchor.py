@@ -201,3 +201,70 @@ def test_indexed_read_closed_forms():
         logit = (q[0, 0, t, 0] @ k[0, 5, 0]).item() / math.sqrt(8)
         p = math.exp(logit) / (math.exp(logit) + 1.0)
         assert torch.allclose(out[0, 0, t, 0], p * v[0, 5, 0], atol=1e-12)
+
+
+def _warm_state(b, g, cap, pc, chunk, d, steps, gen, dtype=torch.float32):
+    """A state after ``steps`` decode pushes (random activity), so it carries
+    committed slots, a partial pending chunk and per-row totals."""
+    st = MemoryState.empty(b, g, cap, pc, d, dtype=dtype)
+    for _ in range(steps):
+        k = torch.randn(b, 1, g, d, generator=gen).to(dtype)
+        v = torch.randn(b, 1, g, d, generator=gen).to(dtype)
+        sc = torch.randn(b, 1, g, generator=gen)
+        act = torch.rand(b, generator=gen) < 0.8
+        anchor.commit_decode(k, v, sc, act, chunk, st)
+    return st
+
+
+def _token_by_token(query, key, value, scores, valid, chunk, st):
+    """The decode sequence a prefill replaces: read the committed slots, then
+    push (and commit on a full chunk), one token at a time."""
+    b, length = query.shape[:2]
+    act = torch.ones(b, length, dtype=torch.bool) if valid is None else valid
+    reads = []
+    for t in range(length):
+        reads.append(anchor.committed_read(query[:, t:t + 1], st)[:, 0])
+        anchor.commit_decode(key[:, t:t + 1], value[:, t:t + 1], scores[:, t:t + 1], act[:, t], chunk, st)
+    return torch.stack(reads, 1) * act[..., None, None].to(query.dtype)
+
+
+def assert_same_state(a: MemoryState, b: MemoryState):
+    """Scores, positions, count and total bit-equal; key / value rows equal
+    wherever a slot holds a token (a slot with no token is zero on one path
+    and a copy of row 0 on the other, and is never read)."""
+    assert torch.equal(a.count, b.count) and torch.equal(a.total, b.total)
+    assert torch.equal(a.positions, b.positions)
+    assert torch.equal(a.scores, b.scores)
+    live = a.positions >= 0
+    assert torch.equal(a.keys[live], b.keys[live]) and torch.equal(a.values[live], b.values[live])
+    pend = torch.arange(a.pending_keys.shape[2])[None, None] < a.count[:, None, None]
+    pend = pend.expand(a.pending_scores.shape)
+    assert torch.equal(a.pending_keys[pend], b.pending_keys[pend])
+    assert torch.equal(a.pending_values[pend], b.pending_values[pend])
+    assert torch.equal(a.pending_scores[pend], b.pending_scores[pend])
+
+
+@pytest.mark.parametrize("seed,cap,chunk,pc,length,warm,holes", [
+    (0, 8, 4, 4, 13, 0, False),      # fresh state, several blocks, a partial tail
+    (1, 8, 4, 6, 13, 7, False),      # old pending tokens open the first block; pending capacity > chunk
+    (2, 6, 3, 3, 2, 5, False),       # shorter than one block
+    (3, 8, 4, 4, 17, 9, True),       # invalid tokens inside the chunk
+    (4, 16, 8, 8, 40, 21, True),
+    (5, 4, 4, 4, 8, 3, False),       # ends exactly on a block boundary
+])
+def test_sequence_equals_token_by_token(seed, cap, chunk, pc, length, warm, holes):
+    gen = torch.Generator().manual_seed(seed)
+    b, g, h, d = 3, 2, 4, 16
+    st = _warm_state(b, g, cap, pc, chunk, d, warm, gen)
+    q = torch.randn(b, length, h, d, generator=gen)
+    k = torch.randn(b, length, g, d, generator=gen)
+    v = torch.randn(b, length, g, d, generator=gen)
+    sc = torch.randn(b, length, g, generator=gen)
+    sc[0, ::3] = sc[0, 1]                   # ties broken by position
+    valid = (torch.rand(b, length, generator=gen) < 0.7) if holes else None
+    ref_state = st.clone()
+    want = _token_by_token(q, k, v, sc, valid, chunk, ref_state)
+    got_state = st.clone()
+    got = anchor.sequence(q, k, v, sc, valid, chunk, got_state)
+    assert torch.allclose(got, want, rtol=1e-5, atol=1e-6), (got - want).abs().max()
+    assert_same_state(got_state, ref_state)

@@ -295,14 +295,6 @@ constexpr int kCommitThreads = 512;
 constexpr int kMaxCand = 2048;
 constexpr int kMaxPieces = 16;  // 16-byte pieces per thread per tensor: 128 KiB per (row, group)
 
-// Order-preserving 32-bit key of an fp32 score (bigger score -> bigger key);
-// -0.0 is mapped to +0.0 first so the two compare equal.
-__device__ __forceinline__ uint32_t score_key(float x) {
-  if (x == 0.f) x = 0.f;
-  const uint32_t u = __float_as_uint(x);
-  return (u & 0x80000000u) ? ~u : (u ^ 0x80000000u);
-}
-
 // Copy `n` bytes (multiple of 16) between two 16-byte aligned rows.
 __device__ __forceinline__ void copy_row16(void* dst, const void* src, int n, int lane, int lanes) {
   const uint4* s = static_cast<const uint4*>(src);
@@ -389,8 +381,7 @@ __global__ void __launch_bounds__(kCommitThreads) anchor_commit_kernel(CommitArg
       sc = n - KC == cnt ? new_score : ps[n - KC];
       p = static_cast<int32_t>(base_pos + (n - KC));
     }
-    const uint32_t pkey = p >= 0 ? static_cast<uint32_t>(p) : 0x7fffffffu;
-    ckey[n] = (static_cast<uint64_t>(~score_key(sc)) << 32) | pkey;
+    ckey[n] = topk_key(sc, p);
     cscore[n] = sc;
     cpos[n] = p;
   }

@@ -151,4 +151,20 @@ __device__ __forceinline__ float wave_max(float x) {
 
 inline bool is_float_dtype(int dt) { return dt == YH_F32 || dt == YH_BF16 || dt == YH_F16; }
 
+// ---- anchor-memory Top-K ordering ---------------------------------------------
+// Order-preserving 32-bit key of an fp32 score (bigger score -> bigger key);
+// -0.0 is mapped to +0.0 first so the two compare equal.
+__device__ __forceinline__ uint32_t score_key(float x) {
+  if (x == 0.f) x = 0.f;
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u ^ 0x80000000u);
+}
+// Candidate key whose ascending order is the Top-K order: score descending,
+// then position ascending with invalid (negative) positions last.  Equal keys
+// are broken by candidate index, which only ever separates invalid entries.
+__device__ __forceinline__ uint64_t topk_key(float score, int32_t position) {
+  const uint32_t pkey = position >= 0 ? static_cast<uint32_t>(position) : 0x7fffffffu;
+  return (static_cast<uint64_t>(~score_key(score)) << 32) | pkey;
+}
+
 }  // namespace yh

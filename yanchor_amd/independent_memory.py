@@ -5,7 +5,9 @@ The reference imports this module through ``_cuda_module('independent_memory')``
 ``indexed_gqa(query, key, value, references)`` (prefill),
 ``committed_gqa(query, state, indices)`` and
 ``commit_decode(key, value, scores, active, chunk, state, indices)``
-(runtime/model/independent_memory.py:177-201).  ``IndependentMemoryState``
+(runtime/model/independent_memory.py:177-201).  ``sequence`` is the stateful
+prefill continuation of IndependentGQAMemory._sequence
+(modeling_yanchor.py:178-275) on the GPU.  ``IndependentMemoryState``
 mirrors the reference dataclass (modeling_yanchor.py:80-120) field for field, so
 a state built by either side works with the other.
 """
@@ -208,6 +210,84 @@ def commit_decode(key, value, scores, active, chunk, state: IndependentMemorySta
            state.positions.data_ptr(), state.pending_keys.data_ptr(), state.pending_values.data_ptr(),
            state.pending_scores.data_ptr(), state.count.data_ptr(), state.total.data_ptr(), b, g, cap, pc,
            int(chunk), d, nb, rs, N.code(k), N.stream_of(k))
+
+
+def sequence(query, key, value, scores, valid, chunk, state: IndependentMemoryState):
+    """The anchor-memory read and write of a prefill chunk that continues
+    ``state``: IndependentGQAMemory._sequence with a state
+    (modeling_yanchor.py:178-275), IN PLACE on ``state``.
+
+    query ``[B, L, H, D]`` (normed, rotated); key, value ``[B, L, G, D]`` the
+    written key / value of every token (the reference computes them only for
+    the tokens that ever enter the memory; the others are never read);
+    scores ``[B, L, G]`` admission scores; valid ``None`` or bool ``[B, L]``
+    (valid tokens of a row are taken in order, as the reference's stable
+    argsort packs them).  Returns the memory read ``[B, L, H, D]``, zero at
+    invalid tokens.  Every token reads the memory committed before its block
+    (the old pending tokens open the first block), exactly what a
+    token-by-token ``committed_gqa`` / ``commit_decode`` sequence reads, and
+    the state ends as that sequence leaves it (slots that hold no token are
+    zeroed, as the reference's masked copies do)."""
+    nb, g, cap, pc, d = _check_state(state)
+    if query.ndim != 4 or key.ndim != 4:
+        raise ValueError("query must be [B, L, H, D] and key/value [B, L, G, D]")
+    b, length, h, qd = query.shape
+    if key.shape != (b, length, g, d) or value.shape != key.shape or qd != d:
+        raise ValueError("key/value must be [B, L, G, D] matching the memory")
+    if scores.shape != (b, length, g):
+        raise ValueError("scores must be [B, L, G]")
+    if nb != b:
+        raise ValueError("the memory state must have one row per batch row")
+    if valid is not None and valid.shape != (b, length):
+        raise ValueError("valid must be [B, L]")
+    c = int(chunk)
+    if not 1 <= c <= pc:
+        raise ValueError(f"chunk {chunk} must lie in [1, {pc}]")
+    if query.dtype != state.keys.dtype or key.dtype != state.keys.dtype or value.dtype != state.keys.dtype:
+        raise ValueError("query/key/value must match the memory dtype")
+    for f in fields(state):
+        if not getattr(state, f.name).is_contiguous():
+            raise ValueError(f"memory state field {f.name} must be contiguous")
+    N.require_device(query, key, value, scores, valid, state.keys)
+    dev = query.device
+    bi = torch.arange(b, device=dev)[:, None]
+    if valid is None:
+        order = None
+        q, k, v, sc = query, key, value, scores
+        counts = torch.full((b,), length, device=dev, dtype=torch.long)
+    else:
+        order = valid.long().argsort(dim=1, descending=True, stable=True)
+        q, k, v, sc = (x[bi, order] for x in (query, key, value, scores))
+        counts = valid.sum(1)
+    blocks = -(-length // c) + 1                  # extent = ceil((L + C) / C) * C
+    extent = blocks * c
+    at = torch.arange(extent, device=dev)[None]
+    old = state.count[:, None]
+    select = torch.where(at < old, at, c + at - old).clamp_max(c + length - 1)
+    q_ext = torch.cat((q.new_zeros(b, c, h, d), q), 1)[bi, select].contiguous()
+    src_k = torch.cat((state.keys.transpose(1, 2), state.pending_keys[:, :, :c].transpose(1, 2), k), 1).contiguous()
+    src_v = torch.cat((state.values.transpose(1, 2), state.pending_values[:, :, :c].transpose(1, 2), v),
+                      1).contiguous()
+    n_src = cap + c + length
+    block_refs = torch.empty(b, blocks, g, cap, device=dev, dtype=torch.int32)
+    final_refs = torch.empty(b, g, cap, device=dev, dtype=torch.int32)
+    pending_refs = torch.empty(b, g, pc, device=dev, dtype=torch.int32)
+    sc = sc.to(torch.float32).contiguous()
+    counts = counts.to(torch.long).contiguous()
+    st = N.stream_of(query)
+    N.call("yh_anchor_prefix", sc.data_ptr(), counts.data_ptr(), state.scores.data_ptr(),
+           state.positions.data_ptr(), state.pending_scores.data_ptr(), state.count.data_ptr(),
+           state.total.data_ptr(), block_refs.data_ptr(), final_refs.data_ptr(), pending_refs.data_ptr(), b, length,
+           g, cap, pc, c, blocks, st)
+    read = indexed_gqa(q_ext.view(b, blocks, c, h, d), src_k, src_v, block_refs).flatten(1, 2)
+    out = read[bi, (old + torch.arange(length, device=dev)[None]).clamp_max(extent - 1)]
+    if order is not None:
+        out = out[bi, order.argsort(1)] * valid[..., None, None].to(out.dtype)
+    N.call("yh_anchor_sequence_commit", src_k.data_ptr(), src_v.data_ptr(), final_refs.data_ptr(),
+           pending_refs.data_ptr(), counts.data_ptr(), state.keys.data_ptr(), state.values.data_ptr(),
+           state.pending_keys.data_ptr(), state.pending_values.data_ptr(), state.count.data_ptr(),
+           state.total.data_ptr(), b, n_src, length, g, cap, pc, c, d, N.code(src_k), st)
+    return out
 
 
 def ring_decode_attention(query, keys, values, positions, indices=None):

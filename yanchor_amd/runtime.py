@@ -66,6 +66,21 @@ class ModelConfig:
 # hot-path operations: the HIP kernels (default) -- a CPU restatement can be
 # injected for a baseline run, nothing here imports one.
 
+def _token_by_token_sequence(ops, q, key, value, scores, valid, chunk, state):
+    """The decode read / commit sequence a prefill chunk stands for:
+    q [B, L, H, D], key / value [B, L, G, D], scores [B, L, G]."""
+    b, length = q.shape[:2]
+    act = torch.ones(b, length, dtype=torch.bool, device=q.device) if valid is None else valid
+    reads = []
+    for t in range(length):
+        reads.append(ops.memory_read(q[:, t:t + 1].contiguous(), state)[:, 0])
+        ops.memory_commit(key[:, t:t + 1].contiguous(), value[:, t:t + 1].contiguous(), scores[:, t:t + 1],
+                          act[:, t].contiguous(), chunk, state)
+    if not reads:
+        return q.new_zeros(q.shape)
+    return torch.stack(reads, 1) * act[..., None, None].to(q.dtype)
+
+
 class HipOps:
     """The package's HIP kernels behind the reference's call signatures."""
 
@@ -133,6 +148,14 @@ class HipOps:
 
     def memory_commit(self, key, value, scores, active, chunk, state):
         self.mem.commit_decode(key, value, scores, active, chunk, state)
+
+    def memory_sequence(self, q, key, value, scores, valid, chunk, state):
+        """Prefill read + write continuing ``state`` (_sequence).  The block
+        kernels take 16-bit K/V; fp32 memories run the decode kernels token by
+        token, which read and leave the same."""
+        if q.dtype in (torch.bfloat16, torch.float16):
+            return self.mem.sequence(q, key, value, scores, valid, chunk, state)
+        return _token_by_token_sequence(self, q, key, value, scores, valid, chunk, state)
 
     def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty):
         return self.ik.sample_top20_counter(logits, attempt_ids, steps, seed=seed, temperature=temperature,
@@ -493,16 +516,10 @@ class Model:
                 tmp.ring_k[i][:, :, :T] = k.transpose(1, 2)
                 tmp.ring_v[i][:, :, :T] = v.transpose(1, 2)
                 tmp.ring_pos[i][:, :, :T] = pos.to(torch.int32)
-                # anchor memory, token by token: the decode read / commit sequence
-                # leaves the same state and outputs as the reference's prefill path
+                # anchor memory: the block-wise prefill read and write (_sequence)
                 mq, mgate, mk, mv, msc = self._memory_qkvs(L, h, cs, sn)
-                valid = torch.ones(R, dtype=torch.bool, device=dev)
-                reads = []
-                for t in range(T):
-                    reads.append(self.ops.memory_read(mq[:, t:t + 1].contiguous(), tmp.memory[i])[:, 0])
-                    self.ops.memory_commit(mk[:, t:t + 1].contiguous(), mv[:, t:t + 1].contiguous(),
-                                           msc[:, t:t + 1], valid, c.memory_chunk, tmp.memory[i])
-                read = torch.stack(reads, 1)
+                read = self.ops.memory_sequence(mq.contiguous(), mk.contiguous(), mv, msc.float(), None,
+                                                c.memory_chunk, tmp.memory[i])
                 mem_out = F.linear((read * mgate[..., None].to(read.dtype)).reshape(R, T, -1), L["m_o"])
                 h = h + out + mem_out
             h = h + self._mlp(L, rms_norm(h, L["post_norm"], c.rms_eps))
