@@ -170,7 +170,10 @@ class _OracleOps:
         self.glue = TorchGlue
         for name in ("rmsnorm", "gdn_prep", "gated_rmsnorm", "silu_mul", "head_norm_rope"):
             setattr(self, name, getattr(TorchGlue, name))
-        self.linear = torch.nn.functional.linear
+
+    @staticmethod
+    def linear(x, w, packed=None):
+        return torch.nn.functional.linear(x, w)
 
     def gdn_decode(self, q, k, v, g, beta, state):
         o, st = self.gdn_ref.recurrent_gated_delta_rule(q, k, v, g, beta, state, dtype=torch.float32)

@@ -274,6 +274,27 @@ int yh_linear(const void* x, int64_t x_stride, const void* w, void* out, int64_t
 int yh_linear_split(int64_t M, int64_t N, int64_t K);
 int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split_k);
 
+/*
+ * The same projection with the weights repacked once into MFMA fragment order
+ * (no counterpart in the reference, which keeps nn.Linear weights row-major;
+ * the packed copy serves the decode step, the row-major one everything else).
+ *
+ * yh_linear_pack: w [N, K] bf16 row-major -> packed [N * K] bf16 with
+ *   packed[((T * K/32 + kb) * 64 + l) * 8 + e] = w[16 T + l % 16][32 kb + 8 (l / 16) + e]
+ *   (column tile T of 16 outputs, K block kb of 32; lane l of a 16x16x32 MFMA
+ *   B operand).  N % 16 == 0, K % 32 == 0.
+ * yh_linear_packed: out[M, N] = x[M, K] . W^T from the packed weights; split_k
+ *   slices K in whole 128-wide phases (yh_linear_packed_split gives the
+ *   library's choice); with more than one slice the workspace must hold
+ *   split_k * M * N * 4 bytes (16-byte aligned) and the partial sums are added
+ *   in a fixed order.  Requirements: 0 <= M <= 128, N % 16 == 0, K % 128 == 0.
+ */
+int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, yh_stream_t stream);
+int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride, int64_t M,
+                     int64_t N, int64_t K, int64_t split_k, void* workspace, int64_t workspace_bytes,
+                     yh_stream_t stream);
+int yh_linear_packed_split(int64_t M, int64_t N, int64_t K);
+
 /* Sampling semantics of yh_topk_sample. */
 enum yh_sample_mode {
   /* _qwen35_top20_counter_sample_kernel (runtime/model/inference_kernels.py:

@@ -176,3 +176,46 @@ def test_linear_strided_rows(gpu):
     x = base[:, 512:]                                    # row stride 3072, 1024-byte offset
     w = rnd(128, 2560, dev=gpu, seed=6)
     ulp_check(layers.linear(x, w), (x.float() @ w.float().t()).to(torch.bfloat16))
+
+
+def test_pack_layout(gpu):
+    """Packed order: column tile of 16, K block of 32, lane l = (K quarter, column)."""
+    n, k = 48, 256
+    w = rnd(n, k, dev=gpu, seed=30)
+    pw = layers.PackedWeight(w)
+    want = w.view(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+    assert torch.equal(pw.data, want)
+    with pytest.raises(ValueError):
+        layers.PackedWeight(rnd(32, 96, dev=gpu, seed=31))           # K not a multiple of 128
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 2560, 4096), (128, 19456, 2560), (128, 2560, 9728), (1, 16, 128),
+                                   (37, 192, 384), (64, 2048, 2560), (100, 2576, 2560), (17, 4096, 1024)])
+def test_linear_packed_matches_fp32_reference(gpu, m, n, k):
+    """fp32-accumulated product rounded once to bf16, as F.linear (1 bf16 ulp)."""
+    x = rnd(m, k, dev=gpu, seed=m + n + 1)
+    w = rnd(n, k, dev=gpu, scale=0.02, seed=k + 1)
+    ref = (x.float() @ w.float().t()).to(torch.bfloat16)
+    got = layers.linear(x, layers.PackedWeight(w))
+    ulp_check(got, ref, max_frac=0.05)
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 7, 32])
+def test_linear_packed_split_is_deterministic(gpu, split):
+    x = rnd(128, 4096, dev=gpu, seed=7)
+    pw = layers.PackedWeight(rnd(2560, 4096, dev=gpu, scale=0.02, seed=8))
+    a = layers.linear(x, pw, split_k=split)
+    layers.linear(rnd(64, 1024, dev=gpu, seed=9), layers.PackedWeight(rnd(640, 1024, dev=gpu, seed=10)), split_k=4)
+    b = layers.linear(x, pw, split_k=split)
+    assert torch.equal(a, b)
+    ulp_check(a, (x.float() @ rnd(2560, 4096, dev=gpu, scale=0.02, seed=8).float().t()).to(torch.bfloat16),
+              max_frac=0.05)
+
+
+def test_linear_packed_strided_rows_and_empty(gpu):
+    base = rnd(16, 3072, dev=gpu, seed=11)
+    x = base[:, 512:]                                    # row stride 3072, 1024-byte offset
+    w = rnd(128, 2560, dev=gpu, seed=12)
+    pw = layers.PackedWeight(w)
+    ulp_check(layers.linear(x, pw), (x.float() @ w.float().t()).to(torch.bfloat16))
+    assert layers.linear(torch.empty(0, 2560, device=gpu, dtype=torch.bfloat16), pw).shape == (0, 128)

@@ -39,6 +39,8 @@ SIGNATURES: dict[str, list] = {
                                   _i64, _i64, _i32, _p],
     "yh_indexed_gqa": [_p, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_linear": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "yh_linear_pack": [_p, _p, _i64, _i64, _p],
+    "yh_linear_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "yh_topk_sample": [_p, _i32, _i64, _p, _i64, _f32, _p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32,
                        _i64, _f32, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "yh_presence_penalty": [_p, _p, _i64, _f32, _p],
@@ -60,6 +62,7 @@ SIGNATURES: dict[str, list] = {
 PLAIN: dict[str, tuple] = {
     "yh_topk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "yh_linear_split": (_i32, [_i64, _i64, _i64]),
+    "yh_linear_packed_split": (_i32, [_i64, _i64, _i64]),
     "yh_gdn_chunk_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "yh_linear_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "yh_topk_segments": (None, [_i64, _i64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),

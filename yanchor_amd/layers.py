@@ -127,34 +127,62 @@ _linear_ws: dict = {}
 
 
 def _linear_workspace(device, nbytes):
-    """Per-device zero-filled split-K workspace, grown on demand (the kernels
-    leave its arrival counters at zero after every call)."""
+    """Per-device split-K workspace, grown on demand (every partial the reduce
+    reads is written first, so it needs no clearing)."""
     key = device.index if device.index is not None else torch.cuda.current_device()
     ws = _linear_ws.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _linear_ws[key] = ws
     return ws
 
 
+class PackedWeight:
+    """A projection weight ``[N, K]`` bf16 repacked once into MFMA fragment
+    order (yh_linear_pack), for the decode projection kernel: ``linear(x, pw)``
+    takes it in place of the row-major weight.  N % 16 == 0, K % 128 == 0."""
+
+    def __init__(self, w):
+        _bf16(w)
+        if w.ndim != 2 or w.shape[0] % 16 or w.shape[1] % 128:
+            raise ValueError("packed weights need [N, K] with N % 16 == 0 and K % 128 == 0")
+        N.require_device(w)
+        self.shape = tuple(w.shape)
+        self.dtype = w.dtype
+        self.data = torch.empty(w.numel(), dtype=w.dtype, device=w.device)
+        wc = w.contiguous()
+        N.call("yh_linear_pack", wc.data_ptr(), self.data.data_ptr(), self.shape[0], self.shape[1], N.stream_of(wc))
+
+    @staticmethod
+    def fits(w):
+        return (w.dtype == torch.bfloat16 and w.ndim == 2 and w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0)
+
+
 def linear(x, w, split_k=None):
     """out = x . w^T for a decode batch (x [M, K] bf16 with M <= 128, w [N, K]
-    bf16): torch.nn.functional.linear without bias on the skinny-projection
-    kernel.  The split-K workspace is cached per device: concurrent calls on
-    different streams of one device must not overlap."""
-    _bf16(x, w)
-    if x.ndim != 2 or w.ndim != 2 or x.shape[1] != w.shape[1]:
+    bf16 or a PackedWeight): torch.nn.functional.linear without bias on the
+    skinny-projection kernels.  The split-K workspace is cached per device:
+    concurrent calls on different streams of one device must not overlap."""
+    packed = isinstance(w, PackedWeight)
+    _bf16(x, w.data if packed else w)
+    n, kw = w.shape
+    if x.ndim != 2 or (not packed and w.ndim != 2) or x.shape[1] != kw:
         raise ValueError("linear expects x [M, K] and w [N, K]")
     m, k = x.shape
-    n = w.shape[0]
     if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
-    w = w.contiguous()
-    dev = N.require_device(x, w)
+    wt = w.data if packed else w.contiguous()
+    dev = N.require_device(x, wt)
     out = torch.empty(m, n, dtype=x.dtype, device=dev)
-    s = int(split_k) if split_k is not None else N.lib().yh_linear_split(m, n, k)
-    nbytes = N.lib().yh_linear_workspace_bytes(m, n, k, s)
+    if packed:
+        s = int(split_k) if split_k is not None else N.lib().yh_linear_packed_split(m, n, k)
+        nbytes = s * m * n * 4 if s > 1 else 0
+        entry = "yh_linear_packed"
+    else:
+        s = int(split_k) if split_k is not None else N.lib().yh_linear_split(m, n, k)
+        nbytes = N.lib().yh_linear_workspace_bytes(m, n, k, s)
+        entry = "yh_linear"
     ws = _linear_workspace(dev, nbytes) if nbytes else None
-    N.call("yh_linear", x.data_ptr(), x.stride(0), w.data_ptr(), out.data_ptr(), n, m, n, k, s, N.ptr(ws),
+    N.call(entry, x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), n, m, n, k, s, N.ptr(ws),
            0 if ws is None else ws.numel(), N.stream_of(x))
     return out

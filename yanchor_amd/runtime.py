@@ -119,15 +119,29 @@ class HipOps:
             return TorchGlue.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
         return self.layers.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
 
-    def linear(self, x, w):
-        """Decode projections: the skinny split-K kernel where it beats the
-        library GEMM on MI355X (bf16, <= 128 rows, output width 1024 ... 4096,
-        K >= 2048: the GDN / attention output, MLP down and memory-writer
-        projections), torch (hipBLASLt) otherwise."""
-        n, k = w.shape
-        if (x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128 and 1024 <= n <= 4096 and n % 64 == 0
-                and k % 64 == 0 and k >= 2048):
-            return self.layers.linear(x, w)
+    # Decode projections that run on the packed-weight kernel: where it beats
+    # the library GEMM on MI355X at 128 rows (the MLP, the GDN / attention /
+    # memory output and memory-writer down projections, the lm_head).  The
+    # q/k/v/z/b/a-sized projections (N ~ 9k-12k) and the memory k/v (N = 2048)
+    # stay on hipBLASLt, which is as fast or faster there.
+    PACKED = ("mlp_gate_up", "mlp_down", "w_out", "w_o", "m_o", "writer_down")
+
+    def prepare(self, model):
+        """Packed copies of the decode projection weights (``name + "@packed"``
+        in each layer dict, ``model.lm_head_packed``); the row-major weights
+        stay for prefill."""
+        for L in model.layers:
+            for name in self.PACKED:
+                if name in L and self.layers.PackedWeight.fits(L[name]):
+                    L[name + "@packed"] = self.layers.PackedWeight(L[name])
+        if self.layers.PackedWeight.fits(model.lm_head):
+            model.lm_head_packed = self.layers.PackedWeight(model.lm_head)
+
+    def linear(self, x, w, packed=None):
+        """out = x . w^T: the packed-weight kernel for a decode batch (bf16,
+        <= 128 rows) when a packed copy exists, torch (hipBLASLt) otherwise."""
+        if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128:
+            return self.layers.linear(x, packed)
         return F.linear(x, w)
 
     def gdn_decode(self, q, k, v, g, beta, state):
@@ -313,6 +327,10 @@ class Model:
                          gnorm=torch.ones(c.gdn_dv, device=self.device, dtype=dtype),
                          w_out=w(c.hidden, c.gdn_heads_v * c.gdn_dv))
             self.layers.append(L)
+        self.lm_head_packed = None
+        prepare = getattr(self.ops, "prepare", None)
+        if prepare is not None:
+            prepare(self)
         self._alloc_caches()
 
     # ---------------- caches ----------------
@@ -346,7 +364,9 @@ class Model:
 
     # ---------------- layers ----------------
     def _mlp(self, L, x):
-        return self.ops.linear(self.ops.silu_mul(self.ops.linear(x, L["mlp_gate_up"])), L["mlp_down"])
+        ops = self.ops
+        return ops.linear(ops.silu_mul(ops.linear(x, L["mlp_gate_up"], L.get("mlp_gate_up@packed"))), L["mlp_down"],
+                          L.get("mlp_down@packed"))
 
     def _gdn_split(self, L, proj):
         c = self.cfg
@@ -369,7 +389,7 @@ class Model:
         o = ops.gdn_decode(q.view(B, 1, c.gdn_heads_k, c.gdn_dk), k.view(B, 1, c.gdn_heads_k, c.gdn_dk),
                            v.view(B, 1, hv, dv), g[:, None], beta[:, None], self.gdn_state[i])
         y = ops.gated_rmsnorm(o.view(B, hv, dv), proj[:, c.conv_dim: c.conv_dim + vd], L["gnorm"], c.rms_eps)
-        return self.ops.linear(y, L["w_out"])
+        return self.ops.linear(y, L["w_out"], L.get("w_out@packed"))
 
     def _attn_project(self, L, x, cos, sin):
         c = self.cfg
@@ -415,7 +435,7 @@ class Model:
             (qn.float() * L["read_gate_w"]).sum(-1) / math.sqrt(D) + L["read_gate_b"])
         q = ops.head_norm_rope(mq, L["m_q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
         scores = ops.linear(F.silu(proj[:, qd: qd + ad]).float(), L["adm_up"])
-        zz = u + ops.linear(ops.silu_mul(proj[:, qd + ad:]), L["writer_down"])
+        zz = u + ops.linear(ops.silu_mul(proj[:, qd + ad:]), L["writer_down"], L.get("writer_down@packed"))
         kv = ops.linear(zz, L["m_kv"])
         key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
                                  c.rms_eps)
@@ -439,12 +459,12 @@ class Model:
         self.ring_v[i][rows, :, slot] = proj[:, hq + KVH * D:].view(B, KVH, D)
         self.ring_pos[i][rows, :, slot] = positions.to(torch.int32)[:, None]
         att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i])
-        out = ops.linear((att[:, 0] * torch.sigmoid(qg[..., D:])).reshape(B, -1), L["w_o"])
+        out = ops.linear((att[:, 0] * torch.sigmoid(qg[..., D:])).reshape(B, -1), L["w_o"], L.get("w_o@packed"))
         mq, mgate, mk, mv, mscores = self._memory_decode(L, hidden, cos, sin)
         read = ops.memory_read(mq[:, None], self.memory[i])
         ops.memory_commit(mk[:, None], mv[:, None], mscores[:, None], valid, c.memory_chunk, self.memory[i])
         read = read[:, 0] * valid[:, None, None].to(read.dtype)
-        mem_out = ops.linear((read * mgate[..., None].to(read.dtype)).reshape(B, -1), L["m_o"])
+        mem_out = ops.linear((read * mgate[..., None].to(read.dtype)).reshape(B, -1), L["m_o"], L.get("m_o@packed"))
         return out + mem_out
 
     def decode_step(self, tokens, positions, valid):
@@ -464,7 +484,7 @@ class Model:
             xn, h = ops.rmsnorm(delta, L["post_norm"], c.rms_eps, residual=h)
             nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
             xn, h = ops.rmsnorm(self._mlp(L, xn), nxt, c.rms_eps, residual=h)
-        return ops.linear(xn, self.lm_head).float()
+        return ops.linear(xn, self.lm_head, self.lm_head_packed).float()
 
     # ---------------- prefill ----------------
     def prefill(self, prompts):
