@@ -168,29 +168,33 @@ class _OracleOps:
         from yanchor_amd.runtime import TorchGlue
         self.gdn_ref, self.anchor, self.sampling, self.slots = gdn, anchor, sampling, slots
         self.glue = TorchGlue
-        for name in ("rmsnorm", "gdn_prep", "gated_rmsnorm", "silu_mul", "head_norm_rope"):
+        from yanchor_amd.runtime import gate_read
+        self.gate_read = gate_read
+        for name in ("rmsnorm", "gdn_prep", "gated_rmsnorm", "silu_mul", "head_norm_rope", "ring_write",
+                     "memory_prologue"):
             setattr(self, name, getattr(TorchGlue, name))
 
     @staticmethod
-    def linear(x, w, packed=None):
-        return torch.nn.functional.linear(x, w)
+    def linear(x, w, packed=None, residual=None):
+        out = torch.nn.functional.linear(x, w)
+        return out if residual is None else out + residual
 
     def gdn_decode(self, q, k, v, g, beta, state):
         o, st = self.gdn_ref.recurrent_gated_delta_rule(q, k, v, g, beta, state, dtype=torch.float32)
         state.copy_(st)
         return o.to(q.dtype)
 
-    def window_attend(self, q, keys, values, positions):
+    def window_attend(self, q, keys, values, positions, gate=None):
         b, _, h, d = q.shape
         g = keys.shape[1]
         qq = q[:, 0].reshape(b, g, h // g, d).float()
         logits = torch.matmul(qq, keys.float().transpose(-1, -2)) / math.sqrt(d)     # [B, G, R, W]
         logits = logits.masked_fill((positions < 0)[:, :, None, :], -math.inf)
         out = torch.matmul(logits.softmax(-1), values.float())
-        return out.reshape(b, 1, h, d).to(q.dtype)
+        return self.gate_read(out.reshape(b, 1, h, d).to(q.dtype), gate=gate)
 
-    def memory_read(self, q, state):
-        return self.anchor.committed_read(q, state, dtype=torch.float32)
+    def memory_read(self, q, state, valid=None, head_gate=None):
+        return self.gate_read(self.anchor.committed_read(q, state, dtype=torch.float32), valid, head_gate)
 
     def memory_commit(self, key, value, scores, active, chunk, state):
         self.anchor.commit_decode(key, value, scores, active, chunk, state)

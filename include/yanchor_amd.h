@@ -148,6 +148,28 @@ int yh_window_attend(const void* query, const void* keys, const void* values, co
                      int64_t n_state_rows, int dtype, yh_stream_t stream);
 
 /*
+ * yh_anchor_read / yh_window_attend with the decode layer's epilogue applied to
+ * the read (each product rounded to the dtype, as the torch ops that follow the
+ * read in the reference's decode layer):
+ *   anchor_read_gated:  out = (read * row_valid[b]) * head_gate[b, h]
+ *                       (modeling_yanchor.py:283-290 read, then the read gate
+ *                       of _query_scores 167-176 applied by the caller)
+ *   window_attend_gated: out = read * sigmoid(gate[b, h, :])  (the gated-q
+ *                       output of the SWA layer, inference_kernels.py:1899-1915)
+ * row_valid uint8 [B] (NULL = all valid); head_gate float [B, H] (NULL = 1);
+ * gate: rows gate_tok_stride, heads gate_head_stride elements apart, query dtype.
+ */
+int yh_anchor_read_gated(const void* query, const void* keys, const void* values, const int32_t* positions,
+                         const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t capacity,
+                         int64_t D, int64_t n_state_rows, int64_t keys_row_stride, int64_t values_row_stride,
+                         int64_t positions_row_stride, const uint8_t* row_valid, const float* head_gate, int dtype,
+                         yh_stream_t stream);
+int yh_window_attend_gated(const void* query, const void* keys, const void* values, const int32_t* positions,
+                           const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t window,
+                           int64_t D, int64_t n_state_rows, const void* gate, int64_t gate_tok_stride,
+                           int64_t gate_head_stride, int dtype, yh_stream_t stream);
+
+/*
  * Anchor memory, decode push and Top-K commit, IN PLACE on the memory state.
  *
  * Replaces commit_decode (_push_select, _gather_commit, _write_commit,
@@ -287,12 +309,15 @@ int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split
  *   slices K in whole 128-wide phases (yh_linear_packed_split gives the
  *   library's choice); with more than one slice the workspace must hold
  *   split_k * M * N * 4 bytes (16-byte aligned) and the partial sums are added
- *   in a fixed order.  Requirements: 0 <= M <= 128, N % 16 == 0, K % 128 == 0.
+ *   in a fixed order.  residual (NULL = none) [M, N] bf16, rows residual_stride
+ *   apart: out = bf16(bf16(x . W^T) + residual), the decode layers'
+ *   `z = x + proj(...)` adds (modeling_yanchor.py:159, 903-905).
+ *   Requirements: 0 <= M <= 128, N % 16 == 0, K % 128 == 0.
  */
 int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, yh_stream_t stream);
 int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride, int64_t M,
-                     int64_t N, int64_t K, int64_t split_k, void* workspace, int64_t workspace_bytes,
-                     yh_stream_t stream);
+                     int64_t N, int64_t K, const void* residual, int64_t residual_stride, int64_t split_k,
+                     void* workspace, int64_t workspace_bytes, yh_stream_t stream);
 int yh_linear_packed_split(int64_t M, int64_t N, int64_t K);
 
 /* Sampling semantics of yh_topk_sample. */
@@ -468,6 +493,38 @@ int yh_head_norm_rope(const void* x, int64_t x_tok_stride, int64_t x_head_stride
                       const float* sin, void* out, int64_t out_tok_stride, int64_t out_head_stride,
                       const int64_t* out_tok_index, int64_t N, int64_t H, int64_t D, int64_t rotary_dim, float eps,
                       yh_stream_t stream);
+
+/*
+ * The ring write of a decode token into the SWA cache: head h of key k is
+ * normed and rotated as yh_head_norm_rope and written to ring_k, the raw value
+ * head to ring_v and positions[n] to ring_pos, all at ring row rows[n]
+ * (rows[n] = n * H * window + positions[n] % window for a per-slot ring):
+ *   ring_k / ring_v [N, H, window, 128]: element rows[n] * 128 + h * window * 128 + d
+ *   ring_pos int32 [N, H, window]:       element rows[n] + h * window
+ * (the chrono ring write of runtime/model/inference_kernels.py:1828-1879 with
+ * the key path of the Qwen3.5 attention)
+ */
+int yh_ring_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride, const void* v, int64_t v_tok_stride,
+                  int64_t v_head_stride, const void* w, const float* cos, const float* sin, const int64_t* rows,
+                  const int64_t* positions, void* ring_k, void* ring_v, int32_t* ring_pos, int64_t N, int64_t H,
+                  int64_t window, int64_t D, int64_t rotary_dim, float eps, yh_stream_t stream);
+
+/*
+ * The anchor-memory read prologue of one decode token per row
+ * (IndependentGQAMemory._query_scores, modeling_yanchor.py:167-176), from the
+ * fused projection proj [B, >= feat_offset + A] bf16 whose first H * 128
+ * columns are the query heads and columns [feat_offset, feat_offset + A) the
+ * admission features:
+ *   q      = RoPE(RMSNorm_(1+w)(q_h))                       bf16 [B, H, 128]
+ *   gate   = tanh(read_scale) * 2 * sigmoid(<qn_h, gate_w_h> / sqrt(128) + gate_b)
+ *            (qn_h the normed, unrotated head as bf16)      float [B, H]
+ *   scores = bf16(silu(features)) . adm_up^T                float [B, G]
+ * read_scale, gate_b float [H]; gate_w float [H, 128]; adm_up float [G, A].
+ */
+int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t feat_offset, const void* q_norm_w,
+                       const float* cos, const float* sin, const float* read_scale, const float* gate_w,
+                       const float* gate_b, const float* adm_up, void* q, float* gate, float* scores, int64_t B,
+                       int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps, yh_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -226,3 +226,36 @@ def _drive_from(gpu, dev_state, o_state, steps, chunk, seed):
         for name in ("scores", "positions", "count", "total"):
             assert torch.equal(getattr(dev_state, name).cpu(), getattr(o_state, name)), name
         assert torch.equal(dev_state.keys.cpu()[live], o_state.keys[live])
+
+
+def test_read_gated_equals_read_then_gates(gpu):
+    """The fused gating epilogue is the torch gating of the plain read, bit for
+    bit (every product rounded to bf16 the same way)."""
+    from yanchor_amd.runtime import gate_read
+    st = _to(workloads.anchor_state(6, 2, 256, 64, 128, seed=70), gpu)
+    q = workloads.anchor_query(6, 8, 128, seed=71).to(gpu)
+    valid = torch.tensor([True, False, True, True, False, True], device=gpu)
+    hg = torch.rand(6, 8, device=gpu) * 2
+    plain = im.committed_gqa(q, st)
+    got = im.committed_gqa_gated(q, st, None, valid, hg)
+    assert torch.equal(got, gate_read(plain, valid, hg))
+    assert torch.equal(im.committed_gqa_gated(q, st, None, valid, None), gate_read(plain, valid))
+
+
+def test_window_attend_gated(gpu):
+    from yanchor_amd.runtime import gate_read
+    b, g, win, d, h = 4, 2, 128, 128, 8
+    gen = torch.Generator(device=gpu).manual_seed(80)
+    keys = torch.randn(b, g, win, d, device=gpu, generator=gen).to(torch.bfloat16)
+    vals = torch.randn(b, g, win, d, device=gpu, generator=gen).to(torch.bfloat16)
+    pos = torch.where(torch.rand(b, g, win, device=gpu, generator=gen) < 0.8,
+                      torch.arange(win, device=gpu, dtype=torch.int32), torch.tensor(-1, device=gpu, dtype=torch.int32))
+    q = torch.randn(b, 1, h, d, device=gpu, generator=gen).to(torch.bfloat16)
+    qg = torch.randn(b, h, 2 * d, device=gpu, generator=gen).to(torch.bfloat16)
+    gate = qg[..., d:]                                       # strided, as in the fused q | gate projection
+    got = im.ring_decode_attention(q, keys, vals, pos, gate=gate)
+    want = gate_read(im.ring_decode_attention(q, keys, vals, pos), gate=gate)
+    assert got.shape == want.shape
+    diff = (got.float() - want.float()).abs()
+    assert (diff <= want.float().abs() * 2.0 ** -7 * 1.0001 + 1e-30).all()
+    assert (got != want).float().mean().item() <= 0.01

@@ -219,3 +219,74 @@ def test_linear_packed_strided_rows_and_empty(gpu):
     pw = layers.PackedWeight(w)
     ulp_check(layers.linear(x, pw), (x.float() @ w.float().t()).to(torch.bfloat16))
     assert layers.linear(torch.empty(0, 2560, device=gpu, dtype=torch.bfloat16), pw).shape == (0, 128)
+
+
+def test_ring_write(gpu):
+    """Key heads normed + rotated, raw value heads and positions land in ring
+    slot positions % window of each row; nothing else moves."""
+    b, kvh, win, d = 6, 4, 16, 128
+    proj = rnd(b, 2 * kvh * d + 64, dev=gpu, seed=40)
+    k = proj[:, :kvh * d].view(b, kvh, d)
+    v = proj[:, kvh * d: 2 * kvh * d].view(b, kvh, d)
+    w = rnd(d, dev=gpu, scale=0.1, seed=41)
+    pos = torch.tensor([0, 5, 15, 16, 33, 1000], device=gpu)
+    cos, sin = rt.rope_tables(pos, rt.ModelConfig())
+    rows = torch.arange(b, device=gpu) * kvh * win + pos % win
+    ring = [rnd(b, kvh, win, d, dev=gpu, seed=42), rnd(b, kvh, win, d, dev=gpu, seed=43),
+            torch.randint(-1, 100, (b, kvh, win), device=gpu, dtype=torch.int32)]
+    ref = [t.clone() for t in ring]
+    layers.ring_write(k, v, w, cos, sin, rows, pos, *ring, 32, 1e-6)
+    TorchGlue.ring_write(k, v, w, cos, sin, rows, pos, *ref, 32, 1e-6)
+    touched = torch.zeros(b, kvh, win, dtype=torch.bool, device=gpu)
+    touched[torch.arange(b, device=gpu), :, pos % win] = True
+    assert torch.equal(ring[0][~touched], ref[0][~touched])
+    ulp_check(ring[0][touched], ref[0][touched])
+    assert torch.equal(ring[1], ref[1]) and torch.equal(ring[2], ref[2])
+
+
+@pytest.mark.parametrize("b", [1, 128])
+def test_memory_prologue(gpu, b):
+    """Query (normed, rotated), read gate and admission scores in one launch
+    against the torch formulation."""
+    cfg = rt.ModelConfig()
+    h, d, a = cfg.attn_heads, cfg.head_dim, cfg.admission_rank
+    proj = rnd(b, h * d + a + 512, dev=gpu, scale=2.0, seed=50)
+    w = rnd(d, dev=gpu, scale=0.1, seed=51)
+    pos = torch.randint(0, 5000, (b,), device=gpu)
+    cos, sin = rt.rope_tables(pos, cfg)
+    g = torch.Generator(device=gpu).manual_seed(52)
+    read_scale = torch.randn(h, device=gpu, generator=g)
+    gate_w = torch.randn(h, d, device=gpu, generator=g) * 0.2
+    gate_b = torch.randn(h, device=gpu, generator=g)
+    adm_up = torch.randn(cfg.kv_heads, a, device=gpu, generator=g) * 0.3
+    args = (proj, h, h * d, a, w, cos, sin, read_scale, gate_w, gate_b, adm_up, cfg.rotary_dim, 1e-6)
+    q, gate, scores = layers.memory_prologue(*args)
+    rq, rgate, rscores = TorchGlue.memory_prologue(*args)
+    # The normed heads agree to 1 bf16 ulp (fp32 sum order); RoPE mixes each
+    # rotary element with its partner, so a 1-ulp input difference moves the
+    # output by up to one input ulp even where the rotation cancels.
+    qn = TorchGlue.head_norm_rope(proj[:, : h * d].view(b, h, d), w, None, None, 0, 1e-6).float()
+    rd = cfg.rotary_dim
+    partner = torch.cat((qn[..., rd // 2: rd], qn[..., : rd // 2], torch.zeros_like(qn[..., rd:])), -1)
+    bound = rq.float().abs() * 2.0 ** -7 + (qn.abs() + partner.abs()) * 2.0 ** -7
+    bound[..., rd:] = rq.float()[..., rd:].abs() * 2.0 ** -7
+    assert ((q.float() - rq.float()).abs() <= bound * 1.0001 + 1e-30).all()
+    assert (q != rq).float().mean().item() <= 0.02
+    assert rel_err(gate, rgate) <= 1e-5 and rel_err(scores, rscores) <= 1e-5
+
+
+@pytest.mark.parametrize("split", [1, 4])
+def test_linear_packed_residual(gpu, split):
+    """out = bf16(x . W^T) + residual, the residual add fused into the store."""
+    x = rnd(128, 2560, dev=gpu, seed=60)
+    w = rnd(2560, 2560, dev=gpu, scale=0.02, seed=61)
+    base = rnd(128, 3072, dev=gpu, seed=62)
+    res = base[:, 256: 256 + 2560]                       # strided residual rows
+    got = layers.linear(x, layers.PackedWeight(w), split_k=split, residual=res)
+    prod = (x.float() @ w.float().t()).to(torch.bfloat16)
+    ref = prod + res
+    # the bf16 product may differ by 1 ulp (fp32 sum order); where the add
+    # cancels that ulp is large next to the sum
+    bound = (ref.float().abs() + prod.float().abs()) * 2.0 ** -7
+    assert ((got.float() - ref.float()).abs() <= bound * 1.0001 + 1e-30).all()
+    assert (got != ref).float().mean().item() <= 0.05

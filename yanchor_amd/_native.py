@@ -40,7 +40,14 @@ SIGNATURES: dict[str, list] = {
     "yh_indexed_gqa": [_p, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_linear": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "yh_linear_pack": [_p, _p, _i64, _i64, _p],
-    "yh_linear_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "yh_linear_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p],
+    "yh_ring_write": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                      _f32, _p],
+    "yh_memory_prologue": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                           _i64, _f32, _p],
+    "yh_anchor_read_gated": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p,
+                             _i32, _p],
+    "yh_window_attend_gated": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i32, _p],
     "yh_topk_sample": [_p, _i32, _i64, _p, _i64, _f32, _p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32,
                        _i64, _f32, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "yh_presence_penalty": [_p, _p, _i64, _f32, _p],

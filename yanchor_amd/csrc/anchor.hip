@@ -38,7 +38,35 @@ struct ReadArgs {
   int64_t n_rows;
   int64_t k_rs, v_rs, p_rs;  // row strides (elements) of keys, values, positions
   float scale;
+  // optional epilogue, in the order the decode layer applies it to the read:
+  //   x = 0 where row_valid[row] == 0; x *= head_gate[row, h];
+  //   x *= sigmoid(gate[row, h, d])   (every product rounded to the dtype)
+  const uint8_t* row_valid;   // [B]
+  const float* head_gate;     // [B, H]
+  const void* gate;           // rows gate_ts apart, heads gate_hs apart
+  int64_t gate_ts, gate_hs;
 };
+
+// A value rounded to the storage precision of DT (a bf16 / fp16 tensor op
+// rounds every intermediate it materialises).
+template <int DT>
+__device__ __forceinline__ float round_dt(float x) {
+  if constexpr (DT == YH_BF16) return bf16_to_f32(f32_to_bf16(x));
+  else if constexpr (DT == YH_F16) return f16_to_f32(f32_to_f16(x));
+  else return x;
+}
+
+template <int DT>
+__device__ __forceinline__ float read_epilogue(const ReadArgs& a, int row, int H, int head, int d, float x) {
+  if (a.row_valid && a.row_valid[row] == 0) return 0.f;
+  x = round_dt<DT>(x);
+  if (a.head_gate) x = round_dt<DT>(x * round_dt<DT>(a.head_gate[static_cast<int64_t>(row) * H + head]));
+  if (a.gate) {
+    const float gv = load_any(a.gate, row * a.gate_ts + head * a.gate_hs + d, DT);
+    x = round_dt<DT>(x * round_dt<DT>(1.f / (1.f + expf(-gv))));
+  }
+  return x;
+}
 
 // 8 consecutive elements of a bf16/fp16/fp32 row as floats (16 B for 2-byte
 // types, 2 x 16 B for fp32).
@@ -102,23 +130,32 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
   }
 }
 
-// One workgroup per (batch row, group), one pass over the committed slots.
-// Each wave takes 64-slot blocks: a ballot of the 64 positions gives the live
-// mask, then every lane issues all of its key AND value loads for the block at
-// once (dead slots are not fetched).  Within a block LPR = D/8 lanes cover one
-// row with 8 elements each and a wave instruction covers RPI = 64/LPR rows, so
-// NI = LPR instructions cover the block; a reduce-scatter butterfly over the
-// LPR lanes leaves lane (s, rr) with the logit of slot s*RPI + rr.  Each wave
-// keeps a running (max, sum, P.V) over its blocks (online softmax); waves are
-// combined at the end together with the sink logit 0, which has value 0:
+// One workgroup per (batch row, group), one pass over the slots.  Its waves
+// take 32-slot blocks in turn.  Within a block LPR = D/8 lanes cover one row
+// (8 elements each) and a wave instruction covers RPI = 64/LPR rows, so
+// NI = 32/RPI instructions cover the block; a reduce-scatter butterfly over the
+// LPR lanes leaves the logit of slot i*RPI + rr on the F = LPR/NI lanes
+// s = i*F .. i*F + F-1 of row group rr.  Loads are unconditional and
+// software-pipelined: the keys (and positions) of a wave's next block are
+// requested as soon as the current logits are formed, its values as soon as
+// the current P.V is done, so every wave keeps a block of keys and a block of
+// values in flight while it computes (a conditional load would make the
+// compiler wait for every load in flight).  A dead slot (position < 0) gets
+// logit -inf and a zero value row, so stale or uninitialised contents never
+// reach the sum.  Past its last block a wave re-reads that block (a cache hit).
+// Each wave keeps a running (max, sum, P.V) over its blocks (online softmax);
+// waves are combined at the end together with the sink logit 0, which has
+// value 0:
 //   out = sum_w acc_w e^{m_w - M} / (e^{-M} + sum_w l_w e^{m_w - M}),
 //   M = max(0, max_w m_w).
 template <int DT, int D, int R, bool SINK>
 __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
   constexpr int LPR = D / 8;
   constexpr int RPI = kWave / LPR;
-  constexpr int NI = LPR;
-  static_assert(NI * RPI == 64, "64-slot blocks");
+  constexpr int BS = 32;
+  constexpr int NI = BS / RPI;
+  constexpr int F = LPR / NI;
+  static_assert(NI * RPI == BS && F * NI == LPR && F >= 1, "32-slot blocks");
 
   __shared__ float wm[kReadWaves][R];
   __shared__ float wl[kReadWaves][R];
@@ -127,17 +164,18 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
   const int bg = blockIdx.x;
   const int row = bg / a.G, g = bg % a.G;
   const int H = a.G * R;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the block loop runs on scalar branches
   const int s = lane % LPR, rr = lane / LPR;
   const int64_t b = a.idx ? static_cast<int64_t>(a.idx[row]) : static_cast<int64_t>(row);
   const int64_t qbase = (static_cast<int64_t>(row) * H + static_cast<int64_t>(g) * R) * D;
-  if (b < 0 || b >= a.n_rows) {
+  if (b < 0 || b >= a.n_rows) {  // reads nothing: 0 (x any gate is 0)
     for (int e = tid; e < R * D; e += kReadThreads) store_any(a.out, qbase + e, DT, 0.f);
     return;
   }
-  const int64_t pos0 = b * a.p_rs + static_cast<int64_t>(g) * a.KC;  // first slot of (b, g)
-  const int64_t kbase = b * a.k_rs + static_cast<int64_t>(g) * a.KC * D;
-  const int64_t vbase = b * a.v_rs + static_cast<int64_t>(g) * a.KC * D;
+  const int32_t* pos = a.pos + b * a.p_rs + static_cast<int64_t>(g) * a.KC;  // slots of (b, g)
+  const int64_t kbase = b * a.k_rs + static_cast<int64_t>(g) * a.KC * D + rr * D + s * 8;
+  const int64_t vbase = b * a.v_rs + static_cast<int64_t>(g) * a.KC * D + rr * D + s * 8;
 
   float qf[R][8];
 #pragma unroll
@@ -158,77 +196,99 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
     for (int j = 0; j < 8; ++j) acc[r][j] = 0.f;
   }
 
-  const int nblk = a.KC / 64;
-  for (int blk = wid; blk < nblk; blk += kReadWaves) {
-    const int base = blk * 64;
-    const uint64_t live = __ballot(a.pos[pos0 + base + lane] >= 0);
+  const int nblk = a.KC / BS;
+  if (wid < nblk) {  // uniform over the wave
     Raw8<DT> kr[NI], vr[NI];
+    // same issue order as the loop (positions, keys, values), so the wait
+    // counts derived at the loop head are those of the steady state
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t pcur = pos[wid * BS + (lane & (BS - 1))];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int n = i * RPI + rr;
-      if ((live >> n) & 1ull) {
-        ld_raw8<DT>(kr[i], a.keys, kbase + static_cast<int64_t>(base + n) * D + s * 8);
-        ld_raw8<DT>(vr[i], a.values, vbase + static_cast<int64_t>(base + n) * D + s * 8);
-      } else {
-        zero_raw8<DT>(kr[i]);
-        zero_raw8<DT>(vr[i]);
-      }
-    }
-    float part[R][NI];
+    for (int i = 0; i < NI; ++i) ld_raw8<DT>(kr[i], a.keys, kbase + static_cast<int64_t>(wid * BS + i * RPI) * D);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      float kf[8];
-      cvt8<DT>(kr[i], kf);
+    for (int i = 0; i < NI; ++i) ld_raw8<DT>(vr[i], a.values, vbase + static_cast<int64_t>(wid * BS + i * RPI) * D);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int blk = wid; blk < nblk; blk += kReadWaves) {
+      const int nxt = (blk + kReadWaves < nblk ? blk + kReadWaves : blk) * BS;  // past the end: this block again
+      const uint32_t live = static_cast<uint32_t>(__ballot(pcur >= 0));
+      float part[R][NI];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float x = 0.f;
+      for (int i = 0; i < NI; ++i) {
+        float kf[8];
+        cvt8<DT>(kr[i], kf);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x = fmaf(qf[r][j], kf[j], x);
-        part[r][i] = x;
-      }
-    }
+        for (int r = 0; r < R; ++r) {
+          float x = 0.f;
 #pragma unroll
-    for (int m = LPR / 2, h = NI / 2; m >= 1; m >>= 1, h >>= 1) {
-      const bool up = (s & m) != 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-#pragma unroll
-        for (int j = 0; j < h; ++j) {
-          const float send = up ? part[r][j] : part[r][j + h];
-          const float keep = up ? part[r][j + h] : part[r][j];
-          part[r][j] = keep + __shfl_xor(send, m, kWave);
+          for (int j = 0; j < 8; ++j) x = fmaf(qf[r][j], kf[j], x);
+          part[r][i] = x;
         }
       }
-    }
-    // lane (s, rr) holds the logit of slot s*RPI + rr of this block
-    const bool mine_live = (live >> (s * RPI + rr)) & 1ull;
-    float pw[R];
+      // the keys and positions of the next block (sched_barrier: issued here,
+      // not sunk to their use in the next iteration)
+      __builtin_amdgcn_sched_barrier(0);
+      pcur = pos[nxt + (lane & (BS - 1))];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float logit = mine_live ? part[r][0] : -INFINITY;
-      const float bm = wave_max(logit);
-      const float m_new = fmaxf(m_run[r], bm);
-      const float m_safe = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __expf(m_run[r] - m_safe);
-      const float p = __expf(logit - m_safe);
-      l_run[r] = l_run[r] * alpha + wave_sum(p);
-      m_run[r] = m_new;
+      for (int i = 0; i < NI; ++i) ld_raw8<DT>(kr[i], a.keys, kbase + static_cast<int64_t>(nxt + i * RPI) * D);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
-      pw[r] = p;
-    }
-    // P.V: each value row is converted once and used for all R heads
+      for (int m = LPR / 2, h = NI / 2; m >= 1; m >>= 1, h >>= 1) {
+        if (h >= 1) {
+          const bool up = (s & m) != 0;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      float vf[8];
-      cvt8<DT>(vr[i], vf);
+          for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int j = 0; j < h; ++j) {
+              const float send = up ? part[r][j] : part[r][j + h];
+              const float keep = up ? part[r][j + h] : part[r][j];
+              part[r][j] = keep + __shfl_xor(send, m, kWave);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < R; ++r) part[r][0] += __shfl_xor(part[r][0], m, kWave);
+        }
+      }
+      // lane (s, rr) holds the logit of slot (s / F) * RPI + rr
+      const bool mine_live = (live >> ((s / F) * RPI + rr)) & 1u;
+      const bool counts = (s % F) == 0;  // one lane of the F copies enters the sum
+      float pw[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        // weight of the row this lane loaded at instruction i (slot i*RPI + rr)
-        const float w = __shfl(pw[r], rr * LPR + i, kWave);
+        const float logit = mine_live ? part[r][0] : -INFINITY;
+        const float bm = wave_max(logit);
+        const float m_new = fmaxf(m_run[r], bm);
+        const float m_safe = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = __expf(m_run[r] - m_safe);
+        const float p = __expf(logit - m_safe);
+        l_run[r] = l_run[r] * alpha + wave_sum(counts ? p : 0.f);
+        m_run[r] = m_new;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(w, vf[j], acc[r][j]);
+        for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
+        pw[r] = p;
       }
+      // P.V: each value row is converted once and used for all R heads
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float vf[8];
+        cvt8<DT>(vr[i], vf);
+        const bool vlive = (live >> (i * RPI + rr)) & 1u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vf[j] = vlive ? vf[j] : 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          // weight of the row this lane loaded at instruction i (slot i*RPI + rr)
+          const float w = __shfl(pw[r], rr * LPR + i * F, kWave);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(w, vf[j], acc[r][j]);
+        }
+      }
+      // the values of the next block
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) ld_raw8<DT>(vr[i], a.values, vbase + static_cast<int64_t>(nxt + i * RPI) * D);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
@@ -264,7 +324,8 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
       den = fmaf(wl[w][r], f, den);
       x = fmaf(accs[w][r][d], f, x);
     }
-    store_any(a.out, qbase + e, DT, den > 0.f ? x / den : 0.f);
+    const float o = den > 0.f ? x / den : 0.f;
+    store_any(a.out, qbase + e, DT, read_epilogue<DT>(a, row, H, g * R + r, d, o));
   }
 }
 
@@ -454,7 +515,9 @@ static int anchor_read_impl(bool sink, const void* query, const void* keys, cons
                               const int32_t* positions, const int32_t* indices, void* out,
                               int64_t B, int64_t H, int64_t G, int64_t capacity, int64_t D,
                               int64_t n_state_rows, int64_t keys_rs, int64_t values_rs, int64_t positions_rs,
-                              int dtype, yh_stream_t stream) {
+                              int dtype, yh_stream_t stream, const uint8_t* row_valid = nullptr,
+                              const float* head_gate = nullptr, const void* gate = nullptr, int64_t gate_ts = 0,
+                              int64_t gate_hs = 0) {
   using namespace yh;
   YH_CHECK_ARG(query && keys && values && positions && out, "anchor_read: null tensor pointer");
   YH_CHECK_ARG(B >= 0 && G > 0 && H > 0 && H % G == 0, "anchor_read: bad B/H/G (%lld/%lld/%lld)",
@@ -480,7 +543,8 @@ static int anchor_read_impl(bool sink, const void* query, const void* keys, cons
                "anchor_read: key/value row strides must keep 16-byte alignment");
   if (B == 0) return YH_OK;
   ReadArgs a{query, keys, values, positions, indices, out, (int)B, (int)G, (int)capacity, n_state_rows,
-             keys_rs, values_rs, positions_rs, 1.0f / sqrtf(static_cast<float>(D))};
+             keys_rs, values_rs, positions_rs, 1.0f / sqrtf(static_cast<float>(D)), row_valid, head_gate, gate,
+             gate_ts, gate_hs};
   const int R = static_cast<int>(H / G);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {
@@ -503,6 +567,30 @@ extern "C" int yh_window_attend(const void* query, const void* keys, const void*
                                 int64_t D, int64_t n_state_rows, int dtype, yh_stream_t stream) {
   return anchor_read_impl(false, query, keys, values, positions, indices, out, B, H, G, window, D, n_state_rows,
                           0, 0, 0, dtype, stream);
+}
+
+extern "C" int yh_anchor_read_gated(const void* query, const void* keys, const void* values,
+                                    const int32_t* positions, const int32_t* indices, void* out, int64_t B, int64_t H,
+                                    int64_t G, int64_t capacity, int64_t D, int64_t n_state_rows,
+                                    int64_t keys_row_stride, int64_t values_row_stride, int64_t positions_row_stride,
+                                    const uint8_t* row_valid, const float* head_gate, int dtype,
+                                    yh_stream_t stream) {
+  return anchor_read_impl(true, query, keys, values, positions, indices, out, B, H, G, capacity, D, n_state_rows,
+                          keys_row_stride, values_row_stride, positions_row_stride, dtype, stream, row_valid,
+                          head_gate);
+}
+
+extern "C" int yh_window_attend_gated(const void* query, const void* keys, const void* values,
+                                      const int32_t* positions, const int32_t* indices, void* out, int64_t B,
+                                      int64_t H, int64_t G, int64_t window, int64_t D, int64_t n_state_rows,
+                                      const void* gate, int64_t gate_tok_stride, int64_t gate_head_stride, int dtype,
+                                      yh_stream_t stream) {
+  if (!gate) {
+    yh::set_error("window_attend_gated: gate required");
+    return YH_ERR_INVALID;
+  }
+  return anchor_read_impl(false, query, keys, values, positions, indices, out, B, H, G, window, D, n_state_rows, 0,
+                          0, 0, dtype, stream, nullptr, nullptr, gate, gate_tok_stride, gate_head_stride);
 }
 
 extern "C" int yh_anchor_commit(const void* key, const void* value, const float* score,

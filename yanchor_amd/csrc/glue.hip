@@ -195,6 +195,15 @@ struct RopeArgs {
   uint16_t* out;
   int64_t out_tok_stride, out_head_stride;
   const int64_t* out_tok_index;  // optional: output row of token n is out_tok_index[n] (e.g. a ring slot)
+  // optional ring write of the same token: head h of v (raw) goes to v_out at
+  // the output row / strides of the normed head, and pos_val[n] (int32) to
+  // pos_out[orow * pos_tok_stride + h * pos_head_stride]
+  const uint16_t* v;
+  int64_t v_tok_stride, v_head_stride;
+  uint16_t* v_out;
+  int32_t* pos_out;
+  const int64_t* pos_val;
+  int64_t pos_tok_stride, pos_head_stride;
   int64_t NH;
   int H, rd;
   float eps;
@@ -226,6 +235,81 @@ __global__ void __launch_bounds__(256) head_norm_rope_kernel(RopeArgs a) {
   const int64_t orow = a.out_tok_index ? a.out_tok_index[n] : n;
   reinterpret_cast<uint32_t*>(a.out + orow * a.out_tok_stride + h * a.out_head_stride)[lane] =
       tobf(y0) | (static_cast<uint32_t>(tobf(y1)) << 16);
+  if (a.v_out) {
+    const uint32_t vv = reinterpret_cast<const uint32_t*>(a.v + n * a.v_tok_stride + h * a.v_head_stride)[lane];
+    reinterpret_cast<uint32_t*>(a.v_out + orow * a.out_tok_stride + h * a.out_head_stride)[lane] = vv;
+  }
+  if (a.pos_out && lane == 0)
+    a.pos_out[orow * a.pos_tok_stride + h * a.pos_head_stride] = static_cast<int32_t>(a.pos_val[n]);
+}
+
+// The memory-read prologue of one decode token (IndependentGQAMemory.
+// _query_scores, modeling_yanchor.py:167-176): from the fused projection
+// [q | admission features | ...] of token b,
+//   q     = RoPE(RMSNorm_(1+w)(q_h))                          bf16 [B, H, 128]
+//   gate  = tanh(read_scale_h) * 2 * sigmoid(<qn_h, gw_h> / sqrt(128) + gb_h)   f32 [B, H]
+//           (qn_h: the normed head before RoPE, as bf16)
+//   score = silu(features) (bf16) . adm_up^T                  f32 [B, G]
+// Grid (B, H/4 + 1): four heads per workgroup (a wave each); the last column
+// computes the admission scores (one wave, 64 features per lane pass).
+struct MemProArgs {
+  const uint16_t* proj;  // [B, P] rows ps apart
+  int64_t ps;
+  const uint16_t* w;     // q norm weight [128]
+  const float* cos;      // [B, rd]
+  const float* sin;
+  const float* read_scale;  // [H]
+  const float* gate_w;      // [H, 128]
+  const float* gate_b;      // [H]
+  const float* adm_up;      // [G, A]
+  uint16_t* q;              // [B, H, 128]
+  float* gate;              // [B, H]
+  float* scores;            // [B, G]
+  int H, G, A, rd, feat_off;
+  float eps;
+};
+
+__global__ void __launch_bounds__(256) memory_prologue_kernel(MemProArgs a) {
+  const int64_t b = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  const uint16_t* row = a.proj + b * a.ps;
+  if (static_cast<int>(blockIdx.y) * 4 >= a.H) {
+    // admission scores: silu(features) rounded to bf16, then fp32 dots
+    if (wv != 0) return;
+    for (int g = 0; g < a.G; ++g) {
+      float acc = 0.f;
+      for (int j = lane; j < a.A; j += kWave) acc = fmaf(bf(tobf(silu(bf(row[a.feat_off + j])))), a.adm_up[g * a.A + j], acc);
+      acc = wave_sum(acc);
+      if (lane == 0) a.scores[b * a.G + g] = acc;
+    }
+    return;
+  }
+  const int h = blockIdx.y * 4 + wv;
+  if (h >= a.H) return;
+  const uint32_t xv = reinterpret_cast<const uint32_t*>(row + h * 128)[lane];
+  const uint32_t wvv = reinterpret_cast<const uint32_t*>(a.w)[lane];
+  const float x0 = bf(xv & 0xffff), x1 = bf(xv >> 16);
+  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / 128.f + a.eps);
+  float y0 = bf(tobf(x0 * r * (1.f + bf(wvv & 0xffff))));
+  float y1 = bf(tobf(x1 * r * (1.f + bf(wvv >> 16))));
+  // read gate from the normed (unrotated) head
+  const float dot = wave_sum(fmaf(y0, a.gate_w[h * 128 + 2 * lane], y1 * a.gate_w[h * 128 + 2 * lane + 1]));
+  if (lane == 0) {
+    const float z = dot / sqrtf(128.f) + a.gate_b[h];
+    a.gate[b * a.H + h] = tanhf(a.read_scale[h]) * 2.f * (1.f / (1.f + expf(-z)));
+  }
+  const int e0 = 2 * lane, half = a.rd / 2;
+  const bool rot = e0 < a.rd;
+  const int pl = e0 < half ? lane + half / 2 : lane - half / 2;
+  const float p0 = __shfl(y0, rot ? pl : lane, kWave), p1 = __shfl(y1, rot ? pl : lane, kWave);
+  if (rot) {
+    const float c0 = a.cos[b * a.rd + e0], c1 = a.cos[b * a.rd + e0 + 1];
+    const float s0 = a.sin[b * a.rd + e0], s1 = a.sin[b * a.rd + e0 + 1];
+    const float sg = e0 < half ? -1.f : 1.f;
+    y0 = y0 * c0 + sg * p0 * s0;
+    y1 = y1 * c1 + sg * p1 * s1;
+  }
+  reinterpret_cast<uint32_t*>(a.q + (b * a.H + h) * 128)[lane] = tobf(y0) | (static_cast<uint32_t>(tobf(y1)) << 16);
 }
 
 }  // namespace
@@ -307,24 +391,76 @@ extern "C" int yh_silu_mul(const void* gate_up, int64_t gate_up_stride, void* ou
   return YH_OK;
 }
 
-extern "C" int yh_head_norm_rope(const void* x, int64_t x_tok_stride, int64_t x_head_stride, const void* w,
-                                 const float* cos, const float* sin, void* out, int64_t out_tok_stride,
-                                 int64_t out_head_stride, const int64_t* out_tok_index, int64_t N, int64_t H,
-                                 int64_t D, int64_t rotary_dim, float eps, yh_stream_t stream) {
+static int head_norm_rope_impl(const void* x, int64_t x_tok_stride, int64_t x_head_stride, const void* w,
+                               const float* cos, const float* sin, void* out, int64_t out_tok_stride,
+                               int64_t out_head_stride, const int64_t* out_tok_index, const void* v,
+                               int64_t v_tok_stride, int64_t v_head_stride, void* v_out, int32_t* pos_out,
+                               const int64_t* pos_val, int64_t pos_tok_stride, int64_t pos_head_stride, int64_t N,
+                               int64_t H, int64_t D, int64_t rotary_dim, float eps, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(N >= 0 && H > 0 && (N == 0 || (x && w && out)), "head_norm_rope: bad arguments");
   YH_CHECK_ARG(D == 128, "head_norm_rope: head dim must be 128");
   YH_CHECK_ARG(rotary_dim >= 0 && rotary_dim <= D && rotary_dim % 4 == 0, "head_norm_rope: rotary dim %lld",
                (long long)rotary_dim);
   YH_CHECK_ARG(rotary_dim == 0 || (cos && sin), "head_norm_rope: cos/sin required");
-  YH_CHECK_ARG((x_tok_stride | x_head_stride | out_tok_stride | out_head_stride) % 2 == 0,
+  YH_CHECK_ARG((x_tok_stride | x_head_stride | out_tok_stride | out_head_stride | v_tok_stride | v_head_stride) % 2 ==
+                   0,
                "head_norm_rope: strides must be even");
+  YH_CHECK_ARG(N == 0 || !v_out || v, "ring write: value source required");
+  YH_CHECK_ARG(N == 0 || !pos_out || pos_val, "ring write: positions required");
   if (N == 0) return YH_OK;
   RopeArgs a{static_cast<const uint16_t*>(x), x_tok_stride, x_head_stride, static_cast<const uint16_t*>(w), cos, sin,
-             static_cast<uint16_t*>(out), out_tok_stride, out_head_stride, out_tok_index, N * H, (int)H,
-             (int)rotary_dim, eps};
+             static_cast<uint16_t*>(out), out_tok_stride, out_head_stride, out_tok_index,
+             static_cast<const uint16_t*>(v), v_tok_stride, v_head_stride, static_cast<uint16_t*>(v_out), pos_out,
+             pos_val, pos_tok_stride, pos_head_stride, N * H, (int)H, (int)rotary_dim, eps};
   hipLaunchKernelGGL(head_norm_rope_kernel, dim3(static_cast<unsigned>((N * H + 3) / 4)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   YH_CHECK_LAUNCH("head_norm_rope");
+  return YH_OK;
+}
+
+extern "C" int yh_head_norm_rope(const void* x, int64_t x_tok_stride, int64_t x_head_stride, const void* w,
+                                 const float* cos, const float* sin, void* out, int64_t out_tok_stride,
+                                 int64_t out_head_stride, const int64_t* out_tok_index, int64_t N, int64_t H,
+                                 int64_t D, int64_t rotary_dim, float eps, yh_stream_t stream) {
+  return head_norm_rope_impl(x, x_tok_stride, x_head_stride, w, cos, sin, out, out_tok_stride, out_head_stride,
+                             out_tok_index, nullptr, 0, 0, nullptr, nullptr, nullptr, 0, 0, N, H, D, rotary_dim, eps,
+                             stream);
+}
+
+extern "C" int yh_ring_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride, const void* v,
+                             int64_t v_tok_stride, int64_t v_head_stride, const void* w, const float* cos,
+                             const float* sin, const int64_t* rows, const int64_t* positions, void* ring_k,
+                             void* ring_v, int32_t* ring_pos, int64_t N, int64_t H, int64_t window, int64_t D,
+                             int64_t rotary_dim, float eps, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(window > 0 && N >= 0, "ring_write: bad sizes");
+  YH_CHECK_ARG(N == 0 || (rows && positions && ring_k && ring_v && ring_pos && v), "ring_write: null pointer");
+  return head_norm_rope_impl(k, k_tok_stride, k_head_stride, w, cos, sin, ring_k, D, window * D, rows, v, v_tok_stride,
+                             v_head_stride, ring_v, ring_pos, positions, 1, window, N, H, D, rotary_dim, eps, stream);
+}
+
+extern "C" int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t feat_offset, const void* q_norm_w,
+                                  const float* cos, const float* sin, const float* read_scale, const float* gate_w,
+                                  const float* gate_b, const float* adm_up, void* q, float* gate, float* scores,
+                                  int64_t B, int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps,
+                                  yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(D == 128, "memory_prologue: head dim must be 128");
+  YH_CHECK_ARG(B >= 0 && H > 0 && G > 0 && A > 0 && G <= 64, "memory_prologue: bad sizes");
+  YH_CHECK_ARG(rotary_dim >= 0 && rotary_dim <= D && rotary_dim % 4 == 0, "memory_prologue: rotary dim");
+  YH_CHECK_ARG(feat_offset >= H * D && feat_offset + A <= proj_stride && proj_stride % 2 == 0,
+               "memory_prologue: the features must follow the query in each projection row");
+  if (B == 0) return YH_OK;
+  YH_CHECK_ARG(proj && q_norm_w && read_scale && gate_w && gate_b && adm_up && q && gate && scores &&
+                   (rotary_dim == 0 || (cos && sin)),
+               "memory_prologue: null pointer");
+  YH_CHECK_ARG((reinterpret_cast<uintptr_t>(proj) & 3) == 0, "memory_prologue: projection must be 4-byte aligned");
+  MemProArgs a{static_cast<const uint16_t*>(proj), proj_stride, static_cast<const uint16_t*>(q_norm_w), cos, sin,
+               read_scale, gate_w, gate_b, adm_up, static_cast<uint16_t*>(q), gate, scores, (int)H, (int)G, (int)A,
+               (int)rotary_dim, (int)feat_offset, eps};
+  const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>((H + 3) / 4 + 1));
+  hipLaunchKernelGGL(memory_prologue_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  YH_CHECK_LAUNCH("memory_prologue");
   return YH_OK;
 }

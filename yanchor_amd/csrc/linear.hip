@@ -51,6 +51,8 @@ struct LinArgs {
   float* part;         // [S, M, N] fp32 partials (S > 1)
   int64_t xs, os;
   int M, N, K, S, chunks_per_slice;
+  const uint16_t* res;  // optional residual [M, N], rows rs apart: out = bf16(bf16(x . W^T) + res)
+  int64_t rs;
 };
 
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
@@ -220,7 +222,7 @@ __global__ void __launch_bounds__(kLinThreads) skinny_linear_kernel(LinArgs a) {
 // out = bf16(sum_s part[s]) in slice order (a fixed order: results do not
 // depend on scheduling); 4 columns per thread.
 __global__ void __launch_bounds__(256) linear_reduce_kernel(const float* part, uint16_t* out, int64_t os, int M,
-                                                            int N, int S) {
+                                                            int N, int S, const uint16_t* res, int64_t rs) {
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t per_row = N / 4;
   if (e >= static_cast<int64_t>(M) * per_row) return;
@@ -234,6 +236,13 @@ __global__ void __launch_bounds__(256) linear_reduce_kernel(const float* part, u
     sum.y += v.y;
     sum.z += v.z;
     sum.w += v.w;
+  }
+  if (res) {  // the product is a bf16 tensor before the residual add
+    const uint2 r = *reinterpret_cast<const uint2*>(res + m * rs + c);
+    sum.x = bf16_to_f32(f32_to_bf16(sum.x)) + bf16_to_f32(static_cast<uint16_t>(r.x & 0xffff));
+    sum.y = bf16_to_f32(f32_to_bf16(sum.y)) + bf16_to_f32(static_cast<uint16_t>(r.x >> 16));
+    sum.z = bf16_to_f32(f32_to_bf16(sum.z)) + bf16_to_f32(static_cast<uint16_t>(r.y & 0xffff));
+    sum.w = bf16_to_f32(f32_to_bf16(sum.w)) + bf16_to_f32(static_cast<uint16_t>(r.y >> 16));
   }
   const uint2 o = make_uint2(static_cast<uint32_t>(f32_to_bf16(sum.x)) | (static_cast<uint32_t>(f32_to_bf16(sum.y)) << 16),
                              static_cast<uint32_t>(f32_to_bf16(sum.z)) | (static_cast<uint32_t>(f32_to_bf16(sum.w)) << 16));
@@ -376,7 +385,11 @@ __device__ __forceinline__ void pk_store_rows(const f32x4v (&acc)[MT][2], const 
       for (int i = 0; i < 4; ++i) {
         const int m = t * 16 + quad * 4 + i;
         if (m >= a.M) continue;
-        if (a.S == 1) a.out[m * a.os + ncol[ct]] = f32_to_bf16(acc[t][ct][i]);
+        if (a.S == 1) {
+          float y = acc[t][ct][i];
+          if (a.res) y = bf16_to_f32(f32_to_bf16(y)) + bf16_to_f32(a.res[m * a.rs + ncol[ct]]);
+          a.out[m * a.os + ncol[ct]] = f32_to_bf16(y);
+        }
         else mine[static_cast<int64_t>(m) * a.N + ncol[ct]] = acc[t][ct][i];
       }
   }
@@ -526,7 +539,7 @@ extern "C" int yh_linear(const void* x, int64_t x_stride, const void* w, void* o
   if (S > 1) {
     const int64_t quads = M * N / 4;
     hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0, st,
-                       part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N, S);
+                       part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N, S, nullptr, 0);
     YH_CHECK_LAUNCH("linear_reduce");
   }
   return YH_OK;
@@ -553,8 +566,8 @@ extern "C" int yh_linear_packed_split(int64_t M, int64_t N, int64_t K) {
 }
 
 extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride,
-                                int64_t M, int64_t N, int64_t K, int64_t split_k, void* workspace,
-                                int64_t workspace_bytes, yh_stream_t stream) {
+                                int64_t M, int64_t N, int64_t K, const void* residual, int64_t residual_stride,
+                                int64_t split_k, void* workspace, int64_t workspace_bytes, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(M >= 0 && M <= kMaxM, "linear_packed: M must be in [0, %d] (got %lld)", kMaxM, (long long)M);
   YH_CHECK_ARG(N > 0 && N % 16 == 0, "linear_packed: N must be a positive multiple of 16");
@@ -575,9 +588,12 @@ extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_p
   YH_CHECK_ARG(S == 1 || (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
                "linear_packed: workspace must be 16-byte aligned");
   YH_CHECK_ARG(S == 1 || (out_stride % 4 == 0 && N % 4 == 0), "linear_packed: split-K output rows must be 8-byte aligned");
+  YH_CHECK_ARG(!residual || (residual_stride >= N && (S == 1 || (residual_stride % 4 == 0 &&
+                                                                (reinterpret_cast<uintptr_t>(residual) & 7) == 0))),
+               "linear_packed: bad residual stride / alignment");
   LinArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_packed), static_cast<uint16_t*>(out),
             S > 1 ? static_cast<float*>(workspace) : nullptr, x_stride, out_stride, (int)M, (int)N, (int)K, S,
-            static_cast<int>(pps * kPh)};
+            static_cast<int>(pps * kPh), static_cast<const uint16_t*>(residual), residual_stride};
   const dim3 grid(static_cast<unsigned>((N + kNT - 1) / kNT), static_cast<unsigned>(S));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int mt = static_cast<int>((M + 15) / 16);
@@ -590,7 +606,7 @@ extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_p
   if (S > 1) {
     const int64_t quads = M * N / 4;
     hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0, st,
-                       a.part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N, S);
+                       a.part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N, S, a.res, a.rs);
     YH_CHECK_LAUNCH("linear_reduce");
   }
   return YH_OK;

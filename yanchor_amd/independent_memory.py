@@ -157,6 +157,14 @@ def committed_gqa(query, state: IndependentMemoryState, indices=None):
     head, softmax over [q.K^T / sqrt(D) on live slots, 0] applied to V (the
     zero-logit sink).  Row b reads state row ``indices[b]`` when given (-1 reads
     nothing and returns 0)."""
+    return committed_gqa_gated(query, state, indices)
+
+
+def committed_gqa_gated(query, state: IndependentMemoryState, indices=None, valid=None, head_gate=None):
+    """``committed_gqa`` followed by the decode layer's gating of the read,
+    in one launch: ``(read * valid[b]) * head_gate[b, h]`` with each product
+    rounded to the query dtype (valid bool ``[B]``, head_gate float ``[B, H]``;
+    None skips either)."""
     nb, g, cap, _, d = _check_state(state)
     if query.ndim != 4 or query.shape[1] != 1 or query.shape[3] != d:
         raise ValueError("query must be [B, 1, H, D] with the memory head dim")
@@ -165,16 +173,27 @@ def committed_gqa(query, state: IndependentMemoryState, indices=None):
         raise ValueError("query heads must be a multiple of memory groups")
     if query.dtype != state.keys.dtype:
         raise ValueError("query and memory must share a dtype")
-    N.require_device(query, state.keys, indices)
+    if valid is not None and valid.shape != (b,):
+        raise ValueError("valid must be [B]")
+    if head_gate is not None and head_gate.shape != (b, h):
+        raise ValueError("head_gate must be [B, H]")
+    N.require_device(query, state.keys, indices, valid, head_gate)
     idx = _indices(indices, b)
     if idx is None and nb < b:
         raise ValueError("memory state has fewer rows than the batch")
     q = query.contiguous()
     out = torch.empty_like(q)
     rs = _row_strides(state)
-    N.call("yh_anchor_read", q.data_ptr(), state.keys.data_ptr(), state.values.data_ptr(),
+    if valid is None and head_gate is None:
+        N.call("yh_anchor_read", q.data_ptr(), state.keys.data_ptr(), state.values.data_ptr(),
+               state.positions.data_ptr(), N.ptr(idx), out.data_ptr(), b, h, g, cap, d, nb, rs[0], rs[1], rs[3],
+               N.code(q), N.stream_of(q))
+        return out
+    vd = None if valid is None else valid.to(torch.uint8).contiguous()
+    hg = None if head_gate is None else head_gate.to(torch.float32).contiguous()
+    N.call("yh_anchor_read_gated", q.data_ptr(), state.keys.data_ptr(), state.values.data_ptr(),
            state.positions.data_ptr(), N.ptr(idx), out.data_ptr(), b, h, g, cap, d, nb, rs[0], rs[1], rs[3],
-           N.code(q), N.stream_of(q))
+           N.ptr(vd), N.ptr(hg), N.code(q), N.stream_of(q))
     return out
 
 
@@ -290,19 +309,22 @@ def sequence(query, key, value, scores, valid, chunk, state: IndependentMemorySt
     return out
 
 
-def ring_decode_attention(query, keys, values, positions, indices=None):
+def ring_decode_attention(query, keys, values, positions, indices=None, gate=None):
     """Decode attention of one token over a physical ring of cached K/V slots
     (the sliding-window decode path, reference runtime/model/
     inference_kernels.py:555-640): softmax over the live slots (positions
     >= 0) without the anchor sink.  query [B, 1, H, D]; keys/values
-    [NB, G, window, D]; positions int32 [NB, G, window]."""
+    [NB, G, window, D]; positions int32 [NB, G, window].  With ``gate``
+    ([B, H, D], any token / head strides, unit last stride) the output is
+    ``read * sigmoid(gate)`` (the gated-q output, products rounded to the
+    dtype) in the same launch."""
     nb, g, window, d = keys.shape
     if values.shape != keys.shape or positions.shape != (nb, g, window) or positions.dtype != torch.int32:
         raise ValueError("ring keys/values must be [NB, G, W, D] with int32 positions [NB, G, W]")
     if query.ndim != 4 or query.shape[1] != 1 or query.shape[3] != d or query.dtype != keys.dtype:
         raise ValueError("query must be [B, 1, H, D] in the cache dtype")
     b, _, h, _ = query.shape
-    N.require_device(query, keys, values, positions, indices)
+    N.require_device(query, keys, values, positions, indices, gate)
     for t in (keys, values, positions):
         if not t.is_contiguous():
             raise ValueError("ring tensors must be contiguous")
@@ -311,6 +333,13 @@ def ring_decode_attention(query, keys, values, positions, indices=None):
         raise ValueError("ring has fewer rows than the batch")
     q = query.contiguous()
     out = torch.empty_like(q)
-    N.call("yh_window_attend", q.data_ptr(), keys.data_ptr(), values.data_ptr(), positions.data_ptr(), N.ptr(idx),
-           out.data_ptr(), b, h, g, window, d, nb, N.code(q), N.stream_of(q))
+    if gate is None:
+        N.call("yh_window_attend", q.data_ptr(), keys.data_ptr(), values.data_ptr(), positions.data_ptr(),
+               N.ptr(idx), out.data_ptr(), b, h, g, window, d, nb, N.code(q), N.stream_of(q))
+        return out
+    if gate.shape != (b, h, d) or gate.stride(-1) != 1 or gate.dtype != q.dtype:
+        raise ValueError("gate must be [B, H, D] in the query dtype with unit last stride")
+    N.call("yh_window_attend_gated", q.data_ptr(), keys.data_ptr(), values.data_ptr(), positions.data_ptr(),
+           N.ptr(idx), out.data_ptr(), b, h, g, window, d, nb, gate.data_ptr(), gate.stride(0), gate.stride(1),
+           N.code(q), N.stream_of(q))
     return out

@@ -123,6 +123,57 @@ def head_norm_rope(x, w, cos, sin, rotary_dim, eps, *, out=None, out_tok_index=N
     return out
 
 
+def ring_write(k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rotary_dim, eps):
+    """Write one decode token per row into the SWA ring: the key heads k
+    [N, H, 128] normed (1 + w) and rotated, the raw value heads v [N, H, 128]
+    and positions [N] go to ring row ``rows[n]`` of ring_k / ring_v
+    [N, H, W, 128] and ring_pos int32 [N, H, W]."""
+    _bf16(k, v, w, ring_k, ring_v)
+    n, h, d = k.shape
+    if v.shape != k.shape or k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("k / v must be [N, H, D] with unit last stride")
+    if ring_k.ndim != 4 or ring_k.shape[1] != h or ring_k.shape[3] != d or ring_v.shape != ring_k.shape:
+        raise ValueError("ring_k / ring_v must be [N, H, W, D]")
+    if ring_pos.shape != ring_k.shape[:3] or ring_pos.dtype != torch.int32:
+        raise ValueError("ring_pos must be int32 [N, H, W]")
+    for t in (ring_k, ring_v, ring_pos):
+        if not t.is_contiguous():
+            raise ValueError("ring tensors must be contiguous")
+    dev = N.require_device(k, v, w, cos, sin, rows, positions, ring_k)
+    cs = None if cos is None else cos.float().contiguous()
+    sn = None if sin is None else sin.float().contiguous()
+    r = rows.to(torch.int64).contiguous()
+    p = positions.to(torch.int64).contiguous()
+    N.call("yh_ring_write", k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+           w.data_ptr(), N.ptr(cs), N.ptr(sn), r.data_ptr(), p.data_ptr(), ring_k.data_ptr(), ring_v.data_ptr(),
+           ring_pos.data_ptr(), n, h, ring_k.shape[2], d, rotary_dim, float(eps), N.stream_of(k))
+
+
+def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b, adm_up,
+                    rotary_dim, eps):
+    """Query, read gate and admission scores of the anchor memory for one
+    decode token per row from the fused projection proj [B, P] (query heads
+    first, admission features at ``feat_offset``): returns q [B, H, 128] bf16,
+    gate [B, H] float, scores [B, G] float (modeling_yanchor.py:167-176)."""
+    _bf16(proj, q_norm_w)
+    b, ps = proj.shape
+    if proj.stride(1) != 1:
+        raise ValueError("proj must have unit last stride")
+    g = adm_up.shape[0]
+    dev = N.require_device(proj, q_norm_w, cos, sin, read_scale, gate_w, gate_b, adm_up)
+    f32 = [t.to(torch.float32).contiguous() for t in (read_scale, gate_w, gate_b, adm_up)]
+    cs = None if cos is None else cos.float().contiguous()
+    sn = None if sin is None else sin.float().contiguous()
+    q = torch.empty(b, heads, 128, dtype=proj.dtype, device=dev)
+    gate = torch.empty(b, heads, dtype=torch.float32, device=dev)
+    scores = torch.empty(b, g, dtype=torch.float32, device=dev)
+    N.call("yh_memory_prologue", proj.data_ptr(), proj.stride(0), feat_offset, q_norm_w.data_ptr(), N.ptr(cs),
+           N.ptr(sn), f32[0].data_ptr(), f32[1].data_ptr(), f32[2].data_ptr(), f32[3].data_ptr(), q.data_ptr(),
+           gate.data_ptr(), scores.data_ptr(), b, heads, 128, g, n_features, rotary_dim, float(eps),
+           N.stream_of(proj))
+    return q, gate, scores
+
+
 _linear_ws: dict = {}
 
 
@@ -158,13 +209,17 @@ class PackedWeight:
         return (w.dtype == torch.bfloat16 and w.ndim == 2 and w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0)
 
 
-def linear(x, w, split_k=None):
+def linear(x, w, split_k=None, residual=None):
     """out = x . w^T for a decode batch (x [M, K] bf16 with M <= 128, w [N, K]
     bf16 or a PackedWeight): torch.nn.functional.linear without bias on the
-    skinny-projection kernels.  The split-K workspace is cached per device:
-    concurrent calls on different streams of one device must not overlap."""
+    skinny-projection kernels; with ``residual`` ([M, N] bf16, unit last
+    stride) out = bf16(x . w^T) + residual.  The split-K workspace is cached
+    per device: concurrent calls on different streams of one device must not
+    overlap."""
     packed = isinstance(w, PackedWeight)
-    _bf16(x, w.data if packed else w)
+    _bf16(x, w.data if packed else w, residual)
+    if not packed and residual is not None:
+        return linear(x, w, split_k) + residual
     n, kw = w.shape
     if x.ndim != 2 or (not packed and w.ndim != 2) or x.shape[1] != kw:
         raise ValueError("linear expects x [M, K] and w [N, K]")
@@ -174,15 +229,23 @@ def linear(x, w, split_k=None):
     wt = w.data if packed else w.contiguous()
     dev = N.require_device(x, wt)
     out = torch.empty(m, n, dtype=x.dtype, device=dev)
+    if residual is not None:
+        if residual.shape != (m, n) or residual.stride(1) != 1:
+            raise ValueError("residual must be [M, N] with unit last stride")
+        N.require_device(residual)
+        if residual.stride(0) % 4 or residual.data_ptr() % 8:
+            residual = residual.contiguous()
     if packed:
         s = int(split_k) if split_k is not None else N.lib().yh_linear_packed_split(m, n, k)
         nbytes = s * m * n * 4 if s > 1 else 0
-        entry = "yh_linear_packed"
-    else:
-        s = int(split_k) if split_k is not None else N.lib().yh_linear_split(m, n, k)
-        nbytes = N.lib().yh_linear_workspace_bytes(m, n, k, s)
-        entry = "yh_linear"
+        ws = _linear_workspace(dev, nbytes) if nbytes else None
+        N.call("yh_linear_packed", x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), n, m, n, k,
+               N.ptr(residual), 0 if residual is None else residual.stride(0), s, N.ptr(ws),
+               0 if ws is None else ws.numel(), N.stream_of(x))
+        return out
+    s = int(split_k) if split_k is not None else N.lib().yh_linear_split(m, n, k)
+    nbytes = N.lib().yh_linear_workspace_bytes(m, n, k, s)
     ws = _linear_workspace(dev, nbytes) if nbytes else None
-    N.call(entry, x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), n, m, n, k, s, N.ptr(ws),
+    N.call("yh_linear", x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), n, m, n, k, s, N.ptr(ws),
            0 if ws is None else ws.numel(), N.stream_of(x))
     return out

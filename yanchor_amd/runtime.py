@@ -137,12 +137,25 @@ class HipOps:
         if self.layers.PackedWeight.fits(model.lm_head):
             model.lm_head_packed = self.layers.PackedWeight(model.lm_head)
 
-    def linear(self, x, w, packed=None):
-        """out = x . w^T: the packed-weight kernel for a decode batch (bf16,
-        <= 128 rows) when a packed copy exists, torch (hipBLASLt) otherwise."""
+    def linear(self, x, w, packed=None, residual=None):
+        """out = x . w^T (+ residual, added to the bf16 product): the
+        packed-weight kernel for a decode batch (bf16, <= 128 rows) when a
+        packed copy exists, torch (hipBLASLt) otherwise."""
         if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128:
-            return self.layers.linear(x, packed)
-        return F.linear(x, w)
+            return self.layers.linear(x, packed, residual=residual)
+        out = F.linear(x, w)
+        return out if residual is None else out + residual
+
+    def ring_write(self, k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rotary_dim, eps):
+        if k.dtype != torch.bfloat16:
+            return TorchGlue.ring_write(k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rotary_dim, eps)
+        self.layers.ring_write(k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rotary_dim, eps)
+
+    def memory_prologue(self, proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b,
+                        adm_up, rotary_dim, eps):
+        f = TorchGlue.memory_prologue if proj.dtype != torch.bfloat16 else self.layers.memory_prologue
+        return f(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b, adm_up,
+                 rotary_dim, eps)
 
     def gdn_decode(self, q, k, v, g, beta, state):
         o, _ = self.gdn.recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=state,
@@ -154,11 +167,11 @@ class HipOps:
                                                use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
                                                lengths=lengths)
 
-    def window_attend(self, q, keys, values, positions):
-        return self.mem.ring_decode_attention(q, keys, values, positions)
+    def window_attend(self, q, keys, values, positions, gate=None):
+        return self.mem.ring_decode_attention(q, keys, values, positions, gate=gate)
 
-    def memory_read(self, q, state):
-        return self.mem.committed_gqa(q, state)
+    def memory_read(self, q, state, valid=None, head_gate=None):
+        return self.mem.committed_gqa_gated(q, state, None, valid, head_gate)
 
     def memory_commit(self, key, value, scores, active, chunk, state):
         self.mem.commit_decode(key, value, scores, active, chunk, state)
@@ -260,6 +273,45 @@ class TorchGlue:
         dst = out.as_strided((rows, h, d), (out_tok_stride, out_head_stride, 1))
         dst[out_tok_index] = y
         return out
+
+
+def _torch_ring_write(k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rotary_dim, eps):
+    n, h, d = k.shape
+    window = ring_k.shape[2]
+    TorchGlue.head_norm_rope(k, w, cos, sin, rotary_dim, eps, out=ring_k, out_tok_index=rows, out_tok_stride=d,
+                             out_head_stride=window * d)
+    slot = positions % window
+    tok = torch.arange(n, device=k.device)
+    ring_v[tok, :, slot] = v
+    ring_pos[tok, :, slot] = positions.to(torch.int32)[:, None]
+
+
+def _torch_memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b,
+                           adm_up, rotary_dim, eps):
+    b = proj.shape[0]
+    d = 128
+    mq = proj[:, : heads * d].view(b, heads, d)
+    qn = TorchGlue.head_norm_rope(mq, q_norm_w, None, None, 0, eps)
+    gate = torch.tanh(read_scale) * 2 * torch.sigmoid((qn.float() * gate_w).sum(-1) / math.sqrt(d) + gate_b)
+    q = TorchGlue.head_norm_rope(mq, q_norm_w, cos, sin, rotary_dim, eps)
+    scores = F.linear(F.silu(proj[:, feat_offset: feat_offset + n_features]).float(), adm_up)
+    return q, gate, scores
+
+
+TorchGlue.ring_write = staticmethod(_torch_ring_write)
+TorchGlue.memory_prologue = staticmethod(_torch_memory_prologue)
+
+
+def gate_read(read, valid=None, head_gate=None, gate=None):
+    """The torch formulation of the decode layer's gating of a read
+    [B, 1, H, D]: (read * valid) * head_gate, or read * sigmoid(gate)."""
+    if valid is not None:
+        read = read * valid[:, None, None, None].to(read.dtype)
+    if head_gate is not None:
+        read = read * head_gate[:, None, :, None].to(read.dtype)
+    if gate is not None:
+        read = read * torch.sigmoid(gate)[:, None]
+    return read
 
 
 class Model:
@@ -429,13 +481,10 @@ class Model:
         u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
         proj = ops.linear(u, L["m_in"])                                    # [q | admission features | gate | up]
         qd, ad = H * D, c.admission_rank
-        mq = proj[:, :qd].view(B, H, D)
-        qn = ops.head_norm_rope(mq, L["m_q_norm"], None, None, 0, c.rms_eps)
-        gate = torch.tanh(L["read_scale"]) * 2 * torch.sigmoid(
-            (qn.float() * L["read_gate_w"]).sum(-1) / math.sqrt(D) + L["read_gate_b"])
-        q = ops.head_norm_rope(mq, L["m_q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
-        scores = ops.linear(F.silu(proj[:, qd: qd + ad]).float(), L["adm_up"])
-        zz = u + ops.linear(ops.silu_mul(proj[:, qd + ad:]), L["writer_down"], L.get("writer_down@packed"))
+        q, gate, scores = ops.memory_prologue(proj, H, qd, ad, L["m_q_norm"], cos, sin, L["read_scale"],
+                                              L["read_gate_w"], L["read_gate_b"], L["adm_up"], c.rotary_dim,
+                                              c.rms_eps)
+        zz = ops.linear(ops.silu_mul(proj[:, qd + ad:]), L["writer_down"], L.get("writer_down@packed"), residual=u)
         kv = ops.linear(zz, L["m_kv"])
         key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
                                  c.rms_eps)
@@ -446,26 +495,20 @@ class Model:
         normalised layer input, hidden the residual stream entering the layer;
         ring_rows[b] = b * kv_heads * window + positions[b] % window."""
         c, B, ops = self.cfg, xn.shape[0], self.ops
-        H, KVH, D, W = c.attn_heads, c.kv_heads, c.head_dim, c.swa_window
+        H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
         proj = ops.linear(xn, L["w_qkv"])                                    # [B, (q|gate) per head | k | v]
         hq = 2 * H * D
         qg = proj[:, :hq].view(B, H, 2 * D)
         q = ops.head_norm_rope(qg[..., :D], L["q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
-        ops.head_norm_rope(proj[:, hq: hq + KVH * D].view(B, KVH, D), L["k_norm"], cos, sin, c.rotary_dim,
-                           c.rms_eps, out=self.ring_k[i], out_tok_index=ring_rows, out_tok_stride=D,
-                           out_head_stride=W * D)
-        slot = positions % W
-        rows = torch.arange(B, device=xn.device)
-        self.ring_v[i][rows, :, slot] = proj[:, hq + KVH * D:].view(B, KVH, D)
-        self.ring_pos[i][rows, :, slot] = positions.to(torch.int32)[:, None]
-        att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i])
-        out = ops.linear((att[:, 0] * torch.sigmoid(qg[..., D:])).reshape(B, -1), L["w_o"], L.get("w_o@packed"))
+        ops.ring_write(proj[:, hq: hq + KVH * D].view(B, KVH, D), proj[:, hq + KVH * D:].view(B, KVH, D), L["k_norm"],
+                       cos, sin, ring_rows, positions, self.ring_k[i], self.ring_v[i], self.ring_pos[i],
+                       c.rotary_dim, c.rms_eps)
+        att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i], gate=qg[..., D:])
+        out = ops.linear(att.reshape(B, -1), L["w_o"], L.get("w_o@packed"))
         mq, mgate, mk, mv, mscores = self._memory_decode(L, hidden, cos, sin)
-        read = ops.memory_read(mq[:, None], self.memory[i])
+        read = ops.memory_read(mq[:, None], self.memory[i], valid=valid, head_gate=mgate)
         ops.memory_commit(mk[:, None], mv[:, None], mscores[:, None], valid, c.memory_chunk, self.memory[i])
-        read = read[:, 0] * valid[:, None, None].to(read.dtype)
-        mem_out = ops.linear((read * mgate[..., None].to(read.dtype)).reshape(B, -1), L["m_o"], L.get("m_o@packed"))
-        return out + mem_out
+        return ops.linear(read.reshape(B, -1), L["m_o"], L.get("m_o@packed"), residual=out)
 
     def decode_step(self, tokens, positions, valid):
         """One token for every slot: tokens, positions [B] int64, valid [B] bool
