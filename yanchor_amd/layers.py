@@ -178,9 +178,11 @@ _linear_ws: dict = {}
 
 
 def _linear_workspace(device, nbytes):
-    """Per-device split-K workspace, grown on demand (every partial the reduce
-    reads is written first, so it needs no clearing)."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
+    """Split-K workspace per (device, stream), grown on demand (every partial
+    the reduce reads is written first, so it needs no clearing); projections
+    on different streams never share one."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(device).cuda_stream)
     ws = _linear_ws.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -214,8 +216,7 @@ def linear(x, w, split_k=None, residual=None):
     bf16 or a PackedWeight): torch.nn.functional.linear without bias on the
     skinny-projection kernels; with ``residual`` ([M, N] bf16, unit last
     stride) out = bf16(x . w^T) + residual.  The split-K workspace is cached
-    per device: concurrent calls on different streams of one device must not
-    overlap."""
+    per (device, stream)."""
     packed = isinstance(w, PackedWeight)
     _bf16(x, w.data if packed else w, residual)
     if not packed and residual is not None:

@@ -318,12 +318,14 @@ class Model:
     """Random-init 4B-shaped hybrid recurrent model with its decode caches."""
 
     def __init__(self, cfg: ModelConfig, batch: int, device, *, seed=0, ops=None, dtype=torch.bfloat16,
-                 init="normal"):
+                 init="normal", overlap=True):
         """``init="normal"`` draws every weight from N(0, init_std);
         ``init="tiled"`` repeats one 16M-value N(0, init_std) block (fast on a
         host, for timing runs where the values do not matter)."""
         self.cfg, self.B, self.device, self.dtype = cfg, int(batch), torch.device(device), dtype
         self.ops = ops if ops is not None else HipOps()
+        self.overlap = overlap
+        self._side = None
         gen = torch.Generator(device=self.device).manual_seed(seed)
         std = cfg.init_std
         block = None
@@ -493,9 +495,18 @@ class Model:
     def _attn_decode(self, i, L, xn, hidden, positions, cos, sin, valid, ring_rows):
         """SWA + anchor-memory mixer for one token per slot.  xn is the
         normalised layer input, hidden the residual stream entering the layer;
-        ring_rows[b] = b * kv_heads * window + positions[b] % window."""
+        ring_rows[b] = b * kv_heads * window + positions[b] % window.  On a GPU
+        the memory path (its own norm, projections, read and commit) runs on a
+        second stream beside the SWA path; they meet at the memory output
+        projection."""
         c, B, ops = self.cfg, xn.shape[0], self.ops
         H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
+        side = self._side_stream(xn)
+        if side is not None:
+            main = torch.cuda.current_stream(xn.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                read = self._memory_path(i, L, hidden, cos, sin, valid)
         proj = ops.linear(xn, L["w_qkv"])                                    # [B, (q|gate) per head | k | v]
         hq = 2 * H * D
         qg = proj[:, :hq].view(B, H, 2 * D)
@@ -505,10 +516,27 @@ class Model:
                        c.rotary_dim, c.rms_eps)
         att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i], gate=qg[..., D:])
         out = ops.linear(att.reshape(B, -1), L["w_o"], L.get("w_o@packed"))
+        if side is None:
+            read = self._memory_path(i, L, hidden, cos, sin, valid)
+        else:
+            main.wait_stream(side)
+            read.record_stream(main)
+        return ops.linear(read.reshape(B, -1), L["m_o"], L.get("m_o@packed"), residual=out)
+
+    def _memory_path(self, i, L, hidden, cos, sin, valid):
+        """Anchor-memory read (gated) and commit of one decode token per slot."""
+        c, ops = self.cfg, self.ops
         mq, mgate, mk, mv, mscores = self._memory_decode(L, hidden, cos, sin)
         read = ops.memory_read(mq[:, None], self.memory[i], valid=valid, head_gate=mgate)
         ops.memory_commit(mk[:, None], mv[:, None], mscores[:, None], valid, c.memory_chunk, self.memory[i])
-        return ops.linear(read.reshape(B, -1), L["m_o"], L.get("m_o@packed"), residual=out)
+        return read
+
+    def _side_stream(self, x):
+        if not (getattr(self, "overlap", False) and x.is_cuda):
+            return None
+        if getattr(self, "_side", None) is None:
+            self._side = torch.cuda.Stream(device=x.device)   # default priority
+        return self._side
 
     def decode_step(self, tokens, positions, valid):
         """One token for every slot: tokens, positions [B] int64, valid [B] bool
