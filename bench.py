@@ -179,6 +179,9 @@ class _OracleOps:
         out = torch.nn.functional.linear(x, w)
         return out if residual is None else out + residual
 
+    def mlp_act(self, x, w, packed=None):
+        return self.silu_mul(torch.nn.functional.linear(x, w))
+
     def gdn_decode(self, q, k, v, g, beta, state):
         o, st = self.gdn_ref.recurrent_gated_delta_rule(q, k, v, g, beta, state, dtype=torch.float32)
         state.copy_(st)

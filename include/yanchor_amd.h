@@ -304,20 +304,26 @@ int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split
  * yh_linear_pack: w [N, K] bf16 row-major -> packed [N * K] bf16 with
  *   packed[((T * K/32 + kb) * 64 + l) * 8 + e] = w[16 T + l % 16][32 kb + 8 (l / 16) + e]
  *   (column tile T of 16 outputs, K block kb of 32; lane l of a 16x16x32 MFMA
- *   B operand).  N % 16 == 0, K % 32 == 0.
+ *   B operand).  N % 16 == 0, K % 32 == 0.  With pair_halves the tiles
+ *   alternate between the row halves of w (tile 2j = rows 16j.., tile 2j+1 =
+ *   rows N/2 + 16j..; N % 32 == 0): the layout of a [gate; up] MLP weight for
+ *   the silu epilogue.
  * yh_linear_packed: out[M, N] = x[M, K] . W^T from the packed weights; split_k
  *   slices K in whole 128-wide phases (yh_linear_packed_split gives the
  *   library's choice); with more than one slice the workspace must hold
  *   split_k * M * N * 4 bytes (16-byte aligned) and the partial sums are added
  *   in a fixed order.  residual (NULL = none) [M, N] bf16, rows residual_stride
  *   apart: out = bf16(bf16(x . W^T) + residual), the decode layers'
- *   `z = x + proj(...)` adds (modeling_yanchor.py:159, 903-905).
+ *   `z = x + proj(...)` adds (modeling_yanchor.py:159, 903-905).  silu_pairs
+ *   (weights packed with pair_halves, split_k == 1, no residual): out is
+ *   [M, N/2] = bf16(bf16(silu(gate)) * up), the MLP activation
+ *   (inference_kernels.py:642-666) in the projection's store.
  *   Requirements: 0 <= M <= 128, N % 16 == 0, K % 128 == 0.
  */
-int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, yh_stream_t stream);
+int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, int pair_halves, yh_stream_t stream);
 int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride, int64_t M,
-                     int64_t N, int64_t K, const void* residual, int64_t residual_stride, int64_t split_k,
-                     void* workspace, int64_t workspace_bytes, yh_stream_t stream);
+                     int64_t N, int64_t K, const void* residual, int64_t residual_stride, int silu_pairs,
+                     int64_t split_k, void* workspace, int64_t workspace_bytes, yh_stream_t stream);
 int yh_linear_packed_split(int64_t M, int64_t N, int64_t K);
 
 /* Sampling semantics of yh_topk_sample. */

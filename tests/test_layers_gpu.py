@@ -290,3 +290,22 @@ def test_linear_packed_residual(gpu, split):
     bound = (ref.float().abs() + prod.float().abs()) * 2.0 ** -7
     assert ((got.float() - ref.float()).abs() <= bound * 1.0001 + 1e-30).all()
     assert (got != ref).float().mean().item() <= 0.05
+
+
+@pytest.mark.parametrize("m,i,k", [(128, 9728, 2560), (37, 256, 384), (1, 32, 128)])
+def test_linear_silu_matches_gemm_then_silu_mul(gpu, m, i, k):
+    """The MLP activation from the paired packing equals F.linear followed by
+    the silu_mul formulation (to 1 bf16 ulp of the products, which the
+    activation then carries)."""
+    x = rnd(m, k, dev=gpu, seed=m + i)
+    w = rnd(2 * i, k, dev=gpu, scale=0.05, seed=k + i)
+    got = layers.linear_silu(x, layers.PackedWeight(w, pair_halves=True))
+    gu = (x.float() @ w.float().t()).to(torch.bfloat16)
+    ref = TorchGlue.silu_mul(gu)
+    g, u = gu.float().chunk(2, -1)
+    # a 1-ulp change of gate / up moves the activation by about that ulp times
+    # the other factor
+    bound = ref.float().abs() * 2.0 ** -7 + (u.abs() + g.abs()) * (g.abs() + u.abs()) * 2.0 ** -7
+    assert got.shape == ref.shape
+    assert ((got.float() - ref.float()).abs() <= bound * 1.0001 + 1e-30).all()
+    assert (got != ref).float().mean().item() <= 0.05

@@ -53,6 +53,7 @@ struct LinArgs {
   int M, N, K, S, chunks_per_slice;
   const uint16_t* res;  // optional residual [M, N], rows rs apart: out = bf16(bf16(x . W^T) + res)
   int64_t rs;
+  int silu_pairs;       // packed gate|up pairs: out[M, N/2] = bf16(bf16(silu(gate)) * up)
 };
 
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
@@ -375,6 +376,23 @@ __device__ __forceinline__ void pk_add_half(f32x4v (&acc)[MT][2], const f32x4v* 
 template <int MT, int T0, int T1>
 __device__ __forceinline__ void pk_store_rows(const f32x4v (&acc)[MT][2], const LinArgs& a, int quad,
                                               const int (&ncol)[2], int slice) {
+  if (a.silu_pairs) {
+    // column tiles 2j (gate) and 2j+1 (up) of intermediate columns 16j.. are
+    // this wave's two tiles; the activation is F.silu(gate) * up in bf16
+    if (ncol[0] >= a.N) return;
+    const int col = ncol[0] % 16, j = ncol[0] / 32;
+#pragma unroll
+    for (int t = T0; t < T1; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = t * 16 + quad * 4 + i;
+        if (m >= a.M) continue;
+        const float g = bf16_to_f32(f32_to_bf16(acc[t][0][i])), u = bf16_to_f32(f32_to_bf16(acc[t][1][i]));
+        const float sg = bf16_to_f32(f32_to_bf16(g / (1.f + expf(-g))));
+        a.out[m * a.os + j * 16 + col] = f32_to_bf16(sg * u);
+      }
+    return;
+  }
   float* mine = a.S == 1 ? nullptr : a.part + static_cast<int64_t>(slice) * a.M * a.N;
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
@@ -389,8 +407,9 @@ __device__ __forceinline__ void pk_store_rows(const f32x4v (&acc)[MT][2], const 
           float y = acc[t][ct][i];
           if (a.res) y = bf16_to_f32(f32_to_bf16(y)) + bf16_to_f32(a.res[m * a.rs + ncol[ct]]);
           a.out[m * a.os + ncol[ct]] = f32_to_bf16(y);
+        } else {
+          mine[static_cast<int64_t>(m) * a.N + ncol[ct]] = acc[t][ct][i];
         }
-        else mine[static_cast<int64_t>(m) * a.N + ncol[ct]] = acc[t][ct][i];
       }
   }
 }
@@ -456,12 +475,17 @@ __global__ void __launch_bounds__(kPkThreads) packed_linear_kernel(LinArgs a) {
 }
 
 // W [N, K] row-major -> packed fragment order; one thread per 16-byte piece.
-__global__ void __launch_bounds__(256) linear_pack_kernel(const uint16_t* w, uint16_t* packed, int64_t N, int64_t K) {
+// With pair_halves the column tiles alternate between the two row halves of W
+// (tile 2j = rows 16j.., tile 2j+1 = rows N/2 + 16j..), so a wave holds a
+// gate tile and its up tile.
+__global__ void __launch_bounds__(256) linear_pack_kernel(const uint16_t* w, uint16_t* packed, int64_t N, int64_t K,
+                                                          int pair_halves) {
   const int64_t piece = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // packed order
   if (piece >= N * K / 8) return;
   const int64_t l = piece & 63, blk = piece >> 6;  // blk = T * K/32 + kb
   const int64_t kbs = K / 32, T = blk / kbs, kb = blk % kbs;
-  const int64_t row = T * 16 + (l & 15), k = kb * 32 + (l >> 4) * 8;
+  const int64_t src_tile = pair_halves ? (T & 1) * (N / 32) + (T >> 1) : T;
+  const int64_t row = src_tile * 16 + (l & 15), k = kb * 32 + (l >> 4) * 8;
   reinterpret_cast<uint4*>(packed)[piece] = *reinterpret_cast<const uint4*>(w + row * K + k);
 }
 
@@ -545,9 +569,11 @@ extern "C" int yh_linear(const void* x, int64_t x_stride, const void* w, void* o
   return YH_OK;
 }
 
-extern "C" int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, yh_stream_t stream) {
+extern "C" int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, int pair_halves,
+                              yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0, "linear_pack: N must be a multiple of 16, K of 32");
+  YH_CHECK_ARG(!pair_halves || N % 32 == 0, "linear_pack: paired halves need N % 32 == 0");
   YH_CHECK_ARG(w && packed && w != packed, "linear_pack: null or aliased pointer");
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(packed)) & 15) == 0,
                "linear_pack: tensors must be 16-byte aligned");
@@ -555,7 +581,7 @@ extern "C" int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K,
   YH_CHECK_ARG((pieces + 255) / 256 < (1LL << 31), "linear_pack: too large");
   hipLaunchKernelGGL(linear_pack_kernel, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), static_cast<uint16_t*>(packed),
-                     N, K);
+                     N, K, pair_halves);
   YH_CHECK_LAUNCH("linear_pack");
   return YH_OK;
 }
@@ -567,12 +593,16 @@ extern "C" int yh_linear_packed_split(int64_t M, int64_t N, int64_t K) {
 
 extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride,
                                 int64_t M, int64_t N, int64_t K, const void* residual, int64_t residual_stride,
-                                int64_t split_k, void* workspace, int64_t workspace_bytes, yh_stream_t stream) {
+                                int silu_pairs, int64_t split_k, void* workspace, int64_t workspace_bytes,
+                                yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(M >= 0 && M <= kMaxM, "linear_packed: M must be in [0, %d] (got %lld)", kMaxM, (long long)M);
   YH_CHECK_ARG(N > 0 && N % 16 == 0, "linear_packed: N must be a positive multiple of 16");
   YH_CHECK_ARG(K > 0 && K % kPhK == 0, "linear_packed: K must be a positive multiple of %d", kPhK);
-  YH_CHECK_ARG(x_stride >= K && x_stride % 8 == 0 && out_stride >= N, "linear_packed: bad strides");
+  YH_CHECK_ARG(x_stride >= K && x_stride % 8 == 0 && out_stride >= (silu_pairs ? N / 2 : N),
+               "linear_packed: bad strides");
+  YH_CHECK_ARG(!silu_pairs || (N % 32 == 0 && !residual && split_k == 1),
+               "linear_packed: the silu epilogue needs N % 32 == 0, no residual and split_k == 1");
   const int64_t phases = K / kPhK;
   YH_CHECK_ARG(split_k >= 1 && split_k <= phases, "linear_packed: split_k must be in [1, K/%d]", kPhK);
   if (M == 0) return YH_OK;
@@ -593,7 +623,7 @@ extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_p
                "linear_packed: bad residual stride / alignment");
   LinArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_packed), static_cast<uint16_t*>(out),
             S > 1 ? static_cast<float*>(workspace) : nullptr, x_stride, out_stride, (int)M, (int)N, (int)K, S,
-            static_cast<int>(pps * kPh), static_cast<const uint16_t*>(residual), residual_stride};
+            static_cast<int>(pps * kPh), static_cast<const uint16_t*>(residual), residual_stride, silu_pairs};
   const dim3 grid(static_cast<unsigned>((N + kNT - 1) / kNT), static_cast<unsigned>(S));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int mt = static_cast<int>((M + 15) / 16);

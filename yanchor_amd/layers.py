@@ -174,6 +174,26 @@ def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, re
     return q, gate, scores
 
 
+def linear_silu(x, w):
+    """The MLP activation F.silu(x . gate^T) * (x . up^T) in bf16 (torch
+    rounding points kept) from a [gate; up] weight packed with pair_halves:
+    x [M, K] bf16 (M <= 128) -> [M, N/2]."""
+    if not isinstance(w, PackedWeight) or not w.pair_halves:
+        raise ValueError("linear_silu takes a PackedWeight packed with pair_halves")
+    _bf16(x)
+    n, k = w.shape
+    if x.ndim != 2 or x.shape[1] != k:
+        raise ValueError("linear_silu expects x [M, K]")
+    m = x.shape[0]
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    dev = N.require_device(x, w.data)
+    out = torch.empty(m, n // 2, dtype=x.dtype, device=dev)
+    N.call("yh_linear_packed", x.data_ptr(), x.stride(0), w.data.data_ptr(), out.data_ptr(), n // 2, m, n, k, None, 0,
+           1, 1, None, 0, N.stream_of(x))
+    return out
+
+
 _linear_ws: dict = {}
 
 
@@ -195,20 +215,25 @@ class PackedWeight:
     order (yh_linear_pack), for the decode projection kernel: ``linear(x, pw)``
     takes it in place of the row-major weight.  N % 16 == 0, K % 128 == 0."""
 
-    def __init__(self, w):
+    def __init__(self, w, pair_halves=False):
+        """``pair_halves``: w is [gate; up] (two halves of N/2 rows) and the
+        tiles are interleaved for ``linear_silu``."""
         _bf16(w)
-        if w.ndim != 2 or w.shape[0] % 16 or w.shape[1] % 128:
-            raise ValueError("packed weights need [N, K] with N % 16 == 0 and K % 128 == 0")
+        if w.ndim != 2 or w.shape[0] % (32 if pair_halves else 16) or w.shape[1] % 128:
+            raise ValueError("packed weights need [N, K] with N % 16 (paired: 32) == 0 and K % 128 == 0")
         N.require_device(w)
         self.shape = tuple(w.shape)
         self.dtype = w.dtype
+        self.pair_halves = bool(pair_halves)
         self.data = torch.empty(w.numel(), dtype=w.dtype, device=w.device)
         wc = w.contiguous()
-        N.call("yh_linear_pack", wc.data_ptr(), self.data.data_ptr(), self.shape[0], self.shape[1], N.stream_of(wc))
+        N.call("yh_linear_pack", wc.data_ptr(), self.data.data_ptr(), self.shape[0], self.shape[1],
+               int(self.pair_halves), N.stream_of(wc))
 
     @staticmethod
-    def fits(w):
-        return (w.dtype == torch.bfloat16 and w.ndim == 2 and w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0)
+    def fits(w, pair_halves=False):
+        return (w.dtype == torch.bfloat16 and w.ndim == 2 and w.shape[0] % (32 if pair_halves else 16) == 0
+                and w.shape[1] % 128 == 0)
 
 
 def linear(x, w, split_k=None, residual=None):
@@ -218,6 +243,8 @@ def linear(x, w, split_k=None, residual=None):
     stride) out = bf16(x . w^T) + residual.  The split-K workspace is cached
     per (device, stream)."""
     packed = isinstance(w, PackedWeight)
+    if packed and w.pair_halves:
+        raise ValueError("weights packed with pair_halves serve linear_silu")
     _bf16(x, w.data if packed else w, residual)
     if not packed and residual is not None:
         return linear(x, w, split_k) + residual
@@ -241,7 +268,7 @@ def linear(x, w, split_k=None, residual=None):
         nbytes = s * m * n * 4 if s > 1 else 0
         ws = _linear_workspace(dev, nbytes) if nbytes else None
         N.call("yh_linear_packed", x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), n, m, n, k,
-               N.ptr(residual), 0 if residual is None else residual.stride(0), s, N.ptr(ws),
+               N.ptr(residual), 0 if residual is None else residual.stride(0), 0, s, N.ptr(ws),
                0 if ws is None else ws.numel(), N.stream_of(x))
         return out
     s = int(split_k) if split_k is not None else N.lib().yh_linear_split(m, n, k)

@@ -132,8 +132,9 @@ class HipOps:
         stay for prefill."""
         for L in model.layers:
             for name in self.PACKED:
-                if name in L and self.layers.PackedWeight.fits(L[name]):
-                    L[name + "@packed"] = self.layers.PackedWeight(L[name])
+                pair = name == "mlp_gate_up"   # [gate; up]: tiles interleaved for the fused silu * up
+                if name in L and self.layers.PackedWeight.fits(L[name], pair):
+                    L[name + "@packed"] = self.layers.PackedWeight(L[name], pair_halves=pair)
         if self.layers.PackedWeight.fits(model.lm_head):
             model.lm_head_packed = self.layers.PackedWeight(model.lm_head)
 
@@ -145,6 +146,13 @@ class HipOps:
             return self.layers.linear(x, packed, residual=residual)
         out = F.linear(x, w)
         return out if residual is None else out + residual
+
+    def mlp_act(self, x, w, packed=None):
+        """silu(x . gate^T) * (x . up^T) of the [gate; up] MLP weight: one
+        launch on the packed weights (decode batch), else GEMM + silu_mul."""
+        if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128:
+            return self.layers.linear_silu(x, packed)
+        return self.silu_mul(F.linear(x, w))
 
     def ring_write(self, k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rotary_dim, eps):
         if k.dtype != torch.bfloat16:
@@ -419,7 +427,7 @@ class Model:
     # ---------------- layers ----------------
     def _mlp(self, L, x):
         ops = self.ops
-        return ops.linear(ops.silu_mul(ops.linear(x, L["mlp_gate_up"], L.get("mlp_gate_up@packed"))), L["mlp_down"],
+        return ops.linear(ops.mlp_act(x, L["mlp_gate_up"], L.get("mlp_gate_up@packed")), L["mlp_down"],
                           L.get("mlp_down@packed"))
 
     def _gdn_split(self, L, proj):
@@ -436,7 +444,7 @@ class Model:
         """GDN mixer for one token per slot; xn is the normalised layer input."""
         c, B, ops = self.cfg, xn.shape[0], self.ops
         hv, dv, vd = c.gdn_heads_v, c.gdn_dv, c.gdn_heads_v * c.gdn_dv
-        proj = self.ops.linear(xn, L["w_in"])                                     # [B, qkv | z | b | a]
+        proj = self.ops.linear(xn, L["w_in"], L.get("w_in@packed"))                                     # [B, qkv | z | b | a]
         q, k, v, g, beta = ops.gdn_prep(proj, self.conv_state[i], L["conv_w"], L["a_log"], L["dt_bias"],
                                         conv_dim=c.conv_dim, qk_dim=c.gdn_heads_k * c.gdn_dk, hv=hv,
                                         b_offset=c.conv_dim + vd, a_offset=c.conv_dim + vd + hv)
@@ -481,13 +489,13 @@ class Model:
         c, B, ops = self.cfg, hidden.shape[0], self.ops
         H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
         u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
-        proj = ops.linear(u, L["m_in"])                                    # [q | admission features | gate | up]
+        proj = ops.linear(u, L["m_in"], L.get("m_in@packed"))                                    # [q | admission features | gate | up]
         qd, ad = H * D, c.admission_rank
         q, gate, scores = ops.memory_prologue(proj, H, qd, ad, L["m_q_norm"], cos, sin, L["read_scale"],
                                               L["read_gate_w"], L["read_gate_b"], L["adm_up"], c.rotary_dim,
                                               c.rms_eps)
         zz = ops.linear(ops.silu_mul(proj[:, qd + ad:]), L["writer_down"], L.get("writer_down@packed"), residual=u)
-        kv = ops.linear(zz, L["m_kv"])
+        kv = ops.linear(zz, L["m_kv"], L.get("m_kv@packed"))
         key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
                                  c.rms_eps)
         return q, gate, key, kv[:, KVH * D:].reshape(B, KVH, D), scores
@@ -507,7 +515,7 @@ class Model:
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 read = self._memory_path(i, L, hidden, cos, sin, valid)
-        proj = ops.linear(xn, L["w_qkv"])                                    # [B, (q|gate) per head | k | v]
+        proj = ops.linear(xn, L["w_qkv"], L.get("w_qkv@packed"))                                    # [B, (q|gate) per head | k | v]
         hq = 2 * H * D
         qg = proj[:, :hq].view(B, H, 2 * D)
         q = ops.head_norm_rope(qg[..., :D], L["q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
