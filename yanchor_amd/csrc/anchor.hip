@@ -23,8 +23,6 @@
 namespace yh {
 namespace {
 
-constexpr int kReadThreads = 256;
-constexpr int kReadWaves = kReadThreads / kWave;
 constexpr int kMaxCap = 1024;
 
 struct ReadArgs {
@@ -104,6 +102,40 @@ __device__ __forceinline__ void ld_raw8(Raw8<DT>& r, const void* p, int64_t i) {
     r.w[0] = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i)[0];
   }
 }
+// Dot product of 8 packed 16-bit elements, fp32 accumulation (dot2 pairs).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <int DT>
+__device__ __forceinline__ float dot8(const Raw8<DT>& a, const Raw8<DT>& b) {
+  const uint32_t x[4] = {a.w[0].x, a.w[0].y, a.w[0].z, a.w[0].w};
+  const uint32_t y[4] = {b.w[0].x, b.w[0].y, b.w[0].z, b.w[0].w};
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (DT == YH_BF16)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x[j]), __builtin_bit_cast(bf16x2_t, y[j]),
+                                            acc, false);
+    else
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x[j]), __builtin_bit_cast(f16x2_t, y[j]), acc, false);
+  }
+  return acc;
+}
+
+// The NI rows of one block: row pointer p (this lane's 8 elements of the
+// block's first row), rows `stride` elements apart -- constant offsets from
+// one base, so the loads need no per-row address registers.
+template <int DT, int NI, int STRIDE>
+__device__ __forceinline__ void ld_block(Raw8<DT> (&r)[NI], const void* p) {
+  constexpr int kEsz = DT == YH_F32 ? 4 : 2;
+  const char* c = static_cast<const char*>(p);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+#pragma unroll
+    for (int j = 0; j < (DT == YH_F32 ? 2 : 1); ++j)
+      r[i].w[j] = *reinterpret_cast<const uint4*>(c + static_cast<int64_t>(i) * STRIDE * kEsz + j * 16);
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ void zero_raw8(Raw8<DT>& r) {
 #pragma unroll
@@ -148,8 +180,15 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 // value 0:
 //   out = sum_w acc_w e^{m_w - M} / (e^{-M} + sum_w l_w e^{m_w - M}),
 //   M = max(0, max_w m_w).
+// 4 waves per workgroup, two workgroups per CU (register budget of two waves
+// per SIMD).
+template <bool SINK> constexpr int read_waves() { return 4; }
+
 template <int DT, int D, int R, bool SINK>
-__global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
+__global__ void __launch_bounds__(read_waves<SINK>() * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+anchor_read_kernel(ReadArgs a) {
+  constexpr int kReadWaves = read_waves<SINK>();
+  constexpr int kReadThreads = kReadWaves * 64;
   constexpr int LPR = D / 8;
   constexpr int RPI = kWave / LPR;
   constexpr int BS = 32;
@@ -174,17 +213,25 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
     return;
   }
   const int32_t* pos = a.pos + b * a.p_rs + static_cast<int64_t>(g) * a.KC;  // slots of (b, g)
-  const int64_t kbase = b * a.k_rs + static_cast<int64_t>(g) * a.KC * D + rr * D + s * 8;
-  const int64_t vbase = b * a.v_rs + static_cast<int64_t>(g) * a.KC * D + rr * D + s * 8;
+  constexpr int kEsz = DT == YH_F32 ? 4 : 2;
+  const char* kptr = static_cast<const char*>(a.keys) +
+                     (b * a.k_rs + static_cast<int64_t>(g) * a.KC * D + rr * D + s * 8) * kEsz;
+  const char* vptr = static_cast<const char*>(a.values) +
+                     (b * a.v_rs + static_cast<int64_t>(g) * a.KC * D + rr * D + s * 8) * kEsz;
 
-  float qf[R][8];
+  // 16-bit queries stay packed (dot2 instructions take bf16 / fp16 pairs and
+  // accumulate in fp32; the 1/sqrt(D) scale is applied to the summed logit);
+  // fp32 queries are pre-scaled
+  Raw8<DT> qraw[R];
+  float qf[DT == YH_F32 ? R : 1][8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    Raw8<DT> raw;
-    ld_raw8<DT>(raw, a.q, qbase + static_cast<int64_t>(r) * D + s * 8);
-    cvt8<DT>(raw, qf[r]);
+    ld_raw8<DT>(qraw[r], a.q, qbase + static_cast<int64_t>(r) * D + s * 8);
+    if constexpr (DT == YH_F32) {
+      cvt8<DT>(qraw[r], qf[r]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qf[r][j] *= a.scale;
+      for (int j = 0; j < 8; ++j) qf[r][j] *= a.scale;
+    }
   }
 
   float m_run[R], l_run[R], acc[R][8];
@@ -203,11 +250,9 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
     // counts derived at the loop head are those of the steady state
     __builtin_amdgcn_sched_barrier(0);
     int32_t pcur = pos[wid * BS + (lane & (BS - 1))];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) ld_raw8<DT>(kr[i], a.keys, kbase + static_cast<int64_t>(wid * BS + i * RPI) * D);
+    ld_block<DT, NI, RPI * D>(kr, kptr + static_cast<int64_t>(wid * BS) * D * kEsz);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < NI; ++i) ld_raw8<DT>(vr[i], a.values, vbase + static_cast<int64_t>(wid * BS + i * RPI) * D);
+    ld_block<DT, NI, RPI * D>(vr, vptr + static_cast<int64_t>(wid * BS) * D * kEsz);
     __builtin_amdgcn_sched_barrier(0);
     for (int blk = wid; blk < nblk; blk += kReadWaves) {
       const int nxt = (blk + kReadWaves < nblk ? blk + kReadWaves : blk) * BS;  // past the end: this block again
@@ -215,22 +260,26 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
       float part[R][NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        float kf[8];
-        cvt8<DT>(kr[i], kf);
+        if constexpr (DT == YH_F32) {
+          float kf[8];
+          cvt8<DT>(kr[i], kf);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float x = 0.f;
+          for (int r = 0; r < R; ++r) {
+            float x = 0.f;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) x = fmaf(qf[r][j], kf[j], x);
-          part[r][i] = x;
+            for (int j = 0; j < 8; ++j) x = fmaf(qf[r][j], kf[j], x);
+            part[r][i] = x;
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < R; ++r) part[r][i] = dot8<DT>(qraw[r], kr[i]);
         }
       }
       // the keys and positions of the next block (sched_barrier: issued here,
       // not sunk to their use in the next iteration)
       __builtin_amdgcn_sched_barrier(0);
       pcur = pos[nxt + (lane & (BS - 1))];
-#pragma unroll
-      for (int i = 0; i < NI; ++i) ld_raw8<DT>(kr[i], a.keys, kbase + static_cast<int64_t>(nxt + i * RPI) * D);
+      ld_block<DT, NI, RPI * D>(kr, kptr + static_cast<int64_t>(nxt) * D * kEsz);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int m = LPR / 2, h = NI / 2; m >= 1; m >>= 1, h >>= 1) {
@@ -256,7 +305,7 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
       float pw[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float logit = mine_live ? part[r][0] : -INFINITY;
+        const float logit = mine_live ? (DT == YH_F32 ? part[r][0] : part[r][0] * a.scale) : -INFINITY;
         const float bm = wave_max(logit);
         const float m_new = fmaxf(m_run[r], bm);
         const float m_safe = m_new == -INFINITY ? 0.f : m_new;
@@ -286,8 +335,7 @@ __global__ void __launch_bounds__(kReadThreads) anchor_read_kernel(ReadArgs a) {
       }
       // the values of the next block
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < NI; ++i) ld_raw8<DT>(vr[i], a.values, vbase + static_cast<int64_t>(nxt + i * RPI) * D);
+      ld_block<DT, NI, RPI * D>(vr, vptr + static_cast<int64_t>(nxt) * D * kEsz);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -489,7 +537,7 @@ __global__ void anchor_advance_kernel(int64_t* count, int64_t* total, const uint
 
 template <int DT, int D, bool SINK>
 int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(kReadThreads);
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(read_waves<SINK>() * 64);
   switch (R) {
     case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK>), grid, block, 0, st, a); break;
     case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK>), grid, block, 0, st, a); break;

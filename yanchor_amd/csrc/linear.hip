@@ -230,13 +230,26 @@ __global__ void __launch_bounds__(256) linear_reduce_kernel(const float* part, u
   const int64_t m = e / per_row, c = (e % per_row) * 4;
   const float* p = part + m * N + c;
   const int64_t plane = static_cast<int64_t>(M) * N;
-  float4 sum = *reinterpret_cast<const float4*>(p);
-  for (int s = 1; s < S; ++s) {
-    const float4 v = *reinterpret_cast<const float4*>(p + s * plane);
-    sum.x += v.x;
-    sum.y += v.y;
-    sum.z += v.z;
-    sum.w += v.w;
+  // planes are loaded eight at a time (all in flight together), then added
+  // in slice order
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j < S) v[j] = *reinterpret_cast<const float4*>(p + (s0 + j) * plane);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (s0 + j >= S) break;
+      if (s0 + j == 0) {
+        sum = v[0];
+      } else {
+        sum.x += v[j].x;
+        sum.y += v[j].y;
+        sum.z += v[j].z;
+        sum.w += v[j].w;
+      }
+    }
   }
   if (res) {  // the product is a bf16 tensor before the residual add
     const uint2 r = *reinterpret_cast<const uint2*>(res + m * rs + c);
