@@ -175,7 +175,7 @@ class _OracleOps:
             setattr(self, name, getattr(TorchGlue, name))
 
     @staticmethod
-    def linear(x, w, packed=None, residual=None):
+    def linear(x, w, packed=None, residual=None, defer=False):
         out = torch.nn.functional.linear(x, w)
         return out if residual is None else out + residual
 

@@ -323,7 +323,8 @@ int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split
 int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, int pair_halves, yh_stream_t stream);
 int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride, int64_t M,
                      int64_t N, int64_t K, const void* residual, int64_t residual_stride, int silu_pairs,
-                     int64_t split_k, void* workspace, int64_t workspace_bytes, yh_stream_t stream);
+                     int64_t split_k, void* workspace, int64_t workspace_bytes, int defer_reduce,
+                     int64_t* slices_out, yh_stream_t stream);
 int yh_linear_packed_split(int64_t M, int64_t N, int64_t K);
 
 /* Sampling semantics of yh_topk_sample. */
@@ -457,6 +458,19 @@ int yh_gather_rows(int n_tensors, const void* const* src, void* const* dst, cons
  */
 int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual, void* residual_out, const void* w, void* out,
                int64_t out_stride, int64_t N, int64_t D, float eps, int plus_one, yh_stream_t stream);
+
+/*
+ * yh_rmsnorm whose input row is a split-K projection still in fp32 partials
+ * (yh_linear_packed with defer_reduce): x = bf16(sum over the S planes of
+ * part [S, N, D] in slice order), x = bf16(x + proj_residual) when given (the
+ * projection's own residual add), then as yh_rmsnorm with `residual`.  The
+ * reduce of the projection and the norm after it in one launch (no reference
+ * counterpart: the reference runs the projection, the adds and the norm as
+ * separate ops).
+ */
+int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual, int64_t proj_residual_stride,
+                        const void* residual, void* residual_out, const void* w, void* out, int64_t out_stride,
+                        int64_t N, int64_t D, float eps, int plus_one, yh_stream_t stream);
 
 /*
  * GDN decode prologue for B rows of the packed projection proj [B, proj_stride]

@@ -309,3 +309,20 @@ def test_linear_silu_matches_gemm_then_silu_mul(gpu, m, i, k):
     assert got.shape == ref.shape
     assert ((got.float() - ref.float()).abs() <= bound * 1.0001 + 1e-30).all()
     assert (got != ref).float().mean().item() <= 0.05
+
+
+@pytest.mark.parametrize("with_res", [False, True])
+def test_deferred_split_k_into_rmsnorm_is_exact(gpu, with_res):
+    """A projection whose split-K reduce is left to the following RMSNorm
+    gives bit for bit what the reduce kernel + RMSNorm give."""
+    x = rnd(128, 4096, dev=gpu, seed=90)
+    pw = layers.PackedWeight(rnd(2560, 4096, dev=gpu, scale=0.02, seed=91))
+    r = rnd(128, 2560, dev=gpu, seed=92) if with_res else None
+    h = rnd(128, 2560, dev=gpu, seed=93)
+    w = rnd(2560, dev=gpu, scale=0.1, seed=94)
+    p = layers.linear(x, pw, split_k=8, residual=r, defer=True)
+    assert isinstance(p, layers.Partials) and p.part.shape[0] > 1
+    got, got_h = layers.rmsnorm(p, w, 1e-6, residual=h)
+    ref, ref_h = layers.rmsnorm(layers.linear(x, pw, split_k=8, residual=r), w, 1e-6, residual=h)
+    assert torch.equal(got, ref) and torch.equal(got_h, ref_h)
+    assert torch.is_tensor(layers.linear(x, pw, split_k=1, residual=r, defer=True))   # one slice: nothing deferred

@@ -49,10 +49,16 @@ __device__ __forceinline__ float block_sum256(float x) {
 // s = residual ? bf16(x + residual) : x; residual_out = s;
 // out = bf16(s / sqrt(mean(s^2) + eps) * (1 + w)).
 constexpr int kNormMaxVec = 4;  // 8-element vectors per thread
+// x may instead come as S fp32 split-K partial planes of a projection (part
+// [S, rows, D]; x = bf16(sum in slice order), plus an optional residual of the
+// projection: x = bf16(x + res1)), so the projection's reduce needs no launch
+// of its own.
 __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(const uint16_t* x, const uint16_t* res,
                                                                uint16_t* res_out, const uint16_t* w, uint16_t* out,
                                                                int D, int64_t x_stride, int64_t out_stride,
-                                                               float eps, int plus_one) {
+                                                               float eps, int plus_one, const float* part, int S,
+                                                               int64_t plane, const uint16_t* res1,
+                                                               int64_t res1_stride) {
   const int64_t row = blockIdx.x;
   const int nvec = D / 8;
   float v[kNormMaxVec][8];
@@ -61,7 +67,40 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(const uint16_t* x
   for (int i = 0; i < kNormMaxVec; ++i) {
     const int c = threadIdx.x + i * kNormThreads;
     if (c < nvec) {
-      const uint4 a = *reinterpret_cast<const uint4*>(x + row * x_stride + c * 8);
+      uint4 a;
+      if (part) {
+        float acc[8];
+        const float* pp = part + row * D + c * 8;
+        for (int s0 = 0; s0 < S; s0 += 4) {  // four planes in flight, added in slice order
+          float4 lo[4], hi[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (s0 + q < S) {
+              lo[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * plane);
+              hi[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * plane + 4);
+            }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (s0 + q >= S) break;
+            const float f[8] = {lo[q].x, lo[q].y, lo[q].z, lo[q].w, hi[q].x, hi[q].y, hi[q].z, hi[q].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = s0 + q == 0 ? f[j] : acc[j] + f[j];
+          }
+        }
+        uint16_t xh[8];
+        if (res1) {
+          const uint4 r1 = *reinterpret_cast<const uint4*>(res1 + row * res1_stride + c * 8);
+          const uint16_t* r1h = reinterpret_cast<const uint16_t*>(&r1);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xh[j] = tobf(bf(tobf(acc[j])) + bf(r1h[j]));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xh[j] = tobf(acc[j]);
+        }
+        a = *reinterpret_cast<const uint4*>(xh);
+      } else {
+        a = *reinterpret_cast<const uint4*>(x + row * x_stride + c * 8);
+      }
       const uint16_t* ah = reinterpret_cast<const uint16_t*>(&a);
       if (res) {
         const uint4 r = *reinterpret_cast<const uint4*>(res + row * D + c * 8);
@@ -331,8 +370,32 @@ extern "C" int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
                      static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
                      static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), (int)D, x_stride, out_stride, eps,
-                     plus_one);
+                     plus_one, nullptr, 0, 0, nullptr, 0);
   YH_CHECK_LAUNCH("rmsnorm");
+  return YH_OK;
+}
+
+extern "C" int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual,
+                                   int64_t proj_residual_stride, const void* residual, void* residual_out,
+                                   const void* w, void* out, int64_t out_stride, int64_t N, int64_t D, float eps,
+                                   int plus_one, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(w && N >= 0 && S >= 1 && (N == 0 || (part && out)), "rmsnorm_partials: bad arguments");
+  YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= 8 * kNormThreads * kNormMaxVec,
+               "rmsnorm_partials: D must be a multiple of 8 up to %d", 8 * kNormThreads * kNormMaxVec);
+  YH_CHECK_ARG(out_stride % 8 == 0 && (!proj_residual || proj_residual_stride % 8 == 0),
+               "rmsnorm_partials: strides must be multiples of 8 elements");
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w) |
+                 reinterpret_cast<uintptr_t>(proj_residual) | reinterpret_cast<uintptr_t>(residual) |
+                 reinterpret_cast<uintptr_t>(residual_out)) & 15) == 0,
+               "rmsnorm_partials: pointers must be 16-byte aligned");
+  if (N == 0) return YH_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(N)), dim3(kNormThreads), 0,
+                     static_cast<hipStream_t>(stream), nullptr, static_cast<const uint16_t*>(residual),
+                     static_cast<uint16_t*>(residual_out), static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out),
+                     (int)D, D, out_stride, eps, plus_one, part, (int)S, N * D,
+                     static_cast<const uint16_t*>(proj_residual), proj_residual_stride);
+  YH_CHECK_LAUNCH("rmsnorm_partials");
   return YH_OK;
 }
 

@@ -607,7 +607,7 @@ extern "C" int yh_linear_packed_split(int64_t M, int64_t N, int64_t K) {
 extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride,
                                 int64_t M, int64_t N, int64_t K, const void* residual, int64_t residual_stride,
                                 int silu_pairs, int64_t split_k, void* workspace, int64_t workspace_bytes,
-                                yh_stream_t stream) {
+                                int defer_reduce, int64_t* slices_out, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(M >= 0 && M <= kMaxM, "linear_packed: M must be in [0, %d] (got %lld)", kMaxM, (long long)M);
   YH_CHECK_ARG(N > 0 && N % 16 == 0, "linear_packed: N must be a positive multiple of 16");
@@ -618,7 +618,10 @@ extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_p
                "linear_packed: the silu epilogue needs N % 32 == 0, no residual and split_k == 1");
   const int64_t phases = K / kPhK;
   YH_CHECK_ARG(split_k >= 1 && split_k <= phases, "linear_packed: split_k must be in [1, K/%d]", kPhK);
-  if (M == 0) return YH_OK;
+  if (M == 0) {
+    if (slices_out) *slices_out = 1;
+    return YH_OK;
+  }
   YH_CHECK_ARG(x && w_packed && out, "linear_packed: null pointer");
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed)) & 15) == 0,
                "linear_packed: x and the packed weights must be 16-byte aligned");
@@ -646,7 +649,8 @@ extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_p
     default: hipLaunchKernelGGL(packed_linear_kernel<8>, grid, dim3(kPkThreads), 0, st, a); break;
   }
   YH_CHECK_LAUNCH("linear_packed");
-  if (S > 1) {
+  if (slices_out) *slices_out = S;
+  if (S > 1 && !defer_reduce) {
     const int64_t quads = M * N / 4;
     hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0, st,
                        a.part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N, S, a.res, a.rs);

@@ -8,6 +8,8 @@ formulation it replaces (cited per function).
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _native as N
@@ -24,6 +26,8 @@ def rmsnorm(x, w, eps, residual=None, plus_one=True):
     ``residual``: s = x + residual is formed first and ``(norm(s), s)`` is
     returned (the fused residual RMSNorm, runtime/model/inference_kernels.py:
     1767-1797)."""
+    if isinstance(x, Partials):
+        return _rmsnorm_partials(x, w, eps, residual, plus_one)
     _bf16(x, w, residual)
     d = x.shape[-1]
     if x.stride(-1) != 1 or (x.ndim > 1 and x.stride(-2) % 8):
@@ -41,6 +45,24 @@ def rmsnorm(x, w, eps, residual=None, plus_one=True):
         x_stride = d
     N.call("yh_rmsnorm", x.data_ptr(), x_stride, N.ptr(residual), N.ptr(res_out), w.data_ptr(), out.data_ptr(), d,
            rows, d, float(eps), int(plus_one), N.stream_of(x))
+    return out if residual is None else (out, res_out)
+
+
+def _rmsnorm_partials(p, w, eps, residual, plus_one):
+    _bf16(w, residual, p.residual)
+    m, d = p.shape
+    N.require_device(p.part, w, residual, p.residual)
+    out = torch.empty(m, d, dtype=torch.bfloat16, device=p.device)
+    res_out = None
+    if residual is not None:
+        residual = residual.contiguous()
+        res_out = torch.empty_like(residual)
+    r1 = p.residual
+    if r1 is not None and (r1.stride(-1) != 1 or r1.stride(0) % 8 or r1.data_ptr() % 16):
+        r1 = r1.contiguous()
+    N.call("yh_rmsnorm_partials", p.part.data_ptr(), p.part.shape[0], N.ptr(r1), 0 if r1 is None else r1.stride(0),
+           N.ptr(residual), N.ptr(res_out), w.data_ptr(), out.data_ptr(), d, m, d, float(eps), int(plus_one),
+           N.stream_of(p.part))
     return out if residual is None else (out, res_out)
 
 
@@ -190,7 +212,7 @@ def linear_silu(x, w):
     dev = N.require_device(x, w.data)
     out = torch.empty(m, n // 2, dtype=x.dtype, device=dev)
     N.call("yh_linear_packed", x.data_ptr(), x.stride(0), w.data.data_ptr(), out.data_ptr(), n // 2, m, n, k, None, 0,
-           1, 1, None, 0, N.stream_of(x))
+           1, 1, None, 0, 0, None, N.stream_of(x))
     return out
 
 
@@ -236,12 +258,26 @@ class PackedWeight:
                 and w.shape[1] % 128 == 0)
 
 
-def linear(x, w, split_k=None, residual=None):
+class Partials:
+    """A projection x . W^T (+ residual) still in S fp32 split-K planes
+    ``part`` [S, M, N] in the stream's workspace: consume it with ``rmsnorm``
+    before the next projection on the same stream."""
+
+    def __init__(self, part, residual):
+        self.part, self.residual = part, residual
+        self.shape = tuple(part.shape[1:])
+        self.dtype = torch.bfloat16
+        self.device = part.device
+
+
+def linear(x, w, split_k=None, residual=None, defer=False):
     """out = x . w^T for a decode batch (x [M, K] bf16 with M <= 128, w [N, K]
     bf16 or a PackedWeight): torch.nn.functional.linear without bias on the
     skinny-projection kernels; with ``residual`` ([M, N] bf16, unit last
     stride) out = bf16(x . w^T) + residual.  The split-K workspace is cached
-    per (device, stream)."""
+    per (device, stream).  ``defer`` (packed weights): when K is split, return
+    the fp32 partials as a ``Partials`` for ``rmsnorm`` to sum (one launch
+    less)."""
     packed = isinstance(w, PackedWeight)
     if packed and w.pair_halves:
         raise ValueError("weights packed with pair_halves serve linear_silu")
@@ -267,9 +303,13 @@ def linear(x, w, split_k=None, residual=None):
         s = int(split_k) if split_k is not None else N.lib().yh_linear_packed_split(m, n, k)
         nbytes = s * m * n * 4 if s > 1 else 0
         ws = _linear_workspace(dev, nbytes) if nbytes else None
+        slices = ctypes.c_int64(1)
         N.call("yh_linear_packed", x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), n, m, n, k,
                N.ptr(residual), 0 if residual is None else residual.stride(0), 0, s, N.ptr(ws),
-               0 if ws is None else ws.numel(), N.stream_of(x))
+               0 if ws is None else ws.numel(), int(defer), ctypes.byref(slices), N.stream_of(x))
+        if defer and slices.value > 1:
+            part = ws[: slices.value * m * n * 4].view(torch.float32).view(slices.value, m, n)
+            return Partials(part, residual)
         return out
     s = int(split_k) if split_k is not None else N.lib().yh_linear_split(m, n, k)
     nbytes = N.lib().yh_linear_workspace_bytes(m, n, k, s)

@@ -95,6 +95,9 @@ class HipOps:
     # served configuration).  A float32 model (used to pin the cache logic
     # without bf16 rounding) runs the torch formulations of the same layers.
     def rmsnorm(self, x, w, eps, residual=None):
+        """x may be a projection's deferred split-K partials (``linear(...,
+        defer=True)``): the reduce, the projection's residual, the residual
+        add and the norm then run as one launch."""
         if x.dtype != torch.bfloat16:
             return TorchGlue.rmsnorm(x, w, eps, residual)
         return self.layers.rmsnorm(x, w, eps, residual=residual)
@@ -138,12 +141,14 @@ class HipOps:
         if self.layers.PackedWeight.fits(model.lm_head):
             model.lm_head_packed = self.layers.PackedWeight(model.lm_head)
 
-    def linear(self, x, w, packed=None, residual=None):
+    def linear(self, x, w, packed=None, residual=None, defer=False):
         """out = x . w^T (+ residual, added to the bf16 product): the
         packed-weight kernel for a decode batch (bf16, <= 128 rows) when a
-        packed copy exists, torch (hipBLASLt) otherwise."""
+        packed copy exists, torch (hipBLASLt) otherwise.  ``defer``: the
+        result is only ever fed to ``rmsnorm``, which may then do the split-K
+        reduce itself."""
         if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128:
-            return self.layers.linear(x, packed, residual=residual)
+            return self.layers.linear(x, packed, residual=residual, defer=defer)
         out = F.linear(x, w)
         return out if residual is None else out + residual
 
@@ -425,10 +430,10 @@ class Model:
         return out
 
     # ---------------- layers ----------------
-    def _mlp(self, L, x):
+    def _mlp(self, L, x, defer=False):
         ops = self.ops
         return ops.linear(ops.mlp_act(x, L["mlp_gate_up"], L.get("mlp_gate_up@packed")), L["mlp_down"],
-                          L.get("mlp_down@packed"))
+                          L.get("mlp_down@packed"), defer=defer)
 
     def _gdn_split(self, L, proj):
         c = self.cfg
@@ -451,7 +456,7 @@ class Model:
         o = ops.gdn_decode(q.view(B, 1, c.gdn_heads_k, c.gdn_dk), k.view(B, 1, c.gdn_heads_k, c.gdn_dk),
                            v.view(B, 1, hv, dv), g[:, None], beta[:, None], self.gdn_state[i])
         y = ops.gated_rmsnorm(o.view(B, hv, dv), proj[:, c.conv_dim: c.conv_dim + vd], L["gnorm"], c.rms_eps)
-        return self.ops.linear(y, L["w_out"], L.get("w_out@packed"))
+        return self.ops.linear(y, L["w_out"], L.get("w_out@packed"), defer=True)
 
     def _attn_project(self, L, x, cos, sin):
         c = self.cfg
@@ -529,7 +534,7 @@ class Model:
         else:
             main.wait_stream(side)
             read.record_stream(main)
-        return ops.linear(read.reshape(B, -1), L["m_o"], L.get("m_o@packed"), residual=out)
+        return ops.linear(read.reshape(B, -1), L["m_o"], L.get("m_o@packed"), residual=out, defer=True)
 
     def _memory_path(self, i, L, hidden, cos, sin, valid):
         """Anchor-memory read (gated) and commit of one decode token per slot."""
@@ -562,7 +567,7 @@ class Model:
                 delta = self._attn_decode(i, L, xn, h, positions, cos, sin, valid, ring_rows)
             xn, h = ops.rmsnorm(delta, L["post_norm"], c.rms_eps, residual=h)
             nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
-            xn, h = ops.rmsnorm(self._mlp(L, xn), nxt, c.rms_eps, residual=h)
+            xn, h = ops.rmsnorm(self._mlp(L, xn, defer=True), nxt, c.rms_eps, residual=h)
         return ops.linear(xn, self.lm_head, self.lm_head_packed).float()
 
     # ---------------- prefill ----------------
