@@ -176,7 +176,9 @@ int yh_window_attend_gated(const void* query, const void* keys, const void* valu
  * _advance) in runtime/model/independent_memory.py:90-175, 190-201 and the
  * torch branch modeling_yanchor.py:291-312.
  *
- *   key, value  [B, G, D] (dtype);  score [B, G] float32;  active uint8/bool [B]
+ *   key, value  [B, G, D] (dtype), batch rows key_row_stride / value_row_stride
+ *               elements apart (<= 0: G * D, dense);  score [B, G] float32;
+ *               active uint8/bool [B]
  *   indices     NULL or int32 [B] (row -> state row; < 0 skips the row)
  *   keys, values [NB, G, capacity, D]; scores float [NB, G, capacity];
  *   positions int32 [NB, G, capacity]; pending_keys, pending_values
@@ -201,8 +203,8 @@ int yh_anchor_commit(const void* key, const void* value, const float* score, con
                      const int32_t* indices, void* keys, void* values, float* scores, int32_t* positions,
                      void* pending_keys, void* pending_values, float* pending_scores, int64_t* count,
                      int64_t* total, int64_t B, int64_t G, int64_t capacity, int64_t pending_capacity,
-                     int64_t chunk, int64_t D, int64_t n_state_rows, const int64_t* row_strides, int dtype,
-                     yh_stream_t stream);
+                     int64_t chunk, int64_t D, int64_t n_state_rows, const int64_t* row_strides,
+                     int64_t key_row_stride, int64_t value_row_stride, int dtype, yh_stream_t stream);
 
 /*
  * Anchor memory, prefill read: each query of a C-token block attends over the
@@ -463,14 +465,17 @@ int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual, void* resi
  * yh_rmsnorm whose input row is a split-K projection still in fp32 partials
  * (yh_linear_packed with defer_reduce): x = bf16(sum over the S planes of
  * part [S, N, D] in slice order), x = bf16(x + proj_residual) when given (the
- * projection's own residual add), then as yh_rmsnorm with `residual`.  The
- * reduce of the projection and the norm after it in one launch (no reference
- * counterpart: the reference runs the projection, the adds and the norm as
- * separate ops).
+ * projection's own residual add), then as yh_rmsnorm with `residual`.  With
+ * w2 / out2 (both or neither) the same row is also normed with the weight w2
+ * into out2 (contiguous [N, D]): the decode layers whose memory path norms
+ * the layer input with its own weight.  The reduce of the projection and the
+ * norms after it in one launch (no reference counterpart: the reference runs
+ * the projection, the adds and each norm as separate ops).
  */
 int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual, int64_t proj_residual_stride,
                         const void* residual, void* residual_out, const void* w, void* out, int64_t out_stride,
-                        int64_t N, int64_t D, float eps, int plus_one, yh_stream_t stream);
+                        int64_t N, int64_t D, float eps, int plus_one, const void* w2, void* out2,
+                        yh_stream_t stream);
 
 /*
  * GDN decode prologue for B rows of the packed projection proj [B, proj_stride]

@@ -72,8 +72,10 @@ def test_read_empty_and_indirect(gpu):
     assert rel_err(got[2], want[2]) <= 2e-2
 
 
-def _drive(gpu, st, steps, chunk, seed, indices=None, tie_scores=False, p_active=0.9):
-    """Run `steps` decode pushes on GPU and oracle, comparing after each."""
+def _drive(gpu, st, steps, chunk, seed, indices=None, tie_scores=False, p_active=0.9, fused_kv=False):
+    """Run `steps` decode pushes on GPU and oracle, comparing after each.
+    fused_kv: the device key / value are the two halves of one [B, 1, 2G, D]
+    row (batch rows 2 G D elements apart, as a fused k/v projection)."""
     b_rows = st.count.shape[0] if indices is None else indices.shape[0]
     g, d = st.keys.shape[1], st.keys.shape[3]
     gen = torch.Generator().manual_seed(seed)
@@ -93,7 +95,13 @@ def _drive(gpu, st, steps, chunk, seed, indices=None, tie_scores=False, p_active
         will = [(int(o_state.count[i if indices is None else int(indices[i])]) + 1 == chunk) and bool(active[i])
                 and (indices is None or int(indices[i]) >= 0) for i in range(b_rows)]
         commits += sum(will)
-        im.commit_decode(key.to(gpu), val.to(gpu), sc.to(gpu), active.to(gpu), chunk, dev_state, dev_idx)
+        if fused_kv:
+            kv = torch.cat((key, val), 2).to(gpu)
+            dk, dv = kv[:, :, :g], kv[:, :, g:]
+            assert dk.stride(0) == 2 * g * d and not dv.is_contiguous()
+        else:
+            dk, dv = key.to(gpu), val.to(gpu)
+        im.commit_decode(dk, dv, sc.to(gpu), active.to(gpu), chunk, dev_state, dev_idx)
         ref.commit_decode(key, val, sc, active, chunk, o_state, indices)
         torch.cuda.synchronize()
         _assert_state_equal(dev_state, o_state)
@@ -116,6 +124,13 @@ def test_commit_decode_config_chunk64(gpu):
     """256 committed slots, commit chunk 64, 128-d bf16 (the decode layout)."""
     st = workloads.anchor_state(4, 4, 256, 64, 128, seed=25, fill_pending=60)
     assert _drive(gpu, st, 10, 64, seed=26, p_active=1.0) >= 4
+
+
+def test_commit_fused_kv_rows(gpu):
+    """Key / value read in place from the halves of a fused projection row."""
+    st = workloads.anchor_state(4, 8, 64, 8, 128, seed=29, fill_pending=3)
+    idx = torch.tensor([3, 1, -1, 0], dtype=torch.int32)
+    assert _drive(gpu, st, 24, 8, seed=30, indices=idx, fused_kv=True) > 2
 
 
 def test_commit_fp32_rows(gpu):

@@ -311,18 +311,35 @@ def test_linear_silu_matches_gemm_then_silu_mul(gpu, m, i, k):
     assert (got != ref).float().mean().item() <= 0.05
 
 
-@pytest.mark.parametrize("with_res", [False, True])
-def test_deferred_split_k_into_rmsnorm_is_exact(gpu, with_res):
+@pytest.mark.parametrize("with_res,split", [(False, 8), (True, 8), (True, 3), (True, 13), (False, 32)])
+def test_deferred_split_k_into_rmsnorm_is_exact(gpu, with_res, split):
     """A projection whose split-K reduce is left to the following RMSNorm
-    gives bit for bit what the reduce kernel + RMSNorm give."""
+    gives bit for bit what the reduce kernel + RMSNorm give (slice counts on
+    both sides of the in-flight plane groups of 4, 8 and 16)."""
     x = rnd(128, 4096, dev=gpu, seed=90)
     pw = layers.PackedWeight(rnd(2560, 4096, dev=gpu, scale=0.02, seed=91))
     r = rnd(128, 2560, dev=gpu, seed=92) if with_res else None
     h = rnd(128, 2560, dev=gpu, seed=93)
     w = rnd(2560, dev=gpu, scale=0.1, seed=94)
-    p = layers.linear(x, pw, split_k=8, residual=r, defer=True)
+    p = layers.linear(x, pw, split_k=split, residual=r, defer=True)
     assert isinstance(p, layers.Partials) and p.part.shape[0] > 1
     got, got_h = layers.rmsnorm(p, w, 1e-6, residual=h)
-    ref, ref_h = layers.rmsnorm(layers.linear(x, pw, split_k=8, residual=r), w, 1e-6, residual=h)
+    ref, ref_h = layers.rmsnorm(layers.linear(x, pw, split_k=split, residual=r), w, 1e-6, residual=h)
     assert torch.equal(got, ref) and torch.equal(got_h, ref_h)
     assert torch.is_tensor(layers.linear(x, pw, split_k=1, residual=r, defer=True))   # one slice: nothing deferred
+
+
+@pytest.mark.parametrize("split", [1, 8])
+def test_rmsnorm_second_weight(gpu, split):
+    """w2: the same residual sum normed with a second weight, equal to a
+    separate RMSNorm of that sum (one launch from partials, two otherwise)."""
+    x = rnd(128, 4096, dev=gpu, seed=95)
+    pw = layers.PackedWeight(rnd(2560, 4096, dev=gpu, scale=0.02, seed=96))
+    h = rnd(128, 2560, dev=gpu, seed=97)
+    w, w2 = rnd(2560, dev=gpu, scale=0.1, seed=98), rnd(2560, dev=gpu, scale=0.1, seed=99)
+    p = layers.linear(x, pw, split_k=split, defer=True)
+    got, got_h, got_u = layers.rmsnorm(p, w, 1e-6, residual=h, w2=w2)
+    ref, ref_h = layers.rmsnorm(layers.linear(x, pw, split_k=split), w, 1e-6, residual=h)
+    assert torch.equal(got, ref) and torch.equal(got_h, ref_h)
+    assert torch.equal(got_u, layers.rmsnorm(ref_h, w2, 1e-6))
+    ulp_check(got_u, TorchGlue.rmsnorm(ref_h, w2, 1e-6))

@@ -33,7 +33,7 @@ SIGNATURES: dict[str, list] = {
     "yh_anchor_read": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_window_attend": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_anchor_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
-                         _i64, _i64, _i64, _p, _i32, _p],
+                         _i64, _i64, _i64, _p, _i64, _i64, _i32, _p],
     "yh_anchor_prefix": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "yh_anchor_sequence_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i32, _p],
@@ -41,7 +41,7 @@ SIGNATURES: dict[str, list] = {
     "yh_linear": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "yh_linear_pack": [_p, _p, _i64, _i64, _i32, _p],
     "yh_linear_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i64, _p, _i64, _i32, _p, _p],
-    "yh_rmsnorm_partials": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p],
+    "yh_rmsnorm_partials": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _p],
     "yh_ring_write": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                       _f32, _p],
     "yh_memory_prologue": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,

@@ -396,6 +396,7 @@ struct CommitArgs {
   int B, G, KC, PC, C, D, esize;
   int64_t n_rows;
   int64_t rs[9];  // row strides (elements) in IndependentMemoryState field order
+  int64_t key_rs, value_rs;  // elements between batch rows of key / value
 };
 
 enum { kRsKeys, kRsValues, kRsScores, kRsPos, kRsPKeys, kRsPValues, kRsPScores, kRsCount, kRsTotal };
@@ -464,8 +465,8 @@ __global__ void __launch_bounds__(kCommitThreads) anchor_commit_kernel(CommitArg
   const int64_t rowbytes = static_cast<int64_t>(a.D) * a.esize;
   char* pk = static_cast<char*>(a.pkeys) + b * a.rs[kRsPKeys] * a.esize + static_cast<int64_t>(g) * a.PC * rowbytes;
   char* pv = static_cast<char*>(a.pvalues) + b * a.rs[kRsPValues] * a.esize + static_cast<int64_t>(g) * a.PC * rowbytes;
-  const char* src_k = static_cast<const char*>(a.key) + (static_cast<int64_t>(row) * a.G + g) * rowbytes;
-  const char* src_v = static_cast<const char*>(a.value) + (static_cast<int64_t>(row) * a.G + g) * rowbytes;
+  const char* src_k = static_cast<const char*>(a.key) + (row * a.key_rs + static_cast<int64_t>(g) * a.D) * a.esize;
+  const char* src_v = static_cast<const char*>(a.value) + (row * a.value_rs + static_cast<int64_t>(g) * a.D) * a.esize;
   float* ps = a.pscores + b * a.rs[kRsPScores] + static_cast<int64_t>(g) * a.PC;
   const float new_score = a.score[static_cast<int64_t>(row) * a.G + g];
   // push
@@ -647,7 +648,8 @@ extern "C" int yh_anchor_commit(const void* key, const void* value, const float*
                                 void* pending_values, float* pending_scores, int64_t* count,
                                 int64_t* total, int64_t B, int64_t G, int64_t capacity,
                                 int64_t pending_capacity, int64_t chunk, int64_t D, int64_t n_state_rows,
-                                const int64_t* row_strides, int dtype, yh_stream_t stream) {
+                                const int64_t* row_strides, int64_t key_row_stride, int64_t value_row_stride,
+                                int dtype, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(key && value && score && active && keys && values && scores && positions && pending_keys &&
                    pending_values && pending_scores && count && total,
@@ -671,7 +673,11 @@ extern "C" int yh_anchor_commit(const void* key, const void* value, const float*
                             G * pending_capacity * D, G * pending_capacity * D, G * pending_capacity, 1, 1};
   CommitArgs a{key, value, score, active, indices, keys, values, scores, positions, pending_keys, pending_values,
                pending_scores, count, total, (int)B, (int)G, (int)capacity, (int)pending_capacity, (int)chunk,
-               (int)D, esize, n_state_rows, {}};
+               (int)D, esize, n_state_rows, {}, key_row_stride > 0 ? key_row_stride : G * D,
+               value_row_stride > 0 ? value_row_stride : G * D};
+  YH_CHECK_ARG(a.key_rs >= G * D && a.value_rs >= G * D && (a.key_rs * esize) % 16 == 0 &&
+                   (a.value_rs * esize) % 16 == 0,
+               "anchor_commit: key/value batch rows must hold G x D elements and keep 16-byte alignment");
   for (int i = 0; i < 9; ++i) {
     a.rs[i] = row_strides ? row_strides[i] : dense[i];
     YH_CHECK_ARG(a.rs[i] >= dense[i], "anchor_commit: row stride %d (%lld) is smaller than one state row", i,

@@ -29,110 +29,137 @@ __device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float(static_
 __device__ __forceinline__ uint16_t tobf(float x) { return f32_to_bf16(x); }
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
 
-constexpr int kNormThreads = 256;
-
-// Block-wide fp32 sum for 256 threads.
-__device__ __forceinline__ float block_sum256(float x) {
-  __shared__ float part[kNormThreads / kWave];
-  x = wave_sum(x);
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  if (lane == 0) part[w] = x;
-  __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int i = 0; i < kNormThreads / kWave; ++i) t += part[i];
-  __syncthreads();
-  return t;
-}
-
-// One workgroup per row of D bf16 elements (D % 8 == 0, D <= 8 * 256 * 4).
+// RMSNorm rows: one workgroup per row, one 8-element vector per thread
+// (blockDim = D / 8 rounded up to whole waves, D <= 8192), so a row's loads
+// are all issued before the first is consumed.
 // s = residual ? bf16(x + residual) : x; residual_out = s;
-// out = bf16(s / sqrt(mean(s^2) + eps) * (1 + w)).
-constexpr int kNormMaxVec = 4;  // 8-element vectors per thread
+// out = bf16(s / sqrt(mean(s^2) + eps) * (1 + w)); out2 the same with w2.
 // x may instead come as S fp32 split-K partial planes of a projection (part
 // [S, rows, D]; x = bf16(sum in slice order), plus an optional residual of the
 // projection: x = bf16(x + res1)), so the projection's reduce needs no launch
 // of its own.
-__global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(const uint16_t* x, const uint16_t* res,
-                                                               uint16_t* res_out, const uint16_t* w, uint16_t* out,
-                                                               int D, int64_t x_stride, int64_t out_stride,
-                                                               float eps, int plus_one, const float* part, int S,
-                                                               int64_t plane, const uint16_t* res1,
-                                                               int64_t res1_stride) {
+constexpr int kNormMaxThreads = 1024;
+constexpr int kNormMaxD = 8 * kNormMaxThreads;
+
+struct NormArgs {
+  const uint16_t* x;
+  int64_t x_stride;
+  const float* part;       // [S, rows, D] or null
+  int64_t plane;
+  int S;
+  const uint16_t* res1;    // projection residual (with part) or null
+  int64_t res1_stride;
+  const uint16_t* res;     // residual stream [rows, D] or null
+  uint16_t* res_out;
+  const uint16_t* w;
+  uint16_t* out;
+  int64_t out_stride;
+  const uint16_t* w2;      // optional second weight: out2 [rows, D]
+  uint16_t* out2;
+  int D, plus_one;
+  float eps;
+};
+
+// Block-wide fp32 sum (blockDim a multiple of 64, at most 1024).
+__device__ __forceinline__ float block_sum(float x) {
+  __shared__ float part[kNormMaxThreads / kWave];
+  x = wave_sum(x);
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  if (lane == 0) part[w] = x;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += part[i];
+  return t;
+}
+
+__device__ __forceinline__ void add_f4(float* acc, float4 lo, float4 hi) {
+  acc[0] += lo.x; acc[1] += lo.y; acc[2] += lo.z; acc[3] += lo.w;
+  acc[4] += hi.x; acc[5] += hi.y; acc[6] += hi.z; acc[7] += hi.w;
+}
+
+// SG = partial planes loaded per round (0: x is a bf16 row); 16 planes in
+// flight need the registers of at most 512 threads (D <= 4096).
+template <int SG>
+__global__ void __launch_bounds__(SG > 8 ? 512 : kNormMaxThreads) rmsnorm_kernel(NormArgs a) {
   const int64_t row = blockIdx.x;
-  const int nvec = D / 8;
-  float v[kNormMaxVec][8];
+  const int c = threadIdx.x, D = a.D;
+  const bool on = c < D / 8;
+  float v[8];
   float ss = 0.f;
+  if (on) {
+    uint4 xa, ra = {}, r1a = {};
+    if (a.res) ra = *reinterpret_cast<const uint4*>(a.res + row * D + c * 8);
+    if constexpr (SG > 0) {
+      if (a.res1) r1a = *reinterpret_cast<const uint4*>(a.res1 + row * a.res1_stride + c * 8);
+      const float* pp = a.part + row * D + c * 8;
+      float acc[8];
+      for (int s0 = 0; s0 < a.S; s0 += SG) {  // SG planes in flight, added in slice order
+        float4 lo[SG], hi[SG];
 #pragma unroll
-  for (int i = 0; i < kNormMaxVec; ++i) {
-    const int c = threadIdx.x + i * kNormThreads;
-    if (c < nvec) {
-      uint4 a;
-      if (part) {
-        float acc[8];
-        const float* pp = part + row * D + c * 8;
-        for (int s0 = 0; s0 < S; s0 += 4) {  // four planes in flight, added in slice order
-          float4 lo[4], hi[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (s0 + q < S) {
-              lo[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * plane);
-              hi[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * plane + 4);
-            }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (s0 + q >= S) break;
-            const float f[8] = {lo[q].x, lo[q].y, lo[q].z, lo[q].w, hi[q].x, hi[q].y, hi[q].z, hi[q].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = s0 + q == 0 ? f[j] : acc[j] + f[j];
+        for (int q = 0; q < SG; ++q)
+          if (s0 + q < a.S) {
+            lo[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * a.plane);
+            hi[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * a.plane + 4);
           }
-        }
-        uint16_t xh[8];
-        if (res1) {
-          const uint4 r1 = *reinterpret_cast<const uint4*>(res1 + row * res1_stride + c * 8);
-          const uint16_t* r1h = reinterpret_cast<const uint16_t*>(&r1);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) xh[j] = tobf(bf(tobf(acc[j])) + bf(r1h[j]));
+        if (s0 == 0) {
+          acc[0] = lo[0].x; acc[1] = lo[0].y; acc[2] = lo[0].z; acc[3] = lo[0].w;
+          acc[4] = hi[0].x; acc[5] = hi[0].y; acc[6] = hi[0].z; acc[7] = hi[0].w;
         } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) xh[j] = tobf(acc[j]);
+          add_f4(acc, lo[0], hi[0]);
         }
-        a = *reinterpret_cast<const uint4*>(xh);
-      } else {
-        a = *reinterpret_cast<const uint4*>(x + row * x_stride + c * 8);
+#pragma unroll
+        for (int q = 1; q < SG; ++q)
+          if (s0 + q < a.S) add_f4(acc, lo[q], hi[q]);
       }
-      const uint16_t* ah = reinterpret_cast<const uint16_t*>(&a);
-      if (res) {
-        const uint4 r = *reinterpret_cast<const uint4*>(res + row * D + c * 8);
-        const uint16_t* rh = reinterpret_cast<const uint16_t*>(&r);
-        uint16_t sh[8];
+      uint16_t xh[8];
+      const uint16_t* r1h = reinterpret_cast<const uint16_t*>(&r1a);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          sh[j] = tobf(bf(ah[j]) + bf(rh[j]));
-          v[i][j] = bf(sh[j]);
-        }
-        if (res_out) *reinterpret_cast<uint4*>(res_out + row * D + c * 8) = *reinterpret_cast<const uint4*>(sh);
-      } else {
+      for (int j = 0; j < 8; ++j) xh[j] = a.res1 ? tobf(bf(tobf(acc[j])) + bf(r1h[j])) : tobf(acc[j]);
+      xa = *reinterpret_cast<const uint4*>(xh);
+    } else {
+      xa = *reinterpret_cast<const uint4*>(a.x + row * a.x_stride + c * 8);
+    }
+    const uint16_t* xh = reinterpret_cast<const uint16_t*>(&xa);
+    if (a.res) {
+      const uint16_t* rh = reinterpret_cast<const uint16_t*>(&ra);
+      uint16_t sh[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[i][j] = bf(ah[j]);
+      for (int j = 0; j < 8; ++j) {
+        sh[j] = tobf(bf(xh[j]) + bf(rh[j]));
+        v[j] = bf(sh[j]);
       }
+      if (a.res_out) *reinterpret_cast<uint4*>(a.res_out + row * D + c * 8) = *reinterpret_cast<const uint4*>(sh);
+    } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], v[i][j], ss);
+      for (int j = 0; j < 8; ++j) v[j] = bf(xh[j]);
     }
-  }
-  const float r = rsqrtf(block_sum256(ss) / static_cast<float>(D) + eps);
 #pragma unroll
-  for (int i = 0; i < kNormMaxVec; ++i) {
-    const int c = threadIdx.x + i * kNormThreads;
-    if (c < nvec) {
-      const uint4 wv = *reinterpret_cast<const uint4*>(w + c * 8);
-      const uint16_t* wh = reinterpret_cast<const uint16_t*>(&wv);
-      uint16_t o[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = tobf(v[i][j] * r * (plus_one ? 1.f + bf(wh[j]) : bf(wh[j])));
-      *reinterpret_cast<uint4*>(out + row * out_stride + c * 8) = *reinterpret_cast<const uint4*>(o);
-    }
+    for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
   }
+  const float r = rsqrtf(block_sum(ss) / static_cast<float>(D) + a.eps);
+  if (!on) return;
+  const uint4 wv = *reinterpret_cast<const uint4*>(a.w + c * 8);
+  const uint16_t* wh = reinterpret_cast<const uint16_t*>(&wv);
+  uint16_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = tobf(v[j] * r * (a.plus_one ? 1.f + bf(wh[j]) : bf(wh[j])));
+  *reinterpret_cast<uint4*>(a.out + row * a.out_stride + c * 8) = *reinterpret_cast<const uint4*>(o);
+  if (a.out2) {
+    const uint4 w2v = *reinterpret_cast<const uint4*>(a.w2 + c * 8);
+    const uint16_t* w2h = reinterpret_cast<const uint16_t*>(&w2v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = tobf(v[j] * r * (a.plus_one ? 1.f + bf(w2h[j]) : bf(w2h[j])));
+    *reinterpret_cast<uint4*>(a.out2 + row * D + c * 8) = *reinterpret_cast<const uint4*>(o);
+  }
+}
+
+void launch_rmsnorm(const NormArgs& a, int64_t N, hipStream_t st) {
+  const unsigned threads = static_cast<unsigned>((a.D / 8 + kWave - 1) / kWave * kWave);
+  const dim3 grid(static_cast<unsigned>(N));
+  if (!a.part) hipLaunchKernelGGL(rmsnorm_kernel<0>, grid, dim3(threads), 0, st, a);
+  else if (a.S <= 4) hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(threads), 0, st, a);
+  else if (a.S <= 8 || threads > 512) hipLaunchKernelGGL(rmsnorm_kernel<8>, grid, dim3(threads), 0, st, a);
+  else hipLaunchKernelGGL(rmsnorm_kernel<16>, grid, dim3(threads), 0, st, a);
 }
 
 // grid (B, ceil(C / 256)): channel c of row b.  proj [B, P] (row stride P)
@@ -359,18 +386,17 @@ extern "C" int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual,
                           yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(w && N >= 0 && (N == 0 || (x && out)), "rmsnorm: bad arguments");
-  YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= 8 * kNormThreads * kNormMaxVec, "rmsnorm: D must be a multiple of 8 up to %d",
-               8 * kNormThreads * kNormMaxVec);
+  YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= kNormMaxD, "rmsnorm: D must be a multiple of 8 up to %d", kNormMaxD);
   YH_CHECK_ARG(x_stride % 8 == 0 && out_stride % 8 == 0, "rmsnorm: strides must be multiples of 8 elements");
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w) |
                  reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(residual_out)) & 15) == 0,
                "rmsnorm: pointers must be 16-byte aligned");
   if (N == 0) return YH_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(N)), dim3(kNormThreads), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
-                     static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
-                     static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), (int)D, x_stride, out_stride, eps,
-                     plus_one, nullptr, 0, 0, nullptr, 0);
+  NormArgs a{static_cast<const uint16_t*>(x), x_stride, nullptr, 0, 0, nullptr, 0,
+             static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
+             static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), out_stride, nullptr, nullptr,
+             (int)D, plus_one, eps};
+  launch_rmsnorm(a, N, static_cast<hipStream_t>(stream));
   YH_CHECK_LAUNCH("rmsnorm");
   return YH_OK;
 }
@@ -378,23 +404,25 @@ extern "C" int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual,
 extern "C" int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual,
                                    int64_t proj_residual_stride, const void* residual, void* residual_out,
                                    const void* w, void* out, int64_t out_stride, int64_t N, int64_t D, float eps,
-                                   int plus_one, yh_stream_t stream) {
+                                   int plus_one, const void* w2, void* out2, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(w && N >= 0 && S >= 1 && (N == 0 || (part && out)), "rmsnorm_partials: bad arguments");
-  YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= 8 * kNormThreads * kNormMaxVec,
-               "rmsnorm_partials: D must be a multiple of 8 up to %d", 8 * kNormThreads * kNormMaxVec);
+  YH_CHECK_ARG(!out2 == !w2, "rmsnorm_partials: out2 and w2 come together");
+  YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= kNormMaxD, "rmsnorm_partials: D must be a multiple of 8 up to %d",
+               kNormMaxD);
   YH_CHECK_ARG(out_stride % 8 == 0 && (!proj_residual || proj_residual_stride % 8 == 0),
                "rmsnorm_partials: strides must be multiples of 8 elements");
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w) |
                  reinterpret_cast<uintptr_t>(proj_residual) | reinterpret_cast<uintptr_t>(residual) |
-                 reinterpret_cast<uintptr_t>(residual_out)) & 15) == 0,
+                 reinterpret_cast<uintptr_t>(residual_out) | reinterpret_cast<uintptr_t>(w2) |
+                 reinterpret_cast<uintptr_t>(out2)) & 15) == 0,
                "rmsnorm_partials: pointers must be 16-byte aligned");
   if (N == 0) return YH_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(N)), dim3(kNormThreads), 0,
-                     static_cast<hipStream_t>(stream), nullptr, static_cast<const uint16_t*>(residual),
-                     static_cast<uint16_t*>(residual_out), static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out),
-                     (int)D, D, out_stride, eps, plus_one, part, (int)S, N * D,
-                     static_cast<const uint16_t*>(proj_residual), proj_residual_stride);
+  NormArgs a{nullptr, 0, part, N * D, (int)S, static_cast<const uint16_t*>(proj_residual), proj_residual_stride,
+             static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
+             static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), out_stride,
+             static_cast<const uint16_t*>(w2), static_cast<uint16_t*>(out2), (int)D, plus_one, eps};
+  launch_rmsnorm(a, N, static_cast<hipStream_t>(stream));
   YH_CHECK_LAUNCH("rmsnorm_partials");
   return YH_OK;
 }

@@ -189,12 +189,26 @@ def committed_gqa_gated(query, state: IndependentMemoryState, indices=None, vali
                state.positions.data_ptr(), N.ptr(idx), out.data_ptr(), b, h, g, cap, d, nb, rs[0], rs[1], rs[3],
                N.code(q), N.stream_of(q))
         return out
-    vd = None if valid is None else valid.to(torch.uint8).contiguous()
+    if valid is None or (valid.dtype == torch.bool and valid.is_contiguous()):
+        vd = valid                                   # bool is one byte, 0 / 1
+    else:
+        vd = valid.to(torch.uint8).contiguous()
     hg = None if head_gate is None else head_gate.to(torch.float32).contiguous()
     N.call("yh_anchor_read_gated", q.data_ptr(), state.keys.data_ptr(), state.values.data_ptr(),
            state.positions.data_ptr(), N.ptr(idx), out.data_ptr(), b, h, g, cap, d, nb, rs[0], rs[1], rs[3],
            N.ptr(vd), N.ptr(hg), N.code(q), N.stream_of(q))
     return out
+
+
+def _batch_rows(t):
+    """t [B, 1, G, D] as it is when its heads are contiguous and its batch rows
+    keep 16-byte alignment (e.g. the value half of a fused k/v projection),
+    a contiguous copy otherwise."""
+    _, _, g, d = t.shape
+    if t.stride(3) == 1 and t.stride(2) == d and t.stride(0) >= g * d and \
+            (t.stride(0) * t.element_size()) % 16 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    return t.contiguous()
 
 
 def commit_decode(key, value, scores, active, chunk, state: IndependentMemoryState, indices=None):
@@ -220,7 +234,7 @@ def commit_decode(key, value, scores, active, chunk, state: IndependentMemorySta
     idx = _indices(indices, b)
     if idx is None and nb < b:
         raise ValueError("memory state has fewer rows than the batch")
-    k, v = key.contiguous(), value.contiguous()
+    k, v = _batch_rows(key), _batch_rows(value)
     sc = scores.to(torch.float32).contiguous()
     act = active.to(torch.bool).contiguous()
     rs = (ctypes.c_int64 * 9)(*_row_strides(state))
@@ -228,7 +242,7 @@ def commit_decode(key, value, scores, active, chunk, state: IndependentMemorySta
            state.keys.data_ptr(), state.values.data_ptr(), state.scores.data_ptr(),
            state.positions.data_ptr(), state.pending_keys.data_ptr(), state.pending_values.data_ptr(),
            state.pending_scores.data_ptr(), state.count.data_ptr(), state.total.data_ptr(), b, g, cap, pc,
-           int(chunk), d, nb, rs, N.code(k), N.stream_of(k))
+           int(chunk), d, nb, rs, k.stride(0), v.stride(0), N.code(k), N.stream_of(k))
 
 
 def sequence(query, key, value, scores, valid, chunk, state: IndependentMemoryState):

@@ -21,13 +21,19 @@ def _bf16(*ts):
             raise ValueError("fused layer kernels take bfloat16 activations")
 
 
-def rmsnorm(x, w, eps, residual=None, plus_one=True):
+def rmsnorm(x, w, eps, residual=None, plus_one=True, w2=None):
     """Qwen3.5 RMSNorm over the last dim (x / rms(x) * (1 + w)).  With
     ``residual``: s = x + residual is formed first and ``(norm(s), s)`` is
     returned (the fused residual RMSNorm, runtime/model/inference_kernels.py:
-    1767-1797)."""
+    1767-1797).  ``w2``: the same row normed with a second weight is appended
+    to the result (one launch when x is split-K partials)."""
     if isinstance(x, Partials):
-        return _rmsnorm_partials(x, w, eps, residual, plus_one)
+        return _rmsnorm_partials(x, w, eps, residual, plus_one, w2)
+    if w2 is not None:
+        first = rmsnorm(x, w, eps, residual, plus_one)
+        if residual is None:
+            return first, rmsnorm(x, w2, eps, None, plus_one)
+        return first + (rmsnorm(first[1], w2, eps, None, plus_one),)
     _bf16(x, w, residual)
     d = x.shape[-1]
     if x.stride(-1) != 1 or (x.ndim > 1 and x.stride(-2) % 8):
@@ -48,11 +54,12 @@ def rmsnorm(x, w, eps, residual=None, plus_one=True):
     return out if residual is None else (out, res_out)
 
 
-def _rmsnorm_partials(p, w, eps, residual, plus_one):
-    _bf16(w, residual, p.residual)
+def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None):
+    _bf16(w, residual, p.residual, w2)
     m, d = p.shape
-    N.require_device(p.part, w, residual, p.residual)
+    N.require_device(p.part, w, residual, p.residual, w2)
     out = torch.empty(m, d, dtype=torch.bfloat16, device=p.device)
+    out2 = None if w2 is None else torch.empty_like(out)
     res_out = None
     if residual is not None:
         residual = residual.contiguous()
@@ -62,8 +69,10 @@ def _rmsnorm_partials(p, w, eps, residual, plus_one):
         r1 = r1.contiguous()
     N.call("yh_rmsnorm_partials", p.part.data_ptr(), p.part.shape[0], N.ptr(r1), 0 if r1 is None else r1.stride(0),
            N.ptr(residual), N.ptr(res_out), w.data_ptr(), out.data_ptr(), d, m, d, float(eps), int(plus_one),
-           N.stream_of(p.part))
-    return out if residual is None else (out, res_out)
+           N.ptr(w2), N.ptr(out2), N.stream_of(p.part))
+    res = (out,) if residual is None else (out, res_out)
+    res = res if out2 is None else res + (out2,)
+    return res[0] if len(res) == 1 else res
 
 
 def gdn_decode_prep(proj, conv_state, conv_w, a_log, dt_bias, *, conv_dim, qk_dim, hv, b_offset, a_offset):

@@ -94,13 +94,14 @@ class HipOps:
     # Fused decode-layer neighbours: HIP kernels for bf16 activations (the
     # served configuration).  A float32 model (used to pin the cache logic
     # without bf16 rounding) runs the torch formulations of the same layers.
-    def rmsnorm(self, x, w, eps, residual=None):
+    def rmsnorm(self, x, w, eps, residual=None, w2=None):
         """x may be a projection's deferred split-K partials (``linear(...,
         defer=True)``): the reduce, the projection's residual, the residual
-        add and the norm then run as one launch."""
+        add and the norms then run as one launch.  ``w2``: the row normed
+        with a second weight is appended to the result."""
         if x.dtype != torch.bfloat16:
-            return TorchGlue.rmsnorm(x, w, eps, residual)
-        return self.layers.rmsnorm(x, w, eps, residual=residual)
+            return TorchGlue.rmsnorm(x, w, eps, residual, w2)
+        return self.layers.rmsnorm(x, w, eps, residual=residual, w2=w2)
 
     def gdn_prep(self, proj, conv_state, conv_w, a_log, dt_bias, **kw):
         if proj.dtype != torch.bfloat16:
@@ -248,11 +249,11 @@ class TorchGlue:
     argument (the definitions the kernels are tested against)."""
 
     @staticmethod
-    def rmsnorm(x, w, eps, residual=None):
-        if residual is None:
-            return rms_norm(x, w, eps)
-        s = x + residual
-        return rms_norm(s, w, eps), s
+    def rmsnorm(x, w, eps, residual=None, w2=None):
+        s = x if residual is None else x + residual
+        res = (rms_norm(s, w, eps),) if residual is None else (rms_norm(s, w, eps), s)
+        res = res if w2 is None else res + (rms_norm(s, w2, eps),)
+        return res[0] if len(res) == 1 else res
 
     @staticmethod
     def gdn_prep(proj, conv_state, conv_w, a_log, dt_bias, *, conv_dim, qk_dim, hv, b_offset, a_offset):
@@ -489,11 +490,14 @@ class Model:
         key = apply_rope(rms_norm(key, L["m_k_norm"], c.rms_eps), cos, sin, c.rotary_dim)
         return q, gate, key, val.contiguous(), scores
 
-    def _memory_decode(self, L, hidden, cos, sin):
-        """``_memory_qkvs`` for one token per slot on the fused kernels."""
+    def _memory_decode(self, L, hidden, cos, sin, u=None):
+        """``_memory_qkvs`` for one token per slot on the fused kernels (u:
+        the layer input already normed with m_in_norm, if the previous norm
+        made it)."""
         c, B, ops = self.cfg, hidden.shape[0], self.ops
         H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
-        u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
+        if u is None:
+            u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
         proj = ops.linear(u, L["m_in"], L.get("m_in@packed"))                                    # [q | admission features | gate | up]
         qd, ad = H * D, c.admission_rank
         q, gate, scores = ops.memory_prologue(proj, H, qd, ad, L["m_q_norm"], cos, sin, L["read_scale"],
@@ -505,7 +509,7 @@ class Model:
                                  c.rms_eps)
         return q, gate, key, kv[:, KVH * D:].reshape(B, KVH, D), scores
 
-    def _attn_decode(self, i, L, xn, hidden, positions, cos, sin, valid, ring_rows):
+    def _attn_decode(self, i, L, xn, hidden, positions, cos, sin, valid, ring_rows, u=None):
         """SWA + anchor-memory mixer for one token per slot.  xn is the
         normalised layer input, hidden the residual stream entering the layer;
         ring_rows[b] = b * kv_heads * window + positions[b] % window.  On a GPU
@@ -519,7 +523,7 @@ class Model:
             main = torch.cuda.current_stream(xn.device)
             side.wait_stream(main)
             with torch.cuda.stream(side):
-                read = self._memory_path(i, L, hidden, cos, sin, valid)
+                read = self._memory_path(i, L, hidden, cos, sin, valid, u)
         proj = ops.linear(xn, L["w_qkv"], L.get("w_qkv@packed"))                                    # [B, (q|gate) per head | k | v]
         hq = 2 * H * D
         qg = proj[:, :hq].view(B, H, 2 * D)
@@ -530,16 +534,16 @@ class Model:
         att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i], gate=qg[..., D:])
         out = ops.linear(att.reshape(B, -1), L["w_o"], L.get("w_o@packed"))
         if side is None:
-            read = self._memory_path(i, L, hidden, cos, sin, valid)
+            read = self._memory_path(i, L, hidden, cos, sin, valid, u)
         else:
             main.wait_stream(side)
             read.record_stream(main)
         return ops.linear(read.reshape(B, -1), L["m_o"], L.get("m_o@packed"), residual=out, defer=True)
 
-    def _memory_path(self, i, L, hidden, cos, sin, valid):
+    def _memory_path(self, i, L, hidden, cos, sin, valid, u=None):
         """Anchor-memory read (gated) and commit of one decode token per slot."""
         c, ops = self.cfg, self.ops
-        mq, mgate, mk, mv, mscores = self._memory_decode(L, hidden, cos, sin)
+        mq, mgate, mk, mv, mscores = self._memory_decode(L, hidden, cos, sin, u)
         read = ops.memory_read(mq[:, None], self.memory[i], valid=valid, head_gate=mgate)
         ops.memory_commit(mk[:, None], mv[:, None], mscores[:, None], valid, c.memory_chunk, self.memory[i])
         return read
@@ -551,24 +555,30 @@ class Model:
             self._side = torch.cuda.Stream(device=x.device)   # default priority
         return self._side
 
-    def decode_step(self, tokens, positions, valid):
+    def decode_step(self, tokens, positions, valid, float_logits=True):
         """One token for every slot: tokens, positions [B] int64, valid [B] bool
-        -> logits [B, V] float32.  Updates every cache in place.  Each residual
-        add is fused into the RMSNorm that follows it."""
+        -> logits [B, V] float32 (the model dtype with ``float_logits`` off:
+        the sampler widens them itself, exactly).  Updates every cache in
+        place.  Each residual add is fused into the RMSNorm that follows it."""
         c, ops, B = self.cfg, self.ops, tokens.shape[0]
         h = self.embed[tokens]
         cos, sin = rope_tables(positions, c)
         ring_rows = torch.arange(B, device=h.device) * (c.kv_heads * c.swa_window) + positions % c.swa_window
-        xn = ops.rmsnorm(h, self.layers[0]["in_norm"], c.rms_eps)
+        xn, u = ops.rmsnorm(h, self.layers[0]["in_norm"], c.rms_eps), None
         for i, L in enumerate(self.layers):
             if L["kind"] == "gdn":
                 delta = self._gdn_decode(i, L, xn)
             else:
-                delta = self._attn_decode(i, L, xn, h, positions, cos, sin, valid, ring_rows)
+                delta = self._attn_decode(i, L, xn, h, positions, cos, sin, valid, ring_rows, u)
             xn, h = ops.rmsnorm(delta, L["post_norm"], c.rms_eps, residual=h)
-            nxt = self.layers[i + 1]["in_norm"] if i + 1 < len(self.layers) else self.final_norm
-            xn, h = ops.rmsnorm(self._mlp(L, xn, defer=True), nxt, c.rms_eps, residual=h)
-        return ops.linear(xn, self.lm_head, self.lm_head_packed).float()
+            nl = self.layers[i + 1] if i + 1 < len(self.layers) else None
+            mlp = self._mlp(L, xn, defer=True)
+            if nl is not None and nl["kind"] != "gdn":   # the memory path's own norm of the same row
+                xn, h, u = ops.rmsnorm(mlp, nl["in_norm"], c.rms_eps, residual=h, w2=nl["m_in_norm"])
+            else:
+                xn, h = ops.rmsnorm(mlp, self.final_norm if nl is None else nl["in_norm"], c.rms_eps, residual=h)
+        logits = ops.linear(xn, self.lm_head, self.lm_head_packed)
+        return logits.float() if float_logits else logits
 
     # ---------------- prefill ----------------
     def prefill(self, prompts):
@@ -705,7 +715,7 @@ class Engine:
     # one decode step on the device (captured)
     def _step(self):
         valid = (~self.finished) & (self.slot_rows >= 0)
-        logits = self.m.decode_step(self.decode_ids[:, 0], self.positions, valid)
+        logits = self.m.decode_step(self.decode_ids[:, 0], self.positions, valid, float_logits=False)
         tok = self.m.ops.sample(logits, self.attempt_ids, self.row_steps, self.dense_seen, seed=self.seed,
                                 temperature=self.temperature, top_k=self.top_k, top_p=self.top_p,
                                 penalty=self.penalty)
