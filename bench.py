@@ -170,7 +170,7 @@ class _OracleOps:
         self.glue = TorchGlue
         from yanchor_amd.runtime import gate_read
         self.gate_read = gate_read
-        for name in ("rmsnorm", "gdn_prep", "gated_rmsnorm", "silu_mul", "head_norm_rope", "ring_write",
+        for name in ("decode_inputs", "rmsnorm", "gdn_prep", "gated_rmsnorm", "silu_mul", "head_norm_rope", "ring_write",
                      "memory_prologue"):
             setattr(self, name, getattr(TorchGlue, name))
 

@@ -462,6 +462,23 @@ int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual, void* resi
                int64_t out_stride, int64_t N, int64_t D, float eps, int plus_one, yh_stream_t stream);
 
 /*
+ * Inputs of one decode step, one launch: h = embed[tokens] (bf16 [B, D]; a
+ * zero row for an id outside [0, V)), xn = RMSNorm(h) * (1 + w) as yh_rmsnorm,
+ * cos / sin float [B, rotary_dim] of float(positions[b]) * inv_freq[j mod
+ * rotary_dim / 2] (rotate-half layout; inv_freq float [rotary_dim / 2]), the
+ * SWA ring row ring_rows[b] = b * ring_stride + positions[b] mod window, and,
+ * when finished (bool [B]), slot_rows (int64 [B]) and valid (bool [B]) are all
+ * given, valid[b] = !finished[b] && slot_rows[b] >= 0.  D % 8 == 0, D <= 8192.
+ * Replaces the embedding lookup and rotary tables of the model forward
+ * (modeling_yanchor.py:932, 951) and the live-slot mask of the decode step
+ * (runtime/model/inference_kernels.py:1176) for the fixed-slot decode graph.
+ */
+int yh_decode_inputs(const int64_t* tokens, const int64_t* positions, const void* embed, int64_t V, const void* w,
+                     const float* inv_freq, const uint8_t* finished, const int64_t* slot_rows, void* h, void* xn,
+                     float* cos, float* sin, int64_t* ring_rows, uint8_t* valid, int64_t B, int64_t D,
+                     int64_t rotary_dim, int64_t ring_stride, int64_t window, float eps, yh_stream_t stream);
+
+/*
  * yh_rmsnorm whose input row is a split-K projection still in fp32 partials
  * (yh_linear_packed with defer_reduce): x = bf16(sum over the S planes of
  * part [S, N, D] in slice order), x = bf16(x + proj_residual) when given (the

@@ -62,6 +62,38 @@ def test_rmsnorm_empty_and_bad(gpu):
         layers.rmsnorm(torch.zeros(2, 256, device=gpu), w, 1e-6)     # fp32 activations
 
 
+@pytest.mark.parametrize("b,d", [(128, 2560), (5, 2560), (3, 512)])
+def test_decode_inputs(gpu, b, d):
+    """Embedding rows and ring rows / live mask exactly; the first norm equal
+    to yh_rmsnorm of the same rows; rotary tables as the torch formulation."""
+    cfg = rt.ModelConfig()
+    v = 1000
+    embed = rnd(v, d, dev=gpu, seed=40)
+    w = rnd(d, dev=gpu, scale=0.1, seed=41)
+    g = torch.Generator(device=gpu).manual_seed(42)
+    tokens = torch.randint(0, v, (b,), device=gpu, generator=g)
+    tokens[0] = v + 7                                    # outside the vocabulary: a zero row
+    positions = torch.randint(0, 1 << 20, (b,), device=gpu, generator=g)
+    finished = torch.rand(b, device=gpu, generator=g) < 0.3
+    slot_rows = torch.randint(-1, 4, (b,), device=gpu, generator=g)
+    inv = rt.rope_inv_freq(cfg, gpu)
+    kw = dict(ring_stride=cfg.kv_heads * cfg.swa_window, window=cfg.swa_window)
+    h, xn, cos, sin, rows, valid = layers.decode_inputs(tokens, positions, embed, w, inv, 1e-6, finished=finished,
+                                                        slot_rows=slot_rows, **kw)
+    want_h = embed[tokens.clamp(max=v - 1)].clone()
+    want_h[0] = 0
+    assert torch.equal(h, want_h)
+    assert torch.equal(xn, layers.rmsnorm(want_h, w, 1e-6))
+    ulp_check(xn, TorchGlue.rmsnorm(want_h, w, 1e-6))
+    rcos, rsin = rt.rope_tables(positions, cfg)
+    for got, want in ((cos, rcos), (sin, rsin)):
+        assert got.shape == want.shape == (b, cfg.rotary_dim)
+        assert (got - want).abs().max().item() <= 2.0 ** -23
+    assert torch.equal(rows, torch.arange(b, device=gpu) * kw["ring_stride"] + positions % kw["window"])
+    assert torch.equal(valid, (~finished) & (slot_rows >= 0))
+    assert layers.decode_inputs(tokens, positions, embed, w, inv, 1e-6, **kw)[5] is None
+
+
 @pytest.mark.parametrize("b", [1, 5, 128])
 def test_gdn_decode_prep(gpu, b):
     cfg = rt.ModelConfig()

@@ -55,14 +55,33 @@ def test_torch_semantics_golden(gpu, case):
     assert bad == amb, f"mismatching rows {bad}"
 
 
-@pytest.mark.parametrize("b,v,k", [(8, 1000, 20), (128, 151936, 20), (5, 70000, 64), (3, 37, 7), (4, 4096, 1)])
-def test_topk_matches_torch(gpu, b, v, k):
+@pytest.mark.parametrize("b,v,k,dtype", [(8, 1000, 20, torch.float32), (128, 151936, 20, torch.float32),
+                                         (128, 151936, 20, torch.bfloat16), (4, 151936, 32, torch.bfloat16),
+                                         (4, 151936, 33, torch.float32), (5, 70000, 64, torch.float32),
+                                         (3, 37, 7, torch.float32), (4, 4096, 1, torch.bfloat16)])
+def test_topk_matches_torch(gpu, b, v, k, dtype):
     g = torch.Generator().manual_seed(b * v + k)
-    logits = torch.randn(b, v, generator=g) * 4
+    logits = (torch.randn(b, v, generator=g) * 4).to(dtype)
     tok, vals, idx = ik.topk_sample(logits.to(gpu), torch.arange(b).to(gpu), 0, seed=1, temperature=0.6,
                                     top_k=k, top_p=0.95, mode=ik.SAMPLE_FUSED, return_topk=True)
-    rv, ri = torch.topk(logits, k)
-    assert torch.equal(idx.cpu(), ri) and torch.equal(vals.cpu(), rv)
+    rv, ri = torch.topk(logits.float(), k)       # bf16 ties: torch.topk keeps no index order, so compare in fp32
+    if dtype == torch.float32:
+        assert torch.equal(idx.cpu(), ri) and torch.equal(vals.cpu(), rv)
+    else:
+        order = torch.sort(-logits.float() * 1.0, dim=-1, stable=True).indices[:, :k]
+        assert torch.equal(idx.cpu(), order) and torch.equal(vals.cpu(), torch.gather(logits.float(), 1, order))
+
+
+@pytest.mark.parametrize("k", [20, 32, 33])
+def test_topk_all_equal_segments(gpu, k):
+    """Every element ties: the lowest k indices, for the wave threshold (k <=
+    32) at its worst candidate count and for the exact one above it."""
+    logits = torch.zeros(3, 151936, dtype=torch.bfloat16)
+    logits[1, 50000:] = 1.0
+    _, vals, idx = ik.topk_sample(logits.to(gpu), torch.arange(3).to(gpu), 0, seed=1, temperature=1.0, top_k=k,
+                                  top_p=1.0, mode=ik.SAMPLE_FUSED, return_topk=True)
+    assert idx[0].cpu().tolist() == list(range(k)) and idx[2].cpu().tolist() == list(range(k))
+    assert idx[1].cpu().tolist() == list(range(50000, 50000 + k))
 
 
 def test_topk_ties_lower_index_first(gpu):

@@ -162,6 +162,68 @@ void launch_rmsnorm(const NormArgs& a, int64_t N, hipStream_t st) {
   else hipLaunchKernelGGL(rmsnorm_kernel<16>, grid, dim3(threads), 0, st, a);
 }
 
+// Per-step decode inputs, one workgroup per slot b (blockDim = hidden / 8
+// rounded up to whole waves): h = embed[tokens[b]] (a zero row for an id
+// outside [0, V)), xn = RMSNorm(h) * (1 + w), cos / sin [B, rd] of
+// positions[b] * inv_freq[j % (rd / 2)] (the rotate-half layout), the SWA ring
+// row b * ring_stride + positions[b] % window, and valid = !finished[b] &&
+// slot_rows[b] >= 0 when both are given.
+struct InputArgs {
+  const int64_t* tokens;
+  const int64_t* positions;
+  const uint16_t* embed;
+  const uint16_t* w;
+  const float* inv_freq;
+  const uint8_t* finished;
+  const int64_t* slot_rows;
+  uint16_t* h;
+  uint16_t* xn;
+  float* cos;
+  float* sin;
+  int64_t* ring_rows;
+  uint8_t* valid;
+  int64_t V, ring_stride, window;
+  int D, rd;
+  float eps;
+};
+
+__global__ void __launch_bounds__(kNormMaxThreads) decode_inputs_kernel(InputArgs a) {
+  const int64_t b = blockIdx.x;
+  const int c = threadIdx.x, D = a.D;
+  const int64_t tok = a.tokens[b], pos = a.positions[b];
+  const bool on = c < D / 8;
+  float v[8];
+  float ss = 0.f;
+  if (on) {
+    uint4 x = {};
+    if (tok >= 0 && tok < a.V) x = *reinterpret_cast<const uint4*>(a.embed + tok * D + c * 8);
+    *reinterpret_cast<uint4*>(a.h + b * D + c * 8) = x;
+    const uint16_t* xh = reinterpret_cast<const uint16_t*>(&x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = bf(xh[j]);
+      ss = fmaf(v[j], v[j], ss);
+    }
+  }
+  if (c < a.rd) {
+    const float ang = static_cast<float>(pos) * a.inv_freq[c % (a.rd / 2)];
+    a.cos[b * a.rd + c] = cosf(ang);
+    a.sin[b * a.rd + c] = sinf(ang);
+  }
+  if (c == 0) {
+    a.ring_rows[b] = b * a.ring_stride + pos % a.window;
+    if (a.valid) a.valid[b] = (a.finished[b] == 0 && a.slot_rows[b] >= 0) ? 1 : 0;
+  }
+  const float r = rsqrtf(block_sum(ss) / static_cast<float>(D) + a.eps);
+  if (!on) return;
+  const uint4 wv = *reinterpret_cast<const uint4*>(a.w + c * 8);
+  const uint16_t* wh = reinterpret_cast<const uint16_t*>(&wv);
+  uint16_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = tobf(v[j] * r * (1.f + bf(wh[j])));
+  *reinterpret_cast<uint4*>(a.xn + b * D + c * 8) = *reinterpret_cast<const uint4*>(o);
+}
+
 // grid (B, ceil(C / 256)): channel c of row b.  proj [B, P] (row stride P)
 // holds [qkv (C) | z | b (HV) | a (HV)] at offsets 0 / -- / boff / aoff.
 // conv_state [B, K-1, C] (time-major), conv_w [C, K], K = 4.
@@ -398,6 +460,34 @@ extern "C" int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual,
              (int)D, plus_one, eps};
   launch_rmsnorm(a, N, static_cast<hipStream_t>(stream));
   YH_CHECK_LAUNCH("rmsnorm");
+  return YH_OK;
+}
+
+extern "C" int yh_decode_inputs(const int64_t* tokens, const int64_t* positions, const void* embed, int64_t V,
+                                const void* w, const float* inv_freq, const uint8_t* finished,
+                                const int64_t* slot_rows, void* h, void* xn, float* cos, float* sin,
+                                int64_t* ring_rows, uint8_t* valid, int64_t B, int64_t D, int64_t rotary_dim,
+                                int64_t ring_stride, int64_t window, float eps, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(B >= 0 && V > 0 && window > 0 && ring_stride >= window, "decode_inputs: bad sizes");
+  YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= kNormMaxD, "decode_inputs: D must be a multiple of 8 up to %d", kNormMaxD);
+  YH_CHECK_ARG(rotary_dim >= 0 && rotary_dim % 2 == 0 && rotary_dim <= (D / 8 + kWave - 1) / kWave * kWave,
+               "decode_inputs: rotary dim must be even and within the workgroup");
+  YH_CHECK_ARG(B == 0 || (tokens && positions && embed && w && h && xn && ring_rows &&
+                          (rotary_dim == 0 || (inv_freq && cos && sin))),
+               "decode_inputs: null pointer");
+  YH_CHECK_ARG(!valid == !finished && !valid == !slot_rows, "decode_inputs: valid needs finished and slot_rows");
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(embed) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(h) |
+                 reinterpret_cast<uintptr_t>(xn)) & 15) == 0,
+               "decode_inputs: embed / w / h / xn must be 16-byte aligned");
+  if (B == 0) return YH_OK;
+  InputArgs a{tokens, positions, static_cast<const uint16_t*>(embed), static_cast<const uint16_t*>(w), inv_freq,
+              finished, slot_rows, static_cast<uint16_t*>(h), static_cast<uint16_t*>(xn), cos, sin, ring_rows, valid,
+              V, ring_stride, window, (int)D, (int)rotary_dim, eps};
+  const unsigned threads = static_cast<unsigned>((D / 8 + kWave - 1) / kWave * kWave);
+  hipLaunchKernelGGL(decode_inputs_kernel, dim3(static_cast<unsigned>(B)), dim3(threads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  YH_CHECK_LAUNCH("decode_inputs");
   return YH_OK;
 }
 

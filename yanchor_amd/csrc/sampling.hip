@@ -9,11 +9,14 @@
 //   _qwen35_dense_presence_penalty_kernel 1095-1114
 //
 // Top-k runs in two launches.  Phase 1: a workgroup per (row, vocabulary
-// segment).  Every thread takes the maximum of its strided elements; the k-th
-// largest of those 256 maxima is a lower bound of the segment's k-th largest
-// element (k threads hold an element at least that large), so only elements at
-// or above it can be in the top k -- at most k * (elements per thread) of
-// them.  They are gathered in LDS and ranked by counting.  Elements are
+// segment).  Every thread takes the maximum of its 32 elements.  A threshold
+// below the segment's k-th largest element is formed from those maxima: for
+// k <= 32 the largest over the four waves of each wave's k-th largest maximum
+// (a wave sorts its 64 maxima), else the k-th largest of all 256 maxima.  In
+// both cases k threads hold an element at least that large, and at most
+// 4 k (or k) threads hold elements above it, so only those elements -- at most
+// 4096 -- can be in the top k.  They are gathered in LDS and ranked by
+// counting.  Elements are
 // compared by the unique key (value, -index): larger value first, lower index
 // on equal values.  Phase 2: a workgroup per row ranks the segment lists, then
 // draws the token.
@@ -53,43 +56,92 @@ constexpr int kVecPerThread = 8;                       // 4-element vectors per 
 constexpr int kSegLen = kTopkThreads * 4 * kVecPerThread;  // 8192 elements per segment
 static_assert(kVecPerThread * 4 <= kMaxPerThread, "elements per thread");
 
-// 4 scores (with the presence penalty) starting at element i of row b.
-template <int DT, bool VEC>
-__device__ __forceinline__ void load_scores4(const TopkArgs& a, int64_t b, int i, float* v) {
-  const int64_t off = b * a.row_stride + i;
-  if constexpr (VEC) {
-    if (i + 3 < a.V) {
-      if constexpr (DT == YH_F32) {
-        const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(a.scores) + off);
-        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-      } else {
-        const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.scores) + off);
-        if constexpr (DT == YH_BF16) {
-          v[0] = __uint_as_float(w.x << 16); v[1] = __uint_as_float(w.x & 0xffff0000u);
-          v[2] = __uint_as_float(w.y << 16); v[3] = __uint_as_float(w.y & 0xffff0000u);
-        } else {
-          v[0] = f16_to_f32(w.x & 0xffff); v[1] = f16_to_f32(w.x >> 16);
-          v[2] = f16_to_f32(w.y & 0xffff); v[3] = f16_to_f32(w.y >> 16);
-        }
-      }
-      if (a.seen) {
-        const uint32_t m = *reinterpret_cast<const uint32_t*>(a.seen + b * a.seen_stride + i);
+// Element e of a thread's 32 scores.  WIDE (16-byte aligned rows): in a full
+// segment the thread reads 16-byte runs, element i = lo + (c * 256 + tid) * E
+// + j for run c and j < E = 16 / element size; otherwise (the row's last
+// segment, or unaligned rows) element i = lo + e * 256 + tid, read one by one
+// at a clamped index and dropped past V.  Every load of the thread is issued
+// before the first is used.
+constexpr int kPerThread = 4 * kVecPerThread;  // 32
+
+template <int DT>
+__device__ __forceinline__ float decode_elem(uint32_t bits) {
+  if constexpr (DT == YH_F32) return __uint_as_float(bits);
+  else if constexpr (DT == YH_BF16) return __uint_as_float(bits << 16);
+  else return f16_to_f32(static_cast<uint16_t>(bits));
+}
+
+template <int DT, bool WIDE>
+__device__ __forceinline__ uint64_t load_keys(const TopkArgs& a, int64_t b, int lo, int tid,
+                                              uint64_t (&key)[kPerThread]) {
+  constexpr int ES = DT == YH_F32 ? 4 : 2;
+  const char* row = static_cast<const char*>(a.scores) + b * a.row_stride * ES;
+  const uint8_t* srow = a.seen ? a.seen + b * a.seen_stride : nullptr;
+  uint64_t best = 0;  // key 0 is below every real element key
+  if (WIDE && lo + kSegLen <= a.V) {
+    constexpr int E = 16 / ES, NC = kPerThread / E;
+    uint4 raw[NC];
+    uint64_t sm[NC];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if ((m >> (8 * j)) & 0xffu) v[j] = v[j] - a.penalty;
+    for (int c = 0; c < NC; ++c)
+      raw[c] = *reinterpret_cast<const uint4*>(row + static_cast<int64_t>(lo + (c * kTopkThreads + tid) * E) * ES);
+    if (srow) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint8_t* sp = srow + lo + (c * kTopkThreads + tid) * E;
+        if constexpr (E == 8) sm[c] = *reinterpret_cast<const uint64_t*>(sp);
+        else sm[c] = *reinterpret_cast<const uint32_t*>(sp);
       }
-      return;
     }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(&raw[c]);
+      const int i0 = lo + (c * kTopkThreads + tid) * E;
+#pragma unroll
+      for (int j = 0; j < E; ++j) {
+        const uint32_t bits = ES == 4 ? w[j] : (w[j / 2] >> (16 * (j & 1))) & 0xffffu;
+        float x = decode_elem<DT>(bits);
+        if (srow && ((sm[c] >> (8 * j)) & 0xffu)) x = x - a.penalty;
+        key[c * E + j] = ckey(x, static_cast<uint32_t>(i0 + j));
+        best = key[c * E + j] > best ? key[c * E + j] : best;
+      }
+    }
+    return best;
+  }
+  uint32_t raw[kPerThread];
+  uint8_t sm[kPerThread];
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) {
+    const int i = min(lo + e * kTopkThreads + tid, a.V - 1);
+    if constexpr (ES == 4) raw[e] = *reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(i) * 4);
+    else raw[e] = *reinterpret_cast<const uint16_t*>(row + static_cast<int64_t>(i) * 2);
+  }
+  if (srow) {
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) sm[e] = srow[min(lo + e * kTopkThreads + tid, a.V - 1)];
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (i + j < a.V) {
-      v[j] = Elem<DT>::ld(static_cast<const typename Elem<DT>::T*>(a.scores), off + j);
-      if (a.seen && a.seen[b * a.seen_stride + i + j]) v[j] = v[j] - a.penalty;
-    } else {
-      v[j] = NAN;  // marks "no element"; never becomes a candidate
-    }
+  for (int e = 0; e < kPerThread; ++e) {
+    const int i = lo + e * kTopkThreads + tid;
+    float x = decode_elem<DT>(raw[e]);
+    if (srow && sm[e]) x = x - a.penalty;
+    key[e] = i < a.V ? ckey(x, static_cast<uint32_t>(i)) : 0ull;
+    best = key[e] > best ? key[e] : best;
   }
+  return best;
+}
+
+constexpr int kWaveThrMaxK = kCandCap / (kTopkThreads / kWave) / (4 * kVecPerThread);  // 32
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, kWave);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, kWave);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+  const uint32_t lo = __shfl(static_cast<uint32_t>(v), src, kWave);
+  const uint32_t hi = __shfl(static_cast<uint32_t>(v >> 32), src, kWave);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 template <int DT, bool VEC>
@@ -104,48 +156,54 @@ __global__ void __launch_bounds__(kTopkThreads) topk_segment_kernel(TopkArgs a) 
     ncand = 0;
     thr_s = 0;
   }
-  // issue every load of this thread first, then build the keys
-  float v[kVecPerThread][4];
+  uint64_t key[kPerThread];
+  const uint64_t best = load_keys<DT, VEC>(a, b, lo, tid, key);
+  if (a.k <= kWaveThrMaxK) {
+    // Threshold = the largest over the waves of each wave's k-th largest
+    // thread maximum (a wave sorts its 64 maxima by a bitonic network):
+    // the wave that attains it holds k elements at or above it, so it bounds
+    // the segment's k-th largest element from below, and no wave has more
+    // than k threads at or above it, so at most 4 k x 32 elements pass.
+    const int lane = tid & (kWave - 1);
+    uint64_t x = best;
 #pragma unroll
-  for (int c = 0; c < kVecPerThread; ++c) {
-    const int i = lo + (c * kTopkThreads + tid) * 4;
-    if (i < a.V) load_scores4<DT, VEC>(a, b, i, v[c]);
-    else v[c][0] = v[c][1] = v[c][2] = v[c][3] = NAN;
-  }
-  uint64_t key[kVecPerThread][4];
-  uint64_t best = 0;  // key 0 is below every real element key
+    for (int size = 2; size <= kWave; size <<= 1)
 #pragma unroll
-  for (int c = 0; c < kVecPerThread; ++c) {
-    const int i = lo + (c * kTopkThreads + tid) * 4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool real = i + j < a.V;
-      key[c][j] = real ? ckey(v[c][j], static_cast<uint32_t>(i + j)) : 0ull;
-      best = key[c][j] > best ? key[c][j] : best;
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint64_t y = shfl_xor_u64(x, stride);
+        const bool keep_max = ((lane & size) == 0) == ((lane & stride) == 0);
+        x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+      }
+    const uint64_t kth = shfl_u64(x, a.k - 1);  // descending: lane j holds the (j+1)-th largest
+    if (lane == 0) maxima[tid / kWave] = kth;
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t t = 0;
+      for (int w = 0; w < kTopkThreads / kWave; ++w) t = maxima[w] > t ? maxima[w] : t;
+      thr_s = t;
     }
-  }
-  maxima[tid] = best;
-  __syncthreads();
-  // Threshold = k-th largest thread maximum.  Real keys are unique, so exactly
-  // one thread has rank k-1 when at least k threads hold elements; otherwise the
-  // threshold stays 0 and every element of the segment is a candidate (fewer
-  // than k threads hold at most (k-1) * per-thread elements).
-  if (best != 0) {
-    int rank = 0;
-    for (int j = 0; j < kTopkThreads; ++j) rank += maxima[j] > best;
-    if (rank == a.k - 1) thr_s = best;
+  } else {
+    maxima[tid] = best;
+    __syncthreads();
+    // Threshold = k-th largest thread maximum.  Real keys are unique, so exactly
+    // one thread has rank k-1 when at least k threads hold elements; otherwise the
+    // threshold stays 0 and every element of the segment is a candidate (fewer
+    // than k threads hold at most (k-1) * per-thread elements).
+    if (best != 0) {
+      int rank = 0;
+      for (int j = 0; j < kTopkThreads; ++j) rank += maxima[j] > best;
+      if (rank == a.k - 1) thr_s = best;
+    }
   }
   __syncthreads();
   const uint64_t thr = thr_s;
   if (best >= thr && best != 0) {
 #pragma unroll
-    for (int c = 0; c < kVecPerThread; ++c)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (key[c][j] >= thr && key[c][j] != 0) {
-          const int slot = atomicAdd(&ncand, 1);
-          if (slot < kCandCap) cand[slot] = key[c][j];
-        }
+    for (int e = 0; e < kPerThread; ++e)
+      if (key[e] >= thr && key[e] != 0) {
+        const int slot = atomicAdd(&ncand, 1);
+        if (slot < kCandCap) cand[slot] = key[e];
+      }
   }
   __syncthreads();
   const int n = min(ncand, kCandCap);
@@ -304,8 +362,9 @@ extern "C" int yh_topk_sample(const void* scores, int dtype, int64_t row_stride,
   TopkArgs ta{scores, seen, static_cast<uint64_t*>(workspace), (int)B, (int)V, S, seg, (int)top_k,
               row_stride, seen_stride, penalty};
   const size_t esz = dtype == YH_F32 ? 4 : 2;
-  const bool vec = (reinterpret_cast<uintptr_t>(scores) % (4 * esz)) == 0 && row_stride % 4 == 0 &&
-                   (seen == nullptr || ((reinterpret_cast<uintptr_t>(seen) & 3) == 0 && seen_stride % 4 == 0));
+  const int64_t run = 16 / static_cast<int64_t>(esz);  // elements per 16-byte load
+  const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16) == 0 && row_stride % run == 0 &&
+                   (seen == nullptr || ((reinterpret_cast<uintptr_t>(seen) % run) == 0 && seen_stride % run == 0));
   const dim3 grid(S, static_cast<unsigned>(B));
   switch (dtype * 2 + (vec ? 1 : 0)) {
     case YH_F32 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_F32, true>), grid, dim3(kTopkThreads), 0, st, ta); break;

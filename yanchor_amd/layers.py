@@ -54,6 +54,42 @@ def rmsnorm(x, w, eps, residual=None, plus_one=True, w2=None):
     return out if residual is None else (out, res_out)
 
 
+def decode_inputs(tokens, positions, embed, w, inv_freq, eps, *, ring_stride, window, finished=None,
+                  slot_rows=None):
+    """Inputs of one decode step in one launch: (h = embed[tokens], xn =
+    RMSNorm(h) * (1 + w), cos, sin [B, 2 len(inv_freq)] float32 of positions *
+    inv_freq (rotate-half layout), ring_rows = arange(B) * ring_stride +
+    positions % window, valid = ~finished & (slot_rows >= 0) or None).  The
+    embedding lookup and rotary tables of the model forward
+    (modeling_yanchor.py:932, 951)."""
+    _bf16(embed, w)
+    if tokens.dtype != torch.int64 or positions.dtype != torch.int64 or tokens.shape != positions.shape or \
+            tokens.ndim != 1:
+        raise ValueError("tokens and positions must be int64 [B]")
+    tokens, positions = tokens.contiguous(), positions.contiguous()
+    if (finished is None) != (slot_rows is None):
+        raise ValueError("valid needs both finished and slot_rows")
+    if finished is not None and (finished.dtype != torch.bool or slot_rows.dtype != torch.int64 or
+                                 finished.shape != tokens.shape or slot_rows.shape != tokens.shape or
+                                 not finished.is_contiguous() or not slot_rows.is_contiguous()):
+        raise ValueError("finished / slot_rows must be contiguous bool / int64 [B]")
+    if inv_freq.dtype != torch.float32 or not inv_freq.is_contiguous() or not embed.is_contiguous():
+        raise ValueError("inv_freq must be contiguous float32 and embed contiguous")
+    dev = N.require_device(tokens, positions, embed, w, inv_freq, finished, slot_rows)
+    b, (v, d), rd = tokens.shape[0], embed.shape, 2 * inv_freq.numel()
+    h = torch.empty(b, d, dtype=torch.bfloat16, device=dev)
+    xn = torch.empty_like(h)
+    cos = torch.empty(b, rd, dtype=torch.float32, device=dev)
+    sin = torch.empty_like(cos)
+    rows = torch.empty(b, dtype=torch.int64, device=dev)
+    valid = None if finished is None else torch.empty(b, dtype=torch.bool, device=dev)
+    N.call("yh_decode_inputs", tokens.data_ptr(), positions.data_ptr(), embed.data_ptr(), v, w.data_ptr(),
+           inv_freq.data_ptr(), N.ptr(finished), N.ptr(slot_rows), h.data_ptr(), xn.data_ptr(), cos.data_ptr(),
+           sin.data_ptr(), rows.data_ptr(), N.ptr(valid), b, d, rd, int(ring_stride), int(window), float(eps),
+           N.stream_of(tokens))
+    return h, xn, cos, sin, rows, valid
+
+
 def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None):
     _bf16(w, residual, p.residual, w2)
     m, d = p.shape

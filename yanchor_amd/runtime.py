@@ -108,6 +108,11 @@ class HipOps:
             return TorchGlue.gdn_prep(proj, conv_state, conv_w, a_log, dt_bias, **kw)
         return self.layers.gdn_decode_prep(proj, conv_state, conv_w, a_log, dt_bias, **kw)
 
+    def decode_inputs(self, tokens, positions, embed, w, inv_freq, eps, **kw):
+        if embed.dtype != torch.bfloat16:
+            return TorchGlue.decode_inputs(tokens, positions, embed, w, inv_freq, eps, **kw)
+        return self.layers.decode_inputs(tokens, positions, embed, w, inv_freq, eps, **kw)
+
     def gated_rmsnorm(self, o, z, w, eps):
         if o.dtype != torch.bfloat16:
             return TorchGlue.gated_rmsnorm(o, z, w, eps)
@@ -226,11 +231,15 @@ def gated_rms_norm(x, gate, w, eps):
     return y.to(x.dtype)
 
 
+def rope_inv_freq(cfg: ModelConfig, device):
+    """theta^(-j / half) for j < rotary_dim / 2, float32."""
+    half = cfg.rotary_dim // 2
+    return 1.0 / (cfg.rope_theta ** (torch.arange(0, half, device=device, dtype=torch.float32) / half))
+
+
 def rope_tables(positions, cfg: ModelConfig):
     """cos / sin [*, rotary_dim] for integer positions (rotate_half layout)."""
-    half = cfg.rotary_dim // 2
-    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, half, device=positions.device, dtype=torch.float32) / half))
-    ang = positions.float()[..., None] * inv
+    ang = positions.float()[..., None] * rope_inv_freq(cfg, positions.device)
     ang = torch.cat((ang, ang), -1)
     return ang.cos(), ang.sin()
 
@@ -254,6 +263,16 @@ class TorchGlue:
         res = (rms_norm(s, w, eps),) if residual is None else (rms_norm(s, w, eps), s)
         res = res if w2 is None else res + (rms_norm(s, w2, eps),)
         return res[0] if len(res) == 1 else res
+
+    @staticmethod
+    def decode_inputs(tokens, positions, embed, w, inv_freq, eps, *, ring_stride, window, finished=None,
+                      slot_rows=None):
+        h = embed[tokens]
+        ang = positions.float()[:, None] * inv_freq
+        ang = torch.cat((ang, ang), -1)
+        rows = torch.arange(tokens.shape[0], device=tokens.device) * ring_stride + positions % window
+        valid = None if finished is None else (~finished) & (slot_rows >= 0)
+        return h, rms_norm(h, w, eps), ang.cos(), ang.sin(), rows, valid
 
     @staticmethod
     def gdn_prep(proj, conv_state, conv_w, a_log, dt_bias, *, conv_dim, qk_dim, hv, b_offset, a_offset):
@@ -362,6 +381,7 @@ class Model:
             return torch.zeros(*shape, device=self.device, dtype=dtype)
 
         c = cfg
+        self.inv_freq = rope_inv_freq(c, self.device)
         self.embed = w(c.vocab, c.hidden)
         self.lm_head = w(c.vocab, c.hidden)
         self.final_norm = zeros(c.hidden)
@@ -555,16 +575,19 @@ class Model:
             self._side = torch.cuda.Stream(device=x.device)   # default priority
         return self._side
 
-    def decode_step(self, tokens, positions, valid, float_logits=True):
-        """One token for every slot: tokens, positions [B] int64, valid [B] bool
+    def decode_step(self, tokens, positions, valid=None, float_logits=True, finished=None, slot_rows=None):
+        """One token for every slot: tokens, positions [B] int64, valid [B]
+        bool (or None: ~finished & (slot_rows >= 0) from those [B] tensors)
         -> logits [B, V] float32 (the model dtype with ``float_logits`` off:
         the sampler widens them itself, exactly).  Updates every cache in
         place.  Each residual add is fused into the RMSNorm that follows it."""
-        c, ops, B = self.cfg, self.ops, tokens.shape[0]
-        h = self.embed[tokens]
-        cos, sin = rope_tables(positions, c)
-        ring_rows = torch.arange(B, device=h.device) * (c.kv_heads * c.swa_window) + positions % c.swa_window
-        xn, u = ops.rmsnorm(h, self.layers[0]["in_norm"], c.rms_eps), None
+        c, ops = self.cfg, self.ops
+        h, xn, cos, sin, ring_rows, live = ops.decode_inputs(
+            tokens, positions, self.embed, self.layers[0]["in_norm"], self.inv_freq, c.rms_eps,
+            ring_stride=c.kv_heads * c.swa_window, window=c.swa_window,
+            finished=finished if valid is None else None, slot_rows=slot_rows if valid is None else None)
+        valid = live if valid is None else valid
+        u = None
         for i, L in enumerate(self.layers):
             if L["kind"] == "gdn":
                 delta = self._gdn_decode(i, L, xn)
@@ -714,8 +737,8 @@ class Engine:
 
     # one decode step on the device (captured)
     def _step(self):
-        valid = (~self.finished) & (self.slot_rows >= 0)
-        logits = self.m.decode_step(self.decode_ids[:, 0], self.positions, valid, float_logits=False)
+        logits = self.m.decode_step(self.decode_ids[:, 0], self.positions, float_logits=False,
+                                    finished=self.finished, slot_rows=self.slot_rows)
         tok = self.m.ops.sample(logits, self.attempt_ids, self.row_steps, self.dense_seen, seed=self.seed,
                                 temperature=self.temperature, top_k=self.top_k, top_p=self.top_p,
                                 penalty=self.penalty)
