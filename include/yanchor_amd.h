@@ -80,6 +80,33 @@ int yh_gdn_recurrent_varlen(const void* q, const void* k, const void* v, const v
                             yh_stream_t stream);
 
 /*
+ * One decode token of a GDN layer's core in one launch: yh_gdn_decode_prep
+ * (conv window update + SiLU, beta, g), yh_gdn_recurrent (T = 1, L2-normed q/k,
+ * state IN PLACE) and yh_gated_rmsnorm of the output, bit for bit what those
+ * three give with the recurrence at its 128-column tile.
+ *
+ *   proj [B, proj_stride] bf16: qkv (conv_dim) | ... with z at z_offset
+ *        (HV * V), b at b_offset (HV), a at a_offset (HV)
+ *   conv_state [B, 3, conv_dim] bf16 (oldest first), shifted in place
+ *   conv_w [conv_dim, 4] bf16;  a_log, dt_bias float [HV]
+ *   state [n_state_rows, HV, K, V] float32 (row b, or state_indices[b]; a
+ *        negative index leaves the state alone and gives a zero output row
+ *        before the norm)
+ *   norm_w [V] bf16;  y [B, HV * V] bf16 = gated RMSNorm (eps) of o with z
+ * Requirements: H == HV, K == V == 128, conv_dim == 2 H K + HV V, conv kernel 4;
+ * proj rows and z_offset multiples of 4 elements.
+ * Replaces the decode-step conv update, fused_recurrent_gated_delta_rule and
+ * gated norm of a linear-attention layer (runtime/model/inference_kernels.py:
+ * 339-376, 668-716; transformers wheel, qwen3_5 Qwen3_5RMSNormGated 175-190)
+ * for the decode graph (no reference counterpart as one launch).
+ */
+int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* conv_state, const void* conv_w,
+                        const float* a_log, const float* dt_bias, float* state, const int32_t* state_indices,
+                        const void* norm_w, void* y, int64_t B, int64_t H, int64_t HV, int64_t K, int64_t V,
+                        int64_t conv_dim, int64_t z_offset, int64_t b_offset, int64_t a_offset,
+                        int64_t n_state_rows, float scale, int use_qk_l2norm, float eps, yh_stream_t stream);
+
+/*
  * Chunked packed-varlen prefill of the gated delta rule on bf16 MFMA (chunk 64).
  *
  * Replaces FLA chunk_gated_delta_rule with cu_seqlens (bound at

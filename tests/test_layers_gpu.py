@@ -375,3 +375,38 @@ def test_rmsnorm_second_weight(gpu, split):
     assert torch.equal(got, ref) and torch.equal(got_h, ref_h)
     assert torch.equal(got_u, layers.rmsnorm(ref_h, w2, 1e-6))
     ulp_check(got_u, TorchGlue.rmsnorm(ref_h, w2, 1e-6))
+
+
+@pytest.mark.parametrize("b", [1, 5, 128])
+def test_gdn_decode_fused_equals_three_launches(gpu, b, monkeypatch):
+    """Conv update + gated delta rule + gated norm in one launch give bit for
+    bit what gdn_decode_prep, the recurrence (at its 128-column tile) and
+    gated_rmsnorm give: output row, shifted conv window and state; a row with
+    a negative state index leaves its state alone."""
+    from yanchor_amd import gdn
+    monkeypatch.setenv("YH_GDN_TILE", "128:512")
+    h, d = 32, 128
+    conv_dim, vd = 3 * h * d, h * d
+    p = conv_dim + vd + 2 * h
+    proj = rnd(b, p + 8, dev=gpu, scale=2.0, seed=60)[:, :p]          # row stride P + 8
+    conv = rnd(b, 3, conv_dim, dev=gpu, seed=61)
+    conv_w = rnd(conv_dim, 4, dev=gpu, scale=0.5, seed=62)
+    a_log = torch.log(torch.linspace(1.0, 16.0, h, device=gpu))
+    dt_bias = torch.linspace(-1.0, 1.0, h, device=gpu)
+    state = rnd(b + 2, h, d, d, dev=gpu, scale=0.1, seed=63, dtype=torch.float32)
+    norm_w = (1.0 + rnd(d, dev=gpu, scale=0.1, seed=64).float()).to(torch.bfloat16)
+    idx = torch.arange(b, device=gpu, dtype=torch.int32) + 2
+    idx[b // 2] = -1
+    kw = dict(conv_dim=conv_dim, qk_dim=h * d, hv=h, b_offset=conv_dim + vd, a_offset=conv_dim + vd + h)
+    conv_ref, state_ref = conv.clone(), state.clone()
+    q, k, v, g, beta = layers.gdn_decode_prep(proj, conv_ref, conv_w, a_log, dt_bias, **kw)
+    o, _ = gdn.recurrent_gated_delta_rule(q.view(b, 1, h, d), k.view(b, 1, h, d), v.view(b, 1, h, d),
+                                          g=g.view(b, 1, h), beta=beta.view(b, 1, h), initial_state=state_ref,
+                                          use_qk_l2norm_in_kernel=True, state_indices=idx)
+    want = layers.gated_rmsnorm(o.view(b, h, d), proj[:, conv_dim: conv_dim + vd], norm_w, 1e-6)
+    got = layers.gdn_decode_fused(proj, conv, conv_w, a_log, dt_bias, state, norm_w, 1e-6, heads=h, head_dim=d,
+                                  z_offset=conv_dim, b_offset=conv_dim + vd, a_offset=conv_dim + vd + h,
+                                  state_indices=idx)
+    assert torch.equal(conv, conv_ref)
+    assert torch.equal(state, state_ref)
+    assert torch.equal(got, want.view(b, h * d))

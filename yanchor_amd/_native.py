@@ -43,6 +43,8 @@ SIGNATURES: dict[str, list] = {
     "yh_linear_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i64, _p, _i64, _i32, _p, _p],
     "yh_decode_inputs": [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                          _f32, _p],
+    "yh_gdn_decode_fused": [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _i64, _i64, _i64, _f32, _i32, _f32, _p],
     "yh_rmsnorm_partials": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _p],
     "yh_ring_write": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                       _f32, _p],

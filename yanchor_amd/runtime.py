@@ -113,6 +113,10 @@ class HipOps:
             return TorchGlue.decode_inputs(tokens, positions, embed, w, inv_freq, eps, **kw)
         return self.layers.decode_inputs(tokens, positions, embed, w, inv_freq, eps, **kw)
 
+    def gdn_decode_fused(self, proj, conv_state, conv_w, a_log, dt_bias, state, norm_w, eps, **kw):
+        """gdn_prep + gdn_decode + gated_rmsnorm of one decode token, one launch."""
+        return self.layers.gdn_decode_fused(proj, conv_state, conv_w, a_log, dt_bias, state, norm_w, eps, **kw)
+
     def gated_rmsnorm(self, o, z, w, eps):
         if o.dtype != torch.bfloat16:
             return TorchGlue.gated_rmsnorm(o, z, w, eps)
@@ -471,6 +475,12 @@ class Model:
         c, B, ops = self.cfg, xn.shape[0], self.ops
         hv, dv, vd = c.gdn_heads_v, c.gdn_dv, c.gdn_heads_v * c.gdn_dv
         proj = self.ops.linear(xn, L["w_in"], L.get("w_in@packed"))                                     # [B, qkv | z | b | a]
+        if proj.dtype == torch.bfloat16 and hasattr(ops, "gdn_decode_fused") and c.gdn_heads_k == hv and \
+                c.gdn_dk == dv == 128:
+            y = ops.gdn_decode_fused(proj, self.conv_state[i], L["conv_w"], L["a_log"], L["dt_bias"],
+                                     self.gdn_state[i], L["gnorm"], c.rms_eps, heads=hv, head_dim=dv,
+                                     z_offset=c.conv_dim, b_offset=c.conv_dim + vd, a_offset=c.conv_dim + vd + hv)
+            return self.ops.linear(y, L["w_out"], L.get("w_out@packed"), defer=True)
         q, k, v, g, beta = ops.gdn_prep(proj, self.conv_state[i], L["conv_w"], L["a_log"], L["dt_bias"],
                                         conv_dim=c.conv_dim, qk_dim=c.gdn_heads_k * c.gdn_dk, hv=hv,
                                         b_offset=c.conv_dim + vd, a_offset=c.conv_dim + vd + hv)
