@@ -17,6 +17,9 @@ Prints one JSON line.  Workloads:
   reference's decode tokens/s definition.
 * ``gdn_decode``: the state-update kernel alone on a [B, 32, 128, 128] fp32
   state (``--batch``, default 64) with bf16 q/k/v, cycling over 4 layer states.
+* ``gdn_decode_fused``: the model's per-layer GDN decode core (conv window
+  update, state update, gated norm; ``--batch``, default 128), 4 rotating
+  layers.
 * ``gdn_prefill``: varlen chunked prefill of one GDN layer on the MFMA chunk
   kernel (32 packed sequences, lengths U[512, 8192]); reports MFMA utilisation
   beside the HBM fraction.
@@ -24,10 +27,11 @@ Prints one JSON line.  Workloads:
   counters behind ``roofline.traffic``.
 
 Timing: W untimed steps, then K steps between two device synchronisations.
-``roofline`` prices the GDN state-update kernel (the dominant hot-path kernel):
-its algorithmic bytes per launch at the model's decode shape over its average
+``roofline`` prices the fused GDN decode core (the dominant hot-path kernel:
+conv window update, state update and gated norm of one GDN layer): its
+algorithmic bytes per launch at the model's decode shape over its average
 launch time, measured here with HIP events on the stream the kernel runs on,
-cycling over the model's 27 layer states.  ``cpu_baseline`` runs the same
+cycling over the model's 27 GDN layers.  ``cpu_baseline`` runs the same
 model's decode step on the host cores with the oracle's recurrence, anchor
 memory, sampler and bookkeeping, on a bounded number of steps.
 """
@@ -53,6 +57,8 @@ METRIC = "decode tokens/s at B=128 on 1 GPU; state-update HBM GB/s as % of peak"
 # ``bench.py --workload gdn_decode --batch B``, scaled by what the same counters
 # read for a 128 MiB float4 copy kernel (FETCH x 2.0, WRITE x 1.0).
 TRAFFIC_GDN_DECODE = {128: (133803.7 * 2.0 + 263283.8) * 1024}
+# The same for gdn_decode_fused_kernel (``--workload gdn_decode_fused``), by batch rows.
+TRAFFIC_GDN_FUSED = {128: (137924.0 * 2.0 + 272580.8) * 1024}
 
 
 def gdn_state_bytes(b, h, hv, kd, vd, qkv_size, gate_size, with_indices):
@@ -63,6 +69,32 @@ def gdn_state_bytes(b, h, hv, kd, vd, qkv_size, gate_size, with_indices):
     out = b * hv * vd * qkv_size                     # o
     idx = 4 * b if with_indices else 0
     return state + inputs + gates + out + idx
+
+
+def gdn_fused_bytes(b, hv, d, conv_dim):
+    """Algorithmic HBM bytes of one decode step of the fused GDN layer core:
+    the fp32 state read + write, the projection row read (conv channels, z,
+    b, a), the conv window read + write, the conv weights, the output row."""
+    state = 2 * b * hv * d * d * 4
+    proj = b * (conv_dim + hv * d + 2 * hv) * 2
+    window = 2 * b * 3 * conv_dim * 2
+    return state + proj + window + conv_dim * 4 * 2 + b * hv * d * 2
+
+
+def _fused_step(dev, b, hv, d, conv_dim, layers_in, seed):
+    """Launch closure of the fused GDN decode core over rotating layers;
+    ``layers_in`` = [(conv_state, conv_w, a_log, dt_bias, state, norm_w)]."""
+    from yanchor_amd import layers
+
+    vd = hv * d
+    g = torch.Generator(device=dev).manual_seed(seed)
+    proj = torch.randn(b, conv_dim + vd + 2 * hv, device=dev, generator=g).to(torch.bfloat16)
+
+    def step(i):
+        conv, conv_w, a_log, dt_bias, state, norm_w = layers_in[i % len(layers_in)]
+        layers.gdn_decode_fused(proj, conv, conv_w, a_log, dt_bias, state, norm_w, 1e-6, heads=hv, head_dim=d,
+                                z_offset=conv_dim, b_offset=conv_dim + vd, a_offset=conv_dim + vd + hv)
+    return step
 
 
 def _log(msg):
@@ -95,6 +127,27 @@ def _time_launches(step, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return wall * 1e3 / steps, ev0.elapsed_time(ev1) / steps
+
+
+def gdn_fused_roofline(model, launches=216, warmup=27):
+    """Average launch time of the model's fused GDN decode core (the kernel
+    the decode step runs per GDN layer) cycling over the model's GDN layers
+    with a fresh bf16 projection row; returns the roofline object."""
+    c, b = model.cfg, model.B
+    hv, d = c.gdn_heads_v, c.gdn_dv
+    ids = sorted(model.gdn_state)
+    layers_in = [(model.conv_state[i], model.layers[i]["conv_w"], model.layers[i]["a_log"], model.layers[i]["dt_bias"],
+                  model.gdn_state[i], model.layers[i]["gnorm"]) for i in ids]
+    step = _fused_step(model.device, b, hv, d, c.conv_dim, layers_in, seed=7)
+    _, ms = _time_launches(step, launches, warmup)
+    nbytes = gdn_fused_bytes(b, hv, d, c.conv_dim)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_GDN_FUSED.get(b),
+            "kernel": "gdn_decode_fused_kernel", "bytes_per_launch": nbytes, "avg_launch_us": ms * 1e3,
+            "launches": launches,
+            "shape": f"state fp32 [{b}, {hv}, {d}, {d}] + conv window bf16 [{b}, 3, {c.conv_dim}], "
+                     f"{len(layers_in)} rotating layers"}
 
 
 def gdn_roofline(states, b, h, kd, vd, launches=216, warmup=27):
@@ -131,9 +184,8 @@ def bench_model_decode(steps, warmup, cpu, batch=128):
     _log(f"model_decode: model built, {warmup} warm-up + {steps} timed steps")
     met = rt.run_decode_benchmark(model, steps=steps, warmup=warmup, rate=4.0, prompt_len=128, mean_len=1024,
                                   poll_interval=32)
-    states = [model.gdn_state[i] for i in sorted(model.gdn_state)]
-    _log(f"model_decode: {met.decode_tokens_per_second:.0f} tokens/s; timing the GDN state update")
-    roof = gdn_roofline(states, batch, cfg.gdn_heads_k, cfg.gdn_dk, cfg.gdn_dv)
+    _log(f"model_decode: {met.decode_tokens_per_second:.0f} tokens/s; timing the fused GDN decode core")
+    roof = gdn_fused_roofline(model)
     res = {
         "value": met.decode_tokens_per_second,
         "unit": "tokens/s",
@@ -152,7 +204,7 @@ def bench_model_decode(steps, warmup, cpu, batch=128):
                    "wall_seconds": met.generation_wall_seconds, "refilled": met.refilled,
                    "completed": met.completed, "peak_hbm_gib": met.peak_allocated_gib, **met.extra},
     }
-    del model, states
+    del model
     torch.cuda.empty_cache()
     if cpu:
         res["cpu_baseline"] = cpu_model_decode(batch)
@@ -291,6 +343,44 @@ def bench_gdn_decode(steps, warmup, cpu, batch=64):
     return res
 
 
+def bench_gdn_decode_fused(steps, warmup, cpu, batch=128):
+    """The fused GDN decode core alone at the model's layer shape, 4 rotating
+    layers of synthetic state / conv window / weights."""
+    dev = torch.device("cuda:0")
+    hv, d, n_layers = 32, 128, 4
+    conv_dim = 3 * hv * d
+    g = torch.Generator(device=dev).manual_seed(11)
+
+    def rnd(*shape, scale=1.0, dtype=torch.bfloat16):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(dtype)
+
+    layers_in = [(rnd(batch, 3, conv_dim), rnd(conv_dim, 4, scale=0.5),
+                  torch.log(torch.linspace(1.0, 16.0, hv, device=dev)), torch.linspace(-1.0, 1.0, hv, device=dev),
+                  rnd(batch, hv, d, d, scale=0.02, dtype=torch.float32), rnd(d, scale=0.1))
+                 for _ in range(n_layers)]
+    step = _fused_step(dev, batch, hv, d, conv_dim, layers_in, seed=12)
+    ms_per_step, kernel_ms = _time_launches(step, steps, warmup)
+    nbytes = gdn_fused_bytes(batch, hv, d, conv_dim)
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    res = {
+        "value": batch / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "ms_per_step": ms_per_step,
+        "dtype": "f32",
+        "config": {"workload": f"gdn_decode_fused: one GDN layer's decode core (conv update, state update, "
+                               f"gated norm), state fp32 [{batch}, 32, 128, 128] in place, bf16 projection row, "
+                               f"4 rotating layers", "global_batch": batch, "seq_len": 1,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_GDN_FUSED.get(batch),
+                     "kernel": "gdn_decode_fused_kernel", "bytes_per_launch": nbytes,
+                     "avg_launch_us": kernel_ms * 1e3},
+    }
+    if cpu:
+        res["cpu_baseline"] = cpu_gdn_decode(batch, 32, hv, d, d)
+    return res
+
+
 def cpu_gdn_decode(b, h, hv, kd, vd, budget_s=12.0) -> dict:
     """The oracle's token recurrence in torch float32 on the host cores, on the
     same decode shape, repeated until ~budget_s of CPU work."""
@@ -417,7 +507,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (model_decode 2048, gdn_decode 200)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (model_decode 64, gdn_decode 20)")
     ap.add_argument("--workload", default="model_decode",
-                    choices=["model_decode", "gdn_decode", "gdn_prefill", "hbm_copy"])
+                    choices=["model_decode", "gdn_decode", "gdn_decode_fused", "gdn_prefill", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=None, help="slots (model_decode 128) / rows (gdn_decode 64)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -430,8 +520,10 @@ def main() -> int:
         res = bench_model_decode(steps, warmup, not args.no_cpu, batch=args.batch or 128)
     else:
         steps, warmup = args.steps or 200, 20 if args.warmup is None else args.warmup
-        fn = {"gdn_decode": bench_gdn_decode, "gdn_prefill": bench_gdn_prefill, "hbm_copy": bench_hbm_copy}
-        res = fn[args.workload](steps, warmup, not args.no_cpu, batch=args.batch or 64)
+        fn = {"gdn_decode": bench_gdn_decode, "gdn_decode_fused": bench_gdn_decode_fused,
+              "gdn_prefill": bench_gdn_prefill, "hbm_copy": bench_hbm_copy}
+        res = fn[args.workload](steps, warmup, not args.no_cpu,
+                                batch=args.batch or (128 if args.workload == "gdn_decode_fused" else 64))
     line = {"metric": res.get("metric", METRIC), "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": steps, "warmup": warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
