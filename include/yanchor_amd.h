@@ -153,7 +153,7 @@ int64_t yh_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t n_seqs, int64
  *              (vllm_yanchor.py:21-24, 49-64).
  * Per head: out = softmax([q.K^T / sqrt(D) over live slots, 0]) . [V; 0] (a
  * sink logit of 0 with value 0), accumulated in fp32.
- * Requirements: D in {64, 128}; H / G in {1, 2, 4}; capacity a multiple of 64,
+ * Requirements: D in {64, 128}; H / G in {1, 2, 4}; capacity a multiple of 16,
  * at most 1024; 16-byte aligned query/keys/values rows.
  */
 int yh_anchor_read(const void* query, const void* keys, const void* values, const int32_t* positions,
@@ -168,7 +168,7 @@ int yh_anchor_read(const void* query, const void* keys, const void* values, cons
  * marks live slots (>= 0).  Replaces the physical-ring SWA decode attention
  * (fixed_memory_physical_ring_decode_attention, runtime/model/
  * inference_kernels.py:555-640) for D in {64, 128}, H / G in {1, 2, 4} and a
- * window that is a multiple of 64, at most 1024.
+ * window that is a multiple of 16, at most 1024.
  */
 int yh_window_attend(const void* query, const void* keys, const void* values, const int32_t* positions,
                      const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t window, int64_t D,

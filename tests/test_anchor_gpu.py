@@ -52,6 +52,25 @@ def test_read_matches_oracle(gpu, dtype, tol, r, d):
     assert rel_err(got, want) <= tol, rel_err(got, want)
 
 
+@pytest.mark.parametrize("cap", [16, 48, 96])
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 2e-2), (torch.float32, 1e-3)])
+def test_read_small_capacities(gpu, cap, dtype, tol):
+    """Capacities that are not multiples of the 32-slot block (16-slot
+    blocks) or give an odd block count."""
+    st = workloads.anchor_state(5, 2, cap, 64, 128, dtype=dtype, seed=cap + 3)
+    q = workloads.anchor_query(5, 8, 128, dtype=dtype, seed=cap + 4)
+    got = im.committed_gqa(q.to(gpu), _to(st, gpu))
+    want = ref.committed_read(q, st)
+    assert rel_err(got, want) <= tol, rel_err(got, want)
+
+
+def test_commit_top16_of_chunk64(gpu):
+    """The long-horizon setting: 16 committed slots, commit chunk 64 (the best
+    16 of 80 candidates kept)."""
+    st = workloads.anchor_state(4, 8, 16, 64, 128, seed=31, fill_pending=50)
+    assert _drive(gpu, st, 40, 64, seed=32, p_active=0.95) >= 4
+
+
 def test_read_decode_config(gpu):
     """64 rows x 32 groups x 256 slots x 128 dims bf16, slots live with p = 0.7."""
     st = workloads.anchor_state(64, 32, 256, 64, 128, seed=workloads.SEED0 + 1)

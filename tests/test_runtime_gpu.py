@@ -28,19 +28,23 @@ def small_cfg(**kw):
     return rt.ModelConfig(**base)
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 5e-2)])
-def test_decode_after_prefill_matches_longer_prefill(gpu, dtype, tol):
+@pytest.mark.parametrize("dtype,tol,b,over", [
+    (torch.float32, 1e-4, 3, {}), (torch.bfloat16, 5e-2, 3, {}),
+    # as many key heads as value heads (the fused GDN decode core), more than
+    # 128 slots (projections past the packed kernel's rows), a 16-slot memory
+    (torch.bfloat16, 5e-2, 130, {"gdn_heads_k": 4, "memory_capacity": 16})])
+def test_decode_after_prefill_matches_longer_prefill(gpu, dtype, tol, b, over):
     """fp32 pins the cache logic tightly; bf16 bounds the rounding drift."""
-    cfg = small_cfg()
-    m = rt.Model(cfg, batch=3, device=gpu, seed=1, dtype=dtype)
+    cfg = small_cfg(**over)
+    m = rt.Model(cfg, batch=b, device=gpu, seed=1, dtype=dtype)
     g = torch.Generator().manual_seed(2)
-    prompts = torch.randint(0, cfg.vocab, (3, 21), generator=g).to(gpu)
+    prompts = torch.randint(0, cfg.vocab, (b, 21), generator=g).to(gpu)
     ref_logits, _ = m.prefill(prompts)                      # 21 tokens
     logits, caches = m.prefill(prompts[:, :20])              # 20 tokens ...
     for dst, src in zip(m.cache_tensors(), caches):
         dst.copy_(src)
-    pos = torch.full((3,), 20, dtype=torch.long, device=gpu)
-    valid = torch.ones(3, dtype=torch.bool, device=gpu)
+    pos = torch.full((b,), 20, dtype=torch.long, device=gpu)
+    valid = torch.ones(b, dtype=torch.bool, device=gpu)
     out = m.decode_step(prompts[:, 20], pos, valid)          # ... plus one decode step
     torch.cuda.synchronize()
     assert rel_err(out, ref_logits) <= tol, rel_err(out, ref_logits)

@@ -163,9 +163,10 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 }
 
 // One workgroup per (batch row, group), one pass over the slots.  Its waves
-// take 32-slot blocks in turn.  Within a block LPR = D/8 lanes cover one row
-// (8 elements each) and a wave instruction covers RPI = 64/LPR rows, so
-// NI = 32/RPI instructions cover the block; a reduce-scatter butterfly over the
+// take BS-slot blocks (32, or 16 for a capacity that is an odd multiple of
+// 16) in turn.  Within a block LPR = D/8 lanes cover one row (8 elements
+// each) and a wave instruction covers RPI = 64/LPR rows, so NI = BS/RPI
+// instructions cover the block; a reduce-scatter butterfly over the
 // LPR lanes leaves the logit of slot i*RPI + rr on the F = LPR/NI lanes
 // s = i*F .. i*F + F-1 of row group rr.  Loads are unconditional and
 // software-pipelined: the keys (and positions) of a wave's next block are
@@ -184,17 +185,16 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 // per SIMD).
 template <bool SINK> constexpr int read_waves() { return 4; }
 
-template <int DT, int D, int R, bool SINK>
+template <int DT, int D, int R, bool SINK, int BS>
 __global__ void __launch_bounds__(read_waves<SINK>() * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 anchor_read_kernel(ReadArgs a) {
   constexpr int kReadWaves = read_waves<SINK>();
   constexpr int kReadThreads = kReadWaves * 64;
   constexpr int LPR = D / 8;
   constexpr int RPI = kWave / LPR;
-  constexpr int BS = 32;
   constexpr int NI = BS / RPI;
   constexpr int F = LPR / NI;
-  static_assert(NI * RPI == BS && F * NI == LPR && F >= 1, "32-slot blocks");
+  static_assert(NI * RPI == BS && F * NI == LPR && F >= 1 && BS <= 32, "slot blocks");
 
   __shared__ float wm[kReadWaves][R];
   __shared__ float wl[kReadWaves][R];
@@ -536,23 +536,31 @@ __global__ void anchor_advance_kernel(int64_t* count, int64_t* total, const uint
   total[b * total_rs] += act;
 }
 
-template <int DT, int D, bool SINK>
+// 32-slot blocks, or 16-slot blocks for a capacity that is an odd multiple of 16.
+template <int DT, int D, bool SINK, int BS>
 int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(read_waves<SINK>() * 64);
   switch (R) {
-    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, BS>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, BS>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, BS>), grid, block, 0, st, a); break;
     default: set_error("anchor_read: heads per group must be 1, 2 or 4 (got %d)", R); return YH_ERR_INVALID;
   }
   YH_CHECK_LAUNCH("anchor_read");
   return YH_OK;
 }
 
+template <int DT, int D>
+int launch_read_b(int R, bool sink, const ReadArgs& a, hipStream_t st) {
+  if (a.KC % 32 == 0)
+    return sink ? launch_read_r<DT, D, true, 32>(R, a, st) : launch_read_r<DT, D, false, 32>(R, a, st);
+  return sink ? launch_read_r<DT, D, true, 16>(R, a, st) : launch_read_r<DT, D, false, 16>(R, a, st);
+}
+
 template <int DT>
 int launch_read_d(int D, int R, bool sink, const ReadArgs& a, hipStream_t st) {
-  if (D == 128) return sink ? launch_read_r<DT, 128, true>(R, a, st) : launch_read_r<DT, 128, false>(R, a, st);
-  if (D == 64) return sink ? launch_read_r<DT, 64, true>(R, a, st) : launch_read_r<DT, 64, false>(R, a, st);
+  if (D == 128) return launch_read_b<DT, 128>(R, sink, a, st);
+  if (D == 64) return launch_read_b<DT, 64>(R, sink, a, st);
   set_error("anchor_read: head dim must be 64 or 128 (got %d)", D);
   return YH_ERR_INVALID;
 }
@@ -571,8 +579,8 @@ static int anchor_read_impl(bool sink, const void* query, const void* keys, cons
   YH_CHECK_ARG(query && keys && values && positions && out, "anchor_read: null tensor pointer");
   YH_CHECK_ARG(B >= 0 && G > 0 && H > 0 && H % G == 0, "anchor_read: bad B/H/G (%lld/%lld/%lld)",
                (long long)B, (long long)H, (long long)G);
-  YH_CHECK_ARG(capacity > 0 && capacity % 64 == 0 && capacity <= kMaxCap,
-               "anchor_read: capacity must be a positive multiple of 64 up to %d (got %lld)", kMaxCap,
+  YH_CHECK_ARG(capacity > 0 && capacity % 16 == 0 && capacity <= kMaxCap,
+               "anchor_read: capacity must be a positive multiple of 16 up to %d (got %lld)", kMaxCap,
                (long long)capacity);
   YH_CHECK_ARG(is_float_dtype(dtype), "anchor_read: unsupported dtype %d", dtype);
   YH_CHECK_ARG(indices != nullptr || n_state_rows >= B, "anchor_read: state has fewer rows than the batch");
