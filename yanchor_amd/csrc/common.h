@@ -32,16 +32,14 @@ void set_error(const char* fmt, ...);
   } while (0)
 
 // ---- scalar conversions ----------------------------------------------------
-// bf16 <-> f32 by bit manipulation; f32 -> bf16 rounds to nearest even, which
-// is what torch's .to(torch.bfloat16) does for finite values.
+// bf16 -> f32 by a shift; f32 -> bf16 on the hardware conversion
+// (v_cvt_pk_bf16_f32), which rounds to nearest even as torch's
+// .to(torch.bfloat16) does, and turns NaN into a quiet NaN.
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));

@@ -154,7 +154,7 @@ struct __align__(16) PrepSmem {
   union {
     uint16_t q[kC * SKR];   // Q [t][d]          (Q K^T)
     float x[3 * 256];       // inversion scratch (after the products)
-    uint16_t out[3 * kC * SK64];  // T beta hi / lo and A staged for coalesced stores (after the inversion)
+    uint16_t out[kC * SK64];  // A staged for coalesced stores (after the inversion)
   } qx;
   float l[kC * SF];         // L
   float rk[kC], rqs[kC], G[kC], beta[kC];
@@ -342,10 +342,10 @@ __global__ void __launch_bounds__(kPrepThreads) chunk_prep_kernel(PrepArgs a) {
 
   invert_unit_lower(sm.l, sm.kt0.t, sm.qx.x);  // ends with a barrier
 
-  // ---- T diag(beta) (hi / lo) and A -> LDS staging -> coalesced stores ----
-  uint16_t* thi_s = &sm.qx.out[0];
-  uint16_t* tlo_s = &sm.qx.out[kC * SK64];
-  uint16_t* a_s = &sm.qx.out[2 * kC * SK64];
+  // ---- T diag(beta) (hi / lo) straight to the workspace (consecutive threads,
+  // consecutive 8-byte pieces); A through LDS for coalesced stores ----
+  uint16_t* thi_g = a.thi + ch * kC * kC;
+  uint16_t* tlo_g = a.tlo + ch * kC * kC;
 #pragma unroll
   for (int it = 0; it < 4; ++it) {  // T rows: 64 x 64, 16 elements per thread
     const int e = (it * kPrepThreads + tid) * 4;
@@ -359,9 +359,10 @@ __global__ void __launch_bounds__(kPrepThreads) chunk_prep_kernel(PrepArgs a) {
       h[j] = f32_to_bf16(x[j]);
       lo[j] = f32_to_bf16(x[j] - bfv(h[j]));
     }
-    *reinterpret_cast<uint2*>(&thi_s[t * SK64 + s4]) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-    *reinterpret_cast<uint2*>(&tlo_s[t * SK64 + s4]) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
+    *reinterpret_cast<uint2*>(thi_g + t * kC + s4) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+    *reinterpret_cast<uint2*>(tlo_g + t * kC + s4) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
   }
+  uint16_t* a_s = sm.qx.out;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     const int tau = w + 4 * tt, m0 = 16 * (tau >> 2), n0 = 16 * (tau & 3);
@@ -369,16 +370,13 @@ __global__ void __launch_bounds__(kPrepThreads) chunk_prep_kernel(PrepArgs a) {
     for (int i = 0; i < 4; ++i) a_s[(m0 + rq4 + i) * SK64 + n0 + r16] = f32_to_bf16(areg[tt][i]);
   }
   __syncthreads();
-  uint16_t* dst[3] = {a.thi + ch * kC * kC, a.tlo + ch * kC * kC, a.aqk + ch * kC * kC};
+  uint16_t* a_g = a.aqk + ch * kC * kC;
 #pragma unroll
-  for (int m = 0; m < 3; ++m)
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int ci = it * kPrepThreads + tid;  // 512 vectors of 8 per matrix
-      const int t = ci >> 3, s8 = (ci & 7) * 8;
-      *reinterpret_cast<uint4*>(dst[m] + t * kC + s8) =
-          *reinterpret_cast<const uint4*>(&sm.qx.out[m * kC * SK64 + t * SK64 + s8]);
-    }
+  for (int it = 0; it < 2; ++it) {
+    const int ci = it * kPrepThreads + tid;  // 512 vectors of 8
+    const int t = ci >> 3, s8 = (ci & 7) * 8;
+    *reinterpret_cast<uint4*>(a_g + t * kC + s8) = *reinterpret_cast<const uint4*>(&a_s[t * SK64 + s8]);
+  }
 }
 
 // ---------------------------------------------------------------------------
