@@ -386,8 +386,9 @@ __global__ void __launch_bounds__(kPrepThreads) chunk_prep_kernel(PrepArgs a) {
 // operand straight from the wave's own registers.  The MFMA reduction index
 // of a 32-deep step is visited in the order the accumulator layout provides:
 // element j of quad q is row 32 ks + 4 q + j (j < 4) or 32 ks + 16 + 4 q +
-// j - 4 (j >= 4), and the A operands (rows of Q, K, T diag(beta), A, K^T in
-// LDS) are read in that same order, two 8-byte pieces per lane.  Only the
+// j - 4 (j >= 4), and the A operands are read in that same order: rows of
+// Q, K, T diag(beta) and A from column-permuted LDS rows (one 16-byte read),
+// K^T and V^T by transposing reads of the row-major K and V.  Only the
 // chunk inputs go through LDS: two barriers per chunk.
 struct ScanArgs {
   const uint16_t* q;     // [total, H, K]
@@ -409,9 +410,8 @@ struct ScanArgs {
 template <int NW>
 struct __align__(16) ScanSmem {
   uint16_t q[kC * SKR];        // Q [t][d]
-  uint16_t k[kC * SKR];        // K [t][d]
-  uint16_t kt[kK * SK64];      // K^T [d][t]
-  uint16_t vt[16 * NW * SK64];  // V^T [v][t]
+  uint16_t k[kC * SKR];        // K [t][d]  (K^T operands by transposing reads)
+  uint16_t v[kC * SKR];        // V [t][v]  (V^T operands by transposing reads)
   uint16_t thi[kC * SK64];     // T diag(beta) [t][s], hi
   uint16_t tlo[kC * SK64];     // lo
   uint16_t aqk[kC * SK64];     // A [t][s]
@@ -440,23 +440,22 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NW>& r, const ScanArgs& a, 
                                            int hv, int hk) {
   using R = ChunkRegs<NW>;
   constexpr int NT = R::NT, V = 16 * NW;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x;
   const int64_t ch = static_cast<int64_t>(chunk) * a.HV + hv;
-  const bool live = lane < Lc;
+  // Row-major pieces: 16 lanes per 128-wide token row (2 NW per V-wide row),
+  // so a wave instruction covers whole lines.
 #pragma unroll
   for (int it = 0; it < R::kRow; ++it) {
-    // lane = token: each wave instruction covers 64 tokens x 8 columns, so the
-    // transposed LDS writes of K are contiguous
-    const int d8 = (it * NW + w) * 8;
-    const int64_t off = ((tok0 + lane) * a.H + hk) * kK + d8;
-    r.q[it] = live ? *reinterpret_cast<const uint4*>(a.q + off) : make_uint4(0, 0, 0, 0);
-    r.k[it] = live ? *reinterpret_cast<const uint4*>(a.k + off) : make_uint4(0, 0, 0, 0);
+    const int ci = it * NT + tid, t = ci >> 4;
+    const int64_t off = ((tok0 + t) * a.H + hk) * kK + (ci & 15) * 8;
+    r.q[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.q + off) : make_uint4(0, 0, 0, 0);
+    r.k[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.k + off) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int it = 0; it < R::kVec; ++it) {
-    const int v8 = (it * NW + w) * 8;
-    r.v[it] = live ? *reinterpret_cast<const uint4*>(a.v + ((tok0 + lane) * a.HV + hv) * V + v8)
-                   : make_uint4(0, 0, 0, 0);
+    const int ci = it * NT + tid, t = ci / (2 * NW);
+    r.v[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.v + ((tok0 + t) * a.HV + hv) * V + (ci % (2 * NW)) * 8)
+                     : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int it = 0; it < R::kSq; ++it) {
@@ -474,13 +473,25 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NW>& r, const ScanArgs& a, 
   }
 }
 
-// 8 bf16 of an LDS row in the permuted reduction order of quad `quad` for the
-// 32-deep step starting at column k0: columns k0 + 4 quad + 0..3, then
-// k0 + 16 + 4 quad + 0..3.
-__device__ __forceinline__ bf16x8_t lds8p(const uint16_t* row, int k0, int quad) {
-  const uint2 lo = *reinterpret_cast<const uint2*>(row + k0 + 4 * quad);
-  const uint2 hi = *reinterpret_cast<const uint2*>(row + k0 + 16 + 4 * quad);
-  return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+// A-operand matrices (Q, K, T diag(beta), A) are stored in LDS with their
+// columns permuted within each 32-column block so that the 8 reduction
+// indices of quad q for a 32-deep step -- columns 4q + 0..3 and 16 + 4q +
+// 0..3 -- sit next to each other: column c (c % 4 == 0) of block b is at
+// 32 b + 8 ((c / 4) % 4) + 4 ((c % 32) / 16).  One 16-byte read then gives a
+// lane its operand.
+__device__ __forceinline__ int pcol(int c) {
+  const int b = (c & 31) >> 2;
+  return (c & ~31) + 8 * (b & 3) + 4 * (b >> 2);
+}
+// Store 8 consecutive columns c8 .. c8 + 7 (c8 % 8 == 0) of a row.
+__device__ __forceinline__ void put8p(uint16_t* row, int c8, uint4 x) {
+  *reinterpret_cast<uint2*>(row + pcol(c8)) = make_uint2(x.x, x.y);
+  *reinterpret_cast<uint2*>(row + pcol(c8 + 4)) = make_uint2(x.z, x.w);
+}
+// The operand of quad `quad` for the 32-deep step starting at column k0 of a
+// column-permuted row.
+__device__ __forceinline__ bf16x8_t lds8r(const uint16_t* row, int k0, int quad) {
+  return lds8(row + k0 + 8 * quad);
 }
 // The B operand of a 32-deep step from two accumulator tiles (rows 32 ks ..
 // 32 ks + 15 and 32 ks + 16 .. 32 ks + 31), as bf16 hi / lo.
@@ -488,14 +499,25 @@ __device__ __forceinline__ void pack_b(const f32x4v& t0, const f32x4v& t1, bf16x
   const float x[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
   split8(x, hi, lo);
 }
-// Transposed write of one 16-byte vector (8 consecutive columns of row `t`).
-__device__ __forceinline__ void put_t(uint16_t* mt, int stride, int c8, int t, uint4 x) {
-  const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    mt[(c8 + 2 * j) * stride + t] = static_cast<uint16_t>(xs[j] & 0xffff);
-    mt[(c8 + 2 * j + 1) * stride + t] = static_cast<uint16_t>(xs[j] >> 16);
-  }
+// Operand of a 32-deep step whose reduction index is the ROW of a row-major
+// LDS matrix m (row stride SKR): lane (i = lane % 16, quad) gets column
+// c0 + i at rows k0 + 4 quad + 0..3 and k0 + 16 + 4 quad + 0..3 -- the
+// permuted reduction order above -- by two ds_read_b64_tr_b16.  That
+// instruction transposes within each 16-lane group: lane 4m + e receives, in
+// slot j, element e of the 8 bytes addressed by lane 4j + m.  So lane
+// 4j + m of the group addresses row k0 (+16) + 4 quad + j, columns
+// c0 + 4m .. c0 + 4m + 3.
+typedef short s16x4v __attribute__((ext_vector_type(4)));
+typedef short s16x8v __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4v lds_s16x4v;
+template <bool PERM>  // m's columns permuted (pcol) or plain
+__device__ __forceinline__ bf16x8_t lds8t(const uint16_t* m, int k0, int c0, int lane) {
+  const int i = lane & 15, quad = lane >> 4;
+  const int c = c0 + 4 * (i & 3);
+  const uint16_t* p = m + (k0 + 4 * quad + (i >> 2)) * SKR + (PERM ? pcol(c) : c);
+  const s16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p));
+  const s16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p + 16 * SKR));
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 template <int NW>
@@ -532,21 +554,23 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
     // ---- this chunk's inputs -> LDS, then prefetch the next chunk ----
 #pragma unroll
     for (int it = 0; it < R::kRow; ++it) {
-      const int d8 = (it * NW + w) * 8;
-      *reinterpret_cast<uint4*>(&sm.q[lane * SKR + d8]) = cur.q[it];
-      *reinterpret_cast<uint4*>(&sm.k[lane * SKR + d8]) = cur.k[it];
-      put_t(sm.kt, SK64, d8, lane, cur.k[it]);
+      const int ci = it * NT + tid, o = (ci >> 4) * SKR, c8 = (ci & 15) * 8;
+      put8p(&sm.q[o], c8, cur.q[it]);
+      put8p(&sm.k[o], c8, cur.k[it]);
     }
 #pragma unroll
-    for (int it = 0; it < R::kVec; ++it) put_t(sm.vt, SK64, (it * NW + w) * 8, lane, cur.v[it]);
+    for (int it = 0; it < R::kVec; ++it) {
+      const int ci = it * NT + tid;
+      *reinterpret_cast<uint4*>(&sm.v[(ci / (2 * NW)) * SKR + (ci % (2 * NW)) * 8]) = cur.v[it];
+    }
 #pragma unroll
     for (int it = 0; it < R::kSq; ++it) {
       const int ci = it * NT + tid;
       if (ci < kC * kC / 8) {
-        const int o = (ci >> 3) * SK64 + (ci & 7) * 8;
-        *reinterpret_cast<uint4*>(&sm.thi[o]) = cur.thi[it];
-        *reinterpret_cast<uint4*>(&sm.tlo[o]) = cur.tlo[it];
-        *reinterpret_cast<uint4*>(&sm.aqk[o]) = cur.aqk[it];
+        const int o = (ci >> 3) * SK64, c8 = (ci & 7) * 8;
+        put8p(&sm.thi[o], c8, cur.thi[it]);
+        put8p(&sm.tlo[o], c8, cur.tlo[it]);
+        put8p(&sm.aqk[o], c8, cur.aqk[it]);
       }
     }
 #pragma unroll
@@ -557,7 +581,6 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       else if (ci < 3 * kC) sm.ek[ci - 2 * kC] = cur.scal[it];
       else if (ci == 3 * kC) sm.egl = cur.scal[it];
     }
-    if (c + 1 < ce) load_chunk<NW>(cur, a, c + 1, tok0 + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
     lds_barrier();
 
     // ---- Q S (1 pass) and P = K S (2 passes), four row tiles of this column block ----
@@ -571,18 +594,21 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const int row = (16 * mt + r16) * SKR;
-        const bf16x8_t aq = lds8p(&sm.q[row], 32 * ks, quad);
-        const bf16x8_t ak = lds8p(&sm.k[row], 32 * ks, quad);
+        const bf16x8_t aq = lds8r(&sm.q[row], 32 * ks, quad);
+        const bf16x8_t ak = lds8r(&sm.k[row], 32 * ks, quad);
         qs[mt] = mfma(aq, bh, qs[mt]);
         ps[mt] = mfma(ak, bh, ps[mt]);
         ps[mt] = mfma(ak, bl, ps[mt]);
       }
     }
+    // Prefetch the next chunk while the products above drain: the 8 waves
+    // reach this point at different times, so their loads queue less.
+    if (c + 1 < ce) load_chunk<NW>(cur, a, c + 1, tok0 + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
     // ---- v_new = T diag(beta) V - T diag(beta) (diag(e^G rk) P): 2 + 3 passes, T lower triangular ----
     bf16x8_t vb[2], ph[2], pl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      vb[ks] = lds8p(&sm.vt[vcol * SK64], 32 * ks, quad);
+      vb[ks] = lds8t<false>(sm.v, 32 * ks, 16 * w, lane);
       f32x4v p0 = ps[2 * ks], p1 = ps[2 * ks + 1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -599,8 +625,8 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       for (int ks = 0; ks < 2; ++ks) {
         if (32 * ks <= 16 * mt + 15) {
           const int row = (16 * mt + r16) * SK64;
-          const bf16x8_t th = lds8p(&sm.thi[row], 32 * ks, quad);
-          const bf16x8_t tl = lds8p(&sm.tlo[row], 32 * ks, quad);
+          const bf16x8_t th = lds8r(&sm.thi[row], 32 * ks, quad);
+          const bf16x8_t tl = lds8r(&sm.tlo[row], 32 * ks, quad);
           u = mfma(th, vb[ks], u);
           u = mfma(tl, vb[ks], u);
           y = mfma(th, ph[ks], y);
@@ -625,12 +651,19 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       for (int i = 0; i < 4; ++i) acc[i] *= sm.orow[16 * mt + rq4 + i];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        if (32 * ks <= 16 * mt + 15) acc = mfma(lds8p(&sm.aqk[(16 * mt + r16) * SK64], 32 * ks, quad), vnb[ks], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * mt + rq4 + i;
-        if (t < Lc) a.o[((tok0 + t) * a.HV + hv) * V + vcol] = f32_to_bf16(acc[i]);
-      }
+        if (32 * ks <= 16 * mt + 15) acc = mfma(lds8r(&sm.aqk[(16 * mt + r16) * SK64], 32 * ks, quad), vnb[ks], acc);
+      // Column pairs (vcol, vcol ^ 1) go out as 4-byte stores: the even lane
+      // stores rows 0, 1 of its quad, the odd lane rows 2, 3.
+      const bool odd = r16 & 1;
+      const float y0 = __shfl_xor(odd ? acc[0] : acc[2], 1, kWave);
+      const float y1 = __shfl_xor(odd ? acc[1] : acc[3], 1, kWave);
+      const float2 p0 = odd ? make_float2(y0, acc[2]) : make_float2(acc[0], y0);
+      const float2 p1 = odd ? make_float2(y1, acc[3]) : make_float2(acc[1], y1);
+      const int t0 = 16 * mt + rq4 + (odd ? 2 : 0), c0 = vcol & ~1;
+      if (t0 < Lc)
+        *reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0) * a.HV + hv) * V + c0) = pack2(f32_to_bf16(p0.x), f32_to_bf16(p0.y));
+      if (t0 + 1 < Lc)
+        *reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0 + 1) * a.HV + hv) * V + c0) = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
     }
     // ---- S <- e^{G_last} S + K^T diag(d2) v_new (2 passes) ----
     bf16x8_t zh[2], zl[2];
@@ -650,7 +683,7 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       f32x4v s = S[dt] * egl;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8_t ak = lds8p(&sm.kt[(16 * dt + r16) * SK64], 32 * ks, quad);
+        const bf16x8_t ak = lds8t<true>(sm.k, 32 * ks, 16 * dt, lane);
         s = mfma(ak, zh[ks], s);
         s = mfma(ak, zl[ks], s);
       }
