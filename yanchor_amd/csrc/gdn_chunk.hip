@@ -145,6 +145,7 @@ struct PrepArgs {
 };
 
 constexpr int kPrepThreads = 256;
+constexpr int kPrepGrid = 768;  // persistent prep workgroups: three per CU on 256 CUs
 
 struct __align__(16) PrepSmem {
   union {
@@ -188,7 +189,7 @@ __device__ void invert_unit_lower(const float* l, float* t, float* x) {
       if ((c >> 4) > (r >> 4)) t[r * SF + c] = 0.f;
     }
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll 1
   for (int lev = 1; lev < 4; ++lev) {
     const int nb = 4 - lev;  // blocks (i, i - lev), i = lev..3; 64 threads per block
@@ -211,7 +212,7 @@ __device__ void invert_unit_lower(const float* l, float* t, float* x) {
       }
       *reinterpret_cast<float4*>(&x[bi * 256 + r * 16 + c4]) = acc;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < nb * 64) {
       const int bi = tid >> 6, r = (tid >> 2) & 15, c4 = (tid & 3) * 4;
       const int i = lev + bi, j = i - lev;
@@ -229,99 +230,127 @@ __device__ void invert_unit_lower(const float* l, float* t, float* x) {
       }
       *reinterpret_cast<float4*>(&t[(16 * i + r) * SF + 16 * j + c4]) = make_float4(-acc.x, -acc.y, -acc.z, -acc.w);
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
-__global__ void __launch_bounds__(kPrepThreads) chunk_prep_kernel(PrepArgs a) {
-  __shared__ PrepSmem sm;
-  const int chunk = blockIdx.x, hv = blockIdx.y;
-  if (chunk >= a.cstart[a.n_seqs]) return;
+// Inputs of one (chunk, head) item, held in registers from their load (one
+// item ahead) to their move into LDS.
+struct PrepRegs {
+  uint4 k[4], q[4];
+  float g, b;
+};
+
+__device__ __forceinline__ void prep_load(PrepRegs& r, const PrepArgs& a, int item) {
+  const int chunk = item / a.HV, hv = item % a.HV;
   const int64_t tok0 = a.table[4 * chunk];
   const int Lc = a.table[4 * chunk + 1];
   const int hk = hv / (a.HV / a.H);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int r16 = lane & 15, kq = (lane >> 4) * 8, rq4 = (lane >> 4) * 4;
-  const int64_t ch = static_cast<int64_t>(chunk) * a.HV + hv;  // (chunk, head) record
-
-  // ---- stage K, Q rows (coalesced; rows t >= Lc are zero) and the gates ----
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int ci = it * kPrepThreads + tid;
     const int t = ci >> 4, d8 = (ci & 15) * 8;
-    uint4 kw = make_uint4(0, 0, 0, 0), qw = make_uint4(0, 0, 0, 0);
-    if (t < Lc) {
-      const int64_t off = ((tok0 + t) * a.H + hk) * kK + d8;
-      kw = *reinterpret_cast<const uint4*>(a.k + off);
-      qw = *reinterpret_cast<const uint4*>(a.q + off);
-    }
-    *reinterpret_cast<uint4*>(&sm.kt0.kr[t * SKR + d8]) = kw;
-    *reinterpret_cast<uint4*>(&sm.qx.q[t * SKR + d8]) = qw;
+    const int64_t off = ((tok0 + t) * a.H + hk) * kK + d8;
+    r.k[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.k + off) : make_uint4(0, 0, 0, 0);
+    r.q[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.q + off) : make_uint4(0, 0, 0, 0);
   }
-  if (tid < kC) {
-    float gg = 0.f, bb = 0.f;
-    if (tid < Lc) {
-      gg = load_any(a.g, (tok0 + tid) * a.HV + hv, a.g_dt);
-      bb = load_any(a.beta, (tok0 + tid) * a.HV + hv, a.beta_dt);
-    }
-    sm.G[tid] = gg;
-    sm.beta[tid] = bb;
-  }
-  __syncthreads();
+  r.g = tid < Lc ? load_any(a.g, (tok0 + tid) * a.HV + hv, a.g_dt) : 0.f;
+  r.b = tid < Lc ? load_any(a.beta, (tok0 + tid) * a.HV + hv, a.beta_dt) : 0.f;
+}
 
-  // ---- norms (4 lanes per token) and the decay scan ----
-  {
-    const int t = tid >> 2, p = tid & 3;
-    float sk = 0.f, sq = 0.f;
+// The 10 lower 16 x 16 tiles (mt, nt), nt <= mt, of K K^T and Q K^T, three
+// slots per wave: (mt << 4) | nt, or -1 for an empty slot.
+__device__ __forceinline__ int prep_tile(int w, int slot) {
+  constexpr int8_t kTiles[4][3] = {{0x00, 0x10, 0x33}, {0x11, 0x20, 0x32}, {0x21, 0x22, -1}, {0x30, 0x31, -1}};
+  return kTiles[w][slot];
+}
+
+// Persistent: workgroup b takes items b, b + gridDim.x, ... of the
+// (chunk, value head) list, item = chunk * HV + head, and loads the next
+// item's rows while it works on the current one (so every barrier inside
+// waits for LDS traffic only).
+__global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a) {
+  __shared__ PrepSmem sm;
+  const int n_items = a.cstart[a.n_seqs] * a.HV;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, kq = (lane >> 4) * 8, rq4 = (lane >> 4) * 4;
+  PrepRegs cur;
+  if (static_cast<int>(blockIdx.x) < n_items) prep_load(cur, a, blockIdx.x);
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int chunk = item / a.HV, hv = item % a.HV;
+    const int64_t ch = static_cast<int64_t>(chunk) * a.HV + hv;  // (chunk, head) record
+
+    // ---- stage K, Q rows (rows t >= Lc are zero) and the gates; prefetch the next item ----
 #pragma unroll
-    for (int e = 0; e < 32; e += 8) {
-      const uint4 kv = *reinterpret_cast<const uint4*>(&sm.kt0.kr[t * SKR + 32 * p + e]);
-      const uint4 qv = *reinterpret_cast<const uint4*>(&sm.qx.q[t * SKR + 32 * p + e]);
-      const uint32_t kk[4] = {kv.x, kv.y, kv.z, kv.w}, qq[4] = {qv.x, qv.y, qv.z, qv.w};
+    for (int it = 0; it < 4; ++it) {
+      const int ci = it * kPrepThreads + tid;
+      const int t = ci >> 4, d8 = (ci & 15) * 8;
+      *reinterpret_cast<uint4*>(&sm.kt0.kr[t * SKR + d8]) = cur.k[it];
+      *reinterpret_cast<uint4*>(&sm.qx.q[t * SKR + d8]) = cur.q[it];
+    }
+    if (tid < kC) {
+      sm.G[tid] = cur.g;
+      sm.beta[tid] = cur.b;
+    }
+    if (item + static_cast<int>(gridDim.x) < n_items) prep_load(cur, a, item + gridDim.x);
+    lds_barrier();
+
+    // ---- norms (4 lanes per token) and the decay scan ----
+    {
+      const int t = tid >> 2, p = tid & 3;
+      float sk = 0.f, sq = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float k0 = __uint_as_float(kk[j] << 16), k1 = __uint_as_float(kk[j] & 0xffff0000u);
-        const float q0 = __uint_as_float(qq[j] << 16), q1 = __uint_as_float(qq[j] & 0xffff0000u);
-        sk = fmaf(k0, k0, fmaf(k1, k1, sk));
-        sq = fmaf(q0, q0, fmaf(q1, q1, sq));
+      for (int e = 0; e < 32; e += 8) {
+        const uint4 kv = *reinterpret_cast<const uint4*>(&sm.kt0.kr[t * SKR + 32 * p + e]);
+        const uint4 qv = *reinterpret_cast<const uint4*>(&sm.qx.q[t * SKR + 32 * p + e]);
+        const uint32_t kk[4] = {kv.x, kv.y, kv.z, kv.w}, qq[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float k0 = __uint_as_float(kk[j] << 16), k1 = __uint_as_float(kk[j] & 0xffff0000u);
+          const float q0 = __uint_as_float(qq[j] << 16), q1 = __uint_as_float(qq[j] & 0xffff0000u);
+          sk = fmaf(k0, k0, fmaf(k1, k1, sk));
+          sq = fmaf(q0, q0, fmaf(q1, q1, sq));
+        }
+      }
+      sk += __shfl_xor(sk, 1, kWave);
+      sq += __shfl_xor(sq, 1, kWave);
+      sk += __shfl_xor(sk, 2, kWave);
+      sq += __shfl_xor(sq, 2, kWave);
+      if (p == 0) {
+        sm.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
+        sm.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
       }
     }
-    sk += __shfl_xor(sk, 1, kWave);
-    sq += __shfl_xor(sq, 1, kWave);
-    sk += __shfl_xor(sk, 2, kWave);
-    sq += __shfl_xor(sq, 2, kWave);
-    if (p == 0) {
-      sm.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
-      sm.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-    }
-  }
-  if (w == 0) {
-    float x = sm.G[lane];
+    if (w == 0) {
+      float x = sm.G[lane];
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const float y = __shfl_up(x, off, kWave);
-      if (lane >= off) x += y;
+      for (int off = 1; off < kWave; off <<= 1) {
+        const float y = __shfl_up(x, off, kWave);
+        if (lane >= off) x += y;
+      }
+      sm.G[lane] = x;
+      if (lane == kWave - 1) sm.gl = x;
     }
-    sm.G[lane] = x;
-    if (lane == kWave - 1) sm.gl = x;
-  }
-  __syncthreads();
-  if (tid < kC) {
-    const float eg = expf(sm.G[tid]);
-    float* sc = a.scal + ch * kScal;
-    sc[tid] = eg * sm.rqs[tid];                           // output row scale of Q S
-    sc[kC + tid] = sm.rk[tid] * expf(sm.gl - sm.G[tid]);  // state-update scale of v_new row t
-    sc[2 * kC + tid] = eg * sm.rk[tid];                   // row scale of K S inside W S
-    if (tid == 0) sc[3 * kC] = expf(sm.gl);
-  }
+    lds_barrier();
+    if (tid < kC) {
+      const float eg = expf(sm.G[tid]);
+      float* sc = a.scal + ch * kScal;
+      sc[tid] = eg * sm.rqs[tid];                           // output row scale of Q S
+      sc[kC + tid] = sm.rk[tid] * expf(sm.gl - sm.G[tid]);  // state-update scale of v_new row t
+      sc[2 * kC + tid] = eg * sm.rk[tid];                   // row scale of K S inside W S
+      if (tid == 0) sc[3 * kC] = expf(sm.gl);
+    }
 
-  // ---- K K^T -> L (LDS), Q K^T -> A (registers); wave w takes tiles w, w+4, ... ----
-  float areg[4][4];
+    // ---- K K^T -> L (LDS), Q K^T -> A (registers), lower tiles only ----
+    float areg[3][4];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int tau = w + 4 * tt, mt = tau >> 2, nt = tau & 3, m0 = 16 * mt, n0 = 16 * nt;
-    f32x4v kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-    if (nt <= mt) {
+    for (int slot = 0; slot < 3; ++slot) {
+      const int code = prep_tile(w, slot);
+      if (code < 0) continue;
+      const int m0 = 16 * (code >> 4), n0 = 16 * (code & 15);
+      f32x4v kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int k0 = 32 * ks;
@@ -329,53 +358,57 @@ __global__ void __launch_bounds__(kPrepThreads) chunk_prep_kernel(PrepArgs a) {
         kk = mfma(lds8(&sm.kt0.kr[(m0 + r16) * SKR + k0 + kq]), b, kk);
         qk = mfma(lds8(&sm.qx.q[(m0 + r16) * SKR + k0 + kq]), b, qk);
       }
-    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = m0 + rq4 + i, s = n0 + r16;
-      const float dec = s <= t ? expf(sm.G[t] - sm.G[s]) : 0.f;
-      sm.l[t * SF + s] = s < t ? sm.beta[t] * sm.rk[t] * sm.rk[s] * dec * kk[i] : 0.f;
-      areg[tt][i] = s <= t ? sm.rqs[t] * sm.rk[s] * dec * qk[i] : 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const int t = m0 + rq4 + i, s = n0 + r16;
+        const float dec = s <= t ? expf(sm.G[t] - sm.G[s]) : 0.f;
+        sm.l[t * SF + s] = s < t ? sm.beta[t] * sm.rk[t] * sm.rk[s] * dec * kk[i] : 0.f;
+        areg[slot][i] = s <= t ? sm.rqs[t] * sm.rk[s] * dec * qk[i] : 0.f;
+      }
     }
-  }
-  __syncthreads();  // K and Q are dead from here on
+    lds_barrier();  // K and Q are dead from here on
 
-  invert_unit_lower(sm.l, sm.kt0.t, sm.qx.x);  // ends with a barrier
+    invert_unit_lower(sm.l, sm.kt0.t, sm.qx.x);  // ends with a barrier
 
-  // ---- T diag(beta) (hi / lo) straight to the workspace (consecutive threads,
-  // consecutive 8-byte pieces); A through LDS for coalesced stores ----
-  uint16_t* thi_g = a.thi + ch * kC * kC;
-  uint16_t* tlo_g = a.tlo + ch * kC * kC;
+    // ---- T diag(beta) (hi / lo) straight to the workspace (consecutive threads,
+    // consecutive 8-byte pieces); A through LDS for coalesced stores ----
+    uint16_t* thi_g = a.thi + ch * kC * kC;
+    uint16_t* tlo_g = a.tlo + ch * kC * kC;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {  // T rows: 64 x 64, 16 elements per thread
-    const int e = (it * kPrepThreads + tid) * 4;
-    const int t = e >> 6, s4 = e & 63;
-    const float4 tv = *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
-    const float4 bv = *reinterpret_cast<const float4*>(&sm.beta[s4]);
-    const float x[4] = {tv.x * bv.x, tv.y * bv.y, tv.z * bv.z, tv.w * bv.w};
-    uint16_t h[4], lo[4];
+    for (int it = 0; it < 4; ++it) {  // T rows: 64 x 64, 16 elements per thread
+      const int e = (it * kPrepThreads + tid) * 4;
+      const int t = e >> 6, s4 = e & 63;
+      const float4 tv = *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
+      const float4 bv = *reinterpret_cast<const float4*>(&sm.beta[s4]);
+      const float x[4] = {tv.x * bv.x, tv.y * bv.y, tv.z * bv.z, tv.w * bv.w};
+      uint16_t h[4], lo[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      h[j] = f32_to_bf16(x[j]);
-      lo[j] = f32_to_bf16(x[j] - bfv(h[j]));
+      for (int j = 0; j < 4; ++j) {
+        h[j] = f32_to_bf16(x[j]);
+        lo[j] = f32_to_bf16(x[j] - bfv(h[j]));
+      }
+      *reinterpret_cast<uint2*>(thi_g + t * kC + s4) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+      *reinterpret_cast<uint2*>(tlo_g + t * kC + s4) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
     }
-    *reinterpret_cast<uint2*>(thi_g + t * kC + s4) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-    *reinterpret_cast<uint2*>(tlo_g + t * kC + s4) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
-  }
-  uint16_t* a_s = sm.qx.out;
+    uint16_t* a_s = sm.qx.out;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int tau = w + 4 * tt, m0 = 16 * (tau >> 2), n0 = 16 * (tau & 3);
+    for (int slot = 0; slot < 3; ++slot) {
+      const int code = prep_tile(w, slot);
+      if (code < 0) continue;
+      const int m0 = 16 * (code >> 4), n0 = 16 * (code & 15);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a_s[(m0 + rq4 + i) * SK64 + n0 + r16] = f32_to_bf16(areg[tt][i]);
-  }
-  __syncthreads();
-  uint16_t* a_g = a.aqk + ch * kC * kC;
+      for (int i = 0; i < 4; ++i) a_s[(m0 + rq4 + i) * SK64 + n0 + r16] = f32_to_bf16(areg[slot][i]);
+    }
+    lds_barrier();
+    uint16_t* a_g = a.aqk + ch * kC * kC;
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int ci = it * kPrepThreads + tid;  // 512 vectors of 8
-    const int t = ci >> 3, s8 = (ci & 7) * 8;
-    *reinterpret_cast<uint4*>(a_g + t * kC + s8) = *reinterpret_cast<const uint4*>(&a_s[t * SK64 + s8]);
+    for (int it = 0; it < 2; ++it) {
+      const int ci = it * kPrepThreads + tid;  // 512 vectors of 8; the upper tiles are zero
+      const int t = ci >> 3, s8 = (ci & 7) * 8;
+      *reinterpret_cast<uint4*>(a_g + t * kC + s8) =
+          (s8 >> 4) > (t >> 4) ? make_uint4(0, 0, 0, 0) : *reinterpret_cast<const uint4*>(&a_s[t * SK64 + s8]);
+    }
+    lds_barrier();  // the next item restages K and Q over T and the A staging
   }
 }
 
@@ -759,7 +792,8 @@ extern "C" int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, 
   if (nc > 0) {
     PrepArgs p{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), g, beta, table, cstart, thi, tlo, aqk,
                scal, (int)n_seqs, (int)H, (int)HV, scale, use_qk_l2norm ? 1 : 0, g_dtype, beta_dtype};
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3(static_cast<unsigned>(nc), static_cast<unsigned>(HV)),
+    const int64_t items = nc * HV;  // an upper bound: the kernel reads the chunk count
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3(static_cast<unsigned>(items < kPrepGrid ? items : kPrepGrid)),
                        dim3(kPrepThreads), 0, st, p);
     YH_CHECK_LAUNCH("gdn_chunk_prep");
   }
