@@ -154,7 +154,6 @@ struct __align__(16) PrepSmem {
   } kt0;
   union {
     uint16_t q[kC * SKR];   // Q [t][d]          (Q K^T)
-    float x[3 * 256];       // inversion scratch (after the products)
     uint16_t out[kC * SK64];  // A staged for coalesced stores (after the inversion)
   } qx;
   float l[kC * SF];         // L
@@ -162,14 +161,45 @@ struct __align__(16) PrepSmem {
   float gl;
 };
 
+// fp32 MFMA 16x16x4: lane l supplies A[l % 16][k] and B[k][l % 16] for the
+// reduction index k it is given; D is in the 16 x 16 accumulator layout (lane
+// l holds D[4 (l / 16) + e][l % 16], e = 0..3).
+__device__ __forceinline__ f32x4v mfma4(float a, float b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// acc += L_im T_mj (16 x 16 blocks of the fp32 LDS matrices); MFMA s gives
+// lane group g the reduction index 4 s + g.
+__device__ __forceinline__ void acc_lt(f32x4v& acc, const float* l, const float* t, int i, int m, int j, int r, int g) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    acc = mfma4(l[(16 * i + r) * SF + 16 * m + 4 * s + g], t[(16 * m + 4 * s + g) * SF + 16 * j + r], acc);
+}
+// acc += T_ab X for X in the accumulator layout: MFMA s gives lane group g the
+// reduction index 4 g + s, which is element s of the lane's own X.
+__device__ __forceinline__ void acc_tx(f32x4v& acc, const float* t, int a, int b, const f32x4v& x, int r, int g) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mfma4(t[(16 * a + r) * SF + 16 * b + 4 * g + s], x[s], acc);
+}
+__device__ __forceinline__ void put_block(float* t, int i, int j, const f32x4v& v, int r, int g) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) t[(16 * i + 4 * g + e) * SF + 16 * j + r] = -v[e];
+}
+
 // T = (I + L)^{-1} for strictly lower triangular L (64 x 64 fp32 in LDS), by
-// 16 x 16 blocks: the diagonal blocks by column-parallel forward substitution
-// (one lane per column), then the off-diagonal blocks level by level,
-// T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj.
-__device__ void invert_unit_lower(const float* l, float* t, float* x) {
-  const int tid = threadIdx.x;
-  if (tid < 64) {
-    const int b = tid >> 4, j = tid & 15;
+// 16 x 16 blocks (the strictly upper blocks of T are left unwritten):
+//   diagonal blocks T_bb by column-parallel forward substitution (one lane per
+//   column, wave 0);
+//   T_10 = -T_11 L_10 T_00 and T_32 = -T_33 L_32 T_22 (waves 0, 1);
+//   the lower-left 32 x 32 block -B^{-1} C A^{-1} of the 2 x 2 block inverse,
+//   with Y = C A^{-1}:  T_20 = -T_22 Y_00, T_21 = -T_22 Y_01,
+//   T_30 = -(T_32 Y_00 + T_33 Y_10), T_31 = -(T_32 Y_01 + T_33 Y_11)
+//   (one wave each, Y recomputed where needed).
+// The block products run on fp32 MFMA.
+__device__ void invert_unit_lower(const float* l, float* t) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  if (w == 0) {
+    const int b = lane >> 4, j = lane & 15;
     float xs[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -183,55 +213,34 @@ __device__ void invert_unit_lower(const float* l, float* t, float* x) {
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) t[(16 * b + i) * SF + 16 * b + j] = xs[i];
-  } else {
-    for (int e = tid - 64; e < 64 * 64; e += kPrepThreads - 64) {  // strictly upper blocks
-      const int r = e >> 6, c = e & 63;
-      if ((c >> 4) > (r >> 4)) t[r * SF + c] = 0.f;
-    }
   }
   lds_barrier();
-#pragma unroll 1
-  for (int lev = 1; lev < 4; ++lev) {
-    const int nb = 4 - lev;  // blocks (i, i - lev), i = lev..3; 64 threads per block
-    if (tid < nb * 64) {
-      const int bi = tid >> 6, r = (tid >> 2) & 15, c4 = (tid & 3) * 4;
-      const int i = lev + bi, j = i - lev;
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int m = j; m < i; ++m) {
-        float lr[16];
-        ld8f(&l[(16 * i + r) * SF + 16 * m], lr);
-        ld8f(&l[(16 * i + r) * SF + 16 * m + 8], lr + 8);
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const float4 tv = *reinterpret_cast<const float4*>(&t[(16 * m + q) * SF + 16 * j + c4]);
-          acc.x = fmaf(lr[q], tv.x, acc.x);
-          acc.y = fmaf(lr[q], tv.y, acc.y);
-          acc.z = fmaf(lr[q], tv.z, acc.z);
-          acc.w = fmaf(lr[q], tv.w, acc.w);
-        }
-      }
-      *reinterpret_cast<float4*>(&x[bi * 256 + r * 16 + c4]) = acc;
-    }
-    lds_barrier();
-    if (tid < nb * 64) {
-      const int bi = tid >> 6, r = (tid >> 2) & 15, c4 = (tid & 3) * 4;
-      const int i = lev + bi, j = i - lev;
-      float tr[16];
-      ld8f(&t[(16 * i + r) * SF + 16 * i], tr);
-      ld8f(&t[(16 * i + r) * SF + 16 * i + 8], tr + 8);
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const float4 xv = *reinterpret_cast<const float4*>(&x[bi * 256 + q * 16 + c4]);
-        acc.x = fmaf(tr[q], xv.x, acc.x);
-        acc.y = fmaf(tr[q], xv.y, acc.y);
-        acc.z = fmaf(tr[q], xv.z, acc.z);
-        acc.w = fmaf(tr[q], xv.w, acc.w);
-      }
-      *reinterpret_cast<float4*>(&t[(16 * i + r) * SF + 16 * j + c4]) = make_float4(-acc.x, -acc.y, -acc.z, -acc.w);
-    }
-    lds_barrier();
+  if (w < 2) {
+    const int i = w == 0 ? 1 : 3, j = i - 1;  // T_10, T_32
+    f32x4v x = {0.f, 0.f, 0.f, 0.f}, o = {0.f, 0.f, 0.f, 0.f};
+    acc_lt(x, l, t, i, j, j, r, g);
+    acc_tx(o, t, i, i, x, r, g);
+    put_block(t, i, j, o, r, g);
   }
+  lds_barrier();
+  {
+    const int i = 2 + (w >> 1), j = w & 1;  // w: T_20, T_21, T_30, T_31
+    f32x4v y0 = {0.f, 0.f, 0.f, 0.f}, o = {0.f, 0.f, 0.f, 0.f};
+    // Y_0j = L_20 T_0j + L_21 T_1j (T_01 = 0)
+    if (j == 0) acc_lt(y0, l, t, 2, 0, 0, r, g);
+    acc_lt(y0, l, t, 2, 1, j, r, g);
+    if (i == 2) {
+      acc_tx(o, t, 2, 2, y0, r, g);
+    } else {
+      f32x4v y1 = {0.f, 0.f, 0.f, 0.f};  // Y_1j = L_30 T_0j + L_31 T_1j
+      if (j == 0) acc_lt(y1, l, t, 3, 0, 0, r, g);
+      acc_lt(y1, l, t, 3, 1, j, r, g);
+      acc_tx(o, t, 3, 2, y0, r, g);
+      acc_tx(o, t, 3, 3, y1, r, g);
+    }
+    put_block(t, i, j, o, r, g);
+  }
+  lds_barrier();
 }
 
 // Inputs of one (chunk, head) item, held in registers from their load (one
@@ -368,7 +377,7 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
     }
     lds_barrier();  // K and Q are dead from here on
 
-    invert_unit_lower(sm.l, sm.kt0.t, sm.qx.x);  // ends with a barrier
+    invert_unit_lower(sm.l, sm.kt0.t);  // ends with a barrier
 
     // ---- T diag(beta) (hi / lo) straight to the workspace (consecutive threads,
     // consecutive 8-byte pieces); A through LDS for coalesced stores ----
@@ -378,7 +387,8 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
     for (int it = 0; it < 4; ++it) {  // T rows: 64 x 64, 16 elements per thread
       const int e = (it * kPrepThreads + tid) * 4;
       const int t = e >> 6, s4 = e & 63;
-      const float4 tv = *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
+      const float4 tv = (s4 >> 4) > (t >> 4) ? make_float4(0.f, 0.f, 0.f, 0.f)  // strictly upper block
+                                             : *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
       const float4 bv = *reinterpret_cast<const float4*>(&sm.beta[s4]);
       const float x[4] = {tv.x * bv.x, tv.y * bv.y, tv.z * bv.z, tv.w * bv.w};
       uint16_t h[4], lo[4];
