@@ -158,6 +158,7 @@ struct __align__(16) PrepSmem {
   } qx;
   float l[kC * SF];         // L
   float rk[kC], rqs[kC], G[kC], beta[kC];
+  float G2[kC];             // G log2(e), for the decays exp2(G2_t - G2_s)
   float gl;
 };
 
@@ -340,6 +341,7 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
         if (lane >= off) x += y;
       }
       sm.G[lane] = x;
+      sm.G2[lane] = x * 1.4426950408889634f;
       if (lane == kWave - 1) sm.gl = x;
     }
     lds_barrier();
@@ -367,12 +369,21 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
         kk = mfma(lds8(&sm.kt0.kr[(m0 + r16) * SKR + k0 + kq]), b, kk);
         qk = mfma(lds8(&sm.qx.q[(m0 + r16) * SKR + k0 + kq]), b, qk);
       }
+      // rows t = m0 + rq4 + i (four consecutive), column s = n0 + r16
+      const int s = n0 + r16, t0 = m0 + rq4;
+      const float4 g2t = *reinterpret_cast<const float4*>(&sm.G2[t0]);
+      const float4 bt = *reinterpret_cast<const float4*>(&sm.beta[t0]);
+      const float4 rkt = *reinterpret_cast<const float4*>(&sm.rk[t0]);
+      const float4 rqt = *reinterpret_cast<const float4*>(&sm.rqs[t0]);
+      const float g2s = sm.G2[s], rks = sm.rk[s];
+      const float g2v[4] = {g2t.x, g2t.y, g2t.z, g2t.w}, bv[4] = {bt.x, bt.y, bt.z, bt.w};
+      const float rkv[4] = {rkt.x, rkt.y, rkt.z, rkt.w}, rqv[4] = {rqt.x, rqt.y, rqt.z, rqt.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = m0 + rq4 + i, s = n0 + r16;
-        const float dec = s <= t ? expf(sm.G[t] - sm.G[s]) : 0.f;
-        sm.l[t * SF + s] = s < t ? sm.beta[t] * sm.rk[t] * sm.rk[s] * dec * kk[i] : 0.f;
-        areg[slot][i] = s <= t ? sm.rqs[t] * sm.rk[s] * dec * qk[i] : 0.f;
+        const int t = t0 + i;
+        const float dec = s <= t ? exp2f(g2v[i] - g2s) : 0.f;
+        sm.l[t * SF + s] = s < t ? bv[i] * rkv[i] * rks * dec * kk[i] : 0.f;
+        areg[slot][i] = s <= t ? rqv[i] * rks * dec * qk[i] : 0.f;
       }
     }
     lds_barrier();  // K and Q are dead from here on
