@@ -574,10 +574,51 @@ __device__ __forceinline__ bf16x8_t lds8t(const uint16_t* m, int k0, int c0, int
   return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// One chunk's inputs from registers to an LDS buffer (A operands with
+// permuted columns, V row-major, the per-token scalings).
+template <int NW>
+__device__ __forceinline__ void stage_chunk(ScanSmem<NW>& sm, const ChunkRegs<NW>& cur) {
+  using R = ChunkRegs<NW>;
+  constexpr int NT = NW * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < R::kRow; ++it) {
+    const int ci = it * NT + tid, o = (ci >> 4) * SKR, c8 = (ci & 15) * 8;
+    put8p(&sm.q[o], c8, cur.q[it]);
+    put8p(&sm.k[o], c8, cur.k[it]);
+  }
+#pragma unroll
+  for (int it = 0; it < R::kVec; ++it) {
+    const int ci = it * NT + tid;
+    *reinterpret_cast<uint4*>(&sm.v[(ci / (2 * NW)) * SKR + (ci % (2 * NW)) * 8]) = cur.v[it];
+  }
+#pragma unroll
+  for (int it = 0; it < R::kSq; ++it) {
+    const int ci = it * NT + tid;
+    if (ci < kC * kC / 8) {
+      const int o = (ci >> 3) * SK64, c8 = (ci & 7) * 8;
+      put8p(&sm.thi[o], c8, cur.thi[it]);
+      put8p(&sm.tlo[o], c8, cur.tlo[it]);
+      put8p(&sm.aqk[o], c8, cur.aqk[it]);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < R::kSc; ++it) {
+    const int ci = it * NT + tid;
+    if (ci < kC) sm.orow[ci] = cur.scal[it];
+    else if (ci < 2 * kC) sm.d2[ci - kC] = cur.scal[it];
+    else if (ci < 3 * kC) sm.ek[ci - 2 * kC] = cur.scal[it];
+    else if (ci == 3 * kC) sm.egl = cur.scal[it];
+  }
+}
+
+// Two LDS buffers: chunk c computes from one while chunk c + 1 (loaded into
+// registers during chunk c - 1) is staged into the other, so one barrier per
+// chunk separates them.
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
   using R = ChunkRegs<NW>;
-  __shared__ ScanSmem<NW> sm;
+  __shared__ ScanSmem<NW> smb[2];
   constexpr int V = 16 * NW;
   constexpr int NT = NW * 64;
   const int hv = blockIdx.x % a.HV;
@@ -600,43 +641,17 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
     for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + 16 * dt + rq4 + i) * V + vcol] : 0.f;
 
   R cur;
-  if (cs < ce) load_chunk<NW>(cur, a, cs, seq0, min(kC, seqlen), hv, hk);
+  if (cs < ce) {
+    load_chunk<NW>(cur, a, cs, seq0, min(kC, seqlen), hv, hk);
+    stage_chunk<NW>(smb[0], cur);
+    if (cs + 1 < ce) load_chunk<NW>(cur, a, cs + 1, seq0 + kC, min(kC, seqlen - kC), hv, hk);
+    lds_barrier();
+  }
   for (int c = cs; c < ce; ++c) {
     const int j = c - cs;
     const int64_t tok0 = seq0 + static_cast<int64_t>(j) * kC;
     const int Lc = min(kC, seqlen - j * kC);
-    // ---- this chunk's inputs -> LDS, then prefetch the next chunk ----
-#pragma unroll
-    for (int it = 0; it < R::kRow; ++it) {
-      const int ci = it * NT + tid, o = (ci >> 4) * SKR, c8 = (ci & 15) * 8;
-      put8p(&sm.q[o], c8, cur.q[it]);
-      put8p(&sm.k[o], c8, cur.k[it]);
-    }
-#pragma unroll
-    for (int it = 0; it < R::kVec; ++it) {
-      const int ci = it * NT + tid;
-      *reinterpret_cast<uint4*>(&sm.v[(ci / (2 * NW)) * SKR + (ci % (2 * NW)) * 8]) = cur.v[it];
-    }
-#pragma unroll
-    for (int it = 0; it < R::kSq; ++it) {
-      const int ci = it * NT + tid;
-      if (ci < kC * kC / 8) {
-        const int o = (ci >> 3) * SK64, c8 = (ci & 7) * 8;
-        put8p(&sm.thi[o], c8, cur.thi[it]);
-        put8p(&sm.tlo[o], c8, cur.tlo[it]);
-        put8p(&sm.aqk[o], c8, cur.aqk[it]);
-      }
-    }
-#pragma unroll
-    for (int it = 0; it < R::kSc; ++it) {
-      const int ci = it * NT + tid;
-      if (ci < kC) sm.orow[ci] = cur.scal[it];
-      else if (ci < 2 * kC) sm.d2[ci - kC] = cur.scal[it];
-      else if (ci < 3 * kC) sm.ek[ci - 2 * kC] = cur.scal[it];
-      else if (ci == 3 * kC) sm.egl = cur.scal[it];
-    }
-    lds_barrier();
-
+    ScanSmem<NW>& sm = smb[j & 1];
     // ---- Q S (1 pass) and P = K S (2 passes), four row tiles of this column block ----
     f32x4v qs[4], ps[4];
 #pragma unroll
@@ -655,9 +670,12 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
         ps[mt] = mfma(ak, bl, ps[mt]);
       }
     }
-    // Prefetch the next chunk while the products above drain: the 8 waves
-    // reach this point at different times, so their loads queue less.
-    if (c + 1 < ce) load_chunk<NW>(cur, a, c + 1, tok0 + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
+    // Stage chunk c + 1 into the other buffer and prefetch chunk c + 2 while
+    // the products above drain.
+    if (c + 1 < ce) {
+      stage_chunk<NW>(smb[(j & 1) ^ 1], cur);
+      if (c + 2 < ce) load_chunk<NW>(cur, a, c + 2, tok0 + 2 * kC, min(kC, seqlen - (j + 2) * kC), hv, hk);
+    }
     // ---- v_new = T diag(beta) V - T diag(beta) (diag(e^G rk) P): 2 + 3 passes, T lower triangular ----
     bf16x8_t vb[2], ph[2], pl[2];
 #pragma unroll
@@ -743,7 +761,7 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       }
       S[dt] = s;
     }
-    lds_barrier();  // the next chunk restages every LDS buffer
+    lds_barrier();  // chunk c + 1's buffer is complete; chunk c's may be restaged
   }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
