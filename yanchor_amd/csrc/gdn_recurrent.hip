@@ -158,6 +158,10 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
   // tokens of row b: [t0, t0 + Tb) of the token axis
   const int64_t t0 = a.cu ? static_cast<int64_t>(a.cu[b]) : static_cast<int64_t>(b) * a.T;
   const int Tb = a.cu ? a.cu[b + 1] - a.cu[b] : a.T;
+  // The token inputs do not depend on the state row: their loads go out
+  // before the slot index is waited for.
+  TokIn<DT, KPL> in;
+  if (Tb > 0) load_tok<DT, K, KPL>(in, a, t0, hk, hv, col0, norm_wave, lane);
   int64_t srow = a.idx ? static_cast<int64_t>(a.idx[b]) : static_cast<int64_t>(b);
   if (srow < 0 || srow >= a.n_rows) {
     if (rg == 0) {
@@ -168,9 +172,6 @@ __global__ void __launch_bounds__(NT) gdn_recurrent_kernel(GdnArgs a) {
     }
     return;
   }
-
-  TokIn<DT, KPL> in;
-  if (Tb > 0) load_tok<DT, K, KPL>(in, a, t0, hk, hv, col0, norm_wave, lane);
 
   float* S = a.state + (srow * a.HV + hv) * static_cast<int64_t>(K) * a.V + col0;
   float4 s[RPT];
