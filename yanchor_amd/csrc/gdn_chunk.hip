@@ -307,19 +307,20 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
     if (item + static_cast<int>(gridDim.x) < n_items) prep_load(cur, a, item + gridDim.x);
     lds_barrier();
 
-    // ---- norms (4 lanes per token) and the decay scan ----
-    {
+    // ---- norms (4 lanes per token) and the decay scan, in the same phase as
+    // the products below ----
+    {  // norms: 4 lanes per token
       const int t = tid >> 2, p = tid & 3;
       float sk = 0.f, sq = 0.f;
 #pragma unroll
       for (int e = 0; e < 32; e += 8) {
         const uint4 kv = *reinterpret_cast<const uint4*>(&sm.kt0.kr[t * SKR + 32 * p + e]);
         const uint4 qv = *reinterpret_cast<const uint4*>(&sm.qx.q[t * SKR + 32 * p + e]);
-        const uint32_t kk[4] = {kv.x, kv.y, kv.z, kv.w}, qq[4] = {qv.x, qv.y, qv.z, qv.w};
+        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float k0 = __uint_as_float(kk[j] << 16), k1 = __uint_as_float(kk[j] & 0xffff0000u);
-          const float q0 = __uint_as_float(qq[j] << 16), q1 = __uint_as_float(qq[j] & 0xffff0000u);
+          const float k0 = __uint_as_float(kw[j] << 16), k1 = __uint_as_float(kw[j] & 0xffff0000u);
+          const float q0 = __uint_as_float(qw[j] << 16), q1 = __uint_as_float(qw[j] & 0xffff0000u);
           sk = fmaf(k0, k0, fmaf(k1, k1, sk));
           sq = fmaf(q0, q0, fmaf(q1, q1, sq));
         }
@@ -344,6 +345,22 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
       sm.G2[lane] = x * 1.4426950408889634f;
       if (lane == kWave - 1) sm.gl = x;
     }
+    // ---- K K^T and Q K^T on MFMA (lower tiles only); scaled after the barrier ----
+    f32x4v kk[3], qk[3];
+#pragma unroll
+    for (int slot = 0; slot < 3; ++slot) {
+      kk[slot] = qk[slot] = f32x4v{0.f, 0.f, 0.f, 0.f};
+      const int code = prep_tile(w, slot);
+      if (code < 0) continue;
+      const int m0 = 16 * (code >> 4), n0 = 16 * (code & 15);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int k0 = 32 * ks;
+        const bf16x8_t b = lds8(&sm.kt0.kr[(n0 + r16) * SKR + k0 + kq]);
+        kk[slot] = mfma(lds8(&sm.kt0.kr[(m0 + r16) * SKR + k0 + kq]), b, kk[slot]);
+        qk[slot] = mfma(lds8(&sm.qx.q[(m0 + r16) * SKR + k0 + kq]), b, qk[slot]);
+      }
+    }
     lds_barrier();
     if (tid < kC) {
       const float eg = expf(sm.G[tid]);
@@ -354,21 +371,13 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
       if (tid == 0) sc[3 * kC] = expf(sm.gl);
     }
 
-    // ---- K K^T -> L (LDS), Q K^T -> A (registers), lower tiles only ----
+    // ---- scale: L (strictly lower, to LDS) and A (registers) ----
     float areg[3][4];
 #pragma unroll
     for (int slot = 0; slot < 3; ++slot) {
       const int code = prep_tile(w, slot);
       if (code < 0) continue;
       const int m0 = 16 * (code >> 4), n0 = 16 * (code & 15);
-      f32x4v kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int k0 = 32 * ks;
-        const bf16x8_t b = lds8(&sm.kt0.kr[(n0 + r16) * SKR + k0 + kq]);
-        kk = mfma(lds8(&sm.kt0.kr[(m0 + r16) * SKR + k0 + kq]), b, kk);
-        qk = mfma(lds8(&sm.qx.q[(m0 + r16) * SKR + k0 + kq]), b, qk);
-      }
       // rows t = m0 + rq4 + i (four consecutive), column s = n0 + r16
       const int s = n0 + r16, t0 = m0 + rq4;
       const float4 g2t = *reinterpret_cast<const float4*>(&sm.G2[t0]);
@@ -382,8 +391,8 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
       for (int i = 0; i < 4; ++i) {
         const int t = t0 + i;
         const float dec = s <= t ? exp2f(g2v[i] - g2s) : 0.f;
-        sm.l[t * SF + s] = s < t ? bv[i] * rkv[i] * rks * dec * kk[i] : 0.f;
-        areg[slot][i] = s <= t ? rqv[i] * rks * dec * qk[i] : 0.f;
+        sm.l[t * SF + s] = s < t ? bv[i] * rkv[i] * rks * dec * kk[slot][i] : 0.f;
+        areg[slot][i] = s <= t ? rqv[i] * rks * dec * qk[slot][i] : 0.f;
       }
     }
     lds_barrier();  // K and Q are dead from here on
