@@ -717,6 +717,31 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       }
       vn[mt] = u - y;
     }
+    // ---- S <- e^{G_last} S + K^T diag(d2) v_new (2 passes); issued before the
+    // output, which the next chunk does not wait for ----
+    bf16x8_t zh[2], zl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      f32x4v z0 = vn[2 * ks], z1 = vn[2 * ks + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        z0[i] *= sm.d2[32 * ks + rq4 + i];
+        z1[i] *= sm.d2[32 * ks + 16 + rq4 + i];
+      }
+      pack_b(z0, z1, zh[ks], zl[ks]);
+    }
+    const float egl = sm.egl;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      f32x4v s = S[dt] * egl;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8_t ak = lds8t<true>(sm.k, 32 * ks, 16 * dt, lane);
+        s = mfma(ak, zh[ks], s);
+        s = mfma(ak, zl[ks], s);
+      }
+      S[dt] = s;
+    }
     // ---- o = diag(orow) Q S + A v_new (A lower triangular, 1 pass) ----
     bf16x8_t vnb[2];
 #pragma unroll
@@ -741,34 +766,16 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       const float2 p0 = odd ? make_float2(y0, acc[2]) : make_float2(acc[0], y0);
       const float2 p1 = odd ? make_float2(y1, acc[3]) : make_float2(acc[1], y1);
       const int t0 = 16 * mt + rq4 + (odd ? 2 : 0), c0 = vcol & ~1;
-      if (t0 < Lc)
-        *reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0) * a.HV + hv) * V + c0) = pack2(f32_to_bf16(p0.x), f32_to_bf16(p0.y));
-      if (t0 + 1 < Lc)
-        *reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0 + 1) * a.HV + hv) * V + c0) = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
-    }
-    // ---- S <- e^{G_last} S + K^T diag(d2) v_new (2 passes) ----
-    bf16x8_t zh[2], zl[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      f32x4v z0 = vn[2 * ks], z1 = vn[2 * ks + 1];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        z0[i] *= sm.d2[32 * ks + rq4 + i];
-        z1[i] *= sm.d2[32 * ks + 16 + rq4 + i];
+      uint32_t* o0 = reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0) * a.HV + hv) * V + c0);
+      uint32_t* o1 = reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0 + 1) * a.HV + hv) * V + c0);
+      const uint32_t w0 = pack2(f32_to_bf16(p0.x), f32_to_bf16(p0.y)), w1 = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
+      if (Lc == kC) {  // uniform: every chunk but a sequence's last
+        *o0 = w0;
+        *o1 = w1;
+      } else {
+        if (t0 < Lc) *o0 = w0;
+        if (t0 + 1 < Lc) *o1 = w1;
       }
-      pack_b(z0, z1, zh[ks], zl[ks]);
-    }
-    const float egl = sm.egl;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      f32x4v s = S[dt] * egl;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8_t ak = lds8t<true>(sm.k, 32 * ks, 16 * dt, lane);
-        s = mfma(ak, zh[ks], s);
-        s = mfma(ak, zl[ks], s);
-      }
-      S[dt] = s;
     }
     lds_barrier();  // chunk c + 1's buffer is complete; chunk c's may be restaged
   }
