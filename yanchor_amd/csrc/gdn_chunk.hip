@@ -12,11 +12,12 @@
 //
 // T and A = Q K^T o Gamma do not depend on the state S, so the work is split
 // in two kernels:
-//   chunk_prep_kernel   one workgroup per (chunk, value head), all chunks of
-//                       all sequences at once: norms, decays, K K^T and Q K^T
-//                       on MFMA, the fp32 inverse T.  Writes T diag(beta)
-//                       (bf16 hi + lo), A (bf16, with the q / k scalings) and
-//                       the per-token scalings to a workspace -- 25 KiB per
+//   chunk_prep_kernel   a persistent grid over the (chunk, value head) items
+//                       of all sequences: norms, decays, K K^T and Q K^T on
+//                       MFMA, the fp32 inverse T (block products on MFMA).
+//                       Writes the lower 16 x 16 blocks of T diag(beta) (bf16
+//                       hi + lo) and A (bf16, with the q / k scalings), and the
+//                       per-token scalings, to a workspace -- 15.8 KiB per
 //                       chunk and head.
 //   chunk_scan_kernel   one workgroup per (sequence, value head), walking the
 //                       sequence's chunks with the 128 x V fp32 state in MFMA
@@ -47,6 +48,13 @@ constexpr int SKR = 136;      // bf16 row stride of 128-wide matrices (padded: c
 constexpr int SK64 = 72;      // bf16 row stride of 64-wide matrices
 constexpr int SF = 68;        // fp32 row stride of 64-wide matrices
 constexpr int kScal = 196;    // per (chunk, head) scalars: orow[64], d2[64], ek[64], e^{G_last}, pad
+// T diag(beta) and A are lower triangular by 16 x 16 blocks: the workspace
+// holds only the 10 lower blocks (bi, bj), bj <= bi, block lblock(bi, bj),
+// each 16 x 16 row-major.
+constexpr int kLB = 10;
+constexpr int kLBElems = kLB * 256;
+__device__ __forceinline__ int lblock(int bi, int bj) { return bi * (bi + 1) / 2 + bj; }
+__device__ __forceinline__ int lblock_row(int q) { return (q >= 1) + (q >= 3) + (q >= 6); }
 
 __device__ __forceinline__ bf16x8_t lds8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
@@ -135,9 +143,9 @@ struct PrepArgs {
   const void* beta;
   const int32_t* table;
   const int32_t* cstart;
-  uint16_t* thi;         // [nc, HV, C, C]  T diag(beta), bf16 hi
-  uint16_t* tlo;         //                 bf16 lo
-  uint16_t* aqk;         // [nc, HV, C, C]  A
+  uint16_t* thi;         // [nc, HV, kLBElems]  T diag(beta) (lower blocks), bf16 hi
+  uint16_t* tlo;         //                     bf16 lo
+  uint16_t* aqk;         // [nc, HV, kLBElems]  A (lower blocks)
   float* scal;           // [nc, HV, kScal]
   int n_seqs, H, HV;
   float scale;
@@ -399,16 +407,17 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
 
     invert_unit_lower(sm.l, sm.kt0.t);  // ends with a barrier
 
-    // ---- T diag(beta) (hi / lo) straight to the workspace (consecutive threads,
-    // consecutive 8-byte pieces); A through LDS for coalesced stores ----
-    uint16_t* thi_g = a.thi + ch * kC * kC;
-    uint16_t* tlo_g = a.tlo + ch * kC * kC;
+    // ---- T diag(beta) (hi / lo) straight to the workspace's lower blocks
+    // (8-byte pieces); A through LDS for 16-byte stores ----
+    uint16_t* thi_g = a.thi + ch * kLBElems;
+    uint16_t* tlo_g = a.tlo + ch * kLBElems;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {  // T rows: 64 x 64, 16 elements per thread
       const int e = (it * kPrepThreads + tid) * 4;
       const int t = e >> 6, s4 = e & 63;
-      const float4 tv = (s4 >> 4) > (t >> 4) ? make_float4(0.f, 0.f, 0.f, 0.f)  // strictly upper block
-                                             : *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
+      if ((s4 >> 4) > (t >> 4)) continue;  // strictly upper block: not stored
+      const int off = lblock(t >> 4, s4 >> 4) * 256 + (t & 15) * 16 + (s4 & 15);
+      const float4 tv = *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
       const float4 bv = *reinterpret_cast<const float4*>(&sm.beta[s4]);
       const float x[4] = {tv.x * bv.x, tv.y * bv.y, tv.z * bv.z, tv.w * bv.w};
       uint16_t h[4], lo[4];
@@ -417,8 +426,8 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
         h[j] = f32_to_bf16(x[j]);
         lo[j] = f32_to_bf16(x[j] - bfv(h[j]));
       }
-      *reinterpret_cast<uint2*>(thi_g + t * kC + s4) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-      *reinterpret_cast<uint2*>(tlo_g + t * kC + s4) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
+      *reinterpret_cast<uint2*>(thi_g + off) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+      *reinterpret_cast<uint2*>(tlo_g + off) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
     }
     uint16_t* a_s = sm.qx.out;
 #pragma unroll
@@ -430,13 +439,14 @@ __global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a)
       for (int i = 0; i < 4; ++i) a_s[(m0 + rq4 + i) * SK64 + n0 + r16] = f32_to_bf16(areg[slot][i]);
     }
     lds_barrier();
-    uint16_t* a_g = a.aqk + ch * kC * kC;
+    uint16_t* a_g = a.aqk + ch * kLBElems;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-      const int ci = it * kPrepThreads + tid;  // 512 vectors of 8; the upper tiles are zero
+      const int ci = it * kPrepThreads + tid;  // 512 vectors of 8, the lower blocks' stored
       const int t = ci >> 3, s8 = (ci & 7) * 8;
-      *reinterpret_cast<uint4*>(a_g + t * kC + s8) =
-          (s8 >> 4) > (t >> 4) ? make_uint4(0, 0, 0, 0) : *reinterpret_cast<const uint4*>(&a_s[t * SK64 + s8]);
+      if ((s8 >> 4) <= (t >> 4))
+        *reinterpret_cast<uint4*>(a_g + lblock(t >> 4, s8 >> 4) * 256 + (t & 15) * 16 + (s8 & 15)) =
+            *reinterpret_cast<const uint4*>(&a_s[t * SK64 + s8]);
     }
     lds_barrier();  // the next item restages K and Q over T and the A staging
   }
@@ -489,7 +499,7 @@ struct ChunkRegs {
   static constexpr int NT = NW * 64;
   static constexpr int kRow = kC * kK / 8 / NT;        // 16-byte vectors per thread of a 64 x 128 matrix
   static constexpr int kVec = kC * 16 * NW / 8 / NT;   // ... of the 64 x V value rows (= 2)
-  static constexpr int kSq = (kC * kC / 8 + NT - 1) / NT;  // ... of a 64 x 64 matrix
+  static constexpr int kSq = (kLB * 32 + NT - 1) / NT;  // ... of the lower blocks of a 64 x 64 matrix
   static constexpr int kSc = (3 * kC + 1 + NT - 1) / NT;
   uint4 q[kRow], k[kRow], v[kVec];
   uint4 thi[kSq], tlo[kSq], aqk[kSq];
@@ -523,8 +533,8 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NW>& r, const ScanArgs& a, 
 #pragma unroll
   for (int it = 0; it < R::kSq; ++it) {
     const int ci = it * NT + tid;
-    const bool in = ci < kC * kC / 8;
-    const int64_t off = ch * kC * kC + (ci >> 3) * kC + (ci & 7) * 8;
+    const bool in = ci < kLB * 32;
+    const int64_t off = ch * kLBElems + ci * 8;
     r.thi[it] = in ? *reinterpret_cast<const uint4*>(a.thi + off) : make_uint4(0, 0, 0, 0);
     r.tlo[it] = in ? *reinterpret_cast<const uint4*>(a.tlo + off) : make_uint4(0, 0, 0, 0);
     r.aqk[it] = in ? *reinterpret_cast<const uint4*>(a.aqk + off) : make_uint4(0, 0, 0, 0);
@@ -604,8 +614,9 @@ __device__ __forceinline__ void stage_chunk(ScanSmem<NW>& sm, const ChunkRegs<NW
 #pragma unroll
   for (int it = 0; it < R::kSq; ++it) {
     const int ci = it * NT + tid;
-    if (ci < kC * kC / 8) {
-      const int o = (ci >> 3) * SK64, c8 = (ci & 7) * 8;
+    if (ci < kLB * 32) {  // vector ci: block q = ci / 32, row (ci % 32) / 2, half ci % 2
+      const int q = ci >> 5, bi = lblock_row(q), bj = q - bi * (bi + 1) / 2;
+      const int o = (16 * bi + ((ci & 31) >> 1)) * SK64, c8 = 16 * bj + 8 * (ci & 1);
       put8p(&sm.thi[o], c8, cur.thi[it]);
       put8p(&sm.tlo[o], c8, cur.tlo[it]);
       put8p(&sm.aqk[o], c8, cur.aqk[it]);
@@ -649,6 +660,16 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + 16 * dt + rq4 + i) * V + vcol] : 0.f;
 
+  // The upper blocks of T diag(beta) and A are zero and never staged: clear
+  // them once in both buffers (disjoint from every staged element).
+  for (int e = tid; e < 2 * 6 * 32; e += NT) {
+    const int buf = e / 192, u = (e % 192) >> 5, v = e & 31;  // upper block u: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+    const int bi = u < 3 ? 0 : (u < 5 ? 1 : 2), bj = u < 3 ? u + 1 : (u < 5 ? u - 1 : 3);
+    const int o = (16 * bi + (v >> 1)) * SK64, c8 = 16 * bj + 8 * (v & 1);
+    put8p(&smb[buf].thi[o], c8, make_uint4(0, 0, 0, 0));
+    put8p(&smb[buf].tlo[o], c8, make_uint4(0, 0, 0, 0));
+    put8p(&smb[buf].aqk[o], c8, make_uint4(0, 0, 0, 0));
+  }
   R cur;
   if (cs < ce) {
     load_chunk<NW>(cur, a, cs, seq0, min(kC, seqlen), hv, hk);
@@ -797,9 +818,9 @@ WsLayout ws_layout(int64_t total, int64_t n_seqs, int64_t HV) {
   l.table = 0;
   l.cstart = up(nc * 16);
   l.thi = up(l.cstart + (n_seqs + 1) * 4);
-  l.tlo = l.thi + up(nc * HV * kC * kC * 2);
-  l.aqk = l.tlo + up(nc * HV * kC * kC * 2);
-  l.scal = l.aqk + up(nc * HV * kC * kC * 2);
+  l.tlo = l.thi + up(nc * HV * kLBElems * 2);
+  l.aqk = l.tlo + up(nc * HV * kLBElems * 2);
+  l.scal = l.aqk + up(nc * HV * kLBElems * 2);
   l.bytes = l.scal + up(nc * HV * kScal * 4);
   return l;
 }
