@@ -62,6 +62,9 @@ METRIC = "decode tokens/s at B=128 on 1 GPU; state-update HBM GB/s as % of peak"
 TRAFFIC_GDN_DECODE = {128: (133803.7 * 2.0 + 263283.8) * 1024}
 # The same for gdn_decode_fused_kernel (``--workload gdn_decode_fused``), by batch rows.
 TRAFFIC_GDN_FUSED = {128: (137924.0 * 2.0 + 272580.8) * 1024}
+# The same for one call of the chunked prefill (``--workload gdn_prefill``):
+# chunk_prep_kernel + chunk_scan_kernel, FETCH and WRITE KiB per dispatch summed.
+TRAFFIC_PREFILL = ((1544449.8 + 2551212.8) * 2.0 + (1268339.0 + 1341755.4)) * 1024
 
 
 def gdn_state_bytes(b, h, hv, kd, vd, qkv_size, gate_size, with_indices):
@@ -486,7 +489,8 @@ def bench_gdn_prefill(steps, warmup, cpu, batch=None):
                                   f"({tokens} tokens), H=HV=32, dk=dv=128, chunk 64, bf16 q/k/v/o, fp32 gates/state",
                       "global_batch": len(lengths), "seq_len": tokens, "parallelism": "single GPU"},
            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "gdn_chunk_kernel",
+                        "frac": gbs / HBM_PEAK_GBS, "traffic": TRAFFIC_PREFILL,
+                        "kernel": "chunk_prep_kernel + chunk_scan_kernel",
                         "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3,
                         "mfma_tflops": tflops, "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
                         "mfma_util": tflops / MFMA_BF16_PEAK_TFLOPS, "flops_per_launch": flops,
