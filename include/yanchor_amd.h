@@ -123,7 +123,7 @@ int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* conv_state,
  *   first balances the grid); every sequence must appear once.
  *   workspace  device scratch of yh_gdn_chunk_workspace_bytes(total_tokens,
  *   n_seqs, HV, V) bytes, 16-byte aligned: the per-chunk quantities the
- *   state-independent pass hands to the sequential pass (about 25 KiB per
+ *   state-independent pass hands to the sequential pass (about 16 KiB per
  *   chunk of 64 tokens and value head).  Calls sharing it must not overlap.
  */
 int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, const void* g, const void* beta,
