@@ -49,6 +49,19 @@ def test_packed_zero_state_and_value_tiles(gpu):
     assert rel_err(o, ro) <= 2e-2 and rel_err(st, rs) <= 1e-3
 
 
+def test_packed_value_tiles_many_chunks(gpu):
+    """V = 64 (four-wave scan) over sequences of 1 to 5 chunks with GQA: the
+    scan's two LDS buffers alternate several times per sequence."""
+    x = workloads.packed_inputs([300, 129, 1, 64, 192], 2, 4, 128, 64, seed=11, h0_std=0.05)
+    d = x.to(gpu)
+    o, st = gdn.chunk_gated_delta_rule(d.q, d.k, d.v, g=d.g, beta=d.beta, initial_state=d.h0,
+                                       output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                       cu_seqlens=d.cu_seqlens, lengths=x.lengths)
+    ro, rs = _oracle(x)
+    assert rel_err(o, ro) <= 2e-2, rel_err(o, ro)
+    assert rel_err(st, rs) <= 1e-3, rel_err(st, rs)
+
+
 def test_batched_form(gpu):
     x = workloads.gdn_inputs(2, 70, 2, 2, 128, 128, dtype=torch.bfloat16, seed=8, state_std=0.02)
     d = x.to(gpu)
