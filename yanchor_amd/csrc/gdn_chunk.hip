@@ -23,10 +23,11 @@
 //                       sequence's chunks with the 128 x V fp32 state in MFMA
 //                       accumulators (wave w owns value columns 16w..16w+15):
 //                       Q S and W S, v_new, o, and the state update, with S
-//                       and v_new never leaving registers -- two barriers per
-//                       chunk, and the next chunk's inputs (which do not
-//                       depend on S) loaded into registers while the current
-//                       chunk computes.
+//                       and v_new never leaving registers.  The chunk inputs
+//                       (which do not depend on S) are double-buffered in LDS:
+//                       chunk c + 1 is staged while chunk c computes, from
+//                       registers loaded during chunk c - 1; one barrier per
+//                       chunk.
 // Per-token L2 norms, beta and decays are diagonal factors, so products with
 // the raw q / k / v tensors take exact bf16 MFMA operands and the factors go
 // into the epilogues or the fp32 operand.  Products whose operands are fp32 on
