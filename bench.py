@@ -528,6 +528,40 @@ def cpu_gdn_prefill(lengths, h, hv, d, budget_s=15.0):
                       f"the float32 torch oracle's chunked form, {el:.1f} s"}
 
 
+def bench_anchor_read(steps, warmup, cpu, batch=64):
+    """Anchor-memory read of one decode token (committed_gqa) at the decode
+    config: 64 rows, 32 heads with a memory per head, 256 slots of 128 bf16
+    dims, each slot live with p = 0.7; three rotating states (806 MB) so the
+    slots stream from HBM."""
+    from yanchor_amd import independent_memory as im, workloads
+
+    del cpu
+    g, cap, d, n_states = 32, 256, 128, 3
+    states = [workloads.anchor_state(batch, g, cap, 64, d, seed=workloads.SEED0 + 1 + 7 * i)
+              for i in range(n_states)]
+    for st in states:
+        st.to_("cuda:0")
+    q = workloads.anchor_query(batch, g, d).to("cuda:0")
+
+    def step(i):
+        im.committed_gqa(q, states[i % n_states])
+
+    ms_per_step, kernel_ms = _time_launches(step, steps, warmup)
+    # every slot's key and value row is read (dead slots are masked, not skipped),
+    # plus positions, the query and the output
+    nbytes = 2 * batch * g * cap * d * 2 + batch * g * cap * 4 + 2 * batch * g * d * 2
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    del states
+    return {"metric": "anchor-memory read per decode token (HBM GB/s)", "value": achieved, "unit": "GB/s",
+            "ms_per_step": ms_per_step, "dtype": "bf16",
+            "config": {"workload": f"anchor_read: committed_gqa, {batch} rows x {g} heads x {cap} slots x {d} "
+                                   "bf16, p_live 0.7, 3 rotating states", "global_batch": batch, "seq_len": 1,
+                       "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "anchor_read_kernel",
+                         "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3}}
+
+
 def bench_hbm_copy(steps, warmup, cpu, batch=None):
     """A plain 128 MiB device-to-device copy (torch's copy kernel): the
     calibration kernel for the HBM byte counters, and the bandwidth a simple
@@ -554,7 +588,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (model_decode 64, gdn_decode 20)")
     ap.add_argument("--workload", default="model_decode",
                     choices=["model_decode", "long_horizon", "gdn_decode", "gdn_decode_fused", "gdn_prefill",
-                             "hbm_copy"])
+                             "anchor_read", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=None, help="slots (model_decode 128) / rows (gdn_decode 64)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -571,7 +605,7 @@ def main() -> int:
     else:
         steps, warmup = args.steps or 200, 20 if args.warmup is None else args.warmup
         fn = {"gdn_decode": bench_gdn_decode, "gdn_decode_fused": bench_gdn_decode_fused,
-              "gdn_prefill": bench_gdn_prefill, "hbm_copy": bench_hbm_copy}
+              "gdn_prefill": bench_gdn_prefill, "anchor_read": bench_anchor_read, "hbm_copy": bench_hbm_copy}
         res = fn[args.workload](steps, warmup, not args.no_cpu,
                                 batch=args.batch or (128 if args.workload == "gdn_decode_fused" else 64))
     line = {"metric": res.get("metric", METRIC), "value": res["value"], "unit": res["unit"], "n_gpus": 1,
