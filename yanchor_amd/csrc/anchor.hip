@@ -181,14 +181,15 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 // value 0:
 //   out = sum_w acc_w e^{m_w - M} / (e^{-M} + sum_w l_w e^{m_w - M}),
 //   M = max(0, max_w m_w).
-// 4 waves per workgroup, two workgroups per CU (register budget of two waves
-// per SIMD).
-template <bool SINK> constexpr int read_waves() { return 4; }
+// 4 waves per workgroup (2 for one head per memory, whose 256-slot pass is
+// short: each wave then keeps its pipeline over twice the blocks), register
+// budget of two waves per SIMD.
+template <bool SINK, int R = 4> constexpr int read_waves() { return R == 1 ? 2 : 4; }
 
 template <int DT, int D, int R, bool SINK, int BS>
-__global__ void __launch_bounds__(read_waves<SINK>() * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__((read_waves<SINK, R>() * 64)) __attribute__((amdgpu_waves_per_eu(2, 2)))
 anchor_read_kernel(ReadArgs a) {
-  constexpr int kReadWaves = read_waves<SINK>();
+  constexpr int kReadWaves = read_waves<SINK, R>();
   constexpr int kReadThreads = kReadWaves * 64;
   constexpr int LPR = D / 8;
   constexpr int RPI = kWave / LPR;
@@ -541,7 +542,7 @@ template <int DT, int D, bool SINK, int BS>
 int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(read_waves<SINK>() * 64);
   switch (R) {
-    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, BS>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, BS>), grid, dim3(read_waves<SINK, 1>() * 64), 0, st, a); break;
     case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, BS>), grid, block, 0, st, a); break;
     case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, BS>), grid, block, 0, st, a); break;
     default: set_error("anchor_read: heads per group must be 1, 2 or 4 (got %d)", R); return YH_ERR_INVALID;
