@@ -8,13 +8,17 @@ Prints one JSON line.  Workloads:
   4B-shaped hybrid model (36 layers: 27 Gated DeltaNet + 9 sliding-window /
   anchor-memory layers, hidden 2560, 32 heads, dk = dv = 128, 256 anchor slots,
   vocab 151936, bf16 weights ~ N(0, 0.02)) over a physical batch of 128 slots.
-  Requests arrive as a Poisson process (mean 4 per step) with random 128-token
-  prompts and geometric generation lengths (mean 1024); finished slots are
-  refilled at poll points every 32 steps; sampling is top-k 20 / top-p 0.95 /
+  One request per slot is queued before the first step and prefilled into the
+  batch (the reference's initial fill); then requests arrive as a Poisson
+  process (mean 4 per step) with random 128-token prompts and geometric
+  generation lengths (mean 1024); finished slots are refilled at poll points
+  every 32 steps and once more before the timed window, so it starts with
+  every slot live; sampling is top-k 20 / top-p 0.95 /
   T = 0.6 with presence penalty 1.5.  One step = one captured HIP graph of the
   whole model forward + sampling + slot bookkeeping for all 128 slots.
   value = useful decode tokens / (timed wall - refill prefill time), the
-  reference's decode tokens/s definition.
+  reference's decode tokens/s definition; ``decode.live_slots`` gives the
+  live slots per timed step (min / mean / first / last).
 * ``long_horizon``: B=256 fixed sequences generating 32768 tokens from
   256-token prompts, 16-slot anchor memory committed every 64 tokens;
   sustained tokens/s over a bounded window of steps and peak HBM use.
@@ -108,12 +112,39 @@ def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_threads() -> int:
+def _affinity() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU legs: the CPUs this process may run on,
+    limited by ``OMP_NUM_THREADS`` when the environment declares the job's CPU
+    share that way (a one-GPU job's share of a shared host)."""
+    n = _affinity()
+    declared = os.environ.get("OMP_NUM_THREADS", "")
+    if declared.isdigit() and int(declared) > 0:
+        n = min(n, int(declared))
+    return max(1, n)
+
+
+def cpu_host_info() -> dict:
+    """What the CPU legs ran on: logical CPUs, the affinity set, the declared
+    thread share, torch's thread count and the CPU model name."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "affinity_cpus": _affinity(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "torch_threads": torch.get_num_threads(),
+            "cpu_model": model}
 
 
 def _time_launches(step, steps, warmup):
@@ -199,9 +230,9 @@ def bench_model_decode(steps, warmup, cpu, batch=128):
         "dtype": "bf16",
         "config": {"workload": "model_decode: random-init 4B-shaped hybrid recurrent model (36 layers = 27 GDN "
                                "+ 9 SWA/anchor-memory, hidden 2560, 32 heads, dk=dv=128, 256 anchor slots, "
-                               "vocab 151936), continuous batching over 128 slots, Poisson(4) arrivals of "
-                               "128-token prompts, geometric(1024) lengths, refill every 32 steps, "
-                               "top-k 20 / top-p 0.95 / T 0.6 sampling",
+                               f"vocab 151936), continuous batching over {batch} slots filled before the first step, then "
+                               "Poisson(4) arrivals of 128-token prompts, geometric(1024) lengths, refill every "
+                               "32 steps, top-k 20 / top-p 0.95 / T 0.6 sampling",
                    "global_batch": batch, "seq_len": 1, "parallelism": "single GPU"},
         "roofline": roof,
         "decode": {"useful_token_events": met.decode_useful_token_events,
@@ -272,15 +303,17 @@ class _OracleOps:
         self.slots.decode_state_update_torch(*args, **kw)
 
 
-def cpu_model_decode(batch, budget_s=20.0, max_steps=32):
+def cpu_model_decode(batch, budget_s=20.0, max_steps=32, single_thread=True):
     """Decode steps of the same model shape on the host cores: float32 weights
     (tiled N(0, 0.02) block), every slot live at position 128, the oracle's
     recurrence / anchor memory / sampler / bookkeeping.  Timed until
-    ``budget_s`` of CPU work (at least one step after one warm-up step)."""
+    ``budget_s`` of CPU work (at least one step after one warm-up step) on
+    ``cpu_threads()`` threads; then one more step on a single thread."""
     from yanchor_amd import runtime as rt
 
     threads = cpu_threads()
     torch.set_num_threads(threads)
+    host = cpu_host_info()
     cfg = rt.ModelConfig()
     m = rt.Model(cfg, batch=batch, device="cpu", seed=0, ops=_OracleOps(), dtype=torch.float32, init="tiled")
     gen = torch.Generator().manual_seed(5)
@@ -305,10 +338,21 @@ def cpu_model_decode(batch, budget_s=20.0, max_steps=32):
         _log(f"cpu baseline: step {n} done, {el:.1f} s")
         if el >= budget_s or n >= max_steps:
             break
-    return {"value": batch * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps x {batch} live slots of the same 36-layer model in float32 on "
-                      f"{threads} host threads (oracle recurrence, anchor memory, sampler), {el:.1f} s; "
-                      "refill prefill excluded as in the GPU figure"}
+    res = {"value": batch * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": f"{n} decode steps x {batch} live slots of the same 36-layer model in float32 on "
+                     f"{threads} host threads (oracle recurrence, anchor memory, sampler), {el:.1f} s; "
+                     "refill prefill excluded as in the GPU figure",
+           "host": host}
+    if single_thread:
+        torch.set_num_threads(1)
+        t0 = time.perf_counter()
+        step(n + 1)
+        el1 = time.perf_counter() - t0
+        _log(f"cpu baseline: one step on 1 thread, {el1:.1f} s")
+        res["single_thread"] = {"value": batch / el1, "unit": "tokens/s", "cores": 1,
+                                "sample": f"1 decode step x {batch} live slots on 1 thread, {el1:.1f} s"}
+        torch.set_num_threads(threads)
+    return res
 
 
 # ---------------------------------------------------------------------------

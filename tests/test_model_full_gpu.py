@@ -1,0 +1,123 @@
+"""The decode runtime at the full 4B shape (GPU).
+
+* Full-model decode: 36 layers (27 GDN + 9 SWA / anchor memory), hidden 2560,
+  32 heads of 128, 256 anchor slots, vocab 151936, B = 128 slots.
+* Long horizon: the same model with a 16-slot anchor memory committed every
+  64 tokens, B = 256 slots.
+
+The checks are the small-model ones run at these shapes: the captured HIP
+graph of the decode step reproduces eager steps bit for bit (with unrelated
+eager work and synchronisations between replays), and one decode step after
+a prefill reproduces the prefill of one more token (last-token logits within
+5e-2 relative error with bf16 activations: decode and prefill run different
+GEMM shapes).  At B = 256 the decode step is the 64th token of a memory
+chunk, so it commits: the anchor state it leaves is checked against the
+longer prefill's (slot counters exact, selected positions agreeing).
+"""
+import copy
+
+import pytest
+import torch
+
+from yanchor_amd import runtime as rt
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+FULL = rt.ModelConfig()                                            # 4B-shaped, 256 slots
+LONG = rt.ModelConfig(memory_capacity=16, memory_chunk=64)         # 16-slot memory
+
+
+def _prompts(b, t, vocab, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (b, t), generator=g)
+
+
+def _eager_twin(eng):
+    twin = rt.Engine.__new__(rt.Engine)
+    twin.__dict__.update({k: (v.clone() if torch.is_tensor(v) else v) for k, v in eng.__dict__.items()})
+    twin.m = copy.copy(eng.m)
+    twin.m._alloc_caches()
+    for dst, src in zip(twin.m.cache_tensors(), eng.m.cache_tensors()):
+        dst.copy_(src)
+    twin.use_graph, twin.graph = False, None
+    return twin
+
+
+@pytest.mark.parametrize("cfg,b,prompt,steps", [(FULL, 128, 24, 4), (LONG, 256, 61, 5)],
+                         ids=["decode_b128_256slots", "long_horizon_b256_16slots"])
+def test_full_model_graph_replay_matches_eager(gpu, cfg, b, prompt, steps):
+    """Every slot live; at B = 256 the steps cover positions 61..65, so the
+    64th token of the first memory chunk commits inside the replayed graph."""
+    m = rt.Model(cfg, batch=b, device=gpu, seed=11, init="tiled")
+    eng = rt.Engine(m, poll_interval=1 << 30, max_rows=b, max_new_tokens=64)
+    eng.capture()
+    prompts = _prompts(b, prompt, cfg.vocab, 12)
+    reqs = [rt.Request(i, prompts[i], 64, 0) for i in range(b)]
+    assert eng.fill(reqs) > 0 and not reqs
+    assert eng.live_slots() == b
+    twin = _eager_twin(eng)
+    for step in range(steps):
+        eng.step()
+        twin.step()
+        torch.cuda.synchronize()
+        print(f"step {step} compared", flush=True)
+        assert torch.equal(eng.decode_ids, twin.decode_ids), step
+        assert torch.equal(eng.finished, twin.finished) and torch.equal(eng.useful, twin.useful), step
+        for x, y in zip(eng.m.cache_tensors(), twin.m.cache_tensors()):
+            assert torch.equal(x, y), step
+        _ = torch.randn(1000, device=gpu).sum().item()   # unrelated eager work between replays
+    assert int(eng.useful) == b * steps
+    if cfg is LONG:
+        st = eng.m.memory[next(iter(eng.m.memory))]
+        assert bool((st.total == prompt + steps).all()) and bool((st.count == (prompt + steps) % 64).all())
+        assert bool((st.positions >= 0).all())       # the 16 slots hold committed tokens
+
+
+@pytest.mark.parametrize("cfg,b,t", [(FULL, 128, 20), (LONG, 256, 127)],
+                         ids=["decode_b128_256slots", "long_horizon_b256_commit"])
+def test_full_model_decode_after_prefill(gpu, cfg, b, t):
+    m = rt.Model(cfg, batch=b, device=gpu, seed=13, init="tiled")
+    prompts = _prompts(b, t + 1, cfg.vocab, 14).to(gpu)
+    ref_logits, ref_caches = m.prefill(prompts)                 # t + 1 tokens
+    logits, caches = m.prefill(prompts[:, :t])                   # t tokens ...
+    for dst, src in zip(m.cache_tensors(), caches):
+        dst.copy_(src)
+    del caches
+    pos = torch.full((b,), t, dtype=torch.long, device=gpu)
+    valid = torch.ones(b, dtype=torch.bool, device=gpu)
+    out = m.decode_step(prompts[:, t], pos, valid)               # ... plus one decode step
+    torch.cuda.synchronize()
+    err = rel_err(out, ref_logits)
+    print(f"B={b} T={t}: last-token logits rel err {err:.3e}", flush=True)
+    assert err <= 5e-2, err
+    # the anchor memory left behind: counters exact; at a commit (T + 1 a
+    # multiple of the chunk) the selected slots agree with the prefill's
+    # (near-tied admission scores may swap a slot: decode and prefill round
+    # the activations differently)
+    for layer, (mine, theirs) in _memory_fields(m, ref_caches).items():
+        assert torch.equal(mine["count"], theirs["count"]) and torch.equal(mine["total"], theirs["total"]), layer
+        if (t + 1) % cfg.memory_chunk == 0:
+            assert bool((mine["count"] == 0).all()) and bool((mine["positions"] >= 0).all())
+            same = (mine["positions"][..., :, None] == theirs["positions"][..., None, :]).any(-1).float().mean()
+            print(f"layer {layer}: {same.item():.4f} of the selected positions agree", flush=True)
+            assert same >= 0.9, (layer, same.item())
+
+
+MEMORY_FIELDS = ("keys", "values", "scores", "positions", "pending_keys", "pending_values", "pending_scores",
+                 "count", "total")
+
+
+def _memory_fields(m, ref_caches):
+    """{layer: (this model's memory fields, the same fields of ref_caches)}
+    in cache_tensors() order: per GDN layer the state and conv window, per
+    attention layer the ring keys, values, positions, then the memory fields."""
+    out, k = {}, 2 * len(m.gdn_state)
+    mine = m.cache_tensors()
+    for i in m.ring_k:
+        k += 3
+        out[i] = ({n: mine[k + j] for j, n in enumerate(MEMORY_FIELDS)},
+                  {n: ref_caches[k + j] for j, n in enumerate(MEMORY_FIELDS)})
+        k += len(MEMORY_FIELDS)
+    return out

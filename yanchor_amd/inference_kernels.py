@@ -164,6 +164,35 @@ def _update_fixed_decode_state_(sampled_token, storage, dense_seen, generated_le
            ctypes.cast(eos, ctypes.c_void_p).value, len(eos_token_ids), N.stream_of(storage))
 
 
+def _initial_attempt_order(difficulty, attempt_ids, prefill_group_ids=None):
+    """Order in which attempts take the physical slots at the start
+    (inference_kernels.py:1321-1329): hardest first (largest ``difficulty``,
+    the per-attempt generation cap), ties by ascending attempt id.  With
+    prefill groups, whole groups move together: groups ordered by their
+    hardest member, then their smallest attempt id; members inside a group in
+    the same row order.  Returns row indices into ``attempt_ids``."""
+    diff = [float(x) for x in (difficulty.tolist() if torch.is_tensor(difficulty) else difficulty)]
+    ids = [int(x) for x in attempt_ids]
+
+    def row_key(r):
+        return -diff[r], ids[r]
+
+    if prefill_group_ids is None:
+        return sorted(range(len(ids)), key=row_key)
+    members: dict[int, list[int]] = {}
+    for r, gid in enumerate(prefill_group_ids):
+        members.setdefault(int(gid), []).append(r)
+    groups = sorted(members.values(), key=lambda rows: (-max(diff[r] for r in rows), min(ids[r] for r in rows)))
+    return [r for rows in groups for r in sorted(rows, key=row_key)]
+
+
+def _should_compact_dynamic_decode_tail(live_slots, physical_slots, *, queue_exhausted, live_fraction):
+    """Tail-compaction trigger (inference_kernels.py:1348-1349): no more work
+    queued and at most ``live_fraction`` of the physical slots live."""
+    return bool(queue_exhausted and 0 < live_slots < physical_slots
+                and live_slots <= max(1, int(physical_slots * live_fraction)))
+
+
 def select_slots(finished, slot_rows=None, *, mode):
     """(indices [n] int64 with -1 padding, count [1] int64) of the rows that
     satisfy the mode, ascending; stays on the device."""

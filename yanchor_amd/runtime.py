@@ -744,6 +744,7 @@ class Engine:
         self.graph = None
         self.next_row = 0
         self.slot_request: list = [None] * B
+        self.row_request: list = []          # storage row -> its request, in admission order
 
     # one decode step on the device (captured)
     def _step(self):
@@ -814,8 +815,37 @@ class Engine:
         self.generated[rows] = 1
         for r, s in zip(requests, targets):
             self.slot_request[s] = r
+        self.row_request.extend(requests)
         torch.cuda.synchronize()
         return time.perf_counter() - t0
+
+    def fill(self, queue):
+        """Initial fill of the physical batch (runtime/model/inference_kernels.py:
+        1386-1450): the queued attempts are ordered by ``_initial_attempt_order``
+        (largest cap first, then attempt id), the first ``B`` of them are
+        prefilled together into slots 0..B-1 and the rest stay queued in that
+        order.  Returns the prefill seconds (excluded from decode time, as the
+        reference's initial prefill)."""
+        from . import inference_kernels as ik
+        if not queue:
+            return 0.0
+        order = ik._initial_attempt_order([r.cap for r in queue], [r.attempt_id for r in queue])
+        take = min(self.B, len(queue), self.max_rows - self.next_row)
+        first = [queue[i] for i in order[:take]]
+        queue[:] = [queue[i] for i in order[take:]]
+        return self.admit(first, list(range(take)))
+
+    def outputs(self):
+        """{attempt id: generated token ids} of every admitted request (a
+        host sync)."""
+        n = len(self.row_request)
+        lengths = self.generated[:n].tolist()
+        rows = self.storage[:n].cpu()
+        return {r.attempt_id: rows[i, : lengths[i]].tolist() for i, r in enumerate(self.row_request)}
+
+    def live_slots(self):
+        """Slots that run a sequence this step (a host sync)."""
+        return int(((~self.finished) & (self.slot_rows >= 0)).sum())
 
     def poll(self, queue, exhausted=False):
         """Host sync: refill finished slots (ascending) from the queue; with
@@ -869,11 +899,14 @@ class Engine:
 
 
 def synthetic_requests(steps, *, rate=4.0, prompt_len=128, mean_len=1024, max_len=8192, vocab=151936,
-                       seed=20260923):
-    """Poisson(rate) arrivals per step with uniform-random prompts and
-    geometric(mean_len) generation lengths (capped at max_len)."""
+                       seed=20260923, initial=0):
+    """``initial`` requests queued before step 0 (the backlog that fills the
+    physical batch), then Poisson(rate) arrivals per step; uniform-random
+    prompts and geometric(mean_len) generation lengths (capped at max_len)."""
     gen = torch.Generator().manual_seed(seed)
     arrivals = torch.poisson(torch.full((steps,), float(rate)), generator=gen).long().tolist()
+    if arrivals:
+        arrivals[0] += int(initial)
     reqs, aid = [], 0
     p = 1.0 / mean_len
     for step, n in enumerate(arrivals):
@@ -888,27 +921,43 @@ def synthetic_requests(steps, *, rate=4.0, prompt_len=128, mean_len=1024, max_le
 
 def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=128, mean_len=1024,
                          poll_interval=32, seed=20260923, use_graph=True, max_new_tokens=8192, requests=None,
-                         tail_compaction=False, engine=None):
+                         tail_compaction=False, engine=None, initial_fill=True):
     """Continuous batching for warmup + steps decode steps; returns metrics of
-    the timed steps (the reference's decode tokens/s definition).  Arrivals are
-    ``synthetic_requests`` unless ``requests`` is given."""
+    the timed steps (the reference's decode tokens/s definition).
+
+    Arrivals are ``synthetic_requests`` (a backlog of one request per slot
+    before step 0, then Poisson(rate) per step) unless ``requests`` is given.
+    With ``initial_fill`` the requests queued at step 0 fill the physical
+    batch before the first step (``Engine.fill``, the reference's initial
+    prefill); later arrivals refill finished slots at the poll points.  The
+    live slots of every timed step are recorded (``extra["live_slots"]``:
+    min / mean / first / last) from the device's useful-event counter, one
+    8-byte device copy per step."""
     eng = engine or Engine(model, seed=seed, poll_interval=poll_interval, use_graph=use_graph,
                            max_new_tokens=max_new_tokens, tail_compaction=tail_compaction)
     eng.capture()
     if requests is None:
         requests = synthetic_requests(warmup + steps, rate=rate, prompt_len=prompt_len, mean_len=mean_len,
-                                      max_len=max_new_tokens, vocab=model.cfg.vocab, seed=seed)
+                                      max_len=max_new_tokens, vocab=model.cfg.vocab, seed=seed,
+                                      initial=eng.B if initial_fill else 0)
     queue, pending, idx = [], sorted(requests, key=lambda r: r.arrival_step), 0
     m = EngineMetrics()
     total = warmup + steps
     t_start = None
     useful0 = 0
+    hist = torch.zeros(steps + 1, dtype=torch.long, device=eng.dev)
+    fill_seconds = 0.0
     for step in range(total):
         while idx < len(pending) and pending[idx].arrival_step <= step:
             queue.append(pending[idx])
             idx += 1
+        if step == 0 and initial_fill:
+            fill_seconds = eng.fill(queue)      # before the timed window: not part of its wall time
+        if step == warmup and warmup % poll_interval and initial_fill:
+            eng.poll(queue, exhausted=idx >= len(pending))   # the timed window starts with every slot live
         if step == warmup:
             torch.cuda.synchronize()
+            hist[0].copy_(eng.useful)
             useful0 = int(eng.useful.item())
             t_start = time.perf_counter()
             m.refill_prefill_seconds = 0.0
@@ -922,10 +971,15 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
         if t_start is not None:
             m.decode_steps += 1
             m.decode_scheduled_token_events += eng.B
+            hist[m.decode_steps].copy_(eng.useful)
     torch.cuda.synchronize()
     m.generation_wall_seconds = time.perf_counter() - t_start
     m.decode_useful_token_events = int(eng.useful.item()) - useful0
     m.peak_allocated_gib = torch.cuda.max_memory_allocated() / 2**30
-    m.extra = {"queue_left": len(queue), "live_slots_end": int(((~eng.finished) & (eng.slot_rows >= 0)).sum()),
-               "tail_compactions": list(eng.compactions)}
+    live = (hist[1:] - hist[:-1]).cpu()
+    m.extra = {"queue_left": len(queue), "live_slots_end": eng.live_slots(),
+               "live_slots": {"min": int(live.min()), "mean": float(live.float().mean()),
+                              "first": int(live[0]), "last": int(live[-1])} if steps else {},
+               "physical_slots": eng.B, "tail_compactions": list(eng.compactions),
+               "initial_prefill_seconds": fill_seconds}
     return m
