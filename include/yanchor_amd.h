@@ -399,6 +399,27 @@ int64_t yh_topk_workspace_bytes(int64_t B, int64_t V, int64_t top_k);
 void yh_topk_segments(int64_t V, int64_t top_k, int* n_segments, int* seg_len);
 
 /*
+ * yh_topk_sample without a workspace argument: it allocates nothing and calls
+ * no allocating routine.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same arguments, kernels and results as yh_topk_sample.  The candidate lists
+ * live in a static device array of YH_TOPK_STATIC_SCRATCH_BYTES per GPU
+ * (8 MiB, held until the process ends); calls whose yh_topk_workspace_bytes
+ * (B, V, top_k) exceed it return YH_ERR_INVALID.  At V = 151936 that is up to
+ * 2759 rows at top_k = 20, 862 rows at top_k = 64.  The stream's device must
+ * be the current device.  Every call on a GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams, other host threads) race.
+ */
+#define YH_TOPK_STATIC_SCRATCH_BYTES (8ll << 20)
+int yh_topk_sample_noalloc(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen,
+                           int64_t seen_stride, float penalty, const int64_t* attempt_ids, const int64_t* steps,
+                           int64_t step, uint64_t seed, uint64_t stream_id, float temperature, int64_t top_k,
+                           float top_p, int mode, int64_t* tokens, float* out_values, int64_t* out_indices,
+                           int64_t B, int64_t V, yh_stream_t stream);
+
+/*
  * scores[i] -= penalty where seen[i], float32, in place; n elements.
  * Replaces _qwen35_dense_presence_penalty_kernel / _apply_dense_presence_penalty_
  * (runtime/model/inference_kernels.py:1095-1114).

@@ -55,6 +55,8 @@ SIGNATURES: dict[str, list] = {
     "yh_window_attend_gated": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i32, _p],
     "yh_topk_sample": [_p, _i32, _i64, _p, _i64, _f32, _p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32,
                        _i64, _f32, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "yh_topk_sample_noalloc": [_p, _i32, _i64, _p, _i64, _f32, _p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64,
+                               _f32, _i64, _f32, _i32, _p, _p, _p, _i64, _i64, _p],
     "yh_presence_penalty": [_p, _p, _i64, _f32, _p],
     "yh_counter_uniform": [_p, _p, _i64, ctypes.c_uint64, ctypes.c_uint64, _p, _i64, _p],
     "yh_decode_bookkeeping": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,

@@ -22,6 +22,8 @@
 // draws the token.
 #include "common.h"
 
+#include <mutex>
+
 namespace yh {
 namespace {
 
@@ -336,13 +338,16 @@ __global__ void counter_uniform_kernel(const int64_t* ids, const int64_t* steps,
 }  // namespace
 }  // namespace yh
 
-extern "C" int yh_topk_sample(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen,
-                              int64_t seen_stride, float penalty, const int64_t* attempt_ids,
-                              const int64_t* steps, int64_t step, uint64_t seed, uint64_t stream_id,
-                              float temperature, int64_t top_k, float top_p, int mode, int64_t* tokens,
-                              float* out_values, int64_t* out_indices, void* workspace,
-                              int64_t workspace_bytes, int64_t B, int64_t V, yh_stream_t stream) {
-  using namespace yh;
+namespace yh {
+namespace {
+
+// Both phases of the sampler with the candidate lists in `workspace`; the
+// two entry points differ only in where that memory comes from.
+int topk_sample_launch(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen,
+                       int64_t seen_stride, float penalty, const int64_t* attempt_ids, const int64_t* steps,
+                       int64_t step, uint64_t seed, uint64_t stream_id, float temperature, int64_t top_k,
+                       float top_p, int mode, int64_t* tokens, float* out_values, int64_t* out_indices,
+                       void* workspace, int64_t workspace_bytes, int64_t B, int64_t V, yh_stream_t stream) {
   YH_CHECK_ARG(scores && tokens && workspace && attempt_ids, "topk_sample: null pointer");
   YH_CHECK_ARG(B >= 0 && V > 0 && V <= 64LL * kSegLen, "topk_sample: V must lie in [1, %d]", 64 * kSegLen);
   YH_CHECK_ARG(top_k >= 1 && top_k <= kMaxK && top_k <= V, "topk_sample: top_k must lie in [1, %d]", kMaxK);
@@ -381,6 +386,92 @@ extern "C" int yh_topk_sample(const void* scores, int dtype, int64_t row_stride,
   hipLaunchKernelGGL(sample_rows_kernel, dim3(static_cast<unsigned>(B)), dim3(kTopkThreads), 0, st, sa);
   YH_CHECK_LAUNCH("sample_rows");
   return YH_OK;
+}
+
+// ---- allocation-free variant -----------------------------------------------
+// The candidate lists live in this file-scope array: one copy per GPU, held
+// until the process ends.  Host code never passes `scratch` itself (its name
+// is a host-side stand-in, not a device address): the device address comes
+// from hipGetSymbolAddress, looked up once per device on that device's first
+// call and kept in g_scratch_addr.  Every call on a GPU shares that GPU's
+// array, so calls that overlap on one GPU (different streams, different
+// host threads) race.  Nothing in it has to start at zero: phase 1 writes all
+// k entries of every (row, segment) list before phase 2 reads them.
+__device__ __align__(256) uint64_t scratch[YH_TOPK_STATIC_SCRATCH_BYTES / sizeof(uint64_t)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device the stream runs on (which must
+// be the current device: the symbol lookup is per current device).
+int static_scratch(yh_stream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("topk_sample_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return YH_ERR_HIP;
+  }
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) {
+      set_error("topk_sample_noalloc: hipStreamGetDevice failed: %s", hipGetErrorString(e));
+      return YH_ERR_HIP;
+    }
+    YH_CHECK_ARG(sdev == dev, "topk_sample_noalloc: the stream's device %d is not the current device %d", sdev,
+                 dev);
+  }
+  YH_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "topk_sample_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("topk_sample_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return YH_ERR_HIP;
+    }
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return YH_OK;
+}
+
+}  // namespace
+}  // namespace yh
+
+extern "C" int yh_topk_sample(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen,
+                              int64_t seen_stride, float penalty, const int64_t* attempt_ids,
+                              const int64_t* steps, int64_t step, uint64_t seed, uint64_t stream_id,
+                              float temperature, int64_t top_k, float top_p, int mode, int64_t* tokens,
+                              float* out_values, int64_t* out_indices, void* workspace,
+                              int64_t workspace_bytes, int64_t B, int64_t V, yh_stream_t stream) {
+  return yh::topk_sample_launch(scores, dtype, row_stride, seen, seen_stride, penalty, attempt_ids, steps, step,
+                                seed, stream_id, temperature, top_k, top_p, mode, tokens, out_values,
+                                out_indices, workspace, workspace_bytes, B, V, stream);
+}
+
+extern "C" int yh_topk_sample_noalloc(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen,
+                                      int64_t seen_stride, float penalty, const int64_t* attempt_ids,
+                                      const int64_t* steps, int64_t step, uint64_t seed, uint64_t stream_id,
+                                      float temperature, int64_t top_k, float top_p, int mode, int64_t* tokens,
+                                      float* out_values, int64_t* out_indices, int64_t B, int64_t V,
+                                      yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(B >= 0 && V > 0 && top_k >= 1 && top_k <= kMaxK, "topk_sample_noalloc: bad sizes");
+  const int64_t need = yh_topk_workspace_bytes(B, V, top_k);
+  YH_CHECK_ARG(need <= YH_TOPK_STATIC_SCRATCH_BYTES,
+               "topk_sample_noalloc: B=%lld, V=%lld, top_k=%lld need %lld bytes of scratch, above the static "
+               "maximum of %lld (use yh_topk_sample with a workspace)",
+               (long long)B, (long long)V, (long long)top_k, (long long)need,
+               (long long)YH_TOPK_STATIC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = static_scratch(stream, &ws);
+  if (rc != YH_OK) return rc;
+  return topk_sample_launch(scores, dtype, row_stride, seen, seen_stride, penalty, attempt_ids, steps, step, seed,
+                            stream_id, temperature, top_k, top_p, mode, tokens, out_values, out_indices, ws,
+                            YH_TOPK_STATIC_SCRATCH_BYTES, B, V, stream);
 }
 
 extern "C" void yh_topk_segments(int64_t V, int64_t top_k, int* n_segments, int* seg_len) {
