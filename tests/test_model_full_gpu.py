@@ -75,10 +75,18 @@ def test_full_model_graph_replay_matches_eager(gpu, cfg, b, prompt, steps):
         assert bool((st.positions >= 0).all())       # the 16 slots hold committed tokens
 
 
-@pytest.mark.parametrize("cfg,b,t", [(FULL, 128, 20), (LONG, 256, 127)],
-                         ids=["decode_b128_256slots", "long_horizon_b256_commit"])
-def test_full_model_decode_after_prefill(gpu, cfg, b, t):
-    m = rt.Model(cfg, batch=b, device=gpu, seed=13, init="tiled")
+@pytest.mark.parametrize("cfg,b,t,dtype,tol", [(FULL, 128, 20, torch.float32, 1e-3),
+                                               (FULL, 128, 20, torch.bfloat16, 1e-1),
+                                               (LONG, 256, 127, torch.bfloat16, 1e-1)],
+                         ids=["decode_b128_256slots_fp32", "decode_b128_256slots", "long_horizon_b256_commit"])
+def test_full_model_decode_after_prefill(gpu, cfg, b, t, dtype, tol):
+    """float32 activations pin the cache logic at the full shape (the bf16
+    kernels' float32 twins and torch glue): measured 1.8e-5.  bf16 bounds the
+    rounding drift of the served configuration through 36 layers of a
+    random-init model, where decode and prefill round at different points
+    (fp32 prefill attention, the chunked GDN form, other GEMM shapes):
+    measured 5.7e-2 at B = 128 and 5.9e-2 at B = 256, against 1e-1."""
+    m = rt.Model(cfg, batch=b, device=gpu, seed=13, dtype=dtype)
     prompts = _prompts(b, t + 1, cfg.vocab, 14).to(gpu)
     ref_logits, ref_caches = m.prefill(prompts)                 # t + 1 tokens
     logits, caches = m.prefill(prompts[:, :t])                   # t tokens ...
@@ -90,8 +98,8 @@ def test_full_model_decode_after_prefill(gpu, cfg, b, t):
     out = m.decode_step(prompts[:, t], pos, valid)               # ... plus one decode step
     torch.cuda.synchronize()
     err = rel_err(out, ref_logits)
-    print(f"B={b} T={t}: last-token logits rel err {err:.3e}", flush=True)
-    assert err <= 5e-2, err
+    print(f"B={b} T={t} {dtype}: last-token logits rel err {err:.3e}", flush=True)
+    assert err <= tol, err
     # the anchor memory left behind: counters exact; at a commit (T + 1 a
     # multiple of the chunk) the selected slots agree with the prefill's
     # (near-tied admission scores may swap a slot: decode and prefill round

@@ -406,7 +406,7 @@ __global__ void __launch_bounds__(NT) gdn_decode_fused_kernel(FusedArgs a) {
     if (lane == 0) {
       const float av = bfv(aa) + a.dt_bias[hv];
       const float sp = av > 20.f ? av : log1pf(expf(av));
-      sc[2] = 1.f / (1.f + expf(-bfv(bb)));
+      sc[2] = bfv(f32_to_bf16(1.f / (1.f + expf(-bfv(bb)))));   // beta is stored in the logits' dtype
       sc[1] = expf(-expf(a.a_log[hv]) * sp);
     }
   }

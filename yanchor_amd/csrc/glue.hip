@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(256) gdn_prep_kernel(PrepArgs a) {
     const float bb = bf(a.proj[b * a.P + a.boff + h]);
     const float aa = bf(a.proj[b * a.P + a.aoff + h]) + a.dt_bias[h];
     const float sp = aa > 20.f ? aa : log1pf(expf(aa));
-    a.beta[b * a.HV + h] = 1.f / (1.f + expf(-bb));
+    a.beta[b * a.HV + h] = bf(tobf(1.f / (1.f + expf(-bb))));   // beta is stored in the logits' dtype (bf16)
     a.g[b * a.HV + h] = -expf(a.a_log[h]) * sp;
   }
 }

@@ -283,7 +283,8 @@ class TorchGlue:
         window = torch.cat((conv_state, proj[:, None, :conv_dim]), 1)          # [B, K, C], oldest first
         conv_state.copy_(window[:, 1:])
         mixed = F.silu((window.float() * conv_w.float().t()[None]).sum(1)).to(proj.dtype)
-        beta = torch.sigmoid(proj[:, b_offset: b_offset + hv].float())
+        b = proj[:, b_offset: b_offset + hv]
+        beta = torch.sigmoid(b.float()).to(b.dtype).float()         # beta in the logits' dtype
         g = -torch.exp(a_log) * F.softplus(proj[:, a_offset: a_offset + hv].float() + dt_bias)
         return mixed[:, :qk_dim], mixed[:, qk_dim: 2 * qk_dim], mixed[:, 2 * qk_dim:], g, beta
 
@@ -466,7 +467,7 @@ class Model:
         z = proj[..., c.conv_dim: c.conv_dim + c.gdn_heads_v * c.gdn_dv]
         b = proj[..., c.conv_dim + c.gdn_heads_v * c.gdn_dv: c.conv_dim + c.gdn_heads_v * c.gdn_dv + c.gdn_heads_v]
         a = proj[..., -c.gdn_heads_v:]
-        beta = torch.sigmoid(b.float())
+        beta = torch.sigmoid(b.float()).to(b.dtype).float()          # beta in the logits' dtype (wheel:500)
         g = -torch.exp(L["a_log"]) * F.softplus(a.float() + L["dt_bias"])
         return qkv, z, beta, g
 
