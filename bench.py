@@ -294,7 +294,8 @@ class _OracleOps:
     def memory_sequence(self, q, key, value, scores, valid, chunk, state):
         return self.anchor.sequence(q, key, value, scores, valid, chunk, state, dtype=torch.float32)
 
-    def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty):
+    def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty,
+               backend="triton_top20"):
         sc = self.sampling.presence_penalty(logits, seen, penalty) if seen is not None else logits.float()
         vals, idx = torch.topk(sc / temperature, top_k, dim=-1)
         return self.sampling.top20_counter_sample(vals, idx, attempt_ids, steps, seed=seed, top_p=top_p)

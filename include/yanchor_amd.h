@@ -374,8 +374,14 @@ enum yh_sample_mode {
  *
  * Replaces torch.topk + _qwen35_top20_counter_sample_kernel
  * (_sample_top_k_top_p_counter_triton, runtime/model/inference_kernels.py:
- * 1147-1167) and sample_top_k_top_p_counter (inference_kernels.py:73-88) for
- * 1 <= top_k <= 64.
+ * 1147-1167) and sample_top_k_top_p_counter (inference_kernels.py:73-88).
+ * Both modes take 1 <= top_k <= 64.  The torch-sampler mode also takes the
+ * reference's other branches (inference_kernels.py:78-86): top_k <= 0 with
+ * top_p == 1 draws from the softmax over the whole vocabulary in vocabulary
+ * order; top_k <= 0 (the whole vocabulary) or top_k > 64 with any top_p
+ * keeps the top k by value and truncates at top_p.  Those run one workgroup
+ * per row with exact fixed-point probability sums, need no workspace (it may
+ * be NULL) and return no top-k values.
  *
  *   scores       [B, V] rows `row_stride` elements apart (f32 / bf16 / f16)
  *   seen         NULL or uint8/bool [B, V] rows `seen_stride` apart; where set,
@@ -386,6 +392,7 @@ enum yh_sample_mode {
  *   out_values, out_indices  NULL or [B, top_k] float / int64: the selected
  *                top-k (descending; equal values by ascending index)
  *   workspace    device scratch of at least yh_topk_workspace_bytes(B, V, k)
+ *                (1 <= k <= 64)
  * top_k == 1 returns the argmax.  Otherwise temperature > 0, 0 < top_p <= 1.
  */
 int yh_topk_sample(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen, int64_t seen_stride,

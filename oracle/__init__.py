@@ -18,6 +18,9 @@ the reference file:line it follows:
                       sampler, the dense presence penalty.
 * ``oracle.slots``    slot bookkeeping, cu_seqlens, compaction keep-lists,
                       refill planning.
+* ``oracle.glue``     the decode-layer glue: RMSNorm, gated RMSNorm, conv
+                      update (torch and CUDA-backend forms), GDN gates, RoPE,
+                      the memory projections, the SWA ring read and write.
 
 Floating-point parts are written with torch on the CPU (float64 by default so
 they act as the exact answer; float32 when timed as the CPU baseline).  Integer

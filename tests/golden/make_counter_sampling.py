@@ -58,6 +58,19 @@ def main():
             idx, probs = ref.top_k_top_p_distribution(logits, temperature=t, top_k=int(k), top_p=p)
             out[f"dist_idx_{i}"] = idx.numpy()
             out[f"dist_p_{i}"] = probs.numpy()
+    # the full-vocabulary branches (inference_kernels.py:78-86): top_k <= 0
+    # with top_p == 1 (vocabulary order), top_k <= 0 with top_p < 1 and
+    # top_k > 64 (value order, truncated at top_p); on the same logits and
+    # on bf16-valued logits (exact ties)
+    full_cases = [(0.6, 0, 1.0, 20260923), (1.0, -1, 1.0, 7), (0.8, 0, 0.9, 123), (0.7, 100, 0.95, 5),
+                  (1.3, 300, 1.0, 11), (0.6, 0, 0.5, 77), (2.0, 65, 0.99, 3)]
+    out["full_cases"] = np.array(full_cases, dtype=np.float64)
+    logits_bf16 = (torch.randn(b, v, generator=gen) * 3.0).to(torch.bfloat16).float()
+    out["logits_bf16"] = logits_bf16.numpy()
+    for name, lg in (("", logits), ("bf16_", logits_bf16)):
+        for i, (t, k, p, seed) in enumerate(full_cases):
+            tok = ref.sample_top_k_top_p_counter(lg, att, st, seed=int(seed), temperature=t, top_k=int(k), top_p=p)
+            out[f"full_{name}tokens_{i}"] = tok.numpy()
     np.savez(OUT, **out)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
 

@@ -49,3 +49,37 @@ def test_synthetic_requests_backlog():
     # the same seed without the backlog gives the same Poisson arrivals after step 0
     plain = rt.synthetic_requests(10, rate=4.0, prompt_len=8, vocab=100)
     assert sum(r.arrival_step > 0 for r in plain) == sum(r.arrival_step > 0 for r in reqs)
+
+
+def test_repetition_periods():
+    """The mechanical-repetition stop (runtime/scoring/protocols.py:89-109):
+    the smallest period in [128, 256] whose 8 copies end the sequence."""
+    import numpy as np
+    rng = np.random.default_rng(0)
+    unit = rng.integers(0, 1000, 130)
+    w = 256 * 8
+    rows, lengths = [], []
+
+    def right_aligned(seq):
+        row = np.zeros(w, dtype=np.int64)
+        row[w - len(seq):] = seq
+        return row
+
+    rep = np.concatenate([rng.integers(0, 1000, 50), np.tile(unit, 8)])         # 8 copies of a 130-block
+    rows.append(right_aligned(rep)), lengths.append(len(rep))
+    rows.append(right_aligned(np.tile(unit, 7))), lengths.append(130 * 7)       # only 7 copies
+    short = rng.integers(0, 1000, 100)
+    rows.append(right_aligned(np.tile(short, 16))), lengths.append(1600)       # period 100 < 128: its double 200 counts
+    rows.append(right_aligned(rng.integers(0, 1000, w))), lengths.append(w)    # no repetition
+    rows.append(right_aligned(np.tile(np.arange(128), 8))), lengths.append(1024)
+    got = rt.repetition_periods(np.stack(rows), np.array(lengths))
+    assert got.tolist() == [130, 0, 200, 0, 128]
+    assert rt.repetition_periods(np.zeros((1, 100), dtype=np.int64), np.array([100])).tolist() == [0]
+
+
+def test_text_ids_round_trip():
+    from yanchor_amd import inference
+    ids = inference.encode_text("héllo, world", 151936)
+    assert all(0 <= i < 256 for i in ids)
+    assert inference.decode_ids(ids) == "héllo, world"
+    assert inference.decode_ids([104, 105, 5000]) == "hi�"

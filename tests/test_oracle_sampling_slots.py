@@ -57,6 +57,17 @@ def test_sampler_golden_tokens_and_distribution():
             assert np.allclose(probs.numpy(), GOLD[f"dist_p_{i}"], atol=1e-7)
 
 
+def test_sampler_full_vocabulary_golden_tokens():
+    """The reference's full-vocabulary branches (inference_kernels.py:78-86)."""
+    att, st = torch.from_numpy(GOLD["attempt_ids"]), torch.from_numpy(GOLD["row_steps"])
+    for name, key in (("", "logits"), ("bf16_", "logits_bf16")):
+        logits = torch.from_numpy(GOLD[key])
+        for i, (t, k, p, seed) in enumerate(GOLD["full_cases"].tolist()):
+            tok = sampling.sample_top_k_top_p_counter(logits, att, st, seed=int(seed), temperature=t,
+                                                      top_k=int(k), top_p=p)
+            assert np.array_equal(tok.numpy(), GOLD[f"full_{name}tokens_{i}"]), f"{name}case {i}"
+
+
 def test_sampler_special_cases():
     logits = torch.from_numpy(GOLD["logits"])
     att, st = torch.from_numpy(GOLD["attempt_ids"]), torch.from_numpy(GOLD["row_steps"])

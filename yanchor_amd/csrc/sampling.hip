@@ -341,6 +341,289 @@ __global__ void counter_uniform_kernel(const int64_t* ids, const int64_t* steps,
 namespace yh {
 namespace {
 
+// ---- full-vocabulary sampling ------------------------------------------------
+// sample_top_k_top_p_counter's branches past the top-64 path
+// (inference_kernels.py:78-86): top_k <= 0 with top_p == 1 draws from the
+// softmax over the whole vocabulary in vocabulary order; any other top_k
+// outside [1, 64] (top_k <= 0 meaning the whole vocabulary) keeps the top k,
+// truncates them at top_p in value order and draws from the rest.
+//
+// One workgroup per row.  Every draw is a selection "the first element, in a
+// given order, whose inclusive cumulative weight reaches t": the elements are
+// ordered by a 64-bit key K (descending), (value key << 32 | ~index) for value
+// order (larger value first, lower index first on equal values) or ~index
+// for vocabulary order.  K* is found 4 bits at a time from the top: a pass
+// over the row sums the weight of the elements that share the bits fixed so
+// far into 16 buckets of the next digit, and the largest digit whose
+// cumulative weight (with everything above) reaches t is kept.  Weights are
+// counts (for the top-k cut) or probabilities as 2^62 fixed-point integers,
+// so every sum is exact and independent of summation order.  The row is
+// re-read on every pass (from L2 / the Infinity Cache after the first).
+constexpr int kFullThreads = 1024;
+constexpr int kFullWaves = kFullThreads / kWave;
+constexpr int kFan = 16;
+constexpr double kMassOne = 4611686018427387904.0;  // 2^62: fixed-point probability 1
+
+struct FullArgs {
+  const void* scores;     // [B, V] rows row_stride apart
+  const uint8_t* seen;    // [B, V] rows seen_stride apart, or null
+  const int64_t* ids;     // [B]
+  const int64_t* steps;   // [B] or null (then `step`)
+  int64_t* out;           // [B]
+  int64_t row_stride, seen_stride, step, top_k;
+  int V, vocab_order;
+  uint32_t seed, stream;
+  float penalty, temperature, top_p;
+};
+
+struct FullShared {
+  uint64_t part[kFullWaves][kFan];
+  uint32_t cpart[kFullWaves][kFan];
+  uint64_t bucket[kFan];
+  uint32_t bcount[kFan];
+  double dpart[kFullWaves];
+  float fpart[kFullWaves];
+};
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += shfl_xor_u64(v, off);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Score of element i with the presence penalty applied (before temperature).
+template <int DT>
+__device__ __forceinline__ float full_value(const FullArgs& a, const char* row, const uint8_t* srow, int i) {
+  uint32_t bits;
+  if constexpr (DT == YH_F32) bits = *reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(i) * 4);
+  else bits = *reinterpret_cast<const uint16_t*>(row + static_cast<int64_t>(i) * 2);
+  float x = decode_elem<DT>(bits);
+  if (srow && srow[i]) x = x - a.penalty;
+  return x;
+}
+
+// Selection state of one row: the candidate set is K >= lo; weights are
+// masses (mass) or counts; masses need the row's tempered maximum mt and
+// the candidate set's sum S of exp(x / T - mt).
+struct FullRow {
+  const char* row;
+  const uint8_t* srow;
+  uint64_t lo;
+  float mt;
+  double scale;  // 2^62 / S: fixed-point mass per unit of exp(x / T - mt)
+};
+
+__device__ __forceinline__ uint64_t full_key(const FullArgs& a, float x, int i) {
+  return a.vocab_order ? static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(i)) : ckey(x, static_cast<uint32_t>(i));
+}
+
+template <int DT>
+__device__ __forceinline__ uint64_t full_mass(const FullArgs& a, const FullRow& r, float x) {
+  const float xt = x / a.temperature;
+  return static_cast<uint64_t>(static_cast<double>(expf(xt - r.mt)) * r.scale);
+}
+
+// The largest K* among candidates with W(K >= K*) >= t (t >= 1), and
+// W(K >= K*) in *incl.  Bits from `top` up are fixed to `prefix` (the bits of
+// ~index above bit 19, all ones for an index below 2^20).  If t exceeds the
+// candidates' total weight the smallest candidate key is returned.
+template <int DT, bool MASS>
+__device__ uint64_t full_select(const FullArgs& a, const FullRow& r, uint64_t t, int top, uint64_t prefix,
+                                uint64_t* incl, FullShared& sh) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  uint64_t above = 0;  // weight of candidates with a key above every key of the current prefix
+  for (int pos = top - 4; pos >= 0; pos -= 4) {
+    if (!a.vocab_order && pos == 28) {  // ~index bits 31..20: all ones (index < 2^20)
+      prefix = (prefix << 12) | 0xfffull;
+      pos = 16;
+    }
+    uint64_t acc[kFan];
+    uint32_t cnt[kFan];
+#pragma unroll
+    for (int c = 0; c < kFan; ++c) {
+      acc[c] = 0;
+      cnt[c] = 0;
+    }
+    for (int i = tid; i < a.V; i += kFullThreads) {
+      const float x = full_value<DT>(a, r.row, r.srow, i);
+      const uint64_t K = full_key(a, x, i);
+      if (K < r.lo || (pos + 4 < 64 && (K >> (pos + 4)) != prefix)) continue;
+      const int d = static_cast<int>((K >> pos) & 0xf);
+      const uint64_t w = MASS ? full_mass<DT>(a, r, x) : 1ull;
+#pragma unroll
+      for (int c = 0; c < kFan; ++c) {
+        acc[c] += d == c ? w : 0ull;
+        cnt[c] += d == c ? 1u : 0u;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kFan; ++c) {
+      const uint64_t s = wave_sum_u64(acc[c]);
+      const uint32_t n = wave_sum_u32(cnt[c]);
+      if (lane == 0) {
+        sh.part[wv][c] = s;
+        sh.cpart[wv][c] = n;
+      }
+    }
+    __syncthreads();
+    if (tid < kFan) {
+      uint64_t s = 0;
+      uint32_t n = 0;
+      for (int w = 0; w < kFullWaves; ++w) {
+        s += sh.part[w][tid];
+        n += sh.cpart[w][tid];
+      }
+      sh.bucket[tid] = s;
+      sh.bcount[tid] = n;
+    }
+    __syncthreads();
+    // largest digit whose cumulative weight reaches t; past the total, the
+    // smallest non-empty digit
+    int dsel = -1, last = 0;
+    uint64_t cum = above, cum_last = above;
+    for (int c = kFan - 1; c >= 0; --c) {
+      if (sh.bcount[c]) {
+        last = c;
+        cum_last = cum;
+      }
+      if (cum + sh.bucket[c] >= t && sh.bcount[c]) {
+        dsel = c;
+        break;
+      }
+      cum += sh.bucket[c];
+    }
+    if (dsel < 0) {
+      dsel = last;
+      cum = cum_last;
+    }
+    const uint64_t w_sel = sh.bucket[dsel];
+    const uint32_t n_sel = sh.bcount[dsel];
+    __syncthreads();
+    above = cum;
+    prefix = (prefix << 4) | static_cast<uint64_t>(dsel);
+    if (n_sel == 1 && pos > 0) {
+      // a single element left: its key is the largest key under the prefix
+      uint64_t best = 0;
+      for (int i = tid; i < a.V; i += kFullThreads) {
+        const float x = full_value<DT>(a, r.row, r.srow, i);
+        const uint64_t K = full_key(a, x, i);
+        if (K >= r.lo && (K >> pos) == prefix) best = K > best ? K : best;
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t y = shfl_xor_u64(best, off);
+        best = y > best ? y : best;
+      }
+      if (lane == 0) sh.part[wv][0] = best;
+      __syncthreads();
+      uint64_t k = 0;
+      for (int w = 0; w < kFullWaves; ++w) k = sh.part[w][0] > k ? sh.part[w][0] : k;
+      __syncthreads();
+      *incl = above + w_sel;
+      return k;
+    }
+    if (pos == 0) {
+      *incl = above + w_sel;
+      return prefix;
+    }
+  }
+  *incl = above;
+  return prefix;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kFullThreads) sample_full_kernel(FullArgs a) {
+  __shared__ FullShared sh;
+  constexpr int ES = DT == YH_F32 ? 4 : 2;
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  FullRow r{static_cast<const char*>(a.scores) + b * a.row_stride * ES, a.seen ? a.seen + b * a.seen_stride : nullptr,
+            0ull, 0.f, 0.0};
+
+  // row maximum of the scores (the top of the value order; its tempered
+  // value is the softmax shift torch uses, division being monotone)
+  float m = -INFINITY;
+  for (int i = tid; i < a.V; i += kFullThreads) m = fmaxf(m, full_value<DT>(a, r.row, r.srow, i));
+  m = wave_max(m);
+  if (lane == 0) sh.fpart[wv] = m;
+  __syncthreads();
+  m = sh.fpart[0];
+  for (int w = 1; w < kFullWaves; ++w) m = fmaxf(m, sh.fpart[w]);
+  __syncthreads();
+  r.mt = m / a.temperature;
+
+  uint64_t incl = 0;
+  // top-k cut (1 < k < V, value order): the k-th largest key bounds the candidates
+  if (!a.vocab_order && a.top_k > 1 && a.top_k < a.V)
+    r.lo = full_select<DT, false>(a, r, static_cast<uint64_t>(a.top_k), 64, 0ull, &incl, sh);
+
+  // S = sum of exp(x / T - mt) over the candidates (fixed order: per thread,
+  // then the wave butterfly, then the waves in order)
+  double s = 0.0;
+  for (int i = tid; i < a.V; i += kFullThreads) {
+    const float x = full_value<DT>(a, r.row, r.srow, i);
+    if (full_key(a, x, i) >= r.lo) s += static_cast<double>(expf(x / a.temperature - r.mt));
+  }
+  s = wave_sum_f64(s);
+  if (lane == 0) sh.dpart[wv] = s;
+  __syncthreads();
+  s = 0.0;
+  for (int w = 0; w < kFullWaves; ++w) s += sh.dpart[w];
+  __syncthreads();
+  r.scale = kMassOne / s;
+
+  // total fixed-point mass of the candidates
+  uint64_t tot = 0;
+  for (int i = tid; i < a.V; i += kFullThreads) {
+    const float x = full_value<DT>(a, r.row, r.srow, i);
+    if (full_key(a, x, i) >= r.lo) tot += full_mass<DT>(a, r, x);
+  }
+  tot = wave_sum_u64(tot);
+  if (lane == 0) sh.part[wv][0] = tot;
+  __syncthreads();
+  tot = 0;
+  for (int w = 0; w < kFullWaves; ++w) tot += sh.part[w][0];
+  __syncthreads();
+
+  const uint32_t id = static_cast<uint32_t>(a.ids[b]);
+  const uint32_t st = static_cast<uint32_t>(a.steps ? a.steps[b] : a.step);
+  float u = static_cast<float>((static_cast<double>(counter_word(id, st, a.seed, a.stream)) + 0.5) / 4294967296.0);
+  const float umax = 1.0f - 5.9604644775390625e-08f;  // counter_uniform's clamp: 1 - eps/2
+  u = u < umax ? u : umax;
+  auto at_least = [](double x, uint64_t hi) -> uint64_t {  // ceil(x) clamped to [1, hi]
+    double c = ceil(x);
+    uint64_t t = c < 1.0 ? 1ull : static_cast<uint64_t>(c);
+    return t > hi ? hi : t;
+  };
+  uint64_t key;
+  if (a.vocab_order) {
+    // first index whose cumulative probability reaches u * total; the index
+    // bits above bit 19 are ~index's all-ones
+    key = full_select<DT, true>(a, r, at_least(static_cast<double>(u) * static_cast<double>(tot), tot), 20,
+                                0xfffull, &incl, sh);
+  } else {
+    // last kept element: the first whose inclusive mass reaches top_p (so
+    // every element before it has an exclusive mass below top_p); then the
+    // draw inside the kept mass
+    full_select<DT, true>(a, r, at_least(static_cast<double>(a.top_p) * static_cast<double>(tot), tot), 64, 0ull,
+                          &incl, sh);
+    const uint64_t kept = incl;
+    key = full_select<DT, true>(a, r, at_least(static_cast<double>(u) * static_cast<double>(kept), kept), 64, 0ull,
+                                &incl, sh);
+  }
+  if (tid == 0) a.out[b] = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(key & 0xffffffffu));
+}
+
 // Both phases of the sampler with the candidate lists in `workspace`; the
 // two entry points differ only in where that memory comes from.
 int topk_sample_launch(const void* scores, int dtype, int64_t row_stride, const uint8_t* seen,
@@ -348,10 +631,31 @@ int topk_sample_launch(const void* scores, int dtype, int64_t row_stride, const 
                        int64_t step, uint64_t seed, uint64_t stream_id, float temperature, int64_t top_k,
                        float top_p, int mode, int64_t* tokens, float* out_values, int64_t* out_indices,
                        void* workspace, int64_t workspace_bytes, int64_t B, int64_t V, yh_stream_t stream) {
-  YH_CHECK_ARG(scores && tokens && workspace && attempt_ids, "topk_sample: null pointer");
   YH_CHECK_ARG(B >= 0 && V > 0 && V <= 64LL * kSegLen, "topk_sample: V must lie in [1, %d]", 64 * kSegLen);
-  YH_CHECK_ARG(top_k >= 1 && top_k <= kMaxK && top_k <= V, "topk_sample: top_k must lie in [1, %d]", kMaxK);
   YH_CHECK_ARG(dtype == YH_F32 || dtype == YH_BF16 || dtype == YH_F16, "topk_sample: unsupported dtype");
+  if (top_k <= 0 || top_k > kMaxK) {
+    // the full-vocabulary branches of the torch sampler: no workspace
+    YH_CHECK_ARG(scores && tokens && attempt_ids, "topk_sample: null pointer");
+    YH_CHECK_ARG(mode == YH_SAMPLE_TORCH, "topk_sample: top_k outside [1, %d] needs the torch-sampler mode", kMaxK);
+    YH_CHECK_ARG(temperature > 0.f && top_p > 0.f && top_p <= 1.f,
+                 "topk_sample: needs temperature > 0 and 0 < top_p <= 1");
+    YH_CHECK_ARG(out_values == nullptr && out_indices == nullptr,
+                 "topk_sample: the selected top-k is returned only for top_k <= %d", kMaxK);
+    YH_CHECK_ARG(row_stride >= V && (seen == nullptr || seen_stride >= V), "topk_sample: bad row strides");
+    if (B == 0) return YH_OK;
+    FullArgs fa{scores, seen, attempt_ids, steps, tokens, row_stride, seen_stride, step, top_k, (int)V,
+                (top_k <= 0 && top_p == 1.f) ? 1 : 0, static_cast<uint32_t>(seed & 0xffffffffu),
+                static_cast<uint32_t>(stream_id & 0xffffffffu), penalty, temperature, top_p};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(B));
+    if (dtype == YH_F32) hipLaunchKernelGGL(sample_full_kernel<YH_F32>, grid, dim3(kFullThreads), 0, st, fa);
+    else if (dtype == YH_BF16) hipLaunchKernelGGL(sample_full_kernel<YH_BF16>, grid, dim3(kFullThreads), 0, st, fa);
+    else hipLaunchKernelGGL(sample_full_kernel<YH_F16>, grid, dim3(kFullThreads), 0, st, fa);
+    YH_CHECK_LAUNCH("sample_full");
+    return YH_OK;
+  }
+  YH_CHECK_ARG(scores && tokens && workspace && attempt_ids, "topk_sample: null pointer");
+  YH_CHECK_ARG(top_k <= V, "topk_sample: top_k exceeds the vocabulary");
   YH_CHECK_ARG(mode == YH_SAMPLE_FUSED || mode == YH_SAMPLE_TORCH, "topk_sample: unknown mode %d", mode);
   YH_CHECK_ARG(top_k == 1 || (temperature > 0.f && top_p > 0.f && top_p <= 1.f),
                "topk_sample: needs temperature > 0 and 0 < top_p <= 1");
@@ -459,8 +763,8 @@ extern "C" int yh_topk_sample_noalloc(const void* scores, int dtype, int64_t row
                                       float* out_values, int64_t* out_indices, int64_t B, int64_t V,
                                       yh_stream_t stream) {
   using namespace yh;
-  YH_CHECK_ARG(B >= 0 && V > 0 && top_k >= 1 && top_k <= kMaxK, "topk_sample_noalloc: bad sizes");
-  const int64_t need = yh_topk_workspace_bytes(B, V, top_k);
+  YH_CHECK_ARG(B >= 0 && V > 0, "topk_sample_noalloc: bad sizes");
+  const int64_t need = (top_k >= 1 && top_k <= kMaxK) ? yh_topk_workspace_bytes(B, V, top_k) : 0;
   YH_CHECK_ARG(need <= YH_TOPK_STATIC_SCRATCH_BYTES,
                "topk_sample_noalloc: B=%lld, V=%lld, top_k=%lld need %lld bytes of scratch, above the static "
                "maximum of %lld (use yh_topk_sample with a workspace)",

@@ -98,6 +98,12 @@ def _packed_or_batched(query, key, value, g, beta, cu_seqlens):
 _chunk_ws: dict = {}
 
 
+def _chunk_kernel_fits(query, value):
+    """The MFMA chunk kernels take K = 128, V in {64, 128} and bf16 q/k/v."""
+    return (query.ndim == 4 and value.ndim == 4 and query.shape[-1] == 128 and value.shape[-1] in (64, 128)
+            and query.dtype == torch.bfloat16)
+
+
 def _chunk_workspace(device, nbytes):
     """Per-device scratch of the chunk kernels, grown on demand."""
     key = device.index if device.index is not None else torch.cuda.current_device()
@@ -121,9 +127,11 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
     initial_state ``[N, HV, K, V]``.  ``initial_state`` is read, not modified;
     returns ``(o, final_state or None)``.
 
-    Packed inputs with K = 128, V in {64, 128} and bf16 q/k/v run the MFMA
-    chunk kernels (chunk 64); other shapes, or ``force_recurrent=True``, run
-    the token-recurrent kernel over each sequence.  ``lengths`` (host ints, one
+    Inputs with K = 128, V in {64, 128} and bf16 q/k/v run the MFMA chunk
+    kernels (chunk 64): packed ones as given, batched ones (the reference's
+    own call, T > 1) as B packed sequences of T tokens.  Other shapes, or
+    ``force_recurrent=True``, run the token-recurrent kernel over each
+    sequence.  ``lengths`` (host ints, one
     per sequence) lets the chunk kernels start the longest sequences first.
     The chunk kernels use a per-device workspace that is cached and grown on
     demand: concurrent calls on different streams of one device must not
@@ -132,6 +140,17 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
     if g is None or beta is None:
         raise ValueError("chunk_gated_delta_rule needs g and beta")
     cu = _packed_or_batched(query, key, value, g, beta, cu_seqlens)
+    if cu is None and _chunk_kernel_fits(query, value) and query.shape[1] > 1 and not force_recurrent:
+        # The reference's own call is batched ([B, T, ...], no cu_seqlens):
+        # B sequences of T tokens are B * T packed tokens at offsets i * T.
+        b, t = query.shape[:2]
+        cu_b = torch.arange(0, (b + 1) * t, t, dtype=torch.int32, device=query.device)
+        o, st = chunk_gated_delta_rule(
+            query.reshape(1, b * t, *query.shape[2:]), key.reshape(1, b * t, *key.shape[2:]),
+            value.reshape(1, b * t, *value.shape[2:]), g=g.reshape(1, b * t, -1), beta=beta.reshape(1, b * t, -1),
+            scale=scale, initial_state=initial_state, output_final_state=output_final_state,
+            use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel, cu_seqlens=cu_b)
+        return o.view(b, t, *o.shape[2:]), st
     if cu is None:
         o, st = recurrent_gated_delta_rule(query, key, value, g=g, beta=beta, initial_state=initial_state,
                                            output_final_state=True,
@@ -154,7 +173,7 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
     q, k, v, g_, be = (_contig(x) for x in (query, key, value, g, beta))
     o = torch.empty(1, total, hv, vd, device=dev, dtype=value.dtype)
     sc = float(kd ** -0.5 if scale is None else scale)
-    if kd == 128 and vd in (64, 128) and q.dtype == torch.bfloat16 and not force_recurrent:
+    if _chunk_kernel_fits(q, v) and not force_recurrent:
         h0 = None if initial_state is None else initial_state.contiguous()
         state = torch.empty(n, hv, kd, vd, device=dev, dtype=torch.float32)
         order = None

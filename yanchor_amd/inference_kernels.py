@@ -73,9 +73,13 @@ def topk_sample(scores, attempt_ids, steps, *, seed, temperature, top_k, top_p, 
     if scores.ndim != 2 or scores.stride(1) != 1:
         raise ValueError("sampling scores must have shape [batch, vocabulary] with unit column stride")
     b, v = scores.shape
-    if not 1 <= int(top_k) <= 64 or top_k > v:
-        raise ValueError("top_k must lie in [1, 64] and not exceed the vocabulary")
-    if int(top_k) != 1 and (temperature <= 0.0 or not 0.0 < top_p <= 1.0):
+    top_k = int(top_k)
+    full = top_k <= 0 or top_k > 64
+    if full and (mode != SAMPLE_TORCH or return_topk):
+        raise ValueError("top_k outside [1, 64] is the torch sampler's full-vocabulary branch (no top-k output)")
+    if 1 <= top_k <= 64 and top_k > v:
+        raise ValueError("top-k exceeds the vocabulary")
+    if top_k != 1 and (temperature <= 0.0 or not 0.0 < top_p <= 1.0):
         raise ValueError("invalid top-k/top-p sampling parameters")
     if attempt_ids.shape != (b,):
         raise ValueError("attempt ids must contain one id per row")
@@ -87,7 +91,7 @@ def topk_sample(scores, attempt_ids, steps, *, seed, temperature, top_k, top_p, 
         if seen.shape != scores.shape or seen.dtype != torch.bool or seen.stride(1) != 1:
             raise ValueError("dense presence state must be a boolean scores-shaped tensor")
         seen_ptr, seen_stride = seen.data_ptr(), seen.stride(0)
-    ws = topk_workspace(b, v, top_k, dev)
+    ws = None if full else topk_workspace(b, v, top_k, dev)
     tokens = torch.empty(b, 1, dtype=torch.int64, device=dev)
     vals = idxs = None
     if return_topk:
@@ -97,15 +101,18 @@ def topk_sample(scores, attempt_ids, steps, *, seed, temperature, top_k, top_p, 
            float(presence_penalty), ids.data_ptr(), N.ptr(st), step, int(seed) & 0xFFFFFFFF,
            int(stream) & 0xFFFFFFFF, float(temperature) if top_k != 1 else 1.0, int(top_k),
            float(top_p) if top_k != 1 else 1.0, int(mode), tokens.data_ptr(), N.ptr(vals), N.ptr(idxs),
-           ws.data_ptr(), ws.numel(), b, v, N.stream_of(scores))
+           N.ptr(ws), 0 if ws is None else ws.numel(), b, v, N.stream_of(scores))
     return (tokens, vals, idxs) if return_topk else tokens
 
 
 def sample_top_k_top_p_counter(scores, attempt_ids, steps, *, seed, temperature, top_k, top_p, stream=0):
-    """Torch-sampler semantics (inference_kernels.py:73-88) for 1 <= top_k <= 64.
-    The full-vocabulary branch (top_k <= 0 with top_p == 1) is not provided."""
-    if top_k <= 0:
-        raise NotImplementedError("the GPU sampler draws from the top-k (1 <= top_k <= 64)")
+    """Torch-sampler semantics (inference_kernels.py:73-88), every branch:
+    top_k <= 0 with top_p == 1 draws over the whole vocabulary in vocabulary
+    order; top_k == 1 is the argmax; otherwise the top k (the whole
+    vocabulary for top_k <= 0) truncated at top_p.  top_k > V is refused as
+    the reference refuses it (42-48)."""
+    if int(top_k) > scores.shape[-1]:
+        raise ValueError("top-k exceeds the vocabulary")
     return topk_sample(scores, attempt_ids, steps, seed=seed, temperature=temperature, top_k=top_k,
                        top_p=top_p, mode=SAMPLE_TORCH, stream=stream)
 

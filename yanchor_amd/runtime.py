@@ -207,9 +207,14 @@ class HipOps:
             return self.mem.sequence(q, key, value, scores, valid, chunk, state)
         return _token_by_token_sequence(self, q, key, value, scores, valid, chunk, state)
 
-    def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty):
-        return self.ik.sample_top20_counter(logits, attempt_ids, steps, seed=seed, temperature=temperature,
-                                            top_k=top_k, top_p=top_p, seen=seen, presence_penalty=penalty)
+    def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty,
+               backend="triton_top20"):
+        """One token per row with the presence penalty of ``seen`` fused in:
+        the fused top-k kernel's semantics ("triton_top20") or the torch
+        sampler's ("torch", any top_k)."""
+        mode = self.ik.SAMPLE_FUSED if backend == "triton_top20" else self.ik.SAMPLE_TORCH
+        return self.ik.topk_sample(logits, attempt_ids, steps, seed=seed, temperature=temperature, top_k=top_k,
+                                   top_p=top_p, mode=mode, seen=seen, presence_penalty=penalty)
 
     def bookkeeping(self, *args, **kw):
         self.ik._update_fixed_decode_state_(*args, **kw)
@@ -681,6 +686,36 @@ class Request:
     prompt: torch.Tensor
     cap: int
     arrival_step: int
+    row: int = -1                 # storage row, set at admission
+
+
+# The mechanical-repetition stop (reference runtime/scoring/protocols.py:73-76):
+# a tail of REPEAT_COUNT exact repeats of a period in [MIN, MAX] tokens.
+REPEAT_MIN_PERIOD, REPEAT_MAX_PERIOD, REPEAT_COUNT = 128, 256, 8
+
+
+def repetition_periods(tails, lengths, min_period=REPEAT_MIN_PERIOD, max_period=REPEAT_MAX_PERIOD,
+                       repeats=REPEAT_COUNT):
+    """For each row of ``tails`` [N, W] (a sequence's last W tokens, the
+    valid ones right-aligned: ``lengths`` [N] of them), the smallest period P
+    in [min_period, max_period] such that the last repeats * P valid tokens
+    are ``repeats`` copies of one P-token block, else 0
+    (mechanical_repetition_early_stop_patterns, runtime/scoring/protocols.py:
+    89-109)."""
+    import numpy as np
+    tails = np.asarray(tails)
+    lengths = np.minimum(np.asarray(lengths), tails.shape[1])
+    out = np.zeros(len(tails), dtype=np.int32)
+    top = min(max_period, tails.shape[1] // repeats)
+    for i in range(len(tails)):
+        for period in range(min_period, top + 1):
+            if lengths[i] < period * repeats:
+                break
+            block = tails[i, tails.shape[1] - period * repeats:].reshape(repeats, period)
+            if (block == block[-1]).all():
+                out[i] = period
+                break
+    return out
 
 
 @dataclass
@@ -721,8 +756,21 @@ class Engine:
 
     def __init__(self, model: Model, *, seed=20260923, temperature=0.6, top_k=20, top_p=0.95,
                  presence_penalty=1.5, poll_interval=32, max_rows=4096, max_new_tokens=8192, use_graph=True,
-                 tail_compaction=False, tail_compaction_live_fraction=0.5):
+                 tail_compaction=False, tail_compaction_live_fraction=0.5, eos_token_ids=(), pad_token_id=0,
+                 sampling_backend="triton_top20", mechanical=False):
+        """``sampling_backend``: "triton_top20" (the fused top-k kernel's
+        semantics) or "torch" (sample_top_k_top_p_counter's, every top_k);
+        ``eos_token_ids``: at most two ids that finish a sequence;
+        ``mechanical``: stop a sequence whose tail repeats mechanically
+        (checked at poll points, as the reference)."""
+        if len(eos_token_ids) > 2:
+            raise ValueError("the decode bookkeeping takes at most two EOS ids")
+        if sampling_backend not in ("triton_top20", "torch"):
+            raise ValueError("counter sampling backend must be torch or triton_top20")
         self.m, self.B, self.dev = model, model.B, model.device
+        self.eos, self.pad, self.sampling_backend = tuple(int(x) for x in eos_token_ids), int(pad_token_id), \
+            sampling_backend
+        self.mechanical = mechanical
         self.seed, self.temperature, self.top_k, self.top_p = seed, temperature, top_k, top_p
         self.penalty, self.poll_interval, self.use_graph = presence_penalty, poll_interval, use_graph
         self.tail_compaction, self.tail_fraction = tail_compaction, tail_compaction_live_fraction
@@ -740,6 +788,7 @@ class Engine:
         self.storage = torch.zeros(max_rows + B, max_new_tokens + 1, dtype=torch.int32, device=dev)
         self.generated = torch.zeros(max_rows + B, dtype=torch.long, device=dev)
         self.finished_by_eos = torch.zeros(max_rows + B, dtype=torch.bool, device=dev)
+        self.finished_by_repetition: set = set()      # storage rows stopped by the repetition check
         self.sink_rows = max_rows + torch.arange(B, device=dev)
         self.useful = torch.zeros((), dtype=torch.long, device=dev)
         self.graph = None
@@ -753,11 +802,11 @@ class Engine:
                                     finished=self.finished, slot_rows=self.slot_rows)
         tok = self.m.ops.sample(logits, self.attempt_ids, self.row_steps, self.dense_seen, seed=self.seed,
                                 temperature=self.temperature, top_k=self.top_k, top_p=self.top_p,
-                                penalty=self.penalty)
+                                penalty=self.penalty, backend=self.sampling_backend)
         self.m.ops.bookkeeping(tok, self.storage, self.dense_seen, self.generated, self.finished_by_eos,
                                self.finished, self.slot_rows, self.sink_rows, self.slot_caps, self.row_steps,
                                self.positions, self.decode_ids, self.useful,
-                               maximum_new_tokens=self.max_new, pad_token_id=0, eos_token_ids=())
+                               maximum_new_tokens=self.max_new, pad_token_id=self.pad, eos_token_ids=self.eos)
 
     def capture(self, live=False):
         """Warm up and capture the decode step.  The two eager warm-up steps
@@ -784,41 +833,84 @@ class Engine:
         else:
             self._step()
 
-    def admit(self, requests, targets):
-        """Prefill ``requests`` and place them in slots ``targets`` (host lists)."""
+    def admit(self, requests, targets, rows=None):
+        """Prefill ``requests`` and place them in slots ``targets`` (host
+        lists), their tokens in storage ``rows`` (default: the next free
+        rows).  Prompts of equal length are prefilled together.  Returns the
+        prefill seconds."""
         if not requests:
             return 0.0
         from . import inference_kernels as ik
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        prompts = torch.stack([r.prompt for r in requests]).to(self.dev)
-        logits, caches = self.m.prefill(prompts)
         n = len(requests)
-        ids = torch.tensor([r.attempt_id for r in requests], dtype=torch.long, device=self.dev)
-        first = self.m.ops.sample(logits, ids, 0, None, seed=self.seed, temperature=self.temperature,
-                                  top_k=self.top_k, top_p=self.top_p, penalty=0.0)
-        tgt = torch.tensor(targets, dtype=torch.long, device=self.dev)
-        ik.gather_rows(list(zip(caches, self.m.cache_tensors())), None, tgt, n)
-        rows = torch.arange(self.next_row, self.next_row + n, dtype=torch.long, device=self.dev)
-        self.next_row += n
-        caps = torch.tensor([r.cap for r in requests], dtype=torch.long, device=self.dev)
-        self.slot_rows.index_copy_(0, tgt, rows)
-        self.slot_caps.index_copy_(0, tgt, caps)
-        self.attempt_ids.index_copy_(0, tgt, ids)
-        self.row_steps.index_fill_(0, tgt, 1)
-        self.positions.index_fill_(0, tgt, prompts.shape[1])
-        done = caps <= 1
-        self.finished.index_copy_(0, tgt, done)
-        self.decode_ids.index_copy_(0, tgt, torch.where(done[:, None], torch.zeros_like(first), first))
-        self.dense_seen.index_fill_(0, tgt, False)
-        self.dense_seen[tgt, first[:, 0]] = True
-        self.storage[rows, 0] = first[:, 0].to(torch.int32)
-        self.generated[rows] = 1
-        for r, s in zip(requests, targets):
-            self.slot_request[s] = r
+        if rows is None:
+            rows = list(range(self.next_row, self.next_row + n))
+            self.next_row += n
+        if max(rows) >= self.max_rows:
+            raise ValueError(f"storage row {max(rows)} past the engine's {self.max_rows} rows")
+        groups: dict = {}
+        for j, r in enumerate(requests):
+            groups.setdefault(int(r.prompt.shape[0]), []).append(j)
+        for length, members in groups.items():
+            prompts = torch.stack([requests[j].prompt for j in members]).to(self.dev)
+            logits, caches = self.m.prefill(prompts)
+            ids = torch.tensor([requests[j].attempt_id for j in members], dtype=torch.long, device=self.dev)
+            first = self.m.ops.sample(logits, ids, 0, None, seed=self.seed, temperature=self.temperature,
+                                      top_k=self.top_k, top_p=self.top_p, penalty=0.0,
+                                      backend=self.sampling_backend)
+            tgt = torch.tensor([targets[j] for j in members], dtype=torch.long, device=self.dev)
+            ik.gather_rows(list(zip(caches, self.m.cache_tensors())), None, tgt, len(members))
+            del caches
+            rws = torch.tensor([rows[j] for j in members], dtype=torch.long, device=self.dev)
+            caps = torch.tensor([requests[j].cap for j in members], dtype=torch.long, device=self.dev)
+            is_eos = torch.zeros(len(members), dtype=torch.bool, device=self.dev)
+            for e in self.eos:
+                is_eos |= first[:, 0] == e
+            done = (caps <= 1) | is_eos
+            self.slot_rows.index_copy_(0, tgt, rws)
+            self.slot_caps.index_copy_(0, tgt, caps)
+            self.attempt_ids.index_copy_(0, tgt, ids)
+            self.row_steps.index_fill_(0, tgt, 1)
+            self.positions.index_fill_(0, tgt, length)
+            self.finished.index_copy_(0, tgt, done)
+            self.decode_ids.index_copy_(0, tgt, torch.where(done[:, None], torch.full_like(first, self.pad), first))
+            self.dense_seen.index_fill_(0, tgt, False)
+            self.dense_seen[tgt, first[:, 0]] = True
+            self.storage[rws, 0] = first[:, 0].to(torch.int32)
+            self.generated[rws] = 1
+            self.finished_by_eos[rws] = is_eos
+        for r, s_, w in zip(requests, targets, rows):
+            self.slot_request[s_] = r
+            r.row = w
+            self.finished_by_repetition.discard(w)
         self.row_request.extend(requests)
         torch.cuda.synchronize()
         return time.perf_counter() - t0
+
+    def check_repetition(self):
+        """The reference's mechanical-repetition stop at a poll point
+        (runtime/model/inference_kernels.py:1518-1539): live slots with at
+        least 8 x 128 tokens whose tail is 8 exact repeats of a period in
+        [128, 256] are finished.  Returns the number stopped (a host sync)."""
+        live = ((~self.finished) & (self.slot_rows >= 0) & (self.row_steps >= REPEAT_MIN_PERIOD * REPEAT_COUNT))
+        slots = torch.nonzero(live).flatten()
+        if not slots.numel():
+            return 0
+        rows = self.slot_rows[slots]
+        lengths = self.row_steps[slots]
+        width = REPEAT_MAX_PERIOD * REPEAT_COUNT
+        rel = torch.arange(-width, 0, device=self.dev)[None]
+        pos = lengths[:, None] + rel
+        tails = self.storage[rows[:, None], pos.clamp_min(0)].cpu().numpy()
+        periods = repetition_periods(tails, torch.clamp(lengths, max=width).cpu().numpy())
+        stop = [int(s_) for s_, p in zip(slots.tolist(), periods) if p]
+        for s_, p in zip(slots.tolist(), periods):
+            if p:
+                self.finished_by_repetition.add(int(self.slot_rows[s_]))
+        if stop:
+            self.finished[torch.tensor(stop, device=self.dev)] = True
+        return len(stop)
 
     def fill(self, queue):
         """Initial fill of the physical batch (runtime/model/inference_kernels.py:
@@ -852,6 +944,8 @@ class Engine:
         """Host sync: refill finished slots (ascending) from the queue; with
         tail compaction on and no more arrivals (``exhausted``), shrink the
         physical batch once few slots are live."""
+        if self.mechanical:
+            self.check_repetition()
         fin = self.finished.cpu().tolist()
         free = [s for s, f in enumerate(fin) if f]
         completed = sum(1 for s in free if self.slot_request[s] is not None)
