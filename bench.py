@@ -66,6 +66,8 @@ METRIC = "decode tokens/s at B=128 on 1 GPU; state-update HBM GB/s as % of peak"
 TRAFFIC_GDN_DECODE = {128: (133803.7 * 2.0 + 263283.8) * 1024}
 # The same for gdn_decode_fused_kernel (``--workload gdn_decode_fused``), by batch rows.
 TRAFFIC_GDN_FUSED = {128: (137924.0 * 2.0 + 272580.8) * 1024}
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this kernel at this shape, scaled by the "
+                  "copy-kernel factors (FETCH x 2.0, WRITE x 1.0); a constant, not measured in this run")
 # The same for one call of the chunked prefill (``--workload gdn_prefill``):
 # chunk_prep_kernel + chunk_scan_kernel, FETCH and WRITE KiB per dispatch summed.
 TRAFFIC_PREFILL = ((1544449.8 + 2551212.8) * 2.0 + (1268339.0 + 1341755.4)) * 1024
@@ -181,6 +183,7 @@ def gdn_fused_roofline(model, launches=216, warmup=27):
     achieved = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_GDN_FUSED.get(b),
+            "traffic_source": TRAFFIC_SOURCE if b in TRAFFIC_GDN_FUSED else None,
             "kernel": "gdn_decode_fused_kernel", "bytes_per_launch": nbytes, "avg_launch_us": ms * 1e3,
             "launches": launches,
             "shape": f"state fp32 [{b}, {hv}, {d}, {d}] + conv window bf16 [{b}, 3, {c.conv_dim}], "
