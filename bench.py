@@ -71,6 +71,8 @@ TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this kernel a
 # The same for one call of the chunked prefill (``--workload gdn_prefill``):
 # chunk_prep_kernel + chunk_scan_kernel, FETCH and WRITE KiB per dispatch summed.
 TRAFFIC_PREFILL = ((1544449.8 + 2551212.8) * 2.0 + (1268339.0 + 1341755.4)) * 1024
+# The same for one anchor read (``--workload anchor_read``, 64 x 32 x 256 x 128).
+TRAFFIC_ANCHOR_READ = (98017.4 * 2.0 + 512.0) * 1024
 
 
 def gdn_state_bytes(b, h, hv, kd, vd, qkv_size, gate_size, with_indices):
@@ -595,9 +597,12 @@ def bench_anchor_read(steps, warmup, cpu, batch=64):
         im.committed_gqa(q, states[i % n_states])
 
     ms_per_step, kernel_ms = _time_launches(step, steps, warmup)
-    # every slot's key and value row is read (dead slots are masked, not skipped),
-    # plus positions, the query and the output
-    nbytes = 2 * batch * g * cap * d * 2 + batch * g * cap * 4 + 2 * batch * g * d * 2
+    # algorithmic bytes: the key and value rows of the live slots (a dead
+    # slot's row enters neither the softmax nor the sum), every position, the
+    # query and the output; the mean over the rotating states
+    live = sum(int((st.positions >= 0).sum()) for st in states) / n_states
+    nbytes = int(2 * live * d * 2) + batch * g * cap * 4 + 2 * batch * g * d * 2
+    dense = 2 * batch * g * cap * d * 2 + batch * g * cap * 4 + 2 * batch * g * d * 2
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     del states
     return {"metric": "anchor-memory read per decode token (HBM GB/s)", "value": achieved, "unit": "GB/s",
@@ -606,8 +611,10 @@ def bench_anchor_read(steps, warmup, cpu, batch=64):
                                    "bf16, p_live 0.7, 3 rotating states", "global_batch": batch, "seq_len": 1,
                        "parallelism": "single GPU"},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "anchor_read_kernel",
-                         "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3}}
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC_ANCHOR_READ if batch == 64 else None,
+                         "traffic_source": TRAFFIC_SOURCE if batch == 64 else None, "kernel": "anchor_read_kernel",
+                         "bytes_per_launch": nbytes, "live_slot_fraction": live / (batch * g * cap),
+                         "dense_bytes_per_launch": dense, "avg_launch_us": kernel_ms * 1e3}}
 
 
 def bench_hbm_copy(steps, warmup, cpu, batch=None):

@@ -136,6 +136,31 @@ __device__ __forceinline__ void ld_block(Raw8<DT> (&r)[NI], const void* p) {
   }
 }
 
+// The NI rows of one block of a compacted live-slot list through a buffer
+// resource: row i of this lane is list entry e0 + i * RPI (slot lid[e], at
+// byte offset slot * D * esize + lane_byte_off); entries past n get an offset
+// past the resource's num_records, which the buffer load answers with zeros
+// and no memory request (no branch: the load stream and its wait counts are
+// those of a full block).
+constexpr int kDeadOffset = 0x7ffffff0;
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int DT, int NI, int D, int RPI>
+__device__ __forceinline__ void ld_block_list(Raw8<DT> (&r)[NI], __amdgpu_buffer_rsrc_t rsrc, const uint16_t* lid,
+                                              int e0, int n, int lane_byte_off) {
+  constexpr int kEsz = DT == YH_F32 ? 4 : 2;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int e = e0 + i * RPI;
+    const int o = e < n ? static_cast<int>(lid[e < n ? e : 0]) * D * kEsz + lane_byte_off : kDeadOffset;
+#pragma unroll
+    for (int j = 0; j < (DT == YH_F32 ? 2 : 1); ++j) {
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o + j * 16, 0, 0);
+      r[i].w[j] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ void zero_raw8(Raw8<DT>& r) {
 #pragma unroll
@@ -186,8 +211,31 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 // budget of two waves per SIMD.
 template <bool SINK, int R = 4> constexpr int read_waves() { return R == 1 ? 2 : 4; }
 
-template <int DT, int D, int R, bool SINK, int BS>
-__global__ void __launch_bounds__((read_waves<SINK, R>() * 64)) __attribute__((amdgpu_waves_per_eu(2, 2)))
+//
+// SKIP (anchor memories of at most 256 slots, one or two heads each): a wave fetches its first
+// block whole while every slot position of (b, g) arrives; then each wave
+// compacts the live slots past the waves' first blocks into a list in LDS
+// (ballot + popcount ranks) and the later steps take BS list entries at a
+// time (ld_block_list).  The read moves the live slots' bytes plus the dead
+// rows of the first blocks, and takes ceil(live / BS) list steps.
+constexpr int kSkipMaxCap = 256;
+
+// SKIP takes 16-slot blocks (kSkipBS) and a register budget of four waves
+// per SIMD: at 64 rows x 32 memories that keeps all 2048 two-wave workgroups
+// resident at once (8 per CU), each wave with 16 key and 16 value rows in
+// flight -- 39.7 us per read against 43.4 us for 32-slot blocks at two waves
+// per SIMD and 41.3 us at three.  Two heads per memory fit three waves per
+// SIMD without spilling.  fp32 rows (twice the registers) and reads without
+// SKIP: two waves per SIMD (each wave keeps a block of keys and one of values
+// in flight).
+constexpr int kSkipBS = 16;
+template <int DT, int R, bool SKIP> constexpr int read_occupancy() {
+  return SKIP && DT != YH_F32 ? (R == 1 ? 4 : 3) : 2;
+}
+
+template <int DT, int D, int R, bool SINK, int BS, bool SKIP>
+__global__ void __launch_bounds__((read_waves<SINK, R>() * 64))
+__attribute__((amdgpu_waves_per_eu(read_occupancy<DT, R, SKIP>(), read_occupancy<DT, R, SKIP>())))
 anchor_read_kernel(ReadArgs a) {
   constexpr int kReadWaves = read_waves<SINK, R>();
   constexpr int kReadThreads = kReadWaves * 64;
@@ -200,6 +248,7 @@ anchor_read_kernel(ReadArgs a) {
   __shared__ float wm[kReadWaves][R];
   __shared__ float wl[kReadWaves][R];
   __shared__ float accs[kReadWaves][R][D];
+  __shared__ uint16_t lidx[SKIP ? kReadWaves : 1][SKIP ? kSkipMaxCap : 1];
 
   const int bg = blockIdx.x;
   const int row = bg / a.G, g = bg % a.G;
@@ -245,99 +294,164 @@ anchor_read_kernel(ReadArgs a) {
   }
 
   const int nblk = a.KC / BS;
+  __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0x00020000), vrs = krs;
+  if constexpr (SKIP) {
+    const int bytes = a.KC * D * kEsz;
+    krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(a.keys) + (b * a.k_rs + static_cast<int64_t>(g) * a.KC * D) * kEsz),
+        0, bytes, 0x00020000);
+    vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(a.values) + (b * a.v_rs + static_cast<int64_t>(g) * a.KC * D) * kEsz),
+        0, bytes, 0x00020000);
+  }
+  const uint16_t* lid = lidx[SKIP ? wid : 0];
+  const int lane_off = s * 8 * kEsz;
   if (wid < nblk) {  // uniform over the wave
     Raw8<DT> kr[NI], vr[NI];
     // same issue order as the loop (positions, keys, values), so the wait
-    // counts derived at the loop head are those of the steady state
+    // counts derived at the loop head are those of the steady state; the
+    // first block is fetched whole
+    // SKIP: every position of (b, g) is requested first; the vector-memory
+    // counter is in order, so the ballots below wait for these loads only
+    int32_t pv[SKIP ? kSkipMaxCap / 64 : 1];
+    if constexpr (SKIP) {
+#pragma unroll
+      for (int c = 0; c < kSkipMaxCap / 64; ++c) {
+        const int slot = c * 64 + lane;
+        pv[c] = pos[slot < a.KC ? slot : 0] | (slot < a.KC ? 0 : int32_t(0x80000000));
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
     int32_t pcur = pos[wid * BS + (lane & (BS - 1))];
     ld_block<DT, NI, RPI * D>(kr, kptr + static_cast<int64_t>(wid * BS) * D * kEsz);
     __builtin_amdgcn_sched_barrier(0);
     ld_block<DT, NI, RPI * D>(vr, vptr + static_cast<int64_t>(wid * BS) * D * kEsz);
     __builtin_amdgcn_sched_barrier(0);
-    for (int blk = wid; blk < nblk; blk += kReadWaves) {
-      const int nxt = (blk + kReadWaves < nblk ? blk + kReadWaves : blk) * BS;  // past the end: this block again
-      const uint32_t live = static_cast<uint32_t>(__ballot(pcur >= 0));
+    // SKIP: the list of live slots past the waves' first blocks (slots below
+    // kReadWaves * BS are fetched whole)
+    int n_list = 0;
+    if constexpr (SKIP) {
+      const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;  // lanes under this one
+#pragma unroll
+      for (int c = 0; c < kSkipMaxCap / 64; ++c) {
+        const bool lv = pv[c] >= 0 && c * 64 + lane >= kReadWaves * BS;
+        const uint64_t m = __ballot(lv);
+        if (lv) lidx[wid][n_list + __popcll(m & below)] = static_cast<uint16_t>(c * 64 + lane);
+        n_list += __popcll(m);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    const int n_lblk = (n_list + BS - 1) / BS;
+    // one block step: logits of the rows in kr, the next keys (next_k), the
+    // online softmax and P.V of the rows in vr, the next values (next_v)
+    auto step_block = [&](Raw8<DT> (&kb)[NI], Raw8<DT> (&vb)[NI], uint32_t live, auto&& next_k,
+                          auto&& next_v) {
       float part[R][NI];
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        if constexpr (DT == YH_F32) {
-          float kf[8];
-          cvt8<DT>(kr[i], kf);
+        for (int i = 0; i < NI; ++i) {
+          if constexpr (DT == YH_F32) {
+            float kf[8];
+            cvt8<DT>(kb[i], kf);
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            float x = 0.f;
+            for (int r = 0; r < R; ++r) {
+              float x = 0.f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x = fmaf(qf[r][j], kf[j], x);
-            part[r][i] = x;
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < R; ++r) part[r][i] = dot8<DT>(qraw[r], kr[i]);
-        }
-      }
-      // the keys and positions of the next block (sched_barrier: issued here,
-      // not sunk to their use in the next iteration)
-      __builtin_amdgcn_sched_barrier(0);
-      pcur = pos[nxt + (lane & (BS - 1))];
-      ld_block<DT, NI, RPI * D>(kr, kptr + static_cast<int64_t>(nxt) * D * kEsz);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int m = LPR / 2, h = NI / 2; m >= 1; m >>= 1, h >>= 1) {
-        if (h >= 1) {
-          const bool up = (s & m) != 0;
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-#pragma unroll
-            for (int j = 0; j < h; ++j) {
-              const float send = up ? part[r][j] : part[r][j + h];
-              const float keep = up ? part[r][j + h] : part[r][j];
-              part[r][j] = keep + __shfl_xor(send, m, kWave);
+              for (int j = 0; j < 8; ++j) x = fmaf(qf[r][j], kf[j], x);
+              part[r][i] = x;
             }
+          } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) part[r][i] = dot8<DT>(qraw[r], kb[i]);
           }
-        } else {
-#pragma unroll
-          for (int r = 0; r < R; ++r) part[r][0] += __shfl_xor(part[r][0], m, kWave);
         }
-      }
-      // lane (s, rr) holds the logit of slot (s / F) * RPI + rr
-      const bool mine_live = (live >> ((s / F) * RPI + rr)) & 1u;
-      const bool counts = (s % F) == 0;  // one lane of the F copies enters the sum
-      float pw[R];
+      // the keys (and positions) of the next block (sched_barrier: issued
+      // here, not sunk to their use in the next step)
+      __builtin_amdgcn_sched_barrier(0);
+      next_k();
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float logit = mine_live ? (DT == YH_F32 ? part[r][0] : part[r][0] * a.scale) : -INFINITY;
-        const float bm = wave_max(logit);
-        const float m_new = fmaxf(m_run[r], bm);
-        const float m_safe = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = __expf(m_run[r] - m_safe);
-        const float p = __expf(logit - m_safe);
-        l_run[r] = l_run[r] * alpha + wave_sum(counts ? p : 0.f);
-        m_run[r] = m_new;
+        for (int m = LPR / 2, h = NI / 2; m >= 1; m >>= 1, h >>= 1) {
+          if (h >= 1) {
+            const bool up = (s & m) != 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
-        pw[r] = p;
-      }
-      // P.V: each value row is converted once and used for all R heads
+            for (int r = 0; r < R; ++r) {
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        float vf[8];
-        cvt8<DT>(vr[i], vf);
-        const bool vlive = (live >> (i * RPI + rr)) & 1u;
+              for (int j = 0; j < h; ++j) {
+                const float send = up ? part[r][j] : part[r][j + h];
+                const float keep = up ? part[r][j + h] : part[r][j];
+                part[r][j] = keep + __shfl_xor(send, m, kWave);
+              }
+            }
+          } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vf[j] = vlive ? vf[j] : 0.f;
+            for (int r = 0; r < R; ++r) part[r][0] += __shfl_xor(part[r][0], m, kWave);
+          }
+        }
+        // lane (s, rr) holds the logit of slot (s / F) * RPI + rr
+        const bool mine_live = (live >> ((s / F) * RPI + rr)) & 1u;
+        const bool counts = (s % F) == 0;  // one lane of the F copies enters the sum
+        float pw[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          // weight of the row this lane loaded at instruction i (slot i*RPI + rr)
-          const float w = __shfl(pw[r], rr * LPR + i * F, kWave);
+          const float logit = mine_live ? (DT == YH_F32 ? part[r][0] : part[r][0] * a.scale) : -INFINITY;
+          const float bm = wave_max(logit);
+          const float m_new = fmaxf(m_run[r], bm);
+          const float m_safe = m_new == -INFINITY ? 0.f : m_new;
+          const float alpha = __expf(m_run[r] - m_safe);
+          const float p = __expf(logit - m_safe);
+          l_run[r] = l_run[r] * alpha + wave_sum(counts ? p : 0.f);
+          m_run[r] = m_new;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(w, vf[j], acc[r][j]);
+          for (int j = 0; j < 8; ++j) acc[r][j] *= alpha;
+          pw[r] = p;
         }
-      }
+        // P.V: each value row is converted once and used for all R heads
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          float vf[8];
+          cvt8<DT>(vb[i], vf);
+          const bool vlive = (live >> (i * RPI + rr)) & 1u;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) vf[j] = vlive ? vf[j] : 0.f;
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            // weight of the row this lane loaded at instruction i (slot i*RPI + rr)
+            const float w = __shfl(pw[r], rr * LPR + i * F, kWave);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(w, vf[j], acc[r][j]);
+          }
+        }
       // the values of the next block
       __builtin_amdgcn_sched_barrier(0);
-      ld_block<DT, NI, RPI * D>(vr, vptr + static_cast<int64_t>(nxt) * D * kEsz);
+      next_v();
       __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (SKIP) {
+      uint32_t live = static_cast<uint32_t>(__ballot(pcur >= 0));  // the whole first block
+      for (int step = 0;; ++step) {  // step k >= 1 is list block wid + kReadWaves * (k - 1)
+        const int nb = wid + kReadWaves * step;  // the list block of the next step
+        const bool more = nb < n_lblk;
+        const int e_next = more ? nb * BS + rr : n_list;  // past the list: nothing is fetched
+        const int rem = n_list - nb * BS;
+        const uint32_t lnxt = !more ? 0u : rem >= 32 ? 0xffffffffu : (1u << rem) - 1u;
+        step_block(kr, vr, live, [&] { ld_block_list<DT, NI, D, RPI>(kr, krs, lid, e_next, n_list, lane_off); },
+                   [&] { ld_block_list<DT, NI, D, RPI>(vr, vrs, lid, e_next, n_list, lane_off); });
+        if (!more) break;
+        live = lnxt;
+      }
+    } else {
+      for (int blk = wid; blk < nblk; blk += kReadWaves) {
+        const int nxt = (blk + kReadWaves < nblk ? blk + kReadWaves : blk) * BS;  // past the end: this block again
+        const uint32_t live = static_cast<uint32_t>(__ballot(pcur >= 0));
+        step_block(kr, vr, live,
+                   [&] {
+                     pcur = pos[nxt + (lane & (BS - 1))];
+                     ld_block<DT, NI, RPI * D>(kr, kptr + static_cast<int64_t>(nxt) * D * kEsz);
+                   },
+                   [&] { ld_block<DT, NI, RPI * D>(vr, vptr + static_cast<int64_t>(nxt) * D * kEsz); });
+      }
     }
   }
 #pragma unroll
@@ -541,10 +655,15 @@ __global__ void anchor_advance_kernel(int64_t* count, int64_t* total, const uint
 template <int DT, int D, bool SINK, int BS>
 int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(read_waves<SINK>() * 64);
-  switch (R) {
-    case 1: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, BS>), grid, dim3(read_waves<SINK, 1>() * 64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, BS>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, BS>), grid, block, 0, st, a); break;
+  // anchor memories of up to 256 slots read by one or two heads fetch live
+  // rows only (four heads' state leaves no registers for the list step)
+  const bool skip = SINK && a.KC <= kSkipMaxCap && R <= 2;
+  switch (R * 2 + (skip ? 1 : 0)) {
+    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, BS, false>), grid, dim3(read_waves<SINK, 1>() * 64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, kSkipBS, SINK>), grid, dim3(read_waves<SINK, 1>() * 64), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, BS, false>), grid, block, 0, st, a); break;
+    case 5: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, kSkipBS, SINK>), grid, block, 0, st, a); break;
+    case 8: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, BS, false>), grid, block, 0, st, a); break;
     default: set_error("anchor_read: heads per group must be 1, 2 or 4 (got %d)", R); return YH_ERR_INVALID;
   }
   YH_CHECK_LAUNCH("anchor_read");
