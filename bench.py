@@ -68,9 +68,9 @@ TRAFFIC_GDN_DECODE = {128: (133803.7 * 2.0 + 263283.8) * 1024}
 TRAFFIC_GDN_FUSED = {128: (137924.0 * 2.0 + 272580.8) * 1024}
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this kernel at this shape, scaled by the "
                   "copy-kernel factors (FETCH x 2.0, WRITE x 1.0); a constant, not measured in this run")
-# The same for one call of the chunked prefill (``--workload gdn_prefill``):
-# chunk_prep_kernel + chunk_scan_kernel, FETCH and WRITE KiB per dispatch summed.
-TRAFFIC_PREFILL = ((1544449.8 + 2551212.8) * 2.0 + (1268339.0 + 1341755.4)) * 1024
+# The same for one call of the chunked prefill (``--workload gdn_prefill``,
+# chunk_fused_kernel).
+TRAFFIC_PREFILL = (2074500.0 * 2.0 + 1341740.0) * 1024
 # The same for one anchor read (``--workload anchor_read``, 64 x 32 x 256 x 128).
 TRAFFIC_ANCHOR_READ = (98017.4 * 2.0 + 512.0) * 1024
 
@@ -540,7 +540,7 @@ def bench_gdn_prefill(steps, warmup, cpu, batch=None):
                       "global_batch": len(lengths), "seq_len": tokens, "parallelism": "single GPU"},
            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": gbs / HBM_PEAK_GBS, "traffic": TRAFFIC_PREFILL,
-                        "kernel": "chunk_prep_kernel + chunk_scan_kernel",
+                        "traffic_source": TRAFFIC_SOURCE, "kernel": "chunk_fused_kernel",
                         "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3,
                         "mfma_tflops": tflops, "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
                         "mfma_util": tflops / MFMA_BF16_PEAK_TFLOPS, "flops_per_launch": flops,

@@ -121,10 +121,11 @@ int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* conv_state,
  *   final_state fp32 [n_seqs, HV, 128, V] (written)
  *   order NULL or int32 [n_seqs]: dispatch order of the sequences (longest
  *   first balances the grid); every sequence must appear once.
- *   workspace  device scratch of yh_gdn_chunk_workspace_bytes(total_tokens,
- *   n_seqs, HV, V) bytes, 16-byte aligned: the per-chunk quantities the
- *   state-independent pass hands to the sequential pass (about 16 KiB per
- *   chunk of 64 tokens and value head).  Calls sharing it must not overlap.
+ *   workspace, workspace_bytes: unused (may be NULL / 0); every per-chunk
+ *   quantity stays on chip.  yh_gdn_chunk_workspace_bytes returns 0.
+ *   One launch: a workgroup per (sequence, value head) prepares each chunk
+ *   (norms, decays, K K^T, Q K^T, the inverse of I + L) while it runs the
+ *   state-dependent products of the previous one.
  */
 int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, const void* g, const void* beta,
                         const float* initial_state, float* final_state, void* o, const int32_t* cu_seqlens,

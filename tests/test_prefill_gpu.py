@@ -50,8 +50,8 @@ def test_packed_zero_state_and_value_tiles(gpu):
 
 
 def test_packed_value_tiles_many_chunks(gpu):
-    """V = 64 (four-wave scan) over sequences of 1 to 5 chunks with GQA: the
-    scan's two LDS buffers alternate several times per sequence."""
+    """V = 64 (four-wave workgroups) over sequences of 1 to 5 chunks with GQA:
+    the kernel's two LDS buffers alternate several times per sequence."""
     x = workloads.packed_inputs([300, 129, 1, 64, 192], 2, 4, 128, 64, seed=11, h0_std=0.05)
     d = x.to(gpu)
     o, st = gdn.chunk_gated_delta_rule(d.q, d.k, d.v, g=d.g, beta=d.beta, initial_state=d.h0,

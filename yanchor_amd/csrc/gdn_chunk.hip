@@ -10,24 +10,14 @@
 //   S <- e^{G_last} S + K^T diag(e^{G_last - G}) v_new
 // with q, k L2-normalised (eps 1e-6 inside rsqrt) and q scaled.
 //
-// T and A = Q K^T o Gamma do not depend on the state S, so the work is split
-// in two kernels:
-//   chunk_prep_kernel   a persistent grid over the (chunk, value head) items
-//                       of all sequences: norms, decays, K K^T and Q K^T on
-//                       MFMA, the fp32 inverse T (block products on MFMA).
-//                       Writes the lower 16 x 16 blocks of T diag(beta) (bf16
-//                       hi + lo) and A (bf16, with the q / k scalings), and the
-//                       per-token scalings, to a workspace -- 15.8 KiB per
-//                       chunk and head.
-//   chunk_scan_kernel   one workgroup per (sequence, value head), walking the
-//                       sequence's chunks with the 128 x V fp32 state in MFMA
-//                       accumulators (wave w owns value columns 16w..16w+15):
-//                       Q S and W S, v_new, o, and the state update, with S
-//                       and v_new never leaving registers.  The chunk inputs
-//                       (which do not depend on S) are double-buffered in LDS:
-//                       chunk c + 1 is staged while chunk c computes, from
-//                       registers loaded during chunk c - 1; one barrier per
-//                       chunk.
+// T and A = Q K^T o Gamma do not depend on the state S.  One kernel,
+// chunk_fused_kernel, runs one workgroup per (sequence, value head) that walks
+// the sequence's chunks with the 128 x V fp32 state in MFMA accumulators (wave
+// w owns value columns 16w..16w+15) and prepares chunk j (norms, decays, K K^T
+// and Q K^T, the fp32 inverse T on MFMA block products, A, the scalings) while
+// it runs the state-dependent products of chunk j - 1 (Q S and W S, v_new, o,
+// the state update, with S and v_new never leaving registers).  Only q, k, v,
+// the gates, o and the states cross HBM.
 // Per-token L2 norms, beta and decays are diagonal factors, so products with
 // the raw q / k / v tensors take exact bf16 MFMA operands and the factors go
 // into the epilogues or the fp32 operand.  Products whose operands are fp32 on
@@ -45,21 +35,33 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kC = 64;        // chunk length
 constexpr int kK = 128;       // key dim
-constexpr int SKR = 136;      // bf16 row stride of 128-wide matrices (padded: conflict-free 16 B reads)
-constexpr int SK64 = 72;      // bf16 row stride of 64-wide matrices
 constexpr int SF = 68;        // fp32 row stride of 64-wide matrices
-constexpr int kScal = 196;    // per (chunk, head) scalars: orow[64], d2[64], ek[64], e^{G_last}, pad
-// T diag(beta) and A are lower triangular by 16 x 16 blocks: the workspace
-// holds only the 10 lower blocks (bi, bj), bj <= bi, block lblock(bi, bj),
-// each 16 x 16 row-major.
-constexpr int kLB = 10;
-constexpr int kLBElems = kLB * 256;
-__device__ __forceinline__ int lblock(int bi, int bj) { return bi * (bi + 1) / 2 + bj; }
+// Lower 16 x 16 tile q (0..9, row-major over the lower triangle) lies in row
+// block lblock_row(q).
 __device__ __forceinline__ int lblock_row(int q) { return (q >= 1) + (q >= 3) + (q >= 6); }
 
-__device__ __forceinline__ bf16x8_t lds8(const uint16_t* p) {
-  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
+// T diag(beta) and A are stored in LDS with their
+// columns permuted within each 32-column block so that the 8 reduction
+// indices of quad q for a 32-deep step -- columns 4q + 0..3 and 16 + 4q +
+// 0..3 -- sit next to each other: column c (c % 4 == 0) of block b is at
+// 32 b + 8 ((c / 4) % 4) + 4 ((c % 32) / 16).  One 16-byte read then gives a
+// lane its operand.
+__device__ __forceinline__ int pcol(int c) {
+  const int b = (c & 31) >> 2;
+  return (c & ~31) + 8 * (b & 3) + 4 * (b >> 2);
 }
+
+// LDS rows are unpadded; their 16-byte pieces are XOR-swizzled by row so that
+// every read pattern of the kernel is free of bank conflicts on gfx950's 64
+// banks (checked with the LDS bank-conflict counter on an in-bounds probe):
+//   Q,K,V 128 wide, plain, b64 row reads and transposed
+//         b64 reads:                                      piece p of row r at p ^ swz_kv(r)
+//   T,A   64 wide, columns permuted, b128 row reads:      piece p of row r at p ^ ((r / 2) % 8)
+// (A 16-byte row padding gives these reads 2- to 4-way conflicts.)
+__device__ __forceinline__ int swz_kv(int r) { return (2 * r + ((r >> 3) & 1)) & 15; }
+__device__ __forceinline__ int kvpos(int r, int p) { return r * 16 + ((p ^ swz_kv(r)) & 15); }
+__device__ __forceinline__ int tpos(int r, int p) { return r * 8 + ((p ^ (r >> 1)) & 7); }
+
 __device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) {
   return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
 }
@@ -86,90 +88,24 @@ __device__ __forceinline__ f32x4v mfma(bf16x8_t a, bf16x8_t b, f32x4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 // Workgroup barrier that waits only for LDS traffic (__syncthreads() also
-// drains every outstanding global load, which would empty the prefetch).
+// drains every outstanding vector memory operation).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// ---------------------------------------------------------------------------
-// Chunk table: chunk i of the packed batch starts at token table[4i], holds
-// table[4i+1] tokens and belongs to sequence table[4i+2]; sequence n owns
-// chunks [cstart[n], cstart[n+1]); cstart[n_seqs] is the chunk count.
-constexpr int kIdxThreads = 1024;
-__global__ void __launch_bounds__(kIdxThreads) chunk_index_kernel(const int32_t* cu, int n_seqs, int32_t* table,
-                                                                  int32_t* cstart, int nc_max) {
-  __shared__ int32_t wsum[kIdxThreads / 64];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  int32_t carry = 0;
-  for (int base = 0; base < n_seqs; base += kIdxThreads) {
-    const int i = base + threadIdx.x;
-    int32_t len = 0, cnt = 0;
-    if (i < n_seqs) {
-      len = max(cu[i + 1] - cu[i], 0);
-      cnt = (len + kC - 1) / kC;
-    }
-    int32_t incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int32_t y = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += y;
-    }
-    if (lane == 63) wsum[wid] = incl;
-    __syncthreads();
-    int32_t before = 0, all = 0;
-    for (int w = 0; w < kIdxThreads / 64; ++w) {
-      before += w < wid ? wsum[w] : 0;
-      all += wsum[w];
-    }
-    __syncthreads();
-    const int32_t first = carry + before + incl - cnt;
-    if (i < n_seqs) {
-      cstart[i] = first;
-      for (int j = 0; j < cnt && first + j < nc_max; ++j) {
-        int32_t* e = table + 4 * static_cast<int64_t>(first + j);
-        e[0] = cu[i] + j * kC;
-        e[1] = min(kC, len - j * kC);
-        e[2] = i;
-        e[3] = 0;
-      }
-    }
-    carry += all;
-  }
-  if (threadIdx.x == 0) cstart[n_seqs] = min(carry, nc_max);
+// s_waitcnt vmcnt(0) as a compiler builtin (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14 all zero, expcnt 7 and lgkmcnt 15 -- no wait on those).  The
+// compiler's wait pass sees it, so the state loads before the chunk loop count
+// as complete after it and the pass places no wait at the loop head.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// A gate element from the aligned 32-bit word that holds it (a 16-bit
+// element shares its word with a neighbour; the word never leaves the
+// element's page): the words are copied into LDS with the q / k rows and
+// converted where they are used.
+__device__ __forceinline__ float gate_value(uint32_t w, int64_t i, int dt) {
+  if (dt == YH_F32) return __uint_as_float(w);
+  const uint32_t h = (i & 1) ? (w >> 16) : (w & 0xffffu);
+  return dt == YH_BF16 ? __uint_as_float(h << 16) : f16_to_f32(static_cast<uint16_t>(h));
 }
-
-// ---------------------------------------------------------------------------
-struct PrepArgs {
-  const uint16_t* q;     // [total, H, K]
-  const uint16_t* k;
-  const void* g;         // [total, HV]
-  const void* beta;
-  const int32_t* table;
-  const int32_t* cstart;
-  uint16_t* thi;         // [nc, HV, kLBElems]  T diag(beta) (lower blocks), bf16 hi
-  uint16_t* tlo;         //                     bf16 lo
-  uint16_t* aqk;         // [nc, HV, kLBElems]  A (lower blocks)
-  float* scal;           // [nc, HV, kScal]
-  int n_seqs, H, HV;
-  float scale;
-  int l2, g_dt, beta_dt;
-};
-
-constexpr int kPrepThreads = 256;
-constexpr int kPrepGrid = 768;  // persistent prep workgroups: three per CU on 256 CUs
-
-struct __align__(16) PrepSmem {
-  union {
-    uint16_t kr[kC * SKR];  // K [t][d]          (K K^T, Q K^T)
-    float t[kC * SF];       // T = (I + L)^{-1}   (after the products)
-  } kt0;
-  union {
-    uint16_t q[kC * SKR];   // Q [t][d]          (Q K^T)
-    uint16_t out[kC * SK64];  // A staged for coalesced stores (after the inversion)
-  } qx;
-  float l[kC * SF];         // L
-  float rk[kC], rqs[kC], G[kC], beta[kC];
-  float G2[kC];             // G log2(e), for the decays exp2(G2_t - G2_s)
-  float gl;
-};
 
 // fp32 MFMA 16x16x4: lane l supplies A[l % 16][k] and B[k][l % 16] for the
 // reduction index k it is given; D is in the 16 x 16 accumulator layout (lane
@@ -195,377 +131,25 @@ __device__ __forceinline__ void put_block(float* t, int i, int j, const f32x4v& 
   for (int e = 0; e < 4; ++e) t[(16 * i + 4 * g + e) * SF + 16 * j + r] = -v[e];
 }
 
-// T = (I + L)^{-1} for strictly lower triangular L (64 x 64 fp32 in LDS), by
-// 16 x 16 blocks (the strictly upper blocks of T are left unwritten):
-//   diagonal blocks T_bb by column-parallel forward substitution (one lane per
-//   column, wave 0);
-//   T_10 = -T_11 L_10 T_00 and T_32 = -T_33 L_32 T_22 (waves 0, 1);
-//   the lower-left 32 x 32 block -B^{-1} C A^{-1} of the 2 x 2 block inverse,
-//   with Y = C A^{-1}:  T_20 = -T_22 Y_00, T_21 = -T_22 Y_01,
-//   T_30 = -(T_32 Y_00 + T_33 Y_10), T_31 = -(T_32 Y_01 + T_33 Y_11)
-//   (one wave each, Y recomputed where needed).
-// The block products run on fp32 MFMA.
-__device__ void invert_unit_lower(const float* l, float* t) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int r = lane & 15, g = lane >> 4;
-  if (w == 0) {
-    const int b = lane >> 4, j = lane & 15;
-    float xs[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float lr[16];
-      ld8f(&l[(16 * b + i) * SF + 16 * b], lr);
-      ld8f(&l[(16 * b + i) * SF + 16 * b + 8], lr + 8);
-      float acc = i == j ? 1.f : 0.f;
-#pragma unroll
-      for (int m = 0; m < i; ++m) acc = fmaf(-lr[m], xs[m], acc);
-      xs[i] = acc;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) t[(16 * b + i) * SF + 16 * b + j] = xs[i];
-  }
-  lds_barrier();
-  if (w < 2) {
-    const int i = w == 0 ? 1 : 3, j = i - 1;  // T_10, T_32
-    f32x4v x = {0.f, 0.f, 0.f, 0.f}, o = {0.f, 0.f, 0.f, 0.f};
-    acc_lt(x, l, t, i, j, j, r, g);
-    acc_tx(o, t, i, i, x, r, g);
-    put_block(t, i, j, o, r, g);
-  }
-  lds_barrier();
-  {
-    const int i = 2 + (w >> 1), j = w & 1;  // w: T_20, T_21, T_30, T_31
-    f32x4v y0 = {0.f, 0.f, 0.f, 0.f}, o = {0.f, 0.f, 0.f, 0.f};
-    // Y_0j = L_20 T_0j + L_21 T_1j (T_01 = 0)
-    if (j == 0) acc_lt(y0, l, t, 2, 0, 0, r, g);
-    acc_lt(y0, l, t, 2, 1, j, r, g);
-    if (i == 2) {
-      acc_tx(o, t, 2, 2, y0, r, g);
-    } else {
-      f32x4v y1 = {0.f, 0.f, 0.f, 0.f};  // Y_1j = L_30 T_0j + L_31 T_1j
-      if (j == 0) acc_lt(y1, l, t, 3, 0, 0, r, g);
-      acc_lt(y1, l, t, 3, 1, j, r, g);
-      acc_tx(o, t, 3, 2, y0, r, g);
-      acc_tx(o, t, 3, 3, y1, r, g);
-    }
-    put_block(t, i, j, o, r, g);
-  }
-  lds_barrier();
+typedef __attribute__((address_space(3))) void lds_void;
+// One copy instruction (16 or 4 bytes a lane) into LDS at `lds` (wave-uniform)
+// + 16 l (4 l).  Written as inline assembly: the compiler's wait insertion
+// treats a copy it can see as a write to every LDS byte and would make each
+// later LDS read of the other buffer wait for it; the code waits for the copy
+// itself (vmcnt, then a barrier) before any wave reads what it wrote.
+// The wait for those copies, as inline assembly too, so that the compiler
+// (which does not see the copies) cannot drop it.
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// (The LDS offset is the low half of the flat address of an LDS object.)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, int voff) {
+  const unsigned m0v = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
+               : "memory", "m0");
 }
-
-// Inputs of one (chunk, head) item, held in registers from their load (one
-// item ahead) to their move into LDS.
-struct PrepRegs {
-  uint4 k[4], q[4];
-  float g, b;
-};
-
-__device__ __forceinline__ void prep_load(PrepRegs& r, const PrepArgs& a, int item) {
-  const int chunk = item / a.HV, hv = item % a.HV;
-  const int64_t tok0 = a.table[4 * chunk];
-  const int Lc = a.table[4 * chunk + 1];
-  const int hk = hv / (a.HV / a.H);
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int ci = it * kPrepThreads + tid;
-    const int t = ci >> 4, d8 = (ci & 15) * 8;
-    const int64_t off = ((tok0 + t) * a.H + hk) * kK + d8;
-    r.k[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.k + off) : make_uint4(0, 0, 0, 0);
-    r.q[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.q + off) : make_uint4(0, 0, 0, 0);
-  }
-  r.g = tid < Lc ? load_any(a.g, (tok0 + tid) * a.HV + hv, a.g_dt) : 0.f;
-  r.b = tid < Lc ? load_any(a.beta, (tok0 + tid) * a.HV + hv, a.beta_dt) : 0.f;
-}
-
-// The 10 lower 16 x 16 tiles (mt, nt), nt <= mt, of K K^T and Q K^T, three
-// slots per wave: (mt << 4) | nt, or -1 for an empty slot.
-__device__ __forceinline__ int prep_tile(int w, int slot) {
-  constexpr int8_t kTiles[4][3] = {{0x00, 0x10, 0x33}, {0x11, 0x20, 0x32}, {0x21, 0x22, -1}, {0x30, 0x31, -1}};
-  return kTiles[w][slot];
-}
-
-// Persistent: workgroup b takes items b, b + gridDim.x, ... of the
-// (chunk, value head) list, item = chunk * HV + head, and loads the next
-// item's rows while it works on the current one (so every barrier inside
-// waits for LDS traffic only).
-__global__ void __launch_bounds__(kPrepThreads, 3) chunk_prep_kernel(PrepArgs a) {
-  __shared__ PrepSmem sm;
-  const int n_items = a.cstart[a.n_seqs] * a.HV;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r16 = lane & 15, kq = (lane >> 4) * 8, rq4 = (lane >> 4) * 4;
-  PrepRegs cur;
-  if (static_cast<int>(blockIdx.x) < n_items) prep_load(cur, a, blockIdx.x);
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int chunk = item / a.HV, hv = item % a.HV;
-    const int64_t ch = static_cast<int64_t>(chunk) * a.HV + hv;  // (chunk, head) record
-
-    // ---- stage K, Q rows (rows t >= Lc are zero) and the gates; prefetch the next item ----
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int ci = it * kPrepThreads + tid;
-      const int t = ci >> 4, d8 = (ci & 15) * 8;
-      *reinterpret_cast<uint4*>(&sm.kt0.kr[t * SKR + d8]) = cur.k[it];
-      *reinterpret_cast<uint4*>(&sm.qx.q[t * SKR + d8]) = cur.q[it];
-    }
-    if (tid < kC) {
-      sm.G[tid] = cur.g;
-      sm.beta[tid] = cur.b;
-    }
-    if (item + static_cast<int>(gridDim.x) < n_items) prep_load(cur, a, item + gridDim.x);
-    lds_barrier();
-
-    // ---- norms (4 lanes per token) and the decay scan, in the same phase as
-    // the products below ----
-    {  // norms: 4 lanes per token
-      const int t = tid >> 2, p = tid & 3;
-      float sk = 0.f, sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < 32; e += 8) {
-        const uint4 kv = *reinterpret_cast<const uint4*>(&sm.kt0.kr[t * SKR + 32 * p + e]);
-        const uint4 qv = *reinterpret_cast<const uint4*>(&sm.qx.q[t * SKR + 32 * p + e]);
-        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float k0 = __uint_as_float(kw[j] << 16), k1 = __uint_as_float(kw[j] & 0xffff0000u);
-          const float q0 = __uint_as_float(qw[j] << 16), q1 = __uint_as_float(qw[j] & 0xffff0000u);
-          sk = fmaf(k0, k0, fmaf(k1, k1, sk));
-          sq = fmaf(q0, q0, fmaf(q1, q1, sq));
-        }
-      }
-      sk += __shfl_xor(sk, 1, kWave);
-      sq += __shfl_xor(sq, 1, kWave);
-      sk += __shfl_xor(sk, 2, kWave);
-      sq += __shfl_xor(sq, 2, kWave);
-      if (p == 0) {
-        sm.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
-        sm.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-      }
-    }
-    if (w == 0) {
-      float x = sm.G[lane];
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const float y = __shfl_up(x, off, kWave);
-        if (lane >= off) x += y;
-      }
-      sm.G[lane] = x;
-      sm.G2[lane] = x * 1.4426950408889634f;
-      if (lane == kWave - 1) sm.gl = x;
-    }
-    // ---- K K^T and Q K^T on MFMA (lower tiles only); scaled after the barrier ----
-    f32x4v kk[3], qk[3];
-#pragma unroll
-    for (int slot = 0; slot < 3; ++slot) {
-      kk[slot] = qk[slot] = f32x4v{0.f, 0.f, 0.f, 0.f};
-      const int code = prep_tile(w, slot);
-      if (code < 0) continue;
-      const int m0 = 16 * (code >> 4), n0 = 16 * (code & 15);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int k0 = 32 * ks;
-        const bf16x8_t b = lds8(&sm.kt0.kr[(n0 + r16) * SKR + k0 + kq]);
-        kk[slot] = mfma(lds8(&sm.kt0.kr[(m0 + r16) * SKR + k0 + kq]), b, kk[slot]);
-        qk[slot] = mfma(lds8(&sm.qx.q[(m0 + r16) * SKR + k0 + kq]), b, qk[slot]);
-      }
-    }
-    lds_barrier();
-    if (tid < kC) {
-      const float eg = expf(sm.G[tid]);
-      float* sc = a.scal + ch * kScal;
-      sc[tid] = eg * sm.rqs[tid];                           // output row scale of Q S
-      sc[kC + tid] = sm.rk[tid] * expf(sm.gl - sm.G[tid]);  // state-update scale of v_new row t
-      sc[2 * kC + tid] = eg * sm.rk[tid];                   // row scale of K S inside W S
-      if (tid == 0) sc[3 * kC] = expf(sm.gl);
-    }
-
-    // ---- scale: L (strictly lower, to LDS) and A (registers) ----
-    float areg[3][4];
-#pragma unroll
-    for (int slot = 0; slot < 3; ++slot) {
-      const int code = prep_tile(w, slot);
-      if (code < 0) continue;
-      const int m0 = 16 * (code >> 4), n0 = 16 * (code & 15);
-      // rows t = m0 + rq4 + i (four consecutive), column s = n0 + r16
-      const int s = n0 + r16, t0 = m0 + rq4;
-      const float4 g2t = *reinterpret_cast<const float4*>(&sm.G2[t0]);
-      const float4 bt = *reinterpret_cast<const float4*>(&sm.beta[t0]);
-      const float4 rkt = *reinterpret_cast<const float4*>(&sm.rk[t0]);
-      const float4 rqt = *reinterpret_cast<const float4*>(&sm.rqs[t0]);
-      const float g2s = sm.G2[s], rks = sm.rk[s];
-      const float g2v[4] = {g2t.x, g2t.y, g2t.z, g2t.w}, bv[4] = {bt.x, bt.y, bt.z, bt.w};
-      const float rkv[4] = {rkt.x, rkt.y, rkt.z, rkt.w}, rqv[4] = {rqt.x, rqt.y, rqt.z, rqt.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t0 + i;
-        const float dec = s <= t ? exp2f(g2v[i] - g2s) : 0.f;
-        sm.l[t * SF + s] = s < t ? bv[i] * rkv[i] * rks * dec * kk[slot][i] : 0.f;
-        areg[slot][i] = s <= t ? rqv[i] * rks * dec * qk[slot][i] : 0.f;
-      }
-    }
-    lds_barrier();  // K and Q are dead from here on
-
-    invert_unit_lower(sm.l, sm.kt0.t);  // ends with a barrier
-
-    // ---- T diag(beta) (hi / lo) straight to the workspace's lower blocks
-    // (8-byte pieces); A through LDS for 16-byte stores ----
-    uint16_t* thi_g = a.thi + ch * kLBElems;
-    uint16_t* tlo_g = a.tlo + ch * kLBElems;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {  // T rows: 64 x 64, 16 elements per thread
-      const int e = (it * kPrepThreads + tid) * 4;
-      const int t = e >> 6, s4 = e & 63;
-      if ((s4 >> 4) > (t >> 4)) continue;  // strictly upper block: not stored
-      const int off = lblock(t >> 4, s4 >> 4) * 256 + (t & 15) * 16 + (s4 & 15);
-      const float4 tv = *reinterpret_cast<const float4*>(&sm.kt0.t[t * SF + s4]);
-      const float4 bv = *reinterpret_cast<const float4*>(&sm.beta[s4]);
-      const float x[4] = {tv.x * bv.x, tv.y * bv.y, tv.z * bv.z, tv.w * bv.w};
-      uint16_t h[4], lo[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        h[j] = f32_to_bf16(x[j]);
-        lo[j] = f32_to_bf16(x[j] - bfv(h[j]));
-      }
-      *reinterpret_cast<uint2*>(thi_g + off) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-      *reinterpret_cast<uint2*>(tlo_g + off) = make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
-    }
-    uint16_t* a_s = sm.qx.out;
-#pragma unroll
-    for (int slot = 0; slot < 3; ++slot) {
-      const int code = prep_tile(w, slot);
-      if (code < 0) continue;
-      const int m0 = 16 * (code >> 4), n0 = 16 * (code & 15);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a_s[(m0 + rq4 + i) * SK64 + n0 + r16] = f32_to_bf16(areg[slot][i]);
-    }
-    lds_barrier();
-    uint16_t* a_g = a.aqk + ch * kLBElems;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int ci = it * kPrepThreads + tid;  // 512 vectors of 8, the lower blocks' stored
-      const int t = ci >> 3, s8 = (ci & 7) * 8;
-      if ((s8 >> 4) <= (t >> 4))
-        *reinterpret_cast<uint4*>(a_g + lblock(t >> 4, s8 >> 4) * 256 + (t & 15) * 16 + (s8 & 15)) =
-            *reinterpret_cast<const uint4*>(&a_s[t * SK64 + s8]);
-    }
-    lds_barrier();  // the next item restages K and Q over T and the A staging
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Sequential pass.  The state is partitioned by value column: wave w holds the
-// full 128 x 16 column block S[:, 16w .. 16w+15] as eight 16 x 16 accumulator
-// tiles, so every product that consumes S, K S or v_new takes it as the B
-// operand straight from the wave's own registers.  The MFMA reduction index
-// of a 32-deep step is visited in the order the accumulator layout provides:
-// element j of quad q is row 32 ks + 4 q + j (j < 4) or 32 ks + 16 + 4 q +
-// j - 4 (j >= 4), and the A operands are read in that same order: rows of
-// Q, K, T diag(beta) and A from column-permuted LDS rows (one 16-byte read),
-// K^T and V^T by transposing reads of the row-major K and V.  Only the
-// chunk inputs go through LDS: two barriers per chunk.
-struct ScanArgs {
-  const uint16_t* q;     // [total, H, K]
-  const uint16_t* k;
-  const uint16_t* v;     // [total, HV, V]
-  const uint16_t* thi;
-  const uint16_t* tlo;
-  const uint16_t* aqk;
-  const float* scal;
-  const int32_t* cu;     // [N + 1]
-  const int32_t* cstart;
-  const int32_t* order;  // [N] or null
-  const float* h0;       // [N, HV, K, V] or null
-  float* ht;             // [N, HV, K, V]
-  uint16_t* o;           // [total, HV, V]
-  int n_seqs, H, HV;
-};
-
-template <int NW>
-struct __align__(16) ScanSmem {
-  uint16_t q[kC * SKR];        // Q [t][d]
-  uint16_t k[kC * SKR];        // K [t][d]  (K^T operands by transposing reads)
-  uint16_t v[kC * SKR];        // V [t][v]  (V^T operands by transposing reads)
-  uint16_t thi[kC * SK64];     // T diag(beta) [t][s], hi
-  uint16_t tlo[kC * SK64];     // lo
-  uint16_t aqk[kC * SK64];     // A [t][s]
-  float orow[kC], d2[kC], ek[kC];
-  float egl;
-};
-
-// Inputs of one chunk that do not depend on the state, held in registers
-// between their load and their move to LDS.  NW waves.
-template <int NW>
-struct ChunkRegs {
-  static constexpr int NT = NW * 64;
-  static constexpr int kRow = kC * kK / 8 / NT;        // 16-byte vectors per thread of a 64 x 128 matrix
-  static constexpr int kVec = kC * 16 * NW / 8 / NT;   // ... of the 64 x V value rows (= 2)
-  static constexpr int kSq = (kLB * 32 + NT - 1) / NT;  // ... of the lower blocks of a 64 x 64 matrix
-  static constexpr int kSc = (3 * kC + 1 + NT - 1) / NT;
-  uint4 q[kRow], k[kRow], v[kVec];
-  uint4 thi[kSq], tlo[kSq], aqk[kSq];
-  float scal[kSc];
-};
-
-// chunk `chunk` of a sequence starting at token `tok0` (its j-th chunk) holds
-// tokens tok0 .. tok0 + Lc - 1
-template <int NW>
-__device__ __forceinline__ void load_chunk(ChunkRegs<NW>& r, const ScanArgs& a, int chunk, int64_t tok0, int Lc,
-                                           int hv, int hk) {
-  using R = ChunkRegs<NW>;
-  constexpr int NT = R::NT, V = 16 * NW;
-  const int tid = threadIdx.x;
-  const int64_t ch = static_cast<int64_t>(chunk) * a.HV + hv;
-  // Row-major pieces: 16 lanes per 128-wide token row (2 NW per V-wide row),
-  // so a wave instruction covers whole lines.
-#pragma unroll
-  for (int it = 0; it < R::kRow; ++it) {
-    const int ci = it * NT + tid, t = ci >> 4;
-    const int64_t off = ((tok0 + t) * a.H + hk) * kK + (ci & 15) * 8;
-    r.q[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.q + off) : make_uint4(0, 0, 0, 0);
-    r.k[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.k + off) : make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int it = 0; it < R::kVec; ++it) {
-    const int ci = it * NT + tid, t = ci / (2 * NW);
-    r.v[it] = t < Lc ? *reinterpret_cast<const uint4*>(a.v + ((tok0 + t) * a.HV + hv) * V + (ci % (2 * NW)) * 8)
-                     : make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int it = 0; it < R::kSq; ++it) {
-    const int ci = it * NT + tid;
-    const bool in = ci < kLB * 32;
-    const int64_t off = ch * kLBElems + ci * 8;
-    r.thi[it] = in ? *reinterpret_cast<const uint4*>(a.thi + off) : make_uint4(0, 0, 0, 0);
-    r.tlo[it] = in ? *reinterpret_cast<const uint4*>(a.tlo + off) : make_uint4(0, 0, 0, 0);
-    r.aqk[it] = in ? *reinterpret_cast<const uint4*>(a.aqk + off) : make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int it = 0; it < R::kSc; ++it) {
-    const int ci = it * NT + tid;
-    r.scal[it] = ci < 3 * kC + 1 ? a.scal[ch * kScal + ci] : 0.f;
-  }
-}
-
-// A-operand matrices (Q, K, T diag(beta), A) are stored in LDS with their
-// columns permuted within each 32-column block so that the 8 reduction
-// indices of quad q for a 32-deep step -- columns 4q + 0..3 and 16 + 4q +
-// 0..3 -- sit next to each other: column c (c % 4 == 0) of block b is at
-// 32 b + 8 ((c / 4) % 4) + 4 ((c % 32) / 16).  One 16-byte read then gives a
-// lane its operand.
-__device__ __forceinline__ int pcol(int c) {
-  const int b = (c & 31) >> 2;
-  return (c & ~31) + 8 * (b & 3) + 4 * (b >> 2);
-}
-// Store 8 consecutive columns c8 .. c8 + 7 (c8 % 8 == 0) of a row.
-__device__ __forceinline__ void put8p(uint16_t* row, int c8, uint4 x) {
-  *reinterpret_cast<uint2*>(row + pcol(c8)) = make_uint2(x.x, x.y);
-  *reinterpret_cast<uint2*>(row + pcol(c8 + 4)) = make_uint2(x.z, x.w);
-}
-// The operand of quad `quad` for the 32-deep step starting at column k0 of a
-// column-permuted row.
-__device__ __forceinline__ bf16x8_t lds8r(const uint16_t* row, int k0, int quad) {
-  return lds8(row + k0 + 8 * quad);
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, const void* lds, int voff) {
+  const unsigned m0v = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
+               : "memory", "m0");
 }
 // The B operand of a 32-deep step from two accumulator tiles (rows 32 ks ..
 // 32 ks + 15 and 32 ks + 16 .. 32 ks + 31), as bf16 hi / lo.
@@ -573,118 +157,274 @@ __device__ __forceinline__ void pack_b(const f32x4v& t0, const f32x4v& t1, bf16x
   const float x[8] = {t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
   split8(x, hi, lo);
 }
-// Operand of a 32-deep step whose reduction index is the ROW of a row-major
-// LDS matrix m (row stride SKR): lane (i = lane % 16, quad) gets column
+// The A operand of quad `quad` for the 32-deep step ks of row r: one b128
+// read of a column-permuted row (T / A at tpos) ...
+__device__ __forceinline__ bf16x8_t lds_t(const uint4* m, int r, int ks, int quad) {
+  return __builtin_bit_cast(bf16x8_t, m[tpos(r, 4 * ks + quad)]);
+}
+// ... or two b64 reads of a plain row (Q, K at kvpos): columns 32 ks + 4 quad +
+// 0..3 and 32 ks + 16 + 4 quad + 0..3.
+__device__ __forceinline__ bf16x8_t lds_k(const uint4* m, int r, int ks, int quad) {
+  const uint2 lo = reinterpret_cast<const uint2*>(&m[kvpos(r, 4 * ks + (quad >> 1))])[quad & 1];
+  const uint2 hi = reinterpret_cast<const uint2*>(&m[kvpos(r, 4 * ks + 2 + (quad >> 1))])[quad & 1];
+  return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+// Operand of a 32-deep step whose reduction index is the ROW of a plain
+// LDS matrix m (K or V at kvpos): lane (i = lane % 16, quad) gets column
 // c0 + i at rows k0 + 4 quad + 0..3 and k0 + 16 + 4 quad + 0..3 -- the
 // permuted reduction order above -- by two ds_read_b64_tr_b16.  That
 // instruction transposes within each 16-lane group: lane 4m + e receives, in
 // slot j, element e of the 8 bytes addressed by lane 4j + m.  So lane
 // 4j + m of the group addresses row k0 (+16) + 4 quad + j, columns
-// c0 + 4m .. c0 + 4m + 3.
+// c0 + 4m .. c0 + 4m + 3 (half m % 2 of piece c0 / 8 + m / 2).
 typedef short s16x4v __attribute__((ext_vector_type(4)));
 typedef short s16x8v __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4v lds_s16x4v;
-template <bool PERM>  // m's columns permuted (pcol) or plain
-__device__ __forceinline__ bf16x8_t lds8t(const uint16_t* m, int k0, int c0, int lane) {
-  const int i = lane & 15, quad = lane >> 4;
-  const int c = c0 + 4 * (i & 3);
-  const uint16_t* p = m + (k0 + 4 * quad + (i >> 2)) * SKR + (PERM ? pcol(c) : c);
-  const s16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p));
-  const s16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p + 16 * SKR));
+__device__ __forceinline__ bf16x8_t lds8t(const uint4* m, int k0, int c0, int lane) {
+  const int i = lane & 15, quad = lane >> 4, mm = i & 3;
+  const int r = k0 + 4 * quad + (i >> 2), pc = (c0 >> 3) + (mm >> 1);
+  const uint2* p0 = reinterpret_cast<const uint2*>(&m[kvpos(r, pc)]) + (mm & 1);
+  const uint2* p1 = reinterpret_cast<const uint2*>(&m[kvpos(r + 16, pc)]) + (mm & 1);
+  const s16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p0));
+  const s16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p1));
   return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// One chunk's inputs from registers to an LDS buffer (A operands with
-// permuted columns, V row-major, the per-token scalings).
+// ---------------------------------------------------------------------------
+// chunk_fused_kernel.  Iteration j prepares chunk j in LDS buffer Y from the
+// q / k rows already there, and runs the state-dependent products of chunk
+// j - 1 from buffer X:
+//   P0  copy v (j) into Y (its rows held the previous iteration's T)
+//   P1  L2 norms, decay cumsum, K K^T / Q K^T of j      | Q S, K S of j - 1
+//   P2  L (fp32, over Y's T rows), A, scalings of j     | v_new of j - 1
+//   P3a the inverse's diagonal blocks (wave 0), T fp32
+//       over X's V rows (dead since P2)                 | state update of j - 1
+//   P3b its first off-diagonal level (waves 0, 1)       | output of j - 1
+//   P3c its second level (waves 0..3)                   | output stores of j - 1,
+//                                                         then copy q, k, gates of j + 1 into X
+//   P4  T diag(beta) as bf16 hi / lo into Y's T rows; wait for the copies
+// Six barriers per chunk.  Copies go through the buffer units straight into
+// LDS (dma16 / dma4), in the swizzled layouts.
+struct FusedArgs {
+  const uint16_t* q;     // [total, H, K]
+  const uint16_t* k;
+  const uint16_t* v;     // [total, HV, V]
+  const void* g;         // [total, HV]
+  const void* beta;
+  const int32_t* cu;     // [N + 1]
+  const int32_t* order;  // [N] or null
+  const float* h0;       // [N, HV, K, V] or null
+  float* ht;             // [N, HV, K, V]
+  uint16_t* o;           // [total, HV, V]
+  int n_seqs, H, HV;
+  float scale;
+  int l2, g_dt, beta_dt;
+};
+
+struct __align__(16) FBuf {
+  uint4 q[kC * 16];  // Q [t][d] at kvpos
+  uint4 k[kC * 16];  // K [t][d] at kvpos
+  union {
+    uint4 v[kC * 16];  // V [t][v] at kvpos
+    float t[kC * SF];  // T (fp32) of the chunk prepared while this one is scanned
+  } vt;
+  union {
+    struct {
+      uint4 hi[kC * 8];  // T diag(beta) [t][s], bf16 hi, at tpos
+      uint4 lo[kC * 8];  // lo
+    } p;
+    float l[kC * SF];    // L (fp32) while this chunk is prepared
+  } tt;
+  uint4 aqk[kC * 8];     // A [t][s] at tpos
+  float scal[4 * kC];    // orow [0, 64), d2 [64, 128), ek [128, 192), e^{G_last} [192]
+  uint32_t gw[2 * kC];   // the words holding g [0, 64) and beta [64, 128) of each token
+};
+struct __align__(16) FPrep {
+  float rk[kC], rqs[kC], G[kC], G2[kC], beta[kC];
+  float gl;
+};
+static_assert(2 * sizeof(FBuf) + sizeof(FPrep) <= 160 * 1024, "fused chunk LDS");
+
+// q, k and the gate words of chunk (tok0, Lc) into b: rows past Lc arrive as
+// zeros (q, k) or as a copy of the last row's words (gates, masked on use).
 template <int NW>
-__device__ __forceinline__ void stage_chunk(ScanSmem<NW>& sm, const ChunkRegs<NW>& cur) {
-  using R = ChunkRegs<NW>;
-  constexpr int NT = NW * 64;
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void fdma_qkg(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hv, int hk) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qs = a.H * kK;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.q + (tok0 * a.H + hk) * kK), 0, ((Lc - 1) * qs + kK) * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.k + (tok0 * a.H + hk) * kK), 0, ((Lc - 1) * qs + kK) * 2, 0x00020000);
 #pragma unroll
-  for (int it = 0; it < R::kRow; ++it) {
-    const int ci = it * NT + tid, o = (ci >> 4) * SKR, c8 = (ci & 15) * 8;
-    put8p(&sm.q[o], c8, cur.q[it]);
-    put8p(&sm.k[o], c8, cur.k[it]);
+  for (int bl = w; bl < 16; bl += NW) {
+    const int row = 4 * bl + (lane >> 4), lp = ((lane & 15) ^ swz_kv(row)) & 15;
+    const int oq = (row * qs + lp * 8) * 2;
+    dma16(rq, &b.q[64 * bl], oq);
+    dma16(rk, &b.k[64 * bl], oq);
   }
-#pragma unroll
-  for (int it = 0; it < R::kVec; ++it) {
-    const int ci = it * NT + tid;
-    *reinterpret_cast<uint4*>(&sm.v[(ci / (2 * NW)) * SKR + (ci % (2 * NW)) * 8]) = cur.v[it];
+  if (w < 2) {  // wave 0: g, wave 1: beta
+    const void* src = w == 0 ? a.g : a.beta;
+    const int dt = w == 0 ? a.g_dt : a.beta_dt;
+    const int64_t i = (tok0 + (lane < Lc ? lane : Lc - 1)) * a.HV + hv;
+    const int off = static_cast<int>(dt == YH_F32 ? i * 4 : (i * 2) & ~static_cast<int64_t>(3));
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(src), 0, 0x7fffffff,
+                                                                        0x00020000);
+    dma4(rg, &b.gw[64 * w], off);
   }
+}
+template <int NW>
+__device__ __forceinline__ void fdma_v(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hv) {
+  constexpr int V = 16 * NW;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int vs = a.HV * V;
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.v + (tok0 * a.HV + hv) * V), 0, ((Lc - 1) * vs + V) * 2, 0x00020000);
 #pragma unroll
-  for (int it = 0; it < R::kSq; ++it) {
-    const int ci = it * NT + tid;
-    if (ci < kLB * 32) {  // vector ci: block q = ci / 32, row (ci % 32) / 2, half ci % 2
-      const int q = ci >> 5, bi = lblock_row(q), bj = q - bi * (bi + 1) / 2;
-      const int o = (16 * bi + ((ci & 31) >> 1)) * SK64, c8 = 16 * bj + 8 * (ci & 1);
-      put8p(&sm.thi[o], c8, cur.thi[it]);
-      put8p(&sm.tlo[o], c8, cur.tlo[it]);
-      put8p(&sm.aqk[o], c8, cur.aqk[it]);
-    }
-  }
-#pragma unroll
-  for (int it = 0; it < R::kSc; ++it) {
-    const int ci = it * NT + tid;
-    if (ci < kC) sm.orow[ci] = cur.scal[it];
-    else if (ci < 2 * kC) sm.d2[ci - kC] = cur.scal[it];
-    else if (ci < 3 * kC) sm.ek[ci - 2 * kC] = cur.scal[it];
-    else if (ci == 3 * kC) sm.egl = cur.scal[it];
+  for (int bl = w; bl < 16; bl += NW) {
+    const int row = 4 * bl + (lane >> 4), lp = ((lane & 15) ^ swz_kv(row)) & 15;
+    const int ov = lp * 8 < V ? (row * vs + lp * 8) * 2 : 0x7ffffff0;  // pieces past V: zeros
+    dma16(rv, &b.vt.v[64 * bl], ov);
   }
 }
 
-// Two LDS buffers: chunk c computes from one while chunk c + 1 (loaded into
-// registers during chunk c - 1) is staged into the other, so one barrier per
-// chunk separates them.
+// T = (I + L)^{-1} for strictly lower triangular L (64 x 64 fp32 in LDS, row
+// stride SF), by 16 x 16 blocks, in three barrier-free pieces so that the
+// state-dependent products fill the phases between them (the strictly upper
+// blocks of T are left unwritten):
+//   inv_diag    diagonal blocks T_bb by column-parallel forward substitution
+//               (one lane per column, one wave);
+//   inv_level1  T_10 = -T_11 L_10 T_00 and T_32 = -T_33 L_32 T_22;
+//   inv_level2  the lower-left 32 x 32 block -B^{-1} C A^{-1} of the 2 x 2
+//               block inverse, with Y = C A^{-1}: T_20 = -T_22 Y_00,
+//               T_21 = -T_22 Y_01, T_30 = -(T_32 Y_00 + T_33 Y_10),
+//               T_31 = -(T_32 Y_01 + T_33 Y_11) (one wave each, Y recomputed
+//               where needed).
+// The block products run on fp32 MFMA.
+__device__ __forceinline__ void inv_diag(const float* l, float* t) {  // one wave
+  const int lane = threadIdx.x & 63;
+  const int b = lane >> 4, j = lane & 15;
+  float xs[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float lr[16];
+    ld8f(&l[(16 * b + i) * SF + 16 * b], lr);
+    ld8f(&l[(16 * b + i) * SF + 16 * b + 8], lr + 8);
+    float acc = i == j ? 1.f : 0.f;
+#pragma unroll
+    for (int m = 0; m < i; ++m) acc = fmaf(-lr[m], xs[m], acc);
+    xs[i] = acc;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t[(16 * b + i) * SF + 16 * b + j] = xs[i];
+}
+__device__ __forceinline__ void inv_level1(const float* l, float* t, int u) {  // u = 0, 1: T_10, T_32
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int i = u == 0 ? 1 : 3, j = i - 1;
+  f32x4v x = {0.f, 0.f, 0.f, 0.f}, o = {0.f, 0.f, 0.f, 0.f};
+  acc_lt(x, l, t, i, j, j, r, g);
+  acc_tx(o, t, i, i, x, r, g);
+  put_block(t, i, j, o, r, g);
+}
+__device__ __forceinline__ void inv_level2(const float* l, float* t, int u) {  // u = 0..3: T_20, T_21, T_30, T_31
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int i = 2 + (u >> 1), j = u & 1;
+  f32x4v y0 = {0.f, 0.f, 0.f, 0.f}, o = {0.f, 0.f, 0.f, 0.f};
+  if (j == 0) acc_lt(y0, l, t, 2, 0, 0, r, g);
+  acc_lt(y0, l, t, 2, 1, j, r, g);
+  if (i == 2) {
+    acc_tx(o, t, 2, 2, y0, r, g);
+  } else {
+    f32x4v y1 = {0.f, 0.f, 0.f, 0.f};
+    if (j == 0) acc_lt(y1, l, t, 3, 0, 0, r, g);
+    acc_lt(y1, l, t, 3, 1, j, r, g);
+    acc_tx(o, t, 3, 2, y0, r, g);
+    acc_tx(o, t, 3, 3, y1, r, g);
+  }
+  put_block(t, i, j, o, r, g);
+}
+
 template <int NW>
-__global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
-  using R = ChunkRegs<NW>;
-  __shared__ ScanSmem<NW> smb[2];
-  constexpr int V = 16 * NW;
-  constexpr int NT = NW * 64;
-  const int hv = blockIdx.x % a.HV;
-  const int sidx = blockIdx.x / a.HV;
-  const int n = a.order ? a.order[sidx] : sidx;
-  const int hk = hv / (a.HV / a.H);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+__device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
+                                           FPrep& pp, f32x4v (&S)[8], int j, int nch, int64_t seq0, int seqlen,
+                                           int hv, int hk) {
+  FBuf& Y = *Yp;
+  FBuf& X = *Xp;
+  constexpr int V = 16 * NW, NT = NW * 64;
+  constexpr int kTPW = (10 + NW - 1) / NW;  // K K^T / Q K^T tiles per wave
+  // The lane index is re-derived opaquely in every iteration: the swizzled LDS
+  // offsets then are computed where they are used rather than hoisted out of
+  // the chunk loop, where they would outnumber the registers.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, quad = lane >> 4, rq4 = quad * 4;
-  const int cs = a.cstart[n], ce = a.cstart[n + 1];
-  const int64_t seq0 = a.cu[n];
-  const int seqlen = a.cu[n + 1] - a.cu[n];
-  const int vcol = 16 * w + r16;  // this lane's value column
+  const int vcol = 16 * w + r16;
+  const bool prep = j < nch, scan = j > 0;  // uniform
+  const int64_t tokp = seq0 + static_cast<int64_t>(j) * kC, toks = tokp - kC;
+  const int Lp = min(kC, seqlen - j * kC), Ls = min(kC, seqlen - (j - 1) * kC);
 
-  // S[dt][i] = S[16 dt + 4 quad + i][vcol]
-  f32x4v S[8];
-  const int64_t sbase = (static_cast<int64_t>(n) * a.HV + hv) * kK;
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + 16 * dt + rq4 + i) * V + vcol] : 0.f;
+  // ---- P0: v of chunk j ----
+  if (prep) fdma_v<NW>(Y, a, tokp, Lp, hv);
 
-  // The upper blocks of T diag(beta) and A are zero and never staged: clear
-  // them once in both buffers (disjoint from every staged element).
-  for (int e = tid; e < 2 * 6 * 32; e += NT) {
-    const int buf = e / 192, u = (e % 192) >> 5, v = e & 31;  // upper block u: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
-    const int bi = u < 3 ? 0 : (u < 5 ? 1 : 2), bj = u < 3 ? u + 1 : (u < 5 ? u - 1 : 3);
-    const int o = (16 * bi + (v >> 1)) * SK64, c8 = 16 * bj + 8 * (v & 1);
-    put8p(&smb[buf].thi[o], c8, make_uint4(0, 0, 0, 0));
-    put8p(&smb[buf].tlo[o], c8, make_uint4(0, 0, 0, 0));
-    put8p(&smb[buf].aqk[o], c8, make_uint4(0, 0, 0, 0));
+  // ---- P1: norms, decays, K K^T, Q K^T of j | Q S, K S of j - 1 ----
+  f32x4v kk[kTPW], qk[kTPW];
+  if (prep) {
+    {  // L2 norms: LPT lanes per token, each over 16 / LPT pieces of its row
+      constexpr int LPT = NT / kC, PPL = 16 / LPT;
+      const int t = tid / LPT, p0 = (tid % LPT) * PPL;
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < PPL; ++e) {
+        const uint4 kv = Y.k[kvpos(t, p0 + e)], qv = Y.q[kvpos(t, p0 + e)];
+        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float k0 = __uint_as_float(kw[i] << 16), k1 = __uint_as_float(kw[i] & 0xffff0000u);
+          const float q0 = __uint_as_float(qw[i] << 16), q1 = __uint_as_float(qw[i] & 0xffff0000u);
+          sk = fmaf(k0, k0, fmaf(k1, k1, sk));
+          sq = fmaf(q0, q0, fmaf(q1, q1, sq));
+        }
+      }
+#pragma unroll
+      for (int m = 1; m < LPT; m <<= 1) {
+        sk += __shfl_xor(sk, m, kWave);
+        sq += __shfl_xor(sq, m, kWave);
+      }
+      if (tid % LPT == 0) {
+        pp.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
+        pp.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
+      }
+    }
+    if (w == NW - 1) {  // decay cumsum (a wave without inverse work); lane t holds token t's gates
+      const int64_t gi = (tokp + (lane < Lp ? lane : Lp - 1)) * a.HV + hv;
+      float x = lane < Lp ? gate_value(Y.gw[lane], gi, a.g_dt) : 0.f;
+      const float bt = lane < Lp ? gate_value(Y.gw[kC + lane], gi, a.beta_dt) : 0.f;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const float y = __shfl_up(x, off, kWave);
+        if (lane >= off) x += y;
+      }
+      pp.G[lane] = x;
+      pp.G2[lane] = x * 1.4426950408889634f;
+      pp.beta[lane] = bt;
+      if (lane == kWave - 1) pp.gl = x;
+    }
+#pragma unroll
+    for (int slot = 0; slot < kTPW; ++slot) {  // the extra tiles go to waves without inverse work
+      kk[slot] = qk[slot] = f32x4v{0.f, 0.f, 0.f, 0.f};
+      const int ti = (w + 2) % NW + slot * NW;
+      if (ti >= 10) continue;
+      const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8_t b = lds_k(Y.k, n0 + r16, ks, quad);
+        kk[slot] = mfma(lds_k(Y.k, m0 + r16, ks, quad), b, kk[slot]);
+        qk[slot] = mfma(lds_k(Y.q, m0 + r16, ks, quad), b, qk[slot]);
+      }
+    }
   }
-  R cur;
-  if (cs < ce) {
-    load_chunk<NW>(cur, a, cs, seq0, min(kC, seqlen), hv, hk);
-    stage_chunk<NW>(smb[0], cur);
-    if (cs + 1 < ce) load_chunk<NW>(cur, a, cs + 1, seq0 + kC, min(kC, seqlen - kC), hv, hk);
-    lds_barrier();
-  }
-  for (int c = cs; c < ce; ++c) {
-    const int j = c - cs;
-    const int64_t tok0 = seq0 + static_cast<int64_t>(j) * kC;
-    const int Lc = min(kC, seqlen - j * kC);
-    ScanSmem<NW>& sm = smb[j & 1];
-    // ---- Q S (1 pass) and P = K S (2 passes), four row tiles of this column block ----
-    f32x4v qs[4], ps[4];
+  f32x4v qs[4], ps[4];
+  if (scan) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) qs[mt] = ps[mt] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -693,43 +433,72 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       pack_b(S[2 * ks], S[2 * ks + 1], bh, bl);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const int row = (16 * mt + r16) * SKR;
-        const bf16x8_t aq = lds8r(&sm.q[row], 32 * ks, quad);
-        const bf16x8_t ak = lds8r(&sm.k[row], 32 * ks, quad);
+        const bf16x8_t aq = lds_k(X.q, 16 * mt + r16, ks, quad);
+        const bf16x8_t ak = lds_k(X.k, 16 * mt + r16, ks, quad);
         qs[mt] = mfma(aq, bh, qs[mt]);
         ps[mt] = mfma(ak, bh, ps[mt]);
         ps[mt] = mfma(ak, bl, ps[mt]);
       }
     }
-    // Stage chunk c + 1 into the other buffer and prefetch chunk c + 2 while
-    // the products above drain.
-    if (c + 1 < ce) {
-      stage_chunk<NW>(smb[(j & 1) ^ 1], cur);
-      if (c + 2 < ce) load_chunk<NW>(cur, a, c + 2, tok0 + 2 * kC, min(kC, seqlen - (j + 2) * kC), hv, hk);
+  }
+  lds_barrier();
+
+  // ---- P2: L, A and the scalings of j | v_new of j - 1 ----
+  if (prep) {
+    if (tid < kC) {
+      const float eg = expf(pp.G[tid]);
+      Y.scal[tid] = eg * pp.rqs[tid];                          // output row scale of Q S
+      Y.scal[kC + tid] = pp.rk[tid] * expf(pp.gl - pp.G[tid]);  // state-update scale of v_new row t
+      Y.scal[2 * kC + tid] = eg * pp.rk[tid];                  // row scale of K S inside W S
+      if (tid == 0) Y.scal[3 * kC] = expf(pp.gl);
     }
-    // ---- v_new = T diag(beta) V - T diag(beta) (diag(e^G rk) P): 2 + 3 passes, T lower triangular ----
+#pragma unroll
+    for (int slot = 0; slot < kTPW; ++slot) {
+      const int ti = (w + 2) % NW + slot * NW;
+      if (ti >= 10) continue;
+      const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
+      // rows t = m0 + rq4 + i (four consecutive), column s = n0 + r16
+      const int s = n0 + r16, t0 = m0 + rq4;
+      const float4 g2t = *reinterpret_cast<const float4*>(&pp.G2[t0]);
+      const float4 bt = *reinterpret_cast<const float4*>(&pp.beta[t0]);
+      const float4 rkt = *reinterpret_cast<const float4*>(&pp.rk[t0]);
+      const float4 rqt = *reinterpret_cast<const float4*>(&pp.rqs[t0]);
+      const float g2s = pp.G2[s], rks = pp.rk[s];
+      const float g2v[4] = {g2t.x, g2t.y, g2t.z, g2t.w}, bv[4] = {bt.x, bt.y, bt.z, bt.w};
+      const float rkv[4] = {rkt.x, rkt.y, rkt.z, rkt.w}, rqv[4] = {rqt.x, rqt.y, rqt.z, rqt.w};
+      const int sp = pcol(s & ~3) + (s & 3);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + i;
+        const float dec = s <= t ? exp2f(g2v[i] - g2s) : 0.f;
+        Y.tt.l[t * SF + s] = s < t ? bv[i] * rkv[i] * rks * dec * kk[slot][i] : 0.f;
+        reinterpret_cast<uint16_t*>(&Y.aqk[tpos(t, sp >> 3)])[sp & 7] =
+            f32_to_bf16(s <= t ? rqv[i] * rks * dec * qk[slot][i] : 0.f);
+      }
+    }
+  }
+  f32x4v vn[4];
+  if (scan) {
     bf16x8_t vb[2], ph[2], pl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      vb[ks] = lds8t<false>(sm.v, 32 * ks, 16 * w, lane);
+      vb[ks] = lds8t(X.vt.v, 32 * ks, 16 * w, lane);
       f32x4v p0 = ps[2 * ks], p1 = ps[2 * ks + 1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p0[i] *= sm.ek[32 * ks + rq4 + i];
-        p1[i] *= sm.ek[32 * ks + 16 + rq4 + i];
+        p0[i] *= X.scal[2 * kC + 32 * ks + rq4 + i];
+        p1[i] *= X.scal[2 * kC + 32 * ks + 16 + rq4 + i];
       }
       pack_b(p0, p1, ph[ks], pl[ks]);
     }
-    f32x4v vn[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       f32x4v u = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         if (32 * ks <= 16 * mt + 15) {
-          const int row = (16 * mt + r16) * SK64;
-          const bf16x8_t th = lds8r(&sm.thi[row], 32 * ks, quad);
-          const bf16x8_t tl = lds8r(&sm.tlo[row], 32 * ks, quad);
+          const bf16x8_t th = lds_t(X.tt.p.hi, 16 * mt + r16, ks, quad);
+          const bf16x8_t tl = lds_t(X.tt.p.lo, 16 * mt + r16, ks, quad);
           u = mfma(th, vb[ks], u);
           u = mfma(tl, vb[ks], u);
           y = mfma(th, ph[ks], y);
@@ -739,32 +508,42 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
       }
       vn[mt] = u - y;
     }
-    // ---- S <- e^{G_last} S + K^T diag(d2) v_new (2 passes); issued before the
-    // output, which the next chunk does not wait for ----
+  }
+  lds_barrier();
+
+  // ---- P3a: state update of j - 1 | the inverse's diagonal blocks of j ----
+  float* tf = X.vt.t;  // T of chunk j over X's V rows (dead since P2)
+  if (scan) {
     bf16x8_t zh[2], zl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       f32x4v z0 = vn[2 * ks], z1 = vn[2 * ks + 1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        z0[i] *= sm.d2[32 * ks + rq4 + i];
-        z1[i] *= sm.d2[32 * ks + 16 + rq4 + i];
+        z0[i] *= X.scal[kC + 32 * ks + rq4 + i];
+        z1[i] *= X.scal[kC + 32 * ks + 16 + rq4 + i];
       }
       pack_b(z0, z1, zh[ks], zl[ks]);
     }
-    const float egl = sm.egl;
+    const float egl = X.scal[3 * kC];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      f32x4v s = S[dt] * egl;
+      f32x4v sv = S[dt] * egl;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8_t ak = lds8t<true>(sm.k, 32 * ks, 16 * dt, lane);
-        s = mfma(ak, zh[ks], s);
-        s = mfma(ak, zl[ks], s);
+        const bf16x8_t ak = lds8t(X.k, 32 * ks, 16 * dt, lane);
+        sv = mfma(ak, zh[ks], sv);
+        sv = mfma(ak, zl[ks], sv);
       }
-      S[dt] = s;
+      S[dt] = sv;
     }
-    // ---- o = diag(orow) Q S + A v_new (A lower triangular, 1 pass) ----
+  }
+  if (prep && w == 0) inv_diag(Y.tt.l, tf);
+  lds_barrier();
+
+  // ---- P3b: output of j - 1 | the inverse's first level of j ----
+  uint32_t ow[8];
+  if (scan) {
     bf16x8_t vnb[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -772,66 +551,136 @@ __global__ void __launch_bounds__(NW * 64) chunk_scan_kernel(ScanArgs a) {
                           vn[2 * ks + 1][0], vn[2 * ks + 1][1], vn[2 * ks + 1][2], vn[2 * ks + 1][3]};
       vnb[ks] = round8v(x);
     }
+    const bool odd = r16 & 1;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       f32x4v acc = qs[mt];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= sm.orow[16 * mt + rq4 + i];
+      for (int i = 0; i < 4; ++i) acc[i] *= X.scal[16 * mt + rq4 + i];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        if (32 * ks <= 16 * mt + 15) acc = mfma(lds8r(&sm.aqk[(16 * mt + r16) * SK64], 32 * ks, quad), vnb[ks], acc);
-      // Column pairs (vcol, vcol ^ 1) go out as 4-byte stores: the even lane
-      // stores rows 0, 1 of its quad, the odd lane rows 2, 3.
-      const bool odd = r16 & 1;
+        if (32 * ks <= 16 * mt + 15) acc = mfma(lds_t(X.aqk, 16 * mt + r16, ks, quad), vnb[ks], acc);
+      // Column pairs (vcol, vcol ^ 1) go out as 4-byte words: the even lane
+      // holds rows 0, 1 of its quad, the odd lane rows 2, 3.
       const float y0 = __shfl_xor(odd ? acc[0] : acc[2], 1, kWave);
       const float y1 = __shfl_xor(odd ? acc[1] : acc[3], 1, kWave);
       const float2 p0 = odd ? make_float2(y0, acc[2]) : make_float2(acc[0], y0);
       const float2 p1 = odd ? make_float2(y1, acc[3]) : make_float2(acc[1], y1);
-      const int t0 = 16 * mt + rq4 + (odd ? 2 : 0), c0 = vcol & ~1;
-      uint32_t* o0 = reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0) * a.HV + hv) * V + c0);
-      uint32_t* o1 = reinterpret_cast<uint32_t*>(a.o + ((tok0 + t0 + 1) * a.HV + hv) * V + c0);
-      const uint32_t w0 = pack2(f32_to_bf16(p0.x), f32_to_bf16(p0.y)), w1 = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
-      if (Lc == kC) {  // uniform: every chunk but a sequence's last
-        *o0 = w0;
-        *o1 = w1;
+      ow[2 * mt] = pack2(f32_to_bf16(p0.x), f32_to_bf16(p0.y));
+      ow[2 * mt + 1] = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
+    }
+  }
+  if (prep && w < 2) inv_level1(Y.tt.l, tf, w);
+  lds_barrier();
+
+  // ---- P3c: output stores of j - 1, then q, k and gate words of j + 1 into X
+  // (read there for the last time) | the inverse's second level of j ----
+  if (scan) {
+    const int rodd = (r16 & 1) ? 2 : 0, c0 = vcol & ~1;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int t0 = 16 * mt + rq4 + rodd;
+      uint32_t* o0 = reinterpret_cast<uint32_t*>(a.o + ((toks + t0) * a.HV + hv) * V + c0);
+      uint32_t* o1 = reinterpret_cast<uint32_t*>(a.o + ((toks + t0 + 1) * a.HV + hv) * V + c0);
+      if (Ls == kC) {  // uniform: every chunk but a sequence's last
+        *o0 = ow[2 * mt];
+        *o1 = ow[2 * mt + 1];
       } else {
-        if (t0 < Lc) *o0 = w0;
-        if (t0 + 1 < Lc) *o1 = w1;
+        if (t0 < Ls) *o0 = ow[2 * mt];
+        if (t0 + 1 < Ls) *o1 = ow[2 * mt + 1];
       }
     }
-    lds_barrier();  // chunk c + 1's buffer is complete; chunk c's may be restaged
   }
+  if (j + 1 < nch) fdma_qkg<NW>(X, a, tokp + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
+  if (prep && w < 4) inv_level2(Y.tt.l, tf, w);
+  lds_barrier();
+
+  // ---- P4: T diag(beta) of j as hi / lo over L (dead) ----
+  if (prep) {
+    constexpr int kTv = kC * kC / 4 / NT;  // float4 pieces of T per thread
+#pragma unroll
+    for (int it = 0; it < kTv; ++it) {
+      const int e = (it * NT + tid) * 4, t = e >> 6, s4 = e & 63;
+      const int bi = t >> 4, bj = s4 >> 4;
+      const bool keep = bj <= bi;                                      // lower block
+      const bool zero = (bi == 0 && bj == 1) || (bi == 2 && bj == 3);  // read as zeros by the products
+      if (keep || zero) {
+        const float4 x = *reinterpret_cast<const float4*>(&tf[t * SF + s4]);
+        const float4 bv = *reinterpret_cast<const float4*>(&pp.beta[s4]);
+        const float tv[4] = {x.x * bv.x, x.y * bv.y, x.z * bv.z, x.w * bv.w};
+        uint16_t h[4], lo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float y = keep ? tv[i] : 0.f;
+          h[i] = f32_to_bf16(y);
+          lo[i] = f32_to_bf16(y - bfv(h[i]));
+        }
+        const int pc = pcol(s4);
+        reinterpret_cast<uint2*>(&Y.tt.p.hi[tpos(t, pc >> 3)])[(pc >> 2) & 1] =
+            make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+        reinterpret_cast<uint2*>(&Y.tt.p.lo[tpos(t, pc >> 3)])[(pc >> 2) & 1] =
+            make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
+      }
+    }
+  }
+  dma_wait();     // the copies into Y (v of j) and X (q, k, gates of j + 1) have landed
+  lds_barrier();  // chunk j is ready; X may be reused as chunk j + 1's buffer
+}
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
+  __shared__ FBuf bufs[2];
+  __shared__ FPrep pp;
+  constexpr int V = 16 * NW, NT = NW * 64;
+  const int hv = blockIdx.x % a.HV;
+  const int sidx = blockIdx.x / a.HV;
+  const int n = a.order ? a.order[sidx] : sidx;
+  const int hk = hv / (a.HV / a.H);
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, rq4 = (lane >> 4) * 4;
+  const int64_t seq0 = a.cu[n];
+  const int seqlen = a.cu[n + 1] - a.cu[n];
+  const int nch = (seqlen + kC - 1) / kC;
+  const int vcol = 16 * w + r16;
+  // S[dt][i] = S[16 dt + 4 quad + i][vcol]
+  f32x4v S[8];
+  const int64_t sbase = (static_cast<int64_t>(n) * a.HV + hv) * kK;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + 16 * dt + rq4 + i) * V + vcol] : 0.f;
+  wait_vmem();  // the state has arrived before the loop
+  // A's halves in the upper blocks (0, 1) and (2, 3) are read as zeros and
+  // nothing else writes them: clear them once in both buffers
+  for (int e = tid; e < 2 * 32 * 4; e += NT) {  // buffer, row (0..15 or 32..47), piece 0..3
+    const int bsel = e >> 7, rr = (e >> 2) & 31, pc = e & 3;
+    const int t = rr < 16 ? rr : 16 + rr, p = t < 16 ? pc : 4 + pc;
+    reinterpret_cast<uint2*>(&bufs[bsel].aqk[tpos(t, p)])[1] = make_uint2(0, 0);
+  }
+  if (nch > 0) {
+    fdma_qkg<NW>(bufs[0], a, seq0, min(kC, seqlen), hv, hk);
+    dma_wait();
+  }
+  lds_barrier();
+  // (one loop body for both parities: its LDS addresses are the buffer's base
+  // plus per-lane offsets computed once)
+#pragma unroll 1
+  for (int j = 0; j <= nch; ++j) fused_iter<NW>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, S, j, nch, seq0, seqlen, hv, hk);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) a.ht[(sbase + 16 * dt + rq4 + i) * V + vcol] = S[dt][i];
 }
 
-int64_t chunk_bound(int64_t total, int64_t n_seqs) { return total / kC + n_seqs; }
-
-struct WsLayout {
-  int64_t table, cstart, thi, tlo, aqk, scal, bytes;
-};
-WsLayout ws_layout(int64_t total, int64_t n_seqs, int64_t HV) {
-  const int64_t nc = chunk_bound(total, n_seqs);
-  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
-  WsLayout l;
-  l.table = 0;
-  l.cstart = up(nc * 16);
-  l.thi = up(l.cstart + (n_seqs + 1) * 4);
-  l.tlo = l.thi + up(nc * HV * kLBElems * 2);
-  l.aqk = l.tlo + up(nc * HV * kLBElems * 2);
-  l.scal = l.aqk + up(nc * HV * kLBElems * 2);
-  l.bytes = l.scal + up(nc * HV * kScal * 4);
-  return l;
-}
-
 }  // namespace
 }  // namespace yh
 
 extern "C" int64_t yh_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t n_seqs, int64_t HV, int64_t V) {
-  if (total_tokens < 0 || n_seqs < 0 || HV <= 0 || V <= 0) return 0;
-  return yh::ws_layout(total_tokens, n_seqs, HV).bytes;
+  (void)total_tokens;
+  (void)n_seqs;
+  (void)HV;
+  (void)V;
+  return 0;  // the one-pass kernel keeps every per-chunk quantity on chip
 }
 
 extern "C" int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, const void* g, const void* beta,
@@ -841,47 +690,31 @@ extern "C" int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, 
                                    int use_qk_l2norm, int qkv_dtype, int g_dtype, int beta_dtype, void* workspace,
                                    int64_t workspace_bytes, yh_stream_t stream) {
   using namespace yh;
+  (void)workspace;
+  (void)workspace_bytes;
   YH_CHECK_ARG(n_seqs >= 0 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_chunk: bad sizes");
   YH_CHECK_ARG(K == 128, "gdn_chunk: K must be 128 (got %lld)", (long long)K);
   YH_CHECK_ARG(V == 64 || V == 128, "gdn_chunk: V must be 64 or 128 (got %lld)", (long long)V);
   YH_CHECK_ARG(qkv_dtype == YH_BF16, "gdn_chunk: q/k/v must be bfloat16");
   YH_CHECK_ARG(is_float_dtype(g_dtype) && is_float_dtype(beta_dtype), "gdn_chunk: bad gate dtypes");
   if (n_seqs == 0) return YH_OK;
-  YH_CHECK_ARG(q && k && v && g && beta && final_state && o && cu_seqlens && workspace, "gdn_chunk: null pointer");
-  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
-                 reinterpret_cast<uintptr_t>(workspace)) & 15) == 0,
-               "gdn_chunk: q/k/v and the workspace must be 16-byte aligned");
-  const WsLayout l = ws_layout(total_tokens, n_seqs, HV);
-  YH_CHECK_ARG(workspace_bytes >= l.bytes, "gdn_chunk: workspace of %lld bytes required", (long long)l.bytes);
-  const int64_t nc = chunk_bound(total_tokens, n_seqs);
-  YH_CHECK_ARG(nc < (1LL << 31) && n_seqs * HV < (1LL << 31) && HV < 65536, "gdn_chunk: grid too large");
-  char* ws = static_cast<char*>(workspace);
-  int32_t* table = reinterpret_cast<int32_t*>(ws + l.table);
-  int32_t* cstart = reinterpret_cast<int32_t*>(ws + l.cstart);
+  YH_CHECK_ARG(q && k && v && g && beta && final_state && o && cu_seqlens, "gdn_chunk: null pointer");
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) &
+                15) == 0,
+               "gdn_chunk: q/k/v must be 16-byte aligned");
+  // 32-bit byte offsets of the copies: the gate tensors and one chunk's rows
+  YH_CHECK_ARG(n_seqs * HV < (1LL << 31) && total_tokens * HV * 4 < (1LL << 31) && 64 * H * K * 2 < (1LL << 31) &&
+                   64 * HV * V * 2 < (1LL << 31),
+               "gdn_chunk: sizes too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(chunk_index_kernel, dim3(1), dim3(kIdxThreads), 0, st, cu_seqlens, (int)n_seqs, table, cstart,
-                     (int)nc);
-  YH_CHECK_LAUNCH("gdn_chunk_index");
-  uint16_t* thi = reinterpret_cast<uint16_t*>(ws + l.thi);
-  uint16_t* tlo = reinterpret_cast<uint16_t*>(ws + l.tlo);
-  uint16_t* aqk = reinterpret_cast<uint16_t*>(ws + l.aqk);
-  float* scal = reinterpret_cast<float*>(ws + l.scal);
-  if (nc > 0) {
-    PrepArgs p{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), g, beta, table, cstart, thi, tlo, aqk,
-               scal, (int)n_seqs, (int)H, (int)HV, scale, use_qk_l2norm ? 1 : 0, g_dtype, beta_dtype};
-    const int64_t items = nc * HV;  // an upper bound: the kernel reads the chunk count
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3(static_cast<unsigned>(items < kPrepGrid ? items : kPrepGrid)),
-                       dim3(kPrepThreads), 0, st, p);
-    YH_CHECK_LAUNCH("gdn_chunk_prep");
-  }
-  ScanArgs s{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), thi, tlo,
-             aqk, scal, cu_seqlens, cstart, order, initial_state, final_state, static_cast<uint16_t*>(o), (int)n_seqs,
-             (int)H, (int)HV};
+  FusedArgs f{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), g,
+              beta, cu_seqlens, order, initial_state, final_state, static_cast<uint16_t*>(o), (int)n_seqs, (int)H,
+              (int)HV, scale, use_qk_l2norm ? 1 : 0, g_dtype, beta_dtype};
   const dim3 grid(static_cast<unsigned>(n_seqs * HV));
   if (V == 128)
-    hipLaunchKernelGGL(chunk_scan_kernel<8>, grid, dim3(512), 0, st, s);
+    hipLaunchKernelGGL(chunk_fused_kernel<8>, grid, dim3(512), 0, st, f);
   else
-    hipLaunchKernelGGL(chunk_scan_kernel<4>, grid, dim3(256), 0, st, s);
-  YH_CHECK_LAUNCH("gdn_chunk_scan");
+    hipLaunchKernelGGL(chunk_fused_kernel<4>, grid, dim3(256), 0, st, f);
+  YH_CHECK_LAUNCH("gdn_chunk");
   return YH_OK;
 }

@@ -95,23 +95,10 @@ def _packed_or_batched(query, key, value, g, beta, cu_seqlens):
     return cu
 
 
-_chunk_ws: dict = {}
-
-
 def _chunk_kernel_fits(query, value):
     """The MFMA chunk kernels take K = 128, V in {64, 128} and bf16 q/k/v."""
     return (query.ndim == 4 and value.ndim == 4 and query.shape[-1] == 128 and value.shape[-1] in (64, 128)
             and query.dtype == torch.bfloat16)
-
-
-def _chunk_workspace(device, nbytes):
-    """Per-device scratch of the chunk kernels, grown on demand."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _chunk_ws.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=device)
-        _chunk_ws[key] = ws
-    return ws
 
 
 def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, initial_state=None,
@@ -128,14 +115,12 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
     returns ``(o, final_state or None)``.
 
     Inputs with K = 128, V in {64, 128} and bf16 q/k/v run the MFMA chunk
-    kernels (chunk 64): packed ones as given, batched ones (the reference's
+    kernel (chunk 64): packed ones as given, batched ones (the reference's
     own call, T > 1) as B packed sequences of T tokens.  Other shapes, or
     ``force_recurrent=True``, run the token-recurrent kernel over each
-    sequence.  ``lengths`` (host ints, one
-    per sequence) lets the chunk kernels start the longest sequences first.
-    The chunk kernels use a per-device workspace that is cached and grown on
-    demand: concurrent calls on different streams of one device must not
-    overlap.
+    sequence.  ``lengths`` (host ints, one per sequence) lets the chunk
+    kernel start the longest sequences first.  The chunk kernel needs no
+    scratch memory, so concurrent calls on different streams are independent.
     """
     if g is None or beta is None:
         raise ValueError("chunk_gated_delta_rule needs g and beta")
@@ -180,11 +165,9 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
         if lengths is not None:  # longest sequences first balances the grid
             order = torch.tensor(sorted(range(n), key=lambda i: -int(lengths[i])), dtype=torch.int32,
                                  device=dev)
-        ws = _chunk_workspace(dev, N.lib().yh_gdn_chunk_workspace_bytes(total, n, hv, vd))
         N.call("yh_gdn_chunk_varlen", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_.data_ptr(), be.data_ptr(),
                N.ptr(h0), state.data_ptr(), o.data_ptr(), cu.data_ptr(), N.ptr(order), n, total, h, hv, kd, vd, sc,
-               int(bool(use_qk_l2norm_in_kernel)), N.code(q), N.code(g_), N.code(be), ws.data_ptr(), ws.numel(),
-               N.stream_of(q))
+               int(bool(use_qk_l2norm_in_kernel)), N.code(q), N.code(g_), N.code(be), None, 0, N.stream_of(q))
         return o, (state if output_final_state else None)
     if initial_state is None:
         state = torch.zeros(n, hv, kd, vd, device=dev, dtype=torch.float32)
