@@ -343,7 +343,7 @@ __device__ __forceinline__ void inv_level2(const float* l, float* t, int u) {  /
   put_block(t, i, j, o, r, g);
 }
 
-template <int NW>
+template <int NW, bool PREP, bool SCAN>
 __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
                                            FPrep& pp, f32x4v (&S)[8], int j, int nch, int64_t seq0, int seqlen,
                                            int hv, int hk) {
@@ -359,16 +359,16 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, quad = lane >> 4, rq4 = quad * 4;
   const int vcol = 16 * w + r16;
-  const bool prep = j < nch, scan = j > 0;  // uniform
+  constexpr bool prep = PREP, scan = SCAN;  // chunk j exists / chunk j - 1 exists
   const int64_t tokp = seq0 + static_cast<int64_t>(j) * kC, toks = tokp - kC;
   const int Lp = min(kC, seqlen - j * kC), Ls = min(kC, seqlen - (j - 1) * kC);
 
   // ---- P0: v of chunk j ----
-  if (prep) fdma_v<NW>(Y, a, tokp, Lp, hv);
+  if constexpr (prep) fdma_v<NW>(Y, a, tokp, Lp, hv);
 
   // ---- P1: norms, decays, K K^T, Q K^T of j | Q S, K S of j - 1 ----
   f32x4v kk[kTPW], qk[kTPW];
-  if (prep) {
+  if constexpr (prep) {
     {  // L2 norms: LPT lanes per token, each over 16 / LPT pieces of its row
       constexpr int LPT = NT / kC, PPL = 16 / LPT;
       const int t = tid / LPT, p0 = (tid % LPT) * PPL;
@@ -424,7 +424,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
     }
   }
   f32x4v qs[4], ps[4];
-  if (scan) {
+  if constexpr (scan) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) qs[mt] = ps[mt] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -444,7 +444,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   lds_barrier();
 
   // ---- P2: L, A and the scalings of j | v_new of j - 1 ----
-  if (prep) {
+  if constexpr (prep) {
     if (tid < kC) {
       const float eg = expf(pp.G[tid]);
       Y.scal[tid] = eg * pp.rqs[tid];                          // output row scale of Q S
@@ -478,7 +478,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
     }
   }
   f32x4v vn[4];
-  if (scan) {
+  if constexpr (scan) {
     bf16x8_t vb[2], ph[2], pl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -513,7 +513,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
 
   // ---- P3a: state update of j - 1 | the inverse's diagonal blocks of j ----
   float* tf = X.vt.t;  // T of chunk j over X's V rows (dead since P2)
-  if (scan) {
+  if constexpr (scan) {
     bf16x8_t zh[2], zl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -538,12 +538,13 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       S[dt] = sv;
     }
   }
-  if (prep && w == 0) inv_diag(Y.tt.l, tf);
+  if constexpr (prep)
+    if (w == 0) inv_diag(Y.tt.l, tf);
   lds_barrier();
 
   // ---- P3b: output of j - 1 | the inverse's first level of j ----
   uint32_t ow[8];
-  if (scan) {
+  if constexpr (scan) {
     bf16x8_t vnb[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -570,12 +571,13 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       ow[2 * mt + 1] = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
     }
   }
-  if (prep && w < 2) inv_level1(Y.tt.l, tf, w);
+  if constexpr (prep)
+    if (w < 2) inv_level1(Y.tt.l, tf, w);
   lds_barrier();
 
   // ---- P3c: output stores of j - 1, then q, k and gate words of j + 1 into X
   // (read there for the last time) | the inverse's second level of j ----
-  if (scan) {
+  if constexpr (scan) {
     const int rodd = (r16 & 1) ? 2 : 0, c0 = vcol & ~1;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -592,11 +594,12 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
     }
   }
   if (j + 1 < nch) fdma_qkg<NW>(X, a, tokp + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
-  if (prep && w < 4) inv_level2(Y.tt.l, tf, w);
+  if constexpr (prep)
+    if (w < 4) inv_level2(Y.tt.l, tf, w);
   lds_barrier();
 
   // ---- P4: T diag(beta) of j as hi / lo over L (dead) ----
-  if (prep) {
+  if constexpr (prep) {
     constexpr int kTv = kC * kC / 4 / NT;  // float4 pieces of T per thread
 #pragma unroll
     for (int it = 0; it < kTv; ++it) {
@@ -664,8 +667,13 @@ __global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
   lds_barrier();
   // (one loop body for both parities: its LDS addresses are the buffer's base
   // plus per-lane offsets computed once)
+  // the first iteration only prepares, the last only runs the products; the
+  // ones between do both, with each phase one block of straight-line code
+  if (nch > 0) fused_iter<NW, true, false>(a, &bufs[0], &bufs[1], pp, S, 0, nch, seq0, seqlen, hv, hk);
 #pragma unroll 1
-  for (int j = 0; j <= nch; ++j) fused_iter<NW>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, S, j, nch, seq0, seqlen, hv, hk);
+  for (int j = 1; j < nch; ++j)
+    fused_iter<NW, true, true>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, S, j, nch, seq0, seqlen, hv, hk);
+  if (nch > 0) fused_iter<NW, false, true>(a, &bufs[nch & 1], &bufs[(nch + 1) & 1], pp, S, nch, nch, seq0, seqlen, hv, hk);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
