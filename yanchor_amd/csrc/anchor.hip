@@ -206,10 +206,13 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 // value 0:
 //   out = sum_w acc_w e^{m_w - M} / (e^{-M} + sum_w l_w e^{m_w - M}),
 //   M = max(0, max_w m_w).
-// 4 waves per workgroup (2 for one head per memory, whose 256-slot pass is
-// short: each wave then keeps its pipeline over twice the blocks), register
-// budget of two waves per SIMD.
-template <bool SINK, int R = 4> constexpr int read_waves() { return R == 1 ? 2 : 4; }
+// Waves per workgroup: 2 for one head per memory (its 256-slot pass is short:
+// each wave then keeps its pipeline over twice the blocks) and for four heads
+// per memory (128 rows x 8 memories: the 1024-slot window ring and the
+// 256-slot anchor memory both read fastest with two waves of 32-slot blocks,
+// 109 us and 33 us, against 108 us and 36 us with four waves and 118 us and
+// 33 us with 16-slot blocks at three waves per SIMD); 4 for two heads.
+template <int R> constexpr int read_waves() { return R == 2 ? 4 : 2; }
 
 //
 // SKIP (anchor memories of at most 256 slots, one or two heads each): a wave fetches its first
@@ -234,10 +237,10 @@ template <int DT, int R, bool SKIP> constexpr int read_occupancy() {
 }
 
 template <int DT, int D, int R, bool SINK, int BS, bool SKIP>
-__global__ void __launch_bounds__((read_waves<SINK, R>() * 64))
+__global__ void __launch_bounds__((read_waves<R>() * 64))
 __attribute__((amdgpu_waves_per_eu(read_occupancy<DT, R, SKIP>(), read_occupancy<DT, R, SKIP>())))
 anchor_read_kernel(ReadArgs a) {
-  constexpr int kReadWaves = read_waves<SINK, R>();
+  constexpr int kReadWaves = read_waves<R>();
   constexpr int kReadThreads = kReadWaves * 64;
   constexpr int LPR = D / 8;
   constexpr int RPI = kWave / LPR;
@@ -654,16 +657,17 @@ __global__ void anchor_advance_kernel(int64_t* count, int64_t* total, const uint
 // 32-slot blocks, or 16-slot blocks for a capacity that is an odd multiple of 16.
 template <int DT, int D, bool SINK, int BS>
 int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G)), block(read_waves<SINK>() * 64);
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.B) * a.G));
+  const dim3 b1(read_waves<1>() * 64), b2(read_waves<2>() * 64), b4(read_waves<4>() * 64);
   // anchor memories of up to 256 slots read by one or two heads fetch live
   // rows only (four heads' state leaves no registers for the list step)
   const bool skip = SINK && a.KC <= kSkipMaxCap && R <= 2;
   switch (R * 2 + (skip ? 1 : 0)) {
-    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, BS, false>), grid, dim3(read_waves<SINK, 1>() * 64), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, kSkipBS, SINK>), grid, dim3(read_waves<SINK, 1>() * 64), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, BS, false>), grid, block, 0, st, a); break;
-    case 5: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, kSkipBS, SINK>), grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, BS, false>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, BS, false>), grid, b1, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, kSkipBS, SINK>), grid, b1, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, BS, false>), grid, b2, 0, st, a); break;
+    case 5: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, kSkipBS, SINK>), grid, b2, 0, st, a); break;
+    case 8: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, BS, false>), grid, b4, 0, st, a); break;
     default: set_error("anchor_read: heads per group must be 1, 2 or 4 (got %d)", R); return YH_ERR_INVALID;
   }
   YH_CHECK_LAUNCH("anchor_read");
