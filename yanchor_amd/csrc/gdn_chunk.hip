@@ -69,12 +69,23 @@ __device__ __forceinline__ float bfv(uint16_t h) { return __uint_as_float(static
 
 typedef float f32x8v __attribute__((ext_vector_type(8)));
 
-// 8 fp32 values -> bf16 hi (round to nearest even) and lo = bf16(x - hi), on
-// the packed hardware conversion (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+// Two fp32 values -> packed bf16 hi (round to nearest even) and lo = bf16(x -
+// hi): one packed conversion each, hi unpacked by a shift and a mask (3
+// instructions a value).
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){x0, x1}, bf16x2_t));
+  const f32x2v r = {x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2_t));
+}
+// 8 fp32 values -> bf16 hi and lo.
 __device__ __forceinline__ void split8(const float* x, bf16x8_t& hi, bf16x8_t& lo) {
-  const f32x8v v = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
-  hi = __builtin_convertvector(v, bf16x8_t);
-  lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x8v), bf16x8_t);
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) split2(x[2 * j], x[2 * j + 1], h[j], l[j]);
+  hi = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+  lo = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
 }
 __device__ __forceinline__ bf16x8_t round8v(const float* x) {
   const f32x8v v = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
@@ -162,13 +173,16 @@ __device__ __forceinline__ void pack_b(const f32x4v& t0, const f32x4v& t1, bf16x
 __device__ __forceinline__ bf16x8_t lds_t(const uint4* m, int r, int ks, int quad) {
   return __builtin_bit_cast(bf16x8_t, m[tpos(r, 4 * ks + quad)]);
 }
-// ... or two b64 reads of a plain row (Q, K at kvpos): columns 32 ks + 4 quad +
-// 0..3 and 32 ks + 16 + 4 quad + 0..3.
+// ... or of a plain Q / K row (kvpos) when the reduction index is the key
+// dimension.  The key dimension is relabelled so that the 8 reduction slots of
+// quad `quad` in step ks are the 8 consecutive columns 32 ks + 8 quad .. + 7:
+// the state register S[dt][i] of lane (quad, column) holds key row
+// 32 (dt / 2) + 8 quad + 4 (dt % 2) + i, so pack_b(S[2 ks], S[2 ks + 1]) lines
+// up with this read.
 __device__ __forceinline__ bf16x8_t lds_k(const uint4* m, int r, int ks, int quad) {
-  const uint2 lo = reinterpret_cast<const uint2*>(&m[kvpos(r, 4 * ks + (quad >> 1))])[quad & 1];
-  const uint2 hi = reinterpret_cast<const uint2*>(&m[kvpos(r, 4 * ks + 2 + (quad >> 1))])[quad & 1];
-  return __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+  return __builtin_bit_cast(bf16x8_t, m[kvpos(r, 4 * ks + quad)]);
 }
+__device__ __forceinline__ int state_row(int dt, int quad, int i) { return 32 * (dt >> 1) + 8 * quad + 4 * (dt & 1) + i; }
 // Operand of a 32-deep step whose reduction index is the ROW of a plain
 // LDS matrix m (K or V at kvpos): lane (i = lane % 16, quad) gets column
 // c0 + i at rows k0 + 4 quad + 0..3 and k0 + 16 + 4 quad + 0..3 -- the
@@ -185,6 +199,20 @@ __device__ __forceinline__ bf16x8_t lds8t(const uint4* m, int k0, int c0, int la
   const int r = k0 + 4 * quad + (i >> 2), pc = (c0 >> 3) + (mm >> 1);
   const uint2* p0 = reinterpret_cast<const uint2*>(&m[kvpos(r, pc)]) + (mm & 1);
   const uint2* p1 = reinterpret_cast<const uint2*>(&m[kvpos(r + 16, pc)]) + (mm & 1);
+  const s16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p0));
+  const s16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p1));
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+// The same transposed read of K for the state rows of accumulator tile dt
+// (state_row order): lane i = 4 mm + e of a 16-lane group gets key column
+// 32 (dt / 2) + 4 (dt % 2) + 8 mm + e, so addressing lane 4 j + mm reads the
+// 8 bytes at columns 32 (dt / 2) + 4 (dt % 2) + 8 mm .. + 3 -- piece
+// 4 (dt / 2) + mm, half dt % 2 -- of row k0 (+ 16) + 4 quad + j.
+__device__ __forceinline__ bf16x8_t lds8t_key(const uint4* m, int k0, int dt, int lane) {
+  const int i = lane & 15, quad = lane >> 4;
+  const int r = k0 + 4 * quad + (i >> 2), pc = 4 * (dt >> 1) + (i & 3);
+  const uint2* p0 = reinterpret_cast<const uint2*>(&m[kvpos(r, pc)]) + (dt & 1);
+  const uint2* p1 = reinterpret_cast<const uint2*>(&m[kvpos(r + 16, pc)]) + (dt & 1);
   const s16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p0));
   const s16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p1));
   return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -416,10 +444,10 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       if (ti >= 10) continue;
       const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8_t b = lds_k(Y.k, n0 + r16, ks, quad);
-        kk[slot] = mfma(lds_k(Y.k, m0 + r16, ks, quad), b, kk[slot]);
-        qk[slot] = mfma(lds_k(Y.q, m0 + r16, ks, quad), b, qk[slot]);
+      for (int ks = 0; ks < 4; ++ks) {  // [s][t] = k_s . k_t and k_s . q_t (lane: t, elements: 4 s)
+        const bf16x8_t as = lds_k(Y.k, n0 + r16, ks, quad);
+        kk[slot] = mfma(as, lds_k(Y.k, m0 + r16, ks, quad), kk[slot]);
+        qk[slot] = mfma(as, lds_k(Y.q, m0 + r16, ks, quad), qk[slot]);
       }
     }
   }
@@ -457,24 +485,27 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       const int ti = (w + 2) % NW + slot * NW;
       if (ti >= 10) continue;
       const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
-      // rows t = m0 + rq4 + i (four consecutive), column s = n0 + r16
-      const int s = n0 + r16, t0 = m0 + rq4;
-      const float4 g2t = *reinterpret_cast<const float4*>(&pp.G2[t0]);
-      const float4 bt = *reinterpret_cast<const float4*>(&pp.beta[t0]);
-      const float4 rkt = *reinterpret_cast<const float4*>(&pp.rk[t0]);
-      const float4 rqt = *reinterpret_cast<const float4*>(&pp.rqs[t0]);
-      const float g2s = pp.G2[s], rks = pp.rk[s];
-      const float g2v[4] = {g2t.x, g2t.y, g2t.z, g2t.w}, bv[4] = {bt.x, bt.y, bt.z, bt.w};
-      const float rkv[4] = {rkt.x, rkt.y, rkt.z, rkt.w}, rqv[4] = {rqt.x, rqt.y, rqt.z, rqt.w};
-      const int sp = pcol(s & ~3) + (s & 3);
+      // row t = m0 + r16, columns s = n0 + rq4 + 0..3 (one 16-byte L write and
+      // one 8-byte A write); the decay exponents G_t - G_s are <= 0 for s <= t
+      const int t = m0 + r16, s0 = n0 + rq4;
+      const float g2t = pp.G2[t], lt = pp.beta[t] * pp.rk[t], at = pp.rqs[t];
+      const float4 g2s = *reinterpret_cast<const float4*>(&pp.G2[s0]);
+      const float4 rks = *reinterpret_cast<const float4*>(&pp.rk[s0]);
+      const float g2v[4] = {g2s.x, g2s.y, g2s.z, g2s.w}, rkv[4] = {rks.x, rks.y, rks.z, rks.w};
+      float lv[4], av[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t0 + i;
-        const float dec = s <= t ? exp2f(g2v[i] - g2s) : 0.f;
-        Y.tt.l[t * SF + s] = s < t ? bv[i] * rkv[i] * rks * dec * kk[slot][i] : 0.f;
-        reinterpret_cast<uint16_t*>(&Y.aqk[tpos(t, sp >> 3)])[sp & 7] =
-            f32_to_bf16(s <= t ? rqv[i] * rks * dec * qk[slot][i] : 0.f);
+      for (int e = 0; e < 4; ++e) {
+        const int s = s0 + e;
+        const float dec = s <= t ? __builtin_amdgcn_exp2f(g2t - g2v[e]) * rkv[e] : 0.f;
+        lv[e] = s < t ? lt * dec * kk[slot][e] : 0.f;
+        av[e] = at * dec * qk[slot][e];
       }
+      *reinterpret_cast<float4*>(&Y.tt.l[t * SF + s0]) = make_float4(lv[0], lv[1], lv[2], lv[3]);
+      const int pc = pcol(s0);
+      const f32x4v af = {av[0], av[1], av[2], av[3]};
+      typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+      reinterpret_cast<uint2*>(&Y.aqk[tpos(t, pc >> 3)])[(pc >> 2) & 1] =
+          __builtin_bit_cast(uint2, __builtin_convertvector(af, bf16x4_t));
     }
   }
   f32x4v vn[4];
@@ -531,7 +562,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       f32x4v sv = S[dt] * egl;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8_t ak = lds8t(X.k, 32 * ks, 16 * dt, lane);
+        const bf16x8_t ak = lds8t_key(X.k, 32 * ks, dt, lane);
         sv = mfma(ak, zh[ks], sv);
         sv = mfma(ak, zl[ks], sv);
       }
@@ -610,19 +641,14 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       if (keep || zero) {
         const float4 x = *reinterpret_cast<const float4*>(&tf[t * SF + s4]);
         const float4 bv = *reinterpret_cast<const float4*>(&pp.beta[s4]);
-        const float tv[4] = {x.x * bv.x, x.y * bv.y, x.z * bv.z, x.w * bv.w};
-        uint16_t h[4], lo[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float y = keep ? tv[i] : 0.f;
-          h[i] = f32_to_bf16(y);
-          lo[i] = f32_to_bf16(y - bfv(h[i]));
-        }
+        const float tv[4] = {keep ? x.x * bv.x : 0.f, keep ? x.y * bv.y : 0.f, keep ? x.z * bv.z : 0.f,
+                             keep ? x.w * bv.w : 0.f};
+        uint32_t h[2], lo[2];
+        split2(tv[0], tv[1], h[0], lo[0]);
+        split2(tv[2], tv[3], h[1], lo[1]);
         const int pc = pcol(s4);
-        reinterpret_cast<uint2*>(&Y.tt.p.hi[tpos(t, pc >> 3)])[(pc >> 2) & 1] =
-            make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-        reinterpret_cast<uint2*>(&Y.tt.p.lo[tpos(t, pc >> 3)])[(pc >> 2) & 1] =
-            make_uint2(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]));
+        reinterpret_cast<uint2*>(&Y.tt.p.hi[tpos(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(h[0], h[1]);
+        reinterpret_cast<uint2*>(&Y.tt.p.lo[tpos(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(lo[0], lo[1]);
       }
     }
   }
@@ -640,18 +666,18 @@ __global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
   const int n = a.order ? a.order[sidx] : sidx;
   const int hk = hv / (a.HV / a.H);
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r16 = lane & 15, rq4 = (lane >> 4) * 4;
+  const int r16 = lane & 15, quad = lane >> 4;
   const int64_t seq0 = a.cu[n];
   const int seqlen = a.cu[n + 1] - a.cu[n];
   const int nch = (seqlen + kC - 1) / kC;
   const int vcol = 16 * w + r16;
-  // S[dt][i] = S[16 dt + 4 quad + i][vcol]
+  // S[dt][i] = S[state_row(dt, quad, i)][vcol]
   f32x4v S[8];
   const int64_t sbase = (static_cast<int64_t>(n) * a.HV + hv) * kK;
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + 16 * dt + rq4 + i) * V + vcol] : 0.f;
+    for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + state_row(dt, quad, i)) * V + vcol] : 0.f;
   wait_vmem();  // the state has arrived before the loop
   // A's halves in the upper blocks (0, 1) and (2, 3) are read as zeros and
   // nothing else writes them: clear them once in both buffers
@@ -677,7 +703,7 @@ __global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a.ht[(sbase + 16 * dt + rq4 + i) * V + vcol] = S[dt][i];
+    for (int i = 0; i < 4; ++i) a.ht[(sbase + state_row(dt, quad, i)) * V + vcol] = S[dt][i];
 }
 
 }  // namespace
