@@ -51,16 +51,28 @@ __device__ __forceinline__ int pcol(int c) {
   return (c & ~31) + 8 * (b & 3) + 4 * (b >> 2);
 }
 
-// LDS rows are unpadded; their 16-byte pieces are XOR-swizzled by row so that
-// every read pattern of the kernel is free of bank conflicts on gfx950's 64
-// banks (checked with the LDS bank-conflict counter on an in-bounds probe):
-//   Q,K,V 128 wide, plain, b64 row reads and transposed
-//         b64 reads:                                      piece p of row r at p ^ swz_kv(r)
+// LDS rows are unpadded; their 16-byte pieces are XOR-swizzled by row against
+// gfx950's LDS bank conflicts (measured with the bank-conflict counter and
+// with timed reads on in-bounds probes):
+//   V     128 wide, transposed b64 reads:                 piece p of row r at p ^ swz_kv(r)
+//   Q,K   128 wide, b128 operand reads (lds_k) and, for
+//         K, transposed b64 reads (lds8t_key):            piece p of row r at p ^ swz_qk(r)
 //   T,A   64 wide, columns permuted, b128 row reads:      piece p of row r at p ^ ((r / 2) % 8)
-// (A 16-byte row padding gives these reads 2- to 4-way conflicts.)
+// swz_qk is the XOR-linear map of r % 16 with bit images 1, 4, 10, 9: of all
+// 20160 invertible linear maps, timed on both Q / K read patterns, the
+// fastest for their mix -- b128 reads twice as fast as with swz_kv (which
+// leaves them 2-way conflicted) and transposed reads ~13 % faster.  (A
+// 16-byte row padding gives the T / A reads 2- to 4-way conflicts.)
 __device__ __forceinline__ int swz_kv(int r) { return (2 * r + ((r >> 3) & 1)) & 15; }
 __device__ __forceinline__ int kvpos(int r, int p) { return r * 16 + ((p ^ swz_kv(r)) & 15); }
+__device__ __forceinline__ int swz_qk(int r) { return static_cast<int>((0x6723cd89feba5410ull >> (4 * (r & 15))) & 15); }
+__device__ __forceinline__ int qkpos(int r, int p) { return r * 16 + ((p ^ swz_qk(r)) & 15); }
 __device__ __forceinline__ int tpos(int r, int p) { return r * 8 + ((p ^ (r >> 1)) & 7); }
+// T diag(beta) hi / lo of row r: rows 0-31 take the first 8 KB (hi, then lo) and
+// rows 32-63 the next 8 KB, so that rows 0-31 can be written while L's rows
+// 32-63 (from byte 8704 of the same storage) are still being read.
+__device__ __forceinline__ int thi(int r, int p) { return tpos(r, p) + (r >= 32 ? 256 : 0); }
+__device__ __forceinline__ int tlo(int r, int p) { return tpos(r, p) + (r >= 32 ? 512 : 256); }
 
 __device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) {
   return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
@@ -173,14 +185,14 @@ __device__ __forceinline__ void pack_b(const f32x4v& t0, const f32x4v& t1, bf16x
 __device__ __forceinline__ bf16x8_t lds_t(const uint4* m, int r, int ks, int quad) {
   return __builtin_bit_cast(bf16x8_t, m[tpos(r, 4 * ks + quad)]);
 }
-// ... or of a plain Q / K row (kvpos) when the reduction index is the key
+// ... or of a plain Q / K row (qkpos) when the reduction index is the key
 // dimension.  The key dimension is relabelled so that the 8 reduction slots of
 // quad `quad` in step ks are the 8 consecutive columns 32 ks + 8 quad .. + 7:
 // the state register S[dt][i] of lane (quad, column) holds key row
 // 32 (dt / 2) + 8 quad + 4 (dt % 2) + i, so pack_b(S[2 ks], S[2 ks + 1]) lines
 // up with this read.
 __device__ __forceinline__ bf16x8_t lds_k(const uint4* m, int r, int ks, int quad) {
-  return __builtin_bit_cast(bf16x8_t, m[kvpos(r, 4 * ks + quad)]);
+  return __builtin_bit_cast(bf16x8_t, m[qkpos(r, 4 * ks + quad)]);
 }
 __device__ __forceinline__ int state_row(int dt, int quad, int i) { return 32 * (dt >> 1) + 8 * quad + 4 * (dt & 1) + i; }
 // Operand of a 32-deep step whose reduction index is the ROW of a plain
@@ -211,8 +223,8 @@ __device__ __forceinline__ bf16x8_t lds8t(const uint4* m, int k0, int c0, int la
 __device__ __forceinline__ bf16x8_t lds8t_key(const uint4* m, int k0, int dt, int lane) {
   const int i = lane & 15, quad = lane >> 4;
   const int r = k0 + 4 * quad + (i >> 2), pc = 4 * (dt >> 1) + (i & 3);
-  const uint2* p0 = reinterpret_cast<const uint2*>(&m[kvpos(r, pc)]) + (dt & 1);
-  const uint2* p1 = reinterpret_cast<const uint2*>(&m[kvpos(r + 16, pc)]) + (dt & 1);
+  const uint2* p0 = reinterpret_cast<const uint2*>(&m[qkpos(r, pc)]) + (dt & 1);
+  const uint2* p1 = reinterpret_cast<const uint2*>(&m[qkpos(r + 16, pc)]) + (dt & 1);
   const s16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p0));
   const s16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4v*)(p1));
   return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -250,17 +262,14 @@ struct FusedArgs {
 };
 
 struct __align__(16) FBuf {
-  uint4 q[kC * 16];  // Q [t][d] at kvpos
-  uint4 k[kC * 16];  // K [t][d] at kvpos
+  uint4 q[kC * 16];  // Q [t][d] at qkpos
+  uint4 k[kC * 16];  // K [t][d] at qkpos
   union {
     uint4 v[kC * 16];  // V [t][v] at kvpos
     float t[kC * SF];  // T (fp32) of the chunk prepared while this one is scanned
   } vt;
   union {
-    struct {
-      uint4 hi[kC * 8];  // T diag(beta) [t][s], bf16 hi, at tpos
-      uint4 lo[kC * 8];  // lo
-    } p;
+    uint4 p[kC * 16];    // T diag(beta) [t][s] as bf16 hi and lo at tpos (thi / tlo)
     float l[kC * SF];    // L (fp32) while this chunk is prepared
   } tt;
   uint4 aqk[kC * 8];     // A [t][s] at tpos
@@ -285,7 +294,7 @@ __device__ __forceinline__ void fdma_qkg(FBuf& b, const FusedArgs& a, int64_t to
       const_cast<uint16_t*>(a.k + (tok0 * a.H + hk) * kK), 0, ((Lc - 1) * qs + kK) * 2, 0x00020000);
 #pragma unroll
   for (int bl = w; bl < 16; bl += NW) {
-    const int row = 4 * bl + (lane >> 4), lp = ((lane & 15) ^ swz_kv(row)) & 15;
+    const int row = 4 * bl + (lane >> 4), lp = ((lane & 15) ^ swz_qk(row)) & 15;
     const int oq = (row * qs + lp * 8) * 2;
     dma16(rq, &b.q[64 * bl], oq);
     dma16(rk, &b.k[64 * bl], oq);
@@ -371,6 +380,43 @@ __device__ __forceinline__ void inv_level2(const float* l, float* t, int u) {  /
   put_block(t, i, j, o, r, g);
 }
 
+// Elements e .. e + 3 (row e / 64) of T diag(beta) as bf16 hi / lo; blocks
+// the products read as zeros are written as zeros.
+__device__ __forceinline__ void t_hilo(FBuf& Y, const float* tf, const FPrep& pp, int e) {
+  const int t = e >> 6, s4 = e & 63;
+  const int bi = t >> 4, bj = s4 >> 4;
+  const bool keep = bj <= bi;                                      // lower block
+  const bool zero = (bi == 0 && bj == 1) || (bi == 2 && bj == 3);  // read as zeros by the products
+  if (keep || zero) {
+    const float4 x = *reinterpret_cast<const float4*>(&tf[t * SF + s4]);
+    const float4 bv = *reinterpret_cast<const float4*>(&pp.beta[s4]);
+    const float tv[4] = {keep ? x.x * bv.x : 0.f, keep ? x.y * bv.y : 0.f, keep ? x.z * bv.z : 0.f,
+                         keep ? x.w * bv.w : 0.f};
+    uint32_t h[2], lo[2];
+    split2(tv[0], tv[1], h[0], lo[0]);
+    split2(tv[2], tv[3], h[1], lo[1]);
+    const int pc = pcol(s4);
+    reinterpret_cast<uint2*>(&Y.tt.p[thi(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(h[0], h[1]);
+    reinterpret_cast<uint2*>(&Y.tt.p[tlo(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(lo[0], lo[1]);
+  }
+}
+
+// Inclusive prefix sum over the 64 lanes: DPP row shifts by 1, 2, 4, 8 within
+// each 16-lane row, then the row broadcasts of lanes 15 and 31.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp0(float v) {  // lanes without a source (or outside ROW_MASK) get 0
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
+}
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+  x += dpp0<0x111, 0xf>(x);  // row_shr:1
+  x += dpp0<0x112, 0xf>(x);  // row_shr:2
+  x += dpp0<0x114, 0xf>(x);  // row_shr:4
+  x += dpp0<0x118, 0xf>(x);  // row_shr:8
+  x += dpp0<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+  x += dpp0<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+  return x;
+}
+
 template <int NW, bool PREP, bool SCAN>
 __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
                                            FPrep& pp, f32x4v (&S)[8], int j, int nch, int64_t seq0, int seqlen,
@@ -397,13 +443,16 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   // ---- P1: norms, decays, K K^T, Q K^T of j | Q S, K S of j - 1 ----
   f32x4v kk[kTPW], qk[kTPW];
   if constexpr (prep) {
-    {  // L2 norms: LPT lanes per token, each over 16 / LPT pieces of its row
+    {  // L2 norms: LPT lanes per token, each over 16 / LPT stored pieces of its row
+       // (a sum over the whole row: the piece order does not matter; tokens
+       // of odd rank start in the other 128-byte half of their row)
       constexpr int LPT = NT / kC, PPL = 16 / LPT;
-      const int t = tid / LPT, p0 = (tid % LPT) * PPL;
+      const int t = tid / LPT, p0 = tid % LPT;
       float sk = 0.f, sq = 0.f;
 #pragma unroll
       for (int e = 0; e < PPL; ++e) {
-        const uint4 kv = Y.k[kvpos(t, p0 + e)], qv = Y.q[kvpos(t, p0 + e)];
+        const int pc = (p0 + LPT * e) ^ (8 * (t & 1));
+        const uint4 kv = Y.k[t * 16 + pc], qv = Y.q[t * 16 + pc];
         const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -423,15 +472,10 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
         pp.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
       }
     }
-    if (w == NW - 1) {  // decay cumsum (a wave without inverse work); lane t holds token t's gates
+    if (w == (NW == 8 ? 5 : NW - 1)) {  // decay cumsum (a wave with one tile and no inverse work); lane t: token t
       const int64_t gi = (tokp + (lane < Lp ? lane : Lp - 1)) * a.HV + hv;
-      float x = lane < Lp ? gate_value(Y.gw[lane], gi, a.g_dt) : 0.f;
       const float bt = lane < Lp ? gate_value(Y.gw[kC + lane], gi, a.beta_dt) : 0.f;
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const float y = __shfl_up(x, off, kWave);
-        if (lane >= off) x += y;
-      }
+      const float x = wave_prefix_sum(lane < Lp ? gate_value(Y.gw[lane], gi, a.g_dt) : 0.f);
       pp.G[lane] = x;
       pp.G2[lane] = x * 1.4426950408889634f;
       pp.beta[lane] = bt;
@@ -528,8 +572,8 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         if (32 * ks <= 16 * mt + 15) {
-          const bf16x8_t th = lds_t(X.tt.p.hi, 16 * mt + r16, ks, quad);
-          const bf16x8_t tl = lds_t(X.tt.p.lo, 16 * mt + r16, ks, quad);
+          const bf16x8_t th = __builtin_bit_cast(bf16x8_t, X.tt.p[thi(16 * mt + r16, 4 * ks + quad)]);
+          const bf16x8_t tl = __builtin_bit_cast(bf16x8_t, X.tt.p[tlo(16 * mt + r16, 4 * ks + quad)]);
           u = mfma(th, vb[ks], u);
           u = mfma(tl, vb[ks], u);
           y = mfma(th, ph[ks], y);
@@ -625,32 +669,23 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
     }
   }
   if (j + 1 < nch) fdma_qkg<NW>(X, a, tokp + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
-  if constexpr (prep)
-    if (w < 4) inv_level2(Y.tt.l, tf, w);
+  if constexpr (prep) {
+    if (w < 4) {
+      inv_level2(Y.tt.l, tf, w);
+    } else if constexpr (NW == 8) {  // rows 0-31 of T are final: their hi / lo go over L's dead rows 0-31
+#pragma unroll
+      for (int it = 0; it < 2; ++it) t_hilo(Y, tf, pp, (it * 256 + tid - 256) * 4);
+    }
+  }
   lds_barrier();
 
-  // ---- P4: T diag(beta) of j as hi / lo over L (dead) ----
+  // ---- P4: T diag(beta) of j as hi / lo over L (dead): rows 32-63 (with eight
+  // waves; rows 0-31 were converted in P3c), all rows with four ----
   if constexpr (prep) {
-    constexpr int kTv = kC * kC / 4 / NT;  // float4 pieces of T per thread
+    constexpr int kR0 = NW == 8 ? 32 : 0;
+    constexpr int kTv = (kC - kR0) * kC / 4 / NT;  // float4 pieces of T per thread
 #pragma unroll
-    for (int it = 0; it < kTv; ++it) {
-      const int e = (it * NT + tid) * 4, t = e >> 6, s4 = e & 63;
-      const int bi = t >> 4, bj = s4 >> 4;
-      const bool keep = bj <= bi;                                      // lower block
-      const bool zero = (bi == 0 && bj == 1) || (bi == 2 && bj == 3);  // read as zeros by the products
-      if (keep || zero) {
-        const float4 x = *reinterpret_cast<const float4*>(&tf[t * SF + s4]);
-        const float4 bv = *reinterpret_cast<const float4*>(&pp.beta[s4]);
-        const float tv[4] = {keep ? x.x * bv.x : 0.f, keep ? x.y * bv.y : 0.f, keep ? x.z * bv.z : 0.f,
-                             keep ? x.w * bv.w : 0.f};
-        uint32_t h[2], lo[2];
-        split2(tv[0], tv[1], h[0], lo[0]);
-        split2(tv[2], tv[3], h[1], lo[1]);
-        const int pc = pcol(s4);
-        reinterpret_cast<uint2*>(&Y.tt.p.hi[tpos(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(h[0], h[1]);
-        reinterpret_cast<uint2*>(&Y.tt.p.lo[tpos(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(lo[0], lo[1]);
-      }
-    }
+    for (int it = 0; it < kTv; ++it) t_hilo(Y, tf, pp, kR0 * kC + (it * NT + tid) * 4);
   }
   dma_wait();     // the copies into Y (v of j) and X (q, k, gates of j + 1) have landed
   lds_barrier();  // chunk j is ready; X may be reused as chunk j + 1's buffer
