@@ -234,17 +234,19 @@ __device__ __forceinline__ bf16x8_t lds8t_key(const uint4* m, int k0, int dt, in
 // chunk_fused_kernel.  Iteration j prepares chunk j in LDS buffer Y from the
 // q / k rows already there, and runs the state-dependent products of chunk
 // j - 1 from buffer X:
-//   P0  copy v (j) into Y (its rows held the previous iteration's T)
-//   P1  L2 norms, decay cumsum, K K^T / Q K^T of j      | Q S, K S of j - 1
-//   P2  L (fp32, over Y's T rows), A, scalings of j     | v_new of j - 1
+//   P1  L2 norms, decay cumsum, K K^T / Q K^T of j,
+//       copy v of j into Y (over the previous T)       | Q S, K S of j - 1
+//   P2  L (fp32, over Y's T rows), A, scalings of j     | v_new of j - 1; copy q of j + 1 into X
 //   P3a the inverse's diagonal blocks (wave 0), T fp32
 //       over X's V rows (dead since P2)                 | state update of j - 1
-//   P3b its first off-diagonal level (waves 0, 1)       | output of j - 1
-//   P3c its second level (waves 0..3)                   | output stores of j - 1,
-//                                                         then copy q, k, gates of j + 1 into X
-//   P4  T diag(beta) as bf16 hi / lo into Y's T rows; wait for the copies
+//   P3b its first off-diagonal level (waves 0, 1)       | output of j - 1, staged in X's T rows;
+//                                                         copy k and gates of j + 1 into X
+//   P3c its second level (waves 0..3); T diag(beta)
+//       rows 0-31 as bf16 hi / lo (waves 4..7)          | output stores of j - 1
+//   P4  T diag(beta) rows 32-63 as hi / lo; wait for the copies
 // Six barriers per chunk.  Copies go through the buffer units straight into
-// LDS (dma16 / dma4), in the swizzled layouts.
+// LDS (dma16 / dma4), in the swizzled layouts, each issued in a phase where
+// its target is dead and by waves with time to spare there.
 struct FusedArgs {
   const uint16_t* q;     // [total, H, K]
   const uint16_t* k;
@@ -282,24 +284,45 @@ struct __align__(16) FPrep {
 };
 static_assert(2 * sizeof(FBuf) + sizeof(FPrep) <= 160 * 1024, "fused chunk LDS");
 
-// q, k and the gate words of chunk (tok0, Lc) into b: rows past Lc arrive as
-// zeros (q, k) or as a copy of the last row's words (gates, masked on use).
-template <int NW>
-__device__ __forceinline__ void fdma_qkg(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hv, int hk) {
+// The 64 rows of a chunk of one bf16 matrix (row stride `stride` bytes in
+// global memory, `pieces` 16-byte pieces a row) into LDS rows of 16 pieces,
+// piece p of row r at p ^ swz_qk(r) (QK) or p ^ swz_kv(r), by waves W0 ..
+// W0 + NWV - 1, 16 / NWV copy instructions each.  `r` covers the chunk's
+// valid rows: rows past it and pieces past `pieces` arrive as zeros.
+template <bool QK, int W0, int NWV>
+__device__ __forceinline__ void dma_rows(uint4* dst, __amdgpu_buffer_rsrc_t r, int stride, int pieces) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int qs = a.H * kK;
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.q + (tok0 * a.H + hk) * kK), 0, ((Lc - 1) * qs + kK) * 2, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.k + (tok0 * a.H + hk) * kK), 0, ((Lc - 1) * qs + kK) * 2, 0x00020000);
+  if (w < W0 || w >= W0 + NWV) return;
 #pragma unroll
-  for (int bl = w; bl < 16; bl += NW) {
-    const int row = 4 * bl + (lane >> 4), lp = ((lane & 15) ^ swz_qk(row)) & 15;
-    const int oq = (row * qs + lp * 8) * 2;
-    dma16(rq, &b.q[64 * bl], oq);
-    dma16(rk, &b.k[64 * bl], oq);
+  for (int i = 0; i < 16 / NWV; ++i) {
+    const int bl = w - W0 + i * NWV, row = 4 * bl + (lane >> 4);
+    const int lp = ((lane & 15) ^ (QK ? swz_qk(row) : swz_kv(row))) & 15;
+    dma16(r, &dst[64 * bl], lp < pieces ? row * stride + lp * 16 : 0x7ffffff0);
   }
-  if (w < 2) {  // wave 0: g, wave 1: beta
+}
+// Buffer resource over the Lc valid rows of a chunk that starts at `base`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const uint16_t* base, int Lc, int stride, int row_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, (Lc - 1) * stride + row_bytes, 0x00020000);
+}
+template <int W0, int NWV>
+__device__ __forceinline__ void fdma_q(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hk) {
+  dma_rows<true, W0, NWV>(b.q, chunk_rsrc(a.q + (tok0 * a.H + hk) * kK, Lc, a.H * kK * 2, kK * 2), a.H * kK * 2, 16);
+}
+template <int W0, int NWV>
+__device__ __forceinline__ void fdma_k(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hk) {
+  dma_rows<true, W0, NWV>(b.k, chunk_rsrc(a.k + (tok0 * a.H + hk) * kK, Lc, a.H * kK * 2, kK * 2), a.H * kK * 2, 16);
+}
+template <int V, int W0, int NWV>
+__device__ __forceinline__ void fdma_v(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hv) {
+  dma_rows<false, W0, NWV>(b.vt.v, chunk_rsrc(a.v + (tok0 * a.HV + hv) * V, Lc, a.HV * V * 2, V * 2), a.HV * V * 2,
+                           V / 8);
+}
+// The gate words of chunk (tok0, Lc), by waves W0 (g) and W0 + 1 (beta); rows
+// past Lc repeat the last row's words (masked on use).
+template <int W0>
+__device__ __forceinline__ void fdma_g(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hv) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) - W0;
+  if (w == 0 || w == 1) {
     const void* src = w == 0 ? a.g : a.beta;
     const int dt = w == 0 ? a.g_dt : a.beta_dt;
     const int64_t i = (tok0 + (lane < Lc ? lane : Lc - 1)) * a.HV + hv;
@@ -309,20 +332,12 @@ __device__ __forceinline__ void fdma_qkg(FBuf& b, const FusedArgs& a, int64_t to
     dma4(rg, &b.gw[64 * w], off);
   }
 }
-template <int NW>
-__device__ __forceinline__ void fdma_v(FBuf& b, const FusedArgs& a, int64_t tok0, int Lc, int hv) {
-  constexpr int V = 16 * NW;
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int vs = a.HV * V;
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.v + (tok0 * a.HV + hv) * V), 0, ((Lc - 1) * vs + V) * 2, 0x00020000);
-#pragma unroll
-  for (int bl = w; bl < 16; bl += NW) {
-    const int row = 4 * bl + (lane >> 4), lp = ((lane & 15) ^ swz_kv(row)) & 15;
-    const int ov = lp * 8 < V ? (row * vs + lp * 8) * 2 : 0x7ffffff0;  // pieces past V: zeros
-    dma16(rv, &b.vt.v[64 * bl], ov);
-  }
-}
+// The output tile is staged row-major (V / 8 pieces a row) in the scanned
+// buffer's T hi / lo storage: piece p of row t at p ^ osw(t), which keeps the
+// staging writes (8 rows x 2 pieces per instruction) and the row reads free of
+// bank conflicts.
+template <int V>
+__device__ __forceinline__ int osw(int t) { return 2 * ((t >> 1) & (V / 16 - 1)); }
 
 // T = (I + L)^{-1} for strictly lower triangular L (64 x 64 fp32 in LDS, row
 // stride SF), by 16 x 16 blocks, in three barrier-free pieces so that the
@@ -437,8 +452,6 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   const int64_t tokp = seq0 + static_cast<int64_t>(j) * kC, toks = tokp - kC;
   const int Lp = min(kC, seqlen - j * kC), Ls = min(kC, seqlen - (j - 1) * kC);
 
-  // ---- P0: v of chunk j ----
-  if constexpr (prep) fdma_v<NW>(Y, a, tokp, Lp, hv);
 
   // ---- P1: norms, decays, K K^T, Q K^T of j | Q S, K S of j - 1 ----
   f32x4v kk[kTPW], qk[kTPW];
@@ -494,6 +507,9 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
         qk[slot] = mfma(as, lds_k(Y.q, m0 + r16, ks, quad), qk[slot]);
       }
     }
+    // v of chunk j into Y (its rows held the previous iteration's T), by the
+    // waves with the shorter P1
+    fdma_v<V, 0, NW / 2>(Y, a, tokp, Lp, hv);
   }
   f32x4v qs[4], ps[4];
   if constexpr (scan) {
@@ -516,6 +532,8 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   lds_barrier();
 
   // ---- P2: L, A and the scalings of j | v_new of j - 1 ----
+  const int Ln = min(kC, seqlen - (j + 1) * kC);  // chunk j + 1 (if j + 1 < nch)
+  if (j + 1 < nch) fdma_q<0, NW / 2>(X, a, tokp + kC, Ln, hk);  // X's Q was read for the last time in P1
   if constexpr (prep) {
     if (tid < kC) {
       const float eg = expf(pp.G[tid]);
@@ -645,30 +663,40 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       ow[2 * mt] = pack2(f32_to_bf16(p0.x), f32_to_bf16(p0.y));
       ow[2 * mt + 1] = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
     }
+    // stage the tile in X's T hi / lo storage (read for the last time in P2)
+    uint32_t* stg = reinterpret_cast<uint32_t*>(X.tt.p);
+    const int rodd = odd ? 2 : 0, c0 = vcol & ~1;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int t = 16 * mt + rq4 + rodd + h;
+        stg[(t * (V / 8) + ((c0 >> 3) ^ osw<V>(t))) * 4 + ((c0 & 7) >> 1)] = ow[2 * mt + h];
+      }
+    }
+  }
+  // k and the gate words of chunk j + 1 into X (X's K was read for the last
+  // time in P3a, its gate words in the previous iteration)
+  if (j + 1 < nch) {
+    fdma_k<NW / 2, NW / 2>(X, a, tokp + kC, Ln, hk);
+    fdma_g<2>(X, a, tokp + kC, Ln, hv);
   }
   if constexpr (prep)
     if (w < 2) inv_level1(Y.tt.l, tf, w);
   lds_barrier();
 
-  // ---- P3c: output stores of j - 1, then q, k and gate words of j + 1 into X
-  // (read there for the last time) | the inverse's second level of j ----
+  // ---- P3c: output stores of j - 1 (whole rows, 16 bytes a lane, from the
+  // staging) | the inverse's second level of j ----
   if constexpr (scan) {
-    const int rodd = (r16 & 1) ? 2 : 0, c0 = vcol & ~1;
+    constexpr int PPR = V / 8, RPI = kWave / PPR;  // pieces a row, rows an instruction
+    const uint4* stg = X.tt.p;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int t0 = 16 * mt + rq4 + rodd;
-      uint32_t* o0 = reinterpret_cast<uint32_t*>(a.o + ((toks + t0) * a.HV + hv) * V + c0);
-      uint32_t* o1 = reinterpret_cast<uint32_t*>(a.o + ((toks + t0 + 1) * a.HV + hv) * V + c0);
-      if (Ls == kC) {  // uniform: every chunk but a sequence's last
-        *o0 = ow[2 * mt];
-        *o1 = ow[2 * mt + 1];
-      } else {
-        if (t0 < Ls) *o0 = ow[2 * mt];
-        if (t0 + 1 < Ls) *o1 = ow[2 * mt + 1];
-      }
+    for (int it = 0; it < kC / (RPI * NW); ++it) {
+      const int t = (it * NW + w) * RPI + lane / PPR, pc = lane % PPR;
+      const uint4 val = stg[t * PPR + (pc ^ osw<V>(t))];
+      if (t < Ls) *reinterpret_cast<uint4*>(a.o + ((toks + t) * a.HV + hv) * V + 8 * pc) = val;
     }
   }
-  if (j + 1 < nch) fdma_qkg<NW>(X, a, tokp + kC, min(kC, seqlen - (j + 1) * kC), hv, hk);
   if constexpr (prep) {
     if (w < 4) {
       inv_level2(Y.tt.l, tf, w);
@@ -722,7 +750,9 @@ __global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
     reinterpret_cast<uint2*>(&bufs[bsel].aqk[tpos(t, p)])[1] = make_uint2(0, 0);
   }
   if (nch > 0) {
-    fdma_qkg<NW>(bufs[0], a, seq0, min(kC, seqlen), hv, hk);
+    fdma_q<0, NW>(bufs[0], a, seq0, min(kC, seqlen), hk);
+    fdma_k<0, NW>(bufs[0], a, seq0, min(kC, seqlen), hk);
+    fdma_g<0>(bufs[0], a, seq0, min(kC, seqlen), hv);
     dma_wait();
   }
   lds_barrier();
@@ -768,9 +798,10 @@ extern "C" int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, 
   YH_CHECK_ARG(is_float_dtype(g_dtype) && is_float_dtype(beta_dtype), "gdn_chunk: bad gate dtypes");
   if (n_seqs == 0) return YH_OK;
   YH_CHECK_ARG(q && k && v && g && beta && final_state && o && cu_seqlens, "gdn_chunk: null pointer");
-  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) &
+  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                 reinterpret_cast<uintptr_t>(o)) &
                 15) == 0,
-               "gdn_chunk: q/k/v must be 16-byte aligned");
+               "gdn_chunk: q/k/v/o must be 16-byte aligned");
   // 32-bit byte offsets of the copies: the gate tensors and one chunk's rows
   YH_CHECK_ARG(n_seqs * HV < (1LL << 31) && total_tokens * HV * 4 < (1LL << 31) && 64 * H * K * 2 < (1LL << 31) &&
                    64 * HV * V * 2 < (1LL << 31),
