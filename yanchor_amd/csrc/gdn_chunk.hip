@@ -239,10 +239,10 @@ __device__ __forceinline__ bf16x8_t lds8t_key(const uint4* m, int k0, int dt, in
 //   P2  L (fp32, over Y's T rows), A, scalings of j     | v_new of j - 1; copy q of j + 1 into X
 //   P3a the inverse's diagonal blocks (wave 0), T fp32
 //       over X's V rows (dead since P2)                 | state update of j - 1
-//   P3b its first off-diagonal level (waves 0, 1)       | output of j - 1, staged in X's T rows;
+//   P3b its first off-diagonal level (waves 0, 1)       | output of j - 1 (stored);
 //                                                         copy k and gates of j + 1 into X
 //   P3c its second level (waves 0..3); T diag(beta)
-//       rows 0-31 as bf16 hi / lo (waves 4..7)          | output stores of j - 1
+//       rows 0-31 as bf16 hi / lo (waves 4..7)
 //   P4  T diag(beta) rows 32-63 as hi / lo; wait for the copies
 // Six barriers per chunk.  Copies go through the buffer units straight into
 // LDS (dma16 / dma4), in the swizzled layouts, each issued in a phase where
@@ -275,7 +275,7 @@ struct __align__(16) FBuf {
     float l[kC * SF];    // L (fp32) while this chunk is prepared
   } tt;
   uint4 aqk[kC * 8];     // A [t][s] at tpos
-  float scal[4 * kC];    // orow [0, 64), d2 [64, 128), ek [128, 192), e^{G_last} [192]
+  float scal[4 * kC];    // orow [0, 64), d2 [64, 128), -ek [128, 192), e^{G_last} [192]
   uint32_t gw[2 * kC];   // the words holding g [0, 64) and beta [64, 128) of each token
 };
 struct __align__(16) FPrep {
@@ -332,12 +332,7 @@ __device__ __forceinline__ void fdma_g(FBuf& b, const FusedArgs& a, int64_t tok0
     dma4(rg, &b.gw[64 * w], off);
   }
 }
-// The output tile is staged row-major (V / 8 pieces a row) in the scanned
-// buffer's T hi / lo storage: piece p of row t at p ^ osw(t), which keeps the
-// staging writes (8 rows x 2 pieces per instruction) and the row reads free of
-// bank conflicts.
-template <int V>
-__device__ __forceinline__ int osw(int t) { return 2 * ((t >> 1) & (V / 16 - 1)); }
+
 
 // T = (I + L)^{-1} for strictly lower triangular L (64 x 64 fp32 in LDS, row
 // stride SF), by 16 x 16 blocks, in three barrier-free pieces so that the
@@ -403,13 +398,13 @@ __device__ __forceinline__ void t_hilo(FBuf& Y, const float* tf, const FPrep& pp
   const bool keep = bj <= bi;                                      // lower block
   const bool zero = (bi == 0 && bj == 1) || (bi == 2 && bj == 3);  // read as zeros by the products
   if (keep || zero) {
-    const float4 x = *reinterpret_cast<const float4*>(&tf[t * SF + s4]);
-    const float4 bv = *reinterpret_cast<const float4*>(&pp.beta[s4]);
-    const float tv[4] = {keep ? x.x * bv.x : 0.f, keep ? x.y * bv.y : 0.f, keep ? x.z * bv.z : 0.f,
-                         keep ? x.w * bv.w : 0.f};
-    uint32_t h[2], lo[2];
-    split2(tv[0], tv[1], h[0], lo[0]);
-    split2(tv[2], tv[3], h[1], lo[1]);
+    uint32_t h[2] = {0u, 0u}, lo[2] = {0u, 0u};
+    if (keep) {
+      const float4 x = *reinterpret_cast<const float4*>(&tf[t * SF + s4]);
+      const float4 bv = *reinterpret_cast<const float4*>(&pp.beta[s4]);
+      split2(x.x * bv.x, x.y * bv.y, h[0], lo[0]);
+      split2(x.z * bv.z, x.w * bv.w, h[1], lo[1]);
+    }
     const int pc = pcol(s4);
     reinterpret_cast<uint2*>(&Y.tt.p[thi(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(h[0], h[1]);
     reinterpret_cast<uint2*>(&Y.tt.p[tlo(t, pc >> 3)])[(pc >> 2) & 1] = make_uint2(lo[0], lo[1]);
@@ -468,11 +463,11 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
         const uint4 kv = Y.k[t * 16 + pc], qv = Y.q[t * 16 + pc];
         const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float k0 = __uint_as_float(kw[i] << 16), k1 = __uint_as_float(kw[i] & 0xffff0000u);
-          const float q0 = __uint_as_float(qw[i] << 16), q1 = __uint_as_float(qw[i] & 0xffff0000u);
-          sk = fmaf(k0, k0, fmaf(k1, k1, sk));
-          sq = fmaf(q0, q0, fmaf(q1, q1, sq));
+        for (int i = 0; i < 4; ++i) {  // bf16 pair dot products, fp32 accumulation
+          sk = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kw[i]), __builtin_bit_cast(bf16x2_t, kw[i]), sk,
+                                               false);
+          sq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw[i]), __builtin_bit_cast(bf16x2_t, qw[i]), sq,
+                                               false);
         }
       }
 #pragma unroll
@@ -523,7 +518,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       for (int mt = 0; mt < 4; ++mt) {
         const bf16x8_t aq = lds_k(X.q, 16 * mt + r16, ks, quad);
         const bf16x8_t ak = lds_k(X.k, 16 * mt + r16, ks, quad);
-        qs[mt] = mfma(aq, bh, qs[mt]);
+        qs[mt] = mfma(bh, aq, qs[mt]);  // (Q S)^T: lane (token, quad) holds 4 value columns
         ps[mt] = mfma(ak, bh, ps[mt]);
         ps[mt] = mfma(ak, bl, ps[mt]);
       }
@@ -539,7 +534,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       const float eg = expf(pp.G[tid]);
       Y.scal[tid] = eg * pp.rqs[tid];                          // output row scale of Q S
       Y.scal[kC + tid] = pp.rk[tid] * expf(pp.gl - pp.G[tid]);  // state-update scale of v_new row t
-      Y.scal[2 * kC + tid] = eg * pp.rk[tid];                  // row scale of K S inside W S
+      Y.scal[2 * kC + tid] = -eg * pp.rk[tid];                 // row scale of K S inside -W S
       if (tid == 0) Y.scal[3 * kC] = expf(pp.gl);
     }
 #pragma unroll
@@ -585,8 +580,8 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       pack_b(p0, p1, ph[ks], pl[ks]);
     }
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      f32x4v u = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < 4; ++mt) {  // v_new = T diag(beta) V + T diag(beta) (-W S scaled rows)
+      f32x4v u = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};  // two chains: the MFMA latency stays hidden
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         if (32 * ks <= 16 * mt + 15) {
@@ -599,7 +594,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
           y = mfma(tl, ph[ks], y);
         }
       }
-      vn[mt] = u - y;
+      vn[mt] = u + y;
     }
   }
   lds_barrier();
@@ -636,7 +631,8 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   lds_barrier();
 
   // ---- P3b: output of j - 1 | the inverse's first level of j ----
-  uint32_t ow[8];
+  // o^T = (Q S)^T diag(orow) + v_new^T A^T: lane (r16, quad) holds value
+  // columns 16 w + 4 quad .. + 3 of token 16 mt + r16 and stores them as 8 bytes.
   if constexpr (scan) {
     bf16x8_t vnb[2];
 #pragma unroll
@@ -645,34 +641,18 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
                           vn[2 * ks + 1][0], vn[2 * ks + 1][1], vn[2 * ks + 1][2], vn[2 * ks + 1][3]};
       vnb[ks] = round8v(x);
     }
-    const bool odd = r16 & 1;
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    uint16_t* orow = a.o + ((toks + r16) * a.HV + hv) * V + 16 * w + rq4;  // token r16 of the chunk
+    const int64_t ostep = static_cast<int64_t>(16) * a.HV * V;             // 16 tokens
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      f32x4v acc = qs[mt];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= X.scal[16 * mt + rq4 + i];
+      const int t = 16 * mt + r16;
+      f32x4v acc = qs[mt] * X.scal[t];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        if (32 * ks <= 16 * mt + 15) acc = mfma(lds_t(X.aqk, 16 * mt + r16, ks, quad), vnb[ks], acc);
-      // Column pairs (vcol, vcol ^ 1) go out as 4-byte words: the even lane
-      // holds rows 0, 1 of its quad, the odd lane rows 2, 3.
-      const float y0 = __shfl_xor(odd ? acc[0] : acc[2], 1, kWave);
-      const float y1 = __shfl_xor(odd ? acc[1] : acc[3], 1, kWave);
-      const float2 p0 = odd ? make_float2(y0, acc[2]) : make_float2(acc[0], y0);
-      const float2 p1 = odd ? make_float2(y1, acc[3]) : make_float2(acc[1], y1);
-      ow[2 * mt] = pack2(f32_to_bf16(p0.x), f32_to_bf16(p0.y));
-      ow[2 * mt + 1] = pack2(f32_to_bf16(p1.x), f32_to_bf16(p1.y));
-    }
-    // stage the tile in X's T hi / lo storage (read for the last time in P2)
-    uint32_t* stg = reinterpret_cast<uint32_t*>(X.tt.p);
-    const int rodd = odd ? 2 : 0, c0 = vcol & ~1;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int t = 16 * mt + rq4 + rodd + h;
-        stg[(t * (V / 8) + ((c0 >> 3) ^ osw<V>(t))) * 4 + ((c0 & 7) >> 1)] = ow[2 * mt + h];
-      }
+        if (32 * ks <= 16 * mt + 15) acc = mfma(vnb[ks], lds_t(X.aqk, t, ks, quad), acc);
+      if (t < Ls)
+        *reinterpret_cast<uint2*>(orow + mt * ostep) = __builtin_bit_cast(uint2, __builtin_convertvector(acc, bf16x4_t));
     }
   }
   // k and the gate words of chunk j + 1 into X (X's K was read for the last
@@ -685,18 +665,7 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
     if (w < 2) inv_level1(Y.tt.l, tf, w);
   lds_barrier();
 
-  // ---- P3c: output stores of j - 1 (whole rows, 16 bytes a lane, from the
-  // staging) | the inverse's second level of j ----
-  if constexpr (scan) {
-    constexpr int PPR = V / 8, RPI = kWave / PPR;  // pieces a row, rows an instruction
-    const uint4* stg = X.tt.p;
-#pragma unroll
-    for (int it = 0; it < kC / (RPI * NW); ++it) {
-      const int t = (it * NW + w) * RPI + lane / PPR, pc = lane % PPR;
-      const uint4 val = stg[t * PPR + (pc ^ osw<V>(t))];
-      if (t < Ls) *reinterpret_cast<uint4*>(a.o + ((toks + t) * a.HV + hv) * V + 8 * pc) = val;
-    }
-  }
+  // ---- P3c: the inverse's second level of j ----
   if constexpr (prep) {
     if (w < 4) {
       inv_level2(Y.tt.l, tf, w);
