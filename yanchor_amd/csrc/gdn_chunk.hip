@@ -287,15 +287,14 @@ static_assert(2 * sizeof(FBuf) + sizeof(FPrep) <= 160 * 1024, "fused chunk LDS")
 // The 64 rows of a chunk of one bf16 matrix (row stride `stride` bytes in
 // global memory, `pieces` 16-byte pieces a row) into LDS rows of 16 pieces,
 // piece p of row r at p ^ swz_qk(r) (QK) or p ^ swz_kv(r), by waves W0 ..
-// W0 + NWV - 1, 16 / NWV copy instructions each.  `r` covers the chunk's
+// W0 + NWV - 1, one copy instruction per 4 rows.  `r` covers the chunk's
 // valid rows: rows past it and pieces past `pieces` arrive as zeros.
 template <bool QK, int W0, int NWV>
 __device__ __forceinline__ void dma_rows(uint4* dst, __amdgpu_buffer_rsrc_t r, int stride, int pieces) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (w < W0 || w >= W0 + NWV) return;
-#pragma unroll
-  for (int i = 0; i < 16 / NWV; ++i) {
-    const int bl = w - W0 + i * NWV, row = 4 * bl + (lane >> 4);
+  for (int bl = w - W0; bl < 16; bl += NWV) {
+    const int row = 4 * bl + (lane >> 4);
     const int lp = ((lane & 15) ^ (QK ? swz_qk(row) : swz_kv(row))) & 15;
     dma16(r, &dst[64 * bl], lp < pieces ? row * stride + lp * 16 : 0x7ffffff0);
   }
@@ -427,87 +426,73 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
   return x;
 }
 
+constexpr int kNP = 4;  // prep waves
+
+// K K^T / Q K^T tile ti (0..9, lower 16 x 16 blocks of the chunk) of Y,
+// transposed: [s][t] = k_s . k_t and k_s . q_t (lane: t, elements: 4 s) ...
+__device__ __forceinline__ void kq_tile(const FBuf& Y, int ti, f32x4v& kk, f32x4v& qk, int r16, int quad) {
+  kk = qk = f32x4v{0.f, 0.f, 0.f, 0.f};
+  const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8_t as = lds_k(Y.k, n0 + r16, ks, quad);
+    kk = mfma(as, lds_k(Y.k, m0 + r16, ks, quad), kk);
+    qk = mfma(as, lds_k(Y.q, m0 + r16, ks, quad), qk);
+  }
+}
+// ... and its L and A entries: row t = m0 + r16, columns s = n0 + 4 quad + 0..3
+// (one 16-byte L write and one 8-byte A write); the decay exponents G_t - G_s
+// are <= 0 for s <= t.
+__device__ __forceinline__ void la_tile(FBuf& Y, const FPrep& pp, int ti, const f32x4v& kk, const f32x4v& qk, int r16,
+                                        int quad) {
+  const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
+  const int t = m0 + r16, s0 = n0 + 4 * quad;
+  const float g2t = pp.G2[t], lt = pp.beta[t] * pp.rk[t], at = pp.rqs[t];
+  const float4 g2s = *reinterpret_cast<const float4*>(&pp.G2[s0]);
+  const float4 rks = *reinterpret_cast<const float4*>(&pp.rk[s0]);
+  const float g2v[4] = {g2s.x, g2s.y, g2s.z, g2s.w}, rkv[4] = {rks.x, rks.y, rks.z, rks.w};
+  float lv[4], av[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int s = s0 + e;
+    const float dec = s <= t ? __builtin_amdgcn_exp2f(g2t - g2v[e]) * rkv[e] : 0.f;
+    lv[e] = s < t ? lt * dec * kk[e] : 0.f;
+    av[e] = at * dec * qk[e];
+  }
+  *reinterpret_cast<float4*>(&Y.tt.l[t * SF + s0]) = make_float4(lv[0], lv[1], lv[2], lv[3]);
+  const int pc = pcol(s0);
+  const f32x4v af = {av[0], av[1], av[2], av[3]};
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  reinterpret_cast<uint2*>(&Y.aqk[tpos(t, pc >> 3)])[(pc >> 2) & 1] =
+      __builtin_bit_cast(uint2, __builtin_convertvector(af, bf16x4_t));
+}
+// Both roles run one iteration per chunk (plus one) with the same six
+// workgroup barriers, each role in its own loop: the state and the scan's
+// products are live on the scan waves only, the prep tiles on the prep waves.
+
+// Scan waves 0 .. NW - 1: value columns 16 w .. 16 w + 15, the state in
+// registers.  P1 Q S, K S of j - 1; tile w of j | P2 v_new; L, A of tile w
+// | P3a state update | P3b output | P3c, P4 T diag(beta) of j as bf16 hi / lo
+// (rows 0-31, rows 32-63).
 template <int NW, bool PREP, bool SCAN>
-__device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
-                                           FPrep& pp, f32x4v (&S)[8], int j, int nch, int64_t seq0, int seqlen,
-                                           int hv, int hk) {
+__device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
+                                          const FPrep& pp, f32x4v (&S)[8], int j, int64_t seq0, int seqlen,
+                                          int hv) {
   FBuf& Y = *Yp;
   FBuf& X = *Xp;
-  constexpr int V = 16 * NW, NT = NW * 64;
-  constexpr int kTPW = (10 + NW - 1) / NW;  // K K^T / Q K^T tiles per wave
-  // The lane index is re-derived opaquely in every iteration: the swizzled LDS
-  // offsets then are computed where they are used rather than hoisted out of
-  // the chunk loop, where they would outnumber the registers.
+  constexpr int V = 16 * NW, NS = NW * 64;
   int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid));
+  asm volatile("" : "+v"(tid));  // offsets computed where used, not hoisted out of the chunk loop
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, quad = lane >> 4, rq4 = quad * 4;
-  const int vcol = 16 * w + r16;
-  constexpr bool prep = PREP, scan = SCAN;  // chunk j exists / chunk j - 1 exists
-  const int64_t tokp = seq0 + static_cast<int64_t>(j) * kC, toks = tokp - kC;
-  const int Lp = min(kC, seqlen - j * kC), Ls = min(kC, seqlen - (j - 1) * kC);
+  const int64_t toks = seq0 + static_cast<int64_t>(j - 1) * kC;
+  const int Ls = min(kC, seqlen - (j - 1) * kC);
 
-
-  // ---- P1: norms, decays, K K^T, Q K^T of j | Q S, K S of j - 1 ----
-  f32x4v kk[kTPW], qk[kTPW];
-  if constexpr (prep) {
-    {  // L2 norms: LPT lanes per token, each over 16 / LPT stored pieces of its row
-       // (a sum over the whole row: the piece order does not matter; tokens
-       // of odd rank start in the other 128-byte half of their row)
-      constexpr int LPT = NT / kC, PPL = 16 / LPT;
-      const int t = tid / LPT, p0 = tid % LPT;
-      float sk = 0.f, sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < PPL; ++e) {
-        const int pc = (p0 + LPT * e) ^ (8 * (t & 1));
-        const uint4 kv = Y.k[t * 16 + pc], qv = Y.q[t * 16 + pc];
-        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // bf16 pair dot products, fp32 accumulation
-          sk = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kw[i]), __builtin_bit_cast(bf16x2_t, kw[i]), sk,
-                                               false);
-          sq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw[i]), __builtin_bit_cast(bf16x2_t, qw[i]), sq,
-                                               false);
-        }
-      }
-#pragma unroll
-      for (int m = 1; m < LPT; m <<= 1) {
-        sk += __shfl_xor(sk, m, kWave);
-        sq += __shfl_xor(sq, m, kWave);
-      }
-      if (tid % LPT == 0) {
-        pp.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
-        pp.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-      }
-    }
-    if (w == (NW == 8 ? 5 : NW - 1)) {  // decay cumsum (a wave with one tile and no inverse work); lane t: token t
-      const int64_t gi = (tokp + (lane < Lp ? lane : Lp - 1)) * a.HV + hv;
-      const float bt = lane < Lp ? gate_value(Y.gw[kC + lane], gi, a.beta_dt) : 0.f;
-      const float x = wave_prefix_sum(lane < Lp ? gate_value(Y.gw[lane], gi, a.g_dt) : 0.f);
-      pp.G[lane] = x;
-      pp.G2[lane] = x * 1.4426950408889634f;
-      pp.beta[lane] = bt;
-      if (lane == kWave - 1) pp.gl = x;
-    }
-#pragma unroll
-    for (int slot = 0; slot < kTPW; ++slot) {  // the extra tiles go to waves without inverse work
-      kk[slot] = qk[slot] = f32x4v{0.f, 0.f, 0.f, 0.f};
-      const int ti = (w + 2) % NW + slot * NW;
-      if (ti >= 10) continue;
-      const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {  // [s][t] = k_s . k_t and k_s . q_t (lane: t, elements: 4 s)
-        const bf16x8_t as = lds_k(Y.k, n0 + r16, ks, quad);
-        kk[slot] = mfma(as, lds_k(Y.k, m0 + r16, ks, quad), kk[slot]);
-        qk[slot] = mfma(as, lds_k(Y.q, m0 + r16, ks, quad), qk[slot]);
-      }
-    }
-    // v of chunk j into Y (its rows held the previous iteration's T), by the
-    // waves with the shorter P1
-    fdma_v<V, 0, NW / 2>(Y, a, tokp, Lp, hv);
-  }
+  // ---- P1 ----
+  f32x4v kk, qk;
+  if constexpr (PREP) kq_tile(Y, w, kk, qk, r16, quad);  // tile w of chunk j
   f32x4v qs[4], ps[4];
-  if constexpr (scan) {
+  if constexpr (SCAN) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) qs[mt] = ps[mt] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -526,47 +511,10 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   }
   lds_barrier();
 
-  // ---- P2: L, A and the scalings of j | v_new of j - 1 ----
-  const int Ln = min(kC, seqlen - (j + 1) * kC);  // chunk j + 1 (if j + 1 < nch)
-  if (j + 1 < nch) fdma_q<0, NW / 2>(X, a, tokp + kC, Ln, hk);  // X's Q was read for the last time in P1
-  if constexpr (prep) {
-    if (tid < kC) {
-      const float eg = expf(pp.G[tid]);
-      Y.scal[tid] = eg * pp.rqs[tid];                          // output row scale of Q S
-      Y.scal[kC + tid] = pp.rk[tid] * expf(pp.gl - pp.G[tid]);  // state-update scale of v_new row t
-      Y.scal[2 * kC + tid] = -eg * pp.rk[tid];                 // row scale of K S inside -W S
-      if (tid == 0) Y.scal[3 * kC] = expf(pp.gl);
-    }
-#pragma unroll
-    for (int slot = 0; slot < kTPW; ++slot) {
-      const int ti = (w + 2) % NW + slot * NW;
-      if (ti >= 10) continue;
-      const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
-      // row t = m0 + r16, columns s = n0 + rq4 + 0..3 (one 16-byte L write and
-      // one 8-byte A write); the decay exponents G_t - G_s are <= 0 for s <= t
-      const int t = m0 + r16, s0 = n0 + rq4;
-      const float g2t = pp.G2[t], lt = pp.beta[t] * pp.rk[t], at = pp.rqs[t];
-      const float4 g2s = *reinterpret_cast<const float4*>(&pp.G2[s0]);
-      const float4 rks = *reinterpret_cast<const float4*>(&pp.rk[s0]);
-      const float g2v[4] = {g2s.x, g2s.y, g2s.z, g2s.w}, rkv[4] = {rks.x, rks.y, rks.z, rks.w};
-      float lv[4], av[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = s0 + e;
-        const float dec = s <= t ? __builtin_amdgcn_exp2f(g2t - g2v[e]) * rkv[e] : 0.f;
-        lv[e] = s < t ? lt * dec * kk[slot][e] : 0.f;
-        av[e] = at * dec * qk[slot][e];
-      }
-      *reinterpret_cast<float4*>(&Y.tt.l[t * SF + s0]) = make_float4(lv[0], lv[1], lv[2], lv[3]);
-      const int pc = pcol(s0);
-      const f32x4v af = {av[0], av[1], av[2], av[3]};
-      typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-      reinterpret_cast<uint2*>(&Y.aqk[tpos(t, pc >> 3)])[(pc >> 2) & 1] =
-          __builtin_bit_cast(uint2, __builtin_convertvector(af, bf16x4_t));
-    }
-  }
+  // ---- P2 ----
+  if constexpr (PREP) la_tile(Y, pp, w, kk, qk, r16, quad);
   f32x4v vn[4];
-  if constexpr (scan) {
+  if constexpr (SCAN) {
     bf16x8_t vb[2], ph[2], pl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -599,9 +547,8 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
   }
   lds_barrier();
 
-  // ---- P3a: state update of j - 1 | the inverse's diagonal blocks of j ----
-  float* tf = X.vt.t;  // T of chunk j over X's V rows (dead since P2)
-  if constexpr (scan) {
+  // ---- P3a ----
+  if constexpr (SCAN) {
     bf16x8_t zh[2], zl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -626,14 +573,11 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
       S[dt] = sv;
     }
   }
-  if constexpr (prep)
-    if (w == 0) inv_diag(Y.tt.l, tf);
   lds_barrier();
 
-  // ---- P3b: output of j - 1 | the inverse's first level of j ----
-  // o^T = (Q S)^T diag(orow) + v_new^T A^T: lane (r16, quad) holds value
-  // columns 16 w + 4 quad .. + 3 of token 16 mt + r16 and stores them as 8 bytes.
-  if constexpr (scan) {
+  // ---- P3b: o^T = (Q S)^T diag(orow) + v_new^T A^T: lane (r16, quad) holds
+  // value columns 16 w + 4 quad .. + 3 of token 16 mt + r16, stored as 8 bytes ----
+  if constexpr (SCAN) {
     bf16x8_t vnb[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -655,44 +599,146 @@ __device__ __forceinline__ void fused_iter(const FusedArgs& a, FBuf* __restrict_
         *reinterpret_cast<uint2*>(orow + mt * ostep) = __builtin_bit_cast(uint2, __builtin_convertvector(acc, bf16x4_t));
     }
   }
-  // k and the gate words of chunk j + 1 into X (X's K was read for the last
-  // time in P3a, its gate words in the previous iteration)
-  if (j + 1 < nch) {
-    fdma_k<NW / 2, NW / 2>(X, a, tokp + kC, Ln, hk);
-    fdma_g<2>(X, a, tokp + kC, Ln, hv);
-  }
-  if constexpr (prep)
-    if (w < 2) inv_level1(Y.tt.l, tf, w);
   lds_barrier();
 
-  // ---- P3c: the inverse's second level of j ----
-  if constexpr (prep) {
-    if (w < 4) {
-      inv_level2(Y.tt.l, tf, w);
-    } else if constexpr (NW == 8) {  // rows 0-31 of T are final: their hi / lo go over L's dead rows 0-31
+  // ---- P3c: T diag(beta) rows 0-31 of chunk j (final after P3b) as hi / lo
+  // over L's dead rows 0-31 ----
+  const float* tf = X.vt.t;
+  if constexpr (PREP) {
 #pragma unroll
-      for (int it = 0; it < 2; ++it) t_hilo(Y, tf, pp, (it * 256 + tid - 256) * 4);
+    for (int it = 0; it < 512 / NS; ++it) t_hilo(Y, tf, pp, (it * NS + tid) * 4);
+  }
+  lds_barrier();
+
+  // ---- P4: rows 32-63 ----
+  if constexpr (PREP) {
+#pragma unroll
+    for (int it = 0; it < 512 / NS; ++it) t_hilo(Y, tf, pp, 32 * kC + (it * NS + tid) * 4);
+  }
+  lds_barrier();  // chunk j is ready; X may be reused as chunk j + 1's buffer
+}
+
+// Prep waves NW .. NW + kNP - 1, chunk j in Y: P1 L2 norms, decay cumsum,
+// K K^T / Q K^T tiles NW..9 | P2 their L, A; the scalings | P3a the
+// inverse's diagonal blocks (T over X's V rows, dead since P2); copy v of j
+// into Y and q of j + 1 into X | P3b its first level; copy k and gates of
+// j + 1 into X | P3c its second level | P4 wait for the copies.
+template <int NW, bool PREP>
+__device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
+                                          FPrep& pp, int j, int nch, int64_t seq0, int seqlen, int hv, int hk) {
+  FBuf& Y = *Yp;
+  FBuf& X = *Xp;
+  constexpr int V = 16 * NW, NS = NW * 64;
+  constexpr int kTPW = (10 - NW + kNP - 1) / kNP;  // tiles NW..9, from prep wave 1 on
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pw = w - NW, ptid = tid - NS;
+  auto tile_of = [&](int slot) { return NW + (pw + kNP - 1) % kNP + kNP * slot; };
+  const int r16 = lane & 15, quad = lane >> 4, rq4 = quad * 4;
+  const int64_t tokp = seq0 + static_cast<int64_t>(j) * kC;
+  const int Lp = min(kC, seqlen - j * kC), Ln = min(kC, seqlen - (j + 1) * kC);
+
+  // ---- P1 ----
+  f32x4v kk[kTPW], qk[kTPW];
+  if constexpr (PREP) {
+    {  // L2 norms: LPT lanes per token, each over 16 / LPT stored pieces of its row
+       // (a sum over the whole row: the piece order does not matter; tokens
+       // of odd rank start in the other 128-byte half of their row)
+      constexpr int LPT = kNP * 64 / kC, PPL = 16 / LPT;
+      const int t = ptid / LPT, p0 = ptid % LPT;
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < PPL; ++e) {
+        const int pc = (p0 + LPT * e) ^ (8 * (t & 1));
+        const uint4 kv = Y.k[t * 16 + pc], qv = Y.q[t * 16 + pc];
+        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // bf16 pair dot products, fp32 accumulation
+          sk = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kw[i]), __builtin_bit_cast(bf16x2_t, kw[i]), sk,
+                                               false);
+          sq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw[i]), __builtin_bit_cast(bf16x2_t, qw[i]), sq,
+                                               false);
+        }
+      }
+#pragma unroll
+      for (int m = 1; m < LPT; m <<= 1) {
+        sk += __shfl_xor(sk, m, kWave);
+        sq += __shfl_xor(sq, m, kWave);
+      }
+      if (ptid % LPT == 0) {
+        pp.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
+        pp.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
+      }
+    }
+    if (pw == kNP - 1) {  // decay cumsum; lane t: token t
+      const int64_t gi = (tokp + (lane < Lp ? lane : Lp - 1)) * a.HV + hv;
+      const float bt = lane < Lp ? gate_value(Y.gw[kC + lane], gi, a.beta_dt) : 0.f;
+      const float x = wave_prefix_sum(lane < Lp ? gate_value(Y.gw[lane], gi, a.g_dt) : 0.f);
+      pp.G[lane] = x;
+      pp.G2[lane] = x * 1.4426950408889634f;
+      pp.beta[lane] = bt;
+      if (lane == kWave - 1) pp.gl = x;
+    }
+#pragma unroll
+    for (int slot = 0; slot < kTPW; ++slot) {
+      const int ti = tile_of(slot);
+      if (ti < 10) kq_tile(Y, ti, kk[slot], qk[slot], r16, quad);
     }
   }
   lds_barrier();
 
-  // ---- P4: T diag(beta) of j as hi / lo over L (dead): rows 32-63 (with eight
-  // waves; rows 0-31 were converted in P3c), all rows with four ----
-  if constexpr (prep) {
-    constexpr int kR0 = NW == 8 ? 32 : 0;
-    constexpr int kTv = (kC - kR0) * kC / 4 / NT;  // float4 pieces of T per thread
+  // ---- P2 ----
+  if constexpr (PREP) {
+    if (pw == 0) {  // lane t: token t
+      const float eg = expf(pp.G[lane]);
+      Y.scal[lane] = eg * pp.rqs[lane];                           // output row scale of Q S
+      Y.scal[kC + lane] = pp.rk[lane] * expf(pp.gl - pp.G[lane]);  // state-update scale of v_new row t
+      Y.scal[2 * kC + lane] = -eg * pp.rk[lane];                  // row scale of K S inside -W S
+      if (lane == 0) Y.scal[3 * kC] = expf(pp.gl);
+    }
 #pragma unroll
-    for (int it = 0; it < kTv; ++it) t_hilo(Y, tf, pp, kR0 * kC + (it * NT + tid) * 4);
+    for (int slot = 0; slot < kTPW; ++slot) {
+      const int ti = tile_of(slot);
+      if (ti < 10) la_tile(Y, pp, ti, kk[slot], qk[slot], r16, quad);
+    }
   }
+  lds_barrier();
+
+  // ---- P3a ----
+  float* tf = X.vt.t;  // T of chunk j over X's V rows (dead since P2)
+  if constexpr (PREP) {
+    if (pw == 0) inv_diag(Y.tt.l, tf);
+    fdma_v<V, NW + 1, kNP - 1>(Y, a, tokp, Lp, hv);  // v of chunk j into Y (its rows held the previous T)
+  }
+  if (j + 1 < nch) fdma_q<NW + 1, kNP - 1>(X, a, tokp + kC, Ln, hk);  // X's Q was read for the last time in P1
+  lds_barrier();
+
+  // ---- P3b ----
+  if constexpr (PREP)
+    if (pw < 2) inv_level1(Y.tt.l, tf, pw);
+  if (j + 1 < nch) {  // X's K was read for the last time in P3a, its gate words in the previous iteration
+    fdma_k<NW, kNP>(X, a, tokp + kC, Ln, hk);
+    fdma_g<NW + 2>(X, a, tokp + kC, Ln, hv);
+  }
+  lds_barrier();
+
+  // ---- P3c ----
+  if constexpr (PREP) inv_level2(Y.tt.l, tf, pw);
+  lds_barrier();
+
+  // ---- P4 ----
   dma_wait();     // the copies into Y (v of j) and X (q, k, gates of j + 1) have landed
   lds_barrier();  // chunk j is ready; X may be reused as chunk j + 1's buffer
 }
 
+// NW scan waves (value columns 16 w .. 16 w + 15 each, the state in registers)
+// and kNP prep waves.
 template <int NW>
-__global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
+__global__ void __launch_bounds__((NW + kNP) * 64) chunk_fused_kernel(FusedArgs a) {
   __shared__ FBuf bufs[2];
   __shared__ FPrep pp;
-  constexpr int V = 16 * NW, NT = NW * 64;
+  constexpr int V = 16 * NW, NT = (NW + kNP) * 64;
   const int hv = blockIdx.x % a.HV;
   const int sidx = blockIdx.x / a.HV;
   const int n = a.order ? a.order[sidx] : sidx;
@@ -702,15 +748,6 @@ __global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
   const int64_t seq0 = a.cu[n];
   const int seqlen = a.cu[n + 1] - a.cu[n];
   const int nch = (seqlen + kC - 1) / kC;
-  const int vcol = 16 * w + r16;
-  // S[dt][i] = S[state_row(dt, quad, i)][vcol]
-  f32x4v S[8];
-  const int64_t sbase = (static_cast<int64_t>(n) * a.HV + hv) * kK;
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + state_row(dt, quad, i)) * V + vcol] : 0.f;
-  wait_vmem();  // the state has arrived before the loop
   // A's halves in the upper blocks (0, 1) and (2, 3) are read as zeros and
   // nothing else writes them: clear them once in both buffers
   for (int e = tid; e < 2 * 32 * 4; e += NT) {  // buffer, row (0..15 or 32..47), piece 0..3
@@ -718,26 +755,41 @@ __global__ void __launch_bounds__(NW * 64) chunk_fused_kernel(FusedArgs a) {
     const int t = rr < 16 ? rr : 16 + rr, p = t < 16 ? pc : 4 + pc;
     reinterpret_cast<uint2*>(&bufs[bsel].aqk[tpos(t, p)])[1] = make_uint2(0, 0);
   }
-  if (nch > 0) {
-    fdma_q<0, NW>(bufs[0], a, seq0, min(kC, seqlen), hk);
-    fdma_k<0, NW>(bufs[0], a, seq0, min(kC, seqlen), hk);
-    fdma_g<0>(bufs[0], a, seq0, min(kC, seqlen), hv);
-    dma_wait();
-  }
-  lds_barrier();
-  // (one loop body for both parities: its LDS addresses are the buffer's base
-  // plus per-lane offsets computed once)
   // the first iteration only prepares, the last only runs the products; the
   // ones between do both, with each phase one block of straight-line code
-  if (nch > 0) fused_iter<NW, true, false>(a, &bufs[0], &bufs[1], pp, S, 0, nch, seq0, seqlen, hv, hk);
+  if (w < NW) {
+    const int vcol = 16 * w + r16;
+    // S[dt][i] = S[state_row(dt, quad, i)][vcol]
+    f32x4v S[8];
+    const int64_t sbase = (static_cast<int64_t>(n) * a.HV + hv) * kK;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + state_row(dt, quad, i)) * V + vcol] : 0.f;
+    wait_vmem();  // the state has arrived before the loop
+    lds_barrier();  // (the prep waves' first copies)
+    if (nch > 0) scan_iter<NW, true, false>(a, &bufs[0], &bufs[1], pp, S, 0, seq0, seqlen, hv);
 #pragma unroll 1
-  for (int j = 1; j < nch; ++j)
-    fused_iter<NW, true, true>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, S, j, nch, seq0, seqlen, hv, hk);
-  if (nch > 0) fused_iter<NW, false, true>(a, &bufs[nch & 1], &bufs[(nch + 1) & 1], pp, S, nch, nch, seq0, seqlen, hv, hk);
+    for (int j = 1; j < nch; ++j)
+      scan_iter<NW, true, true>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, S, j, seq0, seqlen, hv);
+    if (nch > 0) scan_iter<NW, false, true>(a, &bufs[nch & 1], &bufs[(nch + 1) & 1], pp, S, nch, seq0, seqlen, hv);
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a.ht[(sbase + state_row(dt, quad, i)) * V + vcol] = S[dt][i];
+      for (int i = 0; i < 4; ++i) a.ht[(sbase + state_row(dt, quad, i)) * V + vcol] = S[dt][i];
+  } else {
+    if (nch > 0) {
+      fdma_q<NW, kNP>(bufs[0], a, seq0, min(kC, seqlen), hk);
+      fdma_k<NW, kNP>(bufs[0], a, seq0, min(kC, seqlen), hk);
+      fdma_g<NW>(bufs[0], a, seq0, min(kC, seqlen), hv);
+      dma_wait();
+    }
+    lds_barrier();
+    if (nch > 0) prep_iter<NW, true>(a, &bufs[0], &bufs[1], pp, 0, nch, seq0, seqlen, hv, hk);
+#pragma unroll 1
+    for (int j = 1; j < nch; ++j) prep_iter<NW, true>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, j, nch, seq0, seqlen, hv, hk);
+    if (nch > 0) prep_iter<NW, false>(a, &bufs[nch & 1], &bufs[(nch + 1) & 1], pp, nch, nch, seq0, seqlen, hv, hk);
+  }
 }
 
 }  // namespace
@@ -781,9 +833,9 @@ extern "C" int yh_gdn_chunk_varlen(const void* q, const void* k, const void* v, 
               (int)HV, scale, use_qk_l2norm ? 1 : 0, g_dtype, beta_dtype};
   const dim3 grid(static_cast<unsigned>(n_seqs * HV));
   if (V == 128)
-    hipLaunchKernelGGL(chunk_fused_kernel<8>, grid, dim3(512), 0, st, f);
+    hipLaunchKernelGGL(chunk_fused_kernel<8>, grid, dim3((8 + kNP) * 64), 0, st, f);
   else
-    hipLaunchKernelGGL(chunk_fused_kernel<4>, grid, dim3(256), 0, st, f);
+    hipLaunchKernelGGL(chunk_fused_kernel<4>, grid, dim3((4 + kNP) * 64), 0, st, f);
   YH_CHECK_LAUNCH("gdn_chunk");
   return YH_OK;
 }
