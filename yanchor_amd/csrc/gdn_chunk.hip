@@ -429,15 +429,30 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
 constexpr int kNP = 4;  // prep waves
 
 // K K^T / Q K^T tile ti (0..9, lower 16 x 16 blocks of the chunk) of Y,
-// transposed: [s][t] = k_s . k_t and k_s . q_t (lane: t, elements: 4 s) ...
-__device__ __forceinline__ void kq_tile(const FBuf& Y, int ti, f32x4v& kk, f32x4v& qk, int r16, int quad) {
+// transposed: [s][t] = k_s . k_t and k_s . q_t (lane: t, elements: 4 s).  A
+// diagonal tile (ti = 0, 2, 5, 9) also yields the squared L2 norms of its 16
+// keys (its diagonal) and, with Q Q^T on the same reads, of its queries: the
+// lane holding [t][t] writes rk[t] and rqs[t] (scale included).
+__device__ __forceinline__ void kq_tile(const FBuf& Y, FPrep& pp, const FusedArgs& a, int ti, f32x4v& kk, f32x4v& qk,
+                                        int r16, int quad) {
   kk = qk = f32x4v{0.f, 0.f, 0.f, 0.f};
   const int mt = lblock_row(ti), m0 = 16 * mt, n0 = 16 * (ti - mt * (mt + 1) / 2);
+  const bool diag = m0 == n0;  // uniform
+  f32x4v qq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const bf16x8_t as = lds_k(Y.k, n0 + r16, ks, quad);
+    const bf16x8_t bq = lds_k(Y.q, m0 + r16, ks, quad);
     kk = mfma(as, lds_k(Y.k, m0 + r16, ks, quad), kk);
-    qk = mfma(as, lds_k(Y.q, m0 + r16, ks, quad), qk);
+    qk = mfma(as, bq, qk);
+    if (diag) qq = mfma(bq, bq, qq);
+  }
+  if (diag && quad == (r16 >> 2)) {
+    const int e = r16 & 3;
+    const float k2 = e == 0 ? kk[0] : e == 1 ? kk[1] : e == 2 ? kk[2] : kk[3];
+    const float q2 = e == 0 ? qq[0] : e == 1 ? qq[1] : e == 2 ? qq[2] : qq[3];
+    pp.rk[m0 + r16] = a.l2 ? rsqrtf(k2 + 1e-6f) : 1.f;
+    pp.rqs[m0 + r16] = (a.l2 ? rsqrtf(q2 + 1e-6f) : 1.f) * a.scale;
   }
 }
 // ... and its L and A entries: row t = m0 + r16, columns s = n0 + 4 quad + 0..3
@@ -471,12 +486,12 @@ __device__ __forceinline__ void la_tile(FBuf& Y, const FPrep& pp, int ti, const 
 // products are live on the scan waves only, the prep tiles on the prep waves.
 
 // Scan waves 0 .. NW - 1: value columns 16 w .. 16 w + 15, the state in
-// registers.  P1 Q S, K S of j - 1; tile w of j | P2 v_new; L, A of tile w
-// | P3a state update | P3b output | P3c, P4 T diag(beta) of j as bf16 hi / lo
-// (rows 0-31, rows 32-63).
+// registers.  P1 Q S, K S of j - 1; tile w of j | P2 v_new; L, A of tile w;
+// copy v of j into Y (waves 0-3) | P3a state update | P3b output | P3c its
+// stores; T diag(beta) rows 0-31 of j as bf16 hi / lo | P4 rows 32-63.
 template <int NW, bool PREP, bool SCAN>
 __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
-                                          const FPrep& pp, f32x4v (&S)[8], int j, int64_t seq0, int seqlen,
+                                          FPrep& pp, f32x4v (&S)[8], int j, int64_t seq0, int seqlen,
                                           int hv) {
   FBuf& Y = *Yp;
   FBuf& X = *Xp;
@@ -490,7 +505,7 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
 
   // ---- P1 ----
   f32x4v kk, qk;
-  if constexpr (PREP) kq_tile(Y, w, kk, qk, r16, quad);  // tile w of chunk j
+  if constexpr (PREP) kq_tile(Y, pp, a, w, kk, qk, r16, quad);  // tile w of chunk j
   f32x4v qs[4], ps[4];
   if constexpr (SCAN) {
 #pragma unroll
@@ -512,7 +527,10 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
   lds_barrier();
 
   // ---- P2 ----
-  if constexpr (PREP) la_tile(Y, pp, w, kk, qk, r16, quad);
+  if constexpr (PREP) {
+    la_tile(Y, pp, w, kk, qk, r16, quad);
+    fdma_v<V, 0, 4>(Y, a, seq0 + static_cast<int64_t>(j) * kC, min(kC, seqlen - j * kC), hv);  // v of j into Y (over the previous T)
+  }
   f32x4v vn[4];
   if constexpr (SCAN) {
     bf16x8_t vb[2], ph[2], pl[2];
@@ -576,7 +594,9 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
   lds_barrier();
 
   // ---- P3b: o^T = (Q S)^T diag(orow) + v_new^T A^T: lane (r16, quad) holds
-  // value columns 16 w + 4 quad .. + 3 of token 16 mt + r16, stored as 8 bytes ----
+  // value columns 16 w + 4 quad .. + 3 of token 16 mt + r16 (8 bytes, stored in
+  // P3c, when the memory pipeline is free of the prep waves' copies) ----
+  uint2 ov[4];
   if constexpr (SCAN) {
     bf16x8_t vnb[2];
 #pragma unroll
@@ -586,8 +606,6 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
       vnb[ks] = round8v(x);
     }
     typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-    uint16_t* orow = a.o + ((toks + r16) * a.HV + hv) * V + 16 * w + rq4;  // token r16 of the chunk
-    const int64_t ostep = static_cast<int64_t>(16) * a.HV * V;             // 16 tokens
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int t = 16 * mt + r16;
@@ -595,14 +613,20 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         if (32 * ks <= 16 * mt + 15) acc = mfma(vnb[ks], lds_t(X.aqk, t, ks, quad), acc);
-      if (t < Ls)
-        *reinterpret_cast<uint2*>(orow + mt * ostep) = __builtin_bit_cast(uint2, __builtin_convertvector(acc, bf16x4_t));
+      ov[mt] = __builtin_bit_cast(uint2, __builtin_convertvector(acc, bf16x4_t));
     }
   }
   lds_barrier();
 
   // ---- P3c: T diag(beta) rows 0-31 of chunk j (final after P3b) as hi / lo
   // over L's dead rows 0-31 ----
+  if constexpr (SCAN) {
+    uint16_t* orow = a.o + ((toks + r16) * a.HV + hv) * V + 16 * w + rq4;  // token r16 of the chunk
+    const int64_t ostep = static_cast<int64_t>(16) * a.HV * V;             // 16 tokens
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      if (16 * mt + r16 < Ls) *reinterpret_cast<uint2*>(orow + mt * ostep) = ov[mt];
+  }
   const float* tf = X.vt.t;
   if constexpr (PREP) {
 #pragma unroll
@@ -615,14 +639,15 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
 #pragma unroll
     for (int it = 0; it < 512 / NS; ++it) t_hilo(Y, tf, pp, 32 * kC + (it * NS + tid) * 4);
   }
+  dma_wait();     // the copy of v of j has landed
   lds_barrier();  // chunk j is ready; X may be reused as chunk j + 1's buffer
 }
 
-// Prep waves NW .. NW + kNP - 1, chunk j in Y: P1 L2 norms, decay cumsum,
-// K K^T / Q K^T tiles NW..9 | P2 their L, A; the scalings | P3a the
-// inverse's diagonal blocks (T over X's V rows, dead since P2); copy v of j
-// into Y and q of j + 1 into X | P3b its first level; copy k and gates of
-// j + 1 into X | P3c its second level | P4 wait for the copies.
+// Prep waves NW .. NW + kNP - 1, chunk j in Y: P1 decay cumsum, K K^T / Q K^T
+// tiles NW..9 | P2 their L, A; the scalings | P3a the inverse's diagonal
+// blocks (T over X's V rows, dead since P2); copy q of j + 1 into X | P3b its
+// first level; copy k and gates of j + 1 into X | P3c its second level | P4
+// wait for the copies.  (The L2 norms come from the diagonal tiles.)
 template <int NW, bool PREP>
 __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
                                           FPrep& pp, int j, int nch, int64_t seq0, int seqlen, int hv, int hk) {
@@ -642,35 +667,6 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
   // ---- P1 ----
   f32x4v kk[kTPW], qk[kTPW];
   if constexpr (PREP) {
-    {  // L2 norms: LPT lanes per token, each over 16 / LPT stored pieces of its row
-       // (a sum over the whole row: the piece order does not matter; tokens
-       // of odd rank start in the other 128-byte half of their row)
-      constexpr int LPT = kNP * 64 / kC, PPL = 16 / LPT;
-      const int t = ptid / LPT, p0 = ptid % LPT;
-      float sk = 0.f, sq = 0.f;
-#pragma unroll
-      for (int e = 0; e < PPL; ++e) {
-        const int pc = (p0 + LPT * e) ^ (8 * (t & 1));
-        const uint4 kv = Y.k[t * 16 + pc], qv = Y.q[t * 16 + pc];
-        const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // bf16 pair dot products, fp32 accumulation
-          sk = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kw[i]), __builtin_bit_cast(bf16x2_t, kw[i]), sk,
-                                               false);
-          sq = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw[i]), __builtin_bit_cast(bf16x2_t, qw[i]), sq,
-                                               false);
-        }
-      }
-#pragma unroll
-      for (int m = 1; m < LPT; m <<= 1) {
-        sk += __shfl_xor(sk, m, kWave);
-        sq += __shfl_xor(sq, m, kWave);
-      }
-      if (ptid % LPT == 0) {
-        pp.rk[t] = a.l2 ? rsqrtf(sk + 1e-6f) : 1.f;
-        pp.rqs[t] = (a.l2 ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-      }
-    }
     if (pw == kNP - 1) {  // decay cumsum; lane t: token t
       const int64_t gi = (tokp + (lane < Lp ? lane : Lp - 1)) * a.HV + hv;
       const float bt = lane < Lp ? gate_value(Y.gw[kC + lane], gi, a.beta_dt) : 0.f;
@@ -683,7 +679,7 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
 #pragma unroll
     for (int slot = 0; slot < kTPW; ++slot) {
       const int ti = tile_of(slot);
-      if (ti < 10) kq_tile(Y, ti, kk[slot], qk[slot], r16, quad);
+      if (ti < 10) kq_tile(Y, pp, a, ti, kk[slot], qk[slot], r16, quad);
     }
   }
   lds_barrier();
@@ -709,7 +705,6 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
   float* tf = X.vt.t;  // T of chunk j over X's V rows (dead since P2)
   if constexpr (PREP) {
     if (pw == 0) inv_diag(Y.tt.l, tf);
-    fdma_v<V, NW + 1, kNP - 1>(Y, a, tokp, Lp, hv);  // v of chunk j into Y (its rows held the previous T)
   }
   if (j + 1 < nch) fdma_q<NW + 1, kNP - 1>(X, a, tokp + kC, Ln, hk);  // X's Q was read for the last time in P1
   lds_barrier();
@@ -718,7 +713,7 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
   if constexpr (PREP)
     if (pw < 2) inv_level1(Y.tt.l, tf, pw);
   if (j + 1 < nch) {  // X's K was read for the last time in P3a, its gate words in the previous iteration
-    fdma_k<NW, kNP>(X, a, tokp + kC, Ln, hk);
+    fdma_k<NW + 2, 2>(X, a, tokp + kC, Ln, hk);
     fdma_g<NW + 2>(X, a, tokp + kC, Ln, hv);
   }
   lds_barrier();
