@@ -344,7 +344,7 @@ __device__ __forceinline__ void fdma_g(FBuf& b, const FusedArgs& a, int64_t tok0
 //               block inverse, with Y = C A^{-1}: T_20 = -T_22 Y_00,
 //               T_21 = -T_22 Y_01, T_30 = -(T_32 Y_00 + T_33 Y_10),
 //               T_31 = -(T_32 Y_01 + T_33 Y_11) (one wave each, Y recomputed
-//               where needed).
+//               where needed; _pre / _fin split at the first level).
 // The block products run on fp32 MFMA.
 __device__ __forceinline__ void inv_diag(const float* l, float* t) {  // one wave
   const int lane = threadIdx.x & 63;
@@ -371,18 +371,28 @@ __device__ __forceinline__ void inv_level1(const float* l, float* t, int u) {  /
   acc_tx(o, t, i, i, x, r, g);
   put_block(t, i, j, o, r, g);
 }
-__device__ __forceinline__ void inv_level2(const float* l, float* t, int u) {  // u = 0..3: T_20, T_21, T_30, T_31
+// The second level in two parts, so that the products that need only the
+// diagonal blocks run a phase earlier: inv_level2_pre forms Y_0j's (and, for
+// block row 3, Y_1j's) terms with T_00 or T_11, inv_level2_fin adds the terms
+// with T_10 and forms the block.
+__device__ __forceinline__ void inv_level2_pre(const float* l, const float* t, int u, f32x4v& y0, f32x4v& y1) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int i = 2 + (u >> 1), j = u & 1;
-  f32x4v y0 = {0.f, 0.f, 0.f, 0.f}, o = {0.f, 0.f, 0.f, 0.f};
-  if (j == 0) acc_lt(y0, l, t, 2, 0, 0, r, g);
-  acc_lt(y0, l, t, 2, 1, j, r, g);
+  y0 = y1 = f32x4v{0.f, 0.f, 0.f, 0.f};
+  acc_lt(y0, l, t, 2, j, j, r, g);  // L_20 T_00 or L_21 T_11
+  if (i == 3) acc_lt(y1, l, t, 3, j, j, r, g);
+}
+__device__ __forceinline__ void inv_level2_fin(const float* l, float* t, int u, f32x4v& y0, f32x4v& y1) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int i = 2 + (u >> 1), j = u & 1;
+  f32x4v o = {0.f, 0.f, 0.f, 0.f};
+  if (j == 0) {
+    acc_lt(y0, l, t, 2, 1, 0, r, g);  // + L_21 T_10
+    if (i == 3) acc_lt(y1, l, t, 3, 1, 0, r, g);
+  }
   if (i == 2) {
     acc_tx(o, t, 2, 2, y0, r, g);
   } else {
-    f32x4v y1 = {0.f, 0.f, 0.f, 0.f};
-    if (j == 0) acc_lt(y1, l, t, 3, 0, 0, r, g);
-    acc_lt(y1, l, t, 3, 1, j, r, g);
     acc_tx(o, t, 3, 2, y0, r, g);
     acc_tx(o, t, 3, 3, y1, r, g);
   }
@@ -594,9 +604,9 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
   lds_barrier();
 
   // ---- P3b: o^T = (Q S)^T diag(orow) + v_new^T A^T: lane (r16, quad) holds
-  // value columns 16 w + 4 quad .. + 3 of token 16 mt + r16 (8 bytes, stored in
-  // P3c, when the memory pipeline is free of the prep waves' copies) ----
-  uint2 ov[4];
+  // value columns 16 w + 4 quad .. + 3 of token 16 mt + r16.  The tile is staged
+  // row-major in X's T hi / lo storage (read for the last time in P2), 16-byte
+  // piece p of row t at p ^ (t % 16), and stored as whole rows in P3c ----
   if constexpr (SCAN) {
     bf16x8_t vnb[2];
 #pragma unroll
@@ -613,19 +623,22 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         if (32 * ks <= 16 * mt + 15) acc = mfma(vnb[ks], lds_t(X.aqk, t, ks, quad), acc);
-      ov[mt] = __builtin_bit_cast(uint2, __builtin_convertvector(acc, bf16x4_t));
+      uint2* st = reinterpret_cast<uint2*>(&X.tt.p[t * (V / 8) + (((4 * w + quad) >> 1) ^ (r16 & (V / 8 - 1)))]);
+      st[quad & 1] = __builtin_bit_cast(uint2, __builtin_convertvector(acc, bf16x4_t));
     }
   }
   lds_barrier();
 
   // ---- P3c: T diag(beta) rows 0-31 of chunk j (final after P3b) as hi / lo
   // over L's dead rows 0-31 ----
-  if constexpr (SCAN) {
-    uint16_t* orow = a.o + ((toks + r16) * a.HV + hv) * V + 16 * w + rq4;  // token r16 of the chunk
-    const int64_t ostep = static_cast<int64_t>(16) * a.HV * V;             // 16 tokens
+  if constexpr (SCAN) {  // whole output rows, 16 bytes a lane
+    constexpr int PPR = V / 8, RPI = kWave / PPR;  // pieces a row, rows an instruction
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      if (16 * mt + r16 < Ls) *reinterpret_cast<uint2*>(orow + mt * ostep) = ov[mt];
+    for (int it = 0; it < kC / (RPI * NW); ++it) {
+      const int t = (it * NW + w) * RPI + lane / PPR, pc = lane % PPR;
+      const uint4 val = X.tt.p[t * PPR + (pc ^ (t & (PPR - 1)))];
+      if (t < Ls) *reinterpret_cast<uint4*>(a.o + ((toks + t) * a.HV + hv) * V + 8 * pc) = val;
+    }
   }
   const float* tf = X.vt.t;
   if constexpr (PREP) {
@@ -710,8 +723,11 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
   lds_barrier();
 
   // ---- P3b ----
-  if constexpr (PREP)
+  f32x4v y0, y1;
+  if constexpr (PREP) {
     if (pw < 2) inv_level1(Y.tt.l, tf, pw);
+    inv_level2_pre(Y.tt.l, tf, pw, y0, y1);
+  }
   if (j + 1 < nch) {  // X's K was read for the last time in P3a, its gate words in the previous iteration
     fdma_k<NW + 2, 2>(X, a, tokp + kC, Ln, hk);
     fdma_g<NW + 2>(X, a, tokp + kC, Ln, hv);
@@ -719,7 +735,7 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
   lds_barrier();
 
   // ---- P3c ----
-  if constexpr (PREP) inv_level2(Y.tt.l, tf, pw);
+  if constexpr (PREP) inv_level2_fin(Y.tt.l, tf, pw, y0, y1);
   lds_barrier();
 
   // ---- P4 ----
