@@ -496,13 +496,14 @@ __device__ __forceinline__ void la_tile(FBuf& Y, const FPrep& pp, int ti, const 
 // products are live on the scan waves only, the prep tiles on the prep waves.
 
 // Scan waves 0 .. NW - 1: value columns 16 w .. 16 w + 15, the state in
-// registers.  P1 Q S, K S of j - 1; tile w of j | P2 v_new; L, A of tile w;
-// copy v of j into Y (waves 0-3) | P3a state update | P3b output | P3c its
-// stores; T diag(beta) rows 0-31 of j as bf16 hi / lo | P4 rows 32-63.
+// registers.  P1 Q S, K S of j - 1; tile w of j (waves 0-3) | P2 v_new; L, A
+// of tile w; copy v of j into Y (waves 0-3) | P3a state update | P3b output,
+// staged; copy k of j + 1 into X (waves 0-3) | P3c its stores; T diag(beta)
+// rows 0-31 of j as bf16 hi / lo | P4 rows 32-63.
 template <int NW, bool PREP, bool SCAN>
 __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
-                                          FPrep& pp, f32x4v (&S)[8], int j, int64_t seq0, int seqlen,
-                                          int hv) {
+                                          FPrep& pp, f32x4v (&S)[8], int j, int nch, int64_t seq0, int seqlen,
+                                          int hv, int hk) {
   FBuf& Y = *Yp;
   FBuf& X = *Xp;
   constexpr int V = 16 * NW, NS = NW * 64;
@@ -515,7 +516,8 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
 
   // ---- P1 ----
   f32x4v kk, qk;
-  if constexpr (PREP) kq_tile(Y, pp, a, w, kk, qk, r16, quad);  // tile w of chunk j
+  if constexpr (PREP)
+    if (w < 4) kq_tile(Y, pp, a, w, kk, qk, r16, quad);  // tile w of chunk j (the first wave of each SIMD)
   f32x4v qs[4], ps[4];
   if constexpr (SCAN) {
 #pragma unroll
@@ -538,7 +540,7 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
 
   // ---- P2 ----
   if constexpr (PREP) {
-    la_tile(Y, pp, w, kk, qk, r16, quad);
+    if (w < 4) la_tile(Y, pp, w, kk, qk, r16, quad);
     fdma_v<V, 0, 4>(Y, a, seq0 + static_cast<int64_t>(j) * kC, min(kC, seqlen - j * kC), hv);  // v of j into Y (over the previous T)
   }
   f32x4v vn[4];
@@ -627,6 +629,8 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
       st[quad & 1] = __builtin_bit_cast(uint2, __builtin_convertvector(acc, bf16x4_t));
     }
   }
+  if (j + 1 < nch)  // k of chunk j + 1 into X (X's K was read for the last time in P3a)
+    fdma_k<0, 4>(X, a, seq0 + static_cast<int64_t>(j + 1) * kC, min(kC, seqlen - (j + 1) * kC), hk);
   lds_barrier();
 
   // ---- P3c: T diag(beta) rows 0-31 of chunk j (final after P3b) as hi / lo
@@ -657,22 +661,23 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
 }
 
 // Prep waves NW .. NW + kNP - 1, chunk j in Y: P1 decay cumsum, K K^T / Q K^T
-// tiles NW..9 | P2 their L, A; the scalings | P3a the inverse's diagonal
+// tiles 4..9 | P2 their L, A; the scalings | P3a the inverse's diagonal
 // blocks (T over X's V rows, dead since P2); copy q of j + 1 into X | P3b its
-// first level; copy k and gates of j + 1 into X | P3c its second level | P4
-// wait for the copies.  (The L2 norms come from the diagonal tiles.)
+// first level and the second level's products with the diagonal blocks;
+// copy the gates of j + 1 into X | P3c the second level | P4 wait for the
+// copies.  (The L2 norms come from the diagonal tiles.)
 template <int NW, bool PREP>
 __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
                                           FPrep& pp, int j, int nch, int64_t seq0, int seqlen, int hv, int hk) {
   FBuf& Y = *Yp;
   FBuf& X = *Xp;
   constexpr int V = 16 * NW, NS = NW * 64;
-  constexpr int kTPW = (10 - NW + kNP - 1) / kNP;  // tiles NW..9, from prep wave 1 on
+  constexpr int kTPW = (10 - 4 + kNP - 1) / kNP;  // tiles 4..9, from prep wave 1 on
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pw = w - NW, ptid = tid - NS;
-  auto tile_of = [&](int slot) { return NW + (pw + kNP - 1) % kNP + kNP * slot; };
+  auto tile_of = [&](int slot) { return 4 + (pw + kNP - 1) % kNP + kNP * slot; };
   const int r16 = lane & 15, quad = lane >> 4, rq4 = quad * 4;
   const int64_t tokp = seq0 + static_cast<int64_t>(j) * kC;
   const int Lp = min(kC, seqlen - j * kC), Ln = min(kC, seqlen - (j + 1) * kC);
@@ -728,10 +733,7 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
     if (pw < 2) inv_level1(Y.tt.l, tf, pw);
     inv_level2_pre(Y.tt.l, tf, pw, y0, y1);
   }
-  if (j + 1 < nch) {  // X's K was read for the last time in P3a, its gate words in the previous iteration
-    fdma_k<NW + 2, 2>(X, a, tokp + kC, Ln, hk);
-    fdma_g<NW + 2>(X, a, tokp + kC, Ln, hv);
-  }
+  if (j + 1 < nch) fdma_g<NW + 2>(X, a, tokp + kC, Ln, hv);  // X's gate words were read in the previous iteration
   lds_barrier();
 
   // ---- P3c ----
@@ -779,11 +781,11 @@ __global__ void __launch_bounds__((NW + kNP) * 64) chunk_fused_kernel(FusedArgs 
       for (int i = 0; i < 4; ++i) S[dt][i] = a.h0 ? a.h0[(sbase + state_row(dt, quad, i)) * V + vcol] : 0.f;
     wait_vmem();  // the state has arrived before the loop
     lds_barrier();  // (the prep waves' first copies)
-    if (nch > 0) scan_iter<NW, true, false>(a, &bufs[0], &bufs[1], pp, S, 0, seq0, seqlen, hv);
+    if (nch > 0) scan_iter<NW, true, false>(a, &bufs[0], &bufs[1], pp, S, 0, nch, seq0, seqlen, hv, hk);
 #pragma unroll 1
     for (int j = 1; j < nch; ++j)
-      scan_iter<NW, true, true>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, S, j, seq0, seqlen, hv);
-    if (nch > 0) scan_iter<NW, false, true>(a, &bufs[nch & 1], &bufs[(nch + 1) & 1], pp, S, nch, seq0, seqlen, hv);
+      scan_iter<NW, true, true>(a, &bufs[j & 1], &bufs[(j + 1) & 1], pp, S, j, nch, seq0, seqlen, hv, hk);
+    if (nch > 0) scan_iter<NW, false, true>(a, &bufs[nch & 1], &bufs[(nch + 1) & 1], pp, S, nch, nch, seq0, seqlen, hv, hk);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
