@@ -498,7 +498,7 @@ __device__ __forceinline__ void la_tile(FBuf& Y, const FPrep& pp, int ti, const 
 // Scan waves 0 .. NW - 1: value columns 16 w .. 16 w + 15, the state in
 // registers.  P1 Q S, K S of j - 1; tile w of j (waves 0-3) | P2 v_new; L, A
 // of tile w; copy v of j into Y (waves 0-3) | P3a state update | P3b output,
-// staged; copy k of j + 1 into X (waves 0-3) | P3c its stores; T diag(beta)
+// staged; copy k of j + 1 into X | P3c its stores; T diag(beta)
 // rows 0-31 of j as bf16 hi / lo | P4 rows 32-63.
 template <int NW, bool PREP, bool SCAN>
 __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__ Yp, FBuf* __restrict__ Xp,
@@ -630,7 +630,7 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
     }
   }
   if (j + 1 < nch)  // k of chunk j + 1 into X (X's K was read for the last time in P3a)
-    fdma_k<0, 4>(X, a, seq0 + static_cast<int64_t>(j + 1) * kC, min(kC, seqlen - (j + 1) * kC), hk);
+    fdma_k<0, NW>(X, a, seq0 + static_cast<int64_t>(j + 1) * kC, min(kC, seqlen - (j + 1) * kC), hk);
   lds_barrier();
 
   // ---- P3c: T diag(beta) rows 0-31 of chunk j (final after P3b) as hi / lo
@@ -672,12 +672,15 @@ __device__ __forceinline__ void prep_iter(const FusedArgs& a, FBuf* __restrict__
   FBuf& Y = *Yp;
   FBuf& X = *Xp;
   constexpr int V = 16 * NW, NS = NW * 64;
-  constexpr int kTPW = (10 - 4 + kNP - 1) / kNP;  // tiles 4..9, from prep wave 1 on
+  constexpr int kTPW = 2;  // tiles per prep wave
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pw = w - NW, ptid = tid - NS;
-  auto tile_of = [&](int slot) { return 4 + (pw + kNP - 1) % kNP + kNP * slot; };
+  // tiles 4..9: one diagonal tile (5, 9) on each of the two waves with two tiles
+  auto tile_of = [&](int slot) {
+    return slot == 0 ? (pw == 0 ? 4 : pw == 1 ? 5 : pw == 2 ? 9 : 8) : (pw == 1 ? 6 : pw == 2 ? 7 : 10);
+  };
   const int r16 = lane & 15, quad = lane >> 4, rq4 = quad * 4;
   const int64_t tokp = seq0 + static_cast<int64_t>(j) * kC;
   const int Lp = min(kC, seqlen - j * kC), Ln = min(kC, seqlen - (j + 1) * kC);
