@@ -12,19 +12,24 @@
 //
 // T and A = Q K^T o Gamma do not depend on the state S.  One kernel,
 // chunk_fused_kernel, runs one workgroup per (sequence, value head) that walks
-// the sequence's chunks with the 128 x V fp32 state in MFMA accumulators (wave
-// w owns value columns 16w..16w+15) and prepares chunk j (norms, decays, K K^T
-// and Q K^T, the fp32 inverse T on MFMA block products, A, the scalings) while
-// it runs the state-dependent products of chunk j - 1 (Q S and W S, v_new, o,
-// the state update, with S and v_new never leaving registers).  Only q, k, v,
-// the gates, o and the states cross HBM.
+// the sequence's chunks.  Eight scan waves hold the 128 x V fp32 state in MFMA
+// accumulators (wave w owns value columns 16w..16w+15) and run the
+// state-dependent products of chunk j - 1 (Q S and K S, v_new, o, the state
+// update, with S and v_new never leaving registers) while four prep waves
+// (with help from the scan waves where those have time to spare) prepare chunk
+// j: decays, K K^T and Q K^T with the L2 norms from their diagonals, the fp32
+// inverse T on MFMA block products, A, the scalings.  Only q, k, v, the gates,
+// o and the states cross HBM.
 // Per-token L2 norms, beta and decays are diagonal factors, so products with
 // the raw q / k / v tensors take exact bf16 MFMA operands and the factors go
 // into the epilogues or the fp32 operand.  Products whose operands are fp32 on
-// chip (T, W, the state, v_new) split each fp32 operand into bf16 hi + lo and
+// chip (T, the state, v_new) split each fp32 operand into bf16 hi + lo and
 // accumulate 2 or 3 MFMA passes (hi.hi, hi.lo, lo.hi), which keeps the state
-// path near fp32 accuracy; the output-only products Q S and A v_new take one
-// pass.
+// path near fp32 accuracy (every pass is needed: dropping any one of them
+// raises the final-state error to 3e-4 .. 1e-3 on slowly decaying inputs);
+// v_new is evaluated as T diag(beta) (V - diag(e^G) K S) with the difference
+// formed in fp32 and split once.  The output-only products Q S and A v_new
+// take one pass.
 #include "common.h"
 
 namespace yh {
@@ -545,31 +550,37 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
   }
   f32x4v vn[4];
   if constexpr (SCAN) {
-    bf16x8_t vb[2], ph[2], pl[2];
+    // v_new = T diag(beta) (V - W' S), W' S = diag(e^G rk) K S: D = V + (-scaled K S)
+    // in fp32 (V from its bf16 rows, in the accumulator row order), split once
+    // into bf16 hi / lo, then three passes T_hi D_hi + T_hi D_lo + T_lo D_hi
+    bf16x8_t dh[2], dl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      vb[ks] = lds8t(X.vt.v, 32 * ks, 16 * w, lane);
-      f32x4v p0 = ps[2 * ks], p1 = ps[2 * ks + 1];
+      const uint4 vw = __builtin_bit_cast(uint4, lds8t(X.vt.v, 32 * ks, 16 * w, lane));
+      const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+      const f32x4v p0 = ps[2 * ks], p1 = ps[2 * ks + 1];
+      float d[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p0[i] *= X.scal[2 * kC + 32 * ks + rq4 + i];
-        p1[i] *= X.scal[2 * kC + 32 * ks + 16 + rq4 + i];
+        const uint32_t w0 = vv[i >> 1], w1 = vv[2 + (i >> 1)];
+        const float v0 = __uint_as_float((i & 1) ? (w0 & 0xffff0000u) : (w0 << 16));
+        const float v1 = __uint_as_float((i & 1) ? (w1 & 0xffff0000u) : (w1 << 16));
+        d[i] = fmaf(p0[i], X.scal[2 * kC + 32 * ks + rq4 + i], v0);
+        d[4 + i] = fmaf(p1[i], X.scal[2 * kC + 32 * ks + 16 + rq4 + i], v1);
       }
-      pack_b(p0, p1, ph[ks], pl[ks]);
+      split8(d, dh[ks], dl[ks]);
     }
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {  // v_new = T diag(beta) V + T diag(beta) (-W S scaled rows)
+    for (int mt = 0; mt < 4; ++mt) {
       f32x4v u = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};  // two chains: the MFMA latency stays hidden
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         if (32 * ks <= 16 * mt + 15) {
           const bf16x8_t th = __builtin_bit_cast(bf16x8_t, X.tt.p[thi(16 * mt + r16, 4 * ks + quad)]);
           const bf16x8_t tl = __builtin_bit_cast(bf16x8_t, X.tt.p[tlo(16 * mt + r16, 4 * ks + quad)]);
-          u = mfma(th, vb[ks], u);
-          u = mfma(tl, vb[ks], u);
-          y = mfma(th, ph[ks], y);
-          y = mfma(th, pl[ks], y);
-          y = mfma(tl, ph[ks], y);
+          u = mfma(th, dh[ks], u);
+          u = mfma(th, dl[ks], u);
+          y = mfma(tl, dh[ks], y);
         }
       }
       vn[mt] = u + y;
