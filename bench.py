@@ -70,7 +70,7 @@ TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this kernel a
                   "copy-kernel factors (FETCH x 2.0, WRITE x 1.0); a constant, not measured in this run")
 # The same for one call of the chunked prefill (``--workload gdn_prefill``,
 # chunk_fused_kernel).
-TRAFFIC_PREFILL = (2074380.0 * 2.0 + 1341740.0) * 1024
+TRAFFIC_PREFILL = (2074512.6 * 2.0 + 1341736.0) * 1024
 # The same for one anchor read (``--workload anchor_read``, 64 x 32 x 256 x 128).
 TRAFFIC_ANCHOR_READ = (98017.4 * 2.0 + 512.0) * 1024
 
