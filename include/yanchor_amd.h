@@ -115,7 +115,8 @@ int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* conv_state,
  * torch_chunk_gated_delta_rule (same file, 234-311).
  *
  *   q, k [total_tokens, H, 128] bf16; v, o [total_tokens, HV, V] bf16 (V 64 or
- *   128); g, beta [total_tokens, HV] (f32 / bf16 / f16); cu_seqlens int32
+ *   128; q, k, v and o 16-byte aligned); g, beta [total_tokens, HV] (f32 / bf16
+ *   / f16); cu_seqlens int32
  *   [n_seqs + 1] (cu_seqlens[n_seqs] <= total_tokens)
  *   initial_state NULL (zeros) or fp32 [n_seqs, HV, 128, V] (read only)
  *   final_state fp32 [n_seqs, HV, 128, V] (written)
