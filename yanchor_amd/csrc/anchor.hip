@@ -90,6 +90,7 @@ __device__ __forceinline__ void load8(const void* p, int64_t i, float* f) {
   }
 }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // Raw 8 elements (16 B for 2-byte types, 32 B for fp32) of a key/value row.
 template <int DT> struct Raw8 { uint4 w[DT == YH_F32 ? 2 : 1]; };
 
@@ -123,7 +124,11 @@ __device__ __forceinline__ float dot8(const Raw8<DT>& a, const Raw8<DT>& b) {
 
 // The NI rows of one block: row pointer p (this lane's 8 elements of the
 // block's first row), rows `stride` elements apart -- constant offsets from
-// one base, so the loads need no per-row address registers.
+// one base, so the loads need no per-row address registers.  Key and value
+// rows are read once per token: the loads are nontemporal, so they stream
+// past the caches instead of evicting what the other kernels of the step
+// reuse (measured: 39.1 -> 34.5 us for 64 rows x 32 memories x 256 slots,
+// 103 -> 95 us for the 1024-slot window ring at 128 rows x 8 groups).
 template <int DT, int NI, int STRIDE>
 __device__ __forceinline__ void ld_block(Raw8<DT> (&r)[NI], const void* p) {
   constexpr int kEsz = DT == YH_F32 ? 4 : 2;
@@ -131,8 +136,11 @@ __device__ __forceinline__ void ld_block(Raw8<DT> (&r)[NI], const void* p) {
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
 #pragma unroll
-    for (int j = 0; j < (DT == YH_F32 ? 2 : 1); ++j)
-      r[i].w[j] = *reinterpret_cast<const uint4*>(c + static_cast<int64_t>(i) * STRIDE * kEsz + j * 16);
+    for (int j = 0; j < (DT == YH_F32 ? 2 : 1); ++j) {
+      const u32x4_t v = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(c + static_cast<int64_t>(i) * STRIDE * kEsz + j * 16));
+      r[i].w[j] = make_uint4(v.x, v.y, v.z, v.w);
+    }
   }
 }
 
@@ -141,9 +149,8 @@ __device__ __forceinline__ void ld_block(Raw8<DT> (&r)[NI], const void* p) {
 // byte offset slot * D * esize + lane_byte_off); entries past n get an offset
 // past the resource's num_records, which the buffer load answers with zeros
 // and no memory request (no branch: the load stream and its wait counts are
-// those of a full block).
+// those of a full block).  Cache policy 2 = nontemporal, as in ld_block.
 constexpr int kDeadOffset = 0x7ffffff0;
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 template <int DT, int NI, int D, int RPI>
 __device__ __forceinline__ void ld_block_list(Raw8<DT> (&r)[NI], __amdgpu_buffer_rsrc_t rsrc, const uint16_t* lid,
@@ -155,7 +162,7 @@ __device__ __forceinline__ void ld_block_list(Raw8<DT> (&r)[NI], __amdgpu_buffer
     const int o = e < n ? static_cast<int>(lid[e < n ? e : 0]) * D * kEsz + lane_byte_off : kDeadOffset;
 #pragma unroll
     for (int j = 0; j < (DT == YH_F32 ? 2 : 1); ++j) {
-      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o + j * 16, 0, 0);
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o + j * 16, 0, 2);
       r[i].w[j] = make_uint4(v.x, v.y, v.z, v.w);
     }
   }
@@ -209,9 +216,8 @@ __device__ __forceinline__ void cvt8(const Raw8<DT>& r, float* f) {
 // Waves per workgroup: 2 for one head per memory (its 256-slot pass is short:
 // each wave then keeps its pipeline over twice the blocks) and for four heads
 // per memory (128 rows x 8 memories: the 1024-slot window ring and the
-// 256-slot anchor memory both read fastest with two waves of 32-slot blocks,
-// 109 us and 33 us, against 108 us and 36 us with four waves and 118 us and
-// 33 us with 16-slot blocks at three waves per SIMD); 4 for two heads.
+// 256-slot anchor memory read in 92.9 us and 27.2 us with two waves, against
+// 97.0 us and 34.1 us with four); 4 for two heads.
 template <int R> constexpr int read_waves() { return R == 2 ? 4 : 2; }
 
 //
@@ -228,12 +234,16 @@ constexpr int kSkipMaxCap = 256;
 // resident at once (8 per CU), each wave with 16 key and 16 value rows in
 // flight -- 39.7 us per read against 43.4 us for 32-slot blocks at two waves
 // per SIMD and 41.3 us at three.  Two heads per memory fit three waves per
-// SIMD without spilling.  fp32 rows (twice the registers) and reads without
-// SKIP: two waves per SIMD (each wave keeps a block of keys and one of values
-// in flight).
+// SIMD without spilling.  Four heads per memory (128 rows x 8 memories) take
+// 16-slot blocks at three waves per SIMD (kR4BS): 92.9 us for the 1024-slot
+// window ring and 27.2 us for the 256-slot anchor memory, against 95.3 us and
+// 31.0 us with 32-slot blocks at two (fp32 rows, twice the registers: at two).
+// The other reads without SKIP: two waves per SIMD (each wave keeps a block
+// of keys and one of values in flight).
 constexpr int kSkipBS = 16;
+constexpr int kR4BS = 16;
 template <int DT, int R, bool SKIP> constexpr int read_occupancy() {
-  return SKIP && DT != YH_F32 ? (R == 1 ? 4 : 3) : 2;
+  return DT == YH_F32 ? 2 : SKIP ? (R == 1 ? 4 : 3) : R == 4 ? 3 : 2;
 }
 
 template <int DT, int D, int R, bool SINK, int BS, bool SKIP>
@@ -667,7 +677,7 @@ int launch_read_r(int R, const ReadArgs& a, hipStream_t st) {
     case 3: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 1, SINK, kSkipBS, SINK>), grid, b1, 0, st, a); break;
     case 4: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, BS, false>), grid, b2, 0, st, a); break;
     case 5: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 2, SINK, kSkipBS, SINK>), grid, b2, 0, st, a); break;
-    case 8: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, BS, false>), grid, b4, 0, st, a); break;
+    case 8: hipLaunchKernelGGL((anchor_read_kernel<DT, D, 4, SINK, kR4BS, false>), grid, b4, 0, st, a); break;
     default: set_error("anchor_read: heads per group must be 1, 2 or 4 (got %d)", R); return YH_ERR_INVALID;
   }
   YH_CHECK_LAUNCH("anchor_read");
