@@ -160,6 +160,7 @@ __device__ __forceinline__ void put_block(float* t, int i, int j, const f32x4v& 
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef unsigned int u32x4n __attribute__((ext_vector_type(4)));
 // One copy instruction (16 or 4 bytes a lane) into LDS at `lds` (wave-uniform)
 // + 16 l (4 l).  Written as inline assembly: the compiler's wait insertion
 // treats a copy it can see as a write to every LDS byte and would make each
@@ -169,9 +170,10 @@ typedef __attribute__((address_space(3))) void lds_void;
 // (which does not see the copies) cannot drop it.
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // (The LDS offset is the low half of the flat address of an LDS object.)
+// The 16-byte copies (q, k, v rows, read once) are nontemporal.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, int voff) {
   const unsigned m0v = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)));
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(m0v), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, const void* lds, int voff) {
@@ -652,7 +654,9 @@ __device__ __forceinline__ void scan_iter(const FusedArgs& a, FBuf* __restrict__
     for (int it = 0; it < kC / (RPI * NW); ++it) {
       const int t = (it * NW + w) * RPI + lane / PPR, pc = lane % PPR;
       const uint4 val = X.tt.p[t * PPR + (pc ^ (t & (PPR - 1)))];
-      if (t < Ls) *reinterpret_cast<uint4*>(a.o + ((toks + t) * a.HV + hv) * V + 8 * pc) = val;
+      if (t < Ls)  // nontemporal: the output is not read again here
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4n, val),
+                                    reinterpret_cast<u32x4n*>(a.o + ((toks + t) * a.HV + hv) * V + 8 * pc));
     }
   }
   const float* tf = X.vt.t;
