@@ -31,7 +31,9 @@ Prints one JSON line.  Workloads:
   kernel (32 packed sequences, lengths U[512, 8192]); reports MFMA utilisation
   beside the HBM fraction.
 * ``hbm_copy``: a 128 MiB device copy, the calibration kernel for the HBM byte
-  counters behind ``roofline.traffic``.
+  counters behind ``roofline.traffic``; ``hbm_streams_gbs`` adds the rates of
+  the library's calibration streams (copy, in-place read-modify-write, read,
+  write; plain and nontemporal) over 1 GiB buffers.
 
 Timing: W untimed steps, then K steps between two device synchronisations.
 ``roofline`` prices the fused GDN decode core (the dominant hot-path kernel:
@@ -617,10 +619,33 @@ def bench_anchor_read(steps, warmup, cpu, batch=64):
                          "dense_bytes_per_launch": dense, "avg_launch_us": kernel_ms * 1e3}}
 
 
+def hbm_stream_rates(steps, warmup, gib=1, grid=16384):
+    """GB/s of the library's calibration streams (yh_hbm_stream) over two
+    `gib` GiB buffers: copy, in-place read-modify-write, read and write, each
+    with plain and with nontemporal loads and stores -- what a streaming
+    kernel reaches on this GPU, beside the 8 TB/s spec figure."""
+    from yanchor_amd import _native
+
+    nbytes = gib << 30
+    a = torch.zeros(nbytes // 4, device="cuda:0")
+    b = torch.zeros_like(a)
+    st = torch.cuda.current_stream().cuda_stream
+    rates = {}
+    for kind, name, moved in ((0, "copy", 2 * nbytes), (1, "rmw", 2 * nbytes), (2, "read", nbytes),
+                              (3, "write", nbytes)):
+        for nt in (0, 1):
+            def step(i, kind=kind, nt=nt):
+                _native.call("yh_hbm_stream", kind, nt, a.data_ptr(), b.data_ptr(), nbytes, grid, st)
+            _, ms = _time_launches(step, steps, warmup)
+            rates[f"{name}{'_nt' if nt else ''}"] = round(moved / (ms * 1e-3) / 1e9, 1)
+    del a, b
+    return rates
+
+
 def bench_hbm_copy(steps, warmup, cpu, batch=None):
     """A plain 128 MiB device-to-device copy (torch's copy kernel): the
-    calibration kernel for the HBM byte counters, and the bandwidth a simple
-    streaming kernel reaches on this GPU."""
+    calibration kernel for the HBM byte counters; beside it the rates of the
+    library's calibration streams over 1 GiB buffers."""
     del cpu, batch
     n = 32 << 20
     src = torch.randn(n, device="cuda:0")
@@ -628,12 +653,17 @@ def bench_hbm_copy(steps, warmup, cpu, batch=None):
     ms_per_step, kernel_ms = _time_launches(lambda i: dst.copy_(src), steps, warmup)
     nbytes = 2 * n * 4
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
-    return {"value": achieved, "unit": "GB/s", "ms_per_step": ms_per_step, "dtype": "f32",
+    del src, dst
+    streams = hbm_stream_rates(steps, warmup)
+    return {"metric": "device copy bandwidth (HBM GB/s)", "value": achieved, "unit": "GB/s",
+            "ms_per_step": ms_per_step, "dtype": "f32",
             "config": {"workload": "hbm_copy: 128 MiB float32 device copy (read 128 MiB + write 128 MiB)",
                        "global_batch": 1, "seq_len": 1, "parallelism": "single GPU"},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "copy",
-                         "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3}}
+                         "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3},
+            "hbm_streams_gbs": {"buffers": "two 1 GiB float32 buffers, 16384 workgroups of 256 threads",
+                                **streams}}
 
 
 def main() -> int:
@@ -668,7 +698,7 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": res["dtype"], "data": "synthetic (seeded random-init weights and requests)",
             "config": res["config"], "roofline": res["roofline"]}
-    for key in ("cpu_baseline", "decode"):
+    for key in ("cpu_baseline", "decode", "hbm_streams_gbs"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

@@ -625,6 +625,18 @@ int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t feat_offse
                        const float* gate_b, const float* adm_up, void* q, float* gate, float* scores, int64_t B,
                        int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps, yh_stream_t stream);
 
+/*
+ * HBM calibration stream (no counterpart in the reference: the measuring stick
+ * for the HBM-bound kernels, whose roofline fractions are quoted against the
+ * 8 TB/s spec figure).  kind 0: dst <- src; 1: dst <- 0.5 dst + 1 in place;
+ * 2: read src (dst receives one float per workgroup); 3: dst <- constant.
+ * nontemporal selects nontemporal loads and stores.  bytes: a positive
+ * multiple of 16; both buffers 16-byte aligned; grid workgroups of 256
+ * threads stride over the buffer.
+ */
+int yh_hbm_stream(int kind, int nontemporal, const void* src, void* dst, int64_t bytes, int grid,
+                  yh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

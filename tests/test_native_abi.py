@@ -73,3 +73,15 @@ def test_wrappers_reject_host_tensors():
         gdn.recurrent_gated_delta_rule(x.q, x.k, x.v, g=x.g, beta=x.beta, initial_state=x.state)
     with pytest.raises(ValueError, match="ROCm device"):
         layers.silu_mul(torch.zeros(2, 16, dtype=torch.bfloat16))
+
+
+def test_hbm_stream_rejects_bad_arguments(lib):
+    fake = ctypes.c_void_p(256)
+    assert lib.yh_hbm_stream(4, 0, fake, fake, 1024, 8, None) == -1
+    assert b"kind" in lib.yh_last_error()
+    assert lib.yh_hbm_stream(0, 0, fake, fake, 1000, 8, None) == -1
+    assert b"multiple of 16" in lib.yh_last_error()
+    assert lib.yh_hbm_stream(0, 0, None, fake, 1024, 8, None) == -1
+    assert b"null" in lib.yh_last_error()
+    assert lib.yh_hbm_stream(2, 0, fake, fake, 16, 8, None) == -1
+    assert b"grid floats" in lib.yh_last_error()

@@ -70,6 +70,7 @@ SIGNATURES: dict[str, list] = {
     "yh_gated_rmsnorm": [_p, _p, _i64, _p, _p, _i64, _i64, _i64, _f32, _p],
     "yh_silu_mul": [_p, _i64, _p, _i64, _i64, _p],
     "yh_head_norm_rope": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p],
+    "yh_hbm_stream": [_i32, _i32, _p, _p, _i64, _i32, _p],
 }
 
 # entry points that do not return a status
