@@ -30,10 +30,13 @@ Prints one JSON line.  Workloads:
 * ``gdn_prefill``: varlen chunked prefill of one GDN layer on the MFMA chunk
   kernel (32 packed sequences, lengths U[512, 8192]); reports MFMA utilisation
   beside the HBM fraction.
+* ``sampling``: the decode step's sampler (fused top-20 semantics, top-p 0.95,
+  presence penalty) on 128 rows of bf16 logits over the full vocabulary.
 * ``hbm_copy``: a 128 MiB device copy, the calibration kernel for the HBM byte
   counters behind ``roofline.traffic``; ``hbm_streams_gbs`` adds the rates of
   the library's calibration streams (copy, in-place read-modify-write, read,
-  write; plain and nontemporal) over 1 GiB buffers.
+  write; plain and nontemporal) over 1 GiB buffers, ``gemm_bf16`` the rate of
+  an 8192^3 bf16 library GEMM beside the 2.5 PFLOP/s MFMA spec.
 
 Timing: W untimed steps, then K steps between two device synchronisations.
 ``roofline`` prices the fused GDN decode core (the dominant hot-path kernel:
@@ -642,6 +645,43 @@ def hbm_stream_rates(steps, warmup, gib=1, grid=16384):
     return rates
 
 
+def bench_sampling(steps, warmup, cpu, batch=128):
+    """The decode step's sampler (top-k 20 / top-p 0.95 / T 0.6, the fused
+    top-20 semantics, presence penalty 1.5 fused in) on B rows of bf16 logits
+    over the 151936-token vocabulary; six rotating (logits, seen) sets, 350 MB,
+    so the rows stream from HBM."""
+    from yanchor_amd import inference_kernels as ik
+
+    del cpu
+    v, n_sets = 151936, 6
+    gen = torch.Generator().manual_seed(20260927)
+    sets = []
+    for _ in range(n_sets):
+        logits = (torch.randn(batch, v, generator=gen) * 2.0).to(torch.bfloat16).to("cuda:0")
+        seen = (torch.rand(batch, v, generator=gen) < 0.007).to("cuda:0")
+        sets.append((logits, seen))
+    ids = torch.arange(batch, dtype=torch.int64, device="cuda:0")
+
+    def step(i):
+        logits, seen = sets[i % n_sets]
+        ik.topk_sample(logits, ids, i, seed=7, temperature=0.6, top_k=20, top_p=0.95, mode=ik.SAMPLE_FUSED,
+                       seen=seen, presence_penalty=1.5)
+
+    ms_per_step, kernel_ms = _time_launches(step, steps, warmup)
+    # algorithmic bytes: every bf16 logit and every byte of the seen mask, the
+    # ids and the tokens
+    nbytes = batch * v * 2 + batch * v + 2 * batch * 8
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    return {"metric": "top-k / top-p sampling of one decode step (HBM GB/s)", "value": achieved, "unit": "GB/s",
+            "ms_per_step": ms_per_step, "dtype": "bf16",
+            "config": {"workload": f"sampling: {batch} rows x {v} bf16 logits, presence mask, top-k 20, top-p 0.95, "
+                                   "T 0.6, penalty 1.5, 6 rotating sets", "global_batch": batch, "seq_len": 1,
+                       "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "topk_segment_kernel + "
+                         "sample_rows_kernel", "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3}}
+
+
 def bench_hbm_copy(steps, warmup, cpu, batch=None):
     """A plain 128 MiB device-to-device copy (torch's copy kernel): the
     calibration kernel for the HBM byte counters; beside it the rates of the
@@ -655,6 +695,14 @@ def bench_hbm_copy(steps, warmup, cpu, batch=None):
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     del src, dst
     streams = hbm_stream_rates(steps, warmup)
+    # the dense bf16 MFMA rate a large library GEMM reaches (8192^3 on hipBLASLt)
+    n = 8192
+    ga = torch.randn(n, n, device="cuda:0").to(torch.bfloat16)
+    gb = torch.randn(n, n, device="cuda:0").to(torch.bfloat16)
+    gc = torch.empty(n, n, device="cuda:0", dtype=torch.bfloat16)
+    _, gemm_ms = _time_launches(lambda i: torch.matmul(ga, gb, out=gc), steps, warmup)
+    gemm_tflops = 2.0 * n ** 3 / (gemm_ms * 1e-3) / 1e12
+    del ga, gb, gc
     return {"metric": "device copy bandwidth (HBM GB/s)", "value": achieved, "unit": "GB/s",
             "ms_per_step": ms_per_step, "dtype": "f32",
             "config": {"workload": "hbm_copy: 128 MiB float32 device copy (read 128 MiB + write 128 MiB)",
@@ -663,7 +711,9 @@ def bench_hbm_copy(steps, warmup, cpu, batch=None):
                          "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "copy",
                          "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3},
             "hbm_streams_gbs": {"buffers": "two 1 GiB float32 buffers, 16384 workgroups of 256 threads",
-                                **streams}}
+                                **streams},
+            "gemm_bf16": {"shape": "8192 x 8192 x 8192 torch.matmul (hipBLASLt)", "tflops": round(gemm_tflops, 1),
+                          "frac_of_2500": round(gemm_tflops / 2500.0, 3)}}
 
 
 def main() -> int:
@@ -673,7 +723,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (model_decode 64, gdn_decode 20)")
     ap.add_argument("--workload", default="model_decode",
                     choices=["model_decode", "long_horizon", "gdn_decode", "gdn_decode_fused", "gdn_prefill",
-                             "anchor_read", "hbm_copy"])
+                             "anchor_read", "sampling", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=None, help="slots (model_decode 128) / rows (gdn_decode 64)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -690,15 +740,16 @@ def main() -> int:
     else:
         steps, warmup = args.steps or 200, 20 if args.warmup is None else args.warmup
         fn = {"gdn_decode": bench_gdn_decode, "gdn_decode_fused": bench_gdn_decode_fused,
-              "gdn_prefill": bench_gdn_prefill, "anchor_read": bench_anchor_read, "hbm_copy": bench_hbm_copy}
+              "gdn_prefill": bench_gdn_prefill, "anchor_read": bench_anchor_read, "sampling": bench_sampling,
+              "hbm_copy": bench_hbm_copy}
         res = fn[args.workload](steps, warmup, not args.no_cpu,
-                                batch=args.batch or (128 if args.workload == "gdn_decode_fused" else 64))
+                                batch=args.batch or (128 if args.workload in ("gdn_decode_fused", "sampling") else 64))
     line = {"metric": res.get("metric", METRIC), "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": steps, "warmup": warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": res["dtype"], "data": "synthetic (seeded random-init weights and requests)",
             "config": res["config"], "roofline": res["roofline"]}
-    for key in ("cpu_baseline", "decode", "hbm_streams_gbs"):
+    for key in ("cpu_baseline", "decode", "hbm_streams_gbs", "gemm_bf16"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

@@ -9,17 +9,14 @@
 //   _qwen35_dense_presence_penalty_kernel 1095-1114
 //
 // Top-k runs in two launches.  Phase 1: a workgroup per (row, vocabulary
-// segment).  Every thread takes the maximum of its 32 elements.  A threshold
-// below the segment's k-th largest element is formed from those maxima: for
-// k <= 32 the largest over the four waves of each wave's k-th largest maximum
-// (a wave sorts its 64 maxima), else the k-th largest of all 256 maxima.  In
-// both cases k threads hold an element at least that large, and at most
-// 4 k (or k) threads hold elements above it, so only those elements -- at most
-// 4096 -- can be in the top k.  They are gathered in LDS and ranked by
-// counting.  Elements are
-// compared by the unique key (value, -index): larger value first, lower index
-// on equal values.  Phase 2: a workgroup per row ranks the segment lists, then
-// draws the token.
+// segment).  Every thread takes the maximum of its 32 elements; the k-th
+// largest of the 256 maxima (each wave sorts its 64, the first k of the four
+// waves are ranked) is at most the segment's k-th largest element, and only
+// the k threads whose maxima reach it can hold elements that do -- at most
+// 32 k, gathered in LDS and ranked by counting.  Elements are compared by the
+// unique key (value, -index): larger value first, lower index on equal
+// values.  Phase 2: a workgroup per row ranks the segment lists' keys by
+// counting, then draws the token.
 #include "common.h"
 
 #include <mutex>
@@ -28,8 +25,8 @@ namespace yh {
 namespace {
 
 constexpr int kTopkThreads = 256;
+constexpr int kSampleThreads = 512;  // phase 2: one thread a candidate key of the row
 constexpr int kMaxK = 64;
-constexpr int kCandCap = 4096;
 constexpr int kMaxPerThread = 64;  // elements per thread per segment
 
 // Larger float -> larger key; -0.0 == +0.0.
@@ -54,17 +51,16 @@ struct TopkArgs {
   float penalty;
 };
 
-constexpr int kVecPerThread = 8;                       // 4-element vectors per thread
+constexpr int kVecPerThread = 8;                           // 4-element vectors per thread
 constexpr int kSegLen = kTopkThreads * 4 * kVecPerThread;  // 8192 elements per segment
-static_assert(kVecPerThread * 4 <= kMaxPerThread, "elements per thread");
+constexpr int kPerThread = 4 * kVecPerThread;              // 32
+static_assert(kPerThread <= kMaxPerThread, "elements per thread");
+// Candidates of a segment: the elements of the at most k threads whose
+// maximum reaches the threshold (the k-th largest thread maximum).
+constexpr int kCandMax = kMaxK * kPerThread;  // 2048
 
-// Element e of a thread's 32 scores.  WIDE (16-byte aligned rows): in a full
-// segment the thread reads 16-byte runs, element i = lo + (c * 256 + tid) * E
-// + j for run c and j < E = 16 / element size; otherwise (the row's last
-// segment, or unaligned rows) element i = lo + e * 256 + tid, read one by one
-// at a clamped index and dropped past V.  Every load of the thread is issued
-// before the first is used.
-constexpr int kPerThread = 4 * kVecPerThread;  // 32
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 template <int DT>
 __device__ __forceinline__ float decode_elem(uint32_t bits) {
@@ -73,83 +69,198 @@ __device__ __forceinline__ float decode_elem(uint32_t bits) {
   else return f16_to_f32(static_cast<uint16_t>(bits));
 }
 
-template <int DT, bool WIDE>
-__device__ __forceinline__ uint64_t load_keys(const TopkArgs& a, int64_t b, int lo, int tid,
-                                              uint64_t (&key)[kPerThread]) {
-  constexpr int ES = DT == YH_F32 ? 4 : 2;
-  const char* row = static_cast<const char*>(a.scores) + b * a.row_stride * ES;
-  const uint8_t* srow = a.seen ? a.seen + b * a.seen_stride : nullptr;
-  uint64_t best = 0;  // key 0 is below every real element key
-  if (WIDE && lo + kSegLen <= a.V) {
-    constexpr int E = 16 / ES, NC = kPerThread / E;
-    uint4 raw[NC];
-    uint64_t sm[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-      raw[c] = *reinterpret_cast<const uint4*>(row + static_cast<int64_t>(lo + (c * kTopkThreads + tid) * E) * ES);
-    if (srow) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const uint8_t* sp = srow + lo + (c * kTopkThreads + tid) * E;
-        if constexpr (E == 8) sm[c] = *reinterpret_cast<const uint64_t*>(sp);
-        else sm[c] = *reinterpret_cast<const uint32_t*>(sp);
-      }
-    }
+// A thread's 32 elements of one segment, kept as loaded (the raw words and
+// seen bytes) and decoded on use, in increasing vocabulary index.  RUNS (rows
+// 16-byte aligned, V a multiple of the run): 16-byte runs, element
+// e = (run c, slot j) at lo + (c * 256 + tid) * E + j, through buffer
+// resources bounded by the row, so runs past V read zeros (and are invalid).
+// Otherwise element e at lo + e * 256 + tid, loaded one by one at a clamped
+// index and invalid past V.  Every load is issued before the first is used.
+template <int DT, bool RUNS> struct SegElems;
+
+template <int DT> struct SegElems<DT, true> {
+  static constexpr int ES = DT == YH_F32 ? 4 : 2, E = 16 / ES, NC = kPerThread / E;
+  uint4 raw[NC];
+  uint64_t sm[NC];
+  int base, V;
+  bool full;
+  __device__ __forceinline__ void load(const char* row, const uint8_t* srow, int lo, int tid, int V_) {
+    V = V_;
+    full = lo + kSegLen <= V;
+    base = lo + tid * E;
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(row), 0, V * ES, 0x00020000);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(&raw[c]);
-      const int i0 = lo + (c * kTopkThreads + tid) * E;
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rr, (base + c * kTopkThreads * E) * ES, 0, 0);
+      raw[c] = make_uint4(v.x, v.y, v.z, v.w);
+    }
 #pragma unroll
-      for (int j = 0; j < E; ++j) {
-        const uint32_t bits = ES == 4 ? w[j] : (w[j / 2] >> (16 * (j & 1))) & 0xffffu;
-        float x = decode_elem<DT>(bits);
-        if (srow && ((sm[c] >> (8 * j)) & 0xffu)) x = x - a.penalty;
-        key[c * E + j] = ckey(x, static_cast<uint32_t>(i0 + j));
-        best = key[c * E + j] > best ? key[c * E + j] : best;
+    for (int c = 0; c < NC; ++c) sm[c] = 0;
+    if (srow) {
+      const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(srow), 0, V, 0x00020000);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int off = base + c * kTopkThreads * E;
+        if constexpr (E == 8) {
+          const u32x2 m = __builtin_amdgcn_raw_buffer_load_b64(sr, off, 0, 0);
+          sm[c] = (static_cast<uint64_t>(m.y) << 32) | m.x;
+        } else {
+          sm[c] = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
+        }
       }
     }
-    return best;
   }
-  uint32_t raw[kPerThread];
-  uint8_t sm[kPerThread];
+  // an opaque use of the loaded words: the second pass decodes them again
+  // instead of keeping 32 keys live across the threshold search
+  __device__ __forceinline__ void touch() {
 #pragma unroll
-  for (int e = 0; e < kPerThread; ++e) {
-    const int i = min(lo + e * kTopkThreads + tid, a.V - 1);
-    if constexpr (ES == 4) raw[e] = *reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(i) * 4);
-    else raw[e] = *reinterpret_cast<const uint16_t*>(row + static_cast<int64_t>(i) * 2);
+    for (int c = 0; c < NC; ++c) {
+      asm volatile("" : "+v"(raw[c].x), "+v"(raw[c].y), "+v"(raw[c].z), "+v"(raw[c].w));
+      uint32_t lo = static_cast<uint32_t>(sm[c]), hi = static_cast<uint32_t>(sm[c] >> 32);
+      asm volatile("" : "+v"(lo), "+v"(hi));
+      sm[c] = (static_cast<uint64_t>(hi) << 32) | lo;
+    }
   }
-  if (srow) {
-#pragma unroll
-    for (int e = 0; e < kPerThread; ++e) sm[e] = srow[min(lo + e * kTopkThreads + tid, a.V - 1)];
+  __device__ __forceinline__ bool valid(int e) const { return full || index(e) < V; }
+  __device__ __forceinline__ int index(int e) const { return base + (e / E) * kTopkThreads * E + e % E; }
+  __device__ __forceinline__ float value(int e, float penalty) const {
+    const int c = e / E, j = e % E;
+    const uint32_t w = reinterpret_cast<const uint32_t*>(&raw[c])[ES == 4 ? j : j / 2];
+    const uint32_t bits = ES == 4 ? w : (w >> (16 * (j & 1))) & 0xffffu;
+    const float x = decode_elem<DT>(bits);
+    return ((sm[c] >> (8 * j)) & 0xffu) ? x - penalty : x;
   }
-#pragma unroll
-  for (int e = 0; e < kPerThread; ++e) {
-    const int i = lo + e * kTopkThreads + tid;
-    float x = decode_elem<DT>(raw[e]);
-    if (srow && sm[e]) x = x - a.penalty;
-    key[e] = i < a.V ? ckey(x, static_cast<uint32_t>(i)) : 0ull;
-    best = key[e] > best ? key[e] : best;
-  }
-  return best;
-}
+};
 
-constexpr int kWaveThrMaxK = kCandCap / (kTopkThreads / kWave) / (4 * kVecPerThread);  // 32
+template <int DT> struct SegElems<DT, false> {
+  static constexpr int ES = DT == YH_F32 ? 4 : 2;
+  uint32_t raw[kPerThread];
+  uint32_t sm;  // bit e: element e was seen
+  int base, V;
+  __device__ __forceinline__ void load(const char* row, const uint8_t* srow, int lo, int tid, int V_) {
+    base = lo + tid;
+    V = V_;
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) {
+      const int i = min(base + e * kTopkThreads, V - 1);
+      if constexpr (ES == 4) raw[e] = *reinterpret_cast<const uint32_t*>(row + static_cast<int64_t>(i) * 4);
+      else raw[e] = *reinterpret_cast<const uint16_t*>(row + static_cast<int64_t>(i) * 2);
+    }
+    sm = 0;
+    if (srow) {
+#pragma unroll
+      for (int e = 0; e < kPerThread; ++e) sm |= (srow[min(base + e * kTopkThreads, V - 1)] ? 1u : 0u) << e;
+    }
+  }
+  __device__ __forceinline__ void touch() {
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) asm volatile("" : "+v"(raw[e]));
+    asm volatile("" : "+v"(sm));
+  }
+  __device__ __forceinline__ bool valid(int e) const { return base + e * kTopkThreads < V; }
+  __device__ __forceinline__ int index(int e) const { return base + e * kTopkThreads; }
+  __device__ __forceinline__ float value(int e, float penalty) const {
+    const float x = decode_elem<DT>(raw[e]);
+    return ((sm >> e) & 1u) ? x - penalty : x;
+  }
+};
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, kWave);
   const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, kWave);
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
-__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
-  const uint32_t lo = __shfl(static_cast<uint32_t>(v), src, kWave);
-  const uint32_t hi = __shfl(static_cast<uint32_t>(v >> 32), src, kWave);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
+
+// The top k of one segment, as keys sorted in descending order (0 past the
+// segment's elements), into out[0 .. k).
+//  1. Each thread's maximum key (the first of equal values: its elements come
+//     in increasing index).
+//  2. Each wave sorts its 64 maxima (bitonic network); its first k go to LDS.
+//  3. The threshold is the k-th largest of those 4 k keys, i.e. the k-th
+//     largest of all 256 thread maxima (0 if fewer than k threads hold an
+//     element): k threads hold an element at least that large, so it does not
+//     exceed the segment's k-th largest element, and only the at most k
+//     threads whose maximum reaches it can hold elements that do.
+//  4. Those threads put their elements at or above it in LDS (at most 32 k);
+//     they are ranked by counting.
+// okey with the zero made canonical by an addition (-0 + 0 = +0) and the sign
+// handled by a mask, without compares: the same keys, fewer instructions.
+__device__ __forceinline__ uint32_t okey_fast(float x) {
+  const uint32_t u = __float_as_uint(x + 0.0f);
+  return u ^ (static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u);
+}
+
+template <bool CHECK, class El>
+__device__ __forceinline__ void segment_topk(El& el, float penalty, int k, uint64_t* __restrict__ out,
+                                             uint64_t (&wtop)[kTopkThreads / kWave][kMaxK],
+                                             uint64_t* __restrict__ cand, uint64_t& thr_s, int& ncand) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  // the value key of element e (0 past the row; real keys are nonzero),
+  // decoded from the loaded words in both passes
+  auto vkey = [&](int e) {
+    const uint32_t kx = okey_fast(el.value(e, penalty));
+    if constexpr (CHECK) return el.valid(e) ? kx : 0u;
+    return kx;
+  };
+  // the thread's maximum key and its first position
+  uint32_t mk = 0;
+  int mi = 0;
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) {
+    const uint32_t kx = vkey(e);
+    const bool gt = kx > mk;
+    mi = gt ? e : mi;
+    mk = gt ? kx : mk;
+    // the running pair is materialised at every element: otherwise the
+    // compiler defers the index selects and keeps every key live
+    asm volatile("" : "+v"(mi), "+v"(mk));
+  }
+  const uint64_t best =
+      mk != 0 ? (static_cast<uint64_t>(mk) << 32) | (0xffffffffu - static_cast<uint32_t>(el.index(mi))) : 0ull;
+  uint64_t x = best;
+#pragma unroll
+  for (int size = 2; size <= kWave; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t y = shfl_xor_u64(x, stride);
+      const bool keep_max = ((lane & size) == 0) == ((lane & stride) == 0);
+      x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+    }
+  if (lane < k) wtop[wv][lane] = x;  // descending: lane j holds the wave's (j + 1)-th largest
+  __syncthreads();
+  if (tid < (kTopkThreads / kWave) * k) {
+    const uint64_t c = wtop[tid / k][tid % k];
+    int rank = 0;
+    for (int w = 0; w < kTopkThreads / kWave; ++w)
+      for (int j = 0; j < k; ++j) rank += wtop[w][j] > c;
+    if (rank == k - 1 && c != 0) thr_s = c;  // real keys are unique: at most one thread
+  }
+  __syncthreads();
+  const uint64_t thr = thr_s;
+  el.touch();
+  if (best != 0 && best >= thr) {
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) {
+      const uint32_t kx = vkey(e);
+      const uint64_t key = (static_cast<uint64_t>(kx) << 32) | (0xffffffffu - static_cast<uint32_t>(el.index(e)));
+      if (kx != 0 && key >= thr) cand[atomicAdd(&ncand, 1)] = key;
+    }
+  }
+  __syncthreads();
+  const int n = ncand;
+  for (int i = tid; i < n; i += kTopkThreads) {
+    const uint64_t mine = cand[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += cand[j] > mine;
+    if (rank < k) out[rank] = mine;
+  }
+  for (int r = n + tid; r < k; r += kTopkThreads) out[r] = 0;  // padding: below every element
 }
 
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(kTopkThreads) topk_segment_kernel(TopkArgs a) {
-  __shared__ uint64_t maxima[kTopkThreads];
-  __shared__ uint64_t cand[kCandCap];
+  __shared__ uint64_t wtop[kTopkThreads / kWave][kMaxK];
+  __shared__ uint64_t cand[kCandMax + 1];  // + a spare entry
   __shared__ uint64_t thr_s;
   __shared__ int ncand;
   const int seg = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
@@ -158,65 +269,16 @@ __global__ void __launch_bounds__(kTopkThreads) topk_segment_kernel(TopkArgs a) 
     ncand = 0;
     thr_s = 0;
   }
-  uint64_t key[kPerThread];
-  const uint64_t best = load_keys<DT, VEC>(a, b, lo, tid, key);
-  if (a.k <= kWaveThrMaxK) {
-    // Threshold = the largest over the waves of each wave's k-th largest
-    // thread maximum (a wave sorts its 64 maxima by a bitonic network):
-    // the wave that attains it holds k elements at or above it, so it bounds
-    // the segment's k-th largest element from below, and no wave has more
-    // than k threads at or above it, so at most 4 k x 32 elements pass.
-    const int lane = tid & (kWave - 1);
-    uint64_t x = best;
-#pragma unroll
-    for (int size = 2; size <= kWave; size <<= 1)
-#pragma unroll
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        const uint64_t y = shfl_xor_u64(x, stride);
-        const bool keep_max = ((lane & size) == 0) == ((lane & stride) == 0);
-        x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
-      }
-    const uint64_t kth = shfl_u64(x, a.k - 1);  // descending: lane j holds the (j+1)-th largest
-    if (lane == 0) maxima[tid / kWave] = kth;
-    __syncthreads();
-    if (tid == 0) {
-      uint64_t t = 0;
-      for (int w = 0; w < kTopkThreads / kWave; ++w) t = maxima[w] > t ? maxima[w] : t;
-      thr_s = t;
-    }
-  } else {
-    maxima[tid] = best;
-    __syncthreads();
-    // Threshold = k-th largest thread maximum.  Real keys are unique, so exactly
-    // one thread has rank k-1 when at least k threads hold elements; otherwise the
-    // threshold stays 0 and every element of the segment is a candidate (fewer
-    // than k threads hold at most (k-1) * per-thread elements).
-    if (best != 0) {
-      int rank = 0;
-      for (int j = 0; j < kTopkThreads; ++j) rank += maxima[j] > best;
-      if (rank == a.k - 1) thr_s = best;
-    }
-  }
-  __syncthreads();
-  const uint64_t thr = thr_s;
-  if (best >= thr && best != 0) {
-#pragma unroll
-    for (int e = 0; e < kPerThread; ++e)
-      if (key[e] >= thr && key[e] != 0) {
-        const int slot = atomicAdd(&ncand, 1);
-        if (slot < kCandCap) cand[slot] = key[e];
-      }
-  }
-  __syncthreads();
-  const int n = min(ncand, kCandCap);
+  constexpr int ES = DT == YH_F32 ? 4 : 2;
+  const char* row = static_cast<const char*>(a.scores) + static_cast<int64_t>(b) * a.row_stride * ES;
+  const uint8_t* srow = a.seen ? a.seen + static_cast<int64_t>(b) * a.seen_stride : nullptr;
   uint64_t* out = a.work + (static_cast<int64_t>(b) * a.S + seg) * a.k;
-  for (int i = tid; i < n; i += kTopkThreads) {
-    const uint64_t mine = cand[i];
-    int rank = 0;
-    for (int j = 0; j < n; ++j) rank += cand[j] > mine;
-    if (rank < a.k) out[rank] = mine;
-  }
-  for (int r = n + tid; r < a.k; r += kTopkThreads) out[r] = 0;  // padding: below every element
+  SegElems<DT, VEC> el;
+  el.load(row, srow, lo, tid, a.V);
+  if (lo + kSegLen <= a.V)  // uniform: no element past the row
+    segment_topk<false>(el, a.penalty, a.k, out, wtop, cand, thr_s, ncand);
+  else
+    segment_topk<true>(el, a.penalty, a.k, out, wtop, cand, thr_s, ncand);
 }
 
 struct SampleArgs {
@@ -249,15 +311,16 @@ __device__ __forceinline__ float wave_scan(float x, int lane) {
   return x;
 }
 
-__global__ void __launch_bounds__(kTopkThreads) sample_rows_kernel(SampleArgs a) {
+__global__ void __launch_bounds__(kSampleThreads) sample_rows_kernel(SampleArgs a) {
   __shared__ uint64_t cand[kMaxK * 64];
   __shared__ uint64_t top[kMaxK];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int n = a.S * a.k;
   const uint64_t* src = a.work + static_cast<int64_t>(b) * n;
-  for (int i = tid; i < n; i += kTopkThreads) cand[i] = src[i];
+  for (int i = tid; i < n; i += kSampleThreads) cand[i] = src[i];
   __syncthreads();
-  for (int i = tid; i < n; i += kTopkThreads) {
+  // rank by counting: one thread a key (S k <= 64 k keys, 512 threads)
+  for (int i = tid; i < n; i += kSampleThreads) {
     const uint64_t mine = cand[i];
     int rank = 0;
     for (int j = 0; j < n; ++j) rank += cand[j] > mine;
@@ -672,7 +735,7 @@ int topk_sample_launch(const void* scores, int dtype, int64_t row_stride, const 
               row_stride, seen_stride, penalty};
   const size_t esz = dtype == YH_F32 ? 4 : 2;
   const int64_t run = 16 / static_cast<int64_t>(esz);  // elements per 16-byte load
-  const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16) == 0 && row_stride % run == 0 &&
+  const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16) == 0 && row_stride % run == 0 && V % run == 0 &&
                    (seen == nullptr || ((reinterpret_cast<uintptr_t>(seen) % run) == 0 && seen_stride % run == 0));
   const dim3 grid(S, static_cast<unsigned>(B));
   switch (dtype * 2 + (vec ? 1 : 0)) {
@@ -687,7 +750,7 @@ int topk_sample_launch(const void* scores, int dtype, int64_t row_stride, const 
   SampleArgs sa{static_cast<const uint64_t*>(workspace), attempt_ids, steps, tokens, out_values, out_indices,
                 (int)B, S, (int)top_k, mode, step, static_cast<uint32_t>(seed & 0xffffffffu),
                 static_cast<uint32_t>(stream_id & 0xffffffffu), temperature, top_p};
-  hipLaunchKernelGGL(sample_rows_kernel, dim3(static_cast<unsigned>(B)), dim3(kTopkThreads), 0, st, sa);
+  hipLaunchKernelGGL(sample_rows_kernel, dim3(static_cast<unsigned>(B)), dim3(kSampleThreads), 0, st, sa);
   YH_CHECK_LAUNCH("sample_rows");
   return YH_OK;
 }
