@@ -219,6 +219,24 @@ def test_fused_presence_penalty(gpu):
     assert torch.equal(sc.cpu(), adjusted)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_topk_elementwise_path_with_penalty(gpu, dtype):
+    """A vocabulary that is not a multiple of the 16-byte run takes the
+    element-by-element loads (three segments, the last partial) with the seen
+    mask's penalty applied: the top k of the penalised scores, lower index
+    first on ties."""
+    b, v, k = 6, 20001, 24
+    g = torch.Generator().manual_seed(31)
+    logits = (torch.randn(b, v, generator=g) * 2).to(dtype)
+    seen = torch.rand(b, v, generator=g) < 0.2
+    _, vals, idx = ik.topk_sample(logits.to(gpu), torch.arange(b).to(gpu), 0, seed=1, temperature=1.0, top_k=k,
+                                  top_p=1.0, mode=ik.SAMPLE_FUSED, return_topk=True, seen=seen.to(gpu),
+                                  presence_penalty=1.5)
+    adjusted = logits.float() - 1.5 * seen.float()
+    order = torch.sort(-adjusted, dim=-1, stable=True).indices[:, :k]
+    assert torch.equal(idx.cpu(), order) and torch.equal(vals.cpu(), torch.gather(adjusted, 1, order))
+
+
 def test_strided_rows(gpu):
     logits = torch.randn(6, 3000)
     view = logits.to(gpu)[:, :2500]
