@@ -30,6 +30,9 @@ Prints one JSON line.  Workloads:
 * ``gdn_prefill``: varlen chunked prefill of one GDN layer on the MFMA chunk
   kernel (32 packed sequences, lengths U[512, 8192]); reports MFMA utilisation
   beside the HBM fraction.
+* ``anchor_prefill``: the anchor-memory half of a prefill that continues a
+  state (32 rows x 2048 tokens, 8 memories of 256 slots, C = 64), and its
+  MFMA block read alone.
 * ``sampling``: the decode step's sampler (fused top-20 semantics, top-p 0.95,
   presence penalty) on 128 rows of bf16 logits over the full vocabulary.
 * ``hbm_copy``: a 128 MiB device copy, the calibration kernel for the HBM byte
@@ -645,6 +648,56 @@ def hbm_stream_rates(steps, warmup, gib=1, grid=16384):
     return rates
 
 
+def bench_anchor_prefill(steps, warmup, cpu, batch=32):
+    """The anchor-memory half of a prefill that continues a state
+    (independent_memory.sequence: the prefix Top-K scan, the MFMA read of
+    every C-token block over the memory committed before it, the commit) for
+    B rows of 2048 tokens, 32 heads over 8 memories of 256 slots, C = 64,
+    bf16; and the block read (yh_indexed_gqa) alone on the same shapes for its
+    roofline."""
+    from yanchor_amd import independent_memory as im, workloads
+
+    del cpu
+    b, length, h, g, cap, c, d = batch, 2048, 32, 8, 256, 64, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(20260928)
+    state = workloads.anchor_state(b, g, cap, c, d, p_live=0.9, seed=workloads.SEED0 + 11)
+    state.to_("cuda:0")
+    q = torch.randn(b, length, h, d, generator=gen).to(torch.bfloat16).to(dev)
+    k = torch.randn(b, length, g, d, generator=gen).to(torch.bfloat16).to(dev)
+    v = torch.randn(b, length, g, d, generator=gen).to(torch.bfloat16).to(dev)
+    sc = torch.randn(b, length, g, generator=gen).to(dev)
+
+    def step(i):
+        im.sequence(q, k, v, sc, None, c, state)
+
+    ms_per_step, kernel_ms = _time_launches(step, steps, warmup)
+    # the block read alone: every block of every row reads cap referenced rows
+    # of its group among the sources (committed slots, pending slots, tokens)
+    blocks = length // c + 1
+    n_src = cap + c + length
+    qb = torch.randn(b, blocks, c, h, d, generator=gen).to(torch.bfloat16).to(dev)
+    src_k = torch.randn(b, n_src, g, d, generator=gen).to(torch.bfloat16).to(dev)
+    src_v = torch.randn(b, n_src, g, d, generator=gen).to(torch.bfloat16).to(dev)
+    refs = torch.randint(0, n_src, (b, blocks, g, cap), generator=gen, dtype=torch.int32).to(dev)
+    _, read_ms = _time_launches(lambda i: im.indexed_gqa(qb, src_k, src_v, refs), steps, warmup)
+    flops = 4.0 * b * blocks * h * c * cap * d           # Q K^T and P V over the referenced rows
+    nbytes = 2 * qb.numel() * 2 + 2 * src_k.numel() * 2 + refs.numel() * 4   # q and out, the sources once, refs
+    t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), flops / 2.5e15
+    achieved = nbytes / (read_ms * 1e-3) / 1e9
+    return {"metric": "anchor-memory prefill tokens/s (sequence with a state)",
+            "value": b * length / (kernel_ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms_per_step,
+            "dtype": "bf16",
+            "config": {"workload": f"anchor_prefill: {b} rows x {length} tokens, {h} heads over {g} memories of "
+                                   f"{cap} slots x {d} bf16, chunk {c}, continuing a state (p_live 0.9)",
+                       "global_batch": b, "seq_len": length, "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm" if t_hbm >= t_mfma else "mfma", "achieved": achieved,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": max(t_hbm, t_mfma) / (read_ms * 1e-3),
+                         "traffic": None, "kernel": "indexed_gqa_kernel", "bytes_per_launch": nbytes,
+                         "flops_per_launch": flops, "mfma_tflops": flops / (read_ms * 1e-3) / 1e12,
+                         "avg_launch_us": read_ms * 1e3, "sequence_call_us": kernel_ms * 1e3}}
+
+
 def bench_sampling(steps, warmup, cpu, batch=128):
     """The decode step's sampler (top-k 20 / top-p 0.95 / T 0.6, the fused
     top-20 semantics, presence penalty 1.5 fused in) on B rows of bf16 logits
@@ -723,7 +776,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (model_decode 64, gdn_decode 20)")
     ap.add_argument("--workload", default="model_decode",
                     choices=["model_decode", "long_horizon", "gdn_decode", "gdn_decode_fused", "gdn_prefill",
-                             "anchor_read", "sampling", "hbm_copy"])
+                             "anchor_read", "anchor_prefill", "sampling", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=None, help="slots (model_decode 128) / rows (gdn_decode 64)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -741,9 +794,11 @@ def main() -> int:
         steps, warmup = args.steps or 200, 20 if args.warmup is None else args.warmup
         fn = {"gdn_decode": bench_gdn_decode, "gdn_decode_fused": bench_gdn_decode_fused,
               "gdn_prefill": bench_gdn_prefill, "anchor_read": bench_anchor_read, "sampling": bench_sampling,
+              "anchor_prefill": bench_anchor_prefill,
               "hbm_copy": bench_hbm_copy}
         res = fn[args.workload](steps, warmup, not args.no_cpu,
-                                batch=args.batch or (128 if args.workload in ("gdn_decode_fused", "sampling") else 64))
+                                batch=args.batch or (128 if args.workload in ("gdn_decode_fused", "sampling") else
+                                                     32 if args.workload == "anchor_prefill" else 64))
     line = {"metric": res.get("metric", METRIC), "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": steps, "warmup": warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

@@ -256,6 +256,22 @@ int yh_indexed_gqa(const void* query, const void* key, const void* value, const 
                    int64_t S, int64_t CAP, int dtype, yh_stream_t stream);
 
 /*
+ * The read of a prefill chunk that continues an anchor-memory state (the
+ * block read of IndependentGQAMemory._sequence, modeling_yanchor.py:249, as
+ * yh_indexed_gqa) with the tokens addressed in place: query and out are the
+ * chunk's tokens [B, L, H, D]; block position p = nb * C + t of row b holds
+ * token p - first[b] (first: the row's pending count before the chunk, int64
+ * [B]); positions without a token are not read and nothing is written for
+ * them.  key, value [B, S, G, D]; references [B, NB, G, CAP] as in
+ * yh_indexed_gqa.  No separate counterpart in the reference: it is that read
+ * without the block-padded copy of the queries and the gather of the output.
+ */
+int yh_anchor_sequence_read(const void* query, const void* key, const void* value, const void* references,
+                            int ref_dtype, const int64_t* first, void* out, int64_t B, int64_t L, int64_t NB,
+                            int64_t C, int64_t H, int64_t G, int64_t D, int64_t S, int64_t CAP, int dtype,
+                            yh_stream_t stream);
+
+/*
  * Anchor memory, prefill continuation, step 1: the block-wise Top-K scan of
  * IndependentGQAMemory._sequence with a state (modeling_yanchor.py:178-275:
  * exclusive_prefix_topk 65-78 on the new blocks, merged with the committed

@@ -38,6 +38,8 @@ SIGNATURES: dict[str, list] = {
     "yh_anchor_sequence_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _i32, _p],
     "yh_indexed_gqa": [_p, _p, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "yh_anchor_sequence_read": [_p, _p, _p, _p, _i32, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                _i32, _p],
     "yh_linear": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "yh_linear_pack": [_p, _p, _i64, _i64, _i32, _p],
     "yh_linear_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i64, _p, _i64, _i32, _p, _p],

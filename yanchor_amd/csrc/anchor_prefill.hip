@@ -44,6 +44,11 @@ struct IdxArgs {
   uint16_t* out;
   int NB, C, H, G, S, CAP, KB, ref64;
   float scale;
+  // tokens in place (yh_anchor_sequence_read): query / out [B, L, H, D]; the
+  // query at block position p = nb * C + t of row b is token p - first[b]
+  // (no token, no read, for p outside [first[b], first[b] + L))
+  const int64_t* first;
+  int L;
 };
 
 template <int DT>
@@ -88,8 +93,15 @@ __global__ void __launch_bounds__(256) indexed_gqa_kernel(IdxArgs a) {
   const int64_t b = bb / a.NB;
   const int qn = lane & 15, quad = lane >> 4;
   const int m = blockIdx.y * 64 + w * 16 + qn;  // query row of this lane (as the MFMA column)
-  const bool mvalid = m < rows;
-  const int64_t qrow = mvalid ? ((bb * a.C + m % a.C) * a.H + g * R + m / a.C) : 0;
+  bool mvalid = m < rows;
+  int64_t qrow;
+  if (a.first == nullptr) {
+    qrow = mvalid ? ((bb * a.C + m % a.C) * a.H + g * R + m / a.C) : 0;
+  } else {
+    const int64_t tok = (bb - b * a.NB) * a.C + m % a.C - a.first[b];
+    mvalid = mvalid && tok >= 0 && tok < a.L;
+    qrow = mvalid ? ((b * a.L + tok) * a.H + g * R + m / a.C) : 0;
+  }
 
   // Q^T operand (B of S^T = K Q^T): lane holds Q[m][step*32 + quad*8 + 0..7].
   vec qv[4];
@@ -219,34 +231,56 @@ __global__ void __launch_bounds__(256) indexed_gqa_kernel(IdxArgs a) {
 }  // namespace
 }  // namespace yh
 
-extern "C" int yh_indexed_gqa(const void* query, const void* key, const void* value, const void* references,
-                              int ref_dtype, void* out, int64_t B, int64_t NB, int64_t C, int64_t H, int64_t G,
-                              int64_t D, int64_t KB, int64_t S, int64_t CAP, int dtype, yh_stream_t stream) {
-  using namespace yh;
-  YH_CHECK_ARG(B >= 0 && NB >= 0 && C > 0 && H > 0 && G > 0 && H % G == 0 && S >= 0 && CAP >= 0,
-               "indexed_gqa: bad sizes");
-  YH_CHECK_ARG(D == kD, "indexed_gqa: head dim must be %d", kD);
-  YH_CHECK_ARG(KB == 1 || KB == B, "indexed_gqa: key batch must be 1 or B");
-  YH_CHECK_ARG(ref_dtype == YH_I32 || ref_dtype == YH_I64, "indexed_gqa: references must be int32 or int64");
+namespace yh {
+namespace {
+int launch_indexed(const void* query, const void* key, const void* value, const void* references, int ref_dtype,
+                   void* out, int64_t B, int64_t NB, int64_t C, int64_t H, int64_t G, int64_t D, int64_t KB,
+                   int64_t S, int64_t CAP, const int64_t* first, int64_t L, int dtype, yh_stream_t stream,
+                   const char* what) {
+  YH_CHECK_ARG(B >= 0 && NB >= 0 && C > 0 && H > 0 && G > 0 && H % G == 0 && S >= 0 && CAP >= 0 && L >= 0,
+               "%s: bad sizes", what);
+  YH_CHECK_ARG(D == kD, "%s: head dim must be %d", what, kD);
+  YH_CHECK_ARG(KB == 1 || KB == B, "%s: key batch must be 1 or B", what);
+  YH_CHECK_ARG(ref_dtype == YH_I32 || ref_dtype == YH_I64, "%s: references must be int32 or int64", what);
   if (dtype != YH_BF16 && dtype != YH_F16) {
-    set_error("indexed_gqa: dtype must be bf16 or fp16");
+    set_error("%s: dtype must be bf16 or fp16", what);
     return YH_ERR_UNSUPPORTED;
   }
   const int64_t groups = B * NB * G;
   if (groups == 0) return YH_OK;
-  YH_CHECK_ARG(query && key && value && out && (CAP == 0 || references), "indexed_gqa: null pointer");
+  YH_CHECK_ARG(query && key && value && out && (CAP == 0 || references), "%s: null pointer", what);
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(key) |
                  reinterpret_cast<uintptr_t>(value) | reinterpret_cast<uintptr_t>(out)) & 15) == 0,
-               "indexed_gqa: tensors must be 16-byte aligned");
-  YH_CHECK_ARG(groups < (1ll << 31) && C * (H / G) < (1ll << 20), "indexed_gqa: grid too large");
+               "%s: tensors must be 16-byte aligned", what);
+  YH_CHECK_ARG(groups < (1ll << 31) && C * (H / G) < (1ll << 20) && L < (1ll << 31), "%s: grid too large", what);
   IdxArgs a{static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key),
             static_cast<const uint16_t*>(value), references, static_cast<uint16_t*>(out), (int)NB, (int)C, (int)H,
-            (int)G, (int)S, (int)CAP, (int)KB, ref_dtype == YH_I64 ? 1 : 0, 1.f / sqrtf(static_cast<float>(D))};
+            (int)G, (int)S, (int)CAP, (int)KB, ref_dtype == YH_I64 ? 1 : 0, 1.f / sqrtf(static_cast<float>(D)),
+            first, (int)L};
   const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>((C * (H / G) + 63) / 64));
   if (dtype == YH_BF16)
     hipLaunchKernelGGL(indexed_gqa_kernel<YH_BF16>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   else
     hipLaunchKernelGGL(indexed_gqa_kernel<YH_F16>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
-  YH_CHECK_LAUNCH("indexed_gqa");
+  YH_CHECK_LAUNCH(what);
   return YH_OK;
+}
+}  // namespace
+}  // namespace yh
+
+extern "C" int yh_indexed_gqa(const void* query, const void* key, const void* value, const void* references,
+                              int ref_dtype, void* out, int64_t B, int64_t NB, int64_t C, int64_t H, int64_t G,
+                              int64_t D, int64_t KB, int64_t S, int64_t CAP, int dtype, yh_stream_t stream) {
+  return yh::launch_indexed(query, key, value, references, ref_dtype, out, B, NB, C, H, G, D, KB, S, CAP, nullptr, 0,
+                            dtype, stream, "indexed_gqa");
+}
+
+extern "C" int yh_anchor_sequence_read(const void* query, const void* key, const void* value,
+                                       const void* references, int ref_dtype, const int64_t* first, void* out,
+                                       int64_t B, int64_t L, int64_t NB, int64_t C, int64_t H, int64_t G, int64_t D,
+                                       int64_t S, int64_t CAP, int dtype, yh_stream_t stream) {
+  using namespace yh;
+  YH_CHECK_ARG(first != nullptr || B == 0, "anchor_sequence_read: null pointer");
+  return launch_indexed(query, key, value, references, ref_dtype, out, B, NB, C, H, G, D, B, S, CAP, first, L, dtype,
+                        stream, "anchor_sequence_read");
 }

@@ -292,12 +292,7 @@ def sequence(query, key, value, scores, valid, chunk, state: IndependentMemorySt
         order = valid.long().argsort(dim=1, descending=True, stable=True)
         q, k, v, sc = (x[bi, order] for x in (query, key, value, scores))
         counts = valid.sum(1)
-    blocks = -(-length // c) + 1                  # extent = ceil((L + C) / C) * C
-    extent = blocks * c
-    at = torch.arange(extent, device=dev)[None]
-    old = state.count[:, None]
-    select = torch.where(at < old, at, c + at - old).clamp_max(c + length - 1)
-    q_ext = torch.cat((q.new_zeros(b, c, h, d), q), 1)[bi, select].contiguous()
+    blocks = -(-length // c) + 1                  # ceil((L + C) / C) blocks of C positions
     src_k = torch.cat((state.keys.transpose(1, 2), state.pending_keys[:, :, :c].transpose(1, 2), k), 1).contiguous()
     src_v = torch.cat((state.values.transpose(1, 2), state.pending_values[:, :, :c].transpose(1, 2), v),
                       1).contiguous()
@@ -312,8 +307,13 @@ def sequence(query, key, value, scores, valid, chunk, state: IndependentMemorySt
            state.positions.data_ptr(), state.pending_scores.data_ptr(), state.count.data_ptr(),
            state.total.data_ptr(), block_refs.data_ptr(), final_refs.data_ptr(), pending_refs.data_ptr(), b, length,
            g, cap, pc, c, blocks, st)
-    read = indexed_gqa(q_ext.view(b, blocks, c, h, d), src_k, src_v, block_refs).flatten(1, 2)
-    out = read[bi, (old + torch.arange(length, device=dev)[None]).clamp_max(extent - 1)]
+    # block position p of row b reads token p - old[b] in place (the old
+    # pending tokens open the first block and read nothing here)
+    first = state.count.contiguous()
+    qc = q.contiguous()
+    out = torch.empty_like(qc)
+    N.call("yh_anchor_sequence_read", qc.data_ptr(), src_k.data_ptr(), src_v.data_ptr(), block_refs.data_ptr(),
+           N.I32, first.data_ptr(), out.data_ptr(), b, length, blocks, c, h, g, d, n_src, cap, N.code(qc), st)
     if order is not None:
         out = out[bi, order.argsort(1)] * valid[..., None, None].to(out.dtype)
     N.call("yh_anchor_sequence_commit", src_k.data_ptr(), src_v.data_ptr(), final_refs.data_ptr(),
