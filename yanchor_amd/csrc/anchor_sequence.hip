@@ -17,8 +17,8 @@
 // commit does one chunk at a time.  One workgroup per (row, group) ranks the
 // committed slots once (the reference merges them into every prefix, so even
 // a chunk with no full block leaves them in rank order), then scans the
-// blocks; every merge ranks the K + C candidates by counting, as the decode
-// commit kernel does.
+// blocks; every merge ranks the block's C candidates by counting and places
+// them and the memory by binary search in each other's rank order.
 //
 // Source rows (per batch row, shared by its groups) number the candidates:
 //   [0, K)          the committed slots of the state
@@ -97,6 +97,79 @@ __device__ __forceinline__ void rank_into_memory(uint64_t* ckey, float* cscore, 
   __syncthreads();
 }
 
+// The memory [0, KC) is in rank order.  Merge the C candidates at [KC, KC + C)
+// in (the next block, in token order) and keep the best KC, in rank order:
+// the same result as rank_into_memory over all KC + C (one strict order:
+// key, then candidate index, so a memory entry wins a tie with a block entry
+// and block entries tie in token order).  The block is ranked by counting
+// (C x C), then each entry's merged rank is its place in its own list plus the
+// number of the other list's entries above it (a binary search).  Starts and
+// ends with a workgroup barrier.
+__device__ __forceinline__ void merge_into_memory(uint64_t* ckey, float* cscore, int32_t* cpos, int32_t* cref,
+                                                  int32_t* chosen, int KC, int C, int tid) {
+  __syncthreads();
+  for (int i = tid; i < KC + C; i += kSeqThreads) ckey[i] = topk_key(cscore[i], cpos[i]);
+  __syncthreads();
+  for (int i = tid; i < C; i += kSeqThreads) {  // the block in rank order: chosen[r] = its candidate
+    const uint64_t mine = ckey[KC + i];
+    int rank = 0;
+    for (int m = 0; m < C; ++m) {
+      const uint64_t o = ckey[KC + m];
+      rank += (o < mine) | ((o == mine) & (m < i));
+    }
+    chosen[rank] = KC + i;
+  }
+  __syncthreads();
+  // merged ranks: memory entry p is above block entries with key >= its own;
+  // block entry q (in block rank order) is above memory entries with key > its own
+  float rs[kSeqPer];
+  int32_t rp[kSeqPer], rr[kSeqPer], rk[kSeqPer];
+#pragma unroll
+  for (int k = 0; k < kSeqPer; ++k) {
+    const int e = tid + k * kSeqThreads;  // [0, KC): memory p = e; [KC, KC + C): block rank q = e - KC
+    rk[k] = KC;                            // not kept
+    if (e < KC + C) {
+      int src, rank;
+      if (e < KC) {
+        src = e;
+        const uint64_t mine = ckey[e];
+        int lo = 0, hi = C;  // block entries (rank order, keys non-decreasing) with key < mine
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (ckey[chosen[mid]] < mine) lo = mid + 1; else hi = mid;
+        }
+        rank = e + lo;
+      } else {
+        const int q = e - KC;
+        src = chosen[q];
+        const uint64_t mine = ckey[src];
+        int lo = 0, hi = KC;  // memory entries (rank order) with key <= mine
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (ckey[mid] <= mine) lo = mid + 1; else hi = mid;
+        }
+        rank = q + lo;
+      }
+      if (rank < KC) {
+        rk[k] = rank;
+        rs[k] = cscore[src];
+        rp[k] = cpos[src];
+        rr[k] = cref[src];
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kSeqPer; ++k) {
+    if (rk[k] < KC) {
+      cscore[rk[k]] = rs[k];
+      cpos[rk[k]] = rp[k];
+      cref[rk[k]] = rr[k];
+    }
+  }
+  __syncthreads();
+}
+
 __global__ void __launch_bounds__(kSeqThreads) anchor_prefix_kernel(PrefixArgs a) {
   __shared__ uint64_t ckey[kSeqMaxCand];
   __shared__ float cscore[kSeqMaxCand];
@@ -152,7 +225,7 @@ __global__ void __launch_bounds__(kSeqThreads) anchor_prefix_kernel(PrefixArgs a
       cpos[n] = static_cast<int32_t>(base_pos + q);
       cref[n] = static_cast<int32_t>(old ? KC + q : KC + C + (q - old_count));
     }
-    rank_into_memory(ckey, cscore, cpos, cref, chosen, N, KC, tid);
+    merge_into_memory(ckey, cscore, cpos, cref, chosen, KC, C, tid);
   }
 
   // the final memory, in rank order, and the tokens left pending
