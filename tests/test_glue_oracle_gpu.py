@@ -221,6 +221,43 @@ def test_window_attend_matches_oracle(gpu, b, g, h, win, live):
     assert ulps(plain, want) <= 2.0001
 
 
+@pytest.mark.parametrize("g,h", [(8, 32), (2, 4), (4, 4)])
+def test_window_attend_dead_blocks(gpu, g, h):
+    """Rings that fill from slot 0 (a sequence shorter than the window) and
+    rings with whole 16-slot blocks dead between live ones: the read skips
+    blocks without a live slot, and must equal the masked softmax over the
+    whole ring (inference_kernels.py:624-640).  Live counts sit on and beside
+    block edges; dead slots hold large garbage so a skipped block that was
+    still summed would show."""
+    d, win = 128, 1024
+    lengths = [1, 2, 15, 16, 17, 31, 32, 33, 64, 100, 500, 1007, 1008, 1023, 1024]
+    b = len(lengths) + 3
+    gen = torch.Generator(device=gpu).manual_seed(97)
+    keys = torch.randn(b, g, win, d, device=gpu, generator=gen).to(torch.bfloat16)
+    vals = torch.randn(b, g, win, d, device=gpu, generator=gen).to(torch.bfloat16)
+    slot = torch.arange(win, device=gpu)
+    live = torch.zeros(b, win, dtype=torch.bool, device=gpu)
+    for r, n in enumerate(lengths):
+        live[r, :n] = True
+    live[len(lengths), (slot // 16) % 3 == 1] = True              # one live block in three
+    live[len(lengths) + 1, 1000] = True                           # one live slot, in the last blocks
+    live[len(lengths) + 2, (slot // 16) % 2 == 0] = True          # even blocks: one wave's share only
+    live[len(lengths) + 2, 16 * 7 + 5] = True                     # and one slot of an odd block
+    keys = torch.where(live[:, None, :, None], keys, torch.full_like(keys, 300.0))
+    vals = torch.where(live[:, None, :, None], vals, torch.full_like(vals, 1e4))
+    pos = torch.where(live, slot.to(torch.int32), -1)[:, None].expand(b, g, win).contiguous()
+    q = torch.randn(b, 1, h, d, device=gpu, generator=gen).to(torch.bfloat16)
+    got = im.ring_decode_attention(q, keys, vals, pos).cpu()
+    want = glue.ring_decode_attention(q.cpu(), keys.cpu(), vals.cpu(), live.cpu())
+    err = rel_err(got, want)
+    print(f"G={g} H={h} W={win}, {b} fill patterns: read {err:.2e}", flush=True)
+    assert err <= BF16_TOL
+    assert ulps(got, want) <= 2.0001
+    # per row: every fill pattern, not only the batch as a whole
+    for r in range(b):
+        assert rel_err(got[r], want[r]) <= BF16_TOL, r
+
+
 @pytest.mark.parametrize("b", [1, 128])
 def test_memory_decode_matches_oracle(gpu, b):
     """The anchor-memory projections of one decode token (input norm, the

@@ -257,6 +257,10 @@ anchor_read_kernel(ReadArgs a) {
   constexpr int NI = BS / RPI;
   constexpr int F = LPR / NI;
   static_assert(NI * RPI == BS && F * NI == LPR && F >= 1 && BS <= 32, "slot blocks");
+  // window reads skip whole blocks without a live slot (a ring fills from slot
+  // 0, so a sequence shorter than the window leaves its tail blocks dead)
+  constexpr bool BSKIP = !SINK;
+  static_assert(kMaxCap / 16 <= 64 && kMaxCap % 64 == 0, "one bit per block");
 
   __shared__ float wm[kReadWaves][R];
   __shared__ float wl[kReadWaves][R];
@@ -326,10 +330,11 @@ anchor_read_kernel(ReadArgs a) {
     // first block is fetched whole
     // SKIP: every position of (b, g) is requested first; the vector-memory
     // counter is in order, so the ballots below wait for these loads only
-    int32_t pv[SKIP ? kSkipMaxCap / 64 : 1];
-    if constexpr (SKIP) {
+    // BSKIP: the same for every slot of the ring (up to kMaxCap)
+    int32_t pv[SKIP ? kSkipMaxCap / 64 : BSKIP ? kMaxCap / 64 : 1];
+    if constexpr (SKIP || BSKIP) {
 #pragma unroll
-      for (int c = 0; c < kSkipMaxCap / 64; ++c) {
+      for (int c = 0; c < (SKIP ? kSkipMaxCap : kMaxCap) / 64; ++c) {
         const int slot = c * 64 + lane;
         pv[c] = pos[slot < a.KC ? slot : 0] | (slot < a.KC ? 0 : int32_t(0x80000000));
       }
@@ -455,8 +460,32 @@ anchor_read_kernel(ReadArgs a) {
         live = lnxt;
       }
     } else {
-      for (int blk = wid; blk < nblk; blk += kReadWaves) {
-        const int nxt = (blk + kReadWaves < nblk ? blk + kReadWaves : blk) * BS;  // past the end: this block again
+      // BSKIP: this wave's blocks (blk = wid mod kReadWaves) that hold a live
+      // slot; the others are never fetched.  A dead block is a no-op of the
+      // online softmax (its logits are -inf, its values 0), so the sum is the
+      // one over every block, bit for bit.
+      uint64_t mine = 0;
+      if constexpr (BSKIP) {
+        constexpr uint64_t kBlkBits = (1ull << BS) - 1;
+#pragma unroll
+        for (int c = 0; c < kMaxCap / 64; ++c) {
+          const uint64_t m = __ballot(pv[c] >= 0);
+#pragma unroll
+          for (int j = 0; j < 64 / BS; ++j)
+            mine |= static_cast<uint64_t>(((m >> (j * BS)) & kBlkBits) != 0) << (c * (64 / BS) + j);
+        }
+        uint64_t res = 0;  // bits wid, wid + kReadWaves, ...
+#pragma unroll
+        for (int j = 0; j < 64; j += kReadWaves) res |= 1ull << j;
+        mine &= res << wid;
+      }
+      for (int blk = wid; blk < nblk;) {
+        int nb = blk + kReadWaves;
+        if constexpr (BSKIP) {
+          const uint64_t rest = mine & ~((2ull << blk) - 1);  // live blocks of this wave past blk
+          nb = rest ? static_cast<int>(__builtin_ctzll(rest)) : nblk;
+        }
+        const int nxt = (nb < nblk ? nb : blk) * BS;  // past the end: this block again
         const uint32_t live = static_cast<uint32_t>(__ballot(pcur >= 0));
         step_block(kr, vr, live,
                    [&] {
@@ -464,6 +493,7 @@ anchor_read_kernel(ReadArgs a) {
                      ld_block<DT, NI, RPI * D>(kr, kptr + static_cast<int64_t>(nxt) * D * kEsz);
                    },
                    [&] { ld_block<DT, NI, RPI * D>(vr, vptr + static_cast<int64_t>(nxt) * D * kEsz); });
+        blk = nb;
       }
     }
   }
