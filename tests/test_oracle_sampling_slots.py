@@ -88,6 +88,54 @@ def test_fused_and_torch_samplers_agree_away_from_ties():
     assert (fused == tor).float().mean().item() > 0.95
 
 
+def _top20_exact_ranks(values, attempt_ids, steps, seed, top_p, prefix_rule="before"):
+    """The fused top-20 rule in float64 (softmax, keep p while the mass before it
+    is below top_p, threshold u * retained, rank = #(cumulative < threshold)),
+    with the margin of each row to its nearest decision boundary."""
+    v = values.double()
+    p = torch.softmax(v, dim=-1)
+    cum_all = p.cumsum(-1)
+    before = cum_all - p if prefix_rule == "before" else cum_all
+    keep = before < top_p
+    trunc = torch.where(keep, p, torch.zeros_like(p))
+    retained = trunc.sum(-1, keepdim=True)
+    cum = trunc.cumsum(-1)
+    u = torch.tensor([(sampling.counter_word(int(a), int(t), seed) + 0.5) / 4294967296.0
+                      for a, t in zip(attempt_ids.tolist(), steps.tolist())], dtype=torch.float64)[:, None]
+    thr = u * retained
+    rank = (cum < thr).sum(-1).clamp_max(values.shape[-1] - 1)
+    margin = torch.minimum((before - top_p).abs().min(-1).values, ((cum - thr).abs() / retained).min(-1).values)
+    return rank, margin
+
+
+def test_top20_sampler_matches_exact_rule_away_from_boundaries():
+    """Pins the fused top-20 restatement (inference_kernels.py:1119-1145) to
+    the same rule evaluated in float64: on every row whose threshold and top-p
+    cut sit more than 1e-5 from a cumulative boundary, the float32 restatement
+    picks the same rank.  Varied temperatures, top_p in (0, 1] and heavy/flat
+    rows; a planted mistake (keep p while cumsum(p), not the mass before p, is
+    below top_p) must fail the same check."""
+    g = torch.Generator().manual_seed(19)
+    rows = 512
+    logits = torch.randn(rows, 1000, generator=g) * torch.linspace(0.2, 6.0, rows)[:, None]
+    att = torch.randint(0, 1 << 31, (rows,), generator=g)
+    steps = torch.randint(0, 1 << 20, (rows,), generator=g)
+    vals, idx = torch.topk(logits, 20)
+    checked = 0
+    for top_p, temp in ((0.95, 0.6), (0.5, 1.0), (1.0, 0.8), (0.05, 1.3)):
+        scaled = vals / temp
+        got = sampling.top20_counter_sample(scaled, idx, att, steps, seed=7, top_p=top_p)[:, 0]
+        rank, margin = _top20_exact_ranks(scaled, att, steps, 7, top_p)
+        want = idx.gather(1, rank[:, None])[:, 0]
+        ok = margin > 1e-5
+        checked += int(ok.sum())
+        assert torch.equal(got[ok], want[ok]), top_p
+        if 0.1 < top_p < 1.0:  # (at top_p 0.05 both rules keep only the top candidate)
+            bad_rank, _ = _top20_exact_ranks(scaled, att, steps, 7, top_p, prefix_rule="cumsum")
+            assert not torch.equal(got[ok], idx.gather(1, bad_rank[:, None])[:, 0][ok]), top_p
+    assert checked > 0.9 * 4 * rows
+
+
 def _bookkeeping_scenario(seed, slots_n=12, attempts=20, width=9, vocab=50):
     g = torch.Generator().manual_seed(seed)
     st = dict(
