@@ -47,8 +47,9 @@ conv window update, state update and gated norm of one GDN layer): its
 algorithmic bytes per launch at the model's decode shape over its average
 launch time, measured here with HIP events on the stream the kernel runs on,
 cycling over the model's 27 GDN layers.  ``cpu_baseline`` runs the same
-model's decode step on the host cores with the oracle's recurrence, anchor
-memory, sampler and bookkeeping, on a bounded number of steps.
+model's decode step on the host cores with every op from the oracle
+(oracle/model_ops.py: recurrence, anchor memory, ring attention, layer glue,
+sampler), on a bounded number of steps.
 """
 from __future__ import annotations
 
@@ -261,62 +262,6 @@ def bench_model_decode(steps, warmup, cpu, batch=128):
     return res
 
 
-class _OracleOps:
-    """The oracle's CPU recurrence, anchor memory, sampler and bookkeeping
-    behind the runtime's ops interface (float32), plus the torch layer glue."""
-
-    def __init__(self):
-        from oracle import anchor, gdn, sampling, slots
-        from yanchor_amd.runtime import TorchGlue
-        self.gdn_ref, self.anchor, self.sampling, self.slots = gdn, anchor, sampling, slots
-        self.glue = TorchGlue
-        from yanchor_amd.runtime import gate_read
-        self.gate_read = gate_read
-        for name in ("decode_inputs", "rmsnorm", "gdn_prep", "gated_rmsnorm", "silu_mul", "head_norm_rope", "ring_write",
-                     "memory_prologue"):
-            setattr(self, name, getattr(TorchGlue, name))
-
-    @staticmethod
-    def linear(x, w, packed=None, residual=None, defer=False):
-        out = torch.nn.functional.linear(x, w)
-        return out if residual is None else out + residual
-
-    def mlp_act(self, x, w, packed=None):
-        return self.silu_mul(torch.nn.functional.linear(x, w))
-
-    def gdn_decode(self, q, k, v, g, beta, state):
-        o, st = self.gdn_ref.recurrent_gated_delta_rule(q, k, v, g, beta, state, dtype=torch.float32)
-        state.copy_(st)
-        return o.to(q.dtype)
-
-    def window_attend(self, q, keys, values, positions, gate=None):
-        b, _, h, d = q.shape
-        g = keys.shape[1]
-        qq = q[:, 0].reshape(b, g, h // g, d).float()
-        logits = torch.matmul(qq, keys.float().transpose(-1, -2)) / math.sqrt(d)     # [B, G, R, W]
-        logits = logits.masked_fill((positions < 0)[:, :, None, :], -math.inf)
-        out = torch.matmul(logits.softmax(-1), values.float())
-        return self.gate_read(out.reshape(b, 1, h, d).to(q.dtype), gate=gate)
-
-    def memory_read(self, q, state, valid=None, head_gate=None):
-        return self.gate_read(self.anchor.committed_read(q, state, dtype=torch.float32), valid, head_gate)
-
-    def memory_commit(self, key, value, scores, active, chunk, state):
-        self.anchor.commit_decode(key, value, scores, active, chunk, state)
-
-    def memory_sequence(self, q, key, value, scores, valid, chunk, state):
-        return self.anchor.sequence(q, key, value, scores, valid, chunk, state, dtype=torch.float32)
-
-    def sample(self, logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty,
-               backend="triton_top20"):
-        sc = self.sampling.presence_penalty(logits, seen, penalty) if seen is not None else logits.float()
-        vals, idx = torch.topk(sc / temperature, top_k, dim=-1)
-        return self.sampling.top20_counter_sample(vals, idx, attempt_ids, steps, seed=seed, top_p=top_p)
-
-    def bookkeeping(self, *args, **kw):
-        self.slots.decode_state_update_torch(*args, **kw)
-
-
 def cpu_model_decode(batch, budget_s=20.0, max_steps=32, single_thread=True):
     """Decode steps of the same model shape on the host cores: float32 weights
     (tiled N(0, 0.02) block), every slot live at position 128, the oracle's
@@ -329,7 +274,9 @@ def cpu_model_decode(batch, budget_s=20.0, max_steps=32, single_thread=True):
     torch.set_num_threads(threads)
     host = cpu_host_info()
     cfg = rt.ModelConfig()
-    m = rt.Model(cfg, batch=batch, device="cpu", seed=0, ops=_OracleOps(), dtype=torch.float32, init="tiled")
+    from oracle.model_ops import HostOps
+
+    m = rt.Model(cfg, batch=batch, device="cpu", seed=0, ops=HostOps(), dtype=torch.float32, init="tiled")
     gen = torch.Generator().manual_seed(5)
     tokens = torch.randint(0, cfg.vocab, (batch,), generator=gen)
     positions = torch.full((batch,), 128, dtype=torch.long)
@@ -354,7 +301,8 @@ def cpu_model_decode(batch, budget_s=20.0, max_steps=32, single_thread=True):
             break
     res = {"value": batch * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
            "sample": f"{n} decode steps x {batch} live slots of the same 36-layer model in float32 on "
-                     f"{threads} host threads (oracle recurrence, anchor memory, sampler), {el:.1f} s; "
+                     f"{threads} host threads (every op from the oracle: recurrence, anchor memory, ring attention, "
+                     f"layer glue, sampler), {el:.1f} s; "
                      "refill prefill excluded as in the GPU figure",
            "host": host}
     if single_thread:

@@ -1,0 +1,166 @@
+"""The decode step's ops on the host, from the oracle's restatements only
+(oracle; test infrastructure: imported by tests/ and by bench.py's CPU
+baseline leg, never by the product).
+
+``HostOps`` implements the ops interface that ``yanchor_amd.runtime.Model``
+calls for one decode token per slot, so the product's model wiring can run on
+the CPU in float32 with every piece of arithmetic taken from ``oracle/``:
+
+* the GDN recurrence          ``oracle.gdn.recurrent_gated_delta_rule``
+                              (wheel transformers/models/qwen3_5/
+                              modeling_qwen3_5.py:314-353);
+* the anchor memory           ``oracle.anchor.committed_read`` /
+                              ``commit_decode`` (modeling_yanchor.py:283-312);
+* the SWA ring read / write   ``oracle.glue.ring_decode_attention``
+                              (runtime/model/inference_kernels.py:624-640) and
+                              the chronological ring write (1828-1856);
+* the layer glue              ``oracle.glue``: Qwen3_5RMSNorm, the gated
+                              norm, the conv update of the CUDA backend, the
+                              gates, RoPE, the memory's query side
+                              (modeling_yanchor.py:168-176) and the writer's
+                              silu * up (147-166);
+* sampling and bookkeeping    ``oracle.sampling`` / ``oracle.slots``.
+
+Arguments and results follow the runtime's ops (the same names, layouts and
+return tuples); tensors are float32 on the host.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from oracle import anchor, gdn, glue, sampling, slots
+
+HEAD_DIM = 128
+
+
+def gate_read(read, valid=None, head_gate=None):
+    """The decode layer's gating of a memory read [B, 1, H, D]:
+    read * valid (modeling_yanchor.py:313) times the per-head read gate of
+    _query_scores (modeling_yanchor.py:170, applied at 316)."""
+    if valid is not None:
+        read = read * valid[:, None, None, None].to(read.dtype)
+    if head_gate is not None:
+        read = read * head_gate[:, None, :, None].to(read.dtype)
+    return read
+
+
+class HostOps:
+    """The runtime's decode ops on the CPU from the oracle's functions."""
+
+    # ---- layer glue ----
+    @staticmethod
+    def decode_inputs(tokens, positions, embed, w, inv_freq, eps, *, ring_stride, window, finished=None,
+                      slot_rows=None):
+        """Embedding row, the first layer's input norm, the rotary tables
+        (rope_cos_sin), the SWA ring row b * ring_stride + position % window
+        and the live-slot mask ~finished & slot_rows >= 0."""
+        h = embed[tokens]
+        cos, sin = glue.rope_cos_sin(positions, inv_freq, torch.float32)
+        rows = torch.arange(tokens.shape[0]) * ring_stride + positions % window
+        valid = None if finished is None else (~finished) & (slot_rows >= 0)
+        return h, glue.rms_norm(h, w, eps), cos, sin, rows, valid
+
+    @staticmethod
+    def rmsnorm(x, w, eps, residual=None, w2=None):
+        """Qwen3_5RMSNorm of x (+ residual); returns the normed row, then the
+        sum when a residual is given, then the row normed with w2."""
+        s = x if residual is None else x + residual
+        out = [glue.rms_norm(s, w, eps)]
+        if residual is not None:
+            out.append(s)
+        if w2 is not None:
+            out.append(glue.rms_norm(s, w2, eps))
+        return out[0] if len(out) == 1 else tuple(out)
+
+    @staticmethod
+    def linear(x, w, packed=None, residual=None, defer=False):
+        out = F.linear(x, w)
+        return out if residual is None else out + residual
+
+    @staticmethod
+    def silu_mul(gate_up):
+        gate, up = gate_up.chunk(2, -1)
+        return glue.silu_mul(gate, up)
+
+    def mlp_act(self, x, w, packed=None):
+        return self.silu_mul(F.linear(x, w))
+
+    @staticmethod
+    def gdn_prep(proj, conv_state, conv_w, a_log, dt_bias, *, conv_dim, qk_dim, hv, b_offset, a_offset):
+        """Conv update of the CUDA backend (the runtime's conv window is
+        time-major [B, K-1, C]; the oracle's state is [B, C, K-1]) and the
+        gates; returns q, k, v, g, beta."""
+        st = conv_state.transpose(1, 2).contiguous()
+        mixed = glue.causal_conv1d_update_cuda(proj[:, :conv_dim, None], st, conv_w)[..., 0]
+        conv_state.copy_(st.transpose(1, 2))
+        beta, g = glue.gdn_gates(proj[:, b_offset: b_offset + hv], proj[:, a_offset: a_offset + hv], a_log, dt_bias)
+        return mixed[:, :qk_dim], mixed[:, qk_dim: 2 * qk_dim], mixed[:, 2 * qk_dim:], g, beta.float()
+
+    @staticmethod
+    def gated_rmsnorm(o, z, w, eps):
+        b, h, d = o.shape
+        return glue.gated_rms_norm(o, z.reshape(b, h, d), w, eps).reshape(b, h * d)
+
+    @staticmethod
+    def head_norm_rope(x, w, cos, sin, rotary_dim, eps):
+        """Per-head Qwen3_5RMSNorm, then RoPE on the first rotary_dim dims."""
+        y = glue.rms_norm(x, w, eps)
+        if rotary_dim:
+            y = glue.memory_rope(y, cos[:, None, :rotary_dim], sin[:, None, :rotary_dim])
+        return y
+
+    def ring_write(self, k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rotary_dim, eps):
+        """The normed, rotated key, the value and the position of the decode
+        token into ring slot position % window (inference_kernels.py:1828-1856)."""
+        key = self.head_norm_rope(k, w, cos, sin, rotary_dim, eps)
+        tok = torch.arange(k.shape[0])
+        slot = positions % ring_k.shape[2]
+        ring_k[tok, :, slot] = key.to(ring_k.dtype)
+        ring_v[tok, :, slot] = v.to(ring_v.dtype)
+        ring_pos[tok, :, slot] = positions.to(torch.int32)[:, None]
+
+    @staticmethod
+    def window_attend(q, keys, values, positions, gate=None):
+        return glue.ring_decode_attention(q, keys, values, positions >= 0, gate)
+
+    @staticmethod
+    def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b,
+                        adm_up, rotary_dim, eps):
+        """_query_scores from the fused projection [q | features | ...]:
+        q_norm, the read gate before RoPE, RoPE, the admission scores."""
+        b = proj.shape[0]
+        qn = glue.rms_norm(proj[:, : heads * HEAD_DIM].view(b, heads, HEAD_DIM), q_norm_w, eps)
+        gate = glue.query_read_gate(qn, read_scale, gate_w, gate_b)
+        q = glue.memory_rope(qn, cos[:, None, :rotary_dim], sin[:, None, :rotary_dim])
+        scores = glue.admission_scores(proj[:, feat_offset: feat_offset + n_features], adm_up)
+        return q, gate, scores
+
+    # ---- the recurrence and the anchor memory ----
+    @staticmethod
+    def gdn_decode(q, k, v, g, beta, state):
+        o, st = gdn.recurrent_gated_delta_rule(q, k, v, g, beta, state, dtype=torch.float32)
+        state.copy_(st)
+        return o.to(q.dtype)
+
+    @staticmethod
+    def memory_read(q, state, valid=None, head_gate=None):
+        return gate_read(anchor.committed_read(q, state, dtype=torch.float32).to(q.dtype), valid, head_gate)
+
+    @staticmethod
+    def memory_commit(key, value, scores, active, chunk, state):
+        anchor.commit_decode(key, value, scores, active, chunk, state)
+
+    # ---- sampling and bookkeeping ----
+    @staticmethod
+    def sample(logits, attempt_ids, steps, seen, *, seed, temperature, top_k, top_p, penalty,
+               backend="triton_top20"):
+        """The fused top-20 sampler (inference_kernels.py:1119-1167) with the
+        presence penalty."""
+        sc = sampling.presence_penalty(logits, seen, penalty) if seen is not None else logits.float()
+        vals, idx = torch.topk(sc / temperature, top_k, dim=-1)
+        return sampling.top20_counter_sample(vals, idx, attempt_ids, steps, seed=seed, top_p=top_p)
+
+    @staticmethod
+    def bookkeeping(*args, **kw):
+        slots.decode_state_update_torch(*args, **kw)
