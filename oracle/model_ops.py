@@ -3,14 +3,17 @@
 baseline leg, never by the product).
 
 ``HostOps`` implements the ops interface that ``yanchor_amd.runtime.Model``
-calls for one decode token per slot, so the product's model wiring can run on
-the CPU in float32 with every piece of arithmetic taken from ``oracle/``:
+calls for one decode token per slot (and the two a prefill calls), so the
+product's model wiring can run on the CPU in float32 with every piece of
+arithmetic of the decode step taken from ``oracle/``:
 
 * the GDN recurrence          ``oracle.gdn.recurrent_gated_delta_rule``
                               (wheel transformers/models/qwen3_5/
-                              modeling_qwen3_5.py:314-353);
+                              modeling_qwen3_5.py:314-353) and, for prefill,
+                              its chunked form per packed sequence (234-311);
 * the anchor memory           ``oracle.anchor.committed_read`` /
-                              ``commit_decode`` (modeling_yanchor.py:283-312);
+                              ``commit_decode`` (modeling_yanchor.py:283-312)
+                              and, for prefill, ``sequence`` (178-275);
 * the SWA ring read / write   ``oracle.glue.ring_decode_attention``
                               (runtime/model/inference_kernels.py:624-640) and
                               the chronological ring write (1828-1856);
@@ -142,6 +145,19 @@ class HostOps:
         o, st = gdn.recurrent_gated_delta_rule(q, k, v, g, beta, state, dtype=torch.float32)
         state.copy_(st)
         return o.to(q.dtype)
+
+    @staticmethod
+    def gdn_prefill(q, k, v, g, beta, cu_seqlens, lengths):
+        """Packed prefill from zero states: the chunked form (wheel:234-311)
+        per sequence of cu_seqlens; returns (o, final states)."""
+        o, st = gdn.varlen(gdn.chunk_gated_delta_rule, q, k, v, g, beta, cu_seqlens.tolist(), dtype=torch.float32)
+        return o.to(q.dtype), st
+
+    @staticmethod
+    def memory_sequence(q, key, value, scores, valid, chunk, state):
+        """Prefill read and write continuing ``state`` (_sequence,
+        modeling_yanchor.py:178-275)."""
+        return anchor.sequence(q, key, value, scores, valid, chunk, state, dtype=torch.float32).to(q.dtype)
 
     @staticmethod
     def memory_read(q, state, valid=None, head_gate=None):
