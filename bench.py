@@ -376,7 +376,7 @@ def bench_long_horizon(steps, warmup, cpu, batch=256, gen_len=32768, prompt_len=
     _log(f"long_horizon: {batch} sequences x {gen_len} tokens; {warmup} warm-up + {steps} timed steps")
     torch.cuda.reset_peak_memory_stats()
     met = rt.run_decode_benchmark(model, steps=steps, warmup=warmup, poll_interval=1 << 30, requests=reqs,
-                                  max_new_tokens=gen_len)
+                                  max_new_tokens=gen_len, progress_every=2048)
     res = {
         "value": met.decode_tokens_per_second,
         "unit": "tokens/s",

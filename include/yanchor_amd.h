@@ -170,7 +170,10 @@ int yh_anchor_read(const void* query, const void* keys, const void* values, cons
  * marks live slots (>= 0).  Replaces the physical-ring SWA decode attention
  * (fixed_memory_physical_ring_decode_attention, runtime/model/
  * inference_kernels.py:555-640) for D in {64, 128}, H / G in {1, 2, 4} and a
- * window that is a multiple of 16, at most 1024.
+ * window that is a multiple of 16, at most 1024.  Key and value rows are
+ * fetched only for blocks of 16 (or 32) slots that hold a live slot, so a ring
+ * that fills from slot 0 costs in proportion to its live slots; the result is
+ * that of the full pass.
  */
 int yh_window_attend(const void* query, const void* keys, const void* values, const int32_t* positions,
                      const int32_t* indices, void* out, int64_t B, int64_t H, int64_t G, int64_t window, int64_t D,

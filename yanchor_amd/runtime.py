@@ -1016,7 +1016,7 @@ def synthetic_requests(steps, *, rate=4.0, prompt_len=128, mean_len=1024, max_le
 
 def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=128, mean_len=1024,
                          poll_interval=32, seed=20260923, use_graph=True, max_new_tokens=8192, requests=None,
-                         tail_compaction=False, engine=None, initial_fill=True):
+                         tail_compaction=False, engine=None, initial_fill=True, progress_every=0):
     """Continuous batching for warmup + steps decode steps; returns metrics of
     the timed steps (the reference's decode tokens/s definition).
 
@@ -1063,6 +1063,8 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
                 m.refilled += taken
                 m.completed += done
         eng.step()
+        if progress_every and (step + 1) % progress_every == 0:
+            print(f"[decode] step {step + 1} of {total} enqueued", flush=True)
         if t_start is not None:
             m.decode_steps += 1
             m.decode_scheduled_token_events += eng.B
