@@ -637,12 +637,18 @@ int yh_ring_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride, co
  *   gate   = tanh(read_scale) * 2 * sigmoid(<qn_h, gate_w_h> / sqrt(128) + gate_b)
  *            (qn_h the normed, unrotated head as bf16)      float [B, H]
  *   scores = bf16(silu(features)) . adm_up^T                float [B, G]
+ *   act    = bf16(bf16(silu(gate)) * up)                    bf16 [B, act_width]
+ *            (the writer's activation of _write_kv, modeling_yanchor.py:
+ *            159-166: gate = proj columns [act_offset, act_offset + act_width),
+ *            up the act_width columns after them; act rows act_stride apart;
+ *            act NULL skips it; 16-byte aligned rows)
  * read_scale, gate_b float [H]; gate_w float [H, 128]; adm_up float [G, A].
  */
 int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t feat_offset, const void* q_norm_w,
                        const float* cos, const float* sin, const float* read_scale, const float* gate_w,
                        const float* gate_b, const float* adm_up, void* q, float* gate, float* scores, int64_t B,
-                       int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps, yh_stream_t stream);
+                       int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps, int64_t act_offset,
+                       int64_t act_width, void* act, int64_t act_stride, yh_stream_t stream);
 
 /*
  * HBM calibration stream (no counterpart in the reference: the measuring stick

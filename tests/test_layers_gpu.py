@@ -305,6 +305,15 @@ def test_memory_prologue(gpu, b):
     assert ((q.float() - rq.float()).abs() <= bound * 1.0001 + 1e-30).all()
     assert (q != rq).float().mean().item() <= 0.02
     assert rel_err(gate, rgate) <= 1e-5 and rel_err(scores, rscores) <= 1e-5
+    # the writer's activation in the same launch: silu_mul's output bit for
+    # bit, and the other outputs unchanged by it
+    wi = 256
+    proj2 = rnd(b, h * d + a + 2 * wi, dev=gpu, scale=2.0, seed=53)
+    args2 = (proj2,) + args[1:]
+    q1, gate1, scores1 = layers.memory_prologue(*args2)
+    q2, gate2, scores2, act = layers.memory_prologue(*args2, act_offset=h * d + a, act_width=wi)
+    assert torch.equal(act, layers.silu_mul(proj2[:, h * d + a:]))
+    assert torch.equal(q1, q2) and torch.equal(gate1, gate2) and torch.equal(scores1, scores2)
 
 
 @pytest.mark.parametrize("split", [1, 4])

@@ -51,7 +51,7 @@ SIGNATURES: dict[str, list] = {
     "yh_ring_write": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                       _f32, _p],
     "yh_memory_prologue": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
-                           _i64, _f32, _p],
+                           _i64, _f32, _i64, _i64, _p, _i64, _p],
     "yh_anchor_read_gated": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p,
                              _i32, _p],
     "yh_window_attend_gated": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i32, _p],

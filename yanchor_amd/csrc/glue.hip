@@ -395,6 +395,9 @@ struct MemProArgs {
   float* scores;            // [B, G]
   int H, G, A, rd, feat_off;
   float eps;
+  uint16_t* act;            // [B, act_w] rows act_s apart, or null
+  int64_t act_s;
+  int act_off, act_w;       // writer gate columns [act_off, act_off + act_w), up columns after them
 };
 
 __global__ void __launch_bounds__(256) memory_prologue_kernel(MemProArgs a) {
@@ -402,8 +405,22 @@ __global__ void __launch_bounds__(256) memory_prologue_kernel(MemProArgs a) {
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
   const uint16_t* row = a.proj + b * a.ps;
   if (static_cast<int>(blockIdx.y) * 4 >= a.H) {
-    // admission scores: silu(features) rounded to bf16, then fp32 dots
-    if (wv != 0) return;
+    if (wv != 0) {
+      // waves 1-3: the writer's silu(gate) * up (silu_mul_kernel's roundings)
+      if (a.act == nullptr) return;
+      for (int v = (wv - 1) * kWave + lane; v < a.act_w / 8; v += 3 * kWave) {
+        const uint4 gv = *reinterpret_cast<const uint4*>(row + a.act_off + 8 * v);
+        const uint4 uv = *reinterpret_cast<const uint4*>(row + a.act_off + a.act_w + 8 * v);
+        const uint16_t* g = reinterpret_cast<const uint16_t*>(&gv);
+        const uint16_t* u = reinterpret_cast<const uint16_t*>(&uv);
+        uint16_t o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = tobf(bf(tobf(silu(bf(g[j])))) * bf(u[j]));
+        *reinterpret_cast<uint4*>(a.act + b * a.act_s + 8 * v) = *reinterpret_cast<const uint4*>(o);
+      }
+      return;
+    }
+    // wave 0: admission scores, silu(features) rounded to bf16, then fp32 dots
     for (int g = 0; g < a.G; ++g) {
       float acc = 0.f;
       for (int j = lane; j < a.A; j += kWave) acc = fmaf(bf(tobf(silu(bf(row[a.feat_off + j])))), a.adm_up[g * a.A + j], acc);
@@ -625,9 +642,15 @@ extern "C" int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t
                                   const float* cos, const float* sin, const float* read_scale, const float* gate_w,
                                   const float* gate_b, const float* adm_up, void* q, float* gate, float* scores,
                                   int64_t B, int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps,
+                                  int64_t act_offset, int64_t act_width, void* act, int64_t act_stride,
                                   yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(D == 128, "memory_prologue: head dim must be 128");
+  YH_CHECK_ARG(!act || (act_width > 0 && act_width % 8 == 0 && act_offset % 8 == 0 && proj_stride % 8 == 0 &&
+                        act_offset >= 0 && act_offset + 2 * act_width <= proj_stride && act_stride >= act_width &&
+                        act_stride % 8 == 0 && (reinterpret_cast<uintptr_t>(act) & 15) == 0 &&
+                        (reinterpret_cast<uintptr_t>(proj) & 15) == 0),
+               "memory_prologue: the writer activation needs 16-byte aligned rows with gate and up inside proj");
   YH_CHECK_ARG(B >= 0 && H > 0 && G > 0 && A > 0 && G <= 64, "memory_prologue: bad sizes");
   YH_CHECK_ARG(rotary_dim >= 0 && rotary_dim <= D && rotary_dim % 4 == 0, "memory_prologue: rotary dim");
   YH_CHECK_ARG(feat_offset >= H * D && feat_offset + A <= proj_stride && proj_stride % 2 == 0,
@@ -639,7 +662,8 @@ extern "C" int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t
   YH_CHECK_ARG((reinterpret_cast<uintptr_t>(proj) & 3) == 0, "memory_prologue: projection must be 4-byte aligned");
   MemProArgs a{static_cast<const uint16_t*>(proj), proj_stride, static_cast<const uint16_t*>(q_norm_w), cos, sin,
                read_scale, gate_w, gate_b, adm_up, static_cast<uint16_t*>(q), gate, scores, (int)H, (int)G, (int)A,
-               (int)rotary_dim, (int)feat_offset, eps};
+               (int)rotary_dim, (int)feat_offset, eps, static_cast<uint16_t*>(act), act_stride, (int)act_offset,
+               (int)act_width};
   const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>((H + 3) / 4 + 1));
   hipLaunchKernelGGL(memory_prologue_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
   YH_CHECK_LAUNCH("memory_prologue");

@@ -243,11 +243,14 @@ def ring_write(k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rot
 
 
 def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b, adm_up,
-                    rotary_dim, eps):
+                    rotary_dim, eps, act_offset=None, act_width=0):
     """Query, read gate and admission scores of the anchor memory for one
     decode token per row from the fused projection proj [B, P] (query heads
     first, admission features at ``feat_offset``): returns q [B, H, 128] bf16,
-    gate [B, H] float, scores [B, G] float (modeling_yanchor.py:167-176)."""
+    gate [B, H] float, scores [B, G] float (modeling_yanchor.py:167-176).
+    With ``act_offset`` (the writer's gate columns, its up columns right
+    after them, ``act_width`` each) the same launch also returns the writer's
+    activation silu(gate) * up [B, act_width] bf16 as a fourth result."""
     _bf16(proj, q_norm_w)
     b, ps = proj.shape
     if proj.stride(1) != 1:
@@ -260,11 +263,13 @@ def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, re
     q = torch.empty(b, heads, 128, dtype=proj.dtype, device=dev)
     gate = torch.empty(b, heads, dtype=torch.float32, device=dev)
     scores = torch.empty(b, g, dtype=torch.float32, device=dev)
+    act = None if act_offset is None else torch.empty(b, act_width, dtype=proj.dtype, device=dev)
     N.call("yh_memory_prologue", proj.data_ptr(), proj.stride(0), feat_offset, q_norm_w.data_ptr(), N.ptr(cs),
            N.ptr(sn), f32[0].data_ptr(), f32[1].data_ptr(), f32[2].data_ptr(), f32[3].data_ptr(), q.data_ptr(),
            gate.data_ptr(), scores.data_ptr(), b, heads, 128, g, n_features, rotary_dim, float(eps),
+           0 if act is None else int(act_offset), int(act_width), N.ptr(act), 0 if act is None else act.stride(0),
            N.stream_of(proj))
-    return q, gate, scores
+    return (q, gate, scores) if act is None else (q, gate, scores, act)
 
 
 def linear_silu(x, w):

@@ -180,6 +180,18 @@ class HipOps:
         return f(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b, adm_up,
                  rotary_dim, eps)
 
+    def memory_prologue_act(self, proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w,
+                            gate_b, adm_up, rotary_dim, eps, act_offset, act_width):
+        """memory_prologue plus the writer's silu(gate) * up in the same
+        launch (bf16; otherwise the two separate ops)."""
+        if proj.dtype != torch.bfloat16:
+            out = TorchGlue.memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale,
+                                            gate_w, gate_b, adm_up, rotary_dim, eps)
+            return out + (self.silu_mul(proj[:, act_offset: act_offset + 2 * act_width]),)
+        return self.layers.memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale,
+                                           gate_w, gate_b, adm_up, rotary_dim, eps, act_offset=act_offset,
+                                           act_width=act_width)
+
     def gdn_decode(self, q, k, v, g, beta, state):
         o, _ = self.gdn.recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=state,
                                                    output_final_state=True, use_qk_l2norm_in_kernel=True)
@@ -536,10 +548,14 @@ class Model:
             u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
         proj = ops.linear(u, L["m_in"], L.get("m_in@packed"))                                    # [q | admission features | gate | up]
         qd, ad = H * D, c.admission_rank
-        q, gate, scores = ops.memory_prologue(proj, H, qd, ad, L["m_q_norm"], cos, sin, L["read_scale"],
-                                              L["read_gate_w"], L["read_gate_b"], L["adm_up"], c.rotary_dim,
-                                              c.rms_eps)
-        zz = ops.linear(ops.silu_mul(proj[:, qd + ad:]), L["writer_down"], L.get("writer_down@packed"), residual=u)
+        args = (proj, H, qd, ad, L["m_q_norm"], cos, sin, L["read_scale"], L["read_gate_w"], L["read_gate_b"],
+                L["adm_up"], c.rotary_dim, c.rms_eps)
+        if hasattr(ops, "memory_prologue_act"):   # the writer's activation in the same launch
+            q, gate, scores, act = ops.memory_prologue_act(*args, qd + ad, c.writer_intermediate)
+        else:
+            q, gate, scores = ops.memory_prologue(*args)
+            act = ops.silu_mul(proj[:, qd + ad:])
+        zz = ops.linear(act, L["writer_down"], L.get("writer_down@packed"), residual=u)
         kv = ops.linear(zz, L["m_kv"], L.get("m_kv@packed"))
         key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
                                  c.rms_eps)
