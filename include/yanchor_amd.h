@@ -169,7 +169,7 @@ int yh_anchor_read(const void* query, const void* keys, const void* values, cons
  * over the live slots; no live slot gives 0).  positions [NB, G, window] int32
  * marks live slots (>= 0).  Replaces the physical-ring SWA decode attention
  * (fixed_memory_physical_ring_decode_attention, runtime/model/
- * inference_kernels.py:555-640) for D in {64, 128}, H / G in {1, 2, 4} and a
+ * inference_kernels.py:1881-1898) for D in {64, 128}, H / G in {1, 2, 4} and a
  * window that is a multiple of 16, at most 1024.  Key and value rows are
  * fetched only for blocks of 16 (or 32) slots that hold a live slot, so a ring
  * that fills from slot 0 costs in proportion to its live slots; the result is
@@ -649,6 +649,72 @@ int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t feat_offse
                        const float* gate_b, const float* adm_up, void* q, float* gate, float* scores, int64_t B,
                        int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps, int64_t act_offset,
                        int64_t act_width, void* act, int64_t act_stride, yh_stream_t stream);
+
+/*
+ * Refill prefill of a packed, ragged set of prompt pieces (cu_seqlens int32
+ * [n_seqs + 1], empty pieces allowed), each continuing its sequence's caches.
+ *
+ * yh_conv_prefill: the GDN layer's causal depthwise conv1d (4 taps) + SiLU
+ * over every packed token, the causal-conv1d prefill of the CUDA backend
+ * (bound at modeling_yanchor.py:392-407; torch form wheel transformers/models/
+ * qwen3_5/modeling_qwen3_5.py:455-470).
+ *   proj    [total_tokens, >= channels] (row stride proj_stride): the conv
+ *           inputs are its first `channels` columns
+ *   window  [n_seqs, 3, channels] time-major (oldest first): the inputs before
+ *           each piece (zeros for a fresh sequence); on return it holds the
+ *           last 3 inputs of [window | piece]
+ *   conv_w  [channels, 4]
+ *   out     [total_tokens, channels] = bf16(silu(sum_j x(t-3+j) w[c, j])),
+ *           fp32 taps in the order of the decode prologue (yh_gdn_decode_prep)
+ * dtype: bf16.
+ */
+int yh_conv_prefill(const void* proj, int64_t proj_stride, void* window, const void* conv_w,
+                    const int32_t* cu_seqlens, int64_t n_seqs, int64_t total_tokens, int64_t channels, void* out,
+                    int dtype, yh_stream_t stream);
+
+/*
+ * yh_swa_prefill: sliding-window causal attention of every packed query over
+ * the `window` keys that end at its own position (key position in
+ * [p - window + 1, p]), GQA (query head h reads KV head h / (H / G)), with the
+ * keys before each piece read from that sequence's physical ring.  Replaces
+ * flash_swa (flash_attn_varlen_func with causal=True, window_size=(W - 1, 0))
+ * and reference_swa with query_start (modeling_yanchor.py:412-449), as called
+ * by Qwen3_5FixedWindowAttention.forward (modeling_yanchor.py:849-870), and the
+ * output gate read * sigmoid(gate) (871-875).
+ *   q       [total, H, 128] (token stride q_stride elements), normed and rotated
+ *   k, v    [total, G, 128] piece keys (normed, rotated) and values
+ *   ring_k, ring_v  [ring_batch, G, window, 128]: slot = position % window
+ *   ring_rows int64 [n_seqs]: each piece's ring row, -1 = no context (a fresh
+ *           sequence); starts int64 [n_seqs]: position of each piece's first
+ *           token; the min(start, window - 1) keys before it come from the ring
+ *   tiles   int32 [n_tiles, 2]: (piece, first token) of every tile of
+ *           64 / (H / G) tokens that covers the pieces
+ *   gate    NULL or [total, H, 128] with the given strides: out = bf16(bf16(o)
+ *           * bf16(sigmoid(gate)))
+ *   out     [total, H, 128]
+ * Requirements: D == 128; H / G divides 64; dtype bf16 or fp16
+ * (YH_ERR_UNSUPPORTED otherwise); 16-byte aligned rows.
+ */
+int yh_swa_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride, const void* v, int64_t v_stride,
+                   const void* ring_k, const void* ring_v, const int64_t* ring_rows, const int64_t* starts,
+                   const int32_t* cu_seqlens, const int32_t* tiles, int64_t n_tiles, const void* gate,
+                   int64_t gate_token_stride, int64_t gate_head_stride, void* out, int64_t n_seqs,
+                   int64_t ring_batch, int64_t H, int64_t G, int64_t D, int64_t window, int dtype,
+                   yh_stream_t stream);
+
+/*
+ * yh_ring_fill: the last min(window, L) keys, values and positions of each
+ * packed piece into its ring row (slot = position % window), the ring a
+ * prefill leaves for the decode read (the chronological ring of
+ * runtime/model/inference_kernels.py:1799-1856 built in place; pieces with
+ * ring_rows[r] < 0 write nothing).  k, v [total, G, 128] with token strides;
+ * ring_k / ring_v [ring rows, G, window, 128]; ring_pos int32 [ring rows, G,
+ * window].
+ */
+int yh_ring_fill(const void* k, int64_t k_stride, const void* v, int64_t v_stride, const int64_t* ring_rows,
+                 const int64_t* starts, const int32_t* cu_seqlens, int64_t n_seqs, int64_t total_tokens,
+                 void* ring_k, void* ring_v, int32_t* ring_pos, int64_t G, int64_t D, int64_t window, int dtype,
+                 yh_stream_t stream);
 
 /*
  * HBM calibration stream (no counterpart in the reference: the measuring stick

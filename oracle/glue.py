@@ -38,7 +38,7 @@ exact function):
                             147-166): z = u + down(silu(gate u) * up u);
                             key = RoPE(k_norm(k_proj z)); value = v_proj z.
 * ``ring_decode_attention`` fixed_memory_physical_ring_decode_attention
-                            (runtime/model/inference_kernels.py:624-640):
+                            (runtime/model/inference_kernels.py:1881-1898):
                             softmax(q K^T / sqrt(D)) V over the live ring
                             slots, query heads grouped on the ring's KV heads,
                             then ``* sigmoid(gate)`` (Qwen3_5FixedWindowAttention
@@ -229,7 +229,7 @@ def write_kv(u, write_gate, write_up, write_down, k_proj, v_proj, k_norm_w, cos,
 
 def ring_decode_attention(query, ring_key, ring_value, valid, gate=None):
     """fixed_memory_physical_ring_decode_attention (inference_kernels.py:
-    624-640) and the output gate.
+    1881-1898) and the output gate.
 
     query [B, 1, H, D]; ring_key / ring_value [B, G, W, D] with H a multiple of
     G (query head h reads KV head h // (H / G)); valid [B, W] (or [B, G, W])
@@ -266,3 +266,59 @@ def ring_write(ring_key, ring_value, ring_valid, key, value, valid, index):
     ring_key[rows, :, idx] = key
     ring_value[rows, :, idx] = value
     ring_valid[rows, idx] = valid
+
+
+def causal_conv1d_prefill(x, window, weight):
+    """The GDN layer's causal conv1d + SiLU over a prompt piece that
+    continues ``window`` (the causal-conv1d prefill call of the CUDA backend,
+    modeling_yanchor.py:392-407, with the previous inputs as the initial
+    state), in the CUDA form: taps widened to fp32 (float64 for float64
+    inputs), sum and SiLU there, one rounding to x's dtype.
+
+    x [T, C] the piece's inputs; window [S, C] the S inputs before it, oldest
+    first (zeros for a fresh sequence); weight [C, S + 1].  Returns (y [T, C],
+    the new window: the last S rows of [window | x]).  Pinned against
+    ``causal_conv1d_update_cuda`` fed one token at a time, and, from a zero
+    window in float64, against F.conv1d over the causally padded sequence."""
+    t, s = x.shape[0], window.shape[0]
+    ct = _compute_dtype(x)
+    full = torch.cat([window.to(x.dtype), x], 0)                    # [S + T, C]
+    k = weight.shape[-1]
+    if t == 0:
+        return x.clone(), full[full.shape[0] - s:].clone()
+    fc, wc = full.to(ct).contiguous(), weight.to(ct).t().contiguous()    # wc[j]: tap j of every channel
+    y = fc[0:t] * wc[0]
+    for j in range(1, k):                                            # the K taps, oldest first
+        y = y + fc[j: j + t] * wc[j]
+    return F.silu(y).to(x.dtype), full[full.shape[0] - s:].clone()
+
+
+def swa_prefill_attention(query, key, value, window, *, query_start=0, key_valid=None):
+    """reference_swa (modeling_yanchor.py:412-427): query [B, L, H, D] at
+    positions query_start .. query_start + L - 1 over key / value [B, S, G, D]
+    at positions 0 .. S - 1, each query reading the keys in
+    [p - window + 1, p] (and ``key_valid`` [B, S] if given), query heads
+    grouped on the KV heads (enable_gqa), fp32 accumulation (float64 for
+    float64 inputs), output in the query dtype.  flash_swa (429-449, the CUDA
+    path's flash_attn call with causal=True and window_size=(window - 1, 0))
+    computes the same function.  Pinned against F.scaled_dot_product_attention
+    with is_causal (window >= S), the token-by-token ring read
+    (``ring_decode_attention`` after each ``ring_write``), and window = 1
+    (each query returns its own value)."""
+    b, l, h, d = query.shape
+    s, g = key.shape[1], key.shape[2]
+    ct = _compute_dtype(query)
+    qpos = torch.arange(l) + int(query_start)
+    kpos = torch.arange(s)
+    allowed = (kpos[None] <= qpos[:, None]) & (kpos[None] >= qpos[:, None] - int(window) + 1)   # [L, S]
+    allowed = allowed[None, None].expand(b, g, l, s)
+    if key_valid is not None:
+        allowed = allowed & key_valid[:, None, None, :].bool()
+    q = query.to(ct).reshape(b, l, g, h // g, d).permute(0, 2, 3, 1, 4)        # [B, G, R, L, D]
+    logits = torch.einsum("bgrld,bgsd->bgrls", q, key.to(ct).transpose(1, 2)) / math.sqrt(d)
+    logits = logits.masked_fill(~allowed[:, :, None], -math.inf)
+    m = logits.amax(-1, keepdim=True)
+    p = torch.exp(logits - torch.where(torch.isfinite(m), m, 0))
+    den = p.sum(-1, keepdim=True)
+    out = torch.einsum("bgrls,bgsd->bgrld", p, value.to(ct).transpose(1, 2)) / torch.where(den > 0, den, 1)
+    return out.permute(0, 3, 1, 2, 4).reshape(b, l, h, d).to(query.dtype)

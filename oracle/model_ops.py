@@ -15,7 +15,7 @@ arithmetic of the decode step taken from ``oracle/``:
                               ``commit_decode`` (modeling_yanchor.py:283-312)
                               and, for prefill, ``sequence`` (178-275);
 * the SWA ring read / write   ``oracle.glue.ring_decode_attention``
-                              (runtime/model/inference_kernels.py:624-640) and
+                              (runtime/model/inference_kernels.py:1881-1898) and
                               the chronological ring write (1828-1856);
 * the layer glue              ``oracle.glue``: Qwen3_5RMSNorm, the gated
                               norm, the conv update of the CUDA backend, the
@@ -147,11 +147,71 @@ class HostOps:
         return o.to(q.dtype)
 
     @staticmethod
-    def gdn_prefill(q, k, v, g, beta, cu_seqlens, lengths):
-        """Packed prefill from zero states: the chunked form (wheel:234-311)
-        per sequence of cu_seqlens; returns (o, final states)."""
-        o, st = gdn.varlen(gdn.chunk_gated_delta_rule, q, k, v, g, beta, cu_seqlens.tolist(), dtype=torch.float32)
+    def gdn_prefill(q, k, v, g, beta, cu_seqlens, lengths, initial_state=None):
+        """Packed prefill pieces from ``initial_state`` (None = zeros): the
+        chunked form (wheel:234-311) per sequence of cu_seqlens; returns (o,
+        final states)."""
+        o, st = gdn.varlen(gdn.chunk_gated_delta_rule, q, k, v, g, beta, cu_seqlens.tolist(),
+                           initial_state=initial_state, dtype=torch.float32)
         return o.to(q.dtype), st
+
+    @staticmethod
+    def conv_prefill(proj, window, conv_w, cu_seqlens, channels, lengths):
+        """``glue.causal_conv1d_prefill`` per packed piece, continuing each
+        row's conv window [R, 3, C] (updated in place)."""
+        outs, off = [], 0
+        for r, n in enumerate(lengths):
+            y, new = glue.causal_conv1d_prefill(proj[off: off + n, :channels], window[r], conv_w)
+            window[r].copy_(new)
+            outs.append(y)
+            off += n
+        return torch.cat(outs)
+
+    @staticmethod
+    def _ring_context(ring, row, start, window):
+        n = min(start, window - 1) if row >= 0 else 0
+        slots = torch.arange(start - n, start) % window
+        return ring[row][:, slots].transpose(0, 1)
+
+    def swa_prefill(self, q, k, v, cu_seqlens, starts, ring_k, ring_v, ring_rows, gate=None, lengths=None):
+        """``glue.swa_prefill_attention`` (reference_swa, modeling_yanchor.py:
+        412-427) per packed piece over [the ring's entries before the piece,
+        oldest first | the piece's keys], then * sigmoid(gate) with the
+        sigmoid rounded to the query dtype (as ring_decode_attention)."""
+        window = ring_k.shape[2]
+        st, rr, cu = starts.tolist(), ring_rows.tolist(), cu_seqlens.tolist()
+        out = torch.empty_like(q)
+        for r in range(len(cu) - 1):
+            s, e = cu[r], cu[r + 1]
+            if e == s:
+                continue
+            kc = torch.cat((self._ring_context(ring_k, rr[r], st[r], window), k[s:e]), 0)
+            vc = torch.cat((self._ring_context(ring_v, rr[r], st[r], window), v[s:e]), 0)
+            nctx = kc.shape[0] - (e - s)
+            for b0 in range(0, e - s, 1024):      # query blocks over the keys they can see
+                b1 = min(e - s, b0 + 1024)
+                lo = max(0, nctx + b0 - window + 1)
+                out[s + b0: s + b1] = glue.swa_prefill_attention(
+                    q[None, s + b0: s + b1], kc[None, lo: nctx + b1], vc[None, lo: nctx + b1], window,
+                    query_start=nctx + b0 - lo)[0]
+        if gate is not None:
+            out = out * torch.sigmoid(gate.float()).to(q.dtype)
+        return out
+
+    @staticmethod
+    def ring_fill(k, v, cu_seqlens, starts, ring_rows, ring_k, ring_v, ring_pos, lengths=None):
+        """The chronological ring write (inference_kernels.py:1828-1856) of a
+        piece's tokens in order; only the last min(window, L) survive."""
+        window = ring_k.shape[2]
+        st, rr, cu = starts.tolist(), ring_rows.tolist(), cu_seqlens.tolist()
+        for r in range(len(cu) - 1):
+            if rr[r] < 0:
+                continue
+            for t in range(cu[r], cu[r + 1]):
+                pos = st[r] + t - cu[r]
+                ring_k[rr[r], :, pos % window] = k[t].to(ring_k.dtype)
+                ring_v[rr[r], :, pos % window] = v[t].to(ring_v.dtype)
+                ring_pos[rr[r], :, pos % window] = pos
 
     @staticmethod
     def memory_sequence(q, key, value, scores, valid, chunk, state):

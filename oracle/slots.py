@@ -10,6 +10,10 @@ Restates runtime/model/inference_kernels.py:
 * ``compaction_keep``           nonzero(~finished & slot_rows >= 0) (1725)
 * ``should_compact``            _should_compact_dynamic_decode_tail (1348-1349)
 * ``cu_seqlens``                exclusive prefix sum of packed lengths
+* ``initial_attempt_order``     _initial_attempt_order (1321-1329)
+* ``group_aligned_prefix``      _group_aligned_prefix_length (1331-1346)
+* ``prefill_expansion``         build_prefill_expansion (90-121): representative
+                                row of each prefill group and every row's group
 
 Integer work, bit-exact; Python ints and torch integer tensors on the CPU.
 """
@@ -91,3 +95,44 @@ def cu_seqlens(lengths):
     for n in lengths:
         out.append(out[-1] + int(n))
     return out
+
+
+def initial_attempt_order(difficulty, attempt_ids, groups=None):
+    """Rows ordered hardest first (largest difficulty, then smallest attempt
+    id); with prefill groups, whole groups: by their hardest member, then
+    their smallest attempt id, rows inside a group by the same key.  Pinned
+    by hand-worked orders (tests/test_host_logic.py)."""
+    key = {r: (-float(difficulty[r]), int(attempt_ids[r])) for r in range(len(attempt_ids))}
+    if groups is None:
+        return sorted(key, key=key.get)
+    members = {}
+    for r, gid in enumerate(groups):
+        members.setdefault(int(gid), []).append(r)
+    ordered = sorted(members.values(), key=lambda rows: (min(key[r][0] for r in rows), min(key[r][1] for r in rows)))
+    return [r for rows in ordered for r in sorted(rows, key=key.get)]
+
+
+def group_aligned_prefix(ordered_rows, groups, limit):
+    """The longest prefix of at most ``limit`` rows that ends where a group
+    ends; ValueError when the first group alone exceeds ``limit``."""
+    if limit <= 0 or not ordered_rows:
+        return 0
+    ends = [i + 1 for i in range(len(ordered_rows))
+            if i + 1 == len(ordered_rows) or groups[ordered_rows[i + 1]] != groups[ordered_rows[i]]]
+    fit = [e for e in ends if e <= limit]
+    if not fit:
+        raise ValueError("the first prefill group is larger than the limit")
+    return fit[-1]
+
+
+def prefill_expansion(groups):
+    """(representative rows, inverse): the first row of each group in row
+    order, and for every row the index of its group's representative."""
+    first, inverse = {}, []
+    for r, gid in enumerate(groups):
+        first.setdefault(int(gid), len(first))
+        inverse.append(first[int(gid)])
+    reps = [0] * len(first)
+    for r, gid in reversed(list(enumerate(groups))):
+        reps[first[int(gid)]] = r
+    return reps, inverse

@@ -196,7 +196,7 @@ def test_ring_write_matches_oracle(gpu):
 @pytest.mark.parametrize("b,g,h,win,live", [(4, 2, 8, 128, 0.8), (128, 8, 32, 1024, 1.0), (3, 1, 4, 64, 0.1)])
 def test_window_attend_matches_oracle(gpu, b, g, h, win, live):
     """The SWA physical-ring decode read against the reference's masked
-    softmax (inference_kernels.py:624-640), with and without the output gate."""
+    softmax (inference_kernels.py:1881-1898), with and without the output gate."""
     d = 128
     gen = torch.Generator(device=gpu).manual_seed(80 + b)
     keys = torch.randn(b, g, win, d, device=gpu, generator=gen).to(torch.bfloat16)
@@ -226,7 +226,7 @@ def test_window_attend_dead_blocks(gpu, g, h):
     """Rings that fill from slot 0 (a sequence shorter than the window) and
     rings with whole 16-slot blocks dead between live ones: the read skips
     blocks without a live slot, and must equal the masked softmax over the
-    whole ring (inference_kernels.py:624-640).  Live counts sit on and beside
+    whole ring (inference_kernels.py:1881-1898).  Live counts sit on and beside
     block edges; dead slots hold large garbage so a skipped block that was
     still summed would show."""
     d, win = 128, 1024

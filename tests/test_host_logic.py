@@ -28,6 +28,25 @@ def test_initial_attempt_order_with_groups():
     # -> 12, 10, 11; inside 10: row 1 (8) then row 0 (1); inside 11: row 2 (3), row 4 (2)
     order = ik._initial_attempt_order([1, 8, 3, 8, 2], [4, 3, 2, 1, 0], [10, 10, 11, 12, 11])
     assert order == [3, 1, 0, 2, 4]
+    from oracle import slots
+    assert slots.initial_attempt_order([1, 8, 3, 8, 2], [4, 3, 2, 1, 0], [10, 10, 11, 12, 11]) == order
+    assert slots.initial_attempt_order([5, 9, 9, 1], [30, 20, 10, 40]) == [2, 1, 0, 3]
+
+
+def test_group_aligned_prefix_and_expansion():
+    """_group_aligned_prefix_length (inference_kernels.py:1331-1346) and
+    build_prefill_expansion (90-121): hand-worked cases, product and oracle."""
+    from oracle import slots
+    order, groups = [3, 1, 0, 2, 4], [10, 10, 11, 12, 11]     # groups along the order: 12 | 10 10 | 11 11
+    for f in (ik._group_aligned_prefix_length, slots.group_aligned_prefix):
+        assert [f(order, groups, k) for k in (1, 2, 3, 4, 5, 9)] == [1, 1, 3, 3, 5, 5]
+        assert f([], groups, 3) == 0 and f(order, groups, 0) == 0
+    import pytest
+    with pytest.raises(ValueError):
+        ik._group_aligned_prefix_length([1, 0, 3], groups, 1)    # group 10 holds two rows
+    with pytest.raises(ValueError):
+        slots.group_aligned_prefix([1, 0, 3], groups, 1)
+    assert slots.prefill_expansion([7, 3, 7, 9, 3]) == ([0, 1, 3], [0, 1, 0, 2, 1])
 
 
 def test_tail_compaction_trigger():

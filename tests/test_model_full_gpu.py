@@ -113,19 +113,35 @@ def test_full_model_decode_after_prefill(gpu, cfg, b, t, dtype, tol):
             assert same >= 0.9, (layer, same.item())
 
 
-@pytest.mark.parametrize("cfg,t", [(FULL, 40), (LONG, 63)], ids=["decode_256slots", "long_horizon_commit"])
+def _record_memory_reads(model):
+    """Wrap the model's memory read so every decode-step read's norm is
+    recorded (a live memory reads non-zero)."""
+    norms = []
+    read = model.ops.memory_read
+
+    def recorded(q, state, valid=None, head_gate=None):
+        out = read(q, state, valid=valid, head_gate=head_gate)
+        norms.append(out.float().norm().item())
+        return out
+
+    model.ops.memory_read = recorded
+    return norms
+
+
+@pytest.mark.parametrize("cfg,t", [(FULL, 100), (LONG, 127)], ids=["decode_256slots_live", "long_horizon_commit"])
 def test_full_model_decode_matches_host_oracle(gpu, cfg, t):
     """One decode step of the 36-layer 4B-shaped model on the GPU (bf16, the
     HIP kernels, the captured step's ops) against the same step on the host
     in float32 with every op from the oracle (oracle/model_ops.py), on the
     same weights and the same caches (those of a GPU prefill of t tokens).
-    Last-token logits and the 27 GDN states within the bf16 drift of 36
-    layers; ring positions and memory counters exact.  With the 16-slot
-    memory the step is the 64th token of a chunk, so it commits: the slots
-    selected on the GPU and on the host agree (near-tied admission scores
-    may swap one: the activations round differently)."""
-    from oracle.model_ops import HostOps
-
+    The prefill has committed memory blocks (64 of 256 slots at t = 100;
+    16 of 16 at t = 127), so every memory layer's decode read is live and
+    non-zero on both sides.  Last-token logits and the 27 GDN states within
+    the bf16 drift of 36 layers; ring positions and memory counters exact.
+    With the 16-slot memory the step is the 64th token of a chunk, so it
+    also commits: the slots selected on the GPU and on the host agree
+    (near-tied admission scores may swap one: the activations round
+    differently)."""
     b = 4
     m = rt.Model(cfg, batch=b, device=gpu, seed=21)
     prompts = _prompts(b, t + 1, cfg.vocab, 22).to(gpu)
@@ -133,16 +149,13 @@ def test_full_model_decode_matches_host_oracle(gpu, cfg, t):
     for dst, src in zip(m.cache_tensors(), caches):
         dst.copy_(src)
     del caches
+    for i in m.memory:
+        assert bool((m.memory[i].positions >= 0).any(-1).all()), i      # every row and group holds slots
     print("host model: building", flush=True)
-    host = rt.Model(cfg, batch=b, device="cpu", seed=0, ops=HostOps(), dtype=torch.float32, init="tiled")
-    for name in ("embed", "lm_head", "final_norm", "inv_freq"):
-        getattr(host, name).copy_(getattr(m, name).cpu())
-    for lh, lg in zip(host.layers, m.layers):
-        for k, v in lg.items():
-            if torch.is_tensor(v) and "@" not in k:
-                lh[k].copy_(v.cpu())
+    host = _host_twin(m, cfg, b)
     for dst, src in zip(host.cache_tensors(), m.cache_tensors()):
         dst.copy_(src.cpu())
+    gpu_reads, host_reads = _record_memory_reads(m), _record_memory_reads(host)
     pos = torch.full((b,), t, dtype=torch.long)
     valid = torch.ones(b, dtype=torch.bool)
     tok = prompts[:, t].cpu()
@@ -150,6 +163,10 @@ def test_full_model_decode_matches_host_oracle(gpu, cfg, t):
     torch.cuda.synchronize()
     print("host model: decode step", flush=True)
     want = host.decode_step(tok, pos, valid)
+    print("memory read norms (GPU / host): " + " ".join(f"{x:.3g}/{y:.3g}" for x, y in zip(gpu_reads, host_reads)),
+          flush=True)
+    assert len(gpu_reads) == len(host_reads) == len(m.memory)
+    assert min(gpu_reads) > 0 and min(host_reads) > 0
     err = rel_err(out, want)
     state_errs = {i: rel_err(m.gdn_state[i], host.gdn_state[i]) for i in m.gdn_state}
     print(f"B={b} T={t}: logits rel err {err:.3e} against the float32 host oracle; GDN state rel err by layer: "
@@ -169,6 +186,54 @@ def test_full_model_decode_matches_host_oracle(gpu, cfg, t):
             same = (mine[..., :, None] == theirs[..., None, :]).any(-1).float().mean().item()
             print(f"layer {i}: {same:.4f} of the committed positions agree with the host's", flush=True)
             assert same >= 0.9, (i, same)
+
+
+def test_full_model_decode_fp32_matches_host_oracle(gpu):
+    """The float32 twin of the check above: the 36-layer model with float32
+    activations on the GPU (the recurrence, ring and memory kernels in fp32,
+    the glue's torch forms) after a GPU prefill of 100 tokens (64 memory
+    slots committed), one decode step against the float32 host oracle: logits
+    and every GDN state within 1e-3, the live memory reads non-zero on both
+    sides, ring and memory positions and counters exact, the memory's live
+    keys and values within 1e-3."""
+    b, t, cfg = 2, 100, FULL
+    m = rt.Model(cfg, batch=b, device=gpu, seed=23, dtype=torch.float32)
+    prompts = _prompts(b, t + 1, cfg.vocab, 24).to(gpu)
+    _, caches = m.prefill(prompts[:, :t])
+    for dst, src in zip(m.cache_tensors(), caches):
+        dst.copy_(src)
+    del caches
+    print("host model: building", flush=True)
+    host = _host_twin(m, cfg, b)
+    for dst, src in zip(host.cache_tensors(), m.cache_tensors()):
+        dst.copy_(src.cpu())
+    gpu_reads, host_reads = _record_memory_reads(m), _record_memory_reads(host)
+    pos = torch.full((b,), t, dtype=torch.long)
+    valid = torch.ones(b, dtype=torch.bool)
+    tok = prompts[:, t].cpu()
+    out = m.decode_step(tok.to(gpu), pos.to(gpu), valid.to(gpu))
+    torch.cuda.synchronize()
+    print("host model: decode step", flush=True)
+    want = host.decode_step(tok, pos, valid)
+    err = rel_err(out, want)
+    state_errs = {i: rel_err(m.gdn_state[i], host.gdn_state[i]) for i in m.gdn_state}
+    print(f"fp32 B={b} T={t}: logits rel err {err:.3e}; worst GDN state rel err {max(state_errs.values()):.2e}; "
+          f"memory read norms {min(gpu_reads):.3g} .. {max(gpu_reads):.3g}", flush=True)
+    assert min(gpu_reads) > 0 and min(host_reads) > 0
+    assert err <= 1e-3, err
+    assert max(state_errs.values()) <= 1e-3, state_errs
+    for i in m.ring_pos:
+        assert torch.equal(m.ring_pos[i].cpu(), host.ring_pos[i]), i
+        mine, theirs = m.memory[i], host.memory[i]
+        for f in ("count", "total", "positions"):
+            assert torch.equal(getattr(mine, f).cpu(), getattr(theirs, f)), (i, f)
+        live = theirs.positions >= 0
+        for f in ("keys", "values"):
+            assert rel_err(getattr(mine, f).cpu()[live], getattr(theirs, f)[live]) <= 1e-3, (i, f)
+        pend = torch.arange(cfg.memory_chunk)[None, None, :] < theirs.count[:, None, None]
+        pend = pend.expand(theirs.pending_keys.shape[:3])
+        for f in ("pending_keys", "pending_values"):
+            assert rel_err(getattr(mine, f).cpu()[pend], getattr(theirs, f)[pend]) <= 1e-3, (i, f)
 
 
 def _host_twin(m, cfg, b):

@@ -85,3 +85,24 @@ def test_hbm_stream_rejects_bad_arguments(lib):
     assert b"null" in lib.yh_last_error()
     assert lib.yh_hbm_stream(2, 0, fake, fake, 16, 8, None) == -1
     assert b"grid floats" in lib.yh_last_error()
+
+
+def test_sampler_refuses_top_k_past_the_vocabulary(lib):
+    """top_k > V is refused in every branch, the full-vocabulary one (top_k
+    > 64) included, as the reference's top_k_top_p_distribution refuses it
+    (runtime/model/inference_kernels.py:46-47); the wrapper refuses it
+    before the C ABI is reached."""
+    import torch
+    from yanchor_amd import inference_kernels as ik
+    fake = ctypes.c_void_p(256)
+    args = lambda k, v: (fake, _native.F32, v, None, 0, 0.0, fake, None, 0, 1, 0, 1.0, k, 1.0,  # noqa: E731
+                         ik.SAMPLE_TORCH, fake, None, None, fake, 1 << 20, 1, v, None)
+    assert lib.yh_topk_sample(*args(100, 80)) == -1
+    assert b"exceeds the vocabulary" in lib.yh_last_error()
+    assert lib.yh_topk_sample(*args(30, 20)) == -1
+    assert b"exceeds the vocabulary" in lib.yh_last_error()
+    scores = torch.zeros(2, 80)
+    ids = torch.zeros(2, dtype=torch.int64)
+    for k in (100, 81):
+        with pytest.raises(ValueError, match="exceeds the vocabulary"):
+            ik.topk_sample(scores, ids, 0, seed=1, temperature=1.0, top_k=k, top_p=1.0, mode=ik.SAMPLE_TORCH)

@@ -249,3 +249,89 @@ def test_rope_cos_sin_tables(dtype):
     assert torch.equal(cos[0], torch.ones(32, dtype=dtype)) and torch.equal(sin[0], torch.zeros(32, dtype=dtype))
     ang = pos[:, None].float() * inv
     assert torch.allclose(cos[:, :16].float(), ang.cos(), atol=1e-2 if dtype == torch.bfloat16 else 1e-6)
+
+
+def _conv_inputs(t, c, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(t, c, generator=g, dtype=torch.float64).to(dtype)
+    win = torch.randn(3, c, generator=g, dtype=torch.float64).to(dtype)
+    w = (torch.randn(c, 4, generator=g, dtype=torch.float64) * 0.5).to(dtype)
+    return x, win, w
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("t", [0, 1, 2, 3, 7, 40])
+def test_conv_prefill_equals_token_by_token_cuda_update(dtype, t):
+    """A piece of t tokens continuing a window reads and leaves what t decode
+    updates of the CUDA form (fed one token at a time) read and leave, in
+    float64 and in bf16 (both round once per output; within one bf16 ulp)."""
+    x, win, w = _conv_inputs(t, 24, dtype, 5 + t)
+    y, new_win = glue.causal_conv1d_prefill(x, win, w)
+    state = win.t().contiguous()[None].clone()                  # [1, C, 3] oldest first
+    outs = [glue.causal_conv1d_update_cuda(x[i][None, :, None], state, w)[0, :, 0] for i in range(t)]
+    want = torch.stack(outs) if outs else y
+    # the two sum the same four fp32 (float64) products in different orders
+    tol = 1e-12 if dtype == torch.float64 else 2.0 ** -7
+    assert torch.allclose(y.double(), want.double(), rtol=tol, atol=tol)
+    assert torch.equal(new_win, state[0].t())
+
+
+def test_conv_prefill_from_a_zero_window_is_the_causal_conv():
+    """From a zero window in float64: F.conv1d over the causally padded
+    sequence, then SiLU; reversed taps (a planted mistake) differ."""
+    x, _, w = _conv_inputs(33, 16, torch.float64, 9)
+    zero = torch.zeros(3, 16, dtype=torch.float64)
+    y, _ = glue.causal_conv1d_prefill(x, zero, w)
+    ref = F.silu(F.conv1d(F.pad(x.t()[None], (3, 0)), w[:, None, :], groups=16))[0].t()
+    assert torch.allclose(y, ref, rtol=0, atol=1e-12)
+    planted, _ = glue.causal_conv1d_prefill(x, zero, w.flip(-1))
+    assert not torch.allclose(planted, ref, atol=1e-3)
+
+
+def _swa_inputs(b, l, h, g, d, seed, dtype=torch.float64):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, l, h, d, generator=gen, dtype=torch.float64).to(dtype)
+    k = torch.randn(b, l, g, d, generator=gen, dtype=torch.float64).to(dtype)
+    v = torch.randn(b, l, g, d, generator=gen, dtype=torch.float64).to(dtype)
+    return q, k, v
+
+
+def test_swa_prefill_inside_the_window_is_causal_sdpa():
+    """Window >= length: plain causal attention, F.scaled_dot_product_attention
+    with is_causal and enable_gqa (the library routine)."""
+    q, k, v = _swa_inputs(2, 37, 8, 2, 16, 1)
+    out = glue.swa_prefill_attention(q, k, v, 64)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
+                                         enable_gqa=True).transpose(1, 2)
+    assert torch.allclose(out, ref, atol=1e-12)
+
+
+def test_swa_prefill_equals_token_by_token_ring_reads():
+    """Past the window: every query's output is the decode read of a ring of
+    `window` slots after the chronological write of the tokens up to it (the
+    decode path's physical ring), so prefill and decode attend alike."""
+    b, l, h, g, d, w = 2, 45, 4, 2, 16, 8
+    q, k, v = _swa_inputs(b, l, h, g, d, 2)
+    out = glue.swa_prefill_attention(q, k, v, w)
+    ring_k = torch.zeros(b, g, w, d, dtype=torch.float64)
+    ring_v = torch.zeros_like(ring_k)
+    valid = torch.zeros(b, w, dtype=torch.bool)
+    for t in range(l):
+        glue.ring_write(ring_k, ring_v, valid, k[:, t], v[:, t], torch.ones(b, dtype=torch.bool), t % w)
+        read = glue.ring_decode_attention(q[:, t:t + 1], ring_k, ring_v, valid)
+        assert torch.allclose(out[:, t:t + 1], read, atol=1e-12), t
+    # a window one slot too wide (a planted mistake) differs past the window
+    wide = glue.swa_prefill_attention(q, k, v, w + 1)
+    assert not torch.allclose(wide[:, w:], out[:, w:], atol=1e-6)
+
+
+def test_swa_prefill_window_one_and_continuation():
+    """window = 1: each query returns its own (GQA-shared) value.  A piece
+    starting at query_start over all keys equals the tail of the whole
+    prefill (the continuation form the chunked prefill uses)."""
+    q, k, v = _swa_inputs(1, 20, 4, 2, 8, 3)
+    one = glue.swa_prefill_attention(q, k, v, 1)
+    assert torch.allclose(one, v.repeat_interleave(2, dim=2), atol=1e-12)
+    full = glue.swa_prefill_attention(q, k, v, 6)
+    tail = glue.swa_prefill_attention(q[:, 13:], k, v, 6, query_start=13)
+    assert torch.allclose(tail, full[:, 13:], atol=1e-12)

@@ -1,0 +1,152 @@
+"""The refill prefill through the generation API (GPU): ragged prompts of any
+length admitted together, and prefill groups.
+
+* bf16, the 4B-shaped model, 8 slots, prompts of 5, 700, 1500 and 4096
+  tokens plus a 4-row prefill group of one 300-token prompt, all in one
+  ``Engine.generate``: the admission is one packed prefill (a spy on the C ABI
+  sees exactly one chunk-kernel launch, one conv and one window-attention
+  launch per layer), the group is prefilled once and expanded to its four
+  slots, and the slot order is the reference's _initial_attempt_order with
+  groups (the oracle's restatement);
+* float32, the same widths with 4 layers (3 GDN + 1 SWA / memory), the same
+  rows: every row's argmax tokens equal those of a host-oracle prefill of its
+  prompt alone followed by host-oracle decode steps (oracle/model_ops.py);
+* a prompt taken in pieces (``token_chunk``) gives the logits and caches of
+  the whole prompt at once (bf16, GPU).
+"""
+from collections import Counter
+
+import pytest
+import torch
+
+from yanchor_amd import _native, inference
+from yanchor_amd import runtime as rt
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+FULL = rt.ModelConfig()
+NARROW_DEPTH = rt.ModelConfig(layers=4, vocab=32768)
+LENGTHS = (5, 700, 1500, 4096)
+GROUP_LEN = 300
+CAPS = (6, 4, 8, 5, 7, 7, 7, 7)
+
+
+def _rows(vocab, seed):
+    g = torch.Generator().manual_seed(seed)
+    prompts = [torch.randint(0, vocab, (n,), generator=g).tolist() for n in LENGTHS]
+    shared = torch.randint(0, vocab, (GROUP_LEN,), generator=g).tolist()
+    rows = [dict(input_ids=p, max_tokens=c) for p, c in zip(prompts, CAPS)]
+    rows += [dict(input_ids=list(shared), max_tokens=c, prefill_group_id=1000) for c in CAPS[4:]]
+    return rows
+
+
+@pytest.fixture
+def spy(monkeypatch):
+    calls = Counter()
+    call = _native.call
+
+    def counted(name, *args):
+        calls[name] += 1
+        return call(name, *args)
+
+    monkeypatch.setattr(_native, "call", counted)
+    return calls
+
+
+def test_generate_packs_a_ragged_refill_and_expands_groups(gpu, spy):
+    from oracle import slots
+
+    m = rt.Model(FULL, batch=8, device=gpu, seed=41)
+    eng = inference.Engine(m, batch=8)
+    rows = _rows(FULL.vocab, 42)
+    out, met = eng.generate(rows, cap=8, temperature=0.0, fixed=True, stop_interval=4)
+    n_gdn = sum(1 for i in range(FULL.layers) if not FULL.is_memory_layer(i))
+    print(f"launches: chunk {spy['yh_gdn_chunk_varlen']}, conv {spy['yh_conv_prefill']}, "
+          f"window {spy['yh_swa_prefill']}; prefill calls {met['prefill_calls']}", flush=True)
+    assert spy["yh_gdn_chunk_varlen"] == n_gdn
+    assert spy["yh_conv_prefill"] == n_gdn
+    assert spy["yh_swa_prefill"] == spy["yh_ring_fill"] == FULL.layers - n_gdn
+    assert met["prefill_calls"] == 1
+    assert met["prefill_unique_rows"] == 5 and met["prefill_expanded_rows"] == 8
+    ids = list(range(len(rows)))
+    groups = [r.get("prefill_group_id", i) for i, r in enumerate(rows)]
+    assert met["initial_attempt_order"] == slots.initial_attempt_order(list(CAPS), ids, groups)
+    for r, want in zip(out, CAPS):
+        assert r["generated_tokens"] == want and r["prompt_tokens"] == len(rows[r["attempt_id"]]["input_ids"])
+    group = [r["response_ids"] for r in out[4:]]
+    for toks in group:   # one prompt, argmax: each member continues the same caches
+        assert toks == group[0][: len(toks)]
+
+
+def _host_greedy(host, prompt, steps):
+    """Host-oracle prefill of ``prompt`` alone, then argmax decode steps."""
+    logits, caches = host.prefill([torch.tensor(prompt)])
+    host.B = 1
+    host._alloc_caches()
+    for dst, src in zip(host.cache_tensors(), caches):
+        dst.copy_(src)
+    toks = [int(logits[0].argmax())]
+    for i in range(steps - 1):
+        out = host.decode_step(torch.tensor([toks[-1]]), torch.tensor([len(prompt) + i]), torch.tensor([True]))
+        toks.append(int(out[0].argmax()))
+    return toks
+
+
+def test_generate_fp32_tokens_match_host_oracle(gpu, spy):
+    from oracle.model_ops import HostOps
+
+    cfg = NARROW_DEPTH
+    m = rt.Model(cfg, batch=8, device=gpu, seed=43, dtype=torch.float32)
+    eng = inference.Engine(m, batch=8)
+    rows = _rows(cfg.vocab, 44)
+    out, met = eng.generate(rows, cap=8, temperature=0.0, fixed=True, stop_interval=4)
+    n_gdn = sum(1 for i in range(cfg.layers) if not cfg.is_memory_layer(i))
+    assert spy["yh_gdn_recurrent_varlen"] == n_gdn and met["prefill_calls"] == 1
+    print("host model: building", flush=True)
+    host = rt.Model(cfg, batch=1, device="cpu", seed=0, ops=HostOps(), dtype=torch.float32, init="tiled")
+    for name in ("embed", "lm_head", "final_norm", "inv_freq"):
+        getattr(host, name).copy_(getattr(m, name).cpu())
+    for lh, lg in zip(host.layers, m.layers):
+        for k, v in lg.items():
+            if torch.is_tensor(v) and "@" not in k:
+                lh[k].copy_(v.cpu())
+    done = {}
+    for r in out:
+        prompt = rows[r["attempt_id"]]["input_ids"]
+        key = tuple(prompt)
+        if key not in done:
+            print(f"host model: {len(prompt)}-token prompt", flush=True)
+            done[key] = _host_greedy(host, prompt, max(CAPS))
+        assert r["response_ids"] == done[key][: r["generated_tokens"]], r["attempt_id"]
+
+
+def test_pieced_prefill_equals_whole_prefill_on_gpu(gpu):
+    """bf16 4B-shaped model: a 3000-token prompt and a 700-token one in
+    pieces of 1024 tokens (the window) and of 640 leave the logits and caches
+    of one pass: GDN states, conv windows and rings within the rounding of
+    different chunk boundaries, ring positions and memory counters exact, the
+    committed memory positions agreeing (near-tied admission scores may swap
+    a slot)."""
+    m = rt.Model(FULL, batch=2, device=gpu, seed=45)
+    g = torch.Generator().manual_seed(46)
+    prompts = [torch.randint(0, FULL.vocab, (n,), generator=g) for n in (3000, 700)]
+    logits, caches = m.prefill(prompts)
+    n_gdn = sum(1 for i in range(FULL.layers) if not FULL.is_memory_layer(i))
+    for piece in (1024, 640):
+        lp, cp = m.prefill(prompts, token_chunk=piece)
+        err = rel_err(lp, logits)
+        print(f"pieces of {piece}: logits rel err {err:.2e}", flush=True)
+        assert err <= 2e-2, (piece, err)
+        for j in range(2 * n_gdn):                        # GDN states and conv windows
+            assert rel_err(cp[j], caches[j]) <= 2e-2, (piece, j)
+        k = 2 * n_gdn
+        while k < len(caches):                            # ring k, v, positions; then the 9 memory fields
+            assert rel_err(cp[k], caches[k]) <= 2e-2 and rel_err(cp[k + 1], caches[k + 1]) <= 2e-2, (piece, k)
+            assert torch.equal(cp[k + 2], caches[k + 2]), (piece, k)
+            pos_a, pos_b = cp[k + 6], caches[k + 6]
+            same = (pos_a[..., :, None] == pos_b[..., None, :]).any(-1).float().mean().item()
+            assert same >= 0.9, (piece, k, same)
+            assert torch.equal(cp[k + 10], caches[k + 10]) and torch.equal(cp[k + 11], caches[k + 11]), (piece, k)
+            k += 12

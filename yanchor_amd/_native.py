@@ -30,6 +30,10 @@ SIGNATURES: dict[str, list] = {
                                 _i32, _i32, _i32, _i32, _p],
     "yh_gdn_chunk_varlen": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                             _i32, _i32, _i32, _i32, _p, _i64, _p],
+    "yh_conv_prefill": [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _p, _i32, _p],
+    "yh_swa_prefill": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64,
+                       _i64, _i64, _i64, _i64, _i32, _p],
+    "yh_ring_fill": [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "yh_anchor_read": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_window_attend": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "yh_anchor_commit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,

@@ -700,6 +700,7 @@ int topk_sample_launch(const void* scores, int dtype, int64_t row_stride, const 
     // the full-vocabulary branches of the torch sampler: no workspace
     YH_CHECK_ARG(scores && tokens && attempt_ids, "topk_sample: null pointer");
     YH_CHECK_ARG(mode == YH_SAMPLE_TORCH, "topk_sample: top_k outside [1, %d] needs the torch-sampler mode", kMaxK);
+    YH_CHECK_ARG(top_k <= V, "topk_sample: top_k exceeds the vocabulary");
     YH_CHECK_ARG(temperature > 0.f && top_p > 0.f && top_p <= 1.f,
                  "topk_sample: needs temperature > 0 and 0 < top_p <= 1");
     YH_CHECK_ARG(out_values == nullptr && out_indices == nullptr,

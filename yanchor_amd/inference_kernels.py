@@ -77,7 +77,7 @@ def topk_sample(scores, attempt_ids, steps, *, seed, temperature, top_k, top_p, 
     full = top_k <= 0 or top_k > 64
     if full and (mode != SAMPLE_TORCH or return_topk):
         raise ValueError("top_k outside [1, 64] is the torch sampler's full-vocabulary branch (no top-k output)")
-    if 1 <= top_k <= 64 and top_k > v:
+    if top_k > v:   # every branch, as the reference refuses it (inference_kernels.py:46-47)
         raise ValueError("top-k exceeds the vocabulary")
     if top_k != 1 and (temperature <= 0.0 or not 0.0 < top_p <= 1.0):
         raise ValueError("invalid top-k/top-p sampling parameters")
@@ -191,6 +191,27 @@ def _initial_attempt_order(difficulty, attempt_ids, prefill_group_ids=None):
         members.setdefault(int(gid), []).append(r)
     groups = sorted(members.values(), key=lambda rows: (-max(diff[r] for r in rows), min(ids[r] for r in rows)))
     return [r for rows in groups for r in sorted(rows, key=row_key)]
+
+
+def _group_aligned_prefix_length(ordered_rows, prefill_group_ids, limit):
+    """The longest prefix of ``ordered_rows`` with at most ``limit`` rows
+    that ends on a prefill-group boundary (inference_kernels.py:1331-1346);
+    a first group larger than ``limit`` is refused."""
+    if limit <= 0 or not ordered_rows:
+        return 0
+    accepted = 0
+    while accepted < len(ordered_rows):
+        gid = int(prefill_group_ids[ordered_rows[accepted]])
+        stop = accepted + 1
+        while stop < len(ordered_rows) and int(prefill_group_ids[ordered_rows[stop]]) == gid:
+            stop += 1
+        if stop > limit:
+            break
+        accepted = stop
+    if accepted == 0:
+        raise ValueError(f"prefill group {int(prefill_group_ids[ordered_rows[0]])} is larger than the "
+                         "ready-bank limit")
+    return accepted
 
 
 def _should_compact_dynamic_decode_tail(live_slots, physical_slots, *, queue_exhausted, live_fraction):

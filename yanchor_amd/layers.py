@@ -393,3 +393,147 @@ def linear(x, w, split_k=None, residual=None, defer=False):
     N.call("yh_linear", x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), n, m, n, k, s, N.ptr(ws),
            0 if ws is None else ws.numel(), N.stream_of(x))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Refill prefill of packed, ragged prompt pieces (cu_seqlens), each continuing
+# its sequence's caches.
+
+def _cu(cu_seqlens, device, total):
+    """cu_seqlens (host or device) as int32 on the device, checked on the
+    host (a prefill is not captured, so the copy is cheap): non-decreasing,
+    from >= 0 to <= total, so no kernel reads past the packed tokens.  The
+    small per-piece vectors (offsets, starts, ring rows) may come from the
+    host; the activations and caches must be device tensors."""
+    cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
+    if cu.ndim != 1 or cu.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D offset vector")
+    h = cu.cpu()
+    if int(h[0]) != 0 or int(h[-1]) > total or bool((h[1:] < h[:-1]).any()):
+        raise ValueError("cu_seqlens must be non-decreasing offsets from 0 within the packed tokens")
+    return cu
+
+
+def _pieces(starts, ring_rows, r, ring_batch, device):
+    st = starts.to(device=device, dtype=torch.int64).contiguous()
+    rr = ring_rows.to(device=device, dtype=torch.int64).contiguous()
+    if st.shape != (r,) or rr.shape != (r,):
+        raise ValueError("starts / ring_rows must hold one entry per piece")
+    if r and (int(st.min()) < 0 or int(rr.max()) >= ring_batch):
+        raise ValueError("starts must be >= 0 and ring rows inside the ring")
+    return st, rr
+
+
+def conv_prefill(proj, window, conv_w, cu_seqlens, channels):
+    """The GDN layer's causal conv1d + SiLU over packed prompt pieces
+    (the causal-conv1d prefill of the CUDA backend, modeling_yanchor.py:
+    392-407): proj [N, >= channels] bf16 (the conv inputs are its first
+    ``channels`` columns, any row stride), window [R, 3, channels] bf16, the
+    inputs before each piece (zeros for a fresh sequence), updated IN PLACE
+    to the last three inputs; conv_w [channels, 4].  Returns [N, channels]."""
+    _bf16(proj, window, conv_w)
+    n = proj.shape[0]
+    dev = N.require_device(proj, window, conv_w)
+    cu = _cu(cu_seqlens, dev, n)
+    r = cu.numel() - 1
+    if proj.ndim != 2 or proj.stride(1) != 1 or proj.shape[1] < channels:
+        raise ValueError("proj must be [N, >= channels] with unit column stride")
+    if window.shape != (r, 3, channels) or not window.is_contiguous():
+        raise ValueError("window must be contiguous [R, 3, channels]")
+    if conv_w.shape != (channels, 4) or not conv_w.is_contiguous():
+        raise ValueError("conv_w must be contiguous [channels, 4]")
+    if int(cu[-1]) != n:
+        raise ValueError("cu_seqlens must cover every packed token")
+    out = torch.empty(n, channels, dtype=proj.dtype, device=dev)
+    N.call("yh_conv_prefill", proj.data_ptr(), proj.stride(0), window.data_ptr(), conv_w.data_ptr(), cu.data_ptr(),
+           r, n, channels, out.data_ptr(), N.BF16, N.stream_of(proj))
+    return out
+
+
+def prefill_tiles(lengths, tokens_per_tile, device):
+    """(piece, first token) int32 [n_tiles, 2] of the tiles of
+    ``tokens_per_tile`` tokens that cover pieces of the given host lengths."""
+    tiles = [(r, t) for r, n in enumerate(lengths) for t in range(0, int(n), tokens_per_tile)]
+    return torch.tensor(tiles, dtype=torch.int32).reshape(-1, 2).to(device)
+
+
+def _rows(x, name):
+    """x [N, heads, 128] with unit head-dim stride, heads contiguous and
+    16-byte aligned rows (a column view of a projection qualifies)."""
+    if x.ndim != 3 or x.stride(2) != 1 or x.stride(1) != x.shape[2] or x.stride(0) % 8 or x.data_ptr() % 16:
+        return x.contiguous()
+    return x
+
+
+def swa_prefill(q, k, v, cu_seqlens, starts, ring_k, ring_v, ring_rows, *, gate=None, lengths=None, tiles=None):
+    """Sliding-window causal attention of packed prompt pieces (flash_swa /
+    reference_swa, modeling_yanchor.py:412-449, with the output gate of
+    871-875): query t of piece r at position starts[r] + t reads the
+    ``window`` keys ending at its position, those before the piece from the
+    ring row ``ring_rows[r]`` (slot = position % window).  q [N, H, 128]
+    normed and rotated; k [N, G, 128] normed and rotated; v [N, G, 128];
+    ring_k / ring_v [RB, G, window, 128]; starts / ring_rows int64 [R];
+    gate None or [N, H, 128] (any token / head strides): the result is then
+    read * sigmoid(gate).  Returns [N, H, 128]."""
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("swa_prefill takes bf16 / fp16 q, k, v")
+    n, h, d = q.shape
+    g = k.shape[1]
+    if k.shape != (n, g, d) or v.shape != k.shape or h % g:
+        raise ValueError("k / v must be [N, G, D] with G dividing the query heads")
+    if ring_k.ndim != 4 or ring_k.shape[1] != g or ring_k.shape[3] != d or ring_v.shape != ring_k.shape:
+        raise ValueError("ring_k / ring_v must be [RB, G, window, D]")
+    if not ring_k.is_contiguous() or not ring_v.is_contiguous() or ring_k.dtype != q.dtype:
+        raise ValueError("ring tensors must be contiguous in the query dtype")
+    dev = N.require_device(q, k, v, ring_k, ring_v, gate)
+    cu = _cu(cu_seqlens, dev, n)
+    r = cu.numel() - 1
+    st, rr = _pieces(starts, ring_rows, r, ring_k.shape[0], dev)
+    if 64 % (h // g):
+        raise ValueError("query heads per KV head must divide 64")
+    lengths = (cu[1:] - cu[:-1]).tolist()
+    if tiles is None:
+        tiles = prefill_tiles(lengths, 64 // (h // g), dev)
+    else:
+        th = tiles.cpu()
+        if tiles.dtype != torch.int32 or tiles.ndim != 2 or tiles.shape[1] != 2 or \
+                any(not (0 <= int(p) < r and 0 <= int(t) < lengths[int(p)]) for p, t in th.tolist()):
+            raise ValueError("tiles must be int32 (piece, first token) pairs inside the pieces")
+        tiles = tiles.to(dev).contiguous()
+    q, k, v = _rows(q, "q"), _rows(k, "k"), _rows(v, "v")
+    gp, gts, ghs = None, 0, 0
+    if gate is not None:
+        if gate.shape != (n, h, d) or gate.stride(2) != 1 or gate.dtype != q.dtype:
+            raise ValueError("gate must be [N, H, D] in the query dtype with unit last stride")
+        gp, gts, ghs = gate.data_ptr(), gate.stride(0), gate.stride(1)
+    out = torch.empty(n, h, d, dtype=q.dtype, device=dev)
+    N.call("yh_swa_prefill", q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
+           ring_k.data_ptr(), ring_v.data_ptr(), rr.data_ptr(), st.data_ptr(), cu.data_ptr(), tiles.data_ptr(),
+           tiles.shape[0], gp, gts, ghs, out.data_ptr(), r, ring_k.shape[0], h, g, d, ring_k.shape[2], N.code(q),
+           N.stream_of(q))
+    return out
+
+
+def ring_fill(k, v, cu_seqlens, starts, ring_rows, ring_k, ring_v, ring_pos):
+    """The last min(window, L) keys, values and positions of each packed
+    piece into ring row ``ring_rows[r]`` at slot position % window (the ring
+    a prefill leaves for the decode read).  k [N, G, 128] normed and rotated,
+    v [N, G, 128]; ring_k / ring_v [RB, G, window, 128]; ring_pos int32
+    [RB, G, window]."""
+    if k.dtype not in (torch.bfloat16, torch.float16) or v.dtype != k.dtype or ring_k.dtype != k.dtype:
+        raise ValueError("ring_fill takes bf16 / fp16 keys and values in the ring dtype")
+    n, g, d = k.shape
+    if v.shape != k.shape or ring_k.ndim != 4 or ring_k.shape[1] != g or ring_k.shape[3] != d or \
+            ring_v.shape != ring_k.shape or ring_pos.shape != ring_k.shape[:3] or ring_pos.dtype != torch.int32:
+        raise ValueError("ring_fill needs k / v [N, G, D], rings [RB, G, W, D] and int32 positions [RB, G, W]")
+    for t in (ring_k, ring_v, ring_pos):
+        if not t.is_contiguous():
+            raise ValueError("ring tensors must be contiguous")
+    dev = N.require_device(k, v, ring_k, ring_v, ring_pos)
+    cu = _cu(cu_seqlens, dev, n)
+    r = cu.numel() - 1
+    st, rr = _pieces(starts, ring_rows, r, ring_k.shape[0], dev)
+    k, v = _rows(k, "k"), _rows(v, "v")
+    N.call("yh_ring_fill", k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), rr.data_ptr(), st.data_ptr(),
+           cu.data_ptr(), r, n, ring_k.data_ptr(), ring_v.data_ptr(), ring_pos.data_ptr(), g, d, ring_k.shape[2],
+           N.code(k), N.stream_of(k))

@@ -197,10 +197,29 @@ class HipOps:
                                                    output_final_state=True, use_qk_l2norm_in_kernel=True)
         return o
 
-    def gdn_prefill(self, q, k, v, g, beta, cu_seqlens, lengths):
-        return self.gdn.chunk_gated_delta_rule(q, k, v, g=g, beta=beta, output_final_state=True,
-                                               use_qk_l2norm_in_kernel=True, cu_seqlens=cu_seqlens,
-                                               lengths=lengths)
+    def gdn_prefill(self, q, k, v, g, beta, cu_seqlens, lengths, initial_state=None):
+        """Packed pieces [1, N, ...] of cu_seqlens from ``initial_state``
+        ([R, HV, K, V], None = zeros): one chunk-kernel launch (bf16) or the
+        token-recurrent kernel (other dtypes); returns (o, final states)."""
+        return self.gdn.chunk_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=initial_state,
+                                               output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                               cu_seqlens=cu_seqlens, lengths=lengths)
+
+    def conv_prefill(self, proj, window, conv_w, cu_seqlens, channels, lengths):
+        if proj.dtype != torch.bfloat16:
+            return TorchGlue.conv_prefill(proj, window, conv_w, cu_seqlens, channels, lengths)
+        return self.layers.conv_prefill(proj, window, conv_w, cu_seqlens, channels)
+
+    def swa_prefill(self, q, k, v, cu_seqlens, starts, ring_k, ring_v, ring_rows, gate=None, lengths=None):
+        if q.dtype not in (torch.bfloat16, torch.float16):
+            return TorchGlue.swa_prefill(q, k, v, cu_seqlens, starts, ring_k, ring_v, ring_rows, gate, lengths)
+        return self.layers.swa_prefill(q, k, v, cu_seqlens, starts, ring_k, ring_v, ring_rows, gate=gate,
+                                       lengths=lengths)
+
+    def ring_fill(self, k, v, cu_seqlens, starts, ring_rows, ring_k, ring_v, ring_pos, lengths=None):
+        if k.dtype not in (torch.bfloat16, torch.float16):
+            return TorchGlue.ring_fill(k, v, cu_seqlens, starts, ring_rows, ring_k, ring_v, ring_pos, lengths)
+        self.layers.ring_fill(k, v, cu_seqlens, starts, ring_rows, ring_k, ring_v, ring_pos)
 
     def window_attend(self, q, keys, values, positions, gate=None):
         return self.mem.ring_decode_attention(q, keys, values, positions, gate=gate)
@@ -353,8 +372,85 @@ def _torch_memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, 
     return q, gate, scores
 
 
+def _torch_conv_prefill(proj, window, conv_w, cu_seqlens, channels, lengths):
+    """Causal conv1d + SiLU over packed pieces, each continuing its row's
+    window [R, 3, C] (updated in place): fp32 taps, one rounding."""
+    x = proj[:, :channels]
+    outs, off = [], 0
+    for r, n in enumerate(lengths):
+        ext = torch.cat((window[r], x[off: off + n].to(window.dtype)), 0)             # [3 + n, C]
+        if n:
+            y = sum(ext[j: j + n].float() * conv_w[:, j].float() for j in range(conv_w.shape[1]))
+            outs.append(F.silu(y).to(proj.dtype))
+        window[r].copy_(ext[n:])
+        off += n
+    return torch.cat(outs) if outs else proj.new_zeros(0, channels)
+
+
+def _ring_context(ring, row, start, window):
+    """The min(start, window - 1) ring entries before position ``start`` of
+    ring row ``row`` [G, W, ...], oldest first, as [n, G, ...]."""
+    n = min(start, window - 1) if row >= 0 else 0
+    slots = torch.arange(start - n, start, device=ring.device) % window
+    return ring[row][:, slots].transpose(0, 1) if n else ring.new_zeros((0,) + (ring.shape[1],) + ring.shape[3:])
+
+
+def _torch_swa_prefill(q, k, v, cu_seqlens, starts, ring_k, ring_v, ring_rows, gate=None, lengths=None):
+    """Sliding-window causal attention of packed pieces with the ring as
+    left context (reference_swa, modeling_yanchor.py:412-427), fp32, query
+    blocks of 1024; then * sigmoid(gate)."""
+    n, h, d = q.shape
+    g, window = k.shape[1], ring_k.shape[2]
+    rep = h // g
+    cu = cu_seqlens.tolist()
+    lengths = lengths if lengths is not None else [cu[i + 1] - cu[i] for i in range(len(cu) - 1)]
+    st, rr = starts.tolist(), ring_rows.tolist()
+    out = torch.empty_like(q)
+    off = 0
+    for r, length in enumerate(lengths):
+        if length:
+            kc = torch.cat((_ring_context(ring_k, rr[r], st[r], window), k[off: off + length]), 0)
+            vc = torch.cat((_ring_context(ring_v, rr[r], st[r], window), v[off: off + length]), 0)
+            nctx = kc.shape[0] - length
+            for b0 in range(0, length, 1024):
+                b1 = min(length, b0 + 1024)
+                lo, hi = max(0, nctx + b0 - window + 1), nctx + b1
+                qp = torch.arange(nctx + b0, nctx + b1, device=q.device)
+                kp = torch.arange(lo, hi, device=q.device)
+                mask = (kp[None] <= qp[:, None]) & (kp[None] > qp[:, None] - window)
+                kb = kc[lo:hi].float().repeat_interleave(rep, 1)
+                vb = vc[lo:hi].float().repeat_interleave(rep, 1)
+                logits = torch.einsum("lhd,shd->hls", q[off + b0: off + b1].float(), kb) / math.sqrt(d)
+                p = logits.masked_fill(~mask[None], -math.inf).softmax(-1)
+                out[off + b0: off + b1] = torch.einsum("hls,shd->lhd", p, vb).to(q.dtype)
+        off += length
+    return out if gate is None else out * torch.sigmoid(gate)
+
+
+def _torch_ring_fill(k, v, cu_seqlens, starts, ring_rows, ring_k, ring_v, ring_pos, lengths=None):
+    """The last min(window, L) keys / values / positions of each packed piece
+    into its ring row at slot position % window."""
+    window = ring_k.shape[2]
+    cu = cu_seqlens.tolist()
+    lengths = lengths if lengths is not None else [cu[i + 1] - cu[i] for i in range(len(cu) - 1)]
+    st, rr = starts.tolist(), ring_rows.tolist()
+    off = 0
+    for r, length in enumerate(lengths):
+        if length and rr[r] >= 0:
+            t = torch.arange(max(0, length - window), length, device=k.device)
+            pos = st[r] + t
+            slots = pos % window
+            ring_k[rr[r]][:, slots] = k[off + t].transpose(0, 1).to(ring_k.dtype)
+            ring_v[rr[r]][:, slots] = v[off + t].transpose(0, 1).to(ring_v.dtype)
+            ring_pos[rr[r]][:, slots] = pos.to(torch.int32)[None]
+        off += length
+
+
 TorchGlue.ring_write = staticmethod(_torch_ring_write)
 TorchGlue.memory_prologue = staticmethod(_torch_memory_prologue)
+TorchGlue.conv_prefill = staticmethod(_torch_conv_prefill)
+TorchGlue.swa_prefill = staticmethod(_torch_swa_prefill)
+TorchGlue.ring_fill = staticmethod(_torch_ring_fill)
 
 
 def gate_read(read, valid=None, head_gate=None, gate=None):
@@ -507,18 +603,6 @@ class Model:
         y = ops.gated_rmsnorm(o.view(B, hv, dv), proj[:, c.conv_dim: c.conv_dim + vd], L["gnorm"], c.rms_eps)
         return self.ops.linear(y, L["w_out"], L.get("w_out@packed"), defer=True)
 
-    def _attn_project(self, L, x, cos, sin):
-        c = self.cfg
-        proj = F.linear(x, L["w_qkv"])
-        hq = 2 * c.attn_heads * c.head_dim
-        qg = proj[..., :hq].unflatten(-1, (c.attn_heads, 2 * c.head_dim))
-        q, gate = qg[..., : c.head_dim], qg[..., c.head_dim:]
-        k = proj[..., hq: hq + c.kv_heads * c.head_dim].unflatten(-1, (c.kv_heads, c.head_dim))
-        v = proj[..., hq + c.kv_heads * c.head_dim:].unflatten(-1, (c.kv_heads, c.head_dim))
-        q = apply_rope(rms_norm(q, L["q_norm"], c.rms_eps), cos, sin, c.rotary_dim)
-        k = apply_rope(rms_norm(k, L["k_norm"], c.rms_eps), cos, sin, c.rotary_dim)
-        return q, gate.reshape(*gate.shape[:-2], -1), k, v
-
     def _memory_qkvs(self, L, hidden, cos, sin):
         """_query_scores + _write_kv of IndependentGQAMemory (modeling_yanchor.py:147-176)."""
         c = self.cfg
@@ -636,64 +720,154 @@ class Model:
         return logits.float() if float_logits else logits
 
     # ---------------- prefill ----------------
-    def prefill(self, prompts):
-        """Prefill fresh sequences from empty caches.  prompts [R, T] int64
-        -> (logits of the last token [R, V] float32, caches dict of [R, ...]
-        tensors in cache_tensors() order)."""
+    def prefill(self, prompts, *, token_chunk=16384, max_tokens=1 << 17):
+        """Prefill fresh sequences from empty caches.
+
+        ``prompts``: [R, T] int64, or a list of R 1-D int64 token tensors of
+        any lengths (>= 1 each).  The prompts are packed into one token stream
+        (cu_seqlens) and every layer runs once over it: one conv, one GDN
+        chunk launch and one window-attention launch per layer for the whole
+        ragged set.  A prompt longer than a piece (``token_chunk`` tokens, and
+        at most ``max_tokens`` packed tokens per pass) is taken in pieces, each
+        continuing the caches the previous one left: the GDN state as the
+        chunk kernel's initial state, the conv window, the SWA ring as the
+        window's left context, the anchor memory through _sequence with a
+        state -- the reference's token-chunked prefill (runtime/model/
+        inference_kernels.py:1246-1270; modeling_yanchor.py:981-1012).
+        Positions start at 0 for every prompt (the logical positions of a
+        left-padded batch, inference_kernels.py:1245).
+
+        Returns (logits of each prompt's last token [R, V] float32, caches of
+        [R, ...] tensors in cache_tensors() order)."""
         c, dev = self.cfg, self.device
-        R, T = prompts.shape
-        if T > c.swa_window:
-            raise ValueError("prompts longer than the SWA window are not supported by this prefill")
+        seqs = list(prompts.unbind(0)) if torch.is_tensor(prompts) and prompts.ndim == 2 else list(prompts)
+        seqs = [torch.as_tensor(x).reshape(-1).to(torch.long) for x in seqs]
+        if not seqs:
+            raise ValueError("prefill needs at least one prompt")
+        lengths = [int(x.numel()) for x in seqs]
+        if min(lengths) < 1:
+            raise ValueError("prompts must hold at least one token")
+        r = len(seqs)
+        piece = max(1, min(int(token_chunk), int(max_tokens) // r))
         tmp = Model.__new__(Model)
-        tmp.cfg, tmp.B, tmp.device, tmp.dtype, tmp.ops, tmp.layers = c, R, dev, self.dtype, self.ops, self.layers
+        tmp.cfg, tmp.B, tmp.device, tmp.dtype, tmp.ops, tmp.layers = c, r, dev, self.dtype, self.ops, self.layers
         tmp._alloc_caches()
-        pos = torch.arange(T, device=dev)
-        cos, sin = rope_tables(pos, c)
-        h = self.embed[prompts]                                            # [R, T, hidden]
-        lengths = [T] * R
-        cu = torch.arange(0, (R + 1) * T, T, device=dev, dtype=torch.int32)
-        for i, L in enumerate(self.layers):
-            if L["kind"] == "gdn":
-                proj = F.linear(rms_norm(h, L["in_norm"], c.rms_eps), L["w_in"])
-                qkv, z, beta, g = self._gdn_split(L, proj)
-                xw = F.pad(qkv.float(), (0, 0, c.conv_kernel - 1, 0))           # causal conv over time
-                mixed = sum(xw[:, j: j + T] * L["conv_w"].float()[:, j] for j in range(c.conv_kernel))
-                mixed = F.silu(mixed).to(self.dtype)
-                tmp.conv_state[i].copy_(xw[:, T:])                              # last K-1 inputs, zero-padded
-                hk, dk, dv = c.gdn_heads_k * c.gdn_dk, c.gdn_dk, c.gdn_dv
-                q = mixed[..., :hk].reshape(1, R * T, c.gdn_heads_k, dk)
-                k = mixed[..., hk: 2 * hk].reshape(1, R * T, c.gdn_heads_k, dk)
-                v = mixed[..., 2 * hk:].reshape(1, R * T, c.gdn_heads_v, dv)
-                o, st = self.ops.gdn_prefill(q, k, v, g.reshape(1, R * T, -1), beta.reshape(1, R * T, -1), cu,
-                                             lengths)
-                tmp.gdn_state[i].copy_(st)
-                o = gated_rms_norm(o.reshape(R, T, c.gdn_heads_v, dv), z.reshape(R, T, c.gdn_heads_v, dv),
-                                   L["gnorm"], c.rms_eps)
-                h = h + F.linear(o.reshape(R, T, -1), L["w_out"])
-            else:
-                cs, sn = cos[None, :, None], sin[None, :, None]
-                q, gate, k, v = self._attn_project(L, rms_norm(h, L["in_norm"], c.rms_eps), cs, sn)
-                # causal attention inside the prompt (T <= window), float32
-                rep = c.attn_heads // c.kv_heads
-                qh = q.float().transpose(1, 2)                                  # [R, H, T, D]
-                kh = k.float().repeat_interleave(rep, 2).transpose(1, 2).contiguous()
-                vh = v.float().repeat_interleave(rep, 2).transpose(1, 2).contiguous()
-                att = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) / math.sqrt(c.head_dim)
-                att = att.masked_fill(torch.ones(T, T, device=dev, dtype=torch.bool).triu(1), float("-inf"))
-                ctx = torch.matmul(att.softmax(-1), vh).transpose(1, 2).reshape(R, T, -1).to(self.dtype)
-                out = F.linear(ctx * torch.sigmoid(gate), L["w_o"])
-                tmp.ring_k[i][:, :, :T] = k.transpose(1, 2)
-                tmp.ring_v[i][:, :, :T] = v.transpose(1, 2)
-                tmp.ring_pos[i][:, :, :T] = pos.to(torch.int32)
-                # anchor memory: the block-wise prefill read and write (_sequence)
-                mq, mgate, mk, mv, msc = self._memory_qkvs(L, h, cs, sn)
-                read = self.ops.memory_sequence(mq.contiguous(), mk.contiguous(), mv, msc.float(), None,
-                                                c.memory_chunk, tmp.memory[i])
-                mem_out = F.linear((read * mgate[..., None].to(read.dtype)).reshape(R, T, -1), L["m_o"])
-                h = h + out + mem_out
-            h = h + self._mlp(L, rms_norm(h, L["post_norm"], c.rms_eps))
-        logits = F.linear(rms_norm(h[:, -1], self.final_norm, c.rms_eps), self.lm_head).float()
+        last = torch.empty(r, c.hidden, dtype=self.dtype, device=dev)
+        for w0 in range(0, max(lengths), piece):
+            starts = [min(w0, n) for n in lengths]
+            lens = [max(0, min(piece, n - w0)) for n in lengths]
+            toks = torch.cat([x[w0: w0 + n] for x, n in zip(seqs, lens) if n]).to(dev)
+            h = self._prefill_piece(tmp, toks, starts, lens)
+            ends = [i for i, n in enumerate(lengths) if w0 < n <= w0 + piece]
+            if ends:
+                off = [0]
+                for n in lens:
+                    off.append(off[-1] + n)
+                src = torch.tensor([off[i] + lens[i] - 1 for i in ends], device=dev)
+                last.index_copy_(0, torch.tensor(ends, device=dev), h.index_select(0, src))
+        xn = self.ops.rmsnorm(last, self.final_norm, c.rms_eps)
+        logits = F.linear(xn, self.lm_head).float()
         return logits, tmp.cache_tensors()
+
+    def _prefill_piece(self, tmp, tokens, starts, lens):
+        """One pass of the layers over packed pieces: tokens [N] (the pieces
+        in row order), starts / lens host ints per row of ``tmp`` (lens may
+        be 0).  Updates tmp's caches in place; returns the last layer's
+        residual stream [N, hidden]."""
+        c, dev, ops = self.cfg, self.device, self.ops
+        off = [0]
+        for n in lens:
+            off.append(off[-1] + n)
+        cu = torch.tensor(off, dtype=torch.int32, device=dev)
+        pos = torch.cat([torch.arange(s, s + n) for s, n in zip(starts, lens)]).to(dev)
+        starts_t = torch.tensor(starts, dtype=torch.int64, device=dev)
+        cos, sin = rope_tables(pos, c)
+        h = self.embed[tokens]
+        for i, L in enumerate(self.layers):
+            xn = ops.rmsnorm(h, L["in_norm"], c.rms_eps)
+            if L["kind"] == "gdn":
+                delta = self._gdn_prefill(i, L, tmp, xn, cu, lens)
+            else:
+                delta = self._attn_prefill(i, L, tmp, xn, h, cos, sin, cu, starts_t, lens)
+            h = h + delta
+            h = h + self._mlp(L, ops.rmsnorm(h, L["post_norm"], c.rms_eps))
+        return h
+
+    def _gdn_prefill(self, i, L, tmp, xn, cu, lens):
+        """GDN mixer over packed pieces: conv (continuing the window), the
+        chunked recurrence from the state each row holds (one launch for all
+        rows), the gated norm and the output projection."""
+        c, ops = self.cfg, self.ops
+        n = xn.shape[0]
+        hk, dk, hv, dv = c.gdn_heads_k, c.gdn_dk, c.gdn_heads_v, c.gdn_dv
+        proj = F.linear(xn, L["w_in"])                                      # [N, qkv | z | b | a]
+        mixed = ops.conv_prefill(proj, tmp.conv_state[i], L["conv_w"], cu, c.conv_dim, lens)
+        _, _, beta, g = self._gdn_split(L, proj)
+        q = mixed[:, : hk * dk].reshape(1, n, hk, dk)
+        k = mixed[:, hk * dk: 2 * hk * dk].reshape(1, n, hk, dk)
+        v = mixed[:, 2 * hk * dk:].reshape(1, n, hv, dv)
+        o, st = ops.gdn_prefill(q, k, v, g[None], beta[None], cu, lens, initial_state=tmp.gdn_state[i])
+        tmp.gdn_state[i].copy_(st)
+        y = ops.gated_rmsnorm(o.reshape(n, hv, dv), proj[:, c.conv_dim: c.conv_dim + hv * dv], L["gnorm"],
+                              c.rms_eps)
+        return F.linear(y, L["w_out"])
+
+    def _attn_prefill(self, i, L, tmp, xn, hidden, cos, sin, cu, starts, lens):
+        """SWA + anchor-memory mixer over packed pieces: the window attention
+        reads each row's ring as left context, the pieces' keys then fill the
+        ring; the memory reads and writes through _sequence with the row's
+        state."""
+        c, ops = self.cfg, self.ops
+        n = xn.shape[0]
+        H, G, D = c.attn_heads, c.kv_heads, c.head_dim
+        proj = F.linear(xn, L["w_qkv"])                                     # [N, (q|gate) per head | k | v]
+        hq = 2 * H * D
+        qg = proj[:, :hq].view(n, H, 2 * D)
+        q = ops.head_norm_rope(qg[..., :D], L["q_norm"], cos, sin, c.rotary_dim, c.rms_eps)
+        k = ops.head_norm_rope(proj[:, hq: hq + G * D].view(n, G, D), L["k_norm"], cos, sin, c.rotary_dim,
+                               c.rms_eps)
+        v = proj[:, hq + G * D:].view(n, G, D)
+        rows = torch.arange(len(lens), device=xn.device)
+        att = ops.swa_prefill(q, k, v, cu, starts, tmp.ring_k[i], tmp.ring_v[i], rows, gate=qg[..., D:],
+                              lengths=lens)
+        ops.ring_fill(k, v, cu, starts, rows, tmp.ring_k[i], tmp.ring_v[i], tmp.ring_pos[i], lengths=lens)
+        out = F.linear(att.reshape(n, H * D), L["w_o"])
+        u = ops.rmsnorm(hidden, L["m_in_norm"], c.rms_eps)
+        mq, mgate, mk, mv, msc = self._memory_decode(L, hidden, cos, sin, u)
+        read = self._memory_prefill(tmp.memory[i], mq, mk, mv, msc, lens)
+        return out + F.linear((read * mgate[..., None].to(read.dtype)).reshape(n, H * D), L["m_o"])
+
+    def _memory_prefill(self, state, q, key, value, scores, lens):
+        """_sequence over packed pieces: the rows with tokens are laid out as
+        a right-padded [R', Lmax] batch (padding invalid, which _sequence's
+        stable argsort takes as absent) on their own state rows; returns the
+        read of every packed token [N, H, D]."""
+        c, dev = self.cfg, q.device
+        live = [r for r, n in enumerate(lens) if n]
+        nl = [lens[r] for r in live]
+        lmax = max(nl)
+        if len(live) == len(lens) and min(nl) == lmax:
+            b = len(live)
+            read = self.ops.memory_sequence(q.view(b, lmax, *q.shape[1:]), key.view(b, lmax, *key.shape[1:]),
+                                            value.reshape(b, lmax, *value.shape[1:]).contiguous(),
+                                            scores.view(b, lmax, -1).float(), None, c.memory_chunk, state)
+            return read.reshape(q.shape)
+        bi = torch.repeat_interleave(torch.arange(len(live), device=dev), torch.tensor(nl, device=dev))
+        ti = torch.cat([torch.arange(n, device=dev) for n in nl])
+
+        def pad(x, fill=0.0):
+            out = torch.full((len(live), lmax) + tuple(x.shape[1:]), fill, dtype=x.dtype, device=dev)
+            out[bi, ti] = x
+            return out
+
+        valid = pad(torch.ones(q.shape[0], dtype=torch.bool, device=dev), False)
+        rows = torch.tensor(live, device=dev)
+        sub = state if len(live) == len(lens) else state.select(rows)
+        read = self.ops.memory_sequence(pad(q), pad(key), pad(value.contiguous()), pad(scores.float()), valid,
+                                        c.memory_chunk, sub)
+        if sub is not state:
+            state.scatter_(sub, rows, torch.arange(len(live), device=dev))
+        return read[bi, ti]
 
 
 @dataclass
@@ -703,6 +877,13 @@ class Request:
     cap: int
     arrival_step: int
     row: int = -1                 # storage row, set at admission
+    group: int | None = None      # prefill group: requests of one group share one prompt and one prefill
+
+    @property
+    def group_id(self):
+        """The prefill group id, the attempt id when none is set (as
+        runtime/inference.py:92 defaults it)."""
+        return self.attempt_id if self.group is None else int(self.group)
 
 
 # The mechanical-repetition stop (reference runtime/scoring/protocols.py:73-76):
@@ -773,12 +954,13 @@ class Engine:
     def __init__(self, model: Model, *, seed=20260923, temperature=0.6, top_k=20, top_p=0.95,
                  presence_penalty=1.5, poll_interval=32, max_rows=4096, max_new_tokens=8192, use_graph=True,
                  tail_compaction=False, tail_compaction_live_fraction=0.5, eos_token_ids=(), pad_token_id=0,
-                 sampling_backend="triton_top20", mechanical=False):
+                 sampling_backend="triton_top20", mechanical=False, prefill_tokens=1 << 17):
         """``sampling_backend``: "triton_top20" (the fused top-k kernel's
         semantics) or "torch" (sample_top_k_top_p_counter's, every top_k);
         ``eos_token_ids``: at most two ids that finish a sequence;
         ``mechanical``: stop a sequence whose tail repeats mechanically
-        (checked at poll points, as the reference)."""
+        (checked at poll points, as the reference); ``prefill_tokens``: prompt
+        tokens per packed prefill of an admission."""
         if len(eos_token_ids) > 2:
             raise ValueError("the decode bookkeeping takes at most two EOS ids")
         if sampling_backend not in ("triton_top20", "torch"):
@@ -810,7 +992,11 @@ class Engine:
         self.graph = None
         self.next_row = 0
         self.slot_request: list = [None] * B
-        self.row_request: list = []          # storage row -> its request, in admission order
+        self.row_request: dict = {}          # storage row -> the request it holds (the latest one)
+        self.prefill_tokens = int(prefill_tokens)
+        self.prefill_calls = 0               # Model.prefill calls (one packed prefill each)
+        self.prefill_unique_rows = self.prefill_expanded_rows = 0
+        self.live_capture_steps = 0          # decode steps run by live re-captures (after compaction)
 
     # one decode step on the device (captured)
     def _step(self):
@@ -824,22 +1010,26 @@ class Engine:
                                self.positions, self.decode_ids, self.useful,
                                maximum_new_tokens=self.max_new, pad_token_id=self.pad, eos_token_ids=self.eos)
 
+    CAPTURE_WARMUP = 2
+
     def capture(self, live=False):
-        """Warm up and capture the decode step.  The two eager warm-up steps
-        are ordinary decode steps: call with every slot empty (they then only
-        touch rows that admission overwrites whole), or with ``live`` set when
-        live slots may take them as real steps (after compaction)."""
+        """Warm up and capture the decode step; returns the number of eager
+        warm-up steps run (0 when nothing is captured).  They are ordinary
+        decode steps: call with every slot empty (they then only touch rows
+        that admission overwrites whole), or with ``live`` set when live slots
+        may take them as real steps (after compaction)."""
         if not self.use_graph or self.graph is not None:
-            return
+            return 0
         if not live and bool(((~self.finished) & (self.slot_rows >= 0)).any()):
             raise RuntimeError("capture() with live slots would advance them; pass live=True to allow it")
-        for _ in range(2):  # warm the allocator and the sampler workspace outside capture
+        for _ in range(self.CAPTURE_WARMUP):  # warm the allocator and the sampler workspace outside capture
             self._step()
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._step()
         torch.cuda.synchronize()
+        return self.CAPTURE_WARMUP
 
     def step(self):
         if self.use_graph:
@@ -852,8 +1042,13 @@ class Engine:
     def admit(self, requests, targets, rows=None):
         """Prefill ``requests`` and place them in slots ``targets`` (host
         lists), their tokens in storage ``rows`` (default: the next free
-        rows).  Prompts of equal length are prefilled together.  Returns the
-        prefill seconds."""
+        rows).  Requests of one prefill group (``Request.group``) must hold
+        the same prompt; each group is prefilled once and its caches copied
+        to every member's slot (build_prefill_expansion /
+        assert_group_rows_identical, runtime/model/inference_kernels.py:
+        90-121, 1226-1238).  The distinct prompts, of any lengths, are packed
+        into one prefill (one GDN chunk launch per layer) per
+        ``prefill_tokens`` of prompt.  Returns the prefill seconds."""
         if not requests:
             return 0.0
         from . import inference_kernels as ik
@@ -865,21 +1060,41 @@ class Engine:
             self.next_row += n
         if max(rows) >= self.max_rows:
             raise ValueError(f"storage row {max(rows)} past the engine's {self.max_rows} rows")
-        groups: dict = {}
+        reps, inverse, seen = [], [], {}
         for j, r in enumerate(requests):
-            groups.setdefault(int(r.prompt.shape[0]), []).append(j)
-        for length, members in groups.items():
-            prompts = torch.stack([requests[j].prompt for j in members]).to(self.dev)
-            logits, caches = self.m.prefill(prompts)
+            u = seen.get(r.group_id)
+            if u is None:
+                seen[r.group_id] = u = len(reps)
+                reps.append(j)
+            elif not torch.equal(requests[reps[u]].prompt, r.prompt):
+                raise ValueError("prefill group contains non-identical rows")
+            inverse.append(u)
+        batches, cur, tokens = [], [], 0
+        for u, j in enumerate(reps):
+            length = int(requests[j].prompt.numel())
+            if cur and tokens + length > self.prefill_tokens:
+                batches.append(cur)
+                cur, tokens = [], 0
+            cur.append(u)
+            tokens += length
+        batches.append(cur)
+        for batch in batches:
+            place = {u: i for i, u in enumerate(batch)}
+            members = [j for j in range(n) if inverse[j] in place]
+            logits, caches = self.m.prefill([requests[reps[u]].prompt for u in batch])
+            self.prefill_calls += 1
+            src = torch.tensor([place[inverse[j]] for j in members], dtype=torch.long, device=self.dev)
             ids = torch.tensor([requests[j].attempt_id for j in members], dtype=torch.long, device=self.dev)
-            first = self.m.ops.sample(logits, ids, 0, None, seed=self.seed, temperature=self.temperature,
-                                      top_k=self.top_k, top_p=self.top_p, penalty=0.0,
-                                      backend=self.sampling_backend)
+            first = self.m.ops.sample(logits.index_select(0, src), ids, 0, None, seed=self.seed,
+                                      temperature=self.temperature, top_k=self.top_k, top_p=self.top_p,
+                                      penalty=0.0, backend=self.sampling_backend)
             tgt = torch.tensor([targets[j] for j in members], dtype=torch.long, device=self.dev)
-            ik.gather_rows(list(zip(caches, self.m.cache_tensors())), None, tgt, len(members))
+            ik.gather_rows(list(zip(caches, self.m.cache_tensors())), src, tgt, len(members))
             del caches
             rws = torch.tensor([rows[j] for j in members], dtype=torch.long, device=self.dev)
             caps = torch.tensor([requests[j].cap for j in members], dtype=torch.long, device=self.dev)
+            lens = torch.tensor([int(requests[j].prompt.numel()) for j in members], dtype=torch.long,
+                                device=self.dev)
             is_eos = torch.zeros(len(members), dtype=torch.bool, device=self.dev)
             for e in self.eos:
                 is_eos |= first[:, 0] == e
@@ -888,7 +1103,7 @@ class Engine:
             self.slot_caps.index_copy_(0, tgt, caps)
             self.attempt_ids.index_copy_(0, tgt, ids)
             self.row_steps.index_fill_(0, tgt, 1)
-            self.positions.index_fill_(0, tgt, length)
+            self.positions.index_copy_(0, tgt, lens)
             self.finished.index_copy_(0, tgt, done)
             self.decode_ids.index_copy_(0, tgt, torch.where(done[:, None], torch.full_like(first, self.pad), first))
             self.dense_seen.index_fill_(0, tgt, False)
@@ -900,7 +1115,9 @@ class Engine:
             self.slot_request[s_] = r
             r.row = w
             self.finished_by_repetition.discard(w)
-        self.row_request.extend(requests)
+            self.row_request[w] = r
+        self.prefill_unique_rows += len(reps)
+        self.prefill_expanded_rows += n
         torch.cuda.synchronize()
         return time.perf_counter() - t0
 
@@ -938,19 +1155,25 @@ class Engine:
         from . import inference_kernels as ik
         if not queue:
             return 0.0
-        order = ik._initial_attempt_order([r.cap for r in queue], [r.attempt_id for r in queue])
+        groups = [r.group_id for r in queue]
+        order = ik._initial_attempt_order([r.cap for r in queue], [r.attempt_id for r in queue], groups)
         take = min(self.B, len(queue), self.max_rows - self.next_row)
+        if take < len(queue) and ik._group_aligned_prefix_length(order, groups, take) != take:
+            raise ValueError("slot batch size splits a repeated-prompt prefill group")
         first = [queue[i] for i in order[:take]]
         queue[:] = [queue[i] for i in order[take:]]
         return self.admit(first, list(range(take)))
 
     def outputs(self):
-        """{attempt id: generated token ids} of every admitted request (a
-        host sync)."""
-        n = len(self.row_request)
-        lengths = self.generated[:n].tolist()
-        rows = self.storage[:n].cpu()
-        return {r.attempt_id: rows[i, : lengths[i]].tolist() for i, r in enumerate(self.row_request)}
+        """{attempt id: generated token ids} of the request each storage row
+        holds (its latest admission; a host sync)."""
+        rows = sorted(self.row_request)
+        if not rows:
+            return {}
+        idx = torch.tensor(rows, dtype=torch.long, device=self.dev)
+        lengths = self.generated.index_select(0, idx).tolist()
+        data = self.storage.index_select(0, idx).cpu()
+        return {self.row_request[w].attempt_id: data[i, : lengths[i]].tolist() for i, w in enumerate(rows)}
 
     def live_slots(self):
         """Slots that run a sequence this step (a host sync)."""
@@ -977,7 +1200,7 @@ class Engine:
         live = self.B - len(free) + take
         if self.tail_compaction and self.B > 1 and exhausted and not queue and \
                 0 < live < self.B and live <= max(1, int(self.B * self.tail_fraction)):
-            self.compact()
+            self.live_capture_steps += self.compact()
         return t, completed, take
 
     def compact(self):
@@ -986,12 +1209,12 @@ class Engine:
         smaller physical batch in one launch, and capture the decode step
         again.  The capture's eager warm-up steps are real decode steps of the
         live slots (bookkeeping counts them), as the reference's
-        consume_capture_steps."""
+        consume_capture_steps; returns their number."""
         from . import inference_kernels as ik
         keep = ik.compaction_keep(self.finished, self.slot_rows)
         n = int(keep.numel())
         if n == 0 or n == self.B:
-            return
+            return 0
         torch.cuda.synchronize()
         self.graph = None
         old = self.m.cache_tensors()
@@ -1006,7 +1229,7 @@ class Engine:
         self.B = n
         self.sink_rows = self.max_rows + torch.arange(n, device=self.dev)
         self.compactions.append(n)
-        self.capture(live=True)
+        return self.capture(live=True)
 
 
 def synthetic_requests(steps, *, rate=4.0, prompt_len=128, mean_len=1024, max_len=8192, vocab=151936,
@@ -1073,11 +1296,14 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
             t_start = time.perf_counter()
             m.refill_prefill_seconds = 0.0
         if step % poll_interval == 0:
+            live_steps = eng.live_capture_steps
             t, done, taken = eng.poll(queue, exhausted=idx >= len(pending))
             if t_start is not None:
                 m.refill_prefill_seconds += t
                 m.refilled += taken
                 m.completed += done
+                # a compaction's re-capture ran real decode steps of the live slots
+                m.decode_scheduled_token_events += (eng.live_capture_steps - live_steps) * eng.B
         eng.step()
         if progress_every and (step + 1) % progress_every == 0:
             print(f"[decode] step {step + 1} of {total} enqueued", flush=True)
