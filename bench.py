@@ -18,7 +18,12 @@ Prints one JSON line.  Workloads:
   whole model forward + sampling + slot bookkeeping for all 128 slots.
   value = useful decode tokens / (timed wall - refill prefill time), the
   reference's decode tokens/s definition; ``decode.live_slots`` gives the
-  live slots per timed step (min / mean / first / last).
+  live slots per timed step (min / mean / first / last), ``decode.ring_fill``
+  the mean live fraction of the SWA rings those steps read (a young ring is
+  cheaper: the window read skips blocks without a live slot).  Beside the
+  decode line the same run reports ``prefill`` (the ``gdn_prefill`` workload:
+  20 timed calls after 20 warm-up calls, with its HBM and MFMA roofline) and
+  ``sampling`` (the ``sampling`` workload at the decode batch).
 * ``long_horizon``: B=256 fixed sequences generating 32768 tokens from
   256-token prompts, 16-slot anchor memory committed every 64 tokens;
   sustained tokens/s over a bounded window of steps and peak HBM use.
@@ -256,6 +261,15 @@ def bench_model_decode(steps, warmup, cpu, batch=128):
                    "completed": met.completed, "peak_hbm_gib": met.peak_allocated_gib, **met.extra},
     }
     del model
+    torch.cuda.empty_cache()
+    _log("model_decode: the chunked prefill and the sampler beside the decode line")
+    pre = bench_gdn_prefill(20, 20, False)
+    res["prefill"] = {"workload": pre["config"]["workload"], "tokens_per_s": pre["value"],
+                      "ms_per_call": pre["roofline"]["avg_launch_us"] * 1e-3, "calls": 20, "warmup_calls": 20,
+                      "roofline": pre["roofline"]}
+    smp = bench_sampling(100, 20, False, batch=batch)
+    res["sampling"] = {"workload": smp["config"]["workload"], "us_per_call": smp["roofline"]["avg_launch_us"],
+                       "calls": 100, "roofline": smp["roofline"]}
     torch.cuda.empty_cache()
     if cpu:
         res["cpu_baseline"] = cpu_model_decode(batch)
@@ -754,7 +768,7 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": res["dtype"], "data": "synthetic (seeded random-init weights and requests)",
             "config": res["config"], "roofline": res["roofline"]}
-    for key in ("cpu_baseline", "decode", "hbm_streams_gbs", "gemm_bf16"):
+    for key in ("cpu_baseline", "decode", "prefill", "sampling", "hbm_streams_gbs", "gemm_bf16"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

@@ -1280,6 +1280,10 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
     t_start = None
     useful0 = 0
     hist = torch.zeros(steps + 1, dtype=torch.long, device=eng.dev)
+    # per timed step, the slots' positions and live flags as the step reads
+    # them (two small device copies a step), for the SWA rings' live fraction
+    pos_hist = torch.zeros(steps, eng.B, dtype=torch.long, device=eng.dev)
+    live_hist = torch.zeros(steps, eng.B, dtype=torch.bool, device=eng.dev)
     fill_seconds = 0.0
     for step in range(total):
         while idx < len(pending) and pending[idx].arrival_step <= step:
@@ -1304,6 +1308,9 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
                 m.completed += done
                 # a compaction's re-capture ran real decode steps of the live slots
                 m.decode_scheduled_token_events += (eng.live_capture_steps - live_steps) * eng.B
+        if t_start is not None and eng.B == pos_hist.shape[1]:
+            pos_hist[m.decode_steps].copy_(eng.positions)
+            torch.logical_not(eng.finished, out=live_hist[m.decode_steps])
         eng.step()
         if progress_every and (step + 1) % progress_every == 0:
             print(f"[decode] step {step + 1} of {total} enqueued", flush=True)
@@ -1316,7 +1323,14 @@ def run_decode_benchmark(model: Model, *, steps, warmup, rate=4.0, prompt_len=12
     m.decode_useful_token_events = int(eng.useful.item()) - useful0
     m.peak_allocated_gib = torch.cuda.max_memory_allocated() / 2**30
     live = (hist[1:] - hist[:-1]).cpu()
-    m.extra = {"queue_left": len(queue), "live_slots_end": eng.live_slots(),
+    # a step at position p reads min(p + 1, W) live ring slots (its own token
+    # is written before the read); averaged over the live slots of the timed
+    # steps recorded at full width
+    window = model.cfg.swa_window
+    lh = live_hist[: m.decode_steps]
+    fill = (pos_hist[: m.decode_steps] + 1).clamp(max=window).float() / window
+    ring_fill = float((fill * lh).sum() / lh.sum().clamp(min=1))
+    m.extra = {"queue_left": len(queue), "live_slots_end": eng.live_slots(), "ring_fill": ring_fill,
                "live_slots": {"min": int(live.min()), "mean": float(live.float().mean()),
                               "first": int(live[0]), "last": int(live[-1])} if steps else {},
                "physical_slots": eng.B, "tail_compactions": list(eng.compactions),
