@@ -40,6 +40,8 @@ Prints one JSON line.  Workloads:
   MFMA block read alone.
 * ``sampling``: the decode step's sampler (fused top-20 semantics, top-p 0.95,
   presence penalty) on 128 rows of bf16 logits over the full vocabulary.
+* ``projections``: every decode projection of the model at M = 128 on the
+  packed-weight kernels, as the step calls them, beside hipBLASLt.
 * ``hbm_copy``: a 128 MiB device copy, the calibration kernel for the HBM byte
   counters behind ``roofline.traffic``; ``hbm_streams_gbs`` adds the rates of
   the library's calibration streams (copy, in-place read-modify-write, read,
@@ -699,6 +701,87 @@ def bench_sampling(steps, warmup, cpu, batch=128):
                          "sample_rows_kernel", "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3}}
 
 
+# The decode step's projections at the 4B shape: (name, N, K, epilogue), the
+# packed weights' shapes per layer (GDN: input and output; attention: q/k/v
+# and output; anchor memory: fused input, writer down, k/v, output; MLP:
+# gate/up with the silu epilogue and down; lm_head) with their calls per step.
+DECODE_PROJECTIONS = [("mlp_gate_up", 19456, 2560, "silu", 36), ("mlp_down", 2560, 9728, "defer", 36),
+                      ("gdn_in", 16448, 2560, "", 27), ("gdn_out", 2560, 4096, "defer", 27),
+                      ("attn_qkv", 10240, 2560, "", 9), ("attn_o", 2560, 4096, "", 9),
+                      ("memory_in", 9280, 2560, "", 9), ("memory_writer_down", 2560, 2560, "residual", 9),
+                      ("memory_kv", 2048, 2560, "", 9), ("memory_o", 2560, 4096, "defer", 9),
+                      ("lm_head", 151936, 2560, "", 1)]
+
+
+def bench_projections(steps, warmup, cpu, batch=128):
+    """Every decode projection of the 4B-shaped model at M = batch rows on
+    the packed-weight kernels, as the decode step calls them (silu
+    epilogue; split-K partials left to the next norm where the step defers
+    them; the residual add), each in a HIP graph of 32 calls over rotating
+    weight copies (> 600 MB, past the Infinity Cache), beside hipBLASLt on the
+    row-major weights.  value = weight bytes of one decode step's
+    projections / their summed time."""
+    from yanchor_amd import _native, layers
+
+    del cpu
+    dev = torch.device("cuda:0")
+    calls = 32
+    out = {}
+    step_bytes = step_us = blas_us = 0.0
+
+    def graph_us(fn, reps=max(2, steps // 32)):
+        for i in range(max(1, warmup // 32)):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(calls):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * calls)
+
+    for name, n, k, epi, per_step in DECODE_PROJECTIONS:
+        copies = max(2, math.ceil(600e6 / (n * k * 2)))
+        gen = torch.Generator(device=dev).manual_seed(7)
+        ws = [(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16) for _ in range(copies)]
+        pws = [layers.PackedWeight(w, pair_halves=epi == "silu") for w in ws]
+        x = torch.randn(batch, k, device=dev, generator=gen).to(torch.bfloat16)
+        res = torch.randn(batch, n, device=dev, generator=gen).to(torch.bfloat16) if epi == "residual" else None
+        if epi == "silu":
+            fn = lambda i: layers.linear_silu(x, pws[i % copies])  # noqa: E731
+        else:
+            fn = lambda i: layers.linear(x, pws[i % copies], residual=res, defer=epi == "defer")  # noqa: E731
+        us = graph_us(fn)
+        ref = graph_us(lambda i: torch.matmul(x, ws[i % copies].t()))
+        nbytes = n * k * 2
+        split = 1 if epi == "silu" else int(_native.lib().yh_linear_packed_split(batch, n, k))
+        out[name] = {"shape": [batch, n, k], "epilogue": epi or "plain", "split_k": split, "us": round(us, 2),
+                     "tb_s": round(nbytes / us / 1e6, 3), "hipblaslt_us": round(ref, 2), "calls_per_step": per_step}
+        _log(f"projections: {name} {n}x{k}: {us:.1f} us ({nbytes / us / 1e6:.2f} TB/s), hipBLASLt {ref:.1f} us")
+        step_bytes += per_step * nbytes
+        step_us += per_step * us
+        blas_us += per_step * ref
+        del ws, pws
+        torch.cuda.empty_cache()
+    achieved = step_bytes / step_us / 1e3
+    return {"metric": "decode-step projections at M=128: weight bytes / summed kernel time (HBM GB/s)",
+            "value": achieved, "unit": "GB/s", "ms_per_step": step_us * 1e-3, "dtype": "bf16",
+            "config": {"workload": f"projections: the 4B-shaped model's decode projections at M={batch} "
+                                   "(packed weights, graphs of 32 calls over rotating weights)",
+                       "global_batch": batch, "seq_len": 1, "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "proj_kernel",
+                         "bytes_per_launch": step_bytes, "avg_launch_us": step_us},
+            "projections": out, "hipblaslt_ms_per_step": blas_us * 1e-3}
+
+
 def bench_hbm_copy(steps, warmup, cpu, batch=None):
     """A plain 128 MiB device-to-device copy (torch's copy kernel): the
     calibration kernel for the HBM byte counters; beside it the rates of the
@@ -740,7 +823,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (model_decode 64, gdn_decode 20)")
     ap.add_argument("--workload", default="model_decode",
                     choices=["model_decode", "long_horizon", "gdn_decode", "gdn_decode_fused", "gdn_prefill",
-                             "anchor_read", "anchor_prefill", "sampling", "hbm_copy"])
+                             "anchor_read", "anchor_prefill", "sampling", "projections", "hbm_copy"])
     ap.add_argument("--batch", type=int, default=None, help="slots (model_decode 128) / rows (gdn_decode 64)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
@@ -758,17 +841,19 @@ def main() -> int:
         steps, warmup = args.steps or 200, 20 if args.warmup is None else args.warmup
         fn = {"gdn_decode": bench_gdn_decode, "gdn_decode_fused": bench_gdn_decode_fused,
               "gdn_prefill": bench_gdn_prefill, "anchor_read": bench_anchor_read, "sampling": bench_sampling,
-              "anchor_prefill": bench_anchor_prefill,
+              "anchor_prefill": bench_anchor_prefill, "projections": bench_projections,
               "hbm_copy": bench_hbm_copy}
         res = fn[args.workload](steps, warmup, not args.no_cpu,
-                                batch=args.batch or (128 if args.workload in ("gdn_decode_fused", "sampling") else
+                                batch=args.batch or (128 if args.workload in ("gdn_decode_fused", "sampling",
+                                                                              "projections") else
                                                      32 if args.workload == "anchor_prefill" else 64))
     line = {"metric": res.get("metric", METRIC), "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": steps, "warmup": warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": res["dtype"], "data": "synthetic (seeded random-init weights and requests)",
             "config": res["config"], "roofline": res["roofline"]}
-    for key in ("cpu_baseline", "decode", "prefill", "sampling", "hbm_streams_gbs", "gemm_bf16"):
+    for key in ("cpu_baseline", "decode", "prefill", "sampling", "projections", "hipblaslt_ms_per_step",
+                "hbm_streams_gbs", "gemm_bf16"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

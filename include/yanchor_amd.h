@@ -367,7 +367,10 @@ int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split
  *   `z = x + proj(...)` adds (modeling_yanchor.py:159, 903-905).  silu_pairs
  *   (weights packed with pair_halves, split_k == 1, no residual): out is
  *   [M, N/2] = bf16(bf16(silu(gate)) * up), the MLP activation
- *   (inference_kernels.py:642-666) in the projection's store.
+ *   (inference_kernels.py:642-666) in the projection's store.  The work
+ *   split (columns per workgroup, waves) is yh_proj_pick's for the shape;
+ *   the output rows (and the residual's) are written 16 bytes at a time and
+ *   must be 16-byte aligned.
  *   Requirements: 0 <= M <= 128, N % 16 == 0, K % 128 == 0.
  */
 int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, int pair_halves, yh_stream_t stream);
@@ -649,6 +652,39 @@ int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t feat_offse
                        const float* gate_b, const float* adm_up, void* q, float* gate, float* scores, int64_t B,
                        int64_t H, int64_t D, int64_t G, int64_t A, int64_t rotary_dim, float eps, int64_t act_offset,
                        int64_t act_width, void* act, int64_t act_stride, yh_stream_t stream);
+
+/*
+ * Decode projection on packed weights with a selectable work split
+ * (configuration `config`, 0 <= config < yh_proj_config_count()): out[M, N] =
+ * x[M, K] . W[N, K]^T, M <= 128, the weights in yh_linear_pack's fragment
+ * order, the epilogues of yh_linear_packed (residual, silu pairs).  No
+ * counterpart in the reference: the reference's decode projections are
+ * torch.nn.functional.linear calls (modeling_yanchor.py:147-176 and the
+ * Qwen3.5 projections of the transformers wheel) and its packed Triton GEMVs
+ * (runtime/model/inference_kernels.py:939-1001).  A configuration fixes the
+ * columns per workgroup (yh_proj_columns) and the K granularity
+ * (yh_proj_phase_k: K and every K slice are multiples of it).  With the K
+ * split over S > 1 slices the fp32 partials [S, M, N] go to `workspace` and
+ * are summed by yh_linear_reduce or a partial-aware norm; *slices_out
+ * receives S.
+ */
+int yh_proj(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride, int64_t M,
+            int64_t N, int64_t K, const void* residual, int64_t residual_stride, int silu_pairs, int config,
+            int64_t split_k, void* workspace, int64_t workspace_bytes, int64_t* slices_out, yh_stream_t stream);
+int yh_proj_config_count(void);
+int yh_proj_phase_k(int config);
+int yh_proj_columns(int config);
+/* The configuration and K split yh_linear_packed uses for a shape (no
+ * counterpart in the reference; K a multiple of 128). */
+int yh_proj_pick(int64_t M, int64_t N, int64_t K, int silu_pairs, int* config, int64_t* split_k);
+
+/*
+ * out[M, N] = bf16(sum over s of part[s]) (+ residual, added to the bf16
+ * sum): the split-K reduce of yh_linear_packed / yh_proj, slices added in
+ * order.  part fp32 [S, M, N]; out rows out_stride apart.
+ */
+int yh_linear_reduce(const float* part, void* out, int64_t out_stride, int64_t M, int64_t N, int64_t S,
+                     const void* residual, int64_t residual_stride, yh_stream_t stream);
 
 /*
  * Refill prefill of a packed, ragged set of prompt pieces (cu_seqlens int32

@@ -30,6 +30,9 @@ SIGNATURES: dict[str, list] = {
                                 _i32, _i32, _i32, _i32, _p],
     "yh_gdn_chunk_varlen": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                             _i32, _i32, _i32, _i32, _p, _i64, _p],
+    "yh_proj": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i32, _i64, _p, _i64, _p, _p],
+    "yh_linear_reduce": [_p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "yh_proj_pick": [_i64, _i64, _i64, _i32, _p, _p],
     "yh_conv_prefill": [_p, _i64, _p, _p, _p, _i64, _i64, _i64, _p, _i32, _p],
     "yh_swa_prefill": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64,
                        _i64, _i64, _i64, _i64, _i32, _p],
@@ -87,6 +90,9 @@ PLAIN: dict[str, tuple] = {
     "yh_gdn_chunk_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "yh_linear_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "yh_topk_segments": (None, [_i64, _i64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
+    "yh_proj_config_count": (_i32, []),
+    "yh_proj_phase_k": (_i32, [_i32]),
+    "yh_proj_columns": (_i32, [_i32]),
 }
 
 _lib = None

@@ -263,229 +263,17 @@ __global__ void __launch_bounds__(256) linear_reduce_kernel(const float* part, u
   *reinterpret_cast<uint2*>(out + m * os + c) = o;
 }
 
-// ---- Packed-weight projection -----------------------------------------------
-// The weights are repacked once (yh_linear_pack) into MFMA fragment order: for
-// column tile T (16 output columns) and K block kb (32 of K) the 1 KiB B
-// operand of one 16x16x32 MFMA is stored contiguously, lane l holding
-// W[16 T + l % 16][32 kb + 8 (l / 16) .. + 8]:
+// ---- Packed weights -----------------------------------------------------------
+// The weights of the decode projections are repacked once (yh_linear_pack)
+// into MFMA fragment order: for column tile T (16 output columns) and K block
+// kb (32 of K) the 1 KiB B operand of one 16x16x32 MFMA is stored
+// contiguously, lane l holding W[16 T + l % 16][32 kb + 8 (l / 16) .. + 8]:
 //   packed[((T * K/32 + kb) * 64 + l) * 8 + e] = W[16 T + l % 16][32 kb + 8 (l / 16) + e]
 // A wave's weight load is then one contiguous 1 KiB (eight whole 128-byte
 // lines).  From the row-major layout every load takes 64 bytes from each of 16
 // rows, and the number of line misses a CU keeps in flight caps the streaming
 // rate (measured on MI355X at M = 128: 3.0 -> 4.5 TB/s on a 168 MB weight).
-//
-// Workgroup = 8 waves: 4 column groups (32 columns each, 128 per workgroup)
-// x 2 K halves (the even and the odd 32-wide K block of every 64-wide chunk),
-// so two waves share each SIMD and cover each other's MFMA and LDS latency.
-// x is staged in LDS a phase of kPh chunks at a time (one barrier per phase),
-// loaded into registers one phase ahead; weight fragments stream kPD of the
-// wave's K blocks ahead of use.  The two K halves of a column group add their
-// accumulators through LDS at the end (a fixed order); split K over S slices
-// goes through fp32 partials and linear_reduce_kernel as above.
-constexpr int kPkThreads = 512;
-constexpr int kPh = 2;                 // 64-wide chunks per x phase
-constexpr int kPhK = kPh * kKC;        // K per phase
-constexpr int kPhPad = kPhK + 8;       // LDS row stride (elements) of an x phase
-constexpr int kPD = 2;                 // weight blocks in flight per wave
-constexpr int kPkSteps = kPh;          // a wave's K blocks per phase (K half of 2 kPh blocks)
-constexpr int kPkUnroll = 2;           // phases per loop iteration (static LDS / ring slots)
-static_assert(kPD == kPkSteps, "one ring turn per phase keeps the ring slots static");
-
-template <int MT>
-struct PkPipe {
-  static constexpr int XV = MT * 16 * kPhK / 8 / kPkThreads;  // x vectors per thread per phase
-  uint4 wr[kPD][2];
-  uint4 xr[XV];
-  f32x4v acc[MT][2];
-};
-
-// x rows [0, 16 MT) x [kbase, kbase + kPhK) into registers (rows >= M re-read
-// row M - 1: their outputs are never stored).
-template <int MT>
-__device__ __forceinline__ void pk_load_x(const LinArgs& a, int kbase, uint4 (&r)[PkPipe<MT>::XV]) {
-#pragma unroll
-  for (int i = 0; i < PkPipe<MT>::XV; ++i) {
-    const int idx = i * kPkThreads + threadIdx.x;
-    const int row = idx / (kPhK / 8), c8 = (idx % (kPhK / 8)) * 8;
-    r[i] = *reinterpret_cast<const uint4*>(a.x + min(row, a.M - 1) * a.xs + kbase + c8);
-  }
-}
-template <int MT>
-__device__ __forceinline__ void pk_store_x(uint16_t (*buf)[kPhPad], const uint4 (&r)[PkPipe<MT>::XV]) {
-#pragma unroll
-  for (int i = 0; i < PkPipe<MT>::XV; ++i) {
-    const int idx = i * kPkThreads + threadIdx.x;
-    const int row = idx / (kPhK / 8), c8 = (idx % (kPhK / 8)) * 8;
-    *reinterpret_cast<uint4*>(&buf[row][c8]) = r[i];
-  }
-}
-
-struct PkWave {
-  const uint16_t* wp[2];  // this lane's 16 bytes of block 0 of each column tile
-  int kb0;                // first 32-wide K block of the slice
-  int nown;               // this wave's K blocks in the slice
-  int h;                  // K half: block kb0 + 2 t + h is the wave's t-th block
-  int col, quad;
-};
-
-template <int MT>
-__device__ __forceinline__ void pk_load_w(PkPipe<MT>& p, int slot, const PkWave& wv, int t) {
-  const int blk = wv.kb0 + 2 * min(t, wv.nown - 1) + wv.h;
-  p.wr[slot][0] = ld_w16(wv.wp[0] + static_cast<int64_t>(blk) * 512);
-  p.wr[slot][1] = ld_w16(wv.wp[1] + static_cast<int64_t>(blk) * 512);
-}
-
-// Phase ph (parity U of the loop unroll): prefetch the next phase's x, then
-// the wave's kPkSteps K blocks: A fragments from LDS, 2 MT MFMAs each, the
-// weight ring refilled kPD blocks ahead; store the next x phase, barrier.
-template <int MT, int U>
-__device__ __forceinline__ void pk_phase(PkPipe<MT>& p, uint16_t (*xs)[MT * 16][kPhPad], const LinArgs& a,
-                                         const PkWave& wv, int ph, int nph) {
-  pk_load_x<MT>(a, wv.kb0 * 32 + min(ph + 1, nph - 1) * kPhK, p.xr);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < kPkSteps; ++i) {
-    const int kk = (2 * i + wv.h) * 32 + wv.quad * 8;  // K offset inside the phase
-    const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, p.wr[i][0]);
-    const bf16x8_t b1 = __builtin_bit_cast(bf16x8_t, p.wr[i][1]);
-    bf16x8_t av[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-      av[t] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&xs[U][t * 16 + wv.col][kk]));
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      p.acc[t][0] = mfma(av[t], b0, p.acc[t][0]);
-      p.acc[t][1] = mfma(av[t], b1, p.acc[t][1]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    pk_load_w<MT>(p, i, wv, ph * kPkSteps + i + kPD);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  pk_store_x<MT>(xs[U ^ 1], p.xr);
-  lds_barrier();
-}
-
-// acc rows of the other K half's tiles to LDS; then add the partner's.
-template <int MT, int H>
-__device__ __forceinline__ void pk_send_half(const f32x4v (&acc)[MT][2], f32x4v* red, int w, int lane) {
-  constexpr int kHalf = MT / 2, kOther = (1 - H) * kHalf;
-#pragma unroll
-  for (int tt = 0; tt < kHalf; ++tt)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) red[((w * kHalf + tt) * 2 + ct) * 64 + lane] = acc[kOther + tt][ct];
-}
-template <int MT, int H>
-__device__ __forceinline__ void pk_add_half(f32x4v (&acc)[MT][2], const f32x4v* red, int wc, int lane) {
-  constexpr int kHalf = MT / 2, kMine = H * kHalf;
-  const int partner = wc + (1 - H) * 4;
-#pragma unroll
-  for (int tt = 0; tt < kHalf; ++tt)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) acc[kMine + tt][ct] += red[((partner * kHalf + tt) * 2 + ct) * 64 + lane];
-}
-
-// Row tiles [T0, T1) of the accumulators to the output (bf16) or to this
-// slice's fp32 partial plane.
-template <int MT, int T0, int T1>
-__device__ __forceinline__ void pk_store_rows(const f32x4v (&acc)[MT][2], const LinArgs& a, int quad,
-                                              const int (&ncol)[2], int slice) {
-  if (a.silu_pairs) {
-    // column tiles 2j (gate) and 2j+1 (up) of intermediate columns 16j.. are
-    // this wave's two tiles; the activation is F.silu(gate) * up in bf16
-    if (ncol[0] >= a.N) return;
-    const int col = ncol[0] % 16, j = ncol[0] / 32;
-#pragma unroll
-    for (int t = T0; t < T1; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = t * 16 + quad * 4 + i;
-        if (m >= a.M) continue;
-        const float g = bf16_to_f32(f32_to_bf16(acc[t][0][i])), u = bf16_to_f32(f32_to_bf16(acc[t][1][i]));
-        const float sg = bf16_to_f32(f32_to_bf16(g / (1.f + expf(-g))));
-        a.out[m * a.os + j * 16 + col] = f32_to_bf16(sg * u);
-      }
-    return;
-  }
-  float* mine = a.S == 1 ? nullptr : a.part + static_cast<int64_t>(slice) * a.M * a.N;
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    if (ncol[ct] >= a.N) continue;
-#pragma unroll
-    for (int t = T0; t < T1; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = t * 16 + quad * 4 + i;
-        if (m >= a.M) continue;
-        if (a.S == 1) {
-          float y = acc[t][ct][i];
-          if (a.res) y = bf16_to_f32(f32_to_bf16(y)) + bf16_to_f32(a.res[m * a.rs + ncol[ct]]);
-          a.out[m * a.os + ncol[ct]] = f32_to_bf16(y);
-        } else {
-          mine[static_cast<int64_t>(m) * a.N + ncol[ct]] = acc[t][ct][i];
-        }
-      }
-  }
-}
-
-template <int MT>
-__global__ void __launch_bounds__(kPkThreads) packed_linear_kernel(LinArgs a) {
-  static_assert(MT % 2 == 0 && (MT * 16 * kPhK / 8) % kPkThreads == 0, "x phase must split evenly");
-  constexpr int kXBytes = 2 * MT * 16 * kPhPad * 2;
-  constexpr int kRBytes = 8 * (MT / 2) * 2 * 64 * 16;
-  __shared__ __align__(16) char smem[kXBytes > kRBytes ? kXBytes : kRBytes];
-  auto xs = reinterpret_cast<uint16_t (*)[MT * 16][kPhPad]>(smem);
-
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wc = w & 3;
-  const int tile = blockIdx.x, slice = blockIdx.y;
-  const int c0 = slice * a.chunks_per_slice;
-  const int c1 = min(a.K / kKC, c0 + a.chunks_per_slice);
-  const int nph = (c1 - c0) / kPh;  // the host keeps slices in whole phases
-  PkWave wv;
-  wv.h = w >> 2;
-  wv.col = lane & 15;
-  wv.quad = lane >> 4;
-  wv.kb0 = c0 * 2;
-  wv.nown = nph * kPkSteps;
-  int ncol[2];
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    ncol[ct] = tile * kNT + wc * 32 + ct * 16 + wv.col;
-    const int T = min(tile * (kNT / 16) + wc * 2 + ct, a.N / 16 - 1);
-    wv.wp[ct] = a.w + static_cast<int64_t>(T) * (a.K / 32) * 512 + lane * 8;
-  }
-  PkPipe<MT> p;
-#pragma unroll
-  for (int t = 0; t < MT; ++t) p.acc[t][0] = p.acc[t][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
-
-  if (nph > 0) {  // uniform over the workgroup
-    pk_load_x<MT>(a, wv.kb0 * 32, p.xr);
-#pragma unroll
-    for (int i = 0; i < kPD; ++i) pk_load_w<MT>(p, i, wv, i);
-    pk_store_x<MT>(xs[0], p.xr);
-    lds_barrier();
-    int ph = 0;
-    for (; ph + kPkUnroll <= nph; ph += kPkUnroll) {
-      pk_phase<MT, 0>(p, xs, a, wv, ph, nph);
-      pk_phase<MT, 1>(p, xs, a, wv, ph + 1, nph);
-    }
-    if (ph < nph) pk_phase<MT, 0>(p, xs, a, wv, ph, nph);
-  }
-
-  // the two K halves of each column group meet in LDS (x is no longer read)
-  lds_barrier();
-  f32x4v* red = reinterpret_cast<f32x4v*>(smem);
-  if (wv.h == 0) pk_send_half<MT, 0>(p.acc, red, w, lane);
-  else pk_send_half<MT, 1>(p.acc, red, w, lane);
-  lds_barrier();
-  if (wv.h == 0) {
-    pk_add_half<MT, 0>(p.acc, red, wc, lane);
-    pk_store_rows<MT, 0, MT / 2>(p.acc, a, wv.quad, ncol, slice);
-  } else {
-    pk_add_half<MT, 1>(p.acc, red, wc, lane);
-    pk_store_rows<MT, MT / 2, MT>(p.acc, a, wv.quad, ncol, slice);
-  }
-}
+// The projection kernels on this layout are in proj.hip.
 
 // W [N, K] row-major -> packed fragment order; one thread per 16-byte piece.
 // With pair_halves the column tiles alternate between the two row halves of W
@@ -500,18 +288,6 @@ __global__ void __launch_bounds__(256) linear_pack_kernel(const uint16_t* w, uin
   const int64_t src_tile = pair_halves ? (T & 1) * (N / 32) + (T >> 1) : T;
   const int64_t row = src_tile * 16 + (l & 15), k = kb * 32 + (l >> 4) * 8;
   reinterpret_cast<uint4*>(packed)[piece] = *reinterpret_cast<const uint4*>(w + row * K + k);
-}
-
-// Split for the packed kernel: fill the 256 CUs with one workgroup each (a
-// second round of workgroups costs more than it gains), keep >= 6 chunks and
-// whole x phases per slice.  Measured on MI355X at M = 128: S = 1 for
-// N >= 19456, 2-3 for N ~ 10k, 8-12 for N = 2560 with K >= 4096, 4-6 for
-// N <= 2560 with K = 2560.
-int pick_packed_split(int64_t M, int64_t N, int64_t K) {
-  (void)M;
-  const int64_t tiles = (N + kNT - 1) / kNT, chunks = K / kKC;
-  int64_t s = std::max<int64_t>(1, std::min<int64_t>({256 / tiles, chunks / 6, 16}));
-  return static_cast<int>(s);
 }
 
 // Split-K factor S (a power of two, at most 8): grow S while the grid is
@@ -599,62 +375,18 @@ extern "C" int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K,
   return YH_OK;
 }
 
-extern "C" int yh_linear_packed_split(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N < 16 || K < yh::kPhK) return 1;
-  return yh::pick_packed_split(M, N, K);
-}
-
-extern "C" int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride,
-                                int64_t M, int64_t N, int64_t K, const void* residual, int64_t residual_stride,
-                                int silu_pairs, int64_t split_k, void* workspace, int64_t workspace_bytes,
-                                int defer_reduce, int64_t* slices_out, yh_stream_t stream) {
+extern "C" int yh_linear_reduce(const float* part, void* out, int64_t out_stride, int64_t M, int64_t N, int64_t S,
+                                const void* residual, int64_t residual_stride, yh_stream_t stream) {
   using namespace yh;
-  YH_CHECK_ARG(M >= 0 && M <= kMaxM, "linear_packed: M must be in [0, %d] (got %lld)", kMaxM, (long long)M);
-  YH_CHECK_ARG(N > 0 && N % 16 == 0, "linear_packed: N must be a positive multiple of 16");
-  YH_CHECK_ARG(K > 0 && K % kPhK == 0, "linear_packed: K must be a positive multiple of %d", kPhK);
-  YH_CHECK_ARG(x_stride >= K && x_stride % 8 == 0 && out_stride >= (silu_pairs ? N / 2 : N),
-               "linear_packed: bad strides");
-  YH_CHECK_ARG(!silu_pairs || (N % 32 == 0 && !residual && split_k == 1),
-               "linear_packed: the silu epilogue needs N % 32 == 0, no residual and split_k == 1");
-  const int64_t phases = K / kPhK;
-  YH_CHECK_ARG(split_k >= 1 && split_k <= phases, "linear_packed: split_k must be in [1, K/%d]", kPhK);
-  if (M == 0) {
-    if (slices_out) *slices_out = 1;
-    return YH_OK;
-  }
-  YH_CHECK_ARG(x && w_packed && out, "linear_packed: null pointer");
-  YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed)) & 15) == 0,
-               "linear_packed: x and the packed weights must be 16-byte aligned");
-  // slices hold whole phases; S counts the slices that own at least one
-  const int64_t pps = (phases + split_k - 1) / split_k;
-  const int S = static_cast<int>((phases + pps - 1) / pps);
-  const int64_t need = S > 1 ? static_cast<int64_t>(S) * M * N * 4 : 0;
-  YH_CHECK_ARG(S == 1 || (workspace && workspace_bytes >= need), "linear_packed: workspace of %lld bytes required",
-               (long long)need);
-  YH_CHECK_ARG(S == 1 || (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
-               "linear_packed: workspace must be 16-byte aligned");
-  YH_CHECK_ARG(S == 1 || (out_stride % 4 == 0 && N % 4 == 0), "linear_packed: split-K output rows must be 8-byte aligned");
-  YH_CHECK_ARG(!residual || (residual_stride >= N && (S == 1 || (residual_stride % 4 == 0 &&
-                                                                (reinterpret_cast<uintptr_t>(residual) & 7) == 0))),
-               "linear_packed: bad residual stride / alignment");
-  LinArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_packed), static_cast<uint16_t*>(out),
-            S > 1 ? static_cast<float*>(workspace) : nullptr, x_stride, out_stride, (int)M, (int)N, (int)K, S,
-            static_cast<int>(pps * kPh), static_cast<const uint16_t*>(residual), residual_stride, silu_pairs};
-  const dim3 grid(static_cast<unsigned>((N + kNT - 1) / kNT), static_cast<unsigned>(S));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int mt = static_cast<int>((M + 15) / 16);
-  switch (mt <= 2 ? 2 : mt <= 4 ? 4 : 8) {
-    case 2: hipLaunchKernelGGL(packed_linear_kernel<2>, grid, dim3(kPkThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(packed_linear_kernel<4>, grid, dim3(kPkThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL(packed_linear_kernel<8>, grid, dim3(kPkThreads), 0, st, a); break;
-  }
-  YH_CHECK_LAUNCH("linear_packed");
-  if (slices_out) *slices_out = S;
-  if (S > 1 && !defer_reduce) {
-    const int64_t quads = M * N / 4;
-    hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0, st,
-                       a.part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N, S, a.res, a.rs);
-    YH_CHECK_LAUNCH("linear_reduce");
-  }
+  YH_CHECK_ARG(M >= 0 && N > 0 && N % 4 == 0 && S >= 1 && out_stride >= N && out_stride % 4 == 0,
+               "linear_reduce: bad sizes");
+  YH_CHECK_ARG(!residual || (residual_stride >= N && residual_stride % 4 == 0), "linear_reduce: bad residual");
+  if (M == 0) return YH_OK;
+  YH_CHECK_ARG(part && out, "linear_reduce: null pointer");
+  const int64_t quads = M * N / 4;
+  hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N,
+                     (int)S, static_cast<const uint16_t*>(residual), residual_stride);
+  YH_CHECK_LAUNCH("linear_reduce");
   return YH_OK;
 }

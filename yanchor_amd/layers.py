@@ -373,7 +373,7 @@ def linear(x, w, split_k=None, residual=None, defer=False):
         if residual.shape != (m, n) or residual.stride(1) != 1:
             raise ValueError("residual must be [M, N] with unit last stride")
         N.require_device(residual)
-        if residual.stride(0) % 4 or residual.data_ptr() % 8:
+        if residual.stride(0) % 8 or residual.data_ptr() % 16:   # rows read 16 bytes at a time
             residual = residual.contiguous()
     if packed:
         s = int(split_k) if split_k is not None else N.lib().yh_linear_packed_split(m, n, k)

@@ -132,12 +132,13 @@ class HipOps:
             return TorchGlue.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
         return self.layers.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
 
-    # Decode projections that run on the packed-weight kernel: where it beats
-    # the library GEMM on MI355X at 128 rows (the MLP, the GDN / attention /
-    # memory output and memory-writer down projections, the lm_head).  The
-    # q/k/v/z/b/a-sized projections (N ~ 9k-12k) and the memory k/v (N = 2048)
-    # stay on hipBLASLt, which is as fast or faster there.
-    PACKED = ("mlp_gate_up", "mlp_down", "w_out", "w_o", "m_o", "writer_down")
+    # Decode projections on the packed-weight kernels (proj.hip), which beat
+    # the library GEMM on MI355X at 128 rows for every projection of the step
+    # but the anchor memory's 2048-wide k/v (15.3 against 13.3 us): the MLP,
+    # the GDN input and output, the attention q/k/v and output, the memory's
+    # fused input, writer-down and output projections, and the lm_head.
+    # Prefill (more rows) keeps the row-major weights.
+    PACKED = ("mlp_gate_up", "mlp_down", "w_in", "w_out", "w_qkv", "w_o", "m_in", "writer_down", "m_o")
 
     def prepare(self, model):
         """Packed copies of the decode projection weights (``name + "@packed"``
