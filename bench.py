@@ -280,25 +280,49 @@ def bench_model_decode(steps, warmup, cpu, batch=128):
 
 def cpu_model_decode(batch, budget_s=20.0, max_steps=32, single_thread=True):
     """Decode steps of the same model shape on the host cores: float32 weights
-    (tiled N(0, 0.02) block), every slot live at position 128, the oracle's
-    recurrence / anchor memory / sampler / bookkeeping.  Timed until
-    ``budget_s`` of CPU work (at least one step after one warm-up step) on
-    ``cpu_threads()`` threads; then one more step on a single thread."""
+    (tiled N(0, 0.02) block), every slot live in steady state (positions in
+    [1100, 2100): every SWA ring full, every anchor slot committed, the rows
+    at staggered points of their commit chunk, so a sixty-fourth of them
+    commit at each step), the oracle's recurrence / ring attention / sampler /
+    bookkeeping and the batched anchor read and commit of the reference's
+    torch branch.  Timed until ``budget_s`` of CPU work (at least one step
+    after one warm-up step) on ``cpu_threads()`` threads; then one more step
+    on a single thread."""
     from yanchor_amd import runtime as rt
+    from yanchor_amd import workloads
 
     threads = cpu_threads()
     torch.set_num_threads(threads)
     host = cpu_host_info()
     cfg = rt.ModelConfig()
-    from oracle.model_ops import HostOps
+    from oracle.model_ops import BatchedHostOps
 
-    m = rt.Model(cfg, batch=batch, device="cpu", seed=0, ops=HostOps(), dtype=torch.float32, init="tiled")
+    m = rt.Model(cfg, batch=batch, device="cpu", seed=0, ops=BatchedHostOps(), dtype=torch.float32, init="tiled")
     gen = torch.Generator().manual_seed(5)
     tokens = torch.randint(0, cfg.vocab, (batch,), generator=gen)
-    positions = torch.full((batch,), 128, dtype=torch.long)
+    positions = torch.randint(1100, 2100, (batch,), generator=gen)
     valid = torch.ones(batch, dtype=torch.bool)
     ids = torch.arange(batch)
     seen = torch.zeros(batch, cfg.vocab, dtype=torch.bool)
+    w = cfg.swa_window
+    slot = torch.arange(w)
+    for i, L in enumerate(m.layers):
+        if L["kind"] == "gdn":
+            continue
+        # the ring holds the last w positions before each row's: slot s the
+        # latest p' < p with p' % w == s
+        last = (positions - 1)[:, None]
+        ring_pos = (last - (last - slot[None]) % w).to(torch.int32)
+        m.ring_pos[i].copy_(ring_pos[:, None, :].expand_as(m.ring_pos[i]))
+        m.ring_k[i].normal_(generator=gen)
+        m.ring_v[i].normal_(generator=gen)
+        st = workloads.anchor_state(batch, cfg.kv_heads, cfg.memory_capacity, cfg.memory_chunk, cfg.head_dim,
+                                    p_live=1.0, dtype=torch.float32, seed=100 + i)
+        st.count.copy_(positions % cfg.memory_chunk)
+        st.total.copy_(positions)
+        for f in ("keys", "values", "scores", "positions", "pending_keys", "pending_values", "pending_scores",
+                  "count", "total"):
+            getattr(m.memory[i], f).copy_(getattr(st, f))
 
     def step(i):
         logits = m.decode_step(tokens, positions + i, valid)
@@ -317,8 +341,9 @@ def cpu_model_decode(batch, budget_s=20.0, max_steps=32, single_thread=True):
             break
     res = {"value": batch * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
            "sample": f"{n} decode steps x {batch} live slots of the same 36-layer model in float32 on "
-                     f"{threads} host threads (every op from the oracle: recurrence, anchor memory, ring attention, "
-                     f"layer glue, sampler), {el:.1f} s; "
+                     f"{threads} host threads, steady state (positions 1100-2100: full SWA rings, full anchor "
+                     f"memories, staggered commits; every op from the oracle: recurrence, batched anchor read and "
+                     f"commit, ring attention, layer glue, sampler), {el:.1f} s; "
                      "refill prefill excluded as in the GPU figure",
            "host": host}
     if single_thread:

@@ -17,6 +17,11 @@ Restates, from the reference:
 * ``sequence``           the prefill read / write continuing a state,
                          IndependentGQAMemory._sequence, modeling_yanchor.py:
                          178-275 (given every token's key / value)
+* ``committed_read_batched`` / ``commit_decode_batched``  the same decode read
+                         and commit over the whole batch at once, the
+                         reference's torch branch of _decode
+                         (modeling_yanchor.py:283-313): the host CPU baseline's
+                         form, equal to the per-row restatements above
 
 Ordering contract of every Top-K here: candidates are ordered by
 (score descending, position ascending with invalid last, candidate index
@@ -33,7 +38,9 @@ a single token references the committed slots; ``exclusive_prefix_topk``
 is checked against the O(n^2) definition "Top-K of every earlier block";
 ``sequence`` (prefix Top-K of blocks, merged with the committed slots, one
 indexed read per block) equals the token-by-token committed_read /
-commit_decode sequence it replaces -- reads, and the state it leaves.
+commit_decode sequence it replaces -- reads, and the state it leaves; the
+batched read and commit equal the per-row ones (the state bit for bit) over
+staggered commits.
 """
 from __future__ import annotations
 
@@ -230,6 +237,58 @@ def commit_decode(key, value, scores, active, chunk, state: MemoryState, indices
         else:
             state.count[b] = c + 1
         state.total[b] += 1
+    return state
+
+
+def committed_read_batched(query, state: MemoryState, dtype=torch.float32):
+    """committed_read for every row at once (the torch branch of _decode,
+    modeling_yanchor.py:283-290): one batched product per group, masked
+    logits, the zero-logit sink, in ``dtype``."""
+    bq, _, h, d = query.shape
+    g = state.keys.shape[1]
+    q = query[:, 0].to(dtype).reshape(bq, g, h // g, d)
+    logits = q @ state.keys.to(dtype).transpose(-1, -2) / math.sqrt(d)           # [B, G, R, K]
+    logits = logits.masked_fill((state.positions < 0)[:, :, None, :], -math.inf)
+    w = torch.nn.functional.pad(logits, (0, 1), value=0.0).softmax(-1)[..., :-1]
+    return (w @ state.values.to(dtype)).reshape(bq, 1, h, d).to(query.dtype)
+
+
+def commit_decode_batched(key, value, scores, active, chunk, state: MemoryState):
+    """commit_decode for every row at once, IN PLACE (the torch branch of
+    _decode, modeling_yanchor.py:291-313): the push into pending slot
+    ``count``, then one select_topk over committed + pending candidates of
+    every row whose chunk fills."""
+    bsz = key.shape[0]
+    g_n, cap, d = state.keys.shape[1:]
+    rows = torch.arange(bsz)[:, None]
+    grp = torch.arange(g_n)[None]
+    slot = state.count.long()[:, None]
+    act = active.bool()
+    for target, src in ((state.pending_keys, key[:, 0]), (state.pending_values, value[:, 0])):
+        target[rows, grp, slot] = torch.where(act[:, None, None], src.to(target.dtype), target[rows, grp, slot])
+    state.pending_scores[rows, grp, slot] = torch.where(act[:, None], scores[:, 0].to(state.pending_scores.dtype),
+                                                        state.pending_scores[rows, grp, slot])
+    nxt = state.count.long() + act.long()
+    commit = nxt == chunk
+    cr = commit.nonzero()[:, 0]
+    if cr.numel():
+        n = cr.numel()
+        pos = state.positions[cr].long()
+        ref = torch.arange(cap).expand(n, g_n, cap).masked_fill(pos < 0, -1)
+        base = (state.total[cr] - state.count[cr]).long()      # position of pending entry 0
+        pj = torch.arange(chunk)
+        cand_s = torch.cat((state.scores[cr], state.pending_scores[cr][:, :, :chunk]), -1)
+        cand_p = torch.cat((pos, (base[:, None, None] + pj).expand(n, g_n, chunk)), -1)
+        cand_r = torch.cat((ref, (cap + pj).expand(n, g_n, chunk)), -1)
+        ss, pp, rr = select_topk(cand_s, cand_p, cand_r, cap)
+        take = rr.clamp_min(0)[..., None].expand(n, g_n, cap, d)
+        for target, pend in ((state.keys, state.pending_keys), (state.values, state.pending_values)):
+            src = torch.cat((target[cr], pend[cr][:, :, :chunk]), 2)
+            target[cr] = src.gather(2, take)
+        state.scores[cr] = ss.to(state.scores.dtype)
+        state.positions[cr] = pp.to(state.positions.dtype)
+    state.count.copy_(torch.where(commit, torch.zeros_like(nxt), nxt).to(state.count.dtype))
+    state.total.add_(act.to(state.total.dtype))
     return state
 
 

@@ -26,6 +26,11 @@ arithmetic of the decode step taken from ``oracle/``:
 
 Arguments and results follow the runtime's ops (the same names, layouts and
 return tuples); tensors are float32 on the host.
+
+``BatchedHostOps`` is the same with the anchor read and commit over the whole
+batch at once (``committed_read_batched`` / ``commit_decode_batched``, the
+reference's torch branch, pinned equal to the per-row forms): the host CPU
+baseline's ops.
 """
 from __future__ import annotations
 
@@ -240,3 +245,17 @@ class HostOps:
     @staticmethod
     def bookkeeping(*args, **kw):
         slots.decode_state_update_torch(*args, **kw)
+
+
+class BatchedHostOps(HostOps):
+    """HostOps with the anchor memory's decode read and commit batched over
+    the rows, as the reference's torch branch runs them
+    (modeling_yanchor.py:283-313)."""
+
+    @staticmethod
+    def memory_read(q, state, valid=None, head_gate=None):
+        return gate_read(anchor.committed_read_batched(q, state, dtype=torch.float32), valid, head_gate)
+
+    @staticmethod
+    def memory_commit(key, value, scores, active, chunk, state):
+        anchor.commit_decode_batched(key, value, scores, active, chunk, state)

@@ -135,6 +135,38 @@ def test_commit_keeps_topk_of_union():
         assert torch.equal(st.keys[0, grp], src[tr[0].clamp_min(0)])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_batched_read_and_commit_equal_per_row(dtype):
+    """The batched decode read / commit (the host CPU baseline's form) equal
+    the per-row restatements over 40 steps: rows at staggered points of their
+    chunk (so a few commit at every step), some slots dead, tied scores, one
+    row inactive at times.  The state is bit-exact; the reads agree to the
+    float32 rounding of the batched products."""
+    b, g, cap, c, d, h = 6, 2, 16, 8, 16, 4
+    st = workloads.anchor_state(b, g, cap, c, d, dtype=dtype, seed=21, p_live=0.6)
+    st.count.copy_(torch.tensor([0, 3, 7, 5, 6, 1]))
+    st.total.copy_(4 * cap + st.count)
+    one = MemoryState(*(getattr(st, f).clone() for f in MemoryState.__dataclass_fields__))
+    two = MemoryState(*(getattr(st, f).clone() for f in MemoryState.__dataclass_fields__))
+    gen = torch.Generator().manual_seed(22)
+    commits = 0
+    for step in range(40):
+        q = torch.randn(b, 1, h, d, generator=gen).to(dtype)
+        key, val = torch.randn(b, 1, g, d, generator=gen).to(dtype), torch.randn(b, 1, g, d, generator=gen).to(dtype)
+        sc = torch.randint(-2, 3, (b, 1, g), generator=gen).float()   # integer scores: ties
+        active = torch.ones(b, dtype=torch.bool)
+        active[step % b] = step % 3 != 0
+        commits += int(((one.count + active.long()) == c).sum())
+        r1 = anchor.committed_read(q, one, dtype=torch.float32)
+        r2 = anchor.committed_read_batched(q, two)
+        assert torch.allclose(r1.float(), r2.float(), rtol=1e-5, atol=1e-6 if dtype == torch.float32 else 1e-2)
+        anchor.commit_decode(key, val, sc, active, c, one)
+        anchor.commit_decode_batched(key, val, sc, active, c, two)
+        for f in MemoryState.__dataclass_fields__:
+            assert torch.equal(getattr(one, f), getattr(two, f)), (step, f)
+    assert commits >= 25
+
+
 def test_prefix_topk_recursion():
     b, nb, g, c, cap = 1, 5, 2, 4, 6
     gen = torch.Generator().manual_seed(12)
