@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY.  Nothing in the product (``yanchor_amd``) imports,
 calls or links anything here.  The only permitted users are ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``, and
-they use it strictly as the checker (or as the timed CPU path), never as the
+they use it strictly to check results (or as the timed CPU path), never as the
 thing that is measured or shipped.
 
 Each module restates one part of the reference's algorithm on the CPU and cites
