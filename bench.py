@@ -728,13 +728,14 @@ def bench_sampling(steps, warmup, cpu, batch=128):
 
 # The decode step's projections at the 4B shape: (name, N, K, epilogue), the
 # packed weights' shapes per layer (GDN: input and output; attention: q/k/v
-# and output; anchor memory: fused input, writer down, k/v, output; MLP:
-# gate/up with the silu epilogue and down; lm_head) with their calls per step.
+# and output; anchor memory: fused input, fused k/v ([u | act] against
+# [W_kv | W_kv W_down]), output; MLP: gate/up with the silu epilogue and down;
+# lm_head) with their calls per step.
 DECODE_PROJECTIONS = [("mlp_gate_up", 19456, 2560, "silu", 36), ("mlp_down", 2560, 9728, "defer", 36),
                       ("gdn_in", 16448, 2560, "", 27), ("gdn_out", 2560, 4096, "defer", 27),
                       ("attn_qkv", 10240, 2560, "", 9), ("attn_o", 2560, 4096, "", 9),
-                      ("memory_in", 9280, 2560, "", 9), ("memory_writer_down", 2560, 2560, "residual", 9),
-                      ("memory_kv", 2048, 2560, "", 9), ("memory_o", 2560, 4096, "defer", 9),
+                      ("memory_in", 9280, 2560, "", 9), ("memory_kv_fused", 2048, 5120, "", 9),
+                      ("memory_o", 2560, 4096, "defer", 9),
                       ("lm_head", 151936, 2560, "", 1)]
 
 

@@ -563,15 +563,16 @@ int yh_decode_inputs(const int64_t* tokens, const int64_t* positions, const void
  * part [S, N, D] in slice order), x = bf16(x + proj_residual) when given (the
  * projection's own residual add), then as yh_rmsnorm with `residual`.  With
  * w2 / out2 (both or neither) the same row is also normed with the weight w2
- * into out2 (contiguous [N, D]): the decode layers whose memory path norms
- * the layer input with its own weight.  The reduce of the projection and the
+ * into out2 ([N, D], rows out2_stride >= D elements apart; ABI 103 added the
+ * stride): the decode layers whose memory path norms the layer input with its
+ * own weight.  The reduce of the projection and the
  * norms after it in one launch (no reference counterpart: the reference runs
  * the projection, the adds and each norm as separate ops).
  */
 int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual, int64_t proj_residual_stride,
                         const void* residual, void* residual_out, const void* w, void* out, int64_t out_stride,
                         int64_t N, int64_t D, float eps, int plus_one, const void* w2, void* out2,
-                        yh_stream_t stream);
+                        int64_t out2_stride, yh_stream_t stream);
 
 /*
  * GDN decode prologue for B rows of the packed projection proj [B, proj_stride]

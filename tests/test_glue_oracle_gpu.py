@@ -261,12 +261,15 @@ def test_window_attend_dead_blocks(gpu, g, h):
 @pytest.mark.parametrize("b", [1, 128])
 def test_memory_decode_matches_oracle(gpu, b):
     """The anchor-memory projections of one decode token (input norm, the
-    fused q / admission / writer projection, memory_prologue, the writer's
-    down projection with its residual, k / v projection, k norm + RoPE)
-    against _query_scores and _write_kv restated from the same weights."""
+    fused q / admission / writer projection, memory_prologue with the
+    writer's activation, the k / v projection of [u | act] against
+    [W_kv | W_kv W_down], k norm + RoPE) against _query_scores and _write_kv
+    restated from the same weights in the reference's order (writer down
+    projection, residual, then k / v)."""
     cfg = rt.ModelConfig(layers=4)
     m = rt.Model(cfg, batch=b, device=gpu, seed=31)
     L = m.layers[3]
+    assert "m_kv@fused" in L                 # the bf16 model takes the fused k / v projection
     gen = torch.Generator(device=gpu).manual_seed(32)
     for name in ("m_q_norm", "m_k_norm", "m_in_norm"):
         L[name].copy_((torch.randn(L[name].shape, device=gpu, generator=gen) * 0.1).to(L[name].dtype))

@@ -314,6 +314,12 @@ def test_memory_prologue(gpu, b):
     q2, gate2, scores2, act = layers.memory_prologue(*args2, act_offset=h * d + a, act_width=wi)
     assert torch.equal(act, layers.silu_mul(proj2[:, h * d + a:]))
     assert torch.equal(q1, q2) and torch.equal(gate1, gate2) and torch.equal(scores1, scores2)
+    # ... written into given rows (the [u | act] row of the fused memory k/v
+    # projection), the columns before them untouched
+    row = torch.full((b, 384 + wi), 7.0, dtype=torch.bfloat16, device=gpu)
+    _, _, _, act2 = layers.memory_prologue(*args2, act_offset=h * d + a, act_width=wi, act_out=row[:, 384:])
+    assert act2.data_ptr() == row[:, 384:].data_ptr() and torch.equal(row[:, 384:], act)
+    assert bool((row[:, :384] == 7.0).all())
 
 
 @pytest.mark.parametrize("split", [1, 4])
@@ -384,6 +390,10 @@ def test_rmsnorm_second_weight(gpu, split):
     assert torch.equal(got, ref) and torch.equal(got_h, ref_h)
     assert torch.equal(got_u, layers.rmsnorm(ref_h, w2, 1e-6))
     ulp_check(got_u, TorchGlue.rmsnorm(ref_h, w2, 1e-6))
+    if split > 1:   # the second output as the first columns of wider rows, the same values
+        p = layers.linear(x, pw, split_k=split, defer=True)
+        _, _, wide_u = layers.rmsnorm(p, w, 1e-6, residual=h, w2=w2, w2_row=2560 + 512)
+        assert wide_u.stride(0) == 2560 + 512 and torch.equal(wide_u, got_u)
 
 
 @pytest.mark.parametrize("b", [1, 5, 128])

@@ -45,7 +45,7 @@ def test_every_declared_entry_point_has_a_binding():
 
 
 def test_abi_version(lib):
-    assert lib.yh_abi_version() >= 100
+    assert lib.yh_abi_version() == _native.ABI_VERSION
 
 
 def test_invalid_arguments_return_error_without_device_work(lib):

@@ -12,6 +12,8 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libyanchor_amd.so"
+# yh_abi_version() of the library these signatures describe (103: yh_rmsnorm_partials takes out2_stride)
+ABI_VERSION = 103
 
 F32, BF16, F16, I32, I64, U8 = 0, 1, 2, 3, 4, 5
 DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16,
@@ -54,7 +56,7 @@ SIGNATURES: dict[str, list] = {
                          _f32, _p],
     "yh_gdn_decode_fused": [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _f32, _i32, _f32, _p],
-    "yh_rmsnorm_partials": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _p],
+    "yh_rmsnorm_partials": [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _i64, _p],
     "yh_ring_write": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                       _f32, _p],
     "yh_memory_prologue": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
@@ -114,6 +116,10 @@ def lib() -> ctypes.CDLL:
         handle.yh_last_error.restype = ctypes.c_char_p
         handle.yh_last_error.argtypes = []
         handle.yh_abi_version.restype = ctypes.c_int
+        found = handle.yh_abi_version()
+        if found != ABI_VERSION:
+            raise RuntimeError(f"yanchor_amd native library at {LIB_PATH} has ABI version {found}, these bindings "
+                               f"expect {ABI_VERSION}; rebuild it with `python -m yanchor_amd.build`")
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = ctypes.c_int

@@ -54,8 +54,9 @@ struct NormArgs {
   const uint16_t* w;
   uint16_t* out;
   int64_t out_stride;
-  const uint16_t* w2;      // optional second weight: out2 [rows, D]
+  const uint16_t* w2;      // optional second weight: out2 [rows, D], rows out2_stride apart
   uint16_t* out2;
+  int64_t out2_stride;
   int D, plus_one;
   float eps;
 };
@@ -149,7 +150,7 @@ __global__ void __launch_bounds__(SG > 8 ? 512 : kNormMaxThreads) rmsnorm_kernel
     const uint16_t* w2h = reinterpret_cast<const uint16_t*>(&w2v);
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = tobf(v[j] * r * (a.plus_one ? 1.f + bf(w2h[j]) : bf(w2h[j])));
-    *reinterpret_cast<uint4*>(a.out2 + row * D + c * 8) = *reinterpret_cast<const uint4*>(o);
+    *reinterpret_cast<uint4*>(a.out2 + row * a.out2_stride + c * 8) = *reinterpret_cast<const uint4*>(o);
   }
 }
 
@@ -473,7 +474,7 @@ extern "C" int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual,
   if (N == 0) return YH_OK;
   NormArgs a{static_cast<const uint16_t*>(x), x_stride, nullptr, 0, 0, nullptr, 0,
              static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
-             static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), out_stride, nullptr, nullptr,
+             static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), out_stride, nullptr, nullptr, 0,
              (int)D, plus_one, eps};
   launch_rmsnorm(a, N, static_cast<hipStream_t>(stream));
   YH_CHECK_LAUNCH("rmsnorm");
@@ -511,14 +512,15 @@ extern "C" int yh_decode_inputs(const int64_t* tokens, const int64_t* positions,
 extern "C" int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual,
                                    int64_t proj_residual_stride, const void* residual, void* residual_out,
                                    const void* w, void* out, int64_t out_stride, int64_t N, int64_t D, float eps,
-                                   int plus_one, const void* w2, void* out2, yh_stream_t stream) {
+                                   int plus_one, const void* w2, void* out2, int64_t out2_stride, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(w && N >= 0 && S >= 1 && (N == 0 || (part && out)), "rmsnorm_partials: bad arguments");
   YH_CHECK_ARG(!out2 == !w2, "rmsnorm_partials: out2 and w2 come together");
   YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= kNormMaxD, "rmsnorm_partials: D must be a multiple of 8 up to %d",
                kNormMaxD);
-  YH_CHECK_ARG(out_stride % 8 == 0 && (!proj_residual || proj_residual_stride % 8 == 0),
-               "rmsnorm_partials: strides must be multiples of 8 elements");
+  YH_CHECK_ARG(out_stride % 8 == 0 && (!proj_residual || proj_residual_stride % 8 == 0) &&
+                   (!out2 || (out2_stride >= D && out2_stride % 8 == 0)),
+               "rmsnorm_partials: strides must be multiples of 8 elements (out2_stride >= D)");
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w) |
                  reinterpret_cast<uintptr_t>(proj_residual) | reinterpret_cast<uintptr_t>(residual) |
                  reinterpret_cast<uintptr_t>(residual_out) | reinterpret_cast<uintptr_t>(w2) |
@@ -528,7 +530,7 @@ extern "C" int yh_rmsnorm_partials(const float* part, int64_t S, const void* pro
   NormArgs a{nullptr, 0, part, N * D, (int)S, static_cast<const uint16_t*>(proj_residual), proj_residual_stride,
              static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
              static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), out_stride,
-             static_cast<const uint16_t*>(w2), static_cast<uint16_t*>(out2), (int)D, plus_one, eps};
+             static_cast<const uint16_t*>(w2), static_cast<uint16_t*>(out2), out2_stride, (int)D, plus_one, eps};
   launch_rmsnorm(a, N, static_cast<hipStream_t>(stream));
   YH_CHECK_LAUNCH("rmsnorm_partials");
   return YH_OK;

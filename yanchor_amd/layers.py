@@ -39,14 +39,16 @@ def _normed_rows(m, d, dtype, device):
     return torch.empty(m, d, dtype=dtype, device=device)
 
 
-def rmsnorm(x, w, eps, residual=None, plus_one=True, w2=None):
+def rmsnorm(x, w, eps, residual=None, plus_one=True, w2=None, w2_row=None):
     """Qwen3.5 RMSNorm over the last dim (x / rms(x) * (1 + w)).  With
     ``residual``: s = x + residual is formed first and ``(norm(s), s)`` is
     returned (the fused residual RMSNorm, runtime/model/inference_kernels.py:
     1767-1797).  ``w2``: the same row normed with a second weight is appended
-    to the result (one launch when x is split-K partials)."""
+    to the result (one launch when x is split-K partials); with ``w2_row`` (>=
+    D, x split-K partials) it is the first D columns of rows ``w2_row`` wide,
+    the rest left for the caller."""
     if isinstance(x, Partials):
-        return _rmsnorm_partials(x, w, eps, residual, plus_one, w2)
+        return _rmsnorm_partials(x, w, eps, residual, plus_one, w2, w2_row)
     if w2 is not None:
         first = rmsnorm(x, w, eps, residual, plus_one)
         if residual is None:
@@ -109,12 +111,17 @@ def decode_inputs(tokens, positions, embed, w, inv_freq, eps, *, ring_stride, wi
     return h, xn, cos, sin, rows, valid
 
 
-def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None):
+def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None, w2_row=None):
     _bf16(w, residual, p.residual, w2)
     m, d = p.shape
     N.require_device(p.part, w, residual, p.residual, w2)
     out = _normed_rows(m, d, torch.bfloat16, p.device)
-    out2 = None if w2 is None else torch.empty(m, d, dtype=torch.bfloat16, device=p.device)
+    out2 = None
+    if w2 is not None:
+        row = d if w2_row is None else int(w2_row)
+        if row < d or row % 8:
+            raise ValueError("w2_row must be at least D and a multiple of 8")
+        out2 = torch.empty(m, row, dtype=torch.bfloat16, device=p.device)[:, :d]
     res_out = None
     if residual is not None:
         residual = residual.contiguous()
@@ -124,7 +131,7 @@ def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None):
         r1 = r1.contiguous()
     N.call("yh_rmsnorm_partials", p.part.data_ptr(), p.part.shape[0], N.ptr(r1), 0 if r1 is None else r1.stride(0),
            N.ptr(residual), N.ptr(res_out), w.data_ptr(), out.data_ptr(), out.stride(0), m, d, float(eps),
-           int(plus_one), N.ptr(w2), N.ptr(out2), N.stream_of(p.part))
+           int(plus_one), N.ptr(w2), N.ptr(out2), 0 if out2 is None else out2.stride(0), N.stream_of(p.part))
     res = (out,) if residual is None else (out, res_out)
     res = res if out2 is None else res + (out2,)
     return res[0] if len(res) == 1 else res
@@ -262,14 +269,15 @@ def ring_write(k, v, w, cos, sin, rows, positions, ring_k, ring_v, ring_pos, rot
 
 
 def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w, gate_b, adm_up,
-                    rotary_dim, eps, act_offset=None, act_width=0):
+                    rotary_dim, eps, act_offset=None, act_width=0, act_out=None):
     """Query, read gate and admission scores of the anchor memory for one
     decode token per row from the fused projection proj [B, P] (query heads
     first, admission features at ``feat_offset``): returns q [B, H, 128] bf16,
     gate [B, H] float, scores [B, G] float (modeling_yanchor.py:167-176).
     With ``act_offset`` (the writer's gate columns, its up columns right
     after them, ``act_width`` each) the same launch also returns the writer's
-    activation silu(gate) * up [B, act_width] bf16 as a fourth result."""
+    activation silu(gate) * up [B, act_width] bf16 as a fourth result, written
+    into ``act_out`` when given (rows with unit last stride, any row stride)."""
     _bf16(proj, q_norm_w)
     b, ps = proj.shape
     if proj.stride(1) != 1:
@@ -282,7 +290,15 @@ def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, re
     q = torch.empty(b, heads, 128, dtype=proj.dtype, device=dev)
     gate = torch.empty(b, heads, dtype=torch.float32, device=dev)
     scores = torch.empty(b, g, dtype=torch.float32, device=dev)
-    act = None if act_offset is None else torch.empty(b, act_width, dtype=proj.dtype, device=dev)
+    act = None
+    if act_offset is not None:
+        if act_out is not None:
+            if act_out.shape != (b, act_width) or act_out.dtype != proj.dtype or act_out.stride(1) != 1:
+                raise ValueError("act_out must be [B, act_width] in the projection dtype with unit last stride")
+            N.require_device(act_out)
+            act = act_out
+        else:
+            act = torch.empty(b, act_width, dtype=proj.dtype, device=dev)
     N.call("yh_memory_prologue", proj.data_ptr(), proj.stride(0), feat_offset, q_norm_w.data_ptr(), N.ptr(cs),
            N.ptr(sn), f32[0].data_ptr(), f32[1].data_ptr(), f32[2].data_ptr(), f32[3].data_ptr(), q.data_ptr(),
            gate.data_ptr(), scores.data_ptr(), b, heads, 128, g, n_features, rotary_dim, float(eps),

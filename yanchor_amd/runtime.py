@@ -94,14 +94,15 @@ class HipOps:
     # Fused decode-layer neighbours: HIP kernels for bf16 activations (the
     # served configuration).  A float32 model (used to pin the cache logic
     # without bf16 rounding) runs the torch formulations of the same layers.
-    def rmsnorm(self, x, w, eps, residual=None, w2=None):
+    def rmsnorm(self, x, w, eps, residual=None, w2=None, w2_row=None):
         """x may be a projection's deferred split-K partials (``linear(...,
         defer=True)``): the reduce, the projection's residual, the residual
         add and the norms then run as one launch.  ``w2``: the row normed
-        with a second weight is appended to the result."""
+        with a second weight is appended to the result (with ``w2_row``, as
+        the first columns of rows that wide when one launch makes it)."""
         if x.dtype != torch.bfloat16:
             return TorchGlue.rmsnorm(x, w, eps, residual, w2)
-        return self.layers.rmsnorm(x, w, eps, residual=residual, w2=w2)
+        return self.layers.rmsnorm(x, w, eps, residual=residual, w2=w2, w2_row=w2_row)
 
     def gdn_prep(self, proj, conv_state, conv_w, a_log, dt_bias, **kw):
         if proj.dtype != torch.bfloat16:
@@ -134,17 +135,35 @@ class HipOps:
 
     # Decode projections on the packed-weight kernels (proj.hip), which beat
     # the library GEMM on MI355X at 128 rows for every projection of the step
-    # but the anchor memory's 2048-wide k/v (15.3 against 13.3 us): the MLP,
-    # the GDN input and output, the attention q/k/v and output, the memory's
-    # fused input, writer-down and output projections, and the lm_head.
-    # Prefill (more rows) keeps the row-major weights.
-    PACKED = ("mlp_gate_up", "mlp_down", "w_in", "w_out", "w_qkv", "w_o", "m_in", "writer_down", "m_o")
+    # but the anchor memory's 2048-wide k/v (2048 x 5120 fused: 19.2 against
+    # 15.3 us): the MLP, the GDN input and output, the attention q/k/v and
+    # output, the memory's fused input and output projections, and the
+    # lm_head.  Prefill (more rows) keeps the row-major weights.
+    PACKED = ("mlp_gate_up", "mlp_down", "w_in", "w_out", "w_qkv", "w_o", "m_in", "m_o")
+
+    # The anchor memory's key / value of a decode token in one projection:
+    # kv = (u + write_down(act)) . W_kv^T = [u | act] . [W_kv | W_kv W_down]^T
+    # (modeling_yanchor.py:147-166), the product W_kv W_down formed once in
+    # float32 and rounded to the weights' dtype.  The reference rounds the
+    # writer's output and the sum z to bf16 before the k / v projection; this
+    # form rounds the product weight instead.  It takes two dependent
+    # projections and a split-K reduce off the memory path, the longer of an
+    # attention layer's two streams.  The row [u | act] is one buffer: the
+    # norm writes u into its first columns and the prologue act into the rest.
+    # bf16 weights only: a float32 model keeps the reference's order, so its
+    # committed positions match the reference's exactly (a reassociation moves
+    # near-tied admission scores at float32 rounding).
+    fused_memory_kv = True
 
     def prepare(self, model):
         """Packed copies of the decode projection weights (``name + "@packed"``
         in each layer dict, ``model.lm_head_packed``); the row-major weights
-        stay for prefill."""
+        stay for prefill.  Attention layers also get ``m_kv@fused``, the fused
+        memory k/v weight of the decode step."""
         for L in model.layers:
+            if L.get("kind") == "attn" and "m_kv" in L and "writer_down" in L and L["m_kv"].dtype == torch.bfloat16:
+                fused = (L["m_kv"].float() @ L["writer_down"].float()).to(L["m_kv"].dtype)
+                L["m_kv@fused"] = torch.cat((L["m_kv"], fused), dim=1).contiguous()
             for name in self.PACKED:
                 pair = name == "mlp_gate_up"   # [gate; up]: tiles interleaved for the fused silu * up
                 if name in L and self.layers.PackedWeight.fits(L[name], pair):
@@ -182,16 +201,21 @@ class HipOps:
                  rotary_dim, eps)
 
     def memory_prologue_act(self, proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale, gate_w,
-                            gate_b, adm_up, rotary_dim, eps, act_offset, act_width):
+                            gate_b, adm_up, rotary_dim, eps, act_offset, act_width, act_out=None):
         """memory_prologue plus the writer's silu(gate) * up in the same
-        launch (bf16; otherwise the two separate ops)."""
+        launch (bf16; otherwise the two separate ops), into ``act_out`` when
+        given."""
         if proj.dtype != torch.bfloat16:
             out = TorchGlue.memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale,
                                             gate_w, gate_b, adm_up, rotary_dim, eps)
-            return out + (self.silu_mul(proj[:, act_offset: act_offset + 2 * act_width]),)
+            act = self.silu_mul(proj[:, act_offset: act_offset + 2 * act_width])
+            if act_out is not None:
+                act_out.copy_(act)
+                act = act_out
+            return out + (act,)
         return self.layers.memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, read_scale,
                                            gate_w, gate_b, adm_up, rotary_dim, eps, act_offset=act_offset,
-                                           act_width=act_width)
+                                           act_width=act_width, act_out=act_out)
 
     def gdn_decode(self, q, k, v, g, beta, state):
         o, _ = self.gdn.recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=state,
@@ -635,16 +659,37 @@ class Model:
         qd, ad = H * D, c.admission_rank
         args = (proj, H, qd, ad, L["m_q_norm"], cos, sin, L["read_scale"], L["read_gate_w"], L["read_gate_b"],
                 L["adm_up"], c.rotary_dim, c.rms_eps)
-        if hasattr(ops, "memory_prologue_act"):   # the writer's activation in the same launch
-            q, gate, scores, act = ops.memory_prologue_act(*args, qd + ad, c.writer_intermediate)
+        if getattr(ops, "fused_memory_kv", False) and "m_kv@fused" in L:
+            ua = self._memory_row(u)
+            q, gate, scores, _ = ops.memory_prologue_act(*args, qd + ad, c.writer_intermediate,
+                                                         act_out=ua[:, c.hidden:])
+            kv = ops.linear(ua, L["m_kv@fused"])
         else:
-            q, gate, scores = ops.memory_prologue(*args)
-            act = ops.silu_mul(proj[:, qd + ad:])
-        zz = ops.linear(act, L["writer_down"], L.get("writer_down@packed"), residual=u)
-        kv = ops.linear(zz, L["m_kv"], L.get("m_kv@packed"))
+            if hasattr(ops, "memory_prologue_act"):   # the writer's activation in the same launch
+                q, gate, scores, act = ops.memory_prologue_act(*args, qd + ad, c.writer_intermediate)
+            else:
+                q, gate, scores = ops.memory_prologue(*args)
+                act = ops.silu_mul(proj[:, qd + ad:])
+            zz = ops.linear(act, L["writer_down"], L.get("writer_down@packed"), residual=u)
+            kv = ops.linear(zz, L["m_kv"], L.get("m_kv@packed"))
         key = ops.head_norm_rope(kv[:, : KVH * D].view(B, KVH, D), L["m_k_norm"], cos, sin, c.rotary_dim,
                                  c.rms_eps)
         return q, gate, key, kv[:, KVH * D:].reshape(B, KVH, D), scores
+
+    def _memory_row(self, u):
+        """The [u | act] rows of the fused memory k/v projection: u in place
+        when the norm that made it left room for act (rows hidden +
+        writer_intermediate wide), else a copy into a new buffer."""
+        c = self.cfg
+        width = c.hidden + c.writer_intermediate
+        b = u.shape[0]
+        st = u.untyped_storage()
+        if (u.stride(1) == 1 and u.stride(0) == width and u.storage_offset() == 0 and
+                st.nbytes() >= b * width * u.element_size()):
+            return u.as_strided((b, width), (width, 1))
+        ua = torch.empty(b, width, dtype=u.dtype, device=u.device)
+        ua[:, : c.hidden].copy_(u)
+        return ua
 
     def _attn_decode(self, i, L, xn, hidden, positions, cos, sin, valid, ring_rows, u=None):
         """SWA + anchor-memory mixer for one token per slot.  xn is the
@@ -714,7 +759,8 @@ class Model:
             nl = self.layers[i + 1] if i + 1 < len(self.layers) else None
             mlp = self._mlp(L, xn, defer=True)
             if nl is not None and nl["kind"] != "gdn":   # the memory path's own norm of the same row
-                xn, h, u = ops.rmsnorm(mlp, nl["in_norm"], c.rms_eps, residual=h, w2=nl["m_in_norm"])
+                room = {"w2_row": c.hidden + c.writer_intermediate} if "m_kv@fused" in nl else {}
+                xn, h, u = ops.rmsnorm(mlp, nl["in_norm"], c.rms_eps, residual=h, w2=nl["m_in_norm"], **room)
             else:
                 xn, h = ops.rmsnorm(mlp, self.final_norm if nl is None else nl["in_norm"], c.rms_eps, residual=h)
         logits = ops.linear(xn, self.lm_head, self.lm_head_packed)
