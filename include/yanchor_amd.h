@@ -352,9 +352,10 @@ int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split
  * the packed copy serves the decode step, the row-major one everything else).
  *
  * yh_linear_pack: w [N, K] bf16 row-major -> packed [N * K] bf16 with
- *   packed[((T * K/32 + kb) * 64 + l) * 8 + e] = w[16 T + l % 16][32 kb + 8 (l / 16) + e]
+ *   packed[((kb * N/16 + T) * 64 + l) * 8 + e] = w[16 T + l % 16][32 kb + 8 (l / 16) + e]
  *   (column tile T of 16 outputs, K block kb of 32; lane l of a 16x16x32 MFMA
- *   B operand).  N % 16 == 0, K % 32 == 0.  With pair_halves the tiles
+ *   B operand; K blocks outermost since ABI 104, tile-major before).
+ *   N % 16 == 0, K % 32 == 0.  With pair_halves the tiles
  *   alternate between the row halves of w (tile 2j = rows 16j.., tile 2j+1 =
  *   rows N/2 + 16j..; N % 32 == 0): the layout of a [gate; up] MLP weight for
  *   the silu epilogue.

@@ -210,13 +210,21 @@ def test_linear_strided_rows(gpu):
     ulp_check(layers.linear(x, w), (x.float() @ w.float().t()).to(torch.bfloat16))
 
 
-def test_pack_layout(gpu):
-    """Packed order: column tile of 16, K block of 32, lane l = (K quarter, column)."""
-    n, k = 48, 256
-    w = rnd(n, k, dev=gpu, seed=30)
-    pw = layers.PackedWeight(w)
-    want = w.view(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
-    assert torch.equal(pw.data, want)
+@pytest.mark.parametrize("pair", [False, True])
+def test_pack_layout(gpu, pair):
+    """yh_linear_pack's documented order, bit for bit: K blocks of 32
+    outermost, then the N/16 column tiles, then the 64 lanes of a 16x16x32
+    MFMA B operand (lane l = 16 q + r holds row 16 T + r, K 32 kb + 8 q ..
+    + 8); paired halves interleave the tiles of the two row halves."""
+    n, k = 96, 256
+    w = rnd(n, k, dev=gpu, seed=5)
+    pw = layers.PackedWeight(w, pair_halves=pair)
+    src = w.cpu()
+    if pair:   # tile 2j = rows 16j.., tile 2j+1 = rows n/2 + 16j..
+        src = src.view(2, n // 32, 16, k).permute(1, 0, 2, 3).reshape(n, k)
+    want = src.view(n // 16, 16, k // 32, 4, 8).permute(2, 0, 3, 1, 4).reshape(-1)
+    torch.cuda.synchronize()
+    assert torch.equal(pw.data.cpu(), want)
     with pytest.raises(ValueError):
         layers.PackedWeight(rnd(32, 96, dev=gpu, seed=31))           # K not a multiple of 128
 

@@ -12,8 +12,9 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libyanchor_amd.so"
-# yh_abi_version() of the library these signatures describe (103: yh_rmsnorm_partials takes out2_stride)
-ABI_VERSION = 103
+# yh_abi_version() of the library these signatures describe (103: yh_rmsnorm_partials takes
+# out2_stride; 104: yh_linear_pack lays K blocks outermost)
+ABI_VERSION = 104
 
 F32, BF16, F16, I32, I64, U8 = 0, 1, 2, 3, 4, 5
 DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16,

@@ -2,7 +2,8 @@
 // workgroup: out[M, N] = x[M, K] . W[N, K]^T for M <= 128 rows, bf16 in,
 // fp32 accumulation (the decode step's projections: modeling_yanchor.py:
 // 147-176 and the Qwen3.5 GDN / attention / MLP projections of the
-// transformers wheel).  W is in the MFMA fragment order of yh_linear_pack.
+// transformers wheel).  W is in the MFMA fragment order of yh_linear_pack
+// (K blocks outermost, the N/16 column tiles of a block side by side).
 //
 // Workgroup = NCG column groups x KP K parts = NCG * KP waves.  A column
 // group owns 32 output columns (two 16-column MFMA tiles), so every x
@@ -109,6 +110,7 @@ struct WaveLoc {
   int last;               // last K block of the slice
   int part;               // K part of this wave
   int col, quad;
+  int64_t bstride;        // elements from one K block of a tile to the next (N/16 fragments)
 };
 
 // Block I of the wave's BPW blocks in phase ph at unroll position U: A
@@ -133,8 +135,8 @@ __device__ __forceinline__ void block_step(Regs<MT, WD>& g, const uint16_t* cur,
   __builtin_amdgcn_sched_barrier(0);
   const int tn = ph * BPW + I + WD;  // the wave's block WD ahead
   const int blk = min(v.kb0 + (tn / BPW) * KP * BPW + v.part + KP * (tn % BPW), v.last);
-  g.wr[slot][0] = ldw(v.wp[0] + static_cast<int64_t>(blk) * 512);
-  g.wr[slot][1] = ldw(v.wp[1] + static_cast<int64_t>(blk) * 512);
+  g.wr[slot][0] = ldw(v.wp[0] + static_cast<int64_t>(blk) * v.bstride);
+  g.wr[slot][1] = ldw(v.wp[1] + static_cast<int64_t>(blk) * v.bstride);
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -255,10 +257,11 @@ __global__ void __launch_bounds__(64 * NCG * KP) proj_kernel(ProjArgs a) {
   v.quad = lane >> 4;
   v.kb0 = ph0 * C::PB;
   v.last = v.kb0 + max(nph, 1) * C::PB - 1;
+  v.bstride = static_cast<int64_t>(a.N / 16) * 512;
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const int T = min(static_cast<int>(blockIdx.x) * 2 * NCG + cg * 2 + ct, a.N / 16 - 1);
-    v.wp[ct] = a.w + static_cast<int64_t>(T) * (a.K / 32) * 512 + lane * 8;
+    v.wp[ct] = a.w + static_cast<int64_t>(T) * 512 + lane * 8;
   }
   Regs<MT, WD> g;
   u32x4v xr[C::XV];
@@ -270,8 +273,8 @@ __global__ void __launch_bounds__(64 * NCG * KP) proj_kernel(ProjArgs a) {
 #pragma unroll
     for (int s = 0; s < WD; ++s) {
       const int blk = min(v.kb0 + (s / BPW) * KP * BPW + v.part + KP * (s % BPW), v.last);
-      g.wr[s][0] = ldw(v.wp[0] + static_cast<int64_t>(blk) * 512);
-      g.wr[s][1] = ldw(v.wp[1] + static_cast<int64_t>(blk) * 512);
+      g.wr[s][0] = ldw(v.wp[0] + static_cast<int64_t>(blk) * v.bstride);
+      g.wr[s][1] = ldw(v.wp[1] + static_cast<int64_t>(blk) * v.bstride);
     }
     store_x<C>(xs, xr);
     sync_lds();
