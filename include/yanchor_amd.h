@@ -562,7 +562,12 @@ int yh_decode_inputs(const int64_t* tokens, const int64_t* positions, const void
  * yh_rmsnorm whose input row is a split-K projection still in fp32 partials
  * (yh_linear_packed with defer_reduce): x = bf16(sum over the S planes of
  * part [S, N, D] in slice order), x = bf16(x + proj_residual) when given (the
- * projection's own residual add), then as yh_rmsnorm with `residual`.  With
+ * projection's own residual add), then as yh_rmsnorm with `residual`.  The
+ * projection's residual may instead be a second projection's partials part2
+ * [S2, N, D] (ABI 105; NULL = none; not with proj_residual; S + S2 <= 64),
+ * summed in slice order and rounded to bf16 first, as a separate reduce would
+ * store it: the attention layer's output projection joining the memory
+ * output projection without a reduce launch of its own.  With
  * w2 / out2 (both or neither) the same row is also normed with the weight w2
  * into out2 ([N, D], rows out2_stride >= D elements apart; ABI 103 added the
  * stride): the decode layers whose memory path norms the layer input with its
@@ -571,7 +576,8 @@ int yh_decode_inputs(const int64_t* tokens, const int64_t* positions, const void
  * the projection, the adds and each norm as separate ops).
  */
 int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual, int64_t proj_residual_stride,
-                        const void* residual, void* residual_out, const void* w, void* out, int64_t out_stride,
+                        const float* part2, int64_t S2, const void* residual, void* residual_out, const void* w,
+                        void* out, int64_t out_stride,
                         int64_t N, int64_t D, float eps, int plus_one, const void* w2, void* out2,
                         int64_t out2_stride, yh_stream_t stream);
 

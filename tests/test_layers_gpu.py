@@ -404,6 +404,34 @@ def test_rmsnorm_second_weight(gpu, split):
         assert wide_u.stride(0) == 2560 + 512 and torch.equal(wide_u, got_u)
 
 
+@pytest.mark.parametrize("s1,s2", [(12, 12), (3, 13), (8, 2), (16, 16)])
+def test_rmsnorm_two_deferred_projections(gpu, s1, s2):
+    """A projection's partials with a second projection's partials as its
+    residual (the attention layer's memory and attention output projections):
+    bit for bit the second reduced on its own (its bf16 store), then the first
+    with that as its store residual, then the norms, w2 included.
+    reduce_partials equals the projection's own reduce."""
+    x1, x2 = rnd(128, 4096, dev=gpu, seed=100), rnd(128, 4096, dev=gpu, seed=101)
+    pw1 = layers.PackedWeight(rnd(2560, 4096, dev=gpu, scale=0.02, seed=102))
+    pw2 = layers.PackedWeight(rnd(2560, 4096, dev=gpu, scale=0.02, seed=103))
+    h = rnd(128, 2560, dev=gpu, seed=104)
+    w, w2 = rnd(2560, dev=gpu, scale=0.1, seed=105), rnd(2560, dev=gpu, scale=0.1, seed=106)
+    out = layers.linear(x2, pw2, split_k=s2)
+    p2 = layers.linear(x2, pw2, split_k=s2, defer=True)
+    assert isinstance(p2, layers.Partials)
+    p2 = layers.Partials(p2.part.clone(), None)      # one stream, one workspace: keep the planes
+    assert torch.equal(layers.reduce_partials(p2), out)
+    p1 = layers.linear(x1, pw1, split_k=s1, defer=True)
+    got = layers.rmsnorm(layers.Partials(p1.part, p2), w, 1e-6, residual=h, w2=w2)
+    torch.cuda.synchronize()
+    got = [t.clone() for t in got]
+    ref = layers.rmsnorm(layers.linear(x1, pw1, split_k=s1, residual=out, defer=True), w, 1e-6, residual=h, w2=w2)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    with pytest.raises(ValueError):                  # a residual's partials carry no residual of their own
+        layers.rmsnorm(layers.Partials(p1.part, layers.Partials(p2.part, out)), w, 1e-6)
+
+
 @pytest.mark.parametrize("b", [1, 5, 128])
 def test_gdn_decode_fused_equals_three_launches(gpu, b, monkeypatch):
     """Conv update + gated delta rule + gated norm in one launch give bit for

@@ -37,7 +37,9 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
 // x may instead come as S fp32 split-K partial planes of a projection (part
 // [S, rows, D]; x = bf16(sum in slice order), plus an optional residual of the
 // projection: x = bf16(x + res1)), so the projection's reduce needs no launch
-// of its own.
+// of its own.  The projection's residual may itself be the S2 partial planes
+// of a second projection (part2, summed in slice order and rounded to bf16,
+// as a separate reduce would store it).
 constexpr int kNormMaxThreads = 1024;
 constexpr int kNormMaxD = 8 * kNormMaxThreads;
 
@@ -59,6 +61,8 @@ struct NormArgs {
   int64_t out2_stride;
   int D, plus_one;
   float eps;
+  const float* part2;      // [S2, rows, D]: the projection's residual as partials, or null
+  int S2;
 };
 
 // Block-wide fp32 sum (blockDim a multiple of 64, at most 1024).
@@ -71,6 +75,11 @@ __device__ __forceinline__ float block_sum(float x) {
   float t = 0.f;
   for (int i = 0; i < nw; ++i) t += part[i];
   return t;
+}
+
+__device__ __forceinline__ void set_f4(float* acc, float4 lo, float4 hi) {
+  acc[0] = lo.x; acc[1] = lo.y; acc[2] = lo.z; acc[3] = lo.w;
+  acc[4] = hi.x; acc[5] = hi.y; acc[6] = hi.z; acc[7] = hi.w;
 }
 
 __device__ __forceinline__ void add_f4(float* acc, float4 lo, float4 hi) {
@@ -93,29 +102,41 @@ __global__ void __launch_bounds__(SG > 8 ? 512 : kNormMaxThreads) rmsnorm_kernel
     if constexpr (SG > 0) {
       if (a.res1) r1a = *reinterpret_cast<const uint4*>(a.res1 + row * a.res1_stride + c * 8);
       const float* pp = a.part + row * D + c * 8;
-      float acc[8];
-      for (int s0 = 0; s0 < a.S; s0 += SG) {  // SG planes in flight, added in slice order
+      const float* pp2 = a.part2 ? a.part2 + row * D + c * 8 : pp;
+      // planes 0 .. S-1 of part, then S .. S+S2-1 of part2: SG in flight,
+      // each set added in its slice order
+      const int T = a.S + (a.part2 ? a.S2 : 0);
+      float acc[8], acc2[8];
+      for (int s0 = 0; s0 < T; s0 += SG) {
         float4 lo[SG], hi[SG];
 #pragma unroll
-        for (int q = 0; q < SG; ++q)
-          if (s0 + q < a.S) {
-            lo[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * a.plane);
-            hi[q] = *reinterpret_cast<const float4*>(pp + (s0 + q) * a.plane + 4);
+        for (int q = 0; q < SG; ++q) {
+          const int vp = s0 + q;
+          if (vp < T) {
+            const float* src = vp < a.S ? pp + vp * a.plane : pp2 + (vp - a.S) * a.plane;
+            lo[q] = *reinterpret_cast<const float4*>(src);
+            hi[q] = *reinterpret_cast<const float4*>(src + 4);
           }
-        if (s0 == 0) {
-          acc[0] = lo[0].x; acc[1] = lo[0].y; acc[2] = lo[0].z; acc[3] = lo[0].w;
-          acc[4] = hi[0].x; acc[5] = hi[0].y; acc[6] = hi[0].z; acc[7] = hi[0].w;
-        } else {
-          add_f4(acc, lo[0], hi[0]);
         }
 #pragma unroll
-        for (int q = 1; q < SG; ++q)
-          if (s0 + q < a.S) add_f4(acc, lo[q], hi[q]);
+        for (int q = 0; q < SG; ++q) {
+          const int vp = s0 + q;
+          if (vp >= T) break;
+          if (vp == 0) set_f4(acc, lo[q], hi[q]);
+          else if (vp < a.S) add_f4(acc, lo[q], hi[q]);
+          else if (vp == a.S) set_f4(acc2, lo[q], hi[q]);
+          else add_f4(acc2, lo[q], hi[q]);
+        }
       }
       uint16_t xh[8];
-      const uint16_t* r1h = reinterpret_cast<const uint16_t*>(&r1a);
+      uint16_t* r1h = reinterpret_cast<uint16_t*>(&r1a);
+      if (a.part2) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xh[j] = a.res1 ? tobf(bf(tobf(acc[j])) + bf(r1h[j])) : tobf(acc[j]);
+        for (int j = 0; j < 8; ++j) r1h[j] = tobf(acc2[j]);
+      }
+      const bool add1 = a.res1 || a.part2;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xh[j] = add1 ? tobf(bf(tobf(acc[j])) + bf(r1h[j])) : tobf(acc[j]);
       xa = *reinterpret_cast<const uint4*>(xh);
     } else {
       xa = *reinterpret_cast<const uint4*>(a.x + row * a.x_stride + c * 8);
@@ -157,9 +178,10 @@ __global__ void __launch_bounds__(SG > 8 ? 512 : kNormMaxThreads) rmsnorm_kernel
 void launch_rmsnorm(const NormArgs& a, int64_t N, hipStream_t st) {
   const unsigned threads = static_cast<unsigned>((a.D / 8 + kWave - 1) / kWave * kWave);
   const dim3 grid(static_cast<unsigned>(N));
+  const int planes = a.S + (a.part2 ? a.S2 : 0);
   if (!a.part) hipLaunchKernelGGL(rmsnorm_kernel<0>, grid, dim3(threads), 0, st, a);
-  else if (a.S <= 4) hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(threads), 0, st, a);
-  else if (a.S <= 8 || threads > 512) hipLaunchKernelGGL(rmsnorm_kernel<8>, grid, dim3(threads), 0, st, a);
+  else if (planes <= 4) hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(threads), 0, st, a);
+  else if (planes <= 8 || threads > 512) hipLaunchKernelGGL(rmsnorm_kernel<8>, grid, dim3(threads), 0, st, a);
   else hipLaunchKernelGGL(rmsnorm_kernel<16>, grid, dim3(threads), 0, st, a);
 }
 
@@ -475,7 +497,7 @@ extern "C" int yh_rmsnorm(const void* x, int64_t x_stride, const void* residual,
   NormArgs a{static_cast<const uint16_t*>(x), x_stride, nullptr, 0, 0, nullptr, 0,
              static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
              static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), out_stride, nullptr, nullptr, 0,
-             (int)D, plus_one, eps};
+             (int)D, plus_one, eps, nullptr, 0};
   launch_rmsnorm(a, N, static_cast<hipStream_t>(stream));
   YH_CHECK_LAUNCH("rmsnorm");
   return YH_OK;
@@ -510,12 +532,15 @@ extern "C" int yh_decode_inputs(const int64_t* tokens, const int64_t* positions,
 }
 
 extern "C" int yh_rmsnorm_partials(const float* part, int64_t S, const void* proj_residual,
-                                   int64_t proj_residual_stride, const void* residual, void* residual_out,
+                                   int64_t proj_residual_stride, const float* part2, int64_t S2,
+                                   const void* residual, void* residual_out,
                                    const void* w, void* out, int64_t out_stride, int64_t N, int64_t D, float eps,
                                    int plus_one, const void* w2, void* out2, int64_t out2_stride, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(w && N >= 0 && S >= 1 && (N == 0 || (part && out)), "rmsnorm_partials: bad arguments");
   YH_CHECK_ARG(!out2 == !w2, "rmsnorm_partials: out2 and w2 come together");
+  YH_CHECK_ARG(!part2 || (!proj_residual && S2 >= 1 && S + S2 <= 64),
+               "rmsnorm_partials: part2 replaces proj_residual, with 1 <= S2 and S + S2 <= 64");
   YH_CHECK_ARG(D > 0 && D % 8 == 0 && D <= kNormMaxD, "rmsnorm_partials: D must be a multiple of 8 up to %d",
                kNormMaxD);
   YH_CHECK_ARG(out_stride % 8 == 0 && (!proj_residual || proj_residual_stride % 8 == 0) &&
@@ -524,13 +549,14 @@ extern "C" int yh_rmsnorm_partials(const float* part, int64_t S, const void* pro
   YH_CHECK_ARG(((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w) |
                  reinterpret_cast<uintptr_t>(proj_residual) | reinterpret_cast<uintptr_t>(residual) |
                  reinterpret_cast<uintptr_t>(residual_out) | reinterpret_cast<uintptr_t>(w2) |
-                 reinterpret_cast<uintptr_t>(out2)) & 15) == 0,
+                 reinterpret_cast<uintptr_t>(out2) | reinterpret_cast<uintptr_t>(part2)) & 15) == 0,
                "rmsnorm_partials: pointers must be 16-byte aligned");
   if (N == 0) return YH_OK;
   NormArgs a{nullptr, 0, part, N * D, (int)S, static_cast<const uint16_t*>(proj_residual), proj_residual_stride,
              static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(residual_out),
              static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), out_stride,
-             static_cast<const uint16_t*>(w2), static_cast<uint16_t*>(out2), out2_stride, (int)D, plus_one, eps};
+             static_cast<const uint16_t*>(w2), static_cast<uint16_t*>(out2), out2_stride, (int)D, plus_one, eps,
+             part2, part2 ? (int)S2 : 0};
   launch_rmsnorm(a, N, static_cast<hipStream_t>(stream));
   YH_CHECK_LAUNCH("rmsnorm_partials");
   return YH_OK;

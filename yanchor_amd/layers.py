@@ -112,9 +112,15 @@ def decode_inputs(tokens, positions, embed, w, inv_freq, eps, *, ring_stride, wi
 
 
 def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None, w2_row=None):
-    _bf16(w, residual, p.residual, w2)
+    r1, part2 = p.residual, None
+    if isinstance(r1, Partials):   # a second projection's partials: the residual of the first
+        if r1.shape != p.shape or r1.residual is not None:
+            raise ValueError("the residual partials must match the projection and carry no residual")
+        part2, r1 = r1.part, None
+        N.require_device(part2)
+    _bf16(w, residual, r1, w2)
     m, d = p.shape
-    N.require_device(p.part, w, residual, p.residual, w2)
+    N.require_device(p.part, w, residual, r1, w2)
     out = _normed_rows(m, d, torch.bfloat16, p.device)
     out2 = None
     if w2 is not None:
@@ -126,11 +132,10 @@ def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None, w2_row=None):
     if residual is not None:
         residual = residual.contiguous()
         res_out = torch.empty_like(residual)
-    r1 = p.residual
     if r1 is not None and (r1.stride(-1) != 1 or r1.stride(0) % 8 or r1.data_ptr() % 16):
         r1 = r1.contiguous()
     N.call("yh_rmsnorm_partials", p.part.data_ptr(), p.part.shape[0], N.ptr(r1), 0 if r1 is None else r1.stride(0),
-           N.ptr(residual), N.ptr(res_out), w.data_ptr(), out.data_ptr(), out.stride(0), m, d, float(eps),
+           N.ptr(part2), 0 if part2 is None else part2.shape[0], N.ptr(residual), N.ptr(res_out), w.data_ptr(), out.data_ptr(), out.stride(0), m, d, float(eps),
            int(plus_one), N.ptr(w2), N.ptr(out2), 0 if out2 is None else out2.stride(0), N.stream_of(p.part))
     res = (out,) if residual is None else (out, res_out)
     res = res if out2 is None else res + (out2,)
@@ -372,13 +377,31 @@ class PackedWeight:
 class Partials:
     """A projection x . W^T (+ residual) still in S fp32 split-K planes
     ``part`` [S, M, N] in the stream's workspace: consume it with ``rmsnorm``
-    before the next projection on the same stream."""
+    (or ``reduce_partials``) before the next projection on the same stream.
+    The residual is a bf16 [M, N] tensor, None, or a second projection's
+    ``Partials`` (its own residual None), which the consumer sums and rounds
+    to bf16 first: bf16(bf16(x . W^T) + bf16(x2 . W2^T))."""
 
     def __init__(self, part, residual):
         self.part, self.residual = part, residual
         self.shape = tuple(part.shape[1:])
         self.dtype = torch.bfloat16
         self.device = part.device
+
+
+def reduce_partials(p):
+    """``p`` summed as the projection's own reduce stores it: bf16 of the
+    planes' sum in slice order, then bf16(that + residual) (yh_linear_reduce)."""
+    r = p.residual
+    if isinstance(r, Partials):
+        r = reduce_partials(r)
+    m, n = p.shape
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=p.device)
+    if r is not None and (r.stride(-1) != 1 or r.stride(0) % 4):
+        r = r.contiguous()
+    N.call("yh_linear_reduce", p.part.data_ptr(), out.data_ptr(), n, m, n, p.part.shape[0], N.ptr(r),
+           0 if r is None else r.stride(0), N.stream_of(p.part))
+    return out
 
 
 def linear(x, w, split_k=None, residual=None, defer=False):

@@ -182,6 +182,20 @@ class HipOps:
         out = F.linear(x, w)
         return out if residual is None else out + residual
 
+    def add_projections(self, a, b):
+        """a + b of two projections' results, as a projection's store adds its
+        residual: bf16(bf16(a) + bf16(b)).  Deferred split-K partials stay
+        partials for the norm that follows (``layers.Partials`` with the
+        second as its residual); otherwise each is reduced as its own store
+        would and the two are added."""
+        P = self.layers.Partials
+        if isinstance(a, P) and a.residual is None and (torch.is_tensor(b) or (
+                isinstance(b, P) and b.residual is None and b.shape == a.shape)):
+            return P(a.part, b)
+        a = self.layers.reduce_partials(a) if isinstance(a, P) else a
+        b = self.layers.reduce_partials(b) if isinstance(b, P) else b
+        return a + b
+
     def mlp_act(self, x, w, packed=None):
         """silu(x . gate^T) * (x . up^T) of the [gate; up] MLP weight: one
         launch on the packed weights (decode batch), else GEMM + silu_mul."""
@@ -695,9 +709,10 @@ class Model:
         """SWA + anchor-memory mixer for one token per slot.  xn is the
         normalised layer input, hidden the residual stream entering the layer;
         ring_rows[b] = b * kv_heads * window + positions[b] % window.  On a GPU
-        the memory path (its own norm, projections, read and commit) runs on a
-        second stream beside the SWA path; they meet at the memory output
-        projection."""
+        the memory path (its own norm, projections, read, commit and output
+        projection) runs on a second stream beside the SWA path.  The two
+        output projections meet in the norm after the layer, which sums their
+        split-K partials, so neither waits for the other stream."""
         c, B, ops = self.cfg, xn.shape[0], self.ops
         H, KVH, D = c.attn_heads, c.kv_heads, c.head_dim
         side = self._side_stream(xn)
@@ -705,7 +720,7 @@ class Model:
             main = torch.cuda.current_stream(xn.device)
             side.wait_stream(main)
             with torch.cuda.stream(side):
-                read = self._memory_path(i, L, hidden, cos, sin, valid, u)
+                mo = self._memory_out(i, L, hidden, cos, sin, valid, u)
         proj = ops.linear(xn, L["w_qkv"], L.get("w_qkv@packed"))                                    # [B, (q|gate) per head | k | v]
         hq = 2 * H * D
         qg = proj[:, :hq].view(B, H, 2 * D)
@@ -714,13 +729,21 @@ class Model:
                        cos, sin, ring_rows, positions, self.ring_k[i], self.ring_v[i], self.ring_pos[i],
                        c.rotary_dim, c.rms_eps)
         att = ops.window_attend(q[:, None], self.ring_k[i], self.ring_v[i], self.ring_pos[i], gate=qg[..., D:])
-        out = ops.linear(att.reshape(B, -1), L["w_o"], L.get("w_o@packed"))
+        out = ops.linear(att.reshape(B, -1), L["w_o"], L.get("w_o@packed"), defer=True)
         if side is None:
-            read = self._memory_path(i, L, hidden, cos, sin, valid, u)
+            mo = self._memory_out(i, L, hidden, cos, sin, valid, u)
         else:
             main.wait_stream(side)
-            read.record_stream(main)
-        return ops.linear(read.reshape(B, -1), L["m_o"], L.get("m_o@packed"), residual=out, defer=True)
+            if torch.is_tensor(mo):
+                mo.record_stream(main)
+        add = getattr(ops, "add_projections", None)
+        return add(mo, out) if add is not None else mo + out
+
+    def _memory_out(self, i, L, hidden, cos, sin, valid, u=None):
+        """The memory path and its output projection (deferred: the norm after
+        the layer sums it with the attention output projection)."""
+        read = self._memory_path(i, L, hidden, cos, sin, valid, u)
+        return self.ops.linear(read.reshape(read.shape[0], -1), L["m_o"], L.get("m_o@packed"), defer=True)
 
     def _memory_path(self, i, L, hidden, cos, sin, valid, u=None):
         """Anchor-memory read (gated) and commit of one decode token per slot."""
