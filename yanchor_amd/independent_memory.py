@@ -325,10 +325,11 @@ def sequence(query, key, value, scores, valid, chunk, state: IndependentMemorySt
 
 def ring_decode_attention(query, keys, values, positions, indices=None, gate=None):
     """Decode attention of one token over a physical ring of cached K/V slots
-    (the sliding-window decode path, reference runtime/model/
-    inference_kernels.py:555-640): softmax over the live slots (positions
-    >= 0) without the anchor sink.  query [B, 1, H, D]; keys/values
-    [NB, G, window, D]; positions int32 [NB, G, window].  With ``gate``
+    (fixed_memory_physical_ring_decode_attention, reference runtime/model/
+    inference_kernels.py:1881-1898, on the ring set up at 555-640): softmax
+    over the live slots (positions >= 0) without the anchor sink.  query
+    [B, 1, H, D]; keys/values [NB, G, window, D]; positions int32
+    [NB, G, window].  With ``gate``
     ([B, H, D], any token / head strides, unit last stride) the output is
     ``read * sigmoid(gate)`` (the gated-q output, products rounded to the
     dtype) in the same launch."""
