@@ -402,6 +402,13 @@ def test_rmsnorm_second_weight(gpu, split):
         p = layers.linear(x, pw, split_k=split, defer=True)
         _, _, wide_u = layers.rmsnorm(p, w, 1e-6, residual=h, w2=w2, w2_row=2560 + 512)
         assert wide_u.stride(0) == 2560 + 512 and torch.equal(wide_u, got_u)
+        # the decode step's [u | act] row: the norm's wide rows in place, any other u copied
+        m = rt.Model.__new__(rt.Model)
+        m.cfg = rt.ModelConfig(writer_intermediate=512)
+        row = m._memory_row(wide_u)
+        assert row.shape == (128, 2560 + 512) and row.data_ptr() == wide_u.data_ptr()
+        row = m._memory_row(got_u)
+        assert row.data_ptr() != got_u.data_ptr() and torch.equal(row[:, :2560], got_u)
 
 
 @pytest.mark.parametrize("s1,s2", [(12, 12), (3, 13), (8, 2), (16, 16)])

@@ -159,7 +159,8 @@ class HipOps:
         """Packed copies of the decode projection weights (``name + "@packed"``
         in each layer dict, ``model.lm_head_packed``); the row-major weights
         stay for prefill.  Attention layers also get ``m_kv@fused``, the fused
-        memory k/v weight of the decode step."""
+        memory k/v weight of the decode step.  These are copies: after the
+        weights change, call prepare again."""
         for L in model.layers:
             if L.get("kind") == "attn" and "m_kv" in L and "writer_down" in L and L["m_kv"].dtype == torch.bfloat16:
                 fused = (L["m_kv"].float() @ L["writer_down"].float()).to(L["m_kv"].dtype)
@@ -691,16 +692,17 @@ class Model:
         return q, gate, key, kv[:, KVH * D:].reshape(B, KVH, D), scores
 
     def _memory_row(self, u):
-        """The [u | act] rows of the fused memory k/v projection: u in place
-        when the norm that made it left room for act (rows hidden +
-        writer_intermediate wide), else a copy into a new buffer."""
+        """The [u | act] rows of the fused memory k/v projection: in place
+        when u is the first columns of a [B, hidden + writer_intermediate]
+        buffer of its own (the norm's ``w2_row`` output, whose other columns
+        hold nothing), else a copy into a new buffer."""
         c = self.cfg
         width = c.hidden + c.writer_intermediate
         b = u.shape[0]
-        st = u.untyped_storage()
-        if (u.stride(1) == 1 and u.stride(0) == width and u.storage_offset() == 0 and
-                st.nbytes() >= b * width * u.element_size()):
-            return u.as_strided((b, width), (width, 1))
+        base = u._base
+        if (base is not None and base.shape == (b, width) and base.is_contiguous() and base.dtype == u.dtype
+                and u.stride() == (width, 1) and u.data_ptr() == base.data_ptr()):
+            return base
         ua = torch.empty(b, width, dtype=u.dtype, device=u.device)
         ua[:, : c.hidden].copy_(u)
         return ua
