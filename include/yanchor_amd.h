@@ -689,7 +689,8 @@ int yh_proj_pick(int64_t M, int64_t N, int64_t K, int silu_pairs, int* config, i
 /*
  * out[M, N] = bf16(sum over s of part[s]) (+ residual, added to the bf16
  * sum): the split-K reduce of yh_linear_packed / yh_proj, slices added in
- * order.  part fp32 [S, M, N]; out rows out_stride apart.
+ * order.  part fp32 [S, M, N] (16-byte aligned); out rows out_stride apart
+ * (out and residual 8-byte aligned, strides multiples of 4 elements).
  */
 int yh_linear_reduce(const float* part, void* out, int64_t out_stride, int64_t M, int64_t N, int64_t S,
                      const void* residual, int64_t residual_stride, yh_stream_t stream);

@@ -388,6 +388,10 @@ extern "C" int yh_linear_reduce(const float* part, void* out, int64_t out_stride
   YH_CHECK_ARG(!residual || (residual_stride >= N && residual_stride % 4 == 0), "linear_reduce: bad residual");
   if (M == 0) return YH_OK;
   YH_CHECK_ARG(part && out, "linear_reduce: null pointer");
+  // partials are read 16 bytes at a time, the output and residual 8
+  YH_CHECK_ARG((reinterpret_cast<uintptr_t>(part) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(residual) & 7) == 0,
+               "linear_reduce: part must be 16-byte aligned, out and residual 8-byte aligned");
   const int64_t quads = M * N / 4;
   hipLaunchKernelGGL(linear_reduce_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), part, static_cast<uint16_t*>(out), out_stride, (int)M, (int)N,

@@ -397,7 +397,7 @@ def reduce_partials(p):
         r = reduce_partials(r)
     m, n = p.shape
     out = torch.empty(m, n, dtype=torch.bfloat16, device=p.device)
-    if r is not None and (r.stride(-1) != 1 or r.stride(0) % 4):
+    if r is not None and (r.stride(-1) != 1 or r.stride(0) % 4 or r.data_ptr() % 8):   # 4-element reads
         r = r.contiguous()
     N.call("yh_linear_reduce", p.part.data_ptr(), out.data_ptr(), n, m, n, p.part.shape[0], N.ptr(r),
            0 if r is None else r.stride(0), N.stream_of(p.part))
