@@ -106,3 +106,24 @@ def test_sampler_refuses_top_k_past_the_vocabulary(lib):
     for k in (100, 81):
         with pytest.raises(ValueError, match="exceeds the vocabulary"):
             ik.topk_sample(scores, ids, 0, seed=1, temperature=1.0, top_k=k, top_p=1.0, mode=ik.SAMPLE_TORCH)
+
+
+def test_norm_and_reduce_argument_checks(lib):
+    """yh_rmsnorm_partials: a second projection's partials replace the
+    projection residual and count toward the 64-plane limit; out2 rows hold
+    at least D.  yh_linear_reduce: its 16- and 8-byte accesses need aligned
+    pointers.  All refused before any device work."""
+    fake = ctypes.c_void_p(256)
+
+    def norm(proj_res, part2, s, s2, out2_stride=2560):
+        return lib.yh_rmsnorm_partials(fake, s, proj_res, 2560, part2, s2, None, None, fake, fake, 2560, 4, 2560,
+                                       1e-6, 1, fake, fake, out2_stride, None)
+    assert norm(fake, fake, 12, 12) == -1 and b"part2 replaces proj_residual" in lib.yh_last_error()
+    assert norm(None, fake, 40, 25) == -1 and b"S + S2 <= 64" in lib.yh_last_error()
+    assert norm(None, fake, 12, 0) == -1 and b"1 <= S2" in lib.yh_last_error()
+    assert norm(None, None, 12, 0, out2_stride=2048) == -1 and b"out2_stride >= D" in lib.yh_last_error()
+    odd = ctypes.c_void_p(256 + 8)
+    assert lib.yh_linear_reduce(odd, fake, 2560, 4, 2560, 12, None, 0, None) == -1
+    assert b"aligned" in lib.yh_last_error()
+    assert lib.yh_linear_reduce(fake, ctypes.c_void_p(256 + 2), 2560, 4, 2560, 12, None, 0, None) == -1
+    assert lib.yh_linear_reduce(fake, fake, 2560, 4, 2560, 12, ctypes.c_void_p(256 + 4), 2560, None) == -1
