@@ -372,7 +372,8 @@ int64_t yh_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t split
  *   split (columns per workgroup, waves) is yh_proj_pick's for the shape;
  *   the output rows (and the residual's) are written 16 bytes at a time and
  *   must be 16-byte aligned.
- *   Requirements: 0 <= M <= 128, N % 16 == 0, K % 128 == 0.
+ *   Requirements: 0 <= M <= 256 (past 128 rows, one configuration with
+ *   256-row tiles), N % 16 == 0, K % 128 == 0.
  */
 int yh_linear_pack(const void* w, void* packed, int64_t N, int64_t K, int pair_halves, yh_stream_t stream);
 int yh_linear_packed(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride, int64_t M,
@@ -664,7 +665,7 @@ int yh_memory_prologue(const void* proj, int64_t proj_stride, int64_t feat_offse
 /*
  * Decode projection on packed weights with a selectable work split
  * (configuration `config`, 0 <= config < yh_proj_config_count()): out[M, N] =
- * x[M, K] . W[N, K]^T, M <= 128, the weights in yh_linear_pack's fragment
+ * x[M, K] . W[N, K]^T, M <= 256 (M > 128: configuration 0 only), the weights in yh_linear_pack's fragment
  * order, the epilogues of yh_linear_packed (residual, silu pairs).  No
  * counterpart in the reference: the reference's decode projections are
  * torch.nn.functional.linear calls (modeling_yanchor.py:147-176 and the

@@ -229,7 +229,8 @@ def test_pack_layout(gpu, pair):
         layers.PackedWeight(rnd(32, 96, dev=gpu, seed=31))           # K not a multiple of 128
 
 
-@pytest.mark.parametrize("m,n,k", [(128, 2560, 4096), (128, 19456, 2560), (128, 2560, 9728), (1, 16, 128),
+@pytest.mark.parametrize("m,n,k", [(256, 2560, 9728), (256, 10240, 2560), (200, 2576, 2560), (129, 19456, 2560),
+                                   (128, 2560, 4096), (128, 19456, 2560), (128, 2560, 9728), (1, 16, 128),
                                    (37, 192, 384), (64, 2048, 2560), (100, 2576, 2560), (17, 4096, 1024)])
 def test_linear_packed_matches_fp32_reference(gpu, m, n, k):
     """fp32-accumulated product rounded once to bf16, as F.linear (1 bf16 ulp)."""
@@ -347,7 +348,8 @@ def test_linear_packed_residual(gpu, split):
     assert (got != ref).float().mean().item() <= 0.05
 
 
-@pytest.mark.parametrize("m,i,k", [(128, 9728, 2560), (37, 256, 384), (1, 32, 128)])
+@pytest.mark.parametrize("m,i,k", [(256, 9728, 2560), (130, 256, 384), (128, 9728, 2560), (37, 256, 384),
+                                   (1, 32, 128)])
 def test_linear_silu_matches_gemm_then_silu_mul(gpu, m, i, k):
     """The MLP activation from the paired packing equals F.linear followed by
     the silu_mul formulation (to 1 bf16 ulp of the products, which the
@@ -366,15 +368,17 @@ def test_linear_silu_matches_gemm_then_silu_mul(gpu, m, i, k):
     assert (got != ref).float().mean().item() <= 0.05
 
 
-@pytest.mark.parametrize("with_res,split", [(False, 8), (True, 8), (True, 3), (True, 13), (False, 32)])
-def test_deferred_split_k_into_rmsnorm_is_exact(gpu, with_res, split):
+@pytest.mark.parametrize("with_res,split,m", [(False, 8, 128), (True, 8, 128), (True, 3, 128), (True, 13, 128),
+                                             (False, 32, 128), (True, 12, 256), (False, 5, 200)])
+def test_deferred_split_k_into_rmsnorm_is_exact(gpu, with_res, split, m):
     """A projection whose split-K reduce is left to the following RMSNorm
     gives bit for bit what the reduce kernel + RMSNorm give (slice counts on
-    both sides of the in-flight plane groups of 4, 8 and 16)."""
-    x = rnd(128, 4096, dev=gpu, seed=90)
+    both sides of the in-flight plane groups of 4, 8 and 16; 256-row tiles
+    past 128 rows)."""
+    x = rnd(m, 4096, dev=gpu, seed=90)
     pw = layers.PackedWeight(rnd(2560, 4096, dev=gpu, scale=0.02, seed=91))
-    r = rnd(128, 2560, dev=gpu, seed=92) if with_res else None
-    h = rnd(128, 2560, dev=gpu, seed=93)
+    r = rnd(m, 2560, dev=gpu, seed=92) if with_res else None
+    h = rnd(m, 2560, dev=gpu, seed=93)
     w = rnd(2560, dev=gpu, scale=0.1, seed=94)
     p = layers.linear(x, pw, split_k=split, residual=r, defer=True)
     assert isinstance(p, layers.Partials) and p.part.shape[0] > 1

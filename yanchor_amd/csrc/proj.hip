@@ -1,5 +1,5 @@
 // Decode projection on packed weights, generalised over the work split of a
-// workgroup: out[M, N] = x[M, K] . W[N, K]^T for M <= 128 rows, bf16 in,
+// workgroup: out[M, N] = x[M, K] . W[N, K]^T for M <= 256 rows, bf16 in,
 // fp32 accumulation (the decode step's projections: modeling_yanchor.py:
 // 147-176 and the Qwen3.5 GDN / attention / MLP projections of the
 // transformers wheel).  W is in the MFMA fragment order of yh_linear_pack
@@ -33,7 +33,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxRows = 128;
+constexpr int kMaxRows = 256;
 
 struct ProjArgs {
   const uint16_t* x;   // [M, K], row stride xs
@@ -355,8 +355,15 @@ void launch_mt(int id, const ProjArgs& a, int64_t col_blocks, int S, hipStream_t
   }
 }
 
+// Past 128 rows only configuration 0 runs, with 256-row tiles (8 waves at
+// 250 VGPRs, 136 KiB of LDS; the other configurations' registers or x
+// phases do not fit).  At M = 256 it beats hipBLASLt on the decode
+// projections: 29.5 against 40.9 us for 2560 x 9728 (S = 12), 17.1 against
+// 21.5 for 2560 x 4096, 28.5 against 36.5 for 9280 x 2560 (S = 2), 44.7
+// against 46.4 for 16448 x 2560; even for 151936 x 2560.
 void launch_id(int id, const ProjArgs& a, int64_t col_blocks, int S, hipStream_t st) {
-  if (a.M <= 32) launch_mt<2>(id, a, col_blocks, S, st);
+  if (a.M > 128) launch_cfg<16, 4, 2, 2, 2>(a, col_blocks, S, st);
+  else if (a.M <= 32) launch_mt<2>(id, a, col_blocks, S, st);
   else if (a.M <= 64) launch_mt<4>(id, a, col_blocks, S, st);
   else launch_mt<8>(id, a, col_blocks, S, st);
 }
@@ -366,7 +373,14 @@ void launch_id(int id, const ProjArgs& a, int64_t col_blocks, int S, hipStream_t
 // tiles restage x less often per weight byte); a projection narrower than
 // the chip splits K instead, over at most 16 slices of at least two phases.
 void pick(int64_t M, int64_t N, int64_t K, int silu, int* cfg, int* split) {
-  (void)M;
+  if (M > 128) {  // configuration 0 only, K split as below for narrow projections
+    const int64_t blocks = (N + 32 * kCfgs[0].ncg - 1) / (32 * kCfgs[0].ncg), phases = K / phase_k(0);
+    *cfg = 0;
+    *split = blocks < 128 && !silu
+                 ? static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({256 / blocks, phases / 2, 16})))
+                 : 1;
+    return;
+  }
   auto usable = [&](int id) { return K % phase_k(id) == 0; };
   int best = -1;
   int64_t best_blocks = 0;
@@ -412,6 +426,7 @@ extern "C" int yh_proj(const void* x, int64_t x_stride, const void* w_packed, vo
   YH_CHECK_ARG(config >= 0 && config < kNumCfgs, "proj: unknown configuration %d", config);
   const int pk = phase_k(config), cols = 32 * kCfgs[config].ncg;
   YH_CHECK_ARG(M >= 0 && M <= kMaxRows, "proj: M must be in [0, %d]", kMaxRows);
+  YH_CHECK_ARG(M <= 128 || config == 0, "proj: more than 128 rows run on configuration 0 only");
   YH_CHECK_ARG(N > 0 && N % 16 == 0 && (!silu_pairs || N % 32 == 0),
                "proj: N must be a positive multiple of 16 (32 with the silu epilogue)");
   YH_CHECK_ARG(K > 0 && K % pk == 0, "proj: K must be a positive multiple of %d for configuration %d", pk, config);

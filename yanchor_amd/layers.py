@@ -34,7 +34,7 @@ _ROW_PAD = 256
 
 
 def _normed_rows(m, d, dtype, device):
-    if m <= 128 and d % 8 == 0:
+    if m <= 256 and d % 8 == 0:
         return torch.empty(m, d + _ROW_PAD, dtype=dtype, device=device)[:, :d]
     return torch.empty(m, d, dtype=dtype, device=device)
 
@@ -315,7 +315,7 @@ def memory_prologue(proj, heads, feat_offset, n_features, q_norm_w, cos, sin, re
 def linear_silu(x, w):
     """The MLP activation F.silu(x . gate^T) * (x . up^T) in bf16 (torch
     rounding points kept) from a [gate; up] weight packed with pair_halves:
-    x [M, K] bf16 (M <= 128) -> [M, N/2]."""
+    x [M, K] bf16 (M <= 256) -> [M, N/2]."""
     if not isinstance(w, PackedWeight) or not w.pair_halves:
         raise ValueError("linear_silu takes a PackedWeight packed with pair_halves")
     _bf16(x)
@@ -405,7 +405,7 @@ def reduce_partials(p):
 
 
 def linear(x, w, split_k=None, residual=None, defer=False):
-    """out = x . w^T for a decode batch (x [M, K] bf16 with M <= 128, w [N, K]
+    """out = x . w^T for a decode batch (x [M, K] bf16 with M <= 256, w [N, K]
     bf16 or a PackedWeight): torch.nn.functional.linear without bias on the
     skinny-projection kernels; with ``residual`` ([M, N] bf16, unit last
     stride) out = bf16(x . w^T) + residual.  The split-K workspace is cached

@@ -134,7 +134,9 @@ class HipOps:
         return self.layers.head_norm_rope(x, w, cos, sin, rotary_dim, eps, **kw)
 
     # Decode projections on the packed-weight kernels (proj.hip), which beat
-    # the library GEMM on MI355X at 128 rows for every projection of the step
+    # the library GEMM on MI355X at 128 rows (and at 256, the long-horizon
+    # batch, for all but the fused k/v and the MLP gate/up, within 3 % there)
+    # for every projection of the step
     # but the anchor memory's 2048-wide k/v (2048 x 5120 fused: 19.2 against
     # 15.3 us): the MLP, the GDN input and output, the attention q/k/v and
     # output, the memory's fused input and output projections, and the
@@ -174,11 +176,11 @@ class HipOps:
 
     def linear(self, x, w, packed=None, residual=None, defer=False):
         """out = x . w^T (+ residual, added to the bf16 product): the
-        packed-weight kernel for a decode batch (bf16, <= 128 rows) when a
+        packed-weight kernel for a decode batch (bf16, <= 256 rows) when a
         packed copy exists, torch (hipBLASLt) otherwise.  ``defer``: the
         result is only ever fed to ``rmsnorm``, which may then do the split-K
         reduce itself."""
-        if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128:
+        if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 256:
             return self.layers.linear(x, packed, residual=residual, defer=defer)
         out = F.linear(x, w)
         return out if residual is None else out + residual
@@ -200,7 +202,7 @@ class HipOps:
     def mlp_act(self, x, w, packed=None):
         """silu(x . gate^T) * (x . up^T) of the [gate; up] MLP weight: one
         launch on the packed weights (decode batch), else GEMM + silu_mul."""
-        if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 128:
+        if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 256:
             return self.layers.linear_silu(x, packed)
         return self.silu_mul(F.linear(x, w))
 
