@@ -179,9 +179,13 @@ class HipOps:
         packed-weight kernel for a decode batch (bf16, <= 256 rows) when a
         packed copy exists, torch (hipBLASLt) otherwise.  ``defer``: the
         result is only ever fed to ``rmsnorm``, which may then do the split-K
-        reduce itself."""
+        reduce itself.  Past 128 rows a K-split projection whose reduce would
+        need a launch of its own stays on hipBLASLt (at 256 rows, 9280 x 2560:
+        36.5 us against 28.5 + 14.5 for the split and its reduce)."""
         if packed is not None and x.dtype == torch.bfloat16 and x.ndim == 2 and x.shape[0] <= 256:
-            return self.layers.linear(x, packed, residual=residual, defer=defer)
+            m = x.shape[0]
+            if m <= 128 or defer or self.layers.N.lib().yh_linear_packed_split(m, *packed.shape) == 1:
+                return self.layers.linear(x, packed, residual=residual, defer=defer)
         out = F.linear(x, w)
         return out if residual is None else out + residual
 
