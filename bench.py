@@ -722,7 +722,7 @@ def bench_sampling(steps, warmup, cpu, batch=128):
                                    "T 0.6, penalty 1.5, 6 rotating sets", "global_batch": batch, "seq_len": 1,
                        "parallelism": "single GPU"},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "topk_segment_kernel + "
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "topk_wide_kernel + "
                          "sample_rows_kernel", "bytes_per_launch": nbytes, "avg_launch_us": kernel_ms * 1e3}}
 
 

@@ -427,7 +427,9 @@ int yh_topk_sample(const void* scores, int dtype, int64_t row_stride, const uint
                    float* out_values, int64_t* out_indices, void* workspace, int64_t workspace_bytes, int64_t B,
                    int64_t V, yh_stream_t stream);
 
-/* Workspace bytes yh_topk_sample needs, and its vocabulary split. */
+/* Workspace bytes yh_topk_sample needs, and its vocabulary split into
+ * 8192-element segments (bf16 rows of 16-byte runs with top_k <= 32 take half
+ * as many segments of 16384, within the same workspace). */
 int64_t yh_topk_workspace_bytes(int64_t B, int64_t V, int64_t top_k);
 void yh_topk_segments(int64_t V, int64_t top_k, int* n_segments, int* seg_len);
 

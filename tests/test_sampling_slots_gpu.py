@@ -160,6 +160,95 @@ def test_topk_matches_torch(gpu, b, v, k, dtype):
         assert torch.equal(idx.cpu(), order) and torch.equal(vals.cpu(), torch.gather(logits.float(), 1, order))
 
 
+def _topk_two_kernels(logits, seen, penalty, k):
+    """Top-k (values, indices) of bf16 rows on the 16384-element bf16 kernel
+    and of the same values as float32 on the 8192-element kernel."""
+    dev, b = logits.device, logits.shape[0]
+    kw = dict(seed=1, temperature=1.0, top_k=k, top_p=1.0, mode=ik.SAMPLE_FUSED, return_topk=True, seen=seen,
+              presence_penalty=penalty)
+    _, v1, i1 = ik.topk_sample(logits, torch.arange(b, device=dev), 0, **kw)
+    _, v2, i2 = ik.topk_sample(logits.float(), torch.arange(b, device=dev), 0, **kw)
+    return v1.cpu(), i1.cpu(), v2.cpu(), i2.cpu()
+
+
+def _stable_topk(adjusted, k):
+    order = torch.sort(-adjusted, dim=-1, stable=True).indices[:, :k]
+    return torch.gather(adjusted, 1, order), order
+
+
+@pytest.mark.parametrize("v", [151936, 32768, 20000, 40])
+@pytest.mark.parametrize("k", [1, 7, 20, 32])
+@pytest.mark.parametrize("density,penalty", [(0.0, 0.0), (0.01, 1.5), (0.3, 1.5), (0.3, -0.5)])
+def test_bf16_topk_kernel(gpu, v, k, density, penalty):
+    """bf16 rows with top_k <= 32 (the 16384-element kernel; the last segment
+    partial except at 32768, fewer than k thread maxima at V = 40): the same
+    lists as the float32 kernel on the same values, and the stable (value
+    desc, index asc) top k of the penalised scores."""
+    if k > v:
+        pytest.skip("k above the vocabulary")
+    b = 6
+    g = torch.Generator().manual_seed(v + k + int(density * 100))
+    logits = (torch.randn(b, v, generator=g) * 3).to(torch.bfloat16)
+    seen = torch.rand(b, v, generator=g) < density
+    v1, i1, v2, i2 = _topk_two_kernels(logits.to(gpu), seen.to(gpu), penalty, k)
+    assert torch.equal(i1, i2) and torch.equal(v1, v2)
+    rv, ri = _stable_topk(logits.float() - penalty * seen.float(), k)
+    assert torch.equal(i1, ri) and torch.equal(v1, rv)
+
+
+@pytest.mark.parametrize("k", [1, 20, 32])
+def test_bf16_topk_kernel_ties_and_specials(gpu, k):
+    """Rows built against the threshold: every value equal (with and without
+    seen elements), +-0 mixed, a few large values over a sea of equal ones,
+    the largest elements all seen (their penalised values still on top for
+    some rows), and equal maxima in more threads than the list holds."""
+    v = 40000
+    rows, seens = [], []
+    z = torch.zeros(v)
+    rows.append(z.clone()); seens.append(torch.zeros(v, dtype=torch.bool))
+    s = torch.zeros(v, dtype=torch.bool); s[::3] = True
+    rows.append(z.clone()); seens.append(s)
+    r = torch.zeros(v); r[1::2] = -0.0; r[17000] = 0.5; r[39999] = 0.5
+    rows.append(r); seens.append(torch.zeros(v, dtype=torch.bool))
+    r = torch.full((v,), 1.25); r[[5, 900, 20000, 33333]] = 4.0
+    rows.append(r); seens.append(torch.zeros(v, dtype=torch.bool))
+    g = torch.Generator().manual_seed(3)
+    r = torch.randn(v, generator=g)
+    top = torch.topk(r, 64).indices
+    s = torch.zeros(v, dtype=torch.bool); s[top] = True
+    rows.append(r); seens.append(s)
+    r = torch.randn(v, generator=g).clamp(max=1.0)
+    r[torch.randperm(v, generator=g)[:500]] = 2.0         # 500 equal maxima spread over the threads
+    rows.append(r); seens.append(torch.zeros(v, dtype=torch.bool))
+    logits = torch.stack(rows).to(torch.bfloat16)
+    seen = torch.stack(seens)
+    v1, i1, v2, i2 = _topk_two_kernels(logits.to(gpu), seen.to(gpu), 1.5, k)
+    assert torch.equal(i1, i2) and torch.equal(v1, v2)
+    rv, ri = _stable_topk(logits.float() - 1.5 * seen.float(), k)
+    assert torch.equal(i1, ri) and torch.equal(v1, rv)
+
+
+def test_bf16_topk_kernel_nan_and_seen_bytes(gpu):
+    """NaN logits (which the float maxima skip) send the segment through the
+    exact element keys: the same lists as the float32 kernel (positive NaN
+    above every number, negative NaN below).  Seen bytes other than 0 / 1
+    count as seen."""
+    b, v, k = 4, 70000, 20
+    g = torch.Generator().manual_seed(8)
+    logits = (torch.randn(b, v, generator=g) * 2).to(torch.bfloat16)
+    logits[0, 123] = float("nan")
+    logits[1, 50000] = -float("nan")
+    logits[2, [7, 40000]] = float("nan")
+    raw = (torch.rand(b, v, generator=g) < 0.2).to(torch.uint8) * torch.randint(1, 256, (b, v), generator=g,
+                                                                                dtype=torch.uint8)
+    seen = raw.view(torch.bool)                          # nonzero bytes, not only 1
+    v1, i1, v2, i2 = _topk_two_kernels(logits.to(gpu), seen.to(gpu), 1.5, k)
+    assert torch.equal(i1, i2) and torch.equal(v1.isnan(), v2.isnan())
+    assert torch.equal(v1[~v1.isnan()], v2[~v2.isnan()])
+    rv, ri = _stable_topk(logits[3:].float() - 1.5 * (raw[3:] != 0).float(), k)   # the row without NaN
+    assert torch.equal(i1[3:], ri) and torch.equal(v1[3:], rv)
+
+
 @pytest.mark.parametrize("k", [20, 32, 33])
 def test_topk_all_equal_segments(gpu, k):
     """Every element ties: the lowest k indices, for the wave threshold (k <=

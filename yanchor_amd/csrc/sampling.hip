@@ -15,10 +15,13 @@
 // the k threads whose maxima reach it can hold elements that do -- at most
 // 32 k, gathered in LDS and ranked by counting.  Elements are compared by the
 // unique key (value, -index): larger value first, lower index on equal
-// values.  Phase 2: a workgroup per row ranks the segment lists' keys by
-// counting, then draws the token.
+// values.  bf16 rows of 16-byte runs with k <= 32 (the decode step's logits)
+// take topk_wide_kernel instead: 64 elements a thread, float maxima per run,
+// the same lists.  Phase 2: a workgroup per row ranks the segment lists' keys
+// by counting, then draws the token.
 #include "common.h"
 
+#include <cmath>
 #include <mutex>
 
 namespace yh {
@@ -61,6 +64,7 @@ constexpr int kCandMax = kMaxK * kPerThread;  // 2048
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 template <int DT>
 __device__ __forceinline__ float decode_elem(uint32_t bits) {
@@ -279,6 +283,285 @@ __global__ void __launch_bounds__(kTopkThreads) topk_segment_kernel(TopkArgs a) 
     segment_topk<false>(el, a.penalty, a.k, out, wtop, cand, thr_s, ncand);
   else
     segment_topk<true>(el, a.penalty, a.k, out, wtop, cand, thr_s, ncand);
+}
+
+// ---- bf16 rows, top_k <= 32: 64 elements a thread --------------------------
+// The same lists as topk_segment_kernel over 16384-element segments, with
+// fewer VALU operations per element (the 8192-element kernel spends ~37 an
+// element and is bound by their issue):
+//  1. each thread takes the maxima of its eight 8-element runs of penalised
+//     values as floats (max chains; the penalty as x - p * seen, seen 0 / 1),
+//     keyed once per run; a NaN anywhere in the segment (which the float
+//     maxima skip) makes the workgroup key every element instead;
+//  2. the threshold t is the k-th largest of the 256 thread maxima by value
+//     alone (each wave sorts its 64 keys, the first k of the four waves are
+//     ranked, ties counted): k elements reach it, so every element of the
+//     segment's top k does, and they lie in the threads whose maxima do;
+//  3. those threads key the elements of their runs whose maxima reach t,
+//     (value, -index) as in the 8192-element kernel, and the candidates are
+//     ranked by counting.  When ties at t let more than kWideCandThreads
+//     threads reach it, the list takes the elements above t (fewer than k
+//     threads hold them) and then, if they are fewer than k, the elements
+//     equal to t in index order up to k.
+constexpr int kWideRuns = 8;                            // 16-byte runs (8 bf16) a thread
+constexpr int kWidePer = 8 * kWideRuns;                 // 64 elements a thread
+constexpr int kWideSeg = kTopkThreads * kWidePer;       // 16384 elements a segment
+constexpr int kWideMaxK = 32;
+constexpr int kWideCandThreads = kCandMax / kWidePer;   // 32 threads' elements fit the list
+static_assert(kWideCandThreads >= kWideMaxK, "the k - 1 threads above the threshold fit the list");
+
+// A thread's 64 bf16 elements: element e = (run c, slot j) at
+// lo + (c * 256 + tid) * 8 + j, loaded through buffer resources bounded by
+// the row (runs past V read zeros and are invalid).  The first pass keeps
+// the loaded runs; the later passes load the runs they need again (from the
+// cache), so the 48 registers of the first are free after it.
+struct WideRun {
+  uint4 raw;
+  uint32_t sm[2];
+  __device__ __forceinline__ float value(int j, float penalty) const {
+    const uint32_t w = reinterpret_cast<const uint32_t*>(&raw)[j / 2];
+    const float x = __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+    return ((sm[j / 4] >> (8 * (j % 4))) & 0xffu) ? x - penalty : x;
+  }
+  __device__ __forceinline__ uint32_t key(int j, float penalty) const { return okey_fast(value(j, penalty)); }
+};
+
+struct WideElems {
+  __amdgpu_buffer_rsrc_t rr, sr;
+  bool seen;
+  int base, V;
+  bool full;
+  __device__ __forceinline__ void init(const char* row, const uint8_t* srow, int lo, int tid, int V_) {
+    V = V_;
+    full = lo + kWideSeg <= V;
+    base = lo + tid * 8;
+    seen = srow != nullptr;
+    rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(row), 0, V * 2, 0x00020000);
+    sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(seen ? srow : nullptr), 0, seen ? V : 0, 0x00020000);
+  }
+  // again: an opaque offset, so the compiler loads the run anew instead of
+  // keeping the first pass's registers live
+  template <bool AGAIN = true>
+  __device__ __forceinline__ void load(int c, WideRun& r) const {
+    int off = base + c * kTopkThreads * 8;
+    if constexpr (AGAIN) asm volatile("" : "+v"(off));
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rr, off * 2, 0, 0);
+    r.raw = make_uint4(v.x, v.y, v.z, v.w);
+    r.sm[0] = r.sm[1] = 0;
+    if (seen) {
+      const u32x2 m = __builtin_amdgcn_raw_buffer_load_b64(sr, off, 0, 0);
+      r.sm[0] = m.x;
+      r.sm[1] = m.y;
+    }
+  }
+  // the key of one element, loaded on its own (the rare NaN pass)
+  __device__ __forceinline__ uint32_t key(int c, int j, float penalty) const {
+    const int i = base + c * kTopkThreads * 8 + j;
+    const float x = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rr, i * 2, 0, 0)) << 16);
+    const bool s = seen && __builtin_amdgcn_raw_buffer_load_b8(sr, i, 0, 0) != 0;
+    return okey_fast(s ? x - penalty : x);
+  }
+  __device__ __forceinline__ bool run_valid(int c) const { return full || base + c * kTopkThreads * 8 < V; }
+  __device__ __forceinline__ int index(int c, int j) const { return base + c * kTopkThreads * 8 + j; }
+};
+
+// Bytes of s made 0 / 1 (nonzero -> 1), without carries between bytes.
+__device__ __forceinline__ uint32_t nonzero_bytes(uint32_t s) {
+  return ((((s & 0x7f7f7f7fu) + 0x7f7f7f7fu) | s) >> 7) & 0x01010101u;
+}
+
+// Exclusive prefix sum of v over the workgroup in thread order; *total = the sum.
+__device__ __forceinline__ int block_excl_scan(int v, int* total, int (&wsum)[kTopkThreads / kWave]) {
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  __syncthreads();  // wsum free
+  if (lane == kWave - 1) wsum[wv] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kTopkThreads / kWave; ++w) {
+    before += w < wv ? wsum[w] : 0;
+    all += wsum[w];
+  }
+  *total = all;
+  return before + x - v;
+}
+
+// Five workgroups a CU (20 waves): the decode batch's 1280 segments are resident at once.
+template <bool CHECK>
+__global__ void __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(5, 5)))
+topk_wide_kernel(TopkArgs a) {
+  __shared__ uint32_t wtop[kTopkThreads / kWave][kWideMaxK];
+  __shared__ uint64_t cand[kCandMax + 1];  // + a spare entry
+  __shared__ int wsum[kTopkThreads / kWave];
+  __shared__ uint32_t thr_v;
+  __shared__ int ncand, nthreads;
+  const int seg = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wv = tid / kWave, k = a.k;
+  const int lo = seg * kWideSeg;
+  if (tid == 0) {
+    ncand = 0;
+    nthreads = 0;
+    thr_v = 1;  // fewer than k real maxima: every real element is a candidate
+  }
+  const char* row = static_cast<const char*>(a.scores) + static_cast<int64_t>(b) * a.row_stride * 2;
+  const uint8_t* srow = a.seen ? a.seen + static_cast<int64_t>(b) * a.seen_stride : nullptr;
+  uint64_t* out = a.work + (static_cast<int64_t>(b) * a.S + seg) * a.k;
+  WideElems el;
+  el.init(row, srow, lo, tid, a.V);
+  WideRun run[kWideRuns];
+#pragma unroll
+  for (int c = 0; c < kWideRuns; ++c) el.load<false>(c, run[c]);
+  const float pen = a.penalty;
+
+  // 1. run maxima of the penalised values (0: a run past the row); |x| bits
+  // of the raw words to find a NaN
+  const float np = -pen;
+  uint32_t rkey[kWideRuns];
+  float rmax[kWideRuns];
+  u16x2 absmax = {0, 0};
+#pragma unroll
+  for (int c = 0; c < kWideRuns; ++c) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&run[c].raw);
+    const uint32_t s0 = nonzero_bytes(run[c].sm[0]), s1 = nonzero_bytes(run[c].sm[1]);
+    float m = -INFINITY;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t sw = d < 2 ? s0 : s1;
+      const int sh = 16 * (d & 1);
+      const float x0 = fmaf(np, static_cast<float>((sw >> sh) & 0xffu), __uint_as_float(w[d] << 16));
+      const float x1 = fmaf(np, static_cast<float>((sw >> (sh + 8)) & 0xffu), __uint_as_float(w[d] & 0xffff0000u));
+      m = fmaxf(m, fmaxf(x0, x1));
+      absmax = __builtin_elementwise_max(absmax, __builtin_bit_cast(u16x2, w[d] & 0x7fff7fffu));
+    }
+    rmax[c] = m;
+  }
+  const bool nan = absmax.x > 0x7f80u || absmax.y > 0x7f80u;
+  if (__syncthreads_or(nan)) {  // exact keys of every element
+#pragma unroll
+    for (int c = 0; c < kWideRuns; ++c) {
+      uint32_t m = 0;
+#pragma unroll 1
+      for (int j = 0; j < 8; ++j) m = max(m, el.key(c, j, pen));  // element by element: few registers
+      rkey[c] = m;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < kWideRuns; ++c) rkey[c] = okey_fast(rmax[c]);
+  }
+  uint32_t tkey = 0;
+#pragma unroll
+  for (int c = 0; c < kWideRuns; ++c) {
+    if (CHECK && !el.run_valid(c)) rkey[c] = 0;
+    tkey = max(tkey, rkey[c]);
+  }
+
+  // 2. the k-th largest thread maximum by value, ties counted
+  uint32_t x = tkey;
+#pragma unroll
+  for (int size = 2; size <= kWave; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t y = __shfl_xor(x, stride, kWave);
+      const bool keep_max = ((lane & size) == 0) == ((lane & stride) == 0);
+      x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+    }
+  if (lane < k) wtop[wv][lane] = x;  // descending
+  __syncthreads();
+  if (tid < (kTopkThreads / kWave) * k) {
+    const uint32_t c = wtop[tid / k][tid % k];
+    int gt = 0, ge = 0;
+    for (int w = 0; w < kTopkThreads / kWave; ++w)
+      for (int j = 0; j < k; ++j) {
+        const uint32_t o = wtop[w][j];
+        gt += o > c;
+        ge += o >= c;
+      }
+    if (c != 0 && gt < k && ge >= k) thr_v = c;  // every such c holds the same value
+  }
+  __syncthreads();
+  const uint32_t thr = thr_v;
+  if (tkey >= thr) atomicAdd(&nthreads, 1);
+  __syncthreads();
+
+  // 3. the candidates
+  if (nthreads <= kWideCandThreads) {  // uniform
+    if (tkey >= thr) {
+#pragma unroll
+      for (int c = 0; c < kWideRuns; ++c) {
+        if (rkey[c] < thr) continue;
+        WideRun r;
+        el.load(c, r);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t kx = r.key(j, pen);
+          if (kx >= thr) cand[atomicAdd(&ncand, 1)] = (static_cast<uint64_t>(kx) << 32) |
+                                                      (0xffffffffu - static_cast<uint32_t>(el.index(c, j)));
+        }
+      }
+    }
+  } else {
+    // ties at the threshold: the elements above it (fewer than k threads
+    // hold them), then those equal to it in index order until k are listed
+    if (tkey > thr) {
+#pragma unroll
+      for (int c = 0; c < kWideRuns; ++c) {
+        if (rkey[c] <= thr) continue;
+        WideRun r;
+        el.load(c, r);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t kx = r.key(j, pen);
+          if (kx > thr) cand[atomicAdd(&ncand, 1)] = (static_cast<uint64_t>(kx) << 32) |
+                                                     (0xffffffffu - static_cast<uint32_t>(el.index(c, j)));
+        }
+      }
+    }
+    __syncthreads();
+    int need = k - ncand;
+#pragma unroll
+    for (int c = 0; c < kWideRuns; ++c) {
+      if (need <= 0) break;  // uniform
+      int cnt = 0;
+      WideRun r;
+      if (rkey[c] >= thr) {
+        el.load(c, r);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cnt += r.key(j, pen) == thr;
+      }
+      int total = 0;
+      int pos = block_excl_scan(cnt, &total, wsum);
+      if (cnt > 0 && pos < need) {
+        const int base_slot = ncand;  // read before any thread of this run appends
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (r.key(j, pen) == thr && pos < need) {
+            cand[base_slot + pos] = (static_cast<uint64_t>(thr) << 32) |
+                                    (0xffffffffu - static_cast<uint32_t>(el.index(c, j)));
+            ++pos;
+          }
+        }
+      }
+      __syncthreads();
+      if (tid == 0) ncand += min(total, need);
+      need -= total;
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  const int n = ncand;
+  for (int i = tid; i < n; i += kTopkThreads) {
+    const uint64_t me = cand[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += cand[j] > me;
+    if (rank < k) out[rank] = me;
+  }
+  for (int r = n + tid; r < k; r += kTopkThreads) out[r] = 0;  // padding: below every element
 }
 
 struct SampleArgs {
@@ -738,14 +1021,24 @@ int topk_sample_launch(const void* scores, int dtype, int64_t row_stride, const 
   const int64_t run = 16 / static_cast<int64_t>(esz);  // elements per 16-byte load
   const bool vec = (reinterpret_cast<uintptr_t>(scores) % 16) == 0 && row_stride % run == 0 && V % run == 0 &&
                    (seen == nullptr || ((reinterpret_cast<uintptr_t>(seen) % run) == 0 && seen_stride % run == 0));
-  const dim3 grid(S, static_cast<unsigned>(B));
-  switch (dtype * 2 + (vec ? 1 : 0)) {
-    case YH_F32 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_F32, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
-    case YH_F32 * 2: hipLaunchKernelGGL((topk_segment_kernel<YH_F32, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
-    case YH_BF16 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_BF16, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
-    case YH_BF16 * 2: hipLaunchKernelGGL((topk_segment_kernel<YH_BF16, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
-    case YH_F16 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_F16, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
-    default: hipLaunchKernelGGL((topk_segment_kernel<YH_F16, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
+  if (dtype == YH_BF16 && vec && top_k <= kWideMaxK && std::isfinite(penalty)) {
+    // bf16 runs: 16384-element segments of 64 elements a thread
+    S = static_cast<int>((V + kWideSeg - 1) / kWideSeg);
+    ta.S = S;
+    ta.seg = kWideSeg;
+    const dim3 grid(S, static_cast<unsigned>(B));
+    if (V % kWideSeg == 0) hipLaunchKernelGGL(topk_wide_kernel<false>, grid, dim3(kTopkThreads), 0, st, ta);
+    else hipLaunchKernelGGL(topk_wide_kernel<true>, grid, dim3(kTopkThreads), 0, st, ta);
+  } else {
+    const dim3 grid(S, static_cast<unsigned>(B));
+    switch (dtype * 2 + (vec ? 1 : 0)) {
+      case YH_F32 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_F32, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
+      case YH_F32 * 2: hipLaunchKernelGGL((topk_segment_kernel<YH_F32, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
+      case YH_BF16 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_BF16, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
+      case YH_BF16 * 2: hipLaunchKernelGGL((topk_segment_kernel<YH_BF16, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
+      case YH_F16 * 2 + 1: hipLaunchKernelGGL((topk_segment_kernel<YH_F16, true>), grid, dim3(kTopkThreads), 0, st, ta); break;
+      default: hipLaunchKernelGGL((topk_segment_kernel<YH_F16, false>), grid, dim3(kTopkThreads), 0, st, ta); break;
+    }
   }
   YH_CHECK_LAUNCH("topk_segment");
   SampleArgs sa{static_cast<const uint64_t*>(workspace), attempt_ids, steps, tokens, out_values, out_indices,
@@ -843,8 +1136,9 @@ extern "C" int yh_topk_sample_noalloc(const void* scores, int dtype, int64_t row
 }
 
 extern "C" void yh_topk_segments(int64_t V, int64_t top_k, int* n_segments, int* seg_len) {
-  // fixed 8192-element segments: 256 threads x 8 vectors of 4; the candidate
-  // bound k * 32 <= 2048 fits the LDS list for every k <= 64
+  // 8192-element segments: 256 threads x 8 vectors of 4; the candidate bound
+  // k * 32 <= 2048 fits the LDS list for every k <= 64.  bf16 rows with
+  // k <= 32 use half as many 16384-element segments, within this workspace.
   (void)top_k;
   *n_segments = static_cast<int>((V + yh::kSegLen - 1) / yh::kSegLen);
   *seg_len = yh::kSegLen;
