@@ -21,7 +21,9 @@ Prints one JSON line.  Workloads:
   live slots per timed step (min / mean / first / last), ``decode.ring_fill``
   the mean live fraction of the SWA rings those steps read (a young ring is
   cheaper: the window read skips blocks without a live slot).  Beside the
-  decode line the same run reports ``prefill`` (the ``gdn_prefill`` workload:
+  decode line the same run reports ``fp16_state`` (the same workload with the
+  GDN state stored in float16, the reference's "fast" profile; not the line's
+  value, whose state is float32), ``prefill`` (the ``gdn_prefill`` workload:
   20 timed calls after 20 warm-up calls, with its HBM and MFMA roofline) and
   ``sampling`` (the ``sampling`` workload at the decode batch).
 * ``long_horizon``: B=256 fixed sequences generating 32768 tokens from
@@ -262,6 +264,20 @@ def bench_model_decode(steps, warmup, cpu, batch=128):
                    "wall_seconds": met.generation_wall_seconds, "refilled": met.refilled,
                    "completed": met.completed, "peak_hbm_gib": met.peak_allocated_gib, **met.extra},
     }
+    del model
+    torch.cuda.empty_cache()
+    # beside the line: the reference's throughput profile ("fast": the GDN
+    # state stored in float16), the storage of its published batched figures
+    _log("model_decode: the same workload with the float16 GDN state")
+    model = rt.Model(cfg, batch=batch, device=dev, seed=0, state_dtype=torch.float16)
+    m16 = rt.run_decode_benchmark(model, steps=steps, warmup=warmup, rate=4.0, prompt_len=128, mean_len=1024,
+                                  poll_interval=32)
+    res["fp16_state"] = {"profile": "the reference's 'fast' profile: GDN state stored in float16, updated in "
+                                    "float32 (not the headline: the metric's state is float32)",
+                         "tokens_per_s": m16.decode_tokens_per_second,
+                         "ms_per_step": m16.decode_seconds * 1e3 / m16.decode_steps,
+                         "useful_token_events": m16.decode_useful_token_events,
+                         "peak_hbm_gib": m16.peak_allocated_gib}
     del model
     torch.cuda.empty_cache()
     _log("model_decode: the chunked prefill and the sampler beside the decode line")
@@ -878,7 +894,7 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": res["dtype"], "data": "synthetic (seeded random-init weights and requests)",
             "config": res["config"], "roofline": res["roofline"]}
-    for key in ("cpu_baseline", "decode", "prefill", "sampling", "projections", "hipblaslt_ms_per_step",
+    for key in ("cpu_baseline", "decode", "fp16_state", "prefill", "sampling", "projections", "hipblaslt_ms_per_step",
                 "hbm_streams_gbs", "gemm_bf16"):
         if key in res:
             line[key] = res[key]

@@ -89,9 +89,12 @@ int yh_gdn_recurrent_varlen(const void* q, const void* k, const void* v, const v
  *        (HV * V), b at b_offset (HV), a at a_offset (HV)
  *   conv_state [B, 3, conv_dim] bf16 (oldest first), shifted in place
  *   conv_w [conv_dim, 4] bf16;  a_log, dt_bias float [HV]
- *   state [n_state_rows, HV, K, V] float32 (row b, or state_indices[b]; a
- *        negative index leaves the state alone and gives a zero output row
- *        before the norm)
+ *   state [n_state_rows, HV, K, V] of state_dtype (row b, or
+ *        state_indices[b]; a negative index leaves the state alone and gives
+ *        a zero output row before the norm): YH_F32, or YH_F16 for the
+ *        reference's fp16 state storage (inference_kernels.py:1079-1081,
+ *        modeling_yanchor.py:733-750: widened on the load, the update in fp32,
+ *        rounded to nearest on the store)
  *   norm_w [V] bf16;  y [B, HV * V] bf16 = gated RMSNorm (eps) of o with z
  * Requirements: H == HV, K == V == 128, conv_dim == 2 H K + HV V, conv kernel 4;
  * proj rows and z_offset multiples of 4 elements.
@@ -101,7 +104,8 @@ int yh_gdn_recurrent_varlen(const void* q, const void* k, const void* v, const v
  * for the decode graph (no reference counterpart as one launch).
  */
 int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* conv_state, const void* conv_w,
-                        const float* a_log, const float* dt_bias, float* state, const int32_t* state_indices,
+                        const float* a_log, const float* dt_bias, void* state, int state_dtype,
+                        const int32_t* state_indices,
                         const void* norm_w, void* y, int64_t B, int64_t H, int64_t HV, int64_t K, int64_t V,
                         int64_t conv_dim, int64_t z_offset, int64_t b_offset, int64_t a_offset,
                         int64_t n_state_rows, float scale, int use_qk_l2norm, float eps, yh_stream_t stream);

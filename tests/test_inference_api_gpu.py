@@ -38,6 +38,24 @@ def small_cfg(**kw):
     return rt.ModelConfig(**base)
 
 
+def test_profiles_pick_the_state_storage(gpu):
+    """As the reference's engine (runtime/inference.py:53-56): profile "fast"
+    keeps the GDN state in float16 for batches above one, "reference", one
+    row or the eager torch backend in float32; the fast engine generates."""
+    cfg = small_cfg(gdn_heads_k=4, gdn_heads_v=4)
+    for kw, want in ((dict(batch=4), torch.float16), (dict(batch=4, profile="reference"), torch.float32),
+                     (dict(batch=1), torch.float32), (dict(batch=4, backend="torch"), torch.float32)):
+        eng = inference.Engine(cfg, device=gpu, **kw)
+        assert eng.model.state_dtype == want, kw
+        assert eng.operators["recurrent_state"] == str(want).removeprefix("torch."), kw
+        assert all(x.dtype == want for x in eng.model.gdn_state.values())
+    eng = inference.Engine(cfg, device=gpu, batch=4)
+    rows = [dict(input_ids=p, max_tokens=12) for p in _prompts(6, seed=3)]
+    out, met = eng.generate(rows, cap=12, fixed=True, stop_interval=4)
+    assert [r["attempt_id"] for r in out] == list(range(6))
+    assert all(1 <= len(r["response_ids"]) <= 12 for r in out)
+
+
 def _prompts(n, seed=1, lo=5, hi=40):
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(lo, hi, (n,), generator=g).tolist()

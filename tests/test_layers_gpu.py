@@ -444,6 +444,38 @@ def test_rmsnorm_two_deferred_projections(gpu, s1, s2):
 
 
 @pytest.mark.parametrize("b", [1, 5, 128])
+def test_gdn_decode_fused_fp16_state(gpu, b):
+    """The float16 state storage of the reference's throughput profile: bit
+    for bit the float32 kernel run on the widened state, with its updated
+    state rounded to float16 (to nearest even) and the same output row and
+    conv window; a row with a negative state index stays untouched."""
+    h, d = 32, 128
+    conv_dim, vd = 3 * h * d, h * d
+    p = conv_dim + vd + 2 * h
+    proj = rnd(b, p, dev=gpu, scale=2.0, seed=70)
+    conv = rnd(b, 3, conv_dim, dev=gpu, seed=71)
+    conv_w = rnd(conv_dim, 4, dev=gpu, scale=0.5, seed=72)
+    a_log = torch.log(torch.linspace(1.0, 16.0, h, device=gpu))
+    dt_bias = torch.linspace(-1.0, 1.0, h, device=gpu)
+    s16 = rnd(b + 2, h, d, d, dev=gpu, scale=0.1, seed=73, dtype=torch.float16)
+    s32 = s16.float()
+    norm_w = (1.0 + rnd(d, dev=gpu, scale=0.1, seed=74).float()).to(torch.bfloat16)
+    idx = torch.arange(b, device=gpu, dtype=torch.int32) + 2
+    idx[b // 2] = -1
+    kw = dict(heads=h, head_dim=d, z_offset=conv_dim, b_offset=conv_dim + vd, a_offset=conv_dim + vd + h,
+              state_indices=idx)
+    c16, c32 = conv.clone(), conv.clone()
+    before = s16.clone()
+    y16 = layers.gdn_decode_fused(proj, c16, conv_w, a_log, dt_bias, s16, norm_w, 1e-6, **kw)
+    y32 = layers.gdn_decode_fused(proj, c32, conv_w, a_log, dt_bias, s32, norm_w, 1e-6, **kw)
+    assert torch.equal(y16, y32) and torch.equal(c16, c32)
+    assert torch.equal(s16, s32.half())
+    untouched = [r for r in range(b + 2) if r not in set(idx.tolist())]
+    assert torch.equal(s16[untouched], before[untouched])
+    assert b == 1 or not torch.equal(s16, before)        # b = 1: its only row has index -1
+
+
+@pytest.mark.parametrize("b", [1, 5, 128])
 def test_gdn_decode_fused_equals_three_launches(gpu, b, monkeypatch):
     """Conv update + gated delta rule + gated norm in one launch give bit for
     bit what gdn_decode_prep, the recurrence (at its 128-column tile) and

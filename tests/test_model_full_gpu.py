@@ -113,6 +113,40 @@ def test_full_model_decode_after_prefill(gpu, cfg, b, t, dtype, tol):
             assert same >= 0.9, (layer, same.item())
 
 
+def test_full_model_fp16_state_storage(gpu):
+    """The reference's throughput profile stores the GDN state in float16
+    (convert_fixed_memory_recurrent_state_storage_, modeling_yanchor.py:733-
+    750): the update runs in float32 and the stored state is rounded once a
+    step.  A float16-state model gives bit for bit the float32-state model
+    whose states are rounded to float16 after the prefill and after every
+    decode step: the same logits every step, the same states at the end."""
+    b, t, n = 32, 20, 8
+    m32 = rt.Model(FULL, batch=b, device=gpu, seed=13)
+    m16 = rt.Model(FULL, batch=b, device=gpu, seed=13, state_dtype=torch.float16)
+    assert all(x.dtype == torch.float16 for x in m16.gdn_state.values())
+    prompts = _prompts(b, t + n, FULL.vocab, 15).to(gpu)
+
+    def round32():
+        for x in m32.gdn_state.values():
+            x.copy_(x.half().float())
+
+    for m in (m32, m16):
+        _, caches = m.prefill(prompts[:, :t])
+        for dst, src in zip(m.cache_tensors(), caches):
+            dst.copy_(src)
+        del caches
+    round32()
+    valid = torch.ones(b, dtype=torch.bool, device=gpu)
+    for s in range(n):
+        pos = torch.full((b,), t + s, dtype=torch.long, device=gpu)
+        want = m32.decode_step(prompts[:, t + s], pos, valid)
+        round32()
+        got = m16.decode_step(prompts[:, t + s], pos, valid)
+        assert torch.equal(got, want), s
+    for i in m32.gdn_state:
+        assert torch.equal(m16.gdn_state[i], m32.gdn_state[i].half()), i
+
+
 def _record_memory_reads(model):
     """Wrap the model's memory read so every decode-step read's norm is
     recorded (a live memory reads non-zero)."""

@@ -13,8 +13,9 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libyanchor_amd.so"
 # yh_abi_version() of the library these signatures describe (103: yh_rmsnorm_partials takes
-# out2_stride; 104: yh_linear_pack lays K blocks outermost; 105: yh_rmsnorm_partials takes part2)
-ABI_VERSION = 105
+# out2_stride; 104: yh_linear_pack lays K blocks outermost; 105: yh_rmsnorm_partials takes part2;
+# 106: yh_gdn_decode_fused takes the state dtype)
+ABI_VERSION = 106
 
 F32, BF16, F16, I32, I64, U8 = 0, 1, 2, 3, 4, 5
 DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16,
@@ -55,8 +56,8 @@ SIGNATURES: dict[str, list] = {
     "yh_linear_packed": [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i64, _p, _i64, _i32, _p, _p],
     "yh_decode_inputs": [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                          _f32, _p],
-    "yh_gdn_decode_fused": [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                            _i64, _i64, _i64, _f32, _i32, _f32, _p],
+    "yh_gdn_decode_fused": [_p, _i64, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _i64, _i64, _i64, _i64, _f32, _i32, _f32, _p],
     "yh_rmsnorm_partials": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _i64,
                             _p],
     "yh_ring_write": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,

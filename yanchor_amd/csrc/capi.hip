@@ -18,4 +18,4 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* yh_last_error(void) { return yh::g_error; }
 
-extern "C" int yh_abi_version(void) { return 105; }
+extern "C" int yh_abi_version(void) { return 106; }

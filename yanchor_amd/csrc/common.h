@@ -134,6 +134,22 @@ __device__ __forceinline__ void st_stream4(float* p, float4 x) {
   const f32x4_t v = {x.x, x.y, x.z, x.w};
   __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t*>(p));
 }
+// Four fp16 values (8 bytes), widened exactly / rounded to nearest even.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 ld_stream_h4(const uint16_t* p) {
+  const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+  return make_float4(f16_to_f32(v.x & 0xffffu), f16_to_f32(v.x >> 16), f16_to_f32(v.y & 0xffffu),
+                     f16_to_f32(v.y >> 16));
+}
+__device__ __forceinline__ void st_stream_h4(uint16_t* p, float4 x) {
+  // the float32 values first: without this the compiler fuses the producing
+  // FMA into the conversion (v_fma_mix), one rounding instead of the float32
+  // value's rounding to fp16
+  asm volatile("" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
+  const u32x2_t v = {static_cast<uint32_t>(f32_to_f16(x.x)) | (static_cast<uint32_t>(f32_to_f16(x.y)) << 16),
+                     static_cast<uint32_t>(f32_to_f16(x.z)) | (static_cast<uint32_t>(f32_to_f16(x.w)) << 16)};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t*>(p));
+}
 
 // Wave-wide sum (64 lanes) with xor shuffles.
 __device__ __forceinline__ float wave_sum(float x) {

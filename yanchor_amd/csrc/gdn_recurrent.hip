@@ -282,7 +282,7 @@ struct FusedArgs {
   const uint16_t* conv_w;    // [C, 4]
   const float* a_log;        // [HV]
   const float* dt_bias;      // [HV]
-  float* state;              // [n_rows, HV, K, V]
+  void* state;               // [n_rows, HV, K, V] float32, or fp16 (H16)
   const int32_t* idx;        // [B] or null
   const uint16_t* norm_w;    // [V]
   uint16_t* y;               // [B, HV V]
@@ -323,7 +323,9 @@ __device__ __forceinline__ void conv_shift(uint16_t* st, int C, int c, const Con
   st[2 * C + c] = r.x;
 }
 
-template <int K, int V, int NT>
+// H16: the state is stored as fp16 (computed in fp32, rounded once a step on
+// the store), as the reference's throughput profile keeps it.
+template <int K, int V, int NT, bool H16>
 __global__ void __launch_bounds__(NT) gdn_decode_fused_kernel(FusedArgs a) {
   constexpr int LPR = V / 4;
   constexpr int RG = NT / LPR;
@@ -350,11 +352,15 @@ __global__ void __launch_bounds__(NT) gdn_decode_fused_kernel(FusedArgs a) {
   const int64_t srow = a.idx ? static_cast<int64_t>(a.idx[b]) : b;
   const bool live = srow >= 0 && srow < a.n_rows;
 
-  float* S = a.state + (live ? srow * a.HV + hv : 0) * static_cast<int64_t>(K) * V + col0;
+  const int64_t s0 = (live ? srow * a.HV + hv : 0) * static_cast<int64_t>(K) * V + col0;
   float4 s[RPT];
   if (live) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = ld_stream4(S + static_cast<int64_t>(rg + i * RG) * V);
+    for (int i = 0; i < RPT; ++i) {
+      const int64_t e = s0 + static_cast<int64_t>(rg + i * RG) * V;
+      if constexpr (H16) s[i] = ld_stream_h4(static_cast<const uint16_t*>(a.state) + e);
+      else s[i] = ld_stream4(static_cast<const float*>(a.state) + e);
+    }
   }
   const uint16_t* prow = a.proj + b * a.P;
   uint16_t* st = a.conv_state + b * 3 * a.C;
@@ -466,7 +472,11 @@ __global__ void __launch_bounds__(NT) gdn_decode_fused_kernel(FusedArgs a) {
       s[i].w = fmaf(s[i].w, eg, kr * d.w);
     }
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) st_stream4(S + static_cast<int64_t>(rg + i * RG) * V, s[i]);
+    for (int i = 0; i < RPT; ++i) {
+      const int64_t e = s0 + static_cast<int64_t>(rg + i * RG) * V;
+      if constexpr (H16) st_stream_h4(static_cast<uint16_t*>(a.state) + e, s[i]);
+      else st_stream4(static_cast<float*>(a.state) + e, s[i]);
+    }
   }
   if (wid != 0) return;
   // Gated RMSNorm of the bf16-rounded output row (128 values over lanes 0..31,
@@ -598,13 +608,14 @@ extern "C" int yh_gdn_recurrent_varlen(const void* q, const void* k, const void*
 }
 
 extern "C" int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* conv_state, const void* conv_w,
-                                   const float* a_log, const float* dt_bias, float* state,
+                                   const float* a_log, const float* dt_bias, void* state, int state_dtype,
                                    const int32_t* state_indices, const void* norm_w, void* y, int64_t B, int64_t H,
                                    int64_t HV, int64_t K, int64_t V, int64_t conv_dim, int64_t z_offset,
                                    int64_t b_offset, int64_t a_offset, int64_t n_state_rows, float scale,
                                    int use_qk_l2norm, float eps, yh_stream_t stream) {
   using namespace yh;
   YH_CHECK_ARG(B >= 0 && H > 0 && HV == H, "gdn_decode_fused: needs as many value heads as key heads");
+  YH_CHECK_ARG(state_dtype == YH_F32 || state_dtype == YH_F16, "gdn_decode_fused: the state is float32 or fp16");
   YH_CHECK_ARG(K == 128 && V == 128, "gdn_decode_fused: needs 128-dim heads");
   YH_CHECK_ARG(conv_dim == 2 * H * K + HV * V, "gdn_decode_fused: conv_dim must be 2 H K + HV V");
   YH_CHECK_ARG(z_offset >= conv_dim && z_offset + HV * V <= proj_stride && b_offset + HV <= proj_stride &&
@@ -627,8 +638,15 @@ extern "C" int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* 
               use_qk_l2norm ? 1 : 0};
   // 512 threads measured fastest on MI355X at B = 128 (97 us per layer against
   // 104 / 109 us for 256 / 1024 threads)
-  hipLaunchKernelGGL((gdn_decode_fused_kernel<128, 128, 512>), dim3(static_cast<unsigned>(B * HV)), dim3(512), 0,
-                     static_cast<hipStream_t>(stream), a);
+  // fp16 state: 61 us per layer at B = 128 for 256, 512 or 1024 threads alike
+  // (4.4 TB/s in state bytes: with half the bytes a workgroup's conv / norm
+  // chain is no longer hidden under its state loads)
+  if (state_dtype == YH_F16)
+    hipLaunchKernelGGL((gdn_decode_fused_kernel<128, 128, 512, true>), dim3(static_cast<unsigned>(B * HV)), dim3(512),
+                       0, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL((gdn_decode_fused_kernel<128, 128, 512, false>), dim3(static_cast<unsigned>(B * HV)),
+                       dim3(512), 0, static_cast<hipStream_t>(stream), a);
   YH_CHECK_LAUNCH("gdn_decode_fused");
   return YH_OK;
 }

@@ -145,8 +145,9 @@ def _rmsnorm_partials(p, w, eps, residual, plus_one, w2=None, w2_row=None):
 def gdn_decode_fused(proj, conv_state, conv_w, a_log, dt_bias, state, norm_w, eps, *, heads, head_dim, z_offset,
                      b_offset, a_offset, scale=None, state_indices=None):
     """One decode token of a GDN layer's core, one launch: ``gdn_decode_prep``
-    + the gated delta rule (L2-normed q/k, ``state`` [N, H, D, D] float32 in
-    place) + ``gated_rmsnorm`` of the output, bit for bit.  proj [B, P] bf16
+    + the gated delta rule (L2-normed q/k, ``state`` [N, H, D, D] float32, or
+    float16 as the reference's throughput profile stores it, in place) +
+    ``gated_rmsnorm`` of the output, bit for bit.  proj [B, P] bf16
     (qkv | z | b | a), conv_state [B, 3, conv_dim] shifted in place -> y
     [B, H * D] bf16."""
     _bf16(proj, conv_state, conv_w, norm_w)
@@ -155,15 +156,17 @@ def gdn_decode_fused(proj, conv_state, conv_w, a_log, dt_bias, state, norm_w, ep
     conv_dim = 3 * h * d
     if proj.stride(-1) != 1 or conv_state.shape != (b, 3, conv_dim) or not conv_state.is_contiguous():
         raise ValueError("proj must have unit column stride and conv_state be contiguous [B, 3, conv_dim]")
-    if state.dtype != torch.float32 or not state.is_contiguous() or tuple(state.shape[1:]) != (h, d, d):
-        raise ValueError("state must be contiguous float32 [N, H, D, D]")
+    if state.dtype not in (torch.float32, torch.float16) or not state.is_contiguous() or \
+            tuple(state.shape[1:]) != (h, d, d):
+        raise ValueError("state must be contiguous float32 or float16 [N, H, D, D]")
     dev = N.require_device(proj, conv_state, conv_w, a_log, dt_bias, state, norm_w, state_indices)
     idx = None if state_indices is None else state_indices.to(torch.int32).contiguous()
     y = torch.empty(b, h * d, dtype=torch.bfloat16, device=dev)
     sc = float(d ** -0.5 if scale is None else scale)
     N.call("yh_gdn_decode_fused", proj.data_ptr(), proj.stride(0), conv_state.data_ptr(), conv_w.contiguous().data_ptr(),
            a_log.float().contiguous().data_ptr(), dt_bias.float().contiguous().data_ptr(), state.data_ptr(),
-           N.ptr(idx), norm_w.contiguous().data_ptr(), y.data_ptr(), b, h, h, d, d, conv_dim, int(z_offset),
+           N.DTYPE_CODE[state.dtype], N.ptr(idx), norm_w.contiguous().data_ptr(), y.data_ptr(), b, h, h, d, d,
+           conv_dim, int(z_offset),
            int(b_offset), int(a_offset), state.shape[0], sc, 1, float(eps), N.stream_of(proj))
     return y
 

@@ -515,11 +515,21 @@ class Model:
     """Random-init 4B-shaped hybrid recurrent model with its decode caches."""
 
     def __init__(self, cfg: ModelConfig, batch: int, device, *, seed=0, ops=None, dtype=torch.bfloat16,
-                 init="normal", overlap=True):
+                 init="normal", overlap=True, state_dtype=torch.float32):
         """``init="normal"`` draws every weight from N(0, init_std);
         ``init="tiled"`` repeats one 16M-value N(0, init_std) block (fast on a
-        host, for timing runs where the values do not matter)."""
+        host, for timing runs where the values do not matter).
+        ``state_dtype``: the GDN recurrent state's storage, float32 or float16
+        (the reference's throughput profile: convert_fixed_memory_recurrent_
+        state_storage_, modeling_yanchor.py:733-750; bf16 models only)."""
+        if state_dtype not in (torch.float32, torch.float16):
+            raise ValueError("the GDN state is stored as float32 or float16")
+        if state_dtype != torch.float32 and (dtype != torch.bfloat16 or cfg.gdn_heads_k != cfg.gdn_heads_v
+                                            or not cfg.gdn_dk == cfg.gdn_dv == 128):
+            raise ValueError("a float16 GDN state needs a bfloat16 model whose GDN layers take the fused decode "
+                             "core (as many key as value heads, 128-dim heads)")
         self.cfg, self.B, self.device, self.dtype = cfg, int(batch), torch.device(device), dtype
+        self.state_dtype = state_dtype
         self.ops = ops if ops is not None else HipOps()
         self.overlap = overlap
         self._side = None
@@ -592,7 +602,8 @@ class Model:
         from .independent_memory import IndependentMemoryState
         for i, L in enumerate(self.layers):
             if L["kind"] == "gdn":
-                self.gdn_state[i] = torch.zeros(B, c.gdn_heads_v, c.gdn_dk, c.gdn_dv, device=dev)
+                self.gdn_state[i] = torch.zeros(B, c.gdn_heads_v, c.gdn_dk, c.gdn_dv, device=dev,
+                                                dtype=self.state_dtype)
                 # time-major [B, K-1, C]: the decode prologue reads one coalesced row per tap
                 self.conv_state[i] = torch.zeros(B, c.conv_kernel - 1, c.conv_dim, device=dev, dtype=self.dtype)
             else:
@@ -829,6 +840,7 @@ class Model:
         piece = max(1, min(int(token_chunk), int(max_tokens) // r))
         tmp = Model.__new__(Model)
         tmp.cfg, tmp.B, tmp.device, tmp.dtype, tmp.ops, tmp.layers = c, r, dev, self.dtype, self.ops, self.layers
+        tmp.state_dtype = self.state_dtype
         tmp._alloc_caches()
         last = torch.empty(r, c.hidden, dtype=self.dtype, device=dev)
         for w0 in range(0, max(lengths), piece):
@@ -884,7 +896,8 @@ class Model:
         q = mixed[:, : hk * dk].reshape(1, n, hk, dk)
         k = mixed[:, hk * dk: 2 * hk * dk].reshape(1, n, hk, dk)
         v = mixed[:, 2 * hk * dk:].reshape(1, n, hv, dv)
-        o, st = ops.gdn_prefill(q, k, v, g[None], beta[None], cu, lens, initial_state=tmp.gdn_state[i])
+        # the chunked recurrence runs from and to float32; a float16 store rounds once a piece
+        o, st = ops.gdn_prefill(q, k, v, g[None], beta[None], cu, lens, initial_state=tmp.gdn_state[i].float())
         tmp.gdn_state[i].copy_(st)
         y = ops.gated_rmsnorm(o.reshape(n, hv, dv), proj[:, c.conv_dim: c.conv_dim + hv * dv], L["gnorm"],
                               c.rms_eps)
