@@ -323,6 +323,39 @@ __device__ __forceinline__ void conv_shift(uint16_t* st, int C, int c, const Con
   st[2 * C + c] = r.x;
 }
 
+// A thread's state rows: float4 registers (float32 state), or the loaded fp16
+// words (8 bytes a row), widened where they are used -- half the registers, so
+// twice the workgroups fit a CU while their conv / norm chains run.
+template <bool H16, int RPT> struct StateRegs {
+  float4 v[RPT];
+  __device__ __forceinline__ void load(int i, const void* p, int64_t e) {
+    v[i] = ld_stream4(static_cast<const float*>(p) + e);
+  }
+  __device__ __forceinline__ float4 get(int i) const { return v[i]; }
+  __device__ __forceinline__ void opaque() {}
+  __device__ __forceinline__ void store(int i, void* p, int64_t e, float4 x) {
+    st_stream4(static_cast<float*>(p) + e, x);
+  }
+};
+template <int RPT> struct StateRegs<true, RPT> {
+  u32x2_t v[RPT];
+  __device__ __forceinline__ void load(int i, const void* p, int64_t e) {
+    v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(p) + e));
+  }
+  __device__ __forceinline__ float4 get(int i) const {
+    return make_float4(f16_to_f32(v[i].x & 0xffffu), f16_to_f32(v[i].x >> 16), f16_to_f32(v[i].y & 0xffffu),
+                       f16_to_f32(v[i].y >> 16));
+  }
+  // the words stay the only copy: the second pass widens them again
+  __device__ __forceinline__ void opaque() {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) asm volatile("" : "+v"(v[i]));
+  }
+  __device__ __forceinline__ void store(int i, void* p, int64_t e, float4 x) {
+    st_stream_h4(static_cast<uint16_t*>(p) + e, x);
+  }
+};
+
 // H16: the state is stored as fp16 (computed in fp32, rounded once a step on
 // the store), as the reference's throughput profile keeps it.
 template <int K, int V, int NT, bool H16>
@@ -353,14 +386,10 @@ __global__ void __launch_bounds__(NT) gdn_decode_fused_kernel(FusedArgs a) {
   const bool live = srow >= 0 && srow < a.n_rows;
 
   const int64_t s0 = (live ? srow * a.HV + hv : 0) * static_cast<int64_t>(K) * V + col0;
-  float4 s[RPT];
+  StateRegs<H16, RPT> s;
   if (live) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int64_t e = s0 + static_cast<int64_t>(rg + i * RG) * V;
-      if constexpr (H16) s[i] = ld_stream_h4(static_cast<const uint16_t*>(a.state) + e);
-      else s[i] = ld_stream4(static_cast<const float*>(a.state) + e);
-    }
+    for (int i = 0; i < RPT; ++i) s.load(i, a.state, s0 + static_cast<int64_t>(rg + i * RG) * V);
   }
   const uint16_t* prow = a.proj + b * a.P;
   uint16_t* st = a.conv_state + b * 3 * a.C;
@@ -424,9 +453,11 @@ __global__ void __launch_bounds__(NT) gdn_decode_fused_kernel(FusedArgs a) {
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const int r = rg + i * RG;
-      pk = fma4(s[i], kn[r], pk);
-      pq = fma4(s[i], qn[r], pq);
+      const float4 si = s.get(i);
+      pk = fma4(si, kn[r], pk);
+      pq = fma4(si, qn[r], pq);
     }
+    s.opaque();
 #pragma unroll
     for (int off = LPR; off < kWave; off <<= 1) {
       pk.x += __shfl_xor(pk.x, off, kWave);
@@ -466,16 +497,12 @@ __global__ void __launch_bounds__(NT) gdn_decode_fused_kernel(FusedArgs a) {
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const float kr = kn[rg + i * RG];
-      s[i].x = fmaf(s[i].x, eg, kr * d.x);
-      s[i].y = fmaf(s[i].y, eg, kr * d.y);
-      s[i].z = fmaf(s[i].z, eg, kr * d.z);
-      s[i].w = fmaf(s[i].w, eg, kr * d.w);
-    }
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int64_t e = s0 + static_cast<int64_t>(rg + i * RG) * V;
-      if constexpr (H16) st_stream_h4(static_cast<uint16_t*>(a.state) + e, s[i]);
-      else st_stream4(static_cast<float*>(a.state) + e, s[i]);
+      float4 x = s.get(i);
+      x.x = fmaf(x.x, eg, kr * d.x);
+      x.y = fmaf(x.y, eg, kr * d.y);
+      x.z = fmaf(x.z, eg, kr * d.z);
+      x.w = fmaf(x.w, eg, kr * d.w);
+      s.store(i, a.state, s0 + static_cast<int64_t>(rg + i * RG) * V, x);
     }
   }
   if (wid != 0) return;
@@ -638,9 +665,9 @@ extern "C" int yh_gdn_decode_fused(const void* proj, int64_t proj_stride, void* 
               use_qk_l2norm ? 1 : 0};
   // 512 threads measured fastest on MI355X at B = 128 (97 us per layer against
   // 104 / 109 us for 256 / 1024 threads)
-  // fp16 state: 61 us per layer at B = 128 for 256, 512 or 1024 threads alike
-  // (4.4 TB/s in state bytes: with half the bytes a workgroup's conv / norm
-  // chain is no longer hidden under its state loads)
+  // fp16 state: 52.5 us per layer at B = 128 (71 VGPRs, seven waves a SIMD;
+  // 61 us with the state widened in registers, 88 VGPRs, for 256, 512 or
+  // 1024 threads alike; 55.8 us forced to 64 VGPRs and eight waves)
   if (state_dtype == YH_F16)
     hipLaunchKernelGGL((gdn_decode_fused_kernel<128, 128, 512, true>), dim3(static_cast<unsigned>(B * HV)), dim3(512),
                        0, static_cast<hipStream_t>(stream), a);
