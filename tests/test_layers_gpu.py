@@ -475,6 +475,41 @@ def test_gdn_decode_fused_fp16_state(gpu, b):
     assert b == 1 or not torch.equal(s16, before)        # b = 1: its only row has index -1
 
 
+def test_gdn_decode_fused_fp16_state_range_ends(gpu):
+    """The float16 store at both ends of the range, as torch's float32 ->
+    float16 conversion rounds: rows 0-1 hold subnormal states (below 2^-14)
+    with tiny values, so the update stays subnormal; rows 2-4 hold states
+    near 65504 with a decay of ~1, so the update overflows to inf."""
+    b, h, d = 5, 32, 128
+    conv_dim, vd = 3 * h * d, h * d
+    p = conv_dim + vd + 2 * h
+    proj = rnd(b, p, dev=gpu, scale=2.0, seed=80).float()
+    conv = rnd(b, 3, conv_dim, dev=gpu, seed=81).float()
+    proj[:2, 2 * vd:conv_dim] *= 1e-6                    # v of the tiny rows
+    conv[:2, :, 2 * vd:] *= 1e-6
+    proj[2:, conv_dim + vd + h:] = -30.0                 # a: softplus ~ 0, decay ~ 1
+    proj, conv = proj.to(torch.bfloat16), conv.to(torch.bfloat16)
+    conv_w = rnd(conv_dim, 4, dev=gpu, scale=0.5, seed=82)
+    a_log = torch.log(torch.linspace(1.0, 16.0, h, device=gpu))
+    dt_bias = torch.linspace(-1.0, 1.0, h, device=gpu)
+    g = torch.Generator(device=gpu).manual_seed(83)
+    sign = torch.where(torch.rand(b, h, d, d, device=gpu, generator=g) < 0.5, -1.0, 1.0)
+    tiny = 2.0 ** (-24 + 10 * torch.rand(b, h, d, d, device=gpu, generator=g))      # 2^-24 .. 2^-14
+    huge = 60000.0 + 5504.0 * torch.rand(b, h, d, d, device=gpu, generator=g)
+    s16 = (sign * torch.where(torch.arange(b, device=gpu)[:, None, None, None] < 2, tiny, huge)).half()
+    s32 = s16.float()
+    norm_w = (1.0 + rnd(d, dev=gpu, scale=0.1, seed=84).float()).to(torch.bfloat16)
+    kw = dict(heads=h, head_dim=d, z_offset=conv_dim, b_offset=conv_dim + vd, a_offset=conv_dim + vd + h)
+    c16, c32 = conv.clone(), conv.clone()
+    y16 = layers.gdn_decode_fused(proj, c16, conv_w, a_log, dt_bias, s16, norm_w, 1e-6, **kw)
+    y32 = layers.gdn_decode_fused(proj, c32, conv_w, a_log, dt_bias, s32, norm_w, 1e-6, **kw)
+    assert torch.equal(y16, y32) and torch.equal(c16, c32)
+    assert torch.equal(s16, s32.half())
+    lo = s16[:2].float().abs()
+    assert ((lo > 0) & (lo < 2.0 ** -14)).float().mean() > 0.5   # the subnormal range is exercised
+    assert torch.isinf(s16[2:]).any() and torch.isfinite(s16[2:]).any()
+
+
 @pytest.mark.parametrize("b", [1, 5, 128])
 def test_gdn_decode_fused_equals_three_launches(gpu, b, monkeypatch):
     """Conv update + gated delta rule + gated norm in one launch give bit for
